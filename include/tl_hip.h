@@ -1,0 +1,226 @@
+/*
+ * tl_hip.h -- C ABI of libtlhip.so, the MI355X (gfx950) device backend for
+ * TensorLogic's quantized-LLM hot path.
+ *
+ * This header replaces the Metal device contract under the reference's
+ * src/device/ and the tensor operator surface the TL interpreter calls.
+ * Each entry point names the reference function it stands in for.
+ *
+ * Conventions
+ *  - Every function returns tlhip_status (0 = OK).  On error nothing was
+ *    launched; tlhip_last_error() returns a thread-local message.  Error
+ *    codes mirror the reference's TensorError variants (src/error.rs:9-49).
+ *  - One context = one device + one HIP stream.  All launches are
+ *    asynchronous on that stream; tlhip_tensor_download, tlhip_argmax and
+ *    tlhip_sync wait.  Calls on one context are not thread-safe; separate
+ *    contexts may be used from separate threads.
+ *  - Tensors are opaque, reference-counted (tlhip_tensor_retain/free).  A
+ *    free is stream-ordered: memory returns to the pool after the work
+ *    already queued on the context's stream, with no host fence (replaces
+ *    the GPU fence + buffer-pool recycle of src/tensor/tensor.rs:58-121).
+ *  - Shapes are row-major (reference order).  A linear weight is W[N, K].
+ *  - Quantized tensors (Q4_0, Q8_0) are uploaded as GGUF block bytes and
+ *    stay packed and device-resident (no dequantise-on-load).
+ *  - Host buffers in upload/download are plain host memory; sizes in bytes.
+ */
+#ifndef TL_HIP_H
+#define TL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    TLHIP_OK = 0,
+    TLHIP_ERR_SHAPE_MISMATCH = 1,     /* TensorError::ShapeMismatch */
+    TLHIP_ERR_INVALID_DIMENSION = 2,  /* TensorError::InvalidDimension */
+    TLHIP_ERR_INVALID_OPERATION = 3,  /* TensorError::InvalidOperation */
+    TLHIP_ERR_ALLOCATION = 4,         /* TensorError::AllocationError */
+    TLHIP_ERR_INDEX_OUT_OF_BOUNDS = 5,/* TensorError::IndexOutOfBounds */
+    TLHIP_ERR_LOAD = 6,               /* TensorError::LoadError (GGUF) */
+    TLHIP_ERR_DEVICE = 7,             /* TensorError::MetalError -> HIP error */
+    TLHIP_ERR_DTYPE = 8,              /* unsupported dtype for the op */
+    TLHIP_ERR_INVALID_ARGUMENT = 9    /* NULL handle, bad enum, ... */
+} tlhip_status;
+
+typedef enum {
+    TLHIP_F16 = 0,
+    TLHIP_F32 = 1,
+    TLHIP_I32 = 2,
+    TLHIP_Q4_0 = 3,   /* GGUF Q4_0: 32-element blocks along K, 18 B/block */
+    TLHIP_Q8_0 = 4    /* GGUF Q8_0: 32-element blocks along K, 34 B/block */
+} tlhip_dtype;
+
+typedef enum {
+    TLHIP_ROPE_INTERLEAVED = 0,  /* pairs (2i, 2i+1): rope_f16 unified.metal:2355-2418 */
+    TLHIP_ROPE_NEOX = 1          /* pairs (i, i+rot/2), partial rotary allowed */
+} tlhip_rope_layout;
+
+typedef struct tlhip_ctx_s* tlhip_ctx;
+typedef struct tlhip_tensor_s* tlhip_tensor;
+typedef struct tlhip_gguf_s* tlhip_gguf;
+typedef struct tlhip_model_s* tlhip_model;
+
+/* ---- errors / context ---------------------------------------------------- */
+/* Thread-local text of the last error (TensorError Display, src/error.rs). */
+const char* tlhip_last_error(void);
+/* MetalDevice::new() singleton (src/device/metal_device.rs:36-74): picks a
+ * device, creates the stream.  device < 0 selects device 0.                */
+tlhip_status tlhip_init(int device, tlhip_ctx* out);
+tlhip_status tlhip_shutdown(tlhip_ctx ctx);
+/* wait_until_completed() (metal_device.rs:195-200). */
+tlhip_status tlhip_sync(tlhip_ctx ctx);
+/* Name of the device (e.g. "AMD Instinct MI355X") and its gfx target. */
+tlhip_status tlhip_device_name(tlhip_ctx ctx, char* buf, size_t len);
+/* Debug: synchronise and check after every op (the build's counterpart of
+ * the reference's TL_DEBUG* env switches).  Also enabled by the
+ * environment variable TLHIP_SYNC_EVERY_OP=1.                              */
+tlhip_status tlhip_set_sync_every_op(tlhip_ctx ctx, int on);
+
+/* ---- tensors ------------------------------------------------------------- */
+/* MetalBuffer::new_uninit_pooled (metal_buffer.rs:213): device allocation
+ * from the stream-ordered pool.  For Q4_0/Q8_0, ndim must be 2 and shape
+ * [N, K] with K % 32 == 0.                                                 */
+tlhip_status tlhip_tensor_alloc(tlhip_ctx ctx, tlhip_dtype dtype, int ndim,
+                                const int64_t* shape, tlhip_tensor* out);
+/* MetalBuffer::from_slice (metal_buffer.rs:37) / Tensor::from_vec_gpu
+ * (tensor_creation.rs:126).  bytes must equal tlhip_tensor_nbytes(t); for
+ * Q types the host data is GGUF block bytes in file order.                 */
+tlhip_status tlhip_tensor_upload(tlhip_ctx ctx, tlhip_tensor t, const void* host, size_t bytes);
+/* MetalBuffer::to_vec (metal_buffer.rs:113) via sync_and_read
+ * (tensor_io.rs:103-117): waits for queued work, then copies.  Q types are
+ * returned as GGUF block bytes.                                            */
+tlhip_status tlhip_tensor_download(tlhip_ctx ctx, tlhip_tensor t, void* host, size_t bytes);
+tlhip_status tlhip_tensor_retain(tlhip_tensor t);
+tlhip_status tlhip_tensor_free(tlhip_tensor t);
+/* Shape / dtype query (TensorAccessors::dims). shape has room for 8 dims. */
+tlhip_status tlhip_tensor_info(tlhip_tensor t, tlhip_dtype* dtype, int* ndim, int64_t* shape);
+size_t tlhip_tensor_nbytes(tlhip_tensor t);
+/* Metadata-only reshape (Tensor::reshape): returns a new handle sharing
+ * the storage; element count must match.  Not allowed for Q types.        */
+tlhip_status tlhip_tensor_reshape(tlhip_tensor t, int ndim, const int64_t* shape, tlhip_tensor* out);
+
+/* ---- GGUF ------------------------------------------------------------------ */
+/* MmapGGUFLoader::new / parse_header (mmap_gguf.rs:120-275), spec-correct. */
+tlhip_status tlhip_gguf_open(const char* path, tlhip_gguf* out);
+tlhip_status tlhip_gguf_close(tlhip_gguf g);
+int tlhip_gguf_n_tensors(tlhip_gguf g);
+const char* tlhip_gguf_tensor_name(tlhip_gguf g, int i);
+/* get_tensor(model, name) (builtin_model.rs:204) without dequantisation:
+ * F16/F32 tensors upload as F16 (F32 rounded RNE), Q4_0/Q8_0 stay packed.
+ * Replaces GGUFLoader::load's per-tensor dequantize (gguf.rs:256-464).    */
+tlhip_status tlhip_gguf_load_tensor(tlhip_ctx ctx, tlhip_gguf g, const char* name, tlhip_tensor* out);
+tlhip_status tlhip_gguf_kv_u32(tlhip_gguf g, const char* key, uint32_t* v);
+tlhip_status tlhip_gguf_kv_f32(tlhip_gguf g, const char* key, float* v);
+
+/* ---- operators (Tensor methods / TL builtins) ---------------------------- */
+/* dequantize_q4_0 / dequantize_q8_0 (gguf.rs:22-112, mmap_gguf.rs:383-439)
+ * on the device: q [N,K] packed -> out [N,K] f16, bit-exact.              */
+tlhip_status tlhip_dequantize(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor out_f16);
+/* linear(x, W[, b]) (builtin_math.rs:76-131) = matmul_transposed_b
+ * (matmul.rs:241-458) then add(bias): y[M,N] = x[M,K] W[N,K]^T, fp32
+ * accumulation, f16 out.  W may be F16, Q4_0 or Q8_0; M <= 4 uses the
+ * fused dequant-GEMV, larger M the MFMA dequant-GEMM.  bias may be NULL.  */
+tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y);
+/* matmul(a, b) (builtin_math.rs:39, matmul.rs:52-197): c[M,N] = a[M,K] b[K,N]. */
+tlhip_status tlhip_matmul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor c);
+/* rms_norm(x, w[, eps]) (builtin_nn.rs:44-103, normalization.rs:42-250)
+ * over the last dim.                                                       */
+tlhip_status tlhip_rms_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, float eps, tlhip_tensor y);
+/* layer_norm (normalization.rs:271-535); w and b may be NULL.             */
+tlhip_status tlhip_layer_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor b, float eps, tlhip_tensor y);
+/* rope(x[, offset]) (builtin_tensor.rs:514-556, rope.rs:71-300): x [..,S,H,D].
+ * rot_dims 0 = D.  The reference's rope() is layout INTERLEAVED, theta 10000. */
+tlhip_status tlhip_rope(tlhip_ctx ctx, tlhip_tensor x, int offset, float theta,
+                        tlhip_rope_layout layout, int rot_dims, tlhip_tensor y);
+/* softmax(x) over the last dim (activations.rs:107-230). */
+tlhip_status tlhip_softmax_lastdim(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y);
+/* sigmoid (activations.rs:239-266); silu = x * sigmoid(x) as the TL
+ * function silu (chat_demo_optimized.tl:35-37); silu_mul = silu(g) * u
+ * (swiglu_ffn's intermediate); gelu (tanh form, unified.metal:837-848).   */
+tlhip_status tlhip_sigmoid(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y);
+tlhip_status tlhip_silu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y);
+tlhip_status tlhip_silu_mul(tlhip_ctx ctx, tlhip_tensor gate, tlhip_tensor up, tlhip_tensor y);
+tlhip_status tlhip_gelu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y);
+/* add / mul (elementwise.rs, add_f16/mul_f16 unified.metal:701-729); b
+ * may be a 1-D tensor matching a's last dim (row broadcast, as bias).     */
+tlhip_status tlhip_add(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y);
+tlhip_status tlhip_mul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y);
+/* tensor * scalar (mul_scalar): the scalar is rounded to f16 first.       */
+tlhip_status tlhip_mul_scalar(tlhip_ctx ctx, tlhip_tensor a, float s, tlhip_tensor y);
+/* embedding(table, ids) (builtin_nn.rs:627-812): table [V,H] F16/Q4_0/Q8_0,
+ * ids host int32[n] (bounds-checked on the host), out [n,H] f16.          */
+tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* ids, int n, tlhip_tensor out);
+/* apply_attention_mask(scores, mask) (masking.rs:36-51,147-165): where
+ * mask == 0 the score becomes -10000.  mask broadcasts over leading dims. */
+tlhip_status tlhip_apply_attention_mask(tlhip_ctx ctx, tlhip_tensor scores, tlhip_tensor mask, tlhip_tensor y);
+/* einsum("ihd,jhd->ihj") and einsum("ihj,jhd->ihd") (einsum.rs:653-886),
+ * fp32 accumulation, f16 out.  K/V may carry fewer heads than Q (GQA:
+ * head h reads h / (H/Hkv)), replacing broadcast_to + contiguous.         */
+tlhip_status tlhip_einsum_scores(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhip_tensor scores);
+tlhip_status tlhip_einsum_context(tlhip_ctx ctx, tlhip_tensor p, tlhip_tensor v, tlhip_tensor out);
+/* Fused attention = einsum scores -> * scale (f16) -> causal mask (-10000)
+ * -> softmax -> einsum context, with the reference's f16 storage points.
+ * q [S,H,D]; k, v [J,Hkv,D] (a KV cache's first J rows); query row s sits
+ * at position q_pos0 + s.  causal = 0 attends to all J keys.              */
+tlhip_status tlhip_attention(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhip_tensor v,
+                             int q_pos0, float scale, int causal, tlhip_tensor out);
+/* temperature_sample(logits, T<=1e-4) argmax (builtin_sampling.rs:170-176):
+ * last maximum wins; logits [V] or [S,V] (last row).  Synchronous.        */
+tlhip_status tlhip_argmax(tlhip_ctx ctx, tlhip_tensor logits, int32_t* out);
+
+/* ---- KV cache (model::llama::Cache, llama.rs:50-114; KVCache builtins
+ *      eval.rs:1247-1400), preallocated instead of concat-grown ----------- */
+typedef struct tlhip_kvcache_s* tlhip_kvcache;
+/* KVCache::new_f16(n_layers) with room for max_ctx rows of [Hkv, D].      */
+tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads,
+                                  int head_dim, tlhip_kvcache* out);
+tlhip_status tlhip_kvcache_free(tlhip_kvcache c);
+/* cache.set(layer, K, V): replaces the layer's contents with K,V [S,Hkv,D]. */
+tlhip_status tlhip_kvcache_set(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v);
+/* cache.append(layer, K, V): appends S rows. */
+tlhip_status tlhip_kvcache_append(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v);
+/* cache.get_k / get_v: a view [len, Hkv, D] of the layer's rows (shares
+ * storage; later appends do not change the view's length).               */
+tlhip_status tlhip_kvcache_get(tlhip_kvcache c, int layer, int which_v, tlhip_tensor* out);
+int tlhip_kvcache_len(tlhip_kvcache c, int layer);
+
+/* ---- decoder runner (the op sequence of debug/chat_demo_with_kvcache.tl,
+ *      fused; arch 0 = llama/TinyLlama, 1 = phi2) ------------------------- */
+tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* gguf_path, int arch, int max_ctx,
+                              tlhip_model* out);
+tlhip_status tlhip_model_free(tlhip_model m);
+tlhip_status tlhip_model_reset(tlhip_model m);
+/* Prompt pass at positions [pos, pos+n): fills the cache and samples the
+ * next token greedily (temperature_sample with T = 0).                   */
+tlhip_status tlhip_model_prefill(tlhip_model m, const int32_t* ids, int n, int32_t* next_token);
+/* One decode step for `token` at the current position; returns the next. */
+tlhip_status tlhip_model_decode(tlhip_model m, int32_t token, int32_t* next_token);
+/* prefill(prompt) then n_decode greedy steps; tokens_out gets 1 + n_decode
+ * ids.  use_graph = 1 replays one captured HIP graph per step, with the
+ * token and position kept on the device (no per-token host sync).        */
+tlhip_status tlhip_model_generate(tlhip_model m, const int32_t* prompt, int n_prompt,
+                                  int n_decode, int use_graph, int32_t* tokens_out);
+/* Copies the last computed logits row (f16, vocab entries) to host.       */
+tlhip_status tlhip_model_logits(tlhip_model m, uint16_t* host, size_t n);
+/* Architecture numbers: [n_layers, hidden, inter, n_heads, n_kv, head_dim, vocab, rot_dims]. */
+tlhip_status tlhip_model_dims(tlhip_model m, int32_t* dims8);
+
+/* ---- measurement helpers (hipEvent timing on the context's stream) ------ */
+/* Runs linear(x, w) `iters` times cycling over n_w weight tensors of equal
+ * shape (to defeat the LLC) and returns the mean kernel time in us from
+ * hipEvents recorded on the context stream around the launches.          */
+tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tensor* w, int n_w,
+                                tlhip_tensor y, int iters, float* avg_us);
+/* Times `n_decode` greedy steps (graph replay) after a prefill; returns
+ * total decode ms (hipEvents) and the tokens.                            */
+tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode,
+                                int32_t* tokens_out, float* prefill_ms, float* decode_ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TL_HIP_H */

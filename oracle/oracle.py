@@ -1,0 +1,291 @@
+"""ctypes wrapper over oracle/liboracle.so -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, as the parity checker or as the timed CPU baseline.  The product
+(tensorlogic_amd/, libtlhip.so) never imports it.
+
+Arrays are numpy: f16 tensors are np.float16, ids np.int32, packed GGUF blocks
+np.uint8.  Each wrapper names the tl_oracle.h function it calls; the reference
+file:line each one restates is given there.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+ACC_F32, ACC_F16 = 0, 1
+ROPE_INTERLEAVED, ROPE_NEOX = 0, 1
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_u16p = C.POINTER(C.c_uint16)
+_u8p = C.POINTER(C.c_uint8)
+_f32p = C.POINTER(C.c_float)
+_i32p = C.POINTER(C.c_int32)
+
+
+def _declare(L):
+    sz, i, f, vp = C.c_size_t, C.c_int, C.c_float, C.c_void_p
+    sig = {
+        "tlo_h2f": (f, [C.c_uint16]),
+        "tlo_f2h": (C.c_uint16, [f]),
+        "tlo_h2f_array": (None, [vp, vp, sz]),
+        "tlo_f2h_array": (None, [vp, vp, sz]),
+        "tlo_dequant_q4_0": (None, [vp, sz, vp]),
+        "tlo_dequant_q8_0": (None, [vp, sz, vp]),
+        "tlo_linear_f16": (None, [vp, vp, vp, i, i, i, i, vp]),
+        "tlo_linear_q": (None, [vp, vp, i, vp, i, i, i, i, vp]),
+        "tlo_rms_norm": (None, [vp, vp, i, i, f, vp]),
+        "tlo_layer_norm": (None, [vp, vp, vp, i, i, f, vp]),
+        "tlo_rope": (None, [vp, i, i, i, i, f, i, i, vp]),
+        "tlo_rope_table": (None, [i, i, f, vp]),
+        "tlo_softmax": (None, [vp, i, i, vp]),
+        "tlo_sigmoid": (None, [vp, sz, vp]),
+        "tlo_silu": (None, [vp, sz, vp]),
+        "tlo_add": (None, [vp, vp, sz, vp]),
+        "tlo_mul": (None, [vp, vp, sz, vp]),
+        "tlo_mul_scalar": (None, [vp, f, sz, vp]),
+        "tlo_swiglu": (None, [vp, vp, sz, vp]),
+        "tlo_gelu": (None, [vp, sz, vp]),
+        "tlo_attention": (None, [vp, vp, vp, i, i, i, i, i, i, f, i, i, vp]),
+        "tlo_embedding": (i, [vp, i, i, vp, i, vp]),
+        "tlo_argmax_last": (i, [vp, i]),
+        "tlo_model_load": (vp, [C.c_char_p, i, i, i, i]),
+        "tlo_model_free": (None, [vp]),
+        "tlo_model_generate": (i, [vp, vp, i, i, vp, vp, vp]),
+        "tlo_model_forward": (i, [vp, vp, i, i, vp, vp]),
+        "tlo_model_reset": (None, [vp]),
+        "tlo_model_vocab": (i, [vp]),
+        "tlo_model_hidden": (i, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p) if a is not None else None
+
+
+def _h(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float16)
+
+
+def h2f(bits: np.ndarray) -> np.ndarray:
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, np.float32)
+    lib().tlo_h2f_array(_p(bits), _p(out), bits.size)
+    return out
+
+
+def f2h(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().tlo_f2h_array(_p(x), _p(out), x.size)
+    return out
+
+
+def dequant(blocks: np.ndarray, gtype: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    bb = 18 if gtype == 2 else 34
+    nb = blocks.size // bb
+    out = np.empty(nb * 32, np.float16)
+    (lib().tlo_dequant_q4_0 if gtype == 2 else lib().tlo_dequant_q8_0)(_p(blocks), nb, _p(out))
+    return out
+
+
+def linear(x, w, bias=None, acc=ACC_F32) -> np.ndarray:
+    x, w = _h(x), _h(w)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), np.float16)
+    lib().tlo_linear_f16(_p(x), _p(w), _p(_h(bias)) if bias is not None else None, M, N, K, acc, _p(y))
+    return y
+
+
+def linear_q(x, blocks, gtype, N, bias=None, acc=ACC_F32) -> np.ndarray:
+    x = _h(x)
+    M, K = x.shape
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    y = np.empty((M, N), np.float16)
+    lib().tlo_linear_q(_p(x), _p(blocks), gtype, _p(_h(bias)) if bias is not None else None,
+                       M, N, K, acc, _p(y))
+    return y
+
+
+def rms_norm(x, w, eps=1e-6) -> np.ndarray:
+    x, w = _h(x), _h(w)
+    n = x.shape[-1]
+    y = np.empty_like(x)
+    lib().tlo_rms_norm(_p(x), _p(w), x.size // n, n, eps, _p(y))
+    return y
+
+
+def layer_norm(x, w, b, eps=1e-5) -> np.ndarray:
+    x = _h(x)
+    n = x.shape[-1]
+    y = np.empty_like(x)
+    lib().tlo_layer_norm(_p(x), _p(_h(w)) if w is not None else None,
+                         _p(_h(b)) if b is not None else None, x.size // n, n, eps, _p(y))
+    return y
+
+
+def rope(x, offset=0, theta=10000.0, layout=ROPE_INTERLEAVED, rot_dims=0) -> np.ndarray:
+    x = _h(x)
+    S, H, D = x.shape[-3], x.shape[-2], x.shape[-1]
+    lead = x.size // (S * H * D)
+    y = np.empty_like(x)
+    xf, yf = x.reshape(lead, S, H, D), y.reshape(lead, S, H, D)
+    for i in range(lead):
+        lib().tlo_rope(_p(np.ascontiguousarray(xf[i])), S, H, D, offset, theta, layout, rot_dims,
+                       _p(yf[i]))
+    return y
+
+
+def rope_table(max_pos, rot_dims, theta=10000.0) -> np.ndarray:
+    cs = np.empty((max_pos, rot_dims // 2, 2), np.float32)
+    lib().tlo_rope_table(max_pos, rot_dims, theta, _p(cs))
+    return cs
+
+
+def softmax(x) -> np.ndarray:
+    x = _h(x)
+    n = x.shape[-1]
+    y = np.empty_like(x)
+    lib().tlo_softmax(_p(x), x.size // n, n, _p(y))
+    return y
+
+
+def _unary(name, x):
+    x = _h(x)
+    y = np.empty_like(x)
+    getattr(lib(), name)(_p(x), x.size, _p(y))
+    return y
+
+
+def sigmoid(x):
+    return _unary("tlo_sigmoid", x)
+
+
+def silu(x):
+    return _unary("tlo_silu", x)
+
+
+def gelu(x):
+    return _unary("tlo_gelu", x)
+
+
+def _binary(name, a, b):
+    a, b = _h(a), _h(b)
+    y = np.empty_like(a)
+    getattr(lib(), name)(_p(a), _p(b), a.size, _p(y))
+    return y
+
+
+def add(a, b):
+    return _binary("tlo_add", a, b)
+
+
+def mul(a, b):
+    return _binary("tlo_mul", a, b)
+
+
+def swiglu(g, u):
+    return _binary("tlo_swiglu", g, u)
+
+
+def mul_scalar(a, s):
+    a = _h(a)
+    y = np.empty_like(a)
+    lib().tlo_mul_scalar(_p(a), s, a.size, _p(y))
+    return y
+
+
+def attention(q, k, v, q_pos0=0, scale=None, causal=True, acc=ACC_F32) -> np.ndarray:
+    q, k, v = _h(q), _h(k), _h(v)
+    S, H, D = q.shape
+    J, Hkv, _ = k.shape
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    out = np.empty_like(q)
+    lib().tlo_attention(_p(q), _p(k), _p(v), S, J, H, Hkv, D, q_pos0, float(scale),
+                        int(causal), acc, _p(out))
+    return out
+
+
+def embedding(table, ids) -> np.ndarray:
+    table = _h(table)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    V, Hd = table.shape
+    out = np.empty((ids.size, Hd), np.float16)
+    if lib().tlo_embedding(_p(table), V, Hd, _p(ids), ids.size, _p(out)) != 0:
+        raise IndexError("token id out of range")
+    return out
+
+
+def argmax_last(logits) -> int:
+    logits = _h(logits).reshape(-1)
+    return int(lib().tlo_argmax_last(_p(logits), logits.size))
+
+
+class Model:
+    """The oracle's decoder (tlo_model_*): arch 0 = llama, 1 = phi2."""
+
+    def __init__(self, path: str, arch: int = 0, max_ctx: int = 1024, acc: int = ACC_F32,
+                 n_threads: int = 0):
+        self.h = lib().tlo_model_load(path.encode(), arch, max_ctx, acc, n_threads)
+        if not self.h:
+            raise RuntimeError(f"oracle failed to load {path}")
+        self.vocab = lib().tlo_model_vocab(self.h)
+        self.hidden = lib().tlo_model_hidden(self.h)
+
+    def close(self):
+        if self.h:
+            lib().tlo_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def generate(self, prompt, n_decode: int):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        toks = np.empty(n_decode + 1, np.int32)
+        margins = np.empty(n_decode + 1, np.float32)
+        logits = np.empty(self.vocab, np.float16)
+        rc = lib().tlo_model_generate(self.h, _p(prompt), prompt.size, n_decode, _p(toks),
+                                      _p(margins), _p(logits))
+        if rc:
+            raise RuntimeError("oracle generate failed")
+        return toks, margins, logits
+
+    def forward(self, ids, pos0: int):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        hid = np.empty((ids.size, self.hidden), np.float16)
+        logits = np.empty(self.vocab, np.float16)
+        if lib().tlo_model_forward(self.h, _p(ids), ids.size, pos0, _p(hid), _p(logits)):
+            raise RuntimeError("oracle forward failed")
+        return hid, logits
+
+    def reset(self):
+        lib().tlo_model_reset(self.h)

@@ -1,0 +1,14 @@
+"""tensorlogic_amd -- MI355X (gfx950) backend for TensorLogic's quantized-LLM hot path.
+
+The compute lives in libtlhip.so (HIP kernels + C ABI, include/tl_hip.h);
+this package holds the ctypes binding, a host-side mirror of the reference's
+tensor operator surface, the GGUF writer/reader and the seeded synthetic
+model generator.
+"""
+from ._lib import F16, F32, I32, Q4_0, Q8_0, ROPE_INTERLEAVED, ROPE_NEOX, TLHipError  # noqa: F401
+from .tensor import (GGUF, Device, KVCache, Model, Tensor, attention, bench_linear,  # noqa: F401
+                     einsum, embedding, temperature_sample)
+
+__all__ = ["Device", "Tensor", "KVCache", "GGUF", "Model", "TLHipError", "einsum", "attention",
+           "embedding", "temperature_sample", "bench_linear", "F16", "F32", "I32", "Q4_0", "Q8_0",
+           "ROPE_INTERLEAVED", "ROPE_NEOX"]

@@ -1,0 +1,185 @@
+// internal.hpp -- shared declarations of libtlhip (host side).
+//
+// Device memory model: every tensor is one allocation from the HIP
+// stream-ordered pool (hipMallocAsync on the context stream).  Quantized
+// weights are stored structure-of-arrays so that a wavefront streams packed
+// blocks with 16-byte loads:
+//   Q4_0 [N,K]: qs  = N rows x K/2 bytes (block b of a row at bytes 16b..16b+15,
+//                     the GGUF nibble bytes untouched), then
+//               d   = N x K/32 f16 scales, at a 256-byte aligned offset.
+//   Q8_0 [N,K]: qs  = N rows x K int8, then d as above.
+// The byte count is the GGUF one (18 or 34 bytes per 32 weights).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "../../include/tl_hip.h"
+
+namespace tlhip {
+
+void set_error(tlhip_status st, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+tlhip_status fail(tlhip_status st, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+#define TLHIP_CHECK_HIP(expr)                                                          \
+    do {                                                                               \
+        hipError_t e_ = (expr);                                                        \
+        if (e_ != hipSuccess)                                                          \
+            return ::tlhip::fail(TLHIP_ERR_DEVICE, "%s failed: %s", #expr,            \
+                                 hipGetErrorString(e_));                               \
+    } while (0)
+
+#define TLHIP_TRY(expr)                                 \
+    do {                                                \
+        tlhip_status s_ = (expr);                       \
+        if (s_ != TLHIP_OK) return s_;                  \
+    } while (0)
+
+struct RopeTable {
+    float theta = 0.f;
+    int rot_dims = 0;
+    int max_pos = 0;
+    float* dev = nullptr;   // [max_pos][rot/2][2] (cos, sin)
+};
+
+}  // namespace tlhip
+
+struct tlhip_ctx_s {
+    // references: the user's handle plus one per live tensor; the context is
+    // destroyed when the last one goes (tensors may outlive tlhip_shutdown)
+    int refs = 1;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    bool sync_every_op = false;
+    std::vector<tlhip::RopeTable> rope_tables;
+    int32_t* d_scratch_i32 = nullptr;   // small scratch for argmax results
+    int32_t* h_pinned_i32 = nullptr;    // pinned host mirror
+};
+
+struct tlhip_tensor_s {
+    int refcount = 1;
+    tlhip_ctx ctx = nullptr;
+    tlhip_dtype dtype = TLHIP_F16;
+    int ndim = 0;
+    int64_t shape[8] = {0};
+    void* data = nullptr;       // payload (qs for Q types)
+    uint16_t* scales = nullptr; // Q types: f16 scales [N][K/32]
+    size_t alloc_bytes = 0;
+    tlhip_tensor base = nullptr;  // owner when this is a view
+};
+
+namespace tlhip {
+
+inline int64_t numel(const tlhip_tensor_s* t) {
+    int64_t n = 1;
+    for (int i = 0; i < t->ndim; i++) n *= t->shape[i];
+    return n;
+}
+inline int64_t last_dim(const tlhip_tensor_s* t) { return t->ndim ? t->shape[t->ndim - 1] : 1; }
+inline bool is_quant(tlhip_dtype d) { return d == TLHIP_Q4_0 || d == TLHIP_Q8_0; }
+inline size_t qs_row_bytes(tlhip_dtype d, int64_t K) { return d == TLHIP_Q4_0 ? (size_t)K / 2 : (size_t)K; }
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+size_t payload_bytes(tlhip_dtype d, const int64_t* shape, int ndim);
+std::string shape_str(const tlhip_tensor_s* t);
+
+tlhip_status check_ctx(tlhip_ctx ctx);
+void ctx_release(tlhip_ctx ctx);
+tlhip_status check_t(tlhip_tensor t, const char* what);
+tlhip_status check_dtype(tlhip_tensor t, tlhip_dtype d, const char* op);
+tlhip_status after_launch(tlhip_ctx ctx, const char* op);
+
+// Internal allocation of a tensor (used by ops, model and kvcache code).
+tlhip_status alloc_tensor(tlhip_ctx ctx, tlhip_dtype dtype, int ndim, const int64_t* shape,
+                          tlhip_tensor* out);
+
+// RoPE cos/sin table for (theta, rot_dims) covering positions [0, need_pos).
+tlhip_status rope_table(tlhip_ctx ctx, float theta, int rot_dims, int need_pos, const float** dev);
+
+bool gguf_lookup(tlhip_gguf g, const char* name, uint32_t* type, int* ndim, int64_t dims[4],
+                 const uint8_t** data, size_t* nbytes);
+
+// ---- kernel launchers (kernels_*.hip) --------------------------------------
+struct GemvArgs {
+    const uint16_t* x = nullptr;   // [M, K] f16
+    const void* wq = nullptr;      // qs (Q types) or f16 W
+    const uint16_t* wd = nullptr;  // scales (Q types)
+    const uint16_t* bias = nullptr;   // [N] f16, optional (EPI_BIAS)
+    const uint16_t* resid = nullptr;  // [M, N] f16 (EPI_RESID)
+    uint16_t* y = nullptr;
+    int M = 1, N = 0, K = 0;
+    int ldy = 0;                   // row stride of y (elements), default N
+};
+// Epilogues fused into the GEMV/GEMM store (each step rounds to f16 where
+// the reference's separate op would store f16):
+//   STORE      y = f16(acc)
+//   BIAS       y = f16(f16(acc) + b)                 linear(x, W, b)
+//   RESID      y = f16(r + f16(acc))                 x + linear(a, W)
+//   SWIGLU     rows (2i, 2i+1) = (gate_i, up_i):     silu(gate) * up
+//   BIAS_RESID y = f16(r + f16(f16(acc) + b))        x + linear(a, W, b)
+//   BIAS_GELU  y = gelu(f16(f16(acc) + b))           gelu(linear(x, W, b))
+enum GemvEpi { EPI_STORE = 0, EPI_BIAS = 1, EPI_RESID = 2, EPI_SWIGLU_PAIR = 3, EPI_BIAS_RESID = 4,
+               EPI_BIAS_GELU = 5 };
+
+tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi);
+tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi);
+tlhip_status launch_repack(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks, void* qs,
+                           uint16_t* d, int64_t nblocks, int64_t blocks_per_row, int to_gguf);
+tlhip_status launch_repack_rows(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks, void* qs,
+                                uint16_t* d, int64_t nblocks, int64_t bpr, int64_t dst_row0,
+                                int64_t dst_step, int to_gguf);
+tlhip_status launch_dequant(hipStream_t s, tlhip_dtype wt, const void* qs, const uint16_t* d,
+                            uint16_t* out, int64_t N, int64_t K);
+tlhip_status launch_rms_norm(hipStream_t s, const uint16_t* x, const uint16_t* w, uint16_t* y,
+                             int rows, int n, float eps);
+tlhip_status launch_layer_norm(hipStream_t s, const uint16_t* x, const uint16_t* w,
+                               const uint16_t* b, uint16_t* y, int rows, int n, float eps);
+tlhip_status launch_rope(hipStream_t s, const uint16_t* x, uint16_t* y, int S, int H, int D,
+                         int64_t batch, int offset, const int32_t* d_pos, int layout,
+                         int rot_dims, const float* table, int x_row_stride, int y_row_stride);
+tlhip_status launch_softmax(hipStream_t s, const uint16_t* x, uint16_t* y, int64_t rows, int n);
+enum EwOp { EW_SIGMOID = 0, EW_SILU = 1, EW_GELU = 2, EW_ADD = 3, EW_MUL = 4, EW_MUL_SCALAR = 5,
+            EW_SILU_MUL = 6 };
+tlhip_status launch_elementwise(hipStream_t s, int op, const uint16_t* a, const uint16_t* b,
+                                uint16_t* y, int64_t n, int64_t b_period, float scalar);
+tlhip_status launch_mask(hipStream_t s, const uint16_t* sc, const uint16_t* mask, uint16_t* y,
+                         int64_t n, int64_t mask_period);
+tlhip_status launch_embedding(hipStream_t s, tlhip_dtype tt, const void* tq, const uint16_t* td,
+                              const int32_t* ids, const int32_t* d_token, uint16_t* out, int n,
+                              int hidden);
+tlhip_status launch_argmax(hipStream_t s, const uint16_t* x, int n, int32_t* out,
+                           int32_t* token_log, int32_t* d_state);
+tlhip_status launch_scores(hipStream_t s, const uint16_t* q, const uint16_t* k, uint16_t* sc,
+                           int I, int J, int H, int Hkv, int D);
+tlhip_status launch_context(hipStream_t s, const uint16_t* p, const uint16_t* v, uint16_t* out,
+                            int I, int J, int H, int Hkv, int D);
+struct AttnArgs {
+    const uint16_t* q = nullptr;  // [S, H, D]
+    const uint16_t* k = nullptr;  // [>=J, Hkv, D]
+    const uint16_t* v = nullptr;
+    uint16_t* out = nullptr;      // [S, H, D]
+    int S = 1, H = 0, Hkv = 0, D = 0;
+    int q_pos0 = 0;               // position of query row 0
+    const int32_t* d_pos = nullptr;  // when set, q_pos0 is read from *d_pos (decode)
+    int causal = 1;
+    float scale_h = 0.125f;       // f16-rounded scale
+    int q_stride = 0, out_stride = 0;  // row strides (elements); 0 = H*D
+};
+tlhip_status launch_transpose(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows, int cols);
+tlhip_status launch_attention(hipStream_t s, const AttnArgs& a);   // decode: J from *d_pos
+tlhip_status launch_attention_j(hipStream_t s, const AttnArgs& a, int J);
+constexpr int kAttnMaxKeys = 8192;
+tlhip_status launch_copy_rows(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows,
+                              int row_elems, int src_stride, int dst_stride, const int32_t* d_pos,
+                              int dst_row0);
+tlhip_status launch_rope_kv(hipStream_t s, const uint16_t* qkv, int qkv_stride, int S, int H,
+                            int Hkv, int D, int layout, int rot_dims, const float* table,
+                            int pos0, const int32_t* d_pos, uint16_t* q_out, uint16_t* kcache,
+                            uint16_t* vcache);
+
+}  // namespace tlhip

@@ -1,0 +1,462 @@
+// kernels_elem.hip -- bandwidth-bound kernels of the hot path, gfx950:
+// RMSNorm, LayerNorm, RoPE (+ fused KV-cache write), softmax, elementwise
+// activations, attention mask, embedding gather and greedy argmax.
+//
+// Each kernel stores f16 exactly where the reference stores f16 and computes
+// in f32 in between, following the reference op named beside it.
+#include "device_common.hpp"
+#include "internal.hpp"
+
+namespace tlhip {
+
+// Block-wide sum / max over 256 threads in a fixed order (wave xor tree,
+// then the 4 wave partials in order): deterministic for a given launch.
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    v = wave_sum<64>(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __forceinline__ float block_max256(float v, float* red) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm  (rms_norm_cpu normalization.rs:199-250, rms_norm_f16
+// unified.metal:1785-1831): y = f16((x * (1/sqrt(mean(x^2) + eps))) * w)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* __restrict__ x,
+                                                       const uint16_t* __restrict__ w,
+                                                       uint16_t* __restrict__ y, int n, float eps) {
+    __shared__ float red[4];
+    const uint16_t* xr = x + (size_t)blockIdx.x * n;
+    uint16_t* yr = y + (size_t)blockIdx.x * n;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        float v = h2f(xr[i]);
+        s += v * v;
+    }
+    s = block_sum256(s, red);
+    const float mean_sq = s / (float)n;
+    const float rms = sqrtf(mean_sq + eps);
+    const float inv = 1.0f / rms;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        float nv = h2f(xr[i]) * inv;
+        yr[i] = f2h(nv * h2f(w[i]));
+    }
+}
+
+tlhip_status launch_rms_norm(hipStream_t s, const uint16_t* x, const uint16_t* w, uint16_t* y,
+                             int rows, int n, float eps) {
+    if (rows <= 0 || n <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, s, x, w, y, n, eps);
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm (layer_norm_f16 unified.metal:1620-1697): two-pass mean and
+// biased variance in f32, y = f16(((x - mean) * inv_std) * w + b)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void layer_norm_kernel(const uint16_t* __restrict__ x,
+                                                         const uint16_t* __restrict__ w,
+                                                         const uint16_t* __restrict__ b,
+                                                         uint16_t* __restrict__ y, int n, float eps) {
+    __shared__ float red[4];
+    const uint16_t* xr = x + (size_t)blockIdx.x * n;
+    uint16_t* yr = y + (size_t)blockIdx.x * n;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) s += h2f(xr[i]);
+    s = block_sum256(s, red);
+    const float mean = s / (float)n;
+    float q = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        float d = h2f(xr[i]) - mean;
+        q += d * d;
+    }
+    q = block_sum256(q, red);
+    const float var = q / (float)n;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    for (int i = threadIdx.x; i < n; i += 256) {
+        float v = (h2f(xr[i]) - mean) * inv_std;
+        if (w) v = v * h2f(w[i]);
+        if (b) v = v + h2f(b[i]);
+        yr[i] = f2h(v);
+    }
+}
+
+tlhip_status launch_layer_norm(hipStream_t s, const uint16_t* x, const uint16_t* w,
+                               const uint16_t* b, uint16_t* y, int rows, int n, float eps) {
+    if (rows <= 0 || n <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(layer_norm_kernel, dim3(rows), dim3(256), 0, s, x, w, b, y, n, eps);
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// RoPE (rope_f16 unified.metal:2355-2418): rotate pairs by the angle of
+// position pos = offset + s, cos/sin from the precomputed table.
+//   out0 = f16(x0*c - x1*s), out1 = f16(x0*s + x1*c) -- products rounded
+//   separately (no fused multiply-add), as the f32 scalar code rounds.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float& r0, float& r1) {
+    float a = __fmul_rn(x0, c), b = __fmul_rn(x1, s);
+    r0 = __fsub_rn(a, b);
+    float e = __fmul_rn(x0, s), f = __fmul_rn(x1, c);
+    r1 = __fadd_rn(e, f);
+}
+
+__device__ __forceinline__ void rope_indices(int layout, int i, int half, int& i0, int& i1) {
+    if (layout == 0) { i0 = 2 * i; i1 = 2 * i + 1; }
+    else { i0 = i; i1 = i + half; }
+}
+
+// x, y: [batch][S][H][D] with row (per s) strides in elements.
+__global__ void rope_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int S, int H,
+                            int D, int64_t batch, int offset, const int32_t* d_pos, int layout,
+                            int rot, const float* __restrict__ table, int xs, int ys) {
+    const int half = rot / 2;
+    const int64_t per_row = (int64_t)H * (D - half);   // pairs + pass-through elements
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = batch * S * per_row;
+    if (idx >= total) return;
+    const int64_t row = idx / per_row;        // batch*S index
+    const int64_t rem = idx % per_row;
+    const int h = (int)(rem / (D - half)), e = (int)(rem % (D - half));
+    const int s = (int)(row % S);
+    const int pos = offset + s + (d_pos ? *d_pos : 0);
+    const uint16_t* xr = x + (size_t)row * xs + (size_t)h * D;
+    uint16_t* yr = y + (size_t)row * ys + (size_t)h * D;
+    if (e < half) {
+        int i0, i1;
+        rope_indices(layout, e, half, i0, i1);
+        const float c = table[2 * ((size_t)pos * half + e)], sn = table[2 * ((size_t)pos * half + e) + 1];
+        float r0, r1;
+        rope_pair(h2f(xr[i0]), h2f(xr[i1]), c, sn, r0, r1);
+        yr[i0] = f2h(r0);
+        yr[i1] = f2h(r1);
+    } else {
+        const int d = rot + (e - half);   // pass-through dims >= rot
+        yr[d] = xr[d];
+    }
+}
+
+tlhip_status launch_rope(hipStream_t s, const uint16_t* x, uint16_t* y, int S, int H, int D,
+                         int64_t batch, int offset, const int32_t* d_pos, int layout, int rot_dims,
+                         const float* table, int x_row_stride, int y_row_stride) {
+    const int half = rot_dims / 2;
+    int64_t total = batch * S * (int64_t)H * (D - half);
+    if (total <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, y, S,
+                       H, D, batch, offset, d_pos, layout, rot_dims, table,
+                       x_row_stride ? x_row_stride : H * D, y_row_stride ? y_row_stride : H * D);
+    return TLHIP_OK;
+}
+
+// Decoder glue: from a fused projection row [q (H*D) | k (Hkv*D) | v (Hkv*D)]
+// write RoPE(q) to q_out, RoPE(k) and v into the KV cache rows at pos0 + s
+// (model::llama::Cache stores K after RoPE, llama.rs:78-114).
+__global__ void rope_kv_kernel(const uint16_t* __restrict__ qkv, int qkv_stride, int S, int H,
+                               int Hkv, int D, int layout, int rot, const float* __restrict__ table,
+                               int pos0, const int32_t* d_pos, uint16_t* __restrict__ q_out,
+                               uint16_t* __restrict__ kc, uint16_t* __restrict__ vc) {
+    const int half = rot / 2;
+    const int per_head = D - half;               // pairs + pass-through
+    const int nq = H * per_head, nk = Hkv * per_head, nv = Hkv * D;
+    const int per_row = nq + nk + nv;
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)S * per_row) return;
+    const int s = (int)(idx / per_row);
+    int e = (int)(idx % per_row);
+    const int base = pos0 + (d_pos ? *d_pos : 0);
+    const int pos = base + s;
+    const uint16_t* row = qkv + (size_t)s * qkv_stride;
+    if (e >= nq + nk) {   // V: copy into the cache
+        e -= nq + nk;
+        vc[(size_t)pos * nv + e] = row[(size_t)(H + Hkv) * D + e];
+        return;
+    }
+    const bool is_k = e >= nq;
+    if (is_k) e -= nq;
+    const int h = e / per_head, pe = e % per_head;
+    const uint16_t* xr = row + (size_t)(is_k ? H + h : h) * D;
+    uint16_t* yr = is_k ? kc + (size_t)pos * Hkv * D + (size_t)h * D : q_out + (size_t)s * H * D + (size_t)h * D;
+    if (pe < half) {
+        int i0, i1;
+        rope_indices(layout, pe, half, i0, i1);
+        const float c = table[2 * ((size_t)pos * half + pe)], sn = table[2 * ((size_t)pos * half + pe) + 1];
+        float r0, r1;
+        rope_pair(h2f(xr[i0]), h2f(xr[i1]), c, sn, r0, r1);
+        yr[i0] = f2h(r0);
+        yr[i1] = f2h(r1);
+    } else {
+        const int d = rot + (pe - half);
+        yr[d] = xr[d];
+    }
+}
+
+tlhip_status launch_rope_kv(hipStream_t s, const uint16_t* qkv, int qkv_stride, int S, int H,
+                            int Hkv, int D, int layout, int rot_dims, const float* table, int pos0,
+                            const int32_t* d_pos, uint16_t* q_out, uint16_t* kcache,
+                            uint16_t* vcache) {
+    const int per_head = D - rot_dims / 2;
+    int64_t total = (int64_t)S * ((H + Hkv) * per_head + Hkv * D);
+    if (total <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(rope_kv_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, qkv,
+                       qkv_stride, S, H, Hkv, D, layout, rot_dims, table, pos0, d_pos, q_out, kcache,
+                       vcache);
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// softmax over the last dim (softmax_f16 unified.metal:2057-2148 as
+// dispatched one thread per row, activations.rs:204-209):
+//   max over finite values (0 if none); e = exp(x - max) or 0 for
+//   non-finite x; y = f16(e); sum += e (f32); y = f16(f32(y) / sum);
+//   a zero / non-finite sum gives f16(1/n) everywhere.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void softmax_kernel(const uint16_t* __restrict__ x,
+                                                      uint16_t* __restrict__ y, int n) {
+    __shared__ float red[4];
+    const uint16_t* xr = x + (size_t)blockIdx.x * n;
+    uint16_t* yr = y + (size_t)blockIdx.x * n;
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        float v = h2f(xr[i]);
+        if (isfinite(v)) mx = fmaxf(mx, v);
+    }
+    mx = block_max256(mx, red);
+    if (!isfinite(mx)) mx = 0.0f;
+    float sum = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        float v = h2f(xr[i]);
+        float e = isfinite(v) ? expf(v - mx) : 0.0f;
+        yr[i] = f2h(e);
+        sum += e;
+    }
+    sum = block_sum256(sum, red);
+    if (sum > 0.0f && isfinite(sum)) {
+        for (int i = threadIdx.x; i < n; i += 256) yr[i] = f2h(h2f(yr[i]) / sum);
+    } else {
+        const uint16_t u = f2h(1.0f / (float)n);
+        for (int i = threadIdx.x; i < n; i += 256) yr[i] = u;
+    }
+}
+
+tlhip_status launch_softmax(hipStream_t s, const uint16_t* x, uint16_t* y, int64_t rows, int n) {
+    if (rows <= 0 || n <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(softmax_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, y, n);
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// elementwise (f16 in/out, f32 math, one rounding per reference op)
+// ---------------------------------------------------------------------------
+__global__ void elementwise_kernel(int op, const uint16_t* __restrict__ a,
+                                   const uint16_t* __restrict__ b, uint16_t* __restrict__ y,
+                                   int64_t n, int64_t bp, float sc) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint16_t av = a[i];
+    uint16_t r;
+    switch (op) {
+        case EW_SIGMOID: r = sigmoid_h(av); break;
+        case EW_SILU: r = f2h(h2f(av) * h2f(sigmoid_h(av))); break;
+        case EW_GELU: r = gelu_h(av); break;
+        case EW_ADD: r = f2h(h2f(av) + h2f(b[bp ? i % bp : i])); break;
+        case EW_MUL: r = f2h(h2f(av) * h2f(b[bp ? i % bp : i])); break;
+        case EW_MUL_SCALAR: r = f2h(h2f(av) * sc); break;
+        case EW_SILU_MUL: r = swiglu_h(av, b[i]); break;
+        default: r = av;
+    }
+    y[i] = r;
+}
+
+tlhip_status launch_elementwise(hipStream_t s, int op, const uint16_t* a, const uint16_t* b,
+                                uint16_t* y, int64_t n, int64_t b_period, float scalar) {
+    if (n <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(elementwise_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, op, a,
+                       b, y, n, b_period, scalar);
+    return TLHIP_OK;
+}
+
+// apply_attention_mask (masking.rs:147-165, unified.metal:4474-4489):
+// y = mask == 0 ? -10000 : score.  Either the mask repeats every `period`
+// elements of the scores, or scores are [I, H, J] and the mask is [I, J]
+// (the TL pattern reshape(mask, [S,1,S]) + broadcast_to [S,H,S]).
+__global__ void mask_kernel(const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mask,
+                            uint16_t* __restrict__ y, int64_t n, int64_t period, int64_t inner,
+                            int64_t heads) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t mi;
+    if (heads > 1) {   // scores [I, H, J], mask [I, J]
+        const int64_t j = i % inner, ih = i / inner, row = ih / heads;
+        mi = row * inner + j;
+    } else {
+        mi = i % period;
+    }
+    const uint16_t m = mask[mi];
+    y[i] = ((m & 0x7fffu) == 0) ? f2h(-10000.0f) : sc[i];
+}
+
+tlhip_status launch_mask(hipStream_t s, const uint16_t* sc, const uint16_t* mask, uint16_t* y,
+                         int64_t n, int64_t mask_period) {
+    // mask_period > 0: elementwise repeat; mask_period < 0 encodes (-J, H)
+    // packed as -(J * 65536 + H) for scores [I, H, J] with mask [I, J].
+    if (n <= 0) return TLHIP_OK;
+    int64_t period = mask_period, inner = 1, heads = 1;
+    if (mask_period < 0) {
+        int64_t enc = -mask_period;
+        inner = enc >> 16;
+        heads = enc & 0xffff;
+        period = 0;
+    }
+    hipLaunchKernelGGL(mask_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, sc, mask, y, n,
+                       period, inner, heads);
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// embedding (builtin_nn.rs:627-812, embedding_lookup_f16 unified.metal:
+// 658-676): out[s, :] = table[id_s, :]; quantized tables are dequantised
+// row by row (bit-exact with gguf.rs).  ids come from a device array, or in
+// graph-replay decode from the device token slot.
+// ---------------------------------------------------------------------------
+__global__ void embedding_kernel(int tt, const uint8_t* __restrict__ tq, const uint16_t* __restrict__ td,
+                                 const int32_t* __restrict__ ids, const int32_t* d_token,
+                                 uint16_t* __restrict__ out, int n, int hidden) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)n * hidden) return;
+    const int s = (int)(i / hidden), c = (int)(i % hidden);
+    const int id = d_token ? d_token[0] : ids[s];
+    if (tt == TLHIP_F16) {
+        out[i] = ((const uint16_t*)tq)[(size_t)id * hidden + c];
+        return;
+    }
+    const int nbr = hidden / 32, b = c / 32, e = c % 32;
+    const float d = h2f(td[(size_t)id * nbr + b]);
+    float q;
+    if (tt == TLHIP_Q4_0) {
+        const uint8_t byte = tq[(size_t)id * (hidden / 2) + 16 * b + (e & 15)];
+        q = (float)((e < 16 ? (byte & 15) : (byte >> 4)) - 8);
+    } else {
+        q = (float)(int8_t)tq[(size_t)id * hidden + c];
+    }
+    out[i] = f2h(q * d);
+}
+
+tlhip_status launch_embedding(hipStream_t s, tlhip_dtype tt, const void* tq, const uint16_t* td,
+                              const int32_t* ids, const int32_t* d_token, uint16_t* out, int n,
+                              int hidden) {
+    int64_t total = (int64_t)n * hidden;
+    if (total <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(embedding_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, (int)tt,
+                       (const uint8_t*)tq, td, ids, d_token, out, n, hidden);
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// greedy argmax (temperature_sample with T <= 1e-4, builtin_sampling.rs:
+// 170-176): Iterator::max_by keeps the LAST of equal maxima.  Optionally
+// logs the token and advances the device decode state
+// d_state = {token, pos, step}: token <- argmax, pos += 1, step += 1.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ x, int n,
+                                                      int32_t* out, int32_t* token_log,
+                                                      int32_t* d_state) {
+    __shared__ float sv[1024];
+    __shared__ int si[1024];
+    float best = -INFINITY;
+    int bi = -1;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const float v = h2f(x[i]);
+        if (!isnan(v) && (bi < 0 || v >= best)) { best = v; bi = i; }
+    }
+    sv[threadIdx.x] = best;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int st = 512; st > 0; st >>= 1) {
+        if ((int)threadIdx.x < st) {
+            const float v2 = sv[threadIdx.x + st];
+            const int i2 = si[threadIdx.x + st];
+            const float v1 = sv[threadIdx.x];
+            const int i1 = si[threadIdx.x];
+            if (i2 >= 0 && (i1 < 0 || v2 > v1 || (v2 == v1 && i2 > i1))) {
+                sv[threadIdx.x] = v2;
+                si[threadIdx.x] = i2;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const int tok = si[0] < 0 ? 0 : si[0];
+        if (out) out[0] = tok;
+        if (d_state) {
+            if (token_log) token_log[d_state[2]] = tok;
+            d_state[0] = tok;
+            d_state[1] += 1;
+            d_state[2] += 1;
+        }
+    }
+}
+
+tlhip_status launch_argmax(hipStream_t s, const uint16_t* x, int n, int32_t* out, int32_t* token_log,
+                           int32_t* d_state) {
+    if (n <= 0) return fail(TLHIP_ERR_INVALID_DIMENSION, "argmax of an empty tensor");
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, x, n, out, token_log, d_state);
+    return TLHIP_OK;
+}
+
+// Copies rows (e.g. KV-cache set/append): dst row (dst_row0 + *d_pos + r).
+__global__ void copy_rows_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                 int rows, int row_elems, int ss, int ds, const int32_t* d_pos,
+                                 int dst_row0) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)rows * row_elems) return;
+    const int r = (int)(i / row_elems), c = (int)(i % row_elems);
+    const int dr = dst_row0 + r + (d_pos ? *d_pos : 0);
+    dst[(size_t)dr * ds + c] = src[(size_t)r * ss + c];
+}
+
+tlhip_status launch_copy_rows(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows,
+                              int row_elems, int src_stride, int dst_stride, const int32_t* d_pos,
+                              int dst_row0) {
+    int64_t total = (int64_t)rows * row_elems;
+    if (total <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src,
+                       dst, rows, row_elems, src_stride, dst_stride, d_pos, dst_row0);
+    return TLHIP_OK;
+}
+
+// dst[c, r] = src[r, c] for a row-major [rows, cols] f16 matrix.
+__global__ void transpose_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int rows,
+                                 int cols) {
+    __shared__ uint16_t tile[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 256 threads: 32 x 8
+    for (int i = ty; i < 32; i += 8) {
+        const int r = r0 + i, c = c0 + tx;
+        if (r < rows && c < cols) tile[i][tx] = src[(size_t)r * cols + c];
+    }
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8) {
+        const int c = c0 + i, r = r0 + tx;
+        if (r < rows && c < cols) dst[(size_t)c * rows + r] = tile[tx][i];
+    }
+}
+
+tlhip_status launch_transpose(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows, int cols) {
+    if (rows <= 0 || cols <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(transpose_kernel, dim3((cols + 31) / 32, (rows + 31) / 32), dim3(256), 0, s, src, dst,
+                       rows, cols);
+    return TLHIP_OK;
+}
+
+}  // namespace tlhip

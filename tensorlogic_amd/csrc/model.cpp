@@ -1,0 +1,669 @@
+// model.cpp -- KV cache and the decoder runner.
+//
+// The runner executes the operator sequence of the reference's LLM programs
+// (debug/chat_demo_with_kvcache.tl prefill/decode loops, chat_demo_optimized
+// .tl:35-138) with the same f16 storage points, fused into fewer launches:
+//   llama (TinyLlama) per layer, decode step:
+//     rms_norm -> GEMV[q|k|v] -> rope(q,k) + cache write -> attention
+//     -> GEMV[o] + residual -> rms_norm -> GEMV[gate/up rows interleaved]
+//        + silu(gate)*up -> GEMV[down] + residual
+//   phi2 per layer: layer_norm -> GEMV[qkv]+bias -> rope(NeoX, partial) +
+//     cache write -> attention -> GEMV[o]+bias+residual ;
+//     GEMV[up]+bias+gelu -> GEMV[down]+bias+residual
+//   then final norm -> GEMV[lm_head] -> greedy argmax on the device.
+// RoPE is applied at each token's absolute position (the reference's demo
+// calls rope() without an offset in its decode loop, which rotates every new
+// token as position 0; the runner passes the position as rope(x, offset)
+// allows, builtin_tensor.rs:514-556).
+//
+// Decode state lives on the device: {token, pos, step}.  The embedding reads
+// the token, RoPE / cache writes / attention read pos, the argmax writes the
+// next token, advances pos and logs the token.  A decode step therefore has
+// no host inputs and is captured once as a HIP graph and replayed.
+#include <cmath>
+#include <cstring>
+
+#include "internal.hpp"
+
+using namespace tlhip;
+
+struct tlhip_kvcache_s {
+    tlhip_ctx ctx = nullptr;
+    int n_layers = 0, max_ctx = 0, n_kv = 0, head_dim = 0;
+    std::vector<tlhip_tensor> k, v;
+    std::vector<int> len;
+};
+
+namespace {
+
+struct Lin {
+    tlhip_tensor w = nullptr;
+    tlhip_tensor b = nullptr;
+};
+
+struct Layer {
+    tlhip_tensor norm_w = nullptr, norm_b = nullptr, ffn_norm_w = nullptr;
+    Lin qkv, o, gu, up, down;
+};
+
+}  // namespace
+
+struct tlhip_model_s {
+    tlhip_ctx ctx = nullptr;
+    int arch = 0;
+    int n_layers = 0, hidden = 0, inter = 0, n_heads = 0, n_kv = 0, head_dim = 0, vocab = 0, rot = 0;
+    int max_ctx = 0, max_rows = 0;
+    float eps = 1e-5f, theta = 10000.0f;
+    tlhip_tensor embd = nullptr, out_norm_w = nullptr, out_norm_b = nullptr;
+    Lin out;
+    std::vector<Layer> layers;
+    tlhip_kvcache kv = nullptr;
+    // activations, sized for max_rows tokens per pass
+    tlhip_tensor x = nullptr, xn = nullptr, qkv = nullptr, qrot = nullptr, att = nullptr, hmid = nullptr,
+                 logits = nullptr;
+    int32_t* d_state = nullptr;   // {token, pos, step}
+    int32_t* d_tokens = nullptr;  // token log
+    int32_t* d_ids = nullptr;     // prompt ids
+    int32_t* h_state = nullptr;   // pinned
+    const float* rope_tab = nullptr;
+    int pos = 0;
+    hipGraphExec_t gexec = nullptr;
+    hipGraph_t graph = nullptr;
+};
+
+namespace {
+
+uint16_t* P(tlhip_tensor t) { return (uint16_t*)t->data; }
+
+void free_lin(Lin& l) {
+    tlhip_tensor_free(l.w);
+    tlhip_tensor_free(l.b);
+    l.w = l.b = nullptr;
+}
+
+tlhip_dtype dtype_of(uint32_t gt) {
+    switch (gt) {
+        case 0: case 1: return TLHIP_F16;
+        case 2: return TLHIP_Q4_0;
+        case 8: return TLHIP_Q8_0;
+        default: return (tlhip_dtype)-1;
+    }
+}
+
+// Loads a 1-D f16 vector of length n.
+tlhip_status load_vec(tlhip_ctx ctx, tlhip_gguf g, const std::string& name, int64_t n, tlhip_tensor* out) {
+    TLHIP_TRY(tlhip_gguf_load_tensor(ctx, g, name.c_str(), out));
+    const int64_t got = numel(*out);
+    if (got != n || (*out)->dtype != TLHIP_F16) {
+        tlhip_tensor_free(*out);
+        *out = nullptr;
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "%s: %lld elements, expected %lld f16", name.c_str(),
+                    (long long)got, (long long)n);
+    }
+    return TLHIP_OK;
+}
+
+// Places the rows of GGUF weight `name` [n, k] into `dst` rows
+// dst_row0, dst_row0 + step, ... (step 1: concatenation, 2: interleave).
+tlhip_status place_rows(tlhip_ctx ctx, tlhip_gguf g, const std::string& name, int64_t n, int64_t k,
+                        tlhip_tensor dst, int64_t dst_row0, int64_t step) {
+    uint32_t gt;
+    int nd;
+    int64_t dims[4];
+    const uint8_t* data;
+    size_t nbytes;
+    if (!gguf_lookup(g, name.c_str(), &gt, &nd, dims, &data, &nbytes))
+        return fail(TLHIP_ERR_LOAD, "tensor %s not found in GGUF", name.c_str());
+    if (nd != 2 || dims[0] != n || dims[1] != k)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "%s: [%lld, %lld], expected [%lld, %lld]", name.c_str(),
+                    (long long)dims[0], (long long)dims[1], (long long)n, (long long)k);
+    if (dtype_of(gt) != dst->dtype)
+        return fail(TLHIP_ERR_DTYPE, "%s: GGUF type %u differs from the fused tensor's dtype", name.c_str(), gt);
+    if (gt == 0) return fail(TLHIP_ERR_DTYPE, "%s: F32 linear weights are not supported by the runner", name.c_str());
+    void* stage = nullptr;
+    TLHIP_CHECK_HIP(hipMallocAsync(&stage, nbytes, ctx->stream));
+    TLHIP_CHECK_HIP(hipMemcpyAsync(stage, data, nbytes, hipMemcpyHostToDevice, ctx->stream));
+    tlhip_status st = TLHIP_OK;
+    if (is_quant(dst->dtype)) {
+        st = launch_repack_rows(ctx->stream, dst->dtype, (const uint8_t*)stage, dst->data, dst->scales,
+                                n * k / 32, k / 32, dst_row0, step, 0);
+    } else {
+        const size_t rb = (size_t)k * 2;
+        hipError_t e = hipMemcpy2DAsync((uint8_t*)dst->data + (size_t)dst_row0 * rb, rb * step, stage, rb, rb,
+                                        (size_t)n, hipMemcpyDeviceToDevice, ctx->stream);
+        if (e != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "hipMemcpy2DAsync: %s", hipGetErrorString(e));
+    }
+    (void)hipFreeAsync(stage, ctx->stream);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (st == TLHIP_OK && e != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "load %s: %s", name.c_str(), hipGetErrorString(e));
+    return st;
+}
+
+tlhip_status weight_dtype(tlhip_gguf g, const std::string& name, tlhip_dtype* dt) {
+    uint32_t gt;
+    int nd;
+    int64_t dims[4];
+    const uint8_t* data;
+    size_t nbytes;
+    if (!gguf_lookup(g, name.c_str(), &gt, &nd, dims, &data, &nbytes))
+        return fail(TLHIP_ERR_LOAD, "tensor %s not found in GGUF", name.c_str());
+    *dt = dtype_of(gt);
+    if ((int)*dt < 0) return fail(TLHIP_ERR_DTYPE, "%s: GGUF type %u not supported on the device", name.c_str(), gt);
+    return TLHIP_OK;
+}
+
+// A fused weight made of `parts` (name, rows) stacked along N.
+tlhip_status fused_weight(tlhip_ctx ctx, tlhip_gguf g, const std::vector<std::pair<std::string, int64_t>>& parts,
+                          int64_t k, bool interleave, tlhip_tensor* out) {
+    tlhip_dtype dt;
+    TLHIP_TRY(weight_dtype(g, parts[0].first, &dt));
+    int64_t n = 0;
+    for (auto& p : parts) n += p.second;
+    int64_t shp[2] = {n, k};
+    TLHIP_TRY(alloc_tensor(ctx, dt, 2, shp, out));
+    int64_t row0 = 0;
+    for (size_t i = 0; i < parts.size(); i++) {
+        tlhip_status st = interleave ? place_rows(ctx, g, parts[i].first, parts[i].second, k, *out, (int64_t)i,
+                                                  (int64_t)parts.size())
+                                     : place_rows(ctx, g, parts[i].first, parts[i].second, k, *out, row0, 1);
+        if (st != TLHIP_OK) {
+            tlhip_tensor_free(*out);
+            *out = nullptr;
+            return st;
+        }
+        row0 += parts[i].second;
+    }
+    return TLHIP_OK;
+}
+
+tlhip_status linear_into(hipStream_t s, const Lin& l, const uint16_t* x, int M, uint16_t* y, int epi,
+                         const uint16_t* resid, int ldy = 0) {
+    GemvArgs a;
+    a.x = x;
+    a.wq = l.w->data;
+    a.wd = l.w->scales;
+    a.bias = l.b ? P(l.b) : nullptr;
+    a.resid = resid;
+    a.y = y;
+    a.M = M;
+    a.N = (int)l.w->shape[0];
+    a.K = (int)l.w->shape[1];
+    a.ldy = ldy;
+    if (M <= 4) {
+        tlhip_status st = launch_gemv(s, l.w->dtype, a, epi);
+        if (st == TLHIP_OK) return st;
+    }
+    return launch_gemm(s, l.w->dtype, a, epi);
+}
+
+// Enqueues the layers and the head for S tokens at positions pos0.. (plus
+// *d_pos when given), ending with the argmax that updates d_state.
+tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_dev, bool decode) {
+    hipStream_t s = m->ctx->stream;
+    const int H = m->hidden, D = m->head_dim, NH = m->n_heads, NKV = m->n_kv, kvd = NKV * D;
+    const int32_t* d_pos = decode ? m->d_state + 1 : nullptr;
+    TLHIP_TRY(launch_embedding(s, m->embd->dtype, m->embd->data, m->embd->scales, ids_dev,
+                               decode ? m->d_state : nullptr, P(m->x), S, H));
+    const int qkv_w = H + 2 * kvd;
+    for (int li = 0; li < m->n_layers; li++) {
+        Layer& L = m->layers[li];
+        uint16_t* kc = P(m->kv->k[li]);
+        uint16_t* vc = P(m->kv->v[li]);
+        if (m->arch == 0) TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.norm_w), P(m->xn), S, H, m->eps));
+        else TLHIP_TRY(launch_layer_norm(s, P(m->x), P(L.norm_w), P(L.norm_b), P(m->xn), S, H, m->eps));
+        TLHIP_TRY(linear_into(s, L.qkv, P(m->xn), S, P(m->qkv), L.qkv.b ? EPI_BIAS : EPI_STORE, nullptr));
+        TLHIP_TRY(launch_rope_kv(s, P(m->qkv), qkv_w, S, NH, NKV, D, m->arch == 0 ? 0 : 1, m->rot, m->rope_tab,
+                                 decode ? 0 : pos0, d_pos, P(m->qrot), kc, vc));
+        AttnArgs a;
+        a.q = P(m->qrot);
+        a.k = kc;
+        a.v = vc;
+        a.out = P(m->att);
+        a.S = S;
+        a.H = NH;
+        a.Hkv = NKV;
+        a.D = D;
+        a.causal = 1;
+        a.scale_h = (float)(_Float16)(1.0f / sqrtf((float)D));
+        if (decode) {
+            a.d_pos = d_pos;
+            TLHIP_TRY(launch_attention(s, a));
+        } else {
+            a.q_pos0 = pos0;
+            TLHIP_TRY(launch_attention_j(s, a, pos0 + S));
+        }
+        if (m->arch == 0) {
+            TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_RESID, P(m->x)));
+            TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.ffn_norm_w), P(m->xn), S, H, m->eps));
+            TLHIP_TRY(linear_into(s, L.gu, P(m->xn), S, P(m->hmid), EPI_SWIGLU_PAIR, nullptr));
+            TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_RESID, P(m->x)));
+        } else {
+            TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_BIAS_RESID, P(m->x)));
+            TLHIP_TRY(linear_into(s, L.up, P(m->xn), S, P(m->hmid), EPI_BIAS_GELU, nullptr));
+            TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_BIAS_RESID, P(m->x)));
+        }
+    }
+    const uint16_t* last = P(m->x) + (size_t)(S - 1) * H;
+    if (m->arch == 0) TLHIP_TRY(launch_rms_norm(s, last, P(m->out_norm_w), P(m->xn), 1, H, m->eps));
+    else TLHIP_TRY(launch_layer_norm(s, last, P(m->out_norm_w), P(m->out_norm_b), P(m->xn), 1, H, m->eps));
+    TLHIP_TRY(linear_into(s, m->out, P(m->xn), 1, P(m->logits), m->out.b ? EPI_BIAS : EPI_STORE, nullptr));
+    TLHIP_TRY(launch_argmax(s, P(m->logits), m->vocab, nullptr, m->d_tokens, m->d_state));
+    return TLHIP_OK;
+}
+
+tlhip_status set_state(tlhip_model m, int token, int pos, int step) {
+    // h_state is only rewritten after the stream has drained (every caller
+    // synchronises before returning), so the async copy reads stable memory.
+    m->h_state[0] = token;
+    m->h_state[1] = pos;
+    m->h_state[2] = step;
+    TLHIP_CHECK_HIP(hipMemcpyAsync(m->d_state, m->h_state, 3 * sizeof(int32_t), hipMemcpyHostToDevice, m->ctx->stream));
+    return TLHIP_OK;
+}
+
+tlhip_status read_state(tlhip_model m, int32_t* token) {
+    TLHIP_CHECK_HIP(hipMemcpyAsync(m->h_state, m->d_state, 3 * sizeof(int32_t), hipMemcpyDeviceToHost, m->ctx->stream));
+    TLHIP_CHECK_HIP(hipStreamSynchronize(m->ctx->stream));
+    if (token) *token = m->h_state[0];
+    return TLHIP_OK;
+}
+
+// Prefill in chunks of at most max_rows tokens; leaves d_state =
+// {next token, pos0 + n, step + 1} and logs the token at `step`.
+tlhip_status prefill(tlhip_model m, const int32_t* ids, int n, int step) {
+    if (n <= 0) return fail(TLHIP_ERR_INVALID_ARGUMENT, "prefill of %d tokens", n);
+    if (m->pos + n > m->max_ctx)
+        return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "context overflow: %d + %d > %d", m->pos, n, m->max_ctx);
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= m->vocab)
+            return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "token id %d out of range [0, %d)", ids[i], m->vocab);
+    for (int c0 = 0; c0 < n; c0 += m->max_rows) {
+        const int S = std::min(m->max_rows, n - c0);
+        TLHIP_CHECK_HIP(hipMemcpyAsync(m->d_ids, ids + c0, sizeof(int32_t) * S, hipMemcpyHostToDevice, m->ctx->stream));
+        TLHIP_TRY(set_state(m, 0, m->pos + S - 1, step));
+        TLHIP_TRY(enqueue_forward(m, S, m->pos, m->d_ids, false));
+        TLHIP_CHECK_HIP(hipStreamSynchronize(m->ctx->stream));   // ids / h_state reuse
+        m->pos += S;
+    }
+    TLHIP_CHECK_HIP(hipGetLastError());
+    return TLHIP_OK;
+}
+
+tlhip_status ensure_graph(tlhip_model m) {
+    if (m->gexec) return TLHIP_OK;
+    hipStream_t s = m->ctx->stream;
+    TLHIP_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    tlhip_status st = enqueue_forward(m, 1, 0, nullptr, true);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (st != TLHIP_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return st;
+    }
+    if (e != hipSuccess) return fail(TLHIP_ERR_DEVICE, "graph capture failed: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return fail(TLHIP_ERR_DEVICE, "graph instantiate failed: %s", hipGetErrorString(e));
+    }
+    m->graph = g;
+    return TLHIP_OK;
+}
+
+tlhip_status decode_steps(tlhip_model m, int n, bool use_graph) {
+    if (m->pos + n > m->max_ctx)
+        return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "context overflow: %d + %d > %d", m->pos, n, m->max_ctx);
+    if (use_graph) {
+        TLHIP_TRY(ensure_graph(m));
+        for (int i = 0; i < n; i++) TLHIP_CHECK_HIP(hipGraphLaunch(m->gexec, m->ctx->stream));
+    } else {
+        for (int i = 0; i < n; i++) TLHIP_TRY(enqueue_forward(m, 1, 0, nullptr, true));
+    }
+    m->pos += n;
+    return TLHIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---------------------------------------------------------------------------
+// KV cache
+// ---------------------------------------------------------------------------
+tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads, int head_dim,
+                                  tlhip_kvcache* out) {
+    TLHIP_TRY(check_ctx(ctx));
+    if (!out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null output");
+    *out = nullptr;
+    if (n_layers <= 0 || max_ctx <= 0 || n_kv_heads <= 0 || head_dim <= 0)
+        return fail(TLHIP_ERR_INVALID_DIMENSION, "kvcache: bad sizes");
+    auto* c = new tlhip_kvcache_s();
+    c->ctx = ctx;
+    c->n_layers = n_layers;
+    c->max_ctx = max_ctx;
+    c->n_kv = n_kv_heads;
+    c->head_dim = head_dim;
+    c->len.assign(n_layers, 0);
+    int64_t shp[3] = {max_ctx, n_kv_heads, head_dim};
+    for (int i = 0; i < n_layers; i++) {
+        tlhip_tensor k = nullptr, v = nullptr;
+        tlhip_status st = alloc_tensor(ctx, TLHIP_F16, 3, shp, &k);
+        if (st == TLHIP_OK) st = alloc_tensor(ctx, TLHIP_F16, 3, shp, &v);
+        if (st != TLHIP_OK) {
+            tlhip_tensor_free(k);
+            tlhip_kvcache_free(c);
+            return st;
+        }
+        c->k.push_back(k);
+        c->v.push_back(v);
+    }
+    *out = c;
+    return TLHIP_OK;
+}
+
+tlhip_status tlhip_kvcache_free(tlhip_kvcache c) {
+    if (!c) return TLHIP_OK;
+    for (auto t : c->k) tlhip_tensor_free(t);
+    for (auto t : c->v) tlhip_tensor_free(t);
+    delete c;
+    return TLHIP_OK;
+}
+
+static tlhip_status kv_write(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v, bool append) {
+    TLHIP_TRY(check_ctx(ctx));
+    if (!c || layer < 0 || layer >= c->n_layers) return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "kvcache layer %d", layer);
+    TLHIP_TRY(check_t(k, "kvcache K"));
+    TLHIP_TRY(check_t(v, "kvcache V"));
+    TLHIP_TRY(check_dtype(k, TLHIP_F16, "kvcache"));
+    TLHIP_TRY(check_dtype(v, TLHIP_F16, "kvcache"));
+    const int64_t row = (int64_t)c->n_kv * c->head_dim;
+    if (k->ndim < 1 || numel(k) % row != 0 || numel(v) != numel(k) || last_dim(k) != c->head_dim)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "kvcache: K %s / V %s for rows of [%d, %d]", shape_str(k).c_str(),
+                    shape_str(v).c_str(), c->n_kv, c->head_dim);
+    const int S = (int)(numel(k) / row);
+    const int start = append ? c->len[layer] : 0;
+    if (start + S > c->max_ctx)
+        return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "kvcache: %d + %d rows > %d", start, S, c->max_ctx);
+    TLHIP_TRY(launch_copy_rows(ctx->stream, P(k), P(c->k[layer]), S, (int)row, (int)row, (int)row, nullptr, start));
+    TLHIP_TRY(launch_copy_rows(ctx->stream, P(v), P(c->v[layer]), S, (int)row, (int)row, (int)row, nullptr, start));
+    c->len[layer] = start + S;
+    return after_launch(ctx, append ? "kvcache_append" : "kvcache_set");
+}
+
+tlhip_status tlhip_kvcache_set(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v) {
+    return kv_write(ctx, c, layer, k, v, false);
+}
+
+tlhip_status tlhip_kvcache_append(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v) {
+    return kv_write(ctx, c, layer, k, v, true);
+}
+
+tlhip_status tlhip_kvcache_get(tlhip_kvcache c, int layer, int which_v, tlhip_tensor* out) {
+    if (!c || !out || layer < 0 || layer >= c->n_layers)
+        return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "kvcache layer %d", layer);
+    if (c->len[layer] == 0) return fail(TLHIP_ERR_INVALID_OPERATION, "kvcache layer %d is empty", layer);
+    tlhip_tensor src = which_v ? c->v[layer] : c->k[layer];
+    int64_t shp[3] = {c->len[layer], c->n_kv, c->head_dim};
+    // a view of the first len rows: same storage, shorter leading dim
+    auto* view = new tlhip_tensor_s();
+    *view = *src;
+    view->refcount = 1;
+    view->shape[0] = shp[0];
+    view->base = src;
+    src->refcount++;
+    *out = view;
+    return TLHIP_OK;
+}
+
+int tlhip_kvcache_len(tlhip_kvcache c, int layer) {
+    if (!c || layer < 0 || layer >= c->n_layers) return -1;
+    return c->len[layer];
+}
+
+// ---------------------------------------------------------------------------
+// model
+// ---------------------------------------------------------------------------
+tlhip_status tlhip_model_free(tlhip_model m) {
+    if (!m) return TLHIP_OK;
+    if (m->ctx) (void)hipStreamSynchronize(m->ctx->stream);
+    if (m->gexec) (void)hipGraphExecDestroy(m->gexec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    for (auto& L : m->layers) {
+        tlhip_tensor_free(L.norm_w);
+        tlhip_tensor_free(L.norm_b);
+        tlhip_tensor_free(L.ffn_norm_w);
+        free_lin(L.qkv);
+        free_lin(L.o);
+        free_lin(L.gu);
+        free_lin(L.up);
+        free_lin(L.down);
+    }
+    tlhip_tensor_free(m->embd);
+    tlhip_tensor_free(m->out_norm_w);
+    tlhip_tensor_free(m->out_norm_b);
+    free_lin(m->out);
+    tlhip_kvcache_free(m->kv);
+    for (tlhip_tensor t : {m->x, m->xn, m->qkv, m->qrot, m->att, m->hmid, m->logits}) tlhip_tensor_free(t);
+    if (m->d_state) (void)hipFree(m->d_state);
+    if (m->d_tokens) (void)hipFree(m->d_tokens);
+    if (m->d_ids) (void)hipFree(m->d_ids);
+    if (m->h_state) (void)hipHostFree(m->h_state);
+    delete m;
+    return TLHIP_OK;
+}
+
+tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max_ctx, tlhip_model* out) {
+    TLHIP_TRY(check_ctx(ctx));
+    if (!path || !out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (arch != 0 && arch != 1) return fail(TLHIP_ERR_INVALID_ARGUMENT, "arch %d (0 = llama, 1 = phi2)", arch);
+    if (max_ctx <= 0 || max_ctx > kAttnMaxKeys)
+        return fail(TLHIP_ERR_INVALID_DIMENSION, "max_ctx %d not in 1..%d", max_ctx, kAttnMaxKeys);
+    tlhip_gguf g;
+    TLHIP_TRY(tlhip_gguf_open(path, &g));
+    auto* m = new tlhip_model_s();
+    m->ctx = ctx;
+    m->arch = arch;
+    m->max_ctx = max_ctx;
+    const std::string a = arch == 0 ? "llama." : "phi2.";
+    tlhip_status st = TLHIP_OK;
+    auto kv_u = [&](const char* k, int* dst) {
+        uint32_t u;
+        if (st == TLHIP_OK) st = tlhip_gguf_kv_u32(g, (a + k).c_str(), &u);
+        if (st == TLHIP_OK) *dst = (int)u;
+    };
+    kv_u("block_count", &m->n_layers);
+    kv_u("embedding_length", &m->hidden);
+    kv_u("feed_forward_length", &m->inter);
+    kv_u("attention.head_count", &m->n_heads);
+    kv_u("attention.head_count_kv", &m->n_kv);
+    do {
+        if (st != TLHIP_OK) break;
+        if (m->n_heads <= 0 || m->hidden % m->n_heads || m->n_kv <= 0 || m->n_heads % m->n_kv) {
+            st = fail(TLHIP_ERR_LOAD, "inconsistent head counts");
+            break;
+        }
+        m->head_dim = m->hidden / m->n_heads;
+        float f;
+        if (tlhip_gguf_kv_f32(g, (a + (arch == 0 ? "attention.layer_norm_rms_epsilon" : "attention.layer_norm_epsilon")).c_str(), &f) == TLHIP_OK)
+            m->eps = f;
+        if (tlhip_gguf_kv_f32(g, (a + "rope.freq_base").c_str(), &f) == TLHIP_OK) m->theta = f;
+        uint32_t u;
+        m->rot = tlhip_gguf_kv_u32(g, (a + "rope.dimension_count").c_str(), &u) == TLHIP_OK ? (int)u : m->head_dim;
+        if (m->rot <= 0 || m->rot > m->head_dim || m->rot % 2) {
+            st = fail(TLHIP_ERR_LOAD, "bad rope.dimension_count %d", m->rot);
+            break;
+        }
+        const int64_t H = m->hidden, kvd = (int64_t)m->n_kv * m->head_dim, I = m->inter;
+        if ((st = tlhip_gguf_load_tensor(ctx, g, "token_embd.weight", &m->embd)) != TLHIP_OK) break;
+        if (m->embd->ndim != 2 || m->embd->shape[1] != H) {
+            st = fail(TLHIP_ERR_SHAPE_MISMATCH, "token_embd.weight %s", shape_str(m->embd).c_str());
+            break;
+        }
+        m->vocab = (int)m->embd->shape[0];
+        if ((st = load_vec(ctx, g, "output_norm.weight", H, &m->out_norm_w)) != TLHIP_OK) break;
+        if (arch == 1 && (st = load_vec(ctx, g, "output_norm.bias", H, &m->out_norm_b)) != TLHIP_OK) break;
+        if ((st = fused_weight(ctx, g, {{"output.weight", m->vocab}}, H, false, &m->out.w)) != TLHIP_OK) break;
+        if (arch == 1 && (st = load_vec(ctx, g, "output.bias", m->vocab, &m->out.b)) != TLHIP_OK) break;
+        m->layers.resize(m->n_layers);
+        for (int i = 0; i < m->n_layers && st == TLHIP_OK; i++) {
+            Layer& L = m->layers[i];
+            const std::string p = "blk." + std::to_string(i) + ".";
+            if ((st = load_vec(ctx, g, p + "attn_norm.weight", H, &L.norm_w)) != TLHIP_OK) break;
+            if (arch == 0) {
+                if ((st = load_vec(ctx, g, p + "ffn_norm.weight", H, &L.ffn_norm_w)) != TLHIP_OK) break;
+                if ((st = fused_weight(ctx, g, {{p + "attn_q.weight", H}, {p + "attn_k.weight", kvd}, {p + "attn_v.weight", kvd}},
+                                       H, false, &L.qkv.w)) != TLHIP_OK) break;
+                if ((st = fused_weight(ctx, g, {{p + "attn_output.weight", H}}, H, false, &L.o.w)) != TLHIP_OK) break;
+                if ((st = fused_weight(ctx, g, {{p + "ffn_gate.weight", I}, {p + "ffn_up.weight", I}}, H, true, &L.gu.w)) != TLHIP_OK) break;
+                if ((st = fused_weight(ctx, g, {{p + "ffn_down.weight", H}}, I, false, &L.down.w)) != TLHIP_OK) break;
+            } else {
+                if ((st = load_vec(ctx, g, p + "attn_norm.bias", H, &L.norm_b)) != TLHIP_OK) break;
+                if ((st = fused_weight(ctx, g, {{p + "attn_qkv.weight", H + 2 * kvd}}, H, false, &L.qkv.w)) != TLHIP_OK) break;
+                if ((st = load_vec(ctx, g, p + "attn_qkv.bias", H + 2 * kvd, &L.qkv.b)) != TLHIP_OK) break;
+                if ((st = fused_weight(ctx, g, {{p + "attn_output.weight", H}}, H, false, &L.o.w)) != TLHIP_OK) break;
+                if ((st = load_vec(ctx, g, p + "attn_output.bias", H, &L.o.b)) != TLHIP_OK) break;
+                if ((st = fused_weight(ctx, g, {{p + "ffn_up.weight", I}}, H, false, &L.up.w)) != TLHIP_OK) break;
+                if ((st = load_vec(ctx, g, p + "ffn_up.bias", I, &L.up.b)) != TLHIP_OK) break;
+                if ((st = fused_weight(ctx, g, {{p + "ffn_down.weight", H}}, I, false, &L.down.w)) != TLHIP_OK) break;
+                if ((st = load_vec(ctx, g, p + "ffn_down.bias", H, &L.down.b)) != TLHIP_OK) break;
+            }
+        }
+        if (st != TLHIP_OK) break;
+        if ((st = tlhip_kvcache_create(ctx, m->n_layers, max_ctx, m->n_kv, m->head_dim, &m->kv)) != TLHIP_OK) break;
+        m->max_rows = std::min(max_ctx, 512);
+        const int64_t R = m->max_rows;
+        const int64_t wide = std::max<int64_t>(H + 2 * kvd, arch == 0 ? I : I);
+        int64_t s_x[2] = {R, H}, s_qkv[2] = {R, H + 2 * kvd}, s_h[2] = {R, std::max<int64_t>(wide, I)},
+                s_l[1] = {m->vocab};
+        if ((st = alloc_tensor(ctx, TLHIP_F16, 2, s_x, &m->x)) != TLHIP_OK) break;
+        if ((st = alloc_tensor(ctx, TLHIP_F16, 2, s_x, &m->xn)) != TLHIP_OK) break;
+        if ((st = alloc_tensor(ctx, TLHIP_F16, 2, s_qkv, &m->qkv)) != TLHIP_OK) break;
+        if ((st = alloc_tensor(ctx, TLHIP_F16, 2, s_x, &m->qrot)) != TLHIP_OK) break;
+        if ((st = alloc_tensor(ctx, TLHIP_F16, 2, s_x, &m->att)) != TLHIP_OK) break;
+        if ((st = alloc_tensor(ctx, TLHIP_F16, 2, s_h, &m->hmid)) != TLHIP_OK) break;
+        if ((st = alloc_tensor(ctx, TLHIP_F16, 1, s_l, &m->logits)) != TLHIP_OK) break;
+        hipError_t e = hipMalloc(&m->d_state, 4 * sizeof(int32_t));
+        if (e == hipSuccess) e = hipMalloc(&m->d_tokens, sizeof(int32_t) * (max_ctx + 1));
+        if (e == hipSuccess) e = hipMalloc(&m->d_ids, sizeof(int32_t) * R);
+        if (e == hipSuccess) e = hipHostMalloc(&m->h_state, 4 * sizeof(int32_t), hipHostMallocDefault);
+        if (e != hipSuccess) {
+            st = fail(TLHIP_ERR_ALLOCATION, "model buffers: %s", hipGetErrorString(e));
+            break;
+        }
+        st = rope_table(ctx, m->theta, m->rot, max_ctx, &m->rope_tab);
+    } while (0);
+    tlhip_gguf_close(g);
+    if (st == TLHIP_OK) {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "model load: %s", hipGetErrorString(e));
+    }
+    if (st != TLHIP_OK) {
+        std::string msg = tlhip_last_error();
+        tlhip_model_free(m);
+        set_error(st, "%s", msg.c_str() + (msg.find(": ") != std::string::npos ? msg.find(": ") + 2 : 0));
+        return st;
+    }
+    *out = m;
+    return TLHIP_OK;
+}
+
+tlhip_status tlhip_model_reset(tlhip_model m) {
+    if (!m) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null model");
+    m->pos = 0;
+    return TLHIP_OK;
+}
+
+tlhip_status tlhip_model_dims(tlhip_model m, int32_t* d) {
+    if (!m || !d) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
+    int32_t v[8] = {m->n_layers, m->hidden, m->inter, m->n_heads, m->n_kv, m->head_dim, m->vocab, m->rot};
+    memcpy(d, v, sizeof v);
+    return TLHIP_OK;
+}
+
+tlhip_status tlhip_model_prefill(tlhip_model m, const int32_t* ids, int n, int32_t* next) {
+    if (!m || !ids) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
+    TLHIP_TRY(prefill(m, ids, n, 0));
+    return read_state(m, next);
+}
+
+tlhip_status tlhip_model_decode(tlhip_model m, int32_t token, int32_t* next) {
+    if (!m) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null model");
+    if (token < 0 || token >= m->vocab)
+        return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "token id %d out of range [0, %d)", token, m->vocab);
+    TLHIP_TRY(set_state(m, token, m->pos, 0));
+    TLHIP_TRY(decode_steps(m, 1, false));
+    return read_state(m, next);
+}
+
+tlhip_status tlhip_model_generate(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode, int use_graph,
+                                  int32_t* tokens_out) {
+    if (!m || !prompt || !tokens_out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
+    if (n_decode < 0) return fail(TLHIP_ERR_INVALID_ARGUMENT, "n_decode < 0");
+    m->pos = 0;
+    if (n_prompt + n_decode > m->max_ctx)
+        return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "context overflow: %d + %d > %d", n_prompt, n_decode, m->max_ctx);
+    TLHIP_TRY(prefill(m, prompt, n_prompt, 0));
+    TLHIP_TRY(decode_steps(m, n_decode, use_graph != 0));
+    TLHIP_CHECK_HIP(hipMemcpyAsync(tokens_out, m->d_tokens, sizeof(int32_t) * (n_decode + 1), hipMemcpyDeviceToHost,
+                                   m->ctx->stream));
+    TLHIP_CHECK_HIP(hipStreamSynchronize(m->ctx->stream));
+    return TLHIP_OK;
+}
+
+tlhip_status tlhip_model_logits(tlhip_model m, uint16_t* host, size_t n) {
+    if (!m || !host) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
+    if (n != (size_t)m->vocab) return fail(TLHIP_ERR_SHAPE_MISMATCH, "logits has %d entries", m->vocab);
+    TLHIP_CHECK_HIP(hipMemcpyAsync(host, m->logits->data, n * 2, hipMemcpyDeviceToHost, m->ctx->stream));
+    TLHIP_CHECK_HIP(hipStreamSynchronize(m->ctx->stream));
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// measurement helpers
+// ---------------------------------------------------------------------------
+tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tensor* w, int n_w, tlhip_tensor y,
+                                int iters, float* avg_us) {
+    TLHIP_TRY(check_ctx(ctx));
+    if (!w || n_w <= 0 || iters <= 0 || !avg_us) return fail(TLHIP_ERR_INVALID_ARGUMENT, "bad bench arguments");
+    for (int i = 0; i < n_w; i++) TLHIP_TRY(tlhip_linear(ctx, x, w[i], nullptr, y));   // checks + warm-up
+    TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
+    Lin l;
+    TLHIP_CHECK_HIP(hipEventRecord(ctx->ev0, ctx->stream));
+    for (int i = 0; i < iters; i++) {
+        l.w = w[i % n_w];
+        TLHIP_TRY(linear_into(ctx->stream, l, P(x), (int)x->shape[0], P(y), EPI_STORE, nullptr));
+    }
+    TLHIP_CHECK_HIP(hipEventRecord(ctx->ev1, ctx->stream));
+    TLHIP_CHECK_HIP(hipEventSynchronize(ctx->ev1));
+    float ms = 0.f;
+    TLHIP_CHECK_HIP(hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
+    *avg_us = ms * 1000.0f / (float)iters;
+    return TLHIP_OK;
+}
+
+tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode, int32_t* tokens_out,
+                                float* prefill_ms, float* decode_ms) {
+    if (!m || !prompt || !tokens_out || !prefill_ms || !decode_ms)
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
+    if (n_prompt + n_decode > m->max_ctx)
+        return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "context overflow: %d + %d > %d", n_prompt, n_decode, m->max_ctx);
+    tlhip_ctx ctx = m->ctx;
+    TLHIP_TRY(ensure_graph(m));
+    m->pos = 0;
+    TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
+    TLHIP_CHECK_HIP(hipEventRecord(ctx->ev0, ctx->stream));
+    TLHIP_TRY(prefill(m, prompt, n_prompt, 0));
+    TLHIP_CHECK_HIP(hipEventRecord(ctx->ev1, ctx->stream));
+    TLHIP_CHECK_HIP(hipEventSynchronize(ctx->ev1));
+    TLHIP_CHECK_HIP(hipEventElapsedTime(prefill_ms, ctx->ev0, ctx->ev1));
+    TLHIP_CHECK_HIP(hipEventRecord(ctx->ev0, ctx->stream));
+    TLHIP_TRY(decode_steps(m, n_decode, true));
+    TLHIP_CHECK_HIP(hipEventRecord(ctx->ev1, ctx->stream));
+    TLHIP_CHECK_HIP(hipEventSynchronize(ctx->ev1));
+    TLHIP_CHECK_HIP(hipEventElapsedTime(decode_ms, ctx->ev0, ctx->ev1));
+    TLHIP_CHECK_HIP(hipMemcpy(tokens_out, m->d_tokens, sizeof(int32_t) * (n_decode + 1), hipMemcpyDeviceToHost));
+    return TLHIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,350 @@
+// ops.cpp -- C-ABI operator entry points: host-side shape/dtype checks
+// (the reference checks shapes in Rust before encoding, e.g. matmul.rs:
+// 249-280), then one or more stream-ordered launches.  Nothing is launched
+// when a check fails.
+#include <cmath>
+#include <cstring>
+
+#include "internal.hpp"
+
+using namespace tlhip;
+
+namespace {
+
+tlhip_status same_shape(tlhip_tensor a, tlhip_tensor b, const char* op) {
+    if (a->ndim != b->ndim || memcmp(a->shape, b->shape, sizeof(int64_t) * a->ndim) != 0)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "%s: shape %s vs %s", op, shape_str(a).c_str(),
+                    shape_str(b).c_str());
+    return TLHIP_OK;
+}
+
+tlhip_status f16_args(const char* op, std::initializer_list<tlhip_tensor> ts) {
+    for (tlhip_tensor t : ts) {
+        TLHIP_TRY(check_t(t, op));
+        TLHIP_TRY(check_dtype(t, TLHIP_F16, op));
+    }
+    return TLHIP_OK;
+}
+
+uint16_t* P(tlhip_tensor t) { return (uint16_t*)t->data; }
+
+float round_f16(float f) {
+    // scalar operands of f16 ops are f16 values (T::from_f32)
+    _Float16 h = (_Float16)f;
+    return (float)h;
+}
+
+}  // namespace
+
+extern "C" {
+
+tlhip_status tlhip_dequantize(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor out) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(check_t(q, "dequantize"));
+    TLHIP_TRY(f16_args("dequantize", {out}));
+    if (!is_quant(q->dtype)) return fail(TLHIP_ERR_DTYPE, "dequantize: input must be Q4_0 or Q8_0");
+    if (out->ndim != 2 || out->shape[0] != q->shape[0] || out->shape[1] != q->shape[1])
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "dequantize: %s -> %s", shape_str(q).c_str(), shape_str(out).c_str());
+    TLHIP_TRY(launch_dequant(ctx->stream, q->dtype, q->data, q->scales, P(out), q->shape[0], q->shape[1]));
+    return after_launch(ctx, "dequantize");
+}
+
+tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("linear", {x, y}));
+    TLHIP_TRY(check_t(w, "linear weight"));
+    if (w->dtype != TLHIP_F16 && !is_quant(w->dtype))
+        return fail(TLHIP_ERR_DTYPE, "linear: weight dtype %d unsupported", (int)w->dtype);
+    if (x->ndim != 2 || w->ndim != 2)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "matmul_transposed_b requires 2D tensors");
+    const int64_t M = x->shape[0], K = x->shape[1], N = w->shape[0];
+    if (w->shape[1] != K)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "matmul_transposed_b shape mismatch: [%lld, %lld] @ [%lld, %lld].T",
+                    (long long)M, (long long)K, (long long)N, (long long)w->shape[1]);
+    if (y->ndim != 2 || y->shape[0] != M || y->shape[1] != N)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "linear: output %s, expected [%lld, %lld]", shape_str(y).c_str(),
+                    (long long)M, (long long)N);
+    if (bias) {
+        TLHIP_TRY(f16_args("linear bias", {bias}));
+        if (numel(bias) != N) return fail(TLHIP_ERR_SHAPE_MISMATCH, "linear: bias %s for N=%lld", shape_str(bias).c_str(), (long long)N);
+    }
+    if (M == 0 || N == 0) return TLHIP_OK;
+    GemvArgs a;
+    a.x = P(x);
+    a.wq = w->data;
+    a.wd = w->scales;
+    a.bias = bias ? P(bias) : nullptr;
+    a.y = P(y);
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    const int epi = bias ? EPI_BIAS : EPI_STORE;
+    tlhip_status st = TLHIP_ERR_INVALID_OPERATION;
+    if (M <= 4) {
+        st = launch_gemv(ctx->stream, w->dtype, a, epi);
+        if (st != TLHIP_OK) (void)hipGetLastError();
+    }
+    if (st != TLHIP_OK) TLHIP_TRY(launch_gemm(ctx->stream, w->dtype, a, epi));
+    return after_launch(ctx, "linear");
+}
+
+tlhip_status tlhip_matmul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor c) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("matmul", {a, b, c}));
+    if (a->ndim != 2 || b->ndim != 2) return fail(TLHIP_ERR_INVALID_OPERATION, "matmul requires 2D tensors");
+    const int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+    if (b->shape[0] != K)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "matmul: [%lld, %lld] @ %s", (long long)M, (long long)K,
+                    shape_str(b).c_str());
+    if (c->ndim != 2 || c->shape[0] != M || c->shape[1] != N)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "matmul: output %s", shape_str(c).c_str());
+    if (M == 0 || N == 0) return TLHIP_OK;
+    // matmul(a, b) = matmul_transposed_b(a, b^T): one transpose kernel, then
+    // the same fp32-accumulating product as linear().
+    tlhip_tensor bt;
+    int64_t shp[2] = {N, K};
+    TLHIP_TRY(alloc_tensor(ctx, TLHIP_F16, 2, shp, &bt));
+    tlhip_status st = launch_transpose(ctx->stream, P(b), P(bt), (int)K, (int)N);
+    if (st == TLHIP_OK) st = tlhip_linear(ctx, a, bt, nullptr, c);
+    tlhip_tensor_free(bt);
+    return st;
+}
+
+tlhip_status tlhip_rms_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, float eps, tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("rms_norm", {x, w, y}));
+    TLHIP_TRY(same_shape(x, y, "rms_norm"));
+    const int64_t n = last_dim(x);
+    if (w->ndim != 1 || w->shape[0] != n)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "rms_norm: weight %s for normalized_shape [%lld]", shape_str(w).c_str(),
+                    (long long)n);
+    if (n == 0) return TLHIP_OK;
+    TLHIP_TRY(launch_rms_norm(ctx->stream, P(x), P(w), P(y), (int)(numel(x) / n), (int)n, eps));
+    return after_launch(ctx, "rms_norm");
+}
+
+tlhip_status tlhip_layer_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor b, float eps,
+                              tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("layer_norm", {x, y}));
+    TLHIP_TRY(same_shape(x, y, "layer_norm"));
+    const int64_t n = last_dim(x);
+    for (tlhip_tensor t : {w, b}) {
+        if (!t) continue;
+        TLHIP_TRY(f16_args("layer_norm", {t}));
+        if (t->ndim != 1 || t->shape[0] != n)
+            return fail(TLHIP_ERR_SHAPE_MISMATCH, "layer_norm: param %s for [%lld]", shape_str(t).c_str(), (long long)n);
+    }
+    if (n == 0) return TLHIP_OK;
+    TLHIP_TRY(launch_layer_norm(ctx->stream, P(x), w ? P(w) : nullptr, b ? P(b) : nullptr, P(y),
+                                (int)(numel(x) / n), (int)n, eps));
+    return after_launch(ctx, "layer_norm");
+}
+
+tlhip_status tlhip_rope(tlhip_ctx ctx, tlhip_tensor x, int offset, float theta, tlhip_rope_layout layout,
+                        int rot_dims, tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("rope", {x, y}));
+    TLHIP_TRY(same_shape(x, y, "rope"));
+    if (x->ndim < 3) return fail(TLHIP_ERR_INVALID_OPERATION, "RoPE requires at least 3D tensor (got %dD)", x->ndim);
+    const int64_t D = x->shape[x->ndim - 1], H = x->shape[x->ndim - 2], S = x->shape[x->ndim - 3];
+    if (rot_dims <= 0) rot_dims = (int)D;
+    if (D % 2 != 0 || rot_dims % 2 != 0 || rot_dims > D)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "RoPE requires even head_dim (got %lld, rot %d)", (long long)D, rot_dims);
+    if (offset < 0) return fail(TLHIP_ERR_INVALID_ARGUMENT, "negative RoPE offset");
+    if (layout != TLHIP_ROPE_INTERLEAVED && layout != TLHIP_ROPE_NEOX)
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "bad RoPE layout %d", (int)layout);
+    if (numel(x) == 0) return TLHIP_OK;
+    const float* table;
+    TLHIP_TRY(rope_table(ctx, theta, rot_dims, offset + (int)S, &table));
+    TLHIP_TRY(launch_rope(ctx->stream, P(x), P(y), (int)S, (int)H, (int)D, numel(x) / (S * H * D), offset, nullptr,
+                          (int)layout, rot_dims, table, 0, 0));
+    return after_launch(ctx, "rope");
+}
+
+tlhip_status tlhip_softmax_lastdim(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("softmax", {x, y}));
+    TLHIP_TRY(same_shape(x, y, "softmax"));
+    if (x->ndim == 0) return fail(TLHIP_ERR_INVALID_OPERATION, "softmax requires non-empty tensor");
+    const int64_t n = last_dim(x);
+    if (n == 0 || numel(x) == 0) return TLHIP_OK;
+    TLHIP_TRY(launch_softmax(ctx->stream, P(x), P(y), numel(x) / n, (int)n));
+    return after_launch(ctx, "softmax");
+}
+
+static tlhip_status unary(tlhip_ctx ctx, int op, tlhip_tensor x, tlhip_tensor y, const char* nm) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args(nm, {x, y}));
+    TLHIP_TRY(same_shape(x, y, nm));
+    TLHIP_TRY(launch_elementwise(ctx->stream, op, P(x), nullptr, P(y), numel(x), 0, 0.f));
+    return after_launch(ctx, nm);
+}
+
+tlhip_status tlhip_sigmoid(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) { return unary(ctx, EW_SIGMOID, x, y, "sigmoid"); }
+tlhip_status tlhip_silu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) { return unary(ctx, EW_SILU, x, y, "silu"); }
+tlhip_status tlhip_gelu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) { return unary(ctx, EW_GELU, x, y, "gelu"); }
+
+tlhip_status tlhip_silu_mul(tlhip_ctx ctx, tlhip_tensor g, tlhip_tensor u, tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("silu_mul", {g, u, y}));
+    TLHIP_TRY(same_shape(g, u, "silu_mul"));
+    TLHIP_TRY(same_shape(g, y, "silu_mul"));
+    TLHIP_TRY(launch_elementwise(ctx->stream, EW_SILU_MUL, P(g), P(u), P(y), numel(g), 0, 0.f));
+    return after_launch(ctx, "silu_mul");
+}
+
+static tlhip_status binary(tlhip_ctx ctx, int op, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y, const char* nm) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args(nm, {a, b, y}));
+    TLHIP_TRY(same_shape(a, y, nm));
+    int64_t period = 0;
+    if (numel(b) != numel(a)) {
+        // row broadcast: b matches a's last dim (bias-style add)
+        if (b->ndim == 1 && b->shape[0] == last_dim(a)) period = b->shape[0];
+        else return fail(TLHIP_ERR_SHAPE_MISMATCH, "%s: %s vs %s", nm, shape_str(a).c_str(), shape_str(b).c_str());
+    } else {
+        TLHIP_TRY(same_shape(a, b, nm));
+    }
+    TLHIP_TRY(launch_elementwise(ctx->stream, op, P(a), P(b), P(y), numel(a), period, 0.f));
+    return after_launch(ctx, nm);
+}
+
+tlhip_status tlhip_add(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y) { return binary(ctx, EW_ADD, a, b, y, "add"); }
+tlhip_status tlhip_mul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y) { return binary(ctx, EW_MUL, a, b, y, "mul"); }
+
+tlhip_status tlhip_mul_scalar(tlhip_ctx ctx, tlhip_tensor a, float s, tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("mul_scalar", {a, y}));
+    TLHIP_TRY(same_shape(a, y, "mul_scalar"));
+    TLHIP_TRY(launch_elementwise(ctx->stream, EW_MUL_SCALAR, P(a), nullptr, P(y), numel(a), 0, round_f16(s)));
+    return after_launch(ctx, "mul_scalar");
+}
+
+tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* ids, int n, tlhip_tensor out) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(check_t(table, "embedding table"));
+    TLHIP_TRY(f16_args("embedding", {out}));
+    if (table->ndim != 2) return fail(TLHIP_ERR_INVALID_DIMENSION, "embedding table must be 2-D");
+    const int64_t V = table->shape[0], Hd = table->shape[1];
+    if (n < 0 || (n > 0 && !ids)) return fail(TLHIP_ERR_INVALID_ARGUMENT, "embedding: bad ids");
+    if (out->ndim != 2 || out->shape[0] != n || out->shape[1] != Hd)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "embedding: output %s, expected [%d, %lld]", shape_str(out).c_str(), n,
+                    (long long)Hd);
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= V)
+            return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "token id %d out of range [0, %lld)", ids[i], (long long)V);
+    if (n == 0) return TLHIP_OK;
+    int32_t* d_ids = nullptr;
+    TLHIP_CHECK_HIP(hipMallocAsync(&d_ids, sizeof(int32_t) * n, ctx->stream));
+    TLHIP_CHECK_HIP(hipMemcpyAsync(d_ids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, ctx->stream));
+    tlhip_status st = launch_embedding(ctx->stream, table->dtype, table->data, table->scales, d_ids, nullptr, P(out),
+                                       n, (int)Hd);
+    (void)hipFreeAsync(d_ids, ctx->stream);
+    // the host ids buffer must stay valid until the copy ran
+    TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
+    TLHIP_TRY(st);
+    return after_launch(ctx, "embedding");
+}
+
+tlhip_status tlhip_apply_attention_mask(tlhip_ctx ctx, tlhip_tensor sc, tlhip_tensor mask, tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("apply_attention_mask", {sc, mask, y}));
+    TLHIP_TRY(same_shape(sc, y, "apply_attention_mask"));
+    int64_t period;
+    if (numel(mask) == numel(sc)) period = numel(sc);
+    else if (sc->ndim == 3 && mask->ndim == 2 && mask->shape[0] == sc->shape[0] && mask->shape[1] == sc->shape[2] &&
+             sc->shape[2] < 32768 && sc->shape[1] < 65536)
+        period = -(sc->shape[2] * 65536 + sc->shape[1]);
+    else
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "apply_attention_mask: scores %s, mask %s", shape_str(sc).c_str(),
+                    shape_str(mask).c_str());
+    TLHIP_TRY(launch_mask(ctx->stream, P(sc), P(mask), P(y), numel(sc), period));
+    return after_launch(ctx, "apply_attention_mask");
+}
+
+static tlhip_status qkv_dims(tlhip_tensor q, tlhip_tensor k, const char* nm, int* H, int* Hkv, int* D) {
+    if (q->ndim != 3 || k->ndim != 3) return fail(TLHIP_ERR_INVALID_DIMENSION, "%s: expects 3-D tensors", nm);
+    *H = (int)q->shape[1];
+    *Hkv = (int)k->shape[1];
+    *D = (int)k->shape[2];
+    if (*Hkv <= 0 || *H % *Hkv) return fail(TLHIP_ERR_SHAPE_MISMATCH, "%s: %d heads vs %d KV heads", nm, *H, *Hkv);
+    return TLHIP_OK;
+}
+
+tlhip_status tlhip_einsum_scores(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhip_tensor sc) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("einsum ihd,jhd->ihj", {q, k, sc}));
+    int H, Hkv, D;
+    TLHIP_TRY(qkv_dims(q, k, "einsum ihd,jhd->ihj", &H, &Hkv, &D));
+    const int I = (int)q->shape[0], J = (int)k->shape[0];
+    if (q->shape[2] != D) return fail(TLHIP_ERR_SHAPE_MISMATCH, "einsum: head_dim mismatch");
+    if (sc->ndim != 3 || sc->shape[0] != I || sc->shape[1] != H || sc->shape[2] != J)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "einsum: output %s", shape_str(sc).c_str());
+    TLHIP_TRY(launch_scores(ctx->stream, P(q), P(k), P(sc), I, J, H, Hkv, D));
+    return after_launch(ctx, "einsum_scores");
+}
+
+tlhip_status tlhip_einsum_context(tlhip_ctx ctx, tlhip_tensor p, tlhip_tensor v, tlhip_tensor out) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("einsum ihj,jhd->ihd", {p, v, out}));
+    if (p->ndim != 3 || v->ndim != 3 || out->ndim != 3)
+        return fail(TLHIP_ERR_INVALID_DIMENSION, "einsum ihj,jhd->ihd expects 3-D tensors");
+    const int I = (int)p->shape[0], H = (int)p->shape[1], J = (int)p->shape[2];
+    const int Hkv = (int)v->shape[1], D = (int)v->shape[2];
+    if (v->shape[0] != J || Hkv <= 0 || H % Hkv)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "einsum: P %s, V %s", shape_str(p).c_str(), shape_str(v).c_str());
+    if (out->shape[0] != I || out->shape[1] != H || out->shape[2] != D)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "einsum: output %s", shape_str(out).c_str());
+    TLHIP_TRY(launch_context(ctx->stream, P(p), P(v), P(out), I, J, H, Hkv, D));
+    return after_launch(ctx, "einsum_context");
+}
+
+tlhip_status tlhip_attention(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhip_tensor v, int q_pos0, float scale,
+                             int causal, tlhip_tensor out) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("attention", {q, k, v, out}));
+    int H, Hkv, D;
+    TLHIP_TRY(qkv_dims(q, k, "attention", &H, &Hkv, &D));
+    TLHIP_TRY(same_shape(k, v, "attention k/v"));
+    TLHIP_TRY(same_shape(q, out, "attention q/out"));
+    if (q->shape[2] != D) return fail(TLHIP_ERR_SHAPE_MISMATCH, "attention: head_dim mismatch");
+    if (q_pos0 < 0) return fail(TLHIP_ERR_INVALID_ARGUMENT, "attention: negative q_pos0");
+    const int S = (int)q->shape[0], J = (int)k->shape[0];
+    if (J > kAttnMaxKeys) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: %d keys > %d", J, kAttnMaxKeys);
+    if (causal && q_pos0 + S > J)
+        return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: query positions up to %d but only %d keys", q_pos0 + S, J);
+    AttnArgs a;
+    a.q = P(q);
+    a.k = P(k);
+    a.v = P(v);
+    a.out = P(out);
+    a.S = S;
+    a.H = H;
+    a.Hkv = Hkv;
+    a.D = D;
+    a.q_pos0 = q_pos0;
+    a.causal = causal;
+    a.scale_h = round_f16(scale);
+    TLHIP_TRY(launch_attention_j(ctx->stream, a, J));
+    return after_launch(ctx, "attention");
+}
+
+tlhip_status tlhip_argmax(tlhip_ctx ctx, tlhip_tensor logits, int32_t* out) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("argmax", {logits}));
+    if (!out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null output");
+    if (logits->ndim != 1 && logits->ndim != 2)
+        return fail(TLHIP_ERR_INVALID_DIMENSION, "temperature_sample() expects 1D or 2D logits tensor");
+    const int64_t V = last_dim(logits);
+    const int64_t rows = numel(logits) / (V ? V : 1);
+    if (V == 0 || rows == 0) return fail(TLHIP_ERR_INVALID_DIMENSION, "argmax of an empty tensor");
+    const uint16_t* last = P(logits) + (size_t)(rows - 1) * V;
+    TLHIP_TRY(launch_argmax(ctx->stream, last, (int)V, ctx->d_scratch_i32, nullptr, nullptr));
+    TLHIP_CHECK_HIP(hipMemcpyAsync(ctx->h_pinned_i32, ctx->d_scratch_i32, 4, hipMemcpyDeviceToHost, ctx->stream));
+    TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
+    *out = ctx->h_pinned_i32[0];
+    return TLHIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,398 @@
+"""Host-side mirror of the reference's tensor operator surface over the C ABI.
+
+Names and argument meaning follow the reference's `Tensor<f16>` methods and TL
+builtins (`src/ops/*.rs`, `src/interpreter/builtin_*.rs`): `matmul_transposed_b`
+/ `linear`, `rms_norm(normalized_shape, weight, eps)`, `rope(position_offset)`,
+`softmax()`, `sigmoid()`, `embedding(table, ids)`, `KVCache.set/append/get_k/
+get_v`, `temperature_sample(logits, 0)`.  Errors surface as TLHipError with
+the reference's TensorError kind (ShapeMismatch, InvalidOperation, ...).
+
+Every operation runs on the device through libtlhip.so; nothing here computes
+on the host.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import F16, Q4_0, Q8_0, ROPE_INTERLEAVED, ROPE_NEOX, TLHipError, call, lib
+
+_vp = C.c_void_p
+_BLOCK_BYTES = {Q4_0: 18, Q8_0: 34}
+
+
+def _shape_arr(shape):
+    return (C.c_int64 * len(shape))(*[int(s) for s in shape])
+
+
+class Device:
+    """One device context: a HIP device plus one stream (MetalDevice::new)."""
+
+    def __init__(self, index: int = 0):
+        h = _vp()
+        call("tlhip_init", index, C.byref(h))
+        self.h = h
+
+    def sync(self):
+        call("tlhip_sync", self.h)
+
+    def name(self) -> str:
+        buf = C.create_string_buffer(256)
+        call("tlhip_device_name", self.h, buf, 256)
+        return buf.value.decode()
+
+    def set_sync_every_op(self, on: bool):
+        call("tlhip_set_sync_every_op", self.h, int(on))
+
+    def close(self):
+        if self.h:
+            lib().tlhip_shutdown(self.h)
+            self.h = None
+
+    # -- tensor creation ----------------------------------------------------
+    def empty(self, shape, dtype: int = F16) -> "Tensor":
+        h = _vp()
+        call("tlhip_tensor_alloc", self.h, dtype, len(shape), _shape_arr(shape), C.byref(h))
+        return Tensor(self, h)
+
+    def tensor(self, arr) -> "Tensor":
+        """Tensor::from_vec_gpu: upload an f16 array (float arrays are rounded RNE)."""
+        a = np.ascontiguousarray(arr, dtype=np.float16)
+        t = self.empty(a.shape if a.ndim else (1,))
+        call("tlhip_tensor_upload", self.h, t.h, a.ctypes.data_as(_vp), a.nbytes)
+        return t
+
+    def quantized(self, blocks: np.ndarray, shape, qtype: int) -> "Tensor":
+        """A packed Q4_0 / Q8_0 weight [N, K] from GGUF block bytes."""
+        b = np.ascontiguousarray(blocks, dtype=np.uint8)
+        t = self.empty(shape, qtype)
+        call("tlhip_tensor_upload", self.h, t.h, b.ctypes.data_as(_vp), b.nbytes)
+        return t
+
+
+class Tensor:
+    def __init__(self, dev: Device, h):
+        self.dev = dev
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            try:
+                lib().tlhip_tensor_free(self.h)
+            except Exception:
+                pass
+            self.h = None
+
+    # -- metadata -------------------------------------------------------------
+    def _info(self):
+        dt, nd = C.c_int(), C.c_int()
+        shp = (C.c_int64 * 8)()
+        call("tlhip_tensor_info", self.h, C.byref(dt), C.byref(nd), shp)
+        return dt.value, tuple(shp[i] for i in range(nd.value))
+
+    @property
+    def shape(self):
+        return self._info()[1]
+
+    @property
+    def dtype(self):
+        return self._info()[0]
+
+    def numel(self):
+        return int(np.prod(self.shape))
+
+    def nbytes(self):
+        return int(lib().tlhip_tensor_nbytes(self.h))
+
+    # -- transfer ---------------------------------------------------------------
+    def numpy(self) -> np.ndarray:
+        """sync_and_read: f16 array, or GGUF block bytes for Q types."""
+        dt, shape = self._info()
+        if dt in _BLOCK_BYTES:
+            out = np.empty(self.nbytes(), np.uint8)
+        else:
+            out = np.empty(shape, np.float16)
+        call("tlhip_tensor_download", self.dev.h, self.h, out.ctypes.data_as(_vp), out.nbytes)
+        return out
+
+    def reshape(self, shape) -> "Tensor":
+        h = _vp()
+        call("tlhip_tensor_reshape", self.h, len(shape), _shape_arr(shape), C.byref(h))
+        return Tensor(self.dev, h)
+
+    # -- ops --------------------------------------------------------------------
+    def _new(self, shape):
+        return self.dev.empty(shape)
+
+    def dequantize(self) -> "Tensor":
+        out = self._new(self.shape)
+        call("tlhip_dequantize", self.dev.h, self.h, out.h)
+        return out
+
+    def matmul_transposed_b(self, w: "Tensor") -> "Tensor":
+        """self[M,K] @ w[N,K]^T (matmul.rs:241-311)."""
+        return self.linear(w)
+
+    def linear(self, w: "Tensor", bias: "Tensor | None" = None) -> "Tensor":
+        M = self.shape[0] if len(self.shape) == 2 else -1
+        N = w.shape[0]
+        out = self._new((max(M, 0), N)) if M >= 0 else self._new((1, N))
+        call("tlhip_linear", self.dev.h, self.h, w.h, bias.h if bias is not None else None, out.h)
+        return out
+
+    def matmul(self, b: "Tensor") -> "Tensor":
+        out = self._new((self.shape[0], b.shape[1]))
+        call("tlhip_matmul", self.dev.h, self.h, b.h, out.h)
+        return out
+
+    def rms_norm(self, normalized_shape: Sequence[int], weight: "Tensor", eps: float = 1e-6) -> "Tensor":
+        """Tensor::rms_norm (normalization.rs:42-89): normalized_shape must be
+        the trailing dims and match the weight's shape."""
+        dims = list(self.shape)
+        ns = list(normalized_shape)
+        if len(ns) > len(dims) or dims[len(dims) - len(ns):] != ns:
+            raise TLHipError(3, f"normalized_shape {ns} does not match tensor shape {dims}")
+        if list(weight.shape) != ns:
+            raise TLHipError(1, f"expected {ns}, got {list(weight.shape)}")
+        if len(ns) != 1:
+            x = self.reshape((self.numel() // int(np.prod(ns)), int(np.prod(ns))))
+            w = weight.reshape((int(np.prod(ns)),))
+            return x.rms_norm([int(np.prod(ns))], w, eps).reshape(self.shape)
+        out = self._new(self.shape)
+        call("tlhip_rms_norm", self.dev.h, self.h, weight.h, float(eps), out.h)
+        return out
+
+    def layer_norm(self, weight=None, bias=None, eps: float = 1e-5) -> "Tensor":
+        out = self._new(self.shape)
+        call("tlhip_layer_norm", self.dev.h, self.h, weight.h if weight is not None else None,
+             bias.h if bias is not None else None, float(eps), out.h)
+        return out
+
+    def rope(self, position_offset: int = 0, theta: float = 10000.0, layout: int = ROPE_INTERLEAVED,
+             rot_dims: int = 0) -> "Tensor":
+        """Tensor::rope (rope.rs:71-118); layout/theta/rot_dims extend it."""
+        out = self._new(self.shape)
+        call("tlhip_rope", self.dev.h, self.h, int(position_offset), float(theta), int(layout),
+             int(rot_dims), out.h)
+        return out
+
+    def softmax(self) -> "Tensor":
+        out = self._new(self.shape)
+        call("tlhip_softmax_lastdim", self.dev.h, self.h, out.h)
+        return out
+
+    def _unary(self, fn):
+        out = self._new(self.shape)
+        call(fn, self.dev.h, self.h, out.h)
+        return out
+
+    def sigmoid(self):
+        return self._unary("tlhip_sigmoid")
+
+    def silu(self):
+        return self._unary("tlhip_silu")
+
+    def gelu(self):
+        return self._unary("tlhip_gelu")
+
+    def silu_mul(self, up: "Tensor") -> "Tensor":
+        out = self._new(self.shape)
+        call("tlhip_silu_mul", self.dev.h, self.h, up.h, out.h)
+        return out
+
+    def add(self, other: "Tensor") -> "Tensor":
+        out = self._new(self.shape)
+        call("tlhip_add", self.dev.h, self.h, other.h, out.h)
+        return out
+
+    def mul(self, other: "Tensor") -> "Tensor":
+        out = self._new(self.shape)
+        call("tlhip_mul", self.dev.h, self.h, other.h, out.h)
+        return out
+
+    def mul_scalar(self, s: float) -> "Tensor":
+        out = self._new(self.shape)
+        call("tlhip_mul_scalar", self.dev.h, self.h, float(s), out.h)
+        return out
+
+    __add__ = add
+
+    def __mul__(self, other):
+        return self.mul_scalar(other) if isinstance(other, (int, float)) else self.mul(other)
+
+    def apply_attention_mask(self, mask: "Tensor") -> "Tensor":
+        out = self._new(self.shape)
+        call("tlhip_apply_attention_mask", self.dev.h, self.h, mask.h, out.h)
+        return out
+
+    def argmax_last(self) -> int:
+        r = C.c_int32()
+        call("tlhip_argmax", self.dev.h, self.h, C.byref(r))
+        return r.value
+
+
+def einsum(eq: str, a: Tensor, b: Tensor) -> Tensor:
+    """The two attention einsums the TL programs use (einsum.rs:653-886)."""
+    eq = eq.replace(" ", "")
+    if eq == "ihd,jhd->ihj":
+        out = a.dev.empty((a.shape[0], a.shape[1], b.shape[0]))
+        call("tlhip_einsum_scores", a.dev.h, a.h, b.h, out.h)
+        return out
+    if eq == "ihj,jhd->ihd":
+        out = a.dev.empty((a.shape[0], a.shape[1], b.shape[2]))
+        call("tlhip_einsum_context", a.dev.h, a.h, b.h, out.h)
+        return out
+    raise TLHipError(3, f"einsum pattern {eq} not supported")
+
+
+def attention(q: Tensor, k: Tensor, v: Tensor, q_pos0: int = 0, scale: float | None = None,
+              causal: bool = True) -> Tensor:
+    if scale is None:
+        scale = 1.0 / np.sqrt(q.shape[2])
+    out = q.dev.empty(q.shape)
+    call("tlhip_attention", q.dev.h, q.h, k.h, v.h, int(q_pos0), float(scale), int(causal), out.h)
+    return out
+
+
+def embedding(table: Tensor, ids) -> Tensor:
+    ids = np.ascontiguousarray(np.atleast_1d(ids), dtype=np.int32)
+    out = table.dev.empty((ids.size, table.shape[1]))
+    call("tlhip_embedding", table.dev.h, table.h, ids.ctypes.data_as(C.POINTER(C.c_int32)), ids.size, out.h)
+    return out
+
+
+def temperature_sample(logits: Tensor, temperature: float) -> int:
+    """Greedy branch of temperature_sample (builtin_sampling.rs:170-176)."""
+    if temperature > 1e-4:
+        raise TLHipError(3, "only greedy sampling (temperature <= 1e-4) runs on the device")
+    return logits.argmax_last()
+
+
+class KVCache:
+    """KVCache::new_f16 with a preallocated device buffer per layer."""
+
+    def __init__(self, dev: Device, n_layers: int, max_ctx: int, n_kv_heads: int, head_dim: int):
+        self.dev = dev
+        h = _vp()
+        call("tlhip_kvcache_create", dev.h, n_layers, max_ctx, n_kv_heads, head_dim, C.byref(h))
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().tlhip_kvcache_free(self.h)
+            self.h = None
+
+    def set(self, layer: int, k: Tensor, v: Tensor):
+        call("tlhip_kvcache_set", self.dev.h, self.h, layer, k.h, v.h)
+
+    def append(self, layer: int, k: Tensor, v: Tensor):
+        call("tlhip_kvcache_append", self.dev.h, self.h, layer, k.h, v.h)
+
+    def _get(self, layer, which):
+        h = _vp()
+        call("tlhip_kvcache_get", self.h, layer, which, C.byref(h))
+        return Tensor(self.dev, h)
+
+    def get_k(self, layer: int) -> Tensor:
+        return self._get(layer, 0)
+
+    def get_v(self, layer: int) -> Tensor:
+        return self._get(layer, 1)
+
+    def len(self, layer: int) -> int:
+        return lib().tlhip_kvcache_len(self.h, layer)
+
+
+class GGUF:
+    def __init__(self, path: str):
+        h = _vp()
+        call("tlhip_gguf_open", path.encode(), C.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().tlhip_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def names(self):
+        n = lib().tlhip_gguf_n_tensors(self.h)
+        return [lib().tlhip_gguf_tensor_name(self.h, i).decode() for i in range(n)]
+
+    def load_tensor(self, dev: Device, name: str) -> Tensor:
+        h = _vp()
+        call("tlhip_gguf_load_tensor", dev.h, self.h, name.encode(), C.byref(h))
+        return Tensor(dev, h)
+
+    def kv_u32(self, key: str) -> int:
+        v = C.c_uint32()
+        call("tlhip_gguf_kv_u32", self.h, key.encode(), C.byref(v))
+        return v.value
+
+
+class Model:
+    """The decoder runner (tlhip_model_*): arch 0 = llama, 1 = phi2."""
+
+    def __init__(self, dev: Device, path: str, arch: int = 0, max_ctx: int = 1024):
+        self.dev = dev
+        h = _vp()
+        call("tlhip_model_load", dev.h, path.encode(), arch, max_ctx, C.byref(h))
+        self.h = h
+        d = (C.c_int32 * 8)()
+        call("tlhip_model_dims", h, d)
+        (self.n_layers, self.hidden, self.inter, self.n_heads, self.n_kv, self.head_dim, self.vocab,
+         self.rot) = list(d)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().tlhip_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def reset(self):
+        call("tlhip_model_reset", self.h)
+
+    def prefill(self, ids) -> int:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        r = C.c_int32()
+        call("tlhip_model_prefill", self.h, ids.ctypes.data_as(C.POINTER(C.c_int32)), ids.size, C.byref(r))
+        return r.value
+
+    def decode(self, token: int) -> int:
+        r = C.c_int32()
+        call("tlhip_model_decode", self.h, int(token), C.byref(r))
+        return r.value
+
+    def generate(self, prompt, n_decode: int, use_graph: bool = True) -> np.ndarray:
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(n_decode + 1, np.int32)
+        call("tlhip_model_generate", self.h, prompt.ctypes.data_as(C.POINTER(C.c_int32)), prompt.size, n_decode,
+             int(use_graph), out.ctypes.data_as(C.POINTER(C.c_int32)))
+        return out
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.vocab, np.uint16)
+        call("tlhip_model_logits", self.h, out.ctypes.data_as(C.POINTER(C.c_uint16)), out.size)
+        return out.view(np.float16)
+
+    def bench_decode(self, prompt, n_decode: int):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        out = np.empty(n_decode + 1, np.int32)
+        pm, dm = C.c_float(), C.c_float()
+        call("tlhip_bench_decode", self.h, prompt.ctypes.data_as(C.POINTER(C.c_int32)), prompt.size, n_decode,
+             out.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(pm), C.byref(dm))
+        return out, pm.value, dm.value
+
+
+def bench_linear(dev: Device, x: Tensor, ws: Sequence[Tensor], y: Tensor, iters: int) -> float:
+    arr = (_vp * len(ws))(*[w.h for w in ws])
+    us = C.c_float()
+    call("tlhip_bench_linear", dev.h, x.h, arr, len(ws), y.h, iters, C.byref(us))
+    return us.value

@@ -1,0 +1,80 @@
+"""Writes the golden fixtures of tests/golden/ by running the CPU oracle.
+
+    python tests/golden/gen_golden.py [--only NAME]
+
+tinyllama_q4_0_tokens.json -- config 4: the TinyLlama-1.1B-shape Q4_0 model
+    of tensorlogic_amd.synth.write_llama_gguf(seed=4), 46-token prompt
+    token_ids(4, "prompt", 46, 32000), 128 greedy decode steps: the 129
+    oracle tokens, the top1-top2 logit margin of each step and the final
+    logits (f16 values).  The GPU test regenerates the same file from the
+    seed and compares.
+synth_checksums.json -- sha256 of fixed generator draws, pinning the seeded
+    generator across machines.
+"""
+from __future__ import annotations
+
+import argparse
+import hashlib
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from oracle import oracle as O  # noqa: E402
+from tensorlogic_amd import synth as S  # noqa: E402
+
+
+def synth_checksums():
+    draws = {
+        "q4_0_blocks(1,'W',64,256)": S.q4_0_blocks(1, "W", 64, 256).tobytes(),
+        "q8_0_blocks(1,'W',64,256)": S.q8_0_blocks(1, "W", 64, 256).tobytes(),
+        "normal_f16(1,'x',(4,2048))": S.normal_f16(1, "x", (4, 2048)).tobytes(),
+        "token_ids(4,'prompt',46,32000)": S.token_ids(4, "prompt", 46, 32000).tobytes(),
+    }
+    return {k: hashlib.sha256(v).hexdigest() for k, v in draws.items()}
+
+
+def tinyllama_tokens(n_decode=128, seed=4):
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "tinyllama.gguf")
+        S.write_llama_gguf(path, seed=seed, **S.TINYLLAMA_ARGS)
+        prompt = S.token_ids(seed, "prompt", 46, S.TINYLLAMA_ARGS["vocab"])
+        t0 = time.time()
+        m = O.Model(path, arch=0, max_ctx=256)
+        toks, margins, logits = m.generate(prompt, n_decode)
+        m.close()
+        print(f"oracle: {time.time() - t0:.1f} s", file=sys.stderr)
+    return {
+        "config": "TinyLlama-1.1B shape, Q4_0 linear weights, seed 4",
+        "seed": seed,
+        "prompt": prompt.tolist(),
+        "n_decode": n_decode,
+        "tokens": toks.tolist(),
+        "margins": [float(x) for x in margins],
+        "last_logits": [float(x) for x in logits.astype(np.float32)],
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--only", default="")
+    a = ap.parse_args()
+    jobs = {"synth_checksums.json": synth_checksums,
+            "tinyllama_q4_0_tokens.json": tinyllama_tokens}
+    for name, fn in jobs.items():
+        if a.only and a.only != name:
+            continue
+        with open(os.path.join(HERE, name), "w") as f:
+            json.dump(fn(), f)
+        print(f"wrote {name}", file=sys.stderr)
+
+
+if __name__ == "__main__":
+    main()

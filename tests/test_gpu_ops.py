@@ -1,0 +1,277 @@
+"""Operator parity: libtlhip.so on the device vs the CPU oracle, same seeded inputs.
+
+Bars (north star): dequantised weights and pure data movement bit-exact;
+matmul / layer outputs within max-abs 2e-2 and relative L2 1e-3 of the
+fp32-accumulated oracle (the oracle stores f16 exactly where the reference
+does).  Elementwise ops that evaluate exp/tanh are held to 1 f16 ulp.
+"""
+import numpy as np
+import pytest
+
+from tensorlogic_amd import F16, Q4_0, Q8_0, ROPE_INTERLEAVED, ROPE_NEOX, TLHipError
+from tensorlogic_amd import synth as S
+from tensorlogic_amd.tensor import KVCache, attention, einsum, embedding, temperature_sample
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+REL_L2 = 1e-3
+
+
+def f16_ulp(x):
+    """Spacing of f16 values at |x| (2^-24 in the subnormal range)."""
+    a = np.abs(np.asarray(x, np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def assert_close(got, ref, max_abs=MAX_ABS, rel_l2=REL_L2, what=""):
+    """max-abs <= 2e-2 (or one f16 ulp of the reference value where that is
+    coarser: an f16 output cannot be closer than its own spacing, and fp32
+    sums in another order flip the last f16 bit now and then) and rel-L2 <= 1e-3."""
+    g = np.asarray(got, np.float64).ravel()
+    r = np.asarray(ref, np.float64).ravel()
+    assert g.shape == r.shape, what
+    assert np.all(np.isfinite(g)) or not np.all(np.isfinite(r)), f"{what}: non-finite output"
+    d = np.abs(g - r)
+    ma = float(d.max()) if d.size else 0.0
+    rl = float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30)) if d.size else 0.0
+    bound = np.maximum(max_abs, f16_ulp(r))
+    bad = np.nonzero(d > bound)[0]
+    assert bad.size == 0 and rl <= rel_l2, (f"{what}: max_abs {ma:.3e} rel_l2 {rl:.3e}; "
+                                           f"{bad.size} elements beyond max(2e-2, 1 ulp)")
+    return ma, rl
+
+
+def ulp_diff(a, b):
+    ai = np.asarray(a, np.float16).view(np.int16).astype(np.int32)
+    bi = np.asarray(b, np.float16).view(np.int16).astype(np.int32)
+    ai = np.where(ai < 0, -32768 - ai, ai)
+    bi = np.where(bi < 0, -32768 - bi, bi)
+    return np.abs(ai - bi)
+
+
+# ---------------------------------------------------------------------------
+# dequantisation (bit-exact)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("qt,gen,shape", [(Q4_0, S.q4_0_blocks, (2048, 2048)),
+                                          (Q8_0, S.q8_0_blocks, (256, 5632)),
+                                          (Q4_0, S.q4_0_blocks, (3, 32))])
+def test_dequant_bit_exact(dev, oracle, qt, gen, shape):
+    blocks = gen(1, "W", *shape)
+    w = dev.quantized(blocks, shape, qt)
+    assert np.array_equal(w.numpy(), blocks), "packed round trip"
+    got = w.dequantize().numpy().view(np.uint16)
+    ref = oracle.dequant(blocks, 2 if qt == Q4_0 else 8).view(np.uint16).reshape(shape)
+    assert np.array_equal(got, ref)
+
+
+def test_dequant_reference_known_answers(dev):
+    # gguf.rs:622-718: Q8_0 scale 1 -> 0,1,2; two blocks scale 1/2 -> y[42] = 20;
+    # Q4_0 scale 0.5, all nibbles 0xF -> 3.5 everywhere.
+    q8 = np.zeros(68, np.uint8)
+    q8[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    q8[2:34] = np.arange(32)
+    q8[34:36] = np.frombuffer(np.float16(2.0).tobytes(), np.uint8)
+    q8[36:68] = np.arange(32)
+    y = dev.quantized(q8, (1, 64), Q8_0).dequantize().numpy().astype(np.float32).ravel()
+    assert y[0] == 0 and y[1] == 1 and y[2] == 2 and y[10] == 10 and y[32] == 0 and y[42] == 20
+    q4 = np.full(18, 0xFF, np.uint8)
+    q4[0:2] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    y = dev.quantized(q4, (1, 32), Q4_0).dequantize().numpy().astype(np.float32)
+    assert np.all(y == 3.5)
+
+
+# ---------------------------------------------------------------------------
+# linear: GEMV (M <= 4) and MFMA GEMM (M > 4)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("qt", [Q4_0, Q8_0])
+@pytest.mark.parametrize("M,N,K", [(1, 2048, 2048), (1, 5632, 2048), (1, 2048, 5632), (2, 256, 2048),
+                                   (3, 512, 1024), (4, 1000, 2048), (1, 37, 64), (1, 2560, 10240)])
+def test_linear_quant_gemv(dev, oracle, qt, M, N, K):
+    gen = S.q4_0_blocks if qt == Q4_0 else S.q8_0_blocks
+    blocks = gen(2, f"W{N}x{K}", N, K)
+    x = S.normal_f16(2, f"x{M}x{K}", (M, K))
+    w = dev.quantized(blocks, (N, K), qt)
+    y = dev.tensor(x).linear(w).numpy()
+    ref = oracle.linear_q(x, blocks, 2 if qt == Q4_0 else 8, N)
+    assert_close(y, ref, what=f"gemv {qt} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("qt", [Q4_0, Q8_0, F16])
+@pytest.mark.parametrize("M,N,K", [(46, 5632, 2048), (5, 64, 64), (64, 256, 512), (130, 96, 2048),
+                                   (512, 512, 2048)])
+def test_linear_gemm(dev, oracle, qt, M, N, K):
+    x = S.normal_f16(3, f"x{M}x{K}", (M, K))
+    if qt == F16:
+        wh = S.normal_f16(3, f"W{N}x{K}", (N, K), 0.0, 0.05)
+        w = dev.tensor(wh)
+        ref = oracle.linear(x, wh)
+    else:
+        gen = S.q4_0_blocks if qt == Q4_0 else S.q8_0_blocks
+        blocks = gen(3, f"W{N}x{K}", N, K)
+        w = dev.quantized(blocks, (N, K), qt)
+        ref = oracle.linear_q(x, blocks, 2 if qt == Q4_0 else 8, N)
+    y = dev.tensor(x).linear(w).numpy()
+    assert_close(y, ref, what=f"gemm {qt} {M}x{N}x{K}")
+
+
+def test_linear_bias_and_f16_odd_shapes(dev, oracle):
+    # src/ops/tests.rs:248-377 uses a rectangular [50, 122] case
+    x = S.normal_f16(4, "x", (3, 50))
+    w = S.normal_f16(4, "w", (122, 50), 0.0, 0.2)
+    b = S.normal_f16(4, "b", (122,))
+    for M in (1, 3):
+        got = dev.tensor(x[:M]).linear(dev.tensor(w), dev.tensor(b)).numpy()
+        assert_close(got, oracle.linear(x[:M], w, b), what=f"f16 linear M={M}")
+
+
+def test_matmul_known_answer(dev):
+    # tests/test_gpu_operations.rs:81-94: [[1,2],[3,4]] @ [[5,6],[7,8]]
+    a = dev.tensor(np.array([[1, 2], [3, 4]], np.float16))
+    b = dev.tensor(np.array([[5, 6], [7, 8]], np.float16))
+    assert a.matmul(b).numpy().astype(np.float32).tolist() == [[19, 22], [43, 50]]
+
+
+def test_linear_shape_errors(dev):
+    x = dev.tensor(np.zeros((2, 64), np.float16))
+    w = dev.tensor(np.zeros((8, 32), np.float16))
+    with pytest.raises(TLHipError) as e:
+        x.linear(w)
+    assert e.value.kind == "InvalidOperation"
+
+
+# ---------------------------------------------------------------------------
+# normalisation, RoPE, softmax, elementwise
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("rows,n", [(1, 2048), (46, 2048), (34, 2048), (3, 4), (5, 2560)])
+def test_rms_norm(dev, oracle, rows, n):
+    x = S.normal_f16(5, "x", (rows, n))
+    w = S.normal_f16(5, "w", (n,), 1.0, 0.02)
+    got = dev.tensor(x).rms_norm([n], dev.tensor(w), 1e-5).numpy()
+    ref = oracle.rms_norm(x, w, 1e-5)
+    assert ulp_diff(got, ref).max() <= 1
+    assert_close(got, ref)
+
+
+def test_rms_norm_known_answer(dev):
+    # tests/test_gpu_operations.rs:184-205: [1,2,3,4] / sqrt(7.5)
+    x = dev.tensor(np.array([[1, 2, 3, 4]], np.float16))
+    got = x.rms_norm([4], dev.tensor(np.ones(4, np.float16)), 1e-6).numpy().astype(np.float32).ravel()
+    assert np.allclose(got, np.array([1, 2, 3, 4]) / np.sqrt(7.5), atol=1e-3)
+
+
+def test_layer_norm(dev, oracle):
+    x = S.normal_f16(6, "x", (7, 2560), 0.3, 2.0)
+    w = S.normal_f16(6, "w", (2560,), 1.0, 0.1)
+    b = S.normal_f16(6, "b", (2560,), 0.0, 0.1)
+    got = dev.tensor(x).layer_norm(dev.tensor(w), dev.tensor(b), 1e-5).numpy()
+    ref = oracle.layer_norm(x, w, b, 1e-5)
+    assert ulp_diff(got, ref).max() <= 1
+    assert_close(got, ref)
+
+
+@pytest.mark.parametrize("S_,H,D,off,layout,rot", [
+    (3, 2, 8, 0, ROPE_INTERLEAVED, 0),       # test_shader_mathematical_correctness.rs:66-101
+    (46, 32, 64, 0, ROPE_INTERLEAVED, 0), (1, 32, 64, 34, ROPE_INTERLEAVED, 0),
+    (2048, 4, 64, 0, ROPE_NEOX, 0), (5, 32, 80, 511, ROPE_NEOX, 32)])
+def test_rope(dev, oracle, S_, H, D, off, layout, rot):
+    if (S_, H, D) == (3, 2, 8):
+        x = np.sin(0.1 * np.arange(S_ * H * D)).astype(np.float16).reshape(S_, H, D)
+    else:
+        x = S.normal_f16(7, "x", (S_, H, D))
+    got = dev.tensor(x).rope(off, 10000.0, layout, rot).numpy()
+    ref = oracle.rope(x, off, 10000.0, layout, rot)
+    # cos/sin come from the same table formula; the rotation is rounded the same way
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("rows,n", [(1, 3), (32, 46), (4, 2048), (2, 32000)])
+def test_softmax(dev, oracle, rows, n):
+    x = S.normal_f16(8, "x", (rows, n), 0.0, 3.0)
+    got = dev.tensor(x).softmax().numpy()
+    ref = oracle.softmax(x)
+    assert ulp_diff(got, ref).max() <= 1
+    assert np.allclose(got.astype(np.float32).sum(-1), 1.0, atol=2e-2)
+
+
+def test_softmax_known_answer_and_masked(dev):
+    got = dev.tensor(np.array([[1, 2, 3]], np.float16)).softmax().numpy().astype(np.float32)
+    assert np.allclose(got, [[0.0900, 0.2446, 0.6650]], atol=1e-3)
+    x = np.array([[np.inf, -np.inf, np.nan]], np.float16)   # degenerate row -> uniform
+    got = dev.tensor(x).softmax().numpy().astype(np.float32)
+    assert np.allclose(got, 1 / 3, atol=1e-3)
+
+
+def test_elementwise(dev, oracle):
+    x = S.normal_f16(9, "x", (4, 5632), 0.0, 4.0)
+    u = S.normal_f16(9, "u", (4, 5632))
+    tx, tu = dev.tensor(x), dev.tensor(u)
+    for got, ref in ((tx.sigmoid(), oracle.sigmoid(x)), (tx.silu(), oracle.silu(x)),
+                     (tx.gelu(), oracle.gelu(x)), (tx.silu_mul(tu), oracle.swiglu(x, u))):
+        assert ulp_diff(got.numpy(), ref).max() <= 1
+    for got, ref in ((tx + tu, oracle.add(x, u)), (tx * tu, oracle.mul(x, u)),
+                     (tx * 0.125, oracle.mul_scalar(x, 0.125))):
+        assert np.array_equal(got.numpy().view(np.uint16), ref.view(np.uint16))
+    # sigma(0) = 0.5 (src/ops/tests.rs:640-659)
+    assert float(dev.tensor(np.zeros(4, np.float16)).sigmoid().numpy()[0]) == 0.5
+
+
+def test_mask_and_einsums(dev, oracle):
+    Sq, H, Hkv, D = 9, 4, 2, 16
+    q = S.normal_f16(10, "q", (Sq, H, D))
+    k = S.normal_f16(10, "k", (Sq, Hkv, D))
+    v = S.normal_f16(10, "v", (Sq, Hkv, D))
+    sc = einsum("ihd,jhd->ihj", dev.tensor(q), dev.tensor(k)) * 0.25
+    mask = np.tril(np.ones((Sq, Sq), np.float16))
+    p = sc.apply_attention_mask(dev.tensor(mask)).softmax()
+    out = einsum("ihj,jhd->ihd", p, dev.tensor(v)).numpy()
+    ref = oracle.attention(q, k, v, 0, 0.25, True)
+    assert_close(out, ref, what="einsum attention")
+    fused = attention(dev.tensor(q), dev.tensor(k), dev.tensor(v), 0, 0.25, True).numpy()
+    assert_close(fused, ref, what="fused attention")
+
+
+@pytest.mark.parametrize("Sq,J,H,Hkv,D,q0", [(1, 174, 32, 4, 64, 173), (46, 46, 32, 4, 64, 0),
+                                             (1, 768, 32, 32, 80, 767), (300, 300, 8, 4, 64, 0),
+                                             (2048, 2048, 4, 1, 64, 0)])
+def test_attention(dev, oracle, Sq, J, H, Hkv, D, q0):
+    q = S.normal_f16(11, "q", (Sq, H, D))
+    k = S.normal_f16(11, "k", (J, Hkv, D))
+    v = S.normal_f16(11, "v", (J, Hkv, D))
+    got = attention(dev.tensor(q), dev.tensor(k), dev.tensor(v), q0, 1 / np.sqrt(D), True).numpy()
+    ref = oracle.attention(q, k, v, q0, 1 / np.sqrt(D), True)
+    assert_close(got, ref, what=f"attention S={Sq} J={J}")
+
+
+def test_embedding_and_argmax(dev, oracle):
+    table = S.normal_f16(12, "t", (320, 64), 0.0, 0.02)
+    ids = S.token_ids(12, "ids", 46, 320)
+    got = embedding(dev.tensor(table), ids).numpy()
+    assert np.array_equal(got, oracle.embedding(table, ids))
+    with pytest.raises(TLHipError) as e:
+        embedding(dev.tensor(table), [320])
+    assert e.value.kind == "IndexOutOfBounds"
+    # quantized table rows are dequantised bit-exactly
+    blocks = S.q4_0_blocks(12, "tq", 320, 64)
+    got = embedding(dev.quantized(blocks, (320, 64), Q4_0), ids).numpy()
+    assert np.array_equal(got, oracle.dequant(blocks, 2).reshape(320, 64)[ids])
+    # last-max tie-break (builtin_sampling.rs:170-176)
+    logits = np.zeros(32000, np.float16)
+    logits[[5, 17, 31000]] = 3.0
+    assert temperature_sample(dev.tensor(logits), 0.0) == 31000 == oracle.argmax_last(logits)
+    lg = S.normal_f16(12, "lg", (3, 32000))
+    assert temperature_sample(dev.tensor(lg), 0.0) == oracle.argmax_last(lg[-1])
+
+
+def test_kvcache(dev):
+    c = KVCache(dev, 2, 16, 4, 8)
+    k1, v1 = S.normal_f16(13, "k1", (5, 4, 8)), S.normal_f16(13, "v1", (5, 4, 8))
+    k2, v2 = S.normal_f16(13, "k2", (1, 4, 8)), S.normal_f16(13, "v2", (1, 4, 8))
+    c.set(1, dev.tensor(k1), dev.tensor(v1))
+    c.append(1, dev.tensor(k2), dev.tensor(v2))
+    assert c.len(1) == 6 and c.len(0) == 0
+    assert np.array_equal(c.get_k(1).numpy(), np.concatenate([k1, k2]))
+    assert np.array_equal(c.get_v(1).numpy(), np.concatenate([v1, v2]))
+    with pytest.raises(TLHipError):
+        c.append(1, dev.tensor(np.zeros((11, 4, 8), np.float16)), dev.tensor(np.zeros((11, 4, 8), np.float16)))
