@@ -81,6 +81,9 @@ def main():
     ap.add_argument("--gemv-iters", type=int, default=480)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--model", default="", help="reuse an existing TinyLlama GGUF file")
+    ap.add_argument("--decode-launch", choices=("graph", "direct"), default="graph",
+                    help="replay one captured HIP graph per decode step (default) or launch the same "
+                         "kernels one by one (profiler runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (asked for {args.gpus}); the hot path is "
@@ -107,9 +110,10 @@ def main():
     m = Model(dev, path, arch=0, max_ctx=max_ctx)
     log(f"model loaded in {time.time() - t0:.1f} s")
     # warm-up: prefill + W graph-replayed decode steps (also captures the graph)
-    m.generate(prompt, args.warmup, use_graph=True)
+    use_graph = args.decode_launch == "graph"
+    m.generate(prompt, args.warmup, use_graph=use_graph)
     dev.sync()
-    toks, prefill_ms, decode_ms = m.bench_decode(prompt, args.steps)
+    toks, prefill_ms, decode_ms = m.bench_decode(prompt, args.steps, use_graph=use_graph)
     dev.sync()
     tok_s = args.steps / (decode_ms / 1000.0)
     log(f"prefill {n_prompt} tokens: {prefill_ms:.2f} ms; decode {args.steps} steps: {decode_ms:.2f} ms "

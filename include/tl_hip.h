@@ -215,10 +215,12 @@ tlhip_status tlhip_model_dims(tlhip_model m, int32_t* dims8);
  * hipEvents recorded on the context stream around the launches.          */
 tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tensor* w, int n_w,
                                 tlhip_tensor y, int iters, float* avg_us);
-/* Times `n_decode` greedy steps (graph replay) after a prefill; returns
- * total decode ms (hipEvents) and the tokens.                            */
+/* Times `n_decode` greedy steps after a prefill (use_graph = 1: one
+ * captured HIP graph replayed per step; 0: the same kernels launched one
+ * by one); returns the prefill and total decode ms (hipEvents on the
+ * context stream) and the 1 + n_decode tokens.                           */
 tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode,
-                                int32_t* tokens_out, float* prefill_ms, float* decode_ms);
+                                int use_graph, int32_t* tokens_out, float* prefill_ms, float* decode_ms);
 
 #ifdef __cplusplus
 }

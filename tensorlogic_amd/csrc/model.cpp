@@ -642,14 +642,14 @@ tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tenso
     return TLHIP_OK;
 }
 
-tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode, int32_t* tokens_out,
-                                float* prefill_ms, float* decode_ms) {
+tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode, int use_graph,
+                                int32_t* tokens_out, float* prefill_ms, float* decode_ms) {
     if (!m || !prompt || !tokens_out || !prefill_ms || !decode_ms)
         return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     if (n_prompt + n_decode > m->max_ctx)
         return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "context overflow: %d + %d > %d", n_prompt, n_decode, m->max_ctx);
     tlhip_ctx ctx = m->ctx;
-    TLHIP_TRY(ensure_graph(m));
+    if (use_graph) TLHIP_TRY(ensure_graph(m));
     m->pos = 0;
     TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
     TLHIP_CHECK_HIP(hipEventRecord(ctx->ev0, ctx->stream));
@@ -658,7 +658,7 @@ tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prom
     TLHIP_CHECK_HIP(hipEventSynchronize(ctx->ev1));
     TLHIP_CHECK_HIP(hipEventElapsedTime(prefill_ms, ctx->ev0, ctx->ev1));
     TLHIP_CHECK_HIP(hipEventRecord(ctx->ev0, ctx->stream));
-    TLHIP_TRY(decode_steps(m, n_decode, true));
+    TLHIP_TRY(decode_steps(m, n_decode, use_graph != 0));
     TLHIP_CHECK_HIP(hipEventRecord(ctx->ev1, ctx->stream));
     TLHIP_CHECK_HIP(hipEventSynchronize(ctx->ev1));
     TLHIP_CHECK_HIP(hipEventElapsedTime(decode_ms, ctx->ev0, ctx->ev1));

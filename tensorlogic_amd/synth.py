@@ -132,11 +132,12 @@ PHI2_ARGS = dict(n_layers=32, hidden=2560, inter=10240, n_heads=32, vocab=51200,
 def write_llama_gguf(path: str, seed: int, n_layers: int = 22, hidden: int = 2048,
                      inter: int = 5632, n_heads: int = 32, n_kv: int = 4, vocab: int = 32000,
                      eps: float = 1e-5, theta: float = 10000.0, ctx: int = 2048,
-                     qtype: int = GGML_Q4_0) -> None:
+                     qtype: int = GGML_Q4_0, norm_mean: float = 0.0) -> None:
     """TinyLlama-architecture decoder with random-init weights.
 
-    Linear weights (incl. `output.weight`) are Q4_0 (or Q8_0), embeddings and
-    RMSNorm weights f16 N(0, 0.02).  Tensor names follow llama.cpp/GGUF.
+    Linear weights (incl. `output.weight`) are Q4_0 (or Q8_0), embeddings
+    f16 N(0, 0.02) and RMSNorm weights f16 N(norm_mean, 0.02) (the benchmark
+    configuration uses norm_mean 0).  Tensor names follow llama.cpp/GGUF.
     """
     qgen = q4_0_blocks if qtype == GGML_Q4_0 else q8_0_blocks
     hd = hidden // n_heads
@@ -155,17 +156,17 @@ def write_llama_gguf(path: str, seed: int, n_layers: int = 22, hidden: int = 204
     for i in range(n_layers):
         p = f"blk.{i}."
         w.add_tensor(p + "attn_norm.weight", GGML_F16, (hidden,),
-                     normal_f16(seed, p + "attn_norm.weight", (hidden,), 0.0, 0.02))
+                     normal_f16(seed, p + "attn_norm.weight", (hidden,), norm_mean, 0.02))
         for nm, (n, k) in (("attn_q", (hidden, hidden)), ("attn_k", (kvd, hidden)),
                            ("attn_v", (kvd, hidden)), ("attn_output", (hidden, hidden))):
             w.add_tensor(p + nm + ".weight", qtype, (n, k), qgen(seed, p + nm + ".weight", n, k))
         w.add_tensor(p + "ffn_norm.weight", GGML_F16, (hidden,),
-                     normal_f16(seed, p + "ffn_norm.weight", (hidden,), 0.0, 0.02))
+                     normal_f16(seed, p + "ffn_norm.weight", (hidden,), norm_mean, 0.02))
         for nm, (n, k) in (("ffn_gate", (inter, hidden)), ("ffn_up", (inter, hidden)),
                            ("ffn_down", (hidden, inter))):
             w.add_tensor(p + nm + ".weight", qtype, (n, k), qgen(seed, p + nm + ".weight", n, k))
     w.add_tensor("output_norm.weight", GGML_F16, (hidden,),
-                 normal_f16(seed, "output_norm.weight", (hidden,), 0.0, 0.02))
+                 normal_f16(seed, "output_norm.weight", (hidden,), norm_mean, 0.02))
     w.add_tensor("output.weight", qtype, (vocab, hidden), qgen(seed, "output.weight", vocab, hidden))
     w.write(path)
 
@@ -173,12 +174,13 @@ def write_llama_gguf(path: str, seed: int, n_layers: int = 22, hidden: int = 204
 def write_phi2_gguf(path: str, seed: int, n_layers: int = 32, hidden: int = 2560,
                     inter: int = 10240, n_heads: int = 32, vocab: int = 51200, rot: int = 32,
                     eps: float = 1e-5, theta: float = 10000.0, ctx: int = 2048,
-                    qtype: int = GGML_Q8_0) -> None:
+                    qtype: int = GGML_Q8_0, norm_mean: float = 0.0) -> None:
     """Phi-2-architecture decoder with random-init Q8_0 linear weights.
 
     Fused QKV projection, LayerNorm with bias, NeoX partial rotary on the first
     `rot` dims, GELU MLP in parallel with attention.  Norm weights, biases and
-    embeddings are f16 N(0, 0.02).  Names follow llama.cpp's phi2 tensors.
+    embeddings are f16 N(0, 0.02) (LayerNorm weights N(norm_mean, 0.02)).
+    Names follow llama.cpp's phi2 tensors.
     """
     qgen = q4_0_blocks if qtype == GGML_Q4_0 else q8_0_blocks
     w = GGUFWriter()
@@ -191,20 +193,20 @@ def write_phi2_gguf(path: str, seed: int, n_layers: int = 32, hidden: int = 2560
     w.add_f32("phi2.attention.layer_norm_epsilon", eps)
     w.add_f32("phi2.rope.freq_base", theta)
 
-    def vec(name, n):
-        w.add_tensor(name, GGML_F16, (n,), normal_f16(seed, name, (n,), 0.0, 0.02))
+    def vec(name, n, mean=0.0):
+        w.add_tensor(name, GGML_F16, (n,), normal_f16(seed, name, (n,), mean, 0.02))
 
     w.add_tensor("token_embd.weight", GGML_F16, (vocab, hidden),
                  normal_f16(seed, "token_embd.weight", (vocab, hidden), 0.0, 0.02))
     for i in range(n_layers):
         p = f"blk.{i}."
-        vec(p + "attn_norm.weight", hidden)
+        vec(p + "attn_norm.weight", hidden, norm_mean)
         vec(p + "attn_norm.bias", hidden)
         for nm, (n, k) in (("attn_qkv", (3 * hidden, hidden)), ("attn_output", (hidden, hidden)),
                            ("ffn_up", (inter, hidden)), ("ffn_down", (hidden, inter))):
             w.add_tensor(p + nm + ".weight", qtype, (n, k), qgen(seed, p + nm + ".weight", n, k))
             vec(p + nm + ".bias", n)
-    vec("output_norm.weight", hidden)
+    vec("output_norm.weight", hidden, norm_mean)
     vec("output_norm.bias", hidden)
     w.add_tensor("output.weight", qtype, (vocab, hidden), qgen(seed, "output.weight", vocab, hidden))
     vec("output.bias", vocab)

@@ -382,12 +382,12 @@ class Model:
         call("tlhip_model_logits", self.h, out.ctypes.data_as(C.POINTER(C.c_uint16)), out.size)
         return out.view(np.float16)
 
-    def bench_decode(self, prompt, n_decode: int):
+    def bench_decode(self, prompt, n_decode: int, use_graph: bool = True):
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.empty(n_decode + 1, np.int32)
         pm, dm = C.c_float(), C.c_float()
         call("tlhip_bench_decode", self.h, prompt.ctypes.data_as(C.POINTER(C.c_int32)), prompt.size, n_decode,
-             out.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(pm), C.byref(dm))
+             int(use_graph), out.ctypes.data_as(C.POINTER(C.c_int32)), C.byref(pm), C.byref(dm))
         return out, pm.value, dm.value
 
 

@@ -5,9 +5,11 @@
 tinyllama_q4_0_tokens.json -- config 4: the TinyLlama-1.1B-shape Q4_0 model
     of tensorlogic_amd.synth.write_llama_gguf(seed=4), 46-token prompt
     token_ids(4, "prompt", 46, 32000), 128 greedy decode steps: the 129
-    oracle tokens, the top1-top2 logit margin of each step and the final
-    logits (f16 values).  The GPU test regenerates the same file from the
-    seed and compares.
+    oracle tokens, the top1-top2 logit margin of each step, the 8 largest
+    logits of each step (ids and f16 values, from a step-by-step forward
+    that must reproduce the greedy stream) and the final logits (f16
+    values).  The GPU test regenerates the same file from the seed and
+    compares.
 synth_checksums.json -- sha256 of fixed generator draws, pinning the seeded
     generator across machines.
 """
@@ -49,6 +51,18 @@ def tinyllama_tokens(n_decode=128, seed=4):
         t0 = time.time()
         m = O.Model(path, arch=0, max_ctx=256)
         toks, margins, logits = m.generate(prompt, n_decode)
+        # the same stream one forward at a time, keeping each step's top 8
+        m.reset()
+        top_ids, top_vals = [], []
+        _, lg = m.forward(prompt, 0)
+        for step in range(n_decode + 1):
+            order = np.argsort(-lg.astype(np.float32), kind="stable")[:8]
+            top_ids.append([int(i) for i in order])
+            top_vals.append([float(lg[i]) for i in order])
+            if O.argmax_last(lg) != toks[step]:
+                raise RuntimeError(f"step-wise forward diverged from generate at step {step}")
+            if step < n_decode:
+                _, lg = m.forward(np.array([toks[step]], np.int32), len(prompt) + step)
         m.close()
         print(f"oracle: {time.time() - t0:.1f} s", file=sys.stderr)
     return {
@@ -58,6 +72,8 @@ def tinyllama_tokens(n_decode=128, seed=4):
         "n_decode": n_decode,
         "tokens": toks.tolist(),
         "margins": [float(x) for x in margins],
+        "top8_ids": top_ids,
+        "top8_logits": top_vals,
         "last_logits": [float(x) for x in logits.astype(np.float32)],
     }
 

@@ -77,16 +77,62 @@ def _golden(name):
         return json.load(f)
 
 
+def _ulp(v):
+    """f16 spacing at |v|."""
+    a = max(abs(float(v)), 2.0 ** -14)
+    return 2.0 ** (np.floor(np.log2(a)) - 10)
+
+
 def test_tinyllama_full_golden_tokens(dev, tmp_path):
-    """TinyLlama-1.1B shape, Q4_0, 46-token prompt, 128 greedy steps (config 4)."""
+    """TinyLlama-1.1B shape, Q4_0, 46-token prompt, 128 greedy steps (config 4).
+
+    The random-init model's logits are tiny (|l| < 0.25, f16 spacing 1.2e-4)
+    and its top-2 margin falls to exactly 0 at some steps: there the argmax is
+    fixed only by the last bit of an fp32 sum, which no two summation orders
+    share.  So the check runs teacher-forced on the oracle's token stream:
+    every step's logits at the oracle's top-8 ids must be within 2e-2 (and
+    within 8 f16 ulps), and the device argmax must equal the oracle's at every
+    step whose oracle margin exceeds the device's measured logit error there
+    (twice the top-8 deviation, at least 1 ulp).  The free-running graph path
+    must reproduce the stream up to the first such near-tie.
+    """
     g = _golden("tinyllama_q4_0_tokens.json")
+    if "top8_ids" not in g:
+        pytest.skip("golden file predates the per-step top-8 logits")
     path = str(tmp_path / "tinyllama.gguf")
     S.write_llama_gguf(path, seed=g["seed"], **S.TINYLLAMA_ARGS)
     prompt = np.array(g["prompt"], np.int32)
-    m = Model(dev, path, arch=0, max_ctx=256)
-    toks = m.generate(prompt, g["n_decode"], use_graph=True)
     ref = np.array(g["tokens"], np.int32)
-    mism = np.nonzero(toks != ref)[0]
-    assert mism.size == 0, f"first mismatch at step {mism[0]}: {toks[mism[0]]} vs {ref[mism[0]]}"
+    margins = np.array(g["margins"], np.float64)
+    ids = np.array(g["top8_ids"], np.int64)
+    vals = np.array(g["top8_logits"], np.float64)
+    n = g["n_decode"]
+    m = Model(dev, path, arch=0, max_ctx=256)
+
+    # teacher-forced: step i sees exactly the oracle's context
+    worst_ulps, exempt, mism = 0.0, [], []
+    tok = m.prefill(prompt)
+    for step in range(n + 1):
+        if step:
+            tok = m.decode(int(ref[step - 1]))
+        lg = m.logits().astype(np.float64)
+        dev_top = np.abs(lg[ids[step]] - vals[step])
+        err = float(dev_top.max())
+        ulp = _ulp(vals[step][0])
+        worst_ulps = max(worst_ulps, err / ulp)
+        assert err <= 2e-2, f"step {step}: top-8 logits off by {err:.3e}"
+        assert err <= 8 * ulp, f"step {step}: top-8 logits off by {err / ulp:.1f} f16 ulps"
+        if margins[step] <= max(2 * err, ulp):
+            exempt.append(step)
+        elif tok != ref[step]:
+            mism.append((step, int(tok), int(ref[step]), float(margins[step])))
+    print(f"teacher-forced: worst top-8 deviation {worst_ulps:.2f} ulp; near-tie steps {exempt}")
+    assert not mism, f"argmax differs at determined steps (step, device, oracle, margin): {mism}"
     assert_close(m.logits(), np.array(g["last_logits"], np.float16), what="final logits")
+
+    # free-running graph replay agrees up to the first near-tie
+    toks = m.generate(prompt, n, use_graph=True)
+    first = exempt[0] if exempt else n + 1
+    bad = np.nonzero(toks[:first] != ref[:first])[0]
+    assert bad.size == 0, f"free-running stream differs at step {bad[0]} before the first near-tie ({first})"
     m.close()
