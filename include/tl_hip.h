@@ -211,10 +211,12 @@ tlhip_status tlhip_model_dims(tlhip_model m, int32_t* dims8);
 
 /* ---- measurement helpers (hipEvent timing on the context's stream) ------ */
 /* Runs linear(x, w) `iters` times cycling over n_w weight tensors of equal
- * shape (to defeat the LLC) and returns the mean kernel time in us from
- * hipEvents recorded on the context stream around the launches.          */
+ * shape (to defeat the LLC) and returns the mean time per launch in us from
+ * hipEvents on the context stream: per_launch = 0 brackets the whole
+ * back-to-back sequence (throughput, gaps between launches included);
+ * per_launch = 1 brackets every launch with its own event pair.           */
 tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tensor* w, int n_w,
-                                tlhip_tensor y, int iters, float* avg_us);
+                                tlhip_tensor y, int iters, int per_launch, float* avg_us);
 /* Times `n_decode` greedy steps after a prefill (use_graph = 1: one
  * captured HIP graph replayed per step; 0: the same kernels launched one
  * by one); returns the prefill and total decode ms (hipEvents on the

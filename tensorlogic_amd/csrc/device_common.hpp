@@ -71,7 +71,21 @@ __device__ __forceinline__ uint16_t gelu_h(uint16_t a) {
     return f2h(__fmul_rn(__fmul_rn(0.5f, v), __fadd_rn(1.0f, tanhf(inner))));
 }
 
-// Shared epilogue of the GEMV / GEMM kernels (see GemvEpi).
+// Shared epilogue of the GEMV kernels with the bias / residual element
+// already in registers (see GemvEpi).
+__device__ __forceinline__ uint16_t epilogue_v(int epi, float acc, uint16_t b, uint16_t r) {
+    uint16_t y = f2h(acc);
+    switch (epi) {
+        case 1: y = add_h(y, b); break;
+        case 2: y = add_h(r, y); break;
+        case 4: y = add_h(r, add_h(y, b)); break;
+        case 5: y = gelu_h(add_h(y, b)); break;
+        default: break;
+    }
+    return y;
+}
+
+// Shared epilogue of the GEMM kernel (see GemvEpi).
 __device__ __forceinline__ uint16_t epilogue_h(int epi, float acc, const uint16_t* bias,
                                                const uint16_t* resid, size_t ri, int n) {
     uint16_t r = f2h(acc);

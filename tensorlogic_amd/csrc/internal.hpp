@@ -114,7 +114,27 @@ struct GemvArgs {
     uint16_t* y = nullptr;
     int M = 1, N = 0, K = 0;
     int ldy = 0;                   // row stride of y (elements), default N
+    // fused normalisation prologue (GEMV, M = 1): x is the raw residual row
+    int pro = 0;                   // PRO_NONE / PRO_RMS / PRO_LN
+    const uint16_t* norm_w = nullptr;
+    const uint16_t* norm_b = nullptr;
+    float eps = 0.f;
+    // EPI_QKV_ROPE: rows [0, nq) are q, [nq, nq+nk) k, [nq+nk, nq+2nk) v
+    int nq = 0, nk = 0, head_dim = 0, rot = 0, layout = 0;
+    int pos0 = 0;                  // position of activation row 0 (plus *d_pos)
+    const float* rope_tab = nullptr;
+    const int32_t* d_pos = nullptr;
+    uint16_t* q_out = nullptr;     // [M, nq]
+    uint16_t* kc = nullptr;        // K cache rows [pos][nk]
+    uint16_t* vc = nullptr;        // V cache rows [pos][nk]
+    // normalised GEMV only: x row = embd[*d_token] (decode), copied to x_out
+    const uint16_t* embd = nullptr;
+    const int32_t* d_token = nullptr;
+    uint16_t* x_out = nullptr;
+    // EPI_ARGMAX: one (value, index) key per workgroup, gemv_norm_slots(N) of them
+    unsigned long long* amax_slots = nullptr;
 };
+enum GemvPro { PRO_NONE = 0, PRO_RMS = 1, PRO_LN = 2 };
 // Epilogues fused into the GEMV/GEMM store (each step rounds to f16 where
 // the reference's separate op would store f16):
 //   STORE      y = f16(acc)
@@ -123,10 +143,16 @@ struct GemvArgs {
 //   SWIGLU     rows (2i, 2i+1) = (gate_i, up_i):     silu(gate) * up
 //   BIAS_RESID y = f16(r + f16(f16(acc) + b))        x + linear(a, W, b)
 //   BIAS_GELU  y = gelu(f16(f16(acc) + b))           gelu(linear(x, W, b))
+//   QKV_ROPE   rows (2i, 2i+1) of [q | k | v] (+ bias): RoPE'd q to q_out,
+//              RoPE'd k and v into the KV cache at the row's position
+//   ARGMAX     y = f16(acc) (+ bias), plus per-workgroup greedy keys
 enum GemvEpi { EPI_STORE = 0, EPI_BIAS = 1, EPI_RESID = 2, EPI_SWIGLU_PAIR = 3, EPI_BIAS_RESID = 4,
-               EPI_BIAS_GELU = 5 };
+               EPI_BIAS_GELU = 5, EPI_QKV_ROPE = 6, EPI_ARGMAX = 7 };
 
 tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi);
+int gemv_norm_slots(int N);   // workgroups (= argmax keys) of the normalised GEMV
+tlhip_status launch_argmax_slots(hipStream_t s, const unsigned long long* slots, int n, int32_t* out,
+                                 int32_t* token_log, int32_t* d_state);
 tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi);
 tlhip_status launch_repack(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks, void* qs,
                            uint16_t* d, int64_t nblocks, int64_t blocks_per_row, int to_gguf);
@@ -169,6 +195,7 @@ struct AttnArgs {
     int causal = 1;
     float scale_h = 0.125f;       // f16-rounded scale
     int q_stride = 0, out_stride = 0;  // row strides (elements); 0 = H*D
+    int kv_rows = 0;              // rows allocated in k / v (bounds early loads); 0 = J
 };
 tlhip_status launch_transpose(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows, int cols);
 tlhip_status launch_attention(hipStream_t s, const AttnArgs& a);   // decode: J from *d_pos

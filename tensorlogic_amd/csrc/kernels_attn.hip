@@ -96,11 +96,168 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, int J_fixed)
     }
 }
 
+// Head-dim-64 variant with the same arithmetic and storage points, laid out
+// for the memory system: a key is read by 8 lanes with one 16-byte load each
+// (a head's 128-byte K/V row in one coalesced access), 32 keys per pass, and
+// the loads of UNR passes are issued before their dot products so several
+// L2/HBM round trips overlap.  Scores: the 8 lanes' partial dot products are
+// combined with an xor tree.  Context: thread (g, c) accumulates dims
+// 8c..8c+7 over keys g, g+32, ...; the 32 partial rows are summed in g order.
+constexpr int A64_UNR = 8;
+
+__global__ __launch_bounds__(256) void attention64_kernel(AttnArgs a, int J_fixed) {
+    __shared__ float sc[ATT_MAX_J];
+    __shared__ float red[4];
+    __shared__ float part[32][65];
+    const int s = blockIdx.x, h = blockIdx.y;
+    const int Hkv = a.Hkv;
+    const int kvh = h / (a.H / Hkv);
+    const int qs = a.q_stride ? a.q_stride : a.H * 64;
+    const int os = a.out_stride ? a.out_stride : a.H * 64;
+    const int tid = threadIdx.x, c = tid & 7, g = tid >> 3;
+    const size_t kstride = (size_t)Hkv * 64;
+    const uint16_t* kbase = a.k + (size_t)kvh * 64 + 8 * c;
+    const uint16_t* vbase = a.v + (size_t)kvh * 64 + 8 * c;
+    // Loads that do not depend on the decode position go out first: q, and
+    // the first pass of K and V rows (bounded by the rows allocated, so
+    // every address is in bounds; rows past the key count are never used).
+    const u4 qv = *(const u4*)(a.q + (size_t)s * qs + (size_t)h * 64 + 8 * c);
+    const int kv_lim = a.kv_rows > 0 ? a.kv_rows : min(J_fixed, ATT_MAX_J);
+    u4 k0[A64_UNR], vv[A64_UNR];
+#pragma unroll
+    for (int u = 0; u < A64_UNR; u++) {
+        const int j = g + 32 * u;
+        k0[u] = j < kv_lim ? *(const u4*)(kbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < A64_UNR; u++) {
+        const int j = g + 32 * u;
+        vv[u] = j < kv_lim ? *(const u4*)(vbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
+    }
+    const int qpos = (a.d_pos ? *a.d_pos : a.q_pos0) + s;
+    const int J = min(a.d_pos ? qpos + 1 : J_fixed, ATT_MAX_J);
+    const int Jv = a.causal ? min(J, qpos + 1) : J;
+
+    float qf[8];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const h2 p2 = as_h2(qv[t]);
+        qf[2 * t] = (float)p2[0];
+        qf[2 * t + 1] = (float)p2[1];
+    }
+
+    // One pass covers 32 * A64_UNR keys; the first pass uses the rows loaded
+    // above.  When the unmasked row fits in that pass, the V rows loaded
+    // with it are used directly (one round trip to memory in all).
+    const bool one_pass = Jv <= 32 * A64_UNR;
+    float mx = -INFINITY;
+    for (int j0 = g; j0 < Jv; j0 += 32 * A64_UNR) {
+        u4 kv[A64_UNR];
+        if (j0 == g) {
+#pragma unroll
+            for (int u = 0; u < A64_UNR; u++) kv[u] = k0[u];
+        } else {
+#pragma unroll
+            for (int u = 0; u < A64_UNR; u++) {
+                const int j = j0 + 32 * u;
+                kv[u] = j < Jv ? *(const u4*)(kbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < A64_UNR; u++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const h2 k2 = as_h2(kv[u][t]);
+                acc += qf[2 * t] * (float)k2[0];
+                acc += qf[2 * t + 1] * (float)k2[1];
+            }
+            acc += __shfl_xor(acc, 1, 64);
+            acc += __shfl_xor(acc, 2, 64);
+            acc += __shfl_xor(acc, 4, 64);
+            const int j = j0 + 32 * u;
+            if (j < Jv) {
+                const float v = h2f(f2h(h2f(f2h(acc)) * a.scale_h));
+                if (c == 0) sc[j] = v;
+                if (isfinite(v)) mx = fmaxf(mx, v);
+            }
+        }
+    }
+    mx = bmax(mx, red);   // (its barriers also publish sc[])
+    if (!isfinite(mx)) mx = 0.0f;
+    float sum = 0.0f;
+    for (int j = tid; j < Jv; j += 256) {
+        const float v = sc[j];
+        const float e = isfinite(v) ? expf(v - mx) : 0.0f;
+        sc[j] = h2f(f2h(e));
+        sum += e;
+    }
+    sum = bsum(sum, red);
+    const bool degenerate = !(sum > 0.0f && isfinite(sum));
+    const int Jp = degenerate ? J : Jv;
+    const float uni = h2f(f2h(1.0f / (float)J));
+    for (int j = tid; j < Jp; j += 256) sc[j] = degenerate ? uni : h2f(f2h(sc[j] / sum));
+    __syncthreads();
+
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = 0.0f;
+    if (one_pass && !degenerate) {
+#pragma unroll
+        for (int u = 0; u < A64_UNR; u++) {
+            const int j = g + 32 * u;
+            if (j < Jp) {
+                const float pj = sc[j];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const h2 v2 = as_h2(vv[u][t]);
+                    o[2 * t] += pj * (float)v2[0];
+                    o[2 * t + 1] += pj * (float)v2[1];
+                }
+            }
+        }
+    } else {
+        for (int j0 = g; j0 < Jp; j0 += 32 * A64_UNR) {
+#pragma unroll
+            for (int u = 0; u < A64_UNR; u++) {
+                const int j = j0 + 32 * u;
+                vv[u] = j < Jp ? *(const u4*)(vbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < A64_UNR; u++) {
+                const int j = j0 + 32 * u;
+                if (j < Jp) {
+                    const float pj = sc[j];
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        const h2 v2 = as_h2(vv[u][t]);
+                        o[2 * t] += pj * (float)v2[0];
+                        o[2 * t + 1] += pj * (float)v2[1];
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) part[g][8 * c + e] = o[e];
+    __syncthreads();
+    if (tid < 64) {
+        float t = part[0][tid];
+        for (int gg = 1; gg < 32; gg++) t += part[gg][tid];
+        a.out[(size_t)s * os + (size_t)h * 64 + tid] = f2h(t);
+    }
+}
+
+static void launch_attn_any(hipStream_t s, const AttnArgs& a, int J) {
+    if (a.D == 64) hipLaunchKernelGGL(attention64_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, J);
+    else hipLaunchKernelGGL(attention_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, J);
+}
+
 tlhip_status launch_attention(hipStream_t s, const AttnArgs& a) {
     if (a.D > 256 || a.D <= 0) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: head_dim %d", a.D);
     if (a.Hkv <= 0 || a.H % a.Hkv) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: heads %d/%d", a.H, a.Hkv);
     if (a.S <= 0) return TLHIP_OK;
-    hipLaunchKernelGGL(attention_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, 0);
+    launch_attn_any(s, a, 0);
     return TLHIP_OK;
 }
 
@@ -109,7 +266,7 @@ tlhip_status launch_attention_j(hipStream_t s, const AttnArgs& a, int J) {
     if (a.D > 256 || a.D <= 0) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: head_dim %d", a.D);
     if (a.Hkv <= 0 || a.H % a.Hkv) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: heads %d/%d", a.H, a.Hkv);
     if (a.S <= 0) return TLHIP_OK;
-    hipLaunchKernelGGL(attention_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, J);
+    launch_attn_any(s, a, J);
     return TLHIP_OK;
 }
 

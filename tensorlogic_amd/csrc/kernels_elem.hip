@@ -368,35 +368,57 @@ tlhip_status launch_embedding(hipStream_t s, tlhip_dtype tt, const void* tq, con
 // logs the token and advances the device decode state
 // d_state = {token, pos, step}: token <- argmax, pos += 1, step += 1.
 // ---------------------------------------------------------------------------
+// (value, index) order of the reduction: larger value wins, equal values
+// go to the larger index (the last maximum); index -1 means "none".
+__device__ __forceinline__ void amax_merge(float& bv, int& bi, float v, int i) {
+    if (i >= 0 && (bi < 0 || v > bv || (v == bv && i > bi))) {
+        bv = v;
+        bi = i;
+    }
+}
+
 __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* __restrict__ x, int n,
                                                       int32_t* out, int32_t* token_log,
                                                       int32_t* d_state) {
-    __shared__ float sv[1024];
-    __shared__ int si[1024];
+    __shared__ float sv[16];
+    __shared__ int si[16];
     float best = -INFINITY;
     int bi = -1;
-    for (int i = threadIdx.x; i < n; i += 1024) {
+    // 8 elements per 16-byte load over the aligned body, scalar tail
+    const int n8 = ((uintptr_t)x % 16 == 0) ? n / 8 : 0;
+    for (int c = threadIdx.x; c < n8; c += 1024) {
+        const u4 v4 = *(const u4*)(x + (size_t)c * 8);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const h2 p2 = as_h2(v4[t]);
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const float v = (float)p2[e];
+                if (!isnan(v) && (bi < 0 || v >= best)) { best = v; bi = 8 * c + 2 * t + e; }
+            }
+        }
+    }
+    for (int i = 8 * n8 + threadIdx.x; i < n; i += 1024) {
         const float v = h2f(x[i]);
         if (!isnan(v) && (bi < 0 || v >= best)) { best = v; bi = i; }
     }
-    sv[threadIdx.x] = best;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int st = 512; st > 0; st >>= 1) {
-        if ((int)threadIdx.x < st) {
-            const float v2 = sv[threadIdx.x + st];
-            const int i2 = si[threadIdx.x + st];
-            const float v1 = sv[threadIdx.x];
-            const int i1 = si[threadIdx.x];
-            if (i2 >= 0 && (i1 < 0 || v2 > v1 || (v2 == v1 && i2 > i1))) {
-                sv[threadIdx.x] = v2;
-                si[threadIdx.x] = i2;
-            }
-        }
-        __syncthreads();
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float v2 = __shfl_xor(best, off, 64);
+        const int i2 = __shfl_xor(bi, off, 64);
+        amax_merge(best, bi, v2, i2);
     }
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    if (lane == 0) {
+        sv[w] = best;
+        si[w] = bi;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        const int tok = si[0] < 0 ? 0 : si[0];
+        float b = sv[0];
+        int ib = si[0];
+        for (int k = 1; k < 16; k++) amax_merge(b, ib, sv[k], si[k]);
+        const int tok = ib < 0 ? 0 : ib;
         if (out) out[0] = tok;
         if (d_state) {
             if (token_log) token_log[d_state[2]] = tok;

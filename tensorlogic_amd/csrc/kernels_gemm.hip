@@ -148,6 +148,8 @@ tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
     p.K = a.K;
     p.ldy = a.ldy ? a.ldy : (epi == EPI_SWIGLU_PAIR ? a.N / 2 : a.N);
     p.epi = epi;
+    if (epi == EPI_QKV_ROPE || a.pro != PRO_NONE)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "gemm: fused normalisation / RoPE epilogue is GEMV-only");
     if (p.M <= 0 || p.N <= 0) return TLHIP_OK;
     if (p.K % 32 != 0) {
         if (wt != TLHIP_F16 || epi == EPI_SWIGLU_PAIR)

@@ -163,7 +163,34 @@ struct GemvParams {
     const uint16_t* resid;
     uint16_t* y;
     int M, N, K, ldy, epi;
+    // fused normalisation prologue (M = 1)
+    const uint16_t* norm_w;
+    const uint16_t* norm_b;
+    float eps;
+    // EPI_QKV_ROPE
+    int nq, nk, head_dim, rot, layout, pos0;
+    const float* rope_tab;
+    const int32_t* d_pos;
+    uint16_t* q_out;
+    uint16_t* kc;
+    uint16_t* vc;
+    // normalised GEMV: x row = embd[*d_token] (written to x_out by workgroup 0)
+    const uint16_t* embd;
+    const int32_t* d_token;
+    uint16_t* x_out;
+    // EPI_ARGMAX: per-workgroup (value, index) keys
+    unsigned long long* amax_slots;
 };
+
+// 32 consecutive f16 activations as 16 natural pairs xw[i] = (x2i, x2i+1).
+__device__ __forceinline__ void load_x32(const uint16_t* __restrict__ xb, uint32_t xw[16]) {
+    const u4* p = (const u4*)xb;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        u4 t = p[v];
+        xw[4 * v + 0] = t[0]; xw[4 * v + 1] = t[1]; xw[4 * v + 2] = t[2]; xw[4 * v + 3] = t[3];
+    }
+}
 
 // Per-block activation chunk in the pair order of the unpacking:
 //   Q4_0 (16 pairs): [4t+0]=(x4t,x4t+2) [4t+1]=(x4t+1,x4t+3)
@@ -171,14 +198,7 @@ struct GemvParams {
 //   Q8_0 (16 pairs): [2t+0]=(x4t,x4t+2) [2t+1]=(x4t+1,x4t+3), t < 8
 //   F16  (16 pairs): natural pairs (x2i, x2i+1)
 template <int WT>
-__device__ __forceinline__ void load_xchunk(const uint16_t* __restrict__ xb, uint32_t xc[16]) {
-    const u4* p = (const u4*)xb;
-    uint32_t xw[16];   // xw[i] = (x2i, x2i+1)
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-        u4 t = p[v];
-        xw[4 * v + 0] = t[0]; xw[4 * v + 1] = t[1]; xw[4 * v + 2] = t[2]; xw[4 * v + 3] = t[3];
-    }
+__device__ __forceinline__ void order_x(const uint32_t xw[16], uint32_t xc[16]) {
     if (WT == TLHIP_Q4_0) {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -197,6 +217,144 @@ __device__ __forceinline__ void load_xchunk(const uint16_t* __restrict__ xb, uin
 #pragma unroll
         for (int i = 0; i < 16; i++) xc[i] = xw[i];
     }
+}
+
+template <int WT>
+__device__ __forceinline__ void load_xchunk(const uint16_t* __restrict__ xb, uint32_t xc[16]) {
+    uint32_t xw[16];
+    load_x32(xb, xw);
+    order_x<WT>(xw, xc);
+}
+
+// Activation staging for the normalised GEMV (M = 1).  The workgroup loads
+// the row once, forms the row statistics, normalises with exactly the
+// formulas and f16 store of rms_norm_kernel / layer_norm_kernel
+//   RMS: y = f16((x * (1 / sqrt(mean(x^2) + eps))) * w)
+//   LN:  y = f16(((x - mean) * (1 / sqrt(var + eps))) * w + b)
+// and leaves it in LDS already in the pair order of the unpacking.  LDS is
+// quad-major, xs[v][b] = 16 bytes (pairs 4v..4v+3 of block b's chunk), so
+// lane l's reads of block l are consecutive 16-byte words (no conflicts).
+// Quad v of a block holds elements {4v..4v+3, 16+4v..16+4v+3} for Q4_0 and
+// {8v..8v+7} for Q8_0 / f16.
+template <int WT>
+__device__ __forceinline__ int quad_elem(int v, int e) {
+    return WT == TLHIP_Q4_0 ? (e < 4 ? 4 * v + e : 12 + 4 * v + e) : 8 * v + e;
+}
+
+template <int WT>
+__device__ __forceinline__ void load_quad(const uint16_t* __restrict__ src, int b, int v, float f[8]) {
+    uint32_t w[4];
+    if (WT == TLHIP_Q4_0) {
+        const uint2 lo = *(const uint2*)(src + (size_t)b * 32 + 4 * v);
+        const uint2 hi = *(const uint2*)(src + (size_t)b * 32 + 16 + 4 * v);
+        w[0] = lo.x; w[1] = lo.y; w[2] = hi.x; w[3] = hi.y;
+    } else {
+        const u4 t = *(const u4*)(src + (size_t)b * 32 + 8 * v);
+        w[0] = t[0]; w[1] = t[1]; w[2] = t[2]; w[3] = t[3];
+    }
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const h2 h = as_h2(w[t]);
+        f[2 * t] = (float)h[0];
+        f[2 * t + 1] = (float)h[1];
+    }
+}
+
+template <int WT>
+__device__ __forceinline__ u4 pack_quad(const float f[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        h2 h;
+        h[0] = (h16)f[2 * t];
+        h[1] = (h16)f[2 * t + 1];
+        w[t] = as_u32(h);
+    }
+    if (WT == TLHIP_F16) return u4{w[0], w[1], w[2], w[3]};
+    return u4{pack_lo(w[0], w[1]), pack_hi(w[0], w[1]), pack_lo(w[2], w[3]), pack_hi(w[2], w[3])};
+}
+
+template <int WPB>
+__device__ __forceinline__ float wg_sum(float v, float* red) {
+    v = wave_sum<64>(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int k = 1; k < WPB; k++) t += red[k];
+    __syncthreads();
+    return t;
+}
+
+// Items (block b, quad v) are spread over the workgroup; each thread keeps
+// its (at most IPT) items' values in registers between the passes.
+template <int WT, int NB, int WPB, int PRO>
+__device__ __forceinline__ void stage_norm(const GemvParams& p, const uint16_t* __restrict__ xsrc,
+                                           u4 (*xs)[NB * 64], float* red) {
+    constexpr int NT = WPB * 64;
+    constexpr int IPT = (NB * 256 + NT - 1) / NT;
+    const int nbr = p.K >> 5, items = nbr * 4;
+    float f[IPT][8];
+#pragma unroll
+    for (int k = 0; k < IPT; k++) {
+        const int it = threadIdx.x + k * NT;
+        if (it < items) load_quad<WT>(xsrc, it >> 2, it & 3, f[k]);
+        else
+#pragma unroll
+            for (int e = 0; e < 8; e++) f[k][e] = 0.0f;
+    }
+    if (p.x_out && blockIdx.x == 0)   // the residual copy of an embedded row
+#pragma unroll
+        for (int k = 0; k < IPT; k++) {
+            const int it = threadIdx.x + k * NT;
+            if (it < items) {
+                const int b = it >> 2, v = it & 3;
+#pragma unroll
+                for (int e = 0; e < 8; e++) p.x_out[(size_t)b * 32 + quad_elem<WT>(v, e)] = f2h(f[k][e]);
+            }
+        }
+    float mean = 0.0f, inv;
+    if (PRO == PRO_RMS) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < IPT; k++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) ss += f[k][e] * f[k][e];
+        const float t = wg_sum<WPB>(ss, red);
+        inv = 1.0f / sqrtf(t / (float)p.K + p.eps);
+    } else {
+        float sm = 0.0f;
+#pragma unroll
+        for (int k = 0; k < IPT; k++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) sm += f[k][e];
+        mean = wg_sum<WPB>(sm, red) / (float)p.K;
+        float q = 0.0f;
+#pragma unroll
+        for (int k = 0; k < IPT; k++) {
+            if (threadIdx.x + k * NT >= items) continue;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float d = f[k][e] - mean;
+                q += d * d;
+            }
+        }
+        inv = 1.0f / sqrtf(wg_sum<WPB>(q, red) / (float)p.K + p.eps);
+    }
+#pragma unroll
+    for (int k = 0; k < IPT; k++) {
+        const int it = threadIdx.x + k * NT;
+        if (it >= items) continue;
+        const int b = it >> 2, v = it & 3;
+        float w[8], bb[8];
+        load_quad<WT>(p.norm_w, b, v, w);
+        if (PRO == PRO_LN) load_quad<WT>(p.norm_b, b, v, bb);
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            f[k][e] = PRO == PRO_RMS ? (f[k][e] * inv) * w[e] : (((f[k][e] - mean) * inv) * w[e]) + bb[e];
+        xs[v][b] = pack_quad<WT>(f[k]);
+    }
+    __syncthreads();
 }
 
 // Weight payload of one 32-element block: Q4_0 1 x 16 B, Q8_0 2 x 16 B, F16 4 x 16 B.
@@ -235,24 +393,84 @@ __device__ __forceinline__ float block_dot(const u4* q, uint16_t dbits, const ui
     return acc;
 }
 
-__device__ __forceinline__ void gemv_store(const GemvParams& p, int m, int row, float acc) {
-    p.y[(size_t)m * p.ldy + row] = epilogue_h(p.epi, acc, p.bias, p.resid, (size_t)m * p.N + row, row);
+
+// Fused projection epilogue for rows (row, row + 1) of the stacked
+// [q | k | v] weight (M = 1, decode or one prefill row): the linear's f16
+// store (+ bias), then RoPE on q and k at position pos (rope_kernel's
+// arithmetic) written to q_out and the K cache, V copied to the V cache --
+// linear + rope + Cache::update of the reference's program in one store.
+// Rows of a head are in pair order: pair i is (row 2i, row 2i + 1), which is
+// the natural order for the interleaved layout and a load-time permutation
+// of the rows for the half-rotation (NeoX) layout; dims >= rot pass through.
+// The bias pair, the position and the pair's (cos, sin) were loaded at the
+// start of the kernel (QkvPre), so the tail makes no dependent loads.
+struct QkvPre {
+    int pos;
+    uint16_t b0, b1;
+    float c, sn;
+};
+
+__device__ __forceinline__ void qkv_rope_pre(const GemvParams& p, int row, int pos, QkvPre& q) {
+    q.pos = pos;
+    q.b0 = p.bias ? p.bias[row] : 0;
+    q.b1 = p.bias ? p.bias[row + 1] : 0;
+    q.c = 1.0f;
+    q.sn = 0.0f;
+    const int D = p.head_dim;
+    int e = -1;
+    if (row < p.nq) e = row % D;
+    else if (row < p.nq + p.nk) e = (row - p.nq) % D;
+    if (e >= 0 && e < p.rot) {
+        const int half = p.rot >> 1, i = e >> 1;
+        q.c = p.rope_tab[2 * ((size_t)pos * half + i)];
+        q.sn = p.rope_tab[2 * ((size_t)pos * half + i) + 1];
+    }
 }
 
-// NB: blocks per lane (ceil(K/32/64)); RI: rows per wave; MX: max activation rows.
-template <int WT, int NB, int RI, int MX>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
-    const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int row0 = wave * RI;
-    if (row0 >= p.N) return;
-    const int nbr = p.K >> 5;
-    constexpr int NL = BlkLoads<WT>::n;
-    const size_t row_bytes = WT == TLHIP_Q4_0 ? (size_t)p.K / 2 : (WT == TLHIP_Q8_0 ? (size_t)p.K : (size_t)p.K * 2);
+__device__ __forceinline__ void qkv_rope_store(const GemvParams& p, int row, float a0, float a1, const QkvPre& q) {
+    uint16_t r0 = f2h(a0), r1 = f2h(a1);
+    if (p.bias) {
+        r0 = add_h(r0, q.b0);
+        r1 = add_h(r1, q.b1);
+    }
+    const int pos = q.pos;
+    const int D = p.head_dim;
+    uint16_t* dst;
+    int e;
+    if (row < p.nq) {
+        dst = p.q_out + (size_t)(row / D) * D;
+        e = row % D;
+    } else if (row < p.nq + p.nk) {
+        const int c = row - p.nq;
+        dst = p.kc + (size_t)pos * p.nk + (size_t)(c / D) * D;
+        e = c % D;
+    } else {
+        const int c = row - p.nq - p.nk;
+        p.vc[(size_t)pos * p.nk + c] = r0;
+        p.vc[(size_t)pos * p.nk + c + 1] = r1;
+        return;
+    }
+    if (e < p.rot) {
+        const int half = p.rot >> 1, i = e >> 1;
+        const float x0 = h2f(r0), x1 = h2f(r1);
+        const float o0 = __fsub_rn(__fmul_rn(x0, q.c), __fmul_rn(x1, q.sn));
+        const float o1 = __fadd_rn(__fmul_rn(x0, q.sn), __fmul_rn(x1, q.c));
+        const int i0 = p.layout ? i : 2 * i, i1 = p.layout ? i + half : 2 * i + 1;
+        dst[i0] = f2h(o0);
+        dst[i1] = f2h(o1);
+    } else {
+        dst[e] = r0;
+        dst[e + 1] = r1;
+    }
+}
 
-    // issue all weight loads first
-    u4 q[RI][NB][NL];
-    uint16_t ds[RI][NB];
+// Loads of RI rows x NB blocks of the wave, all issued before any use.
+template <int WT, int NB, int RI>
+__device__ __forceinline__ void load_rows(const GemvParams& p, int row0, int lane, u4 (&q)[RI][NB][BlkLoads<WT>::n],
+                                          uint16_t (&ds)[RI][NB]) {
+    constexpr int NL = BlkLoads<WT>::n;
+    const int nbr = p.K >> 5;
+    const size_t row_bytes = WT == TLHIP_Q4_0 ? (size_t)p.K / 2 : (WT == TLHIP_Q8_0 ? (size_t)p.K : (size_t)p.K * 2);
 #pragma unroll
     for (int ri = 0; ri < RI; ri++) {
         const int row = min(row0 + ri, p.N - 1);
@@ -265,13 +483,90 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
             ds[ri][i] = WT == TLHIP_F16 ? 0 : p.wd[(size_t)row * nbr + b];
         }
     }
+}
+
+// Lane 0's bias / residual elements of the wave's rows, loaded right after
+// the weights so the epilogue makes no dependent loads.
+template <int RI, int MX>
+struct EpiPre {
+    uint16_t b[RI];
+    uint16_t r[RI][MX];
+};
+
+template <int RI, int MX>
+__device__ __forceinline__ void epi_preload(const GemvParams& p, int row0, EpiPre<RI, MX>& e) {
+#pragma unroll
+    for (int ri = 0; ri < RI; ri++) {
+        const int row = min(row0 + ri, p.N - 1);
+        e.b[ri] = p.bias ? p.bias[row] : 0;
+#pragma unroll
+        for (int m = 0; m < MX; m++) e.r[ri][m] = (p.resid && m < p.M) ? p.resid[(size_t)m * p.N + row] : 0;
+    }
+}
+
+// Lane 0's stores of the wave's RI reduced rows (m = activation row).
+template <int RI, int MX>
+__device__ __forceinline__ void store_rows(const GemvParams& p, int row0, const float (&acc)[RI][MX],
+                                           const EpiPre<RI, MX>& e) {
+    if (p.epi == EPI_SWIGLU_PAIR) {
+        // row pairs (2i, 2i+1) = (gate_i, up_i); RI is even and row0 even
+#pragma unroll
+        for (int ri = 0; ri < RI; ri += 2) {
+            const int row = row0 + ri;
+            if (row + 1 < p.N)
+#pragma unroll
+                for (int m = 0; m < MX; m++)
+                    if (m < p.M) p.y[(size_t)m * p.ldy + row / 2] = swiglu_h(f2h(acc[ri][m]), f2h(acc[ri + 1][m]));
+        }
+    } else {
+#pragma unroll
+        for (int ri = 0; ri < RI; ri++) {
+            const int row = row0 + ri;
+            if (row < p.N)
+#pragma unroll
+                for (int m = 0; m < MX; m++)
+                    if (m < p.M) p.y[(size_t)m * p.ldy + row] = epilogue_v(p.epi, acc[ri][m], e.b[ri], e.r[ri][m]);
+        }
+    }
+}
+
+// Greedy argmax key of an f16 logit: order-preserving 16-bit image in the
+// high half (NaN lowest, -0 as +0), index in the low half, so the largest
+// key is the largest value and, among equal values, the largest index --
+// the last maximum, as temperature_sample's max_by keeps it.
+__device__ __forceinline__ unsigned long long amax_key(uint16_t h, int idx) {
+    uint32_t k;
+    if ((h & 0x7fffu) > 0x7c00u) k = 0u;                       // NaN
+    else {
+        if (h == 0x8000u) h = 0;                                // -0 == +0
+        k = (h & 0x8000u) ? (~(uint32_t)h & 0xffffu) : ((uint32_t)h | 0x8000u);
+    }
+    return ((unsigned long long)k << 32) | (uint32_t)idx;
+}
+
+__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+
+// NB: blocks per lane (ceil(K/32/64)); RI: rows per wave; MX: max activation
+// rows.  Activation chunks are loaded by every wave from global memory (L2).
+template <int WT, int NB, int RI, int MX>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row0 = wave * RI;
+    if (row0 >= p.N) return;
+    const int nbr = p.K >> 5;
+    constexpr int NL = BlkLoads<WT>::n;
+    u4 q[RI][NB][NL];
+    uint16_t ds[RI][NB];
+    load_rows<WT, NB, RI>(p, row0, lane, q, ds);
+    EpiPre<RI, MX> pre;
+    if (lane == 0) epi_preload<RI, MX>(p, row0, pre);
 
     float acc[RI][MX];
 #pragma unroll
     for (int ri = 0; ri < RI; ri++)
 #pragma unroll
         for (int m = 0; m < MX; m++) acc[ri][m] = 0.0f;
-
 #pragma unroll
     for (int i = 0; i < NB; i++) {
         const int b = lane + 64 * i;
@@ -287,34 +582,97 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
             }
         }
     }
-
 #pragma unroll
     for (int ri = 0; ri < RI; ri++)
 #pragma unroll
         for (int m = 0; m < MX; m++) acc[ri][m] = wave_sum<64>(acc[ri][m]);
+    if (lane == 0) store_rows<RI, MX>(p, row0, acc, pre);
+}
 
-    if (lane == 0) {
-        if (p.epi == EPI_SWIGLU_PAIR) {
-            // rows (2i, 2i+1) hold (gate_i, up_i); RI is even and row0 even.
+// Normalised GEMV (M = 1): norm(x) staged once per workgroup in LDS (the
+// weight loads are issued first, so they are in flight during it), then
+// the same block dots.  EPI_ARGMAX additionally reduces the workgroup's
+// stored logits to one (value, index) key in amax_slots[blockIdx.x].
+template <int WT, int NB, int RI, int WPB, int PRO>
+__global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams p) {
+    __shared__ u4 xs[4][NB * 64];
+    __shared__ float red[WPB];
+    __shared__ unsigned long long wkey[WPB];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * WPB + w) * RI;
+    const int nbr = p.K >> 5;
+    constexpr int NL = BlkLoads<WT>::n;
+    u4 q[RI][NB][NL];
+    uint16_t ds[RI][NB];
+    // position first: the RoPE table loads depend on it
+    const int pos = p.epi == EPI_QKV_ROPE ? p.pos0 + (p.d_pos ? *p.d_pos : 0) : 0;
+    if (row0 < p.N) load_rows<WT, NB, RI>(p, row0, lane, q, ds);
+    EpiPre<RI, 1> pre;
+    QkvPre qp[RI / 2 > 0 ? RI / 2 : 1];
+    if (lane == 0 && row0 < p.N) {
+        if (p.epi == EPI_QKV_ROPE) {
 #pragma unroll
-            for (int ri = 0; ri < RI; ri += 2) {
-                const int row = row0 + ri;
-                if (row + 1 < p.N)
-#pragma unroll
-                    for (int m = 0; m < MX; m++)
-                        if (m < p.M)
-                            p.y[(size_t)m * p.ldy + row / 2] = swiglu_h(f2h(acc[ri][m]), f2h(acc[ri + 1][m]));
-            }
+            for (int ri = 0; ri + 1 < RI; ri += 2)
+                if (row0 + ri + 1 < p.N) qkv_rope_pre(p, row0 + ri, pos, qp[ri / 2]);
         } else {
+            epi_preload<RI, 1>(p, row0, pre);
+        }
+    }
+    const uint16_t* xsrc = p.embd ? p.embd + (size_t)(*p.d_token) * p.K : p.x;
+    stage_norm<WT, NB, WPB, PRO>(p, xsrc, xs, red);
+
+    float acc[RI][1];
 #pragma unroll
-            for (int ri = 0; ri < RI; ri++) {
-                const int row = row0 + ri;
-                if (row < p.N)
+    for (int ri = 0; ri < RI; ri++) acc[ri][0] = 0.0f;
+    if (row0 < p.N) {
 #pragma unroll
-                    for (int m = 0; m < MX; m++)
-                        if (m < p.M) gemv_store(p, m, row, acc[ri][m]);
+        for (int i = 0; i < NB; i++) {
+            const int b = lane + 64 * i;
+            if (b < nbr) {
+                uint32_t xc[16];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const u4 t = xs[v][b];
+                    xc[4 * v] = t[0]; xc[4 * v + 1] = t[1]; xc[4 * v + 2] = t[2]; xc[4 * v + 3] = t[3];
+                }
+#pragma unroll
+                for (int ri = 0; ri < RI; ri++) acc[ri][0] = block_dot<WT>(q[ri][i], ds[ri][i], xc, acc[ri][0]);
             }
         }
+#pragma unroll
+        for (int ri = 0; ri < RI; ri++) acc[ri][0] = wave_sum<64>(acc[ri][0]);
+    }
+    if (p.epi == EPI_QKV_ROPE) {
+        if (lane == 0 && row0 < p.N)
+#pragma unroll
+            for (int ri = 0; ri + 1 < RI; ri += 2)
+                if (row0 + ri + 1 < p.N) qkv_rope_store(p, row0 + ri, acc[ri][0], acc[ri + 1][0], qp[ri / 2]);
+        return;
+    }
+    if (p.epi != EPI_ARGMAX) {
+        if (lane == 0 && row0 < p.N) store_rows<RI, 1>(p, row0, acc, pre);
+        return;
+    }
+    unsigned long long best = 0ull;
+    if (lane == 0 && row0 < p.N) {
+#pragma unroll
+        for (int ri = 0; ri < RI; ri++) {
+            const int row = row0 + ri;
+            if (row < p.N) {
+                uint16_t r = f2h(acc[ri][0]);
+                if (p.bias) r = add_h(r, pre.b[ri]);
+                p.y[row] = r;
+                best = umax64(best, amax_key(r, row));
+            }
+        }
+    }
+    if (lane == 0) wkey[w] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = wkey[0];
+#pragma unroll
+        for (int k = 1; k < WPB; k++) b = umax64(b, wkey[k]);
+        p.amax_slots[blockIdx.x] = b;
     }
 }
 
@@ -330,7 +688,9 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(GemvParams p) {
     float acc = 0.0f;
     for (int k = lane; k < p.K; k += 64) acc += h2f(x[k]) * h2f(w[k]);
     acc = wave_sum<64>(acc);
-    if (lane == 0) gemv_store(p, m, row, acc);
+    if (lane == 0)
+        p.y[(size_t)m * p.ldy + row] = epilogue_v(p.epi, acc, p.bias ? p.bias[row] : 0,
+                                                  p.resid ? p.resid[(size_t)m * p.N + row] : 0);
 }
 
 template <int WT, int NB, int RI, int MX>
@@ -368,8 +728,46 @@ static bool launch_mx(hipStream_t s, const GemvParams& p, int nb, int ri) {
     return false;
 }
 
+// Normalised GEMV shapes: rows per wave and waves per workgroup chosen by
+// the measured optimum of the decoder's shapes on MI355X (more rows per
+// workgroup amortise the staging; tall matrices take 16-wave groups).
+template <int WT, int NB, int PRO>
+static void launch_norm_shape(hipStream_t s, const GemvParams& p) {
+    if (p.N >= 16384 && p.epi != EPI_QKV_ROPE && p.epi != EPI_SWIGLU_PAIR) {
+        const int wgs = (p.N + 63) / 64;   // 16 waves x 4 rows
+        hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 4, 16, PRO>), dim3(wgs), dim3(1024), 0, s, p);
+    } else if (p.N >= 8192) {
+        const int wgs = (p.N + 15) / 16;   // 8 waves x 2 rows
+        hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 2, 8, PRO>), dim3(wgs), dim3(512), 0, s, p);
+    } else {
+        const int wgs = (p.N + 7) / 8;     // 4 waves x 2 rows
+        hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 2, 4, PRO>), dim3(wgs), dim3(256), 0, s, p);
+    }
+}
+
+template <int WT>
+static bool launch_norm(hipStream_t s, const GemvParams& p, int nb, int pro) {
+    if (nb == 1) {
+        if (pro == PRO_RMS) launch_norm_shape<WT, 1, PRO_RMS>(s, p);
+        else launch_norm_shape<WT, 1, PRO_LN>(s, p);
+        return true;
+    }
+    if (nb == 2) {
+        if (pro == PRO_RMS) launch_norm_shape<WT, 2, PRO_RMS>(s, p);
+        else launch_norm_shape<WT, 2, PRO_LN>(s, p);
+        return true;
+    }
+    return false;
+}
+
+int gemv_norm_slots(int N) {
+    if (N >= 16384) return (N + 63) / 64;
+    if (N >= 8192) return (N + 15) / 16;
+    return (N + 7) / 8;
+}
+
 tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi) {
-    GemvParams p;
+    GemvParams p = {};
     p.x = a.x;
     p.wq = (const uint8_t*)a.wq;
     p.wd = a.wd;
@@ -381,25 +779,99 @@ tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
     p.K = a.K;
     p.ldy = a.ldy ? a.ldy : (epi == EPI_SWIGLU_PAIR ? a.N / 2 : a.N);
     p.epi = epi;
+    p.norm_w = a.norm_w;
+    p.norm_b = a.norm_b;
+    p.eps = a.eps;
+    p.nq = a.nq;
+    p.nk = a.nk;
+    p.head_dim = a.head_dim;
+    p.rot = a.rot;
+    p.layout = a.layout;
+    p.pos0 = a.pos0;
+    p.rope_tab = a.rope_tab;
+    p.d_pos = a.d_pos;
+    p.q_out = a.q_out;
+    p.kc = a.kc;
+    p.vc = a.vc;
+    p.embd = a.embd;
+    p.d_token = a.d_token;
+    p.x_out = a.x_out;
+    p.amax_slots = a.amax_slots;
     if (p.N <= 0 || p.M <= 0) return TLHIP_OK;
+    const bool pair_epi = epi == EPI_SWIGLU_PAIR || epi == EPI_QKV_ROPE;
+    if (pair_epi && (p.N % 2))
+        return fail(TLHIP_ERR_INVALID_DIMENSION, "gemv: paired epilogue needs an even row count (N=%d)", p.N);
+    if (epi == EPI_QKV_ROPE && (p.head_dim <= 0 || p.head_dim % 2 || p.rot % 2 || p.rot > p.head_dim ||
+                                p.nq % p.head_dim || p.nk % p.head_dim || p.nq + 2 * p.nk != p.N ||
+                                !p.rope_tab || !p.q_out || !p.kc || !p.vc))
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "gemv: inconsistent QKV/RoPE epilogue arguments");
+    const bool normed = a.pro != PRO_NONE;
+    if (normed && (p.M != 1 || !p.norm_w || (a.pro == PRO_LN && !p.norm_b) || (p.embd && !p.d_token)))
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "gemv: fused normalisation needs M = 1 and its weights");
+    if (epi == EPI_ARGMAX && (!normed || !p.amax_slots))
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "gemv: the argmax epilogue runs on the normalised GEMV");
+    if (!normed && (p.embd || epi == EPI_ARGMAX || epi == EPI_QKV_ROPE))
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "gemv: embedding source needs the normalised GEMV");
     bool done = false;
     if (p.K % 32 == 0 && p.K > 0) {
         const int nbr = p.K / 32;
         const int nb = (nbr + 63) / 64;
-        // Rows per wave: enough waves to fill 256 CUs several times over,
-        // more bytes in flight per lane when the matrix is tall.
-        int ri = p.N >= 8192 ? 4 : (p.N >= 4096 ? 2 : 1);
-        if (epi == EPI_SWIGLU_PAIR && ri < 2) ri = 2;
-        if (wt == TLHIP_Q4_0) done = launch_mx<TLHIP_Q4_0>(s, p, nb, ri);
-        else if (wt == TLHIP_Q8_0) done = launch_mx<TLHIP_Q8_0>(s, p, nb, ri);
-        else done = launch_mx<TLHIP_F16>(s, p, nb, ri);
+        if (normed) {
+            if (wt == TLHIP_Q4_0) done = launch_norm<TLHIP_Q4_0>(s, p, nb, a.pro);
+            else if (wt == TLHIP_Q8_0) done = launch_norm<TLHIP_Q8_0>(s, p, nb, a.pro);
+            else done = launch_norm<TLHIP_F16>(s, p, nb, a.pro);
+        } else {
+            // two rows per wave: the measured optimum for the decoder's shapes
+            // (5632 x 2048 and 2048 x 5632); paired epilogues need it anyway
+            int ri = p.N >= 1024 ? 2 : 1;
+            if (pair_epi) ri = 2;
+            if (wt == TLHIP_Q4_0) done = launch_mx<TLHIP_Q4_0>(s, p, nb, ri);
+            else if (wt == TLHIP_Q8_0) done = launch_mx<TLHIP_Q8_0>(s, p, nb, ri);
+            else done = launch_mx<TLHIP_F16>(s, p, nb, ri);
+        }
     }
     if (!done) {
-        if (wt != TLHIP_F16 || epi == EPI_SWIGLU_PAIR)
+        if (wt != TLHIP_F16 || pair_epi || normed)
             return fail(TLHIP_ERR_INVALID_OPERATION, "gemv: unsupported shape M=%d K=%d", p.M, p.K);
         int64_t waves = (int64_t)p.N * p.M;
         hipLaunchKernelGGL(gemv_generic_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, p);
     }
+    return TLHIP_OK;
+}
+
+// Final step of the fused greedy argmax: the largest of the workgroup keys
+// (value, then index) is the token; advances the device decode state
+// {token, pos, step} and logs the token, as argmax_kernel does.
+__global__ __launch_bounds__(256) void argmax_slots_kernel(const unsigned long long* __restrict__ slots, int n,
+                                                           int32_t* out, int32_t* token_log, int32_t* d_state) {
+    __shared__ unsigned long long wk[4];
+    const int32_t step = d_state ? d_state[2] : 0;   // loaded with the keys, not after them
+    unsigned long long b = 0ull;
+    for (int i = threadIdx.x; i < n; i += 256) b = umax64(b, slots[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)b, off, 64), hi = __shfl_xor((uint32_t)(b >> 32), off, 64);
+        b = umax64(b, ((unsigned long long)hi << 32) | lo);
+    }
+    if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = b;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        b = umax64(umax64(wk[0], wk[1]), umax64(wk[2], wk[3]));
+        const int tok = (b >> 32) == 0ull ? 0 : (int)(uint32_t)b;
+        if (out) out[0] = tok;
+        if (d_state) {
+            if (token_log) token_log[step] = tok;
+            d_state[0] = tok;
+            d_state[1] += 1;
+            d_state[2] = step + 1;
+        }
+    }
+}
+
+tlhip_status launch_argmax_slots(hipStream_t s, const unsigned long long* slots, int n, int32_t* out,
+                                 int32_t* token_log, int32_t* d_state) {
+    if (n <= 0) return fail(TLHIP_ERR_INVALID_DIMENSION, "argmax over no slots");
+    hipLaunchKernelGGL(argmax_slots_kernel, dim3(1), dim3(256), 0, s, slots, n, out, token_log, d_state);
     return TLHIP_OK;
 }
 

@@ -61,6 +61,7 @@ struct tlhip_model_s {
     // activations, sized for max_rows tokens per pass
     tlhip_tensor x = nullptr, xn = nullptr, qkv = nullptr, qrot = nullptr, att = nullptr, hmid = nullptr,
                  logits = nullptr;
+    unsigned long long* d_amax = nullptr;   // per-workgroup greedy keys of the lm_head GEMV
     int32_t* d_state = nullptr;   // {token, pos, step}
     int32_t* d_tokens = nullptr;  // token log
     int32_t* d_ids = nullptr;     // prompt ids
@@ -196,58 +197,136 @@ tlhip_status linear_into(hipStream_t s, const Lin& l, const uint16_t* x, int M, 
     return launch_gemm(s, l.w->dtype, a, epi);
 }
 
+// One activation row through norm -> linear in a single GEMV launch: the
+// normalisation (rms_norm or layer_norm with the reference's formula and
+// f16 store) is formed in registers by every wave.
+GemvArgs fused_norm_args(tlhip_model m, const Lin& l, const uint16_t* x, tlhip_tensor nw, tlhip_tensor nb) {
+    GemvArgs a;
+    a.x = x;
+    a.wq = l.w->data;
+    a.wd = l.w->scales;
+    a.bias = l.b ? P(l.b) : nullptr;
+    a.M = 1;
+    a.N = (int)l.w->shape[0];
+    a.K = (int)l.w->shape[1];
+    a.pro = m->arch == 0 ? PRO_RMS : PRO_LN;
+    a.norm_w = P(nw);
+    a.norm_b = nb ? P(nb) : nullptr;
+    a.eps = m->eps;
+    return a;
+}
+
 // Enqueues the layers and the head for S tokens at positions pos0.. (plus
 // *d_pos when given), ending with the argmax that updates d_state.
+// A single-row pass (every decode step) runs five launches per llama layer:
+//   [rms_norm + qkv + rope + cache write] [attention] [o + residual]
+//   [rms_norm + gate/up + silu*mul] [down + residual]
+// and norm + lm_head as one launch; longer passes run the unfused sequence
+// with the MFMA GEMM.
 tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_dev, bool decode) {
     hipStream_t s = m->ctx->stream;
     const int H = m->hidden, D = m->head_dim, NH = m->n_heads, NKV = m->n_kv, kvd = NKV * D;
     const int32_t* d_pos = decode ? m->d_state + 1 : nullptr;
-    TLHIP_TRY(launch_embedding(s, m->embd->dtype, m->embd->data, m->embd->scales, ids_dev,
-                               decode ? m->d_state : nullptr, P(m->x), S, H));
+    const bool row1 = S == 1;
+    // decode with an f16 table: the embedding row is read by layer 0's fused
+    // norm + QKV GEMV directly (and copied to the residual stream there)
+    const bool embd_fused = decode && m->embd->dtype == TLHIP_F16;
+    if (!embd_fused)
+        TLHIP_TRY(launch_embedding(s, m->embd->dtype, m->embd->data, m->embd->scales, ids_dev,
+                                   decode ? m->d_state : nullptr, P(m->x), S, H));
+    auto embed_into = [&](GemvArgs& a, int li) {
+        if (embd_fused && li == 0) {
+            a.embd = P(m->embd);
+            a.d_token = m->d_state;
+            a.x_out = P(m->x);
+        }
+    };
     const int qkv_w = H + 2 * kvd;
     for (int li = 0; li < m->n_layers; li++) {
         Layer& L = m->layers[li];
         uint16_t* kc = P(m->kv->k[li]);
         uint16_t* vc = P(m->kv->v[li]);
-        if (m->arch == 0) TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.norm_w), P(m->xn), S, H, m->eps));
-        else TLHIP_TRY(launch_layer_norm(s, P(m->x), P(L.norm_w), P(L.norm_b), P(m->xn), S, H, m->eps));
-        TLHIP_TRY(linear_into(s, L.qkv, P(m->xn), S, P(m->qkv), L.qkv.b ? EPI_BIAS : EPI_STORE, nullptr));
-        TLHIP_TRY(launch_rope_kv(s, P(m->qkv), qkv_w, S, NH, NKV, D, m->arch == 0 ? 0 : 1, m->rot, m->rope_tab,
-                                 decode ? 0 : pos0, d_pos, P(m->qrot), kc, vc));
-        AttnArgs a;
-        a.q = P(m->qrot);
-        a.k = kc;
-        a.v = vc;
-        a.out = P(m->att);
-        a.S = S;
-        a.H = NH;
-        a.Hkv = NKV;
-        a.D = D;
-        a.causal = 1;
-        a.scale_h = (float)(_Float16)(1.0f / sqrtf((float)D));
-        if (decode) {
+        if (row1 && m->arch == 0) {
+            GemvArgs a = fused_norm_args(m, L.qkv, P(m->x), L.norm_w, nullptr);
+            embed_into(a, li);
+            a.nq = H;
+            a.nk = kvd;
+            a.head_dim = D;
+            a.rot = m->rot;
+            a.layout = 0;
+            a.pos0 = decode ? 0 : pos0;
             a.d_pos = d_pos;
-            TLHIP_TRY(launch_attention(s, a));
+            a.rope_tab = m->rope_tab;
+            a.q_out = P(m->qrot);
+            a.kc = kc;
+            a.vc = vc;
+            TLHIP_TRY(launch_gemv(s, L.qkv.w->dtype, a, EPI_QKV_ROPE));
         } else {
-            a.q_pos0 = pos0;
-            TLHIP_TRY(launch_attention_j(s, a, pos0 + S));
+            if (row1) {
+                GemvArgs a = fused_norm_args(m, L.qkv, P(m->x), L.norm_w, L.norm_b);
+                embed_into(a, li);
+                a.y = P(m->qkv);
+                TLHIP_TRY(launch_gemv(s, L.qkv.w->dtype, a, L.qkv.b ? EPI_BIAS : EPI_STORE));
+            } else {
+                if (m->arch == 0) TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.norm_w), P(m->xn), S, H, m->eps));
+                else TLHIP_TRY(launch_layer_norm(s, P(m->x), P(L.norm_w), P(L.norm_b), P(m->xn), S, H, m->eps));
+                TLHIP_TRY(linear_into(s, L.qkv, P(m->xn), S, P(m->qkv), L.qkv.b ? EPI_BIAS : EPI_STORE, nullptr));
+            }
+            TLHIP_TRY(launch_rope_kv(s, P(m->qkv), qkv_w, S, NH, NKV, D, m->arch == 0 ? 0 : 1, m->rot,
+                                     m->rope_tab, decode ? 0 : pos0, d_pos, P(m->qrot), kc, vc));
+        }
+        AttnArgs at;
+        at.q = P(m->qrot);
+        at.k = kc;
+        at.v = vc;
+        at.out = P(m->att);
+        at.S = S;
+        at.H = NH;
+        at.Hkv = NKV;
+        at.D = D;
+        at.causal = 1;
+        at.kv_rows = m->max_ctx;
+        at.scale_h = (float)(_Float16)(1.0f / sqrtf((float)D));
+        if (decode) {
+            at.d_pos = d_pos;
+            TLHIP_TRY(launch_attention(s, at));
+        } else {
+            at.q_pos0 = pos0;
+            TLHIP_TRY(launch_attention_j(s, at, pos0 + S));
         }
         if (m->arch == 0) {
             TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_RESID, P(m->x)));
-            TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.ffn_norm_w), P(m->xn), S, H, m->eps));
-            TLHIP_TRY(linear_into(s, L.gu, P(m->xn), S, P(m->hmid), EPI_SWIGLU_PAIR, nullptr));
+            if (row1) {
+                GemvArgs a = fused_norm_args(m, L.gu, P(m->x), L.ffn_norm_w, nullptr);
+                a.y = P(m->hmid);
+                TLHIP_TRY(launch_gemv(s, L.gu.w->dtype, a, EPI_SWIGLU_PAIR));
+            } else {
+                TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.ffn_norm_w), P(m->xn), S, H, m->eps));
+                TLHIP_TRY(linear_into(s, L.gu, P(m->xn), S, P(m->hmid), EPI_SWIGLU_PAIR, nullptr));
+            }
             TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_RESID, P(m->x)));
         } else {
+            // phi2: the MLP reads the same layer_norm output as attention
+            if (row1) {
+                GemvArgs a = fused_norm_args(m, L.up, P(m->x), L.norm_w, L.norm_b);
+                a.y = P(m->hmid);
+                TLHIP_TRY(launch_gemv(s, L.up.w->dtype, a, EPI_BIAS_GELU));
+            }
             TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_BIAS_RESID, P(m->x)));
-            TLHIP_TRY(linear_into(s, L.up, P(m->xn), S, P(m->hmid), EPI_BIAS_GELU, nullptr));
+            if (!row1) TLHIP_TRY(linear_into(s, L.up, P(m->xn), S, P(m->hmid), EPI_BIAS_GELU, nullptr));
             TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_BIAS_RESID, P(m->x)));
         }
     }
     const uint16_t* last = P(m->x) + (size_t)(S - 1) * H;
-    if (m->arch == 0) TLHIP_TRY(launch_rms_norm(s, last, P(m->out_norm_w), P(m->xn), 1, H, m->eps));
-    else TLHIP_TRY(launch_layer_norm(s, last, P(m->out_norm_w), P(m->out_norm_b), P(m->xn), 1, H, m->eps));
-    TLHIP_TRY(linear_into(s, m->out, P(m->xn), 1, P(m->logits), m->out.b ? EPI_BIAS : EPI_STORE, nullptr));
-    TLHIP_TRY(launch_argmax(s, P(m->logits), m->vocab, nullptr, m->d_tokens, m->d_state));
+    {
+        // final norm + lm_head (+ bias) + per-workgroup greedy keys, then the
+        // one-workgroup reduction that picks the token and advances d_state
+        GemvArgs a = fused_norm_args(m, m->out, last, m->out_norm_w, m->out_norm_b);
+        a.y = P(m->logits);
+        a.amax_slots = m->d_amax;
+        TLHIP_TRY(launch_gemv(s, m->out.w->dtype, a, EPI_ARGMAX));
+    }
+    TLHIP_TRY(launch_argmax_slots(s, m->d_amax, gemv_norm_slots(m->vocab), nullptr, m->d_tokens, m->d_state));
     return TLHIP_OK;
 }
 
@@ -444,6 +523,7 @@ tlhip_status tlhip_model_free(tlhip_model m) {
     free_lin(m->out);
     tlhip_kvcache_free(m->kv);
     for (tlhip_tensor t : {m->x, m->xn, m->qkv, m->qrot, m->att, m->hmid, m->logits}) tlhip_tensor_free(t);
+    if (m->d_amax) (void)hipFree(m->d_amax);
     if (m->d_state) (void)hipFree(m->d_state);
     if (m->d_tokens) (void)hipFree(m->d_tokens);
     if (m->d_ids) (void)hipFree(m->d_ids);
@@ -544,6 +624,7 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
         if ((st = alloc_tensor(ctx, TLHIP_F16, 2, s_h, &m->hmid)) != TLHIP_OK) break;
         if ((st = alloc_tensor(ctx, TLHIP_F16, 1, s_l, &m->logits)) != TLHIP_OK) break;
         hipError_t e = hipMalloc(&m->d_state, 4 * sizeof(int32_t));
+        if (e == hipSuccess) e = hipMalloc(&m->d_amax, sizeof(unsigned long long) * gemv_norm_slots(m->vocab));
         if (e == hipSuccess) e = hipMalloc(&m->d_tokens, sizeof(int32_t) * (max_ctx + 1));
         if (e == hipSuccess) e = hipMalloc(&m->d_ids, sizeof(int32_t) * R);
         if (e == hipSuccess) e = hipHostMalloc(&m->h_state, 4 * sizeof(int32_t), hipHostMallocDefault);
@@ -623,23 +704,51 @@ tlhip_status tlhip_model_logits(tlhip_model m, uint16_t* host, size_t n) {
 // measurement helpers
 // ---------------------------------------------------------------------------
 tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tensor* w, int n_w, tlhip_tensor y,
-                                int iters, float* avg_us) {
+                                int iters, int per_launch, float* avg_us) {
     TLHIP_TRY(check_ctx(ctx));
     if (!w || n_w <= 0 || iters <= 0 || !avg_us) return fail(TLHIP_ERR_INVALID_ARGUMENT, "bad bench arguments");
     for (int i = 0; i < n_w; i++) TLHIP_TRY(tlhip_linear(ctx, x, w[i], nullptr, y));   // checks + warm-up
     TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
     Lin l;
-    TLHIP_CHECK_HIP(hipEventRecord(ctx->ev0, ctx->stream));
-    for (int i = 0; i < iters; i++) {
-        l.w = w[i % n_w];
-        TLHIP_TRY(linear_into(ctx->stream, l, P(x), (int)x->shape[0], P(y), EPI_STORE, nullptr));
+    if (!per_launch) {
+        TLHIP_CHECK_HIP(hipEventRecord(ctx->ev0, ctx->stream));
+        for (int i = 0; i < iters; i++) {
+            l.w = w[i % n_w];
+            TLHIP_TRY(linear_into(ctx->stream, l, P(x), (int)x->shape[0], P(y), EPI_STORE, nullptr));
+        }
+        TLHIP_CHECK_HIP(hipEventRecord(ctx->ev1, ctx->stream));
+        TLHIP_CHECK_HIP(hipEventSynchronize(ctx->ev1));
+        float ms = 0.f;
+        TLHIP_CHECK_HIP(hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
+        *avg_us = ms * 1000.0f / (float)iters;
+        return TLHIP_OK;
     }
-    TLHIP_CHECK_HIP(hipEventRecord(ctx->ev1, ctx->stream));
-    TLHIP_CHECK_HIP(hipEventSynchronize(ctx->ev1));
-    float ms = 0.f;
-    TLHIP_CHECK_HIP(hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1));
-    *avg_us = ms * 1000.0f / (float)iters;
-    return TLHIP_OK;
+    // one event pair around every launch: the mean of the bracketed times
+    std::vector<hipEvent_t> ev(2 * (size_t)iters, nullptr);
+    tlhip_status st = TLHIP_OK;
+    for (auto& e : ev)
+        if (hipEventCreate(&e) != hipSuccess) {
+            st = fail(TLHIP_ERR_DEVICE, "hipEventCreate failed");
+            break;
+        }
+    double total = 0.0;
+    for (int i = 0; i < iters && st == TLHIP_OK; i++) {
+        l.w = w[i % n_w];
+        if (hipEventRecord(ev[2 * i], ctx->stream) != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "hipEventRecord");
+        if (st == TLHIP_OK) st = linear_into(ctx->stream, l, P(x), (int)x->shape[0], P(y), EPI_STORE, nullptr);
+        if (st == TLHIP_OK && hipEventRecord(ev[2 * i + 1], ctx->stream) != hipSuccess)
+            st = fail(TLHIP_ERR_DEVICE, "hipEventRecord");
+    }
+    if (st == TLHIP_OK && hipStreamSynchronize(ctx->stream) != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "sync");
+    for (int i = 0; i < iters && st == TLHIP_OK; i++) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]) != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "elapsed");
+        total += ms;
+    }
+    for (auto e : ev)
+        if (e) (void)hipEventDestroy(e);
+    if (st == TLHIP_OK) *avg_us = (float)(total * 1000.0 / iters);
+    return st;
 }
 
 tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode, int use_graph,

@@ -391,8 +391,11 @@ class Model:
         return out, pm.value, dm.value
 
 
-def bench_linear(dev: Device, x: Tensor, ws: Sequence[Tensor], y: Tensor, iters: int) -> float:
+def bench_linear(dev: Device, x: Tensor, ws: Sequence[Tensor], y: Tensor, iters: int,
+                 per_launch: bool = False) -> float:
+    """Mean us per linear launch (hipEvents): back-to-back throughput, or
+    with per_launch every launch bracketed by its own event pair."""
     arr = (_vp * len(ws))(*[w.h for w in ws])
     us = C.c_float()
-    call("tlhip_bench_linear", dev.h, x.h, arr, len(ws), y.h, iters, C.byref(us))
+    call("tlhip_bench_linear", dev.h, x.h, arr, len(ws), y.h, iters, int(per_launch), C.byref(us))
     return us.value
