@@ -8,18 +8,24 @@ greedy decode with an f16 KV cache at batch 1.  A "step" is one decode token:
 `value` = decode tokens / second (prompt prefill excluded), timed with hipEvents
 on the runner's stream, inputs and weights resident in HBM.
 
-Alongside: the dominant kernel's roofline (Q4_0 dequant-GEMV, W [5632 x 2048],
-6,503,424 algorithmic bytes per launch, cycling over 48 weight copies so the
-weights come from HBM, not the 256 MB MALL) and the CPU oracle's restatement
-of the reference CPU path timed on this host.
+Alongside: the dominant kernel's roofline -- the Q4_0 dequant-GEMV at
+5632 x 2048 (6,503,424 algorithmic bytes per launch), launched back to back
+over 48 weight copies (312 MB, more than the 256 MB MALL) so the weights come
+from HBM, timed with hipEvents around the launches on the context stream --
+and the CPU oracle's restatement of the reference CPU path timed on this host.
+`roofline.traffic` is the HBM bytes per launch the profiler counted for that
+kernel (FETCH_SIZE + WRITE_SIZE, scaled by the same counters on a plain copy
+of known size), read from the committed summary under profiles/.
 
     python bench.py [--gpus 1] [--steps 128] [--warmup 16]
+    python bench.py --part gemv        # the GEMV / copy legs only (profiler passes)
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import tempfile
 import time
@@ -30,6 +36,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+GEMV_KERNEL = "gemv_kernel<3, 1, 2, 1> (Q4_0 fused dequant-GEMV, 2 rows per wave)"
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_q4_0_5632x2048_pmc.txt")
 
 
 def log(msg: str) -> None:
@@ -37,7 +45,13 @@ def log(msg: str) -> None:
 
 
 def gemv_roofline(dev, iters: int, copies: int = 48):
-    """Q4_0 GEMV at 2048 x 5632 in both orientations; returns dict of results."""
+    """Q4_0 GEMV at 2048 x 5632 in both orientations; returns dict of results.
+
+    stream_us (the reported figure) = hipEvents around `iters` back-to-back
+    launches / iters; it agrees with the profiler's per-kernel duration
+    because consecutive launches leave no gap on this device.  event_us
+    brackets every launch with its own event pair (adds the events' own
+    cost, ~2 us)."""
     from tensorlogic_amd import Q4_0, bench_linear
     from tensorlogic_amd import synth as S
     out = {}
@@ -46,13 +60,35 @@ def gemv_roofline(dev, iters: int, copies: int = 48):
         ws = [dev.quantized(blocks, (N, K), Q4_0) for _ in range(copies)]
         x = dev.tensor(S.normal_f16(101, "bench_x", (1, K)))
         y = dev.empty((1, N))
-        us = bench_linear(dev, x, ws, y, iters, per_launch=True)
         us_stream = bench_linear(dev, x, ws, y, iters, per_launch=False)
+        us_event = bench_linear(dev, x, ws, y, max(iters // 4, 16), per_launch=True)
         algo = N * K // 32 * 18 + 2 * K + 2 * N
-        out[f"{N}x{K}"] = dict(avg_us=us, stream_us=us_stream, bytes=algo, gbs=algo / us / 1e3)
+        out[f"{N}x{K}"] = dict(stream_us=us_stream, event_us=us_event, bytes=algo, gbs=algo / us_stream / 1e3)
         del ws
         dev.sync()
     return out
+
+
+def copy_reference(dev, iters: int):
+    """Plain copy kernel: 6.5 MB (the GEMV's size, 48 rotating sources) and
+    1 GiB -- the streaming bandwidth this device reaches at each size."""
+    from tensorlogic_amd import bench_copy
+    res = {}
+    for label, nbytes, nbuf, it in (("6.5MB", 6503424 // 16 * 16, 48, iters), ("1GiB", 1 << 30, 2, 10)):
+        us = bench_copy(dev, nbytes, nbuf, it)
+        res[label] = dict(bytes=nbytes, us=us, gbs_read=nbytes / us / 1e3, gbs_rw=2 * nbytes / us / 1e3)
+    return res
+
+
+def pmc_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed PMC
+    summary (None when absent)."""
+    try:
+        text = open(PMC_SUMMARY).read()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch\s*=\s*(\d+)", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def cpu_baseline(path: str, prompt, threads: int = 1):
@@ -85,6 +121,8 @@ def main():
     ap.add_argument("--decode-launch", choices=("graph", "direct"), default="graph",
                     help="replay one captured HIP graph per decode step (default) or launch the same "
                          "kernels one by one (profiler runs)")
+    ap.add_argument("--part", choices=("all", "gemv"), default="all",
+                    help="'gemv': only the GEMV roofline and copy legs (for counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (asked for {args.gpus}); the hot path is "
@@ -93,6 +131,19 @@ def main():
 
     from tensorlogic_amd import Device, Model
     from tensorlogic_amd import synth as S
+
+    dev = Device(0)
+    log(f"device: {dev.name()}")
+    if args.part == "gemv":
+        gem = gemv_roofline(dev, args.gemv_iters)
+        cp = copy_reference(dev, args.gemv_iters)
+        for k, v in gem.items():
+            log(f"Q4_0 GEMV {k}: {v['stream_us']:.2f} us/launch, {v['gbs']:.0f} GB/s")
+        for k, v in cp.items():
+            log(f"copy {k}: {v['us']:.2f} us, {v['gbs_rw']:.0f} GB/s read+write")
+        dev.close()
+        print(json.dumps({"gemv": gem, "copy": cp}), flush=True)
+        return
 
     seed = 4
     n_prompt = 46
@@ -104,13 +155,11 @@ def main():
         log(f"wrote synthetic TinyLlama Q4_0 GGUF ({os.path.getsize(path) / 1e6:.0f} MB) in {time.time() - t0:.1f} s")
     prompt = S.token_ids(seed, "prompt", n_prompt, S.TINYLLAMA_ARGS["vocab"])
 
-    dev = Device(0)
-    log(f"device: {dev.name()}")
     t0 = time.time()
     max_ctx = n_prompt + max(args.steps, args.warmup) + 8
     m = Model(dev, path, arch=0, max_ctx=max_ctx)
     log(f"model loaded in {time.time() - t0:.1f} s")
-    # warm-up: prefill + W graph-replayed decode steps (also captures the graph)
+    # warm-up: prefill + W decode steps (captures the graph on first use)
     use_graph = args.decode_launch == "graph"
     m.generate(prompt, args.warmup, use_graph=use_graph)
     dev.sync()
@@ -123,8 +172,11 @@ def main():
 
     gem = gemv_roofline(dev, args.gemv_iters)
     for k, v in gem.items():
-        log(f"Q4_0 GEMV {k}: {v['avg_us']:.2f} us/launch (event pair per launch; back-to-back "
-            f"{v['stream_us']:.2f} us), {v['gbs']:.0f} GB/s ({v['gbs'] / HBM_PEAK_GBS:.1%} of peak)")
+        log(f"Q4_0 GEMV {k}: {v['stream_us']:.2f} us/launch back to back ({v['event_us']:.2f} us with an "
+            f"event pair per launch), {v['gbs']:.0f} GB/s ({v['gbs'] / HBM_PEAK_GBS:.1%} of peak)")
+    cp = copy_reference(dev, args.gemv_iters)
+    for k, v in cp.items():
+        log(f"copy {k}: {v['us']:.2f} us, {v['gbs_rw']:.0f} GB/s read+write")
     g = gem["5632x2048"]
     dev.close()
 
@@ -160,19 +212,21 @@ def main():
                         "46-token prompt, greedy decode at batch 1, f16 KV cache",
             "prompt_tokens": n_prompt,
             "prefill_ms": round(prefill_ms, 3),
+            "decode_launch": args.decode_launch,
             "decode_tokens": toks.tolist()[:8],
             "hbm_bytes_per_token": weights_per_token,
             "decode_hbm_roofline_frac": round(tok_s * weights_per_token / (HBM_PEAK_GBS * 1e9), 4),
             "gemv_2048x5632": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in gem.items()},
+            "copy_reference": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in cp.items()},
         },
         "roofline": {
-            "kernel": "gemv_kernel<Q4_0> W[5632 x 2048] (fused dequant-GEMV)",
+            "kernel": GEMV_KERNEL,
             "bound": "hbm",
             "achieved": round(g["gbs"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": pmc_traffic(),
         },
         "cpu_baseline": cpu,
     }

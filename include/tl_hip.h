@@ -217,6 +217,12 @@ tlhip_status tlhip_model_dims(tlhip_model m, int32_t* dims8);
  * per_launch = 1 brackets every launch with its own event pair.           */
 tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tensor* w, int n_w,
                                 tlhip_tensor y, int iters, int per_launch, float* avg_us);
+/* Copies `bytes` (multiple of 16) from one of n_buf source buffers to one
+ * destination `iters` times with a plain 16-byte-per-lane copy kernel, back
+ * to back, and returns the mean us per copy (hipEvents): the streaming
+ * bandwidth reference of the device and the known-size kernel that scales
+ * the profiler's HBM byte counters.  Allocates and frees its own buffers. */
+tlhip_status tlhip_bench_copy(tlhip_ctx ctx, size_t bytes, int n_buf, int iters, float* avg_us);
 /* Times `n_decode` greedy steps after a prefill (use_graph = 1: one
  * captured HIP graph replayed per step; 0: the same kernels launched one
  * by one); returns the prefill and total decode ms (hipEvents on the

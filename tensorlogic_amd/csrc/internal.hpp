@@ -197,6 +197,7 @@ struct AttnArgs {
     int q_stride = 0, out_stride = 0;  // row strides (elements); 0 = H*D
     int kv_rows = 0;              // rows allocated in k / v (bounds early loads); 0 = J
 };
+tlhip_status launch_stream_copy(hipStream_t s, const void* src, void* dst, size_t bytes);
 tlhip_status launch_transpose(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows, int cols);
 tlhip_status launch_attention(hipStream_t s, const AttnArgs& a);   // decode: J from *d_pos
 tlhip_status launch_attention_j(hipStream_t s, const AttnArgs& a, int J);

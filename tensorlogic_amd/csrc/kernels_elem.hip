@@ -4,6 +4,8 @@
 //
 // Each kernel stores f16 exactly where the reference stores f16 and computes
 // in f32 in between, following the reference op named beside it.
+#include <algorithm>
+
 #include "device_common.hpp"
 #include "internal.hpp"
 
@@ -454,6 +456,22 @@ tlhip_status launch_copy_rows(hipStream_t s, const uint16_t* src, uint16_t* dst,
     if (total <= 0) return TLHIP_OK;
     hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, src,
                        dst, rows, row_elems, src_stride, dst_stride, d_pos, dst_row0);
+    return TLHIP_OK;
+}
+
+// Plain 16-byte-per-lane copy (measurement reference: the bandwidth a
+// streaming kernel reaches on this device, and the scale of the profiler's
+// FETCH_SIZE / WRITE_SIZE counters for a known byte count).
+__global__ void stream_copy_kernel(const u4* __restrict__ src, u4* __restrict__ dst, size_t n) {
+    const size_t step = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) dst[i] = src[i];
+}
+
+tlhip_status launch_stream_copy(hipStream_t s, const void* src, void* dst, size_t bytes) {
+    const size_t n = bytes / 16;
+    if (n == 0) return TLHIP_OK;
+    const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(stream_copy_kernel, dim3(grid), dim3(256), 0, s, (const u4*)src, (u4*)dst, n);
     return TLHIP_OK;
 }
 

@@ -751,6 +751,34 @@ tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tenso
     return st;
 }
 
+tlhip_status tlhip_bench_copy(tlhip_ctx ctx, size_t bytes, int n_buf, int iters, float* avg_us) {
+    TLHIP_TRY(check_ctx(ctx));
+    if (bytes < 16 || bytes % 16 || n_buf <= 0 || iters <= 0 || !avg_us)
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "bench_copy: bytes must be a positive multiple of 16");
+    std::vector<void*> src(n_buf, nullptr);
+    void* dst = nullptr;
+    tlhip_status st = TLHIP_OK;
+    for (auto& b : src)
+        if (hipMalloc(&b, bytes) != hipSuccess) st = fail(TLHIP_ERR_ALLOCATION, "bench_copy: %zu bytes", bytes);
+    if (st == TLHIP_OK && hipMalloc(&dst, bytes) != hipSuccess) st = fail(TLHIP_ERR_ALLOCATION, "bench_copy");
+    for (auto b : src)
+        if (st == TLHIP_OK && hipMemsetAsync(b, 1, bytes, ctx->stream) != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "memset");
+    for (int i = 0; i < n_buf && st == TLHIP_OK; i++) st = launch_stream_copy(ctx->stream, src[i], dst, bytes);
+    if (st == TLHIP_OK && hipStreamSynchronize(ctx->stream) != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "sync");
+    float ms = 0.f;
+    if (st == TLHIP_OK && hipEventRecord(ctx->ev0, ctx->stream) != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "event");
+    for (int i = 0; i < iters && st == TLHIP_OK; i++) st = launch_stream_copy(ctx->stream, src[i % n_buf], dst, bytes);
+    if (st == TLHIP_OK && hipEventRecord(ctx->ev1, ctx->stream) != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "event");
+    if (st == TLHIP_OK && hipEventSynchronize(ctx->ev1) != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "sync");
+    if (st == TLHIP_OK && hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1) != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "elapsed");
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto b : src)
+        if (b) (void)hipFree(b);
+    if (dst) (void)hipFree(dst);
+    if (st == TLHIP_OK) *avg_us = ms * 1000.0f / (float)iters;
+    return st;
+}
+
 tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode, int use_graph,
                                 int32_t* tokens_out, float* prefill_ms, float* decode_ms) {
     if (!m || !prompt || !tokens_out || !prefill_ms || !decode_ms)

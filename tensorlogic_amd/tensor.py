@@ -399,3 +399,10 @@ def bench_linear(dev: Device, x: Tensor, ws: Sequence[Tensor], y: Tensor, iters:
     us = C.c_float()
     call("tlhip_bench_linear", dev.h, x.h, arr, len(ws), y.h, iters, int(per_launch), C.byref(us))
     return us.value
+
+
+def bench_copy(dev: Device, nbytes: int, n_buf: int, iters: int) -> float:
+    """Mean us per back-to-back plain copy of nbytes (cycling n_buf sources)."""
+    us = C.c_float()
+    call("tlhip_bench_copy", dev.h, nbytes, n_buf, iters, C.byref(us))
+    return us.value
