@@ -69,6 +69,29 @@ def gemv_roofline(dev, iters: int, copies: int = 48):
     return out
 
 
+def config2_q8(dev, iters: int, copies: int = 24):
+    """Config 2: Q8_0 linear at TinyLlama FFN shapes, M = 1 (GEMV, HBM GB/s)
+    and M = 46 / 512 (MFMA GEMM, TFLOP/s), back-to-back hipEvent timing over
+    rotating weight copies."""
+    from tensorlogic_amd import Q8_0, bench_linear
+    from tensorlogic_amd import synth as S
+    res = {}
+    for (N, K) in ((5632, 2048), (2048, 5632)):
+        blocks = S.q8_0_blocks(102, f"bench_q8_W{N}x{K}", N, K)
+        ws = [dev.quantized(blocks, (N, K), Q8_0) for _ in range(copies)]
+        for M in (1, 46, 512):
+            x = dev.tensor(S.normal_f16(102, f"bench_q8_x{M}x{K}", (M, K)))
+            y = dev.empty((M, N))
+            us = bench_linear(dev, x, ws, y, iters if M == 1 else max(iters // 4, 20))
+            wbytes = N * K // 32 * 34
+            byt = wbytes + 2 * M * K + 2 * M * N
+            fl = 2.0 * M * N * K
+            res[f"M{M}_{N}x{K}"] = dict(us=us, gbs=byt / us / 1e3, tflops=fl / us / 1e6)
+        del ws
+        dev.sync()
+    return res
+
+
 def copy_reference(dev, iters: int):
     """Plain copy kernel: 6.5 MB (the GEMV's size, 48 rotating sources) and
     1 GiB -- the streaming bandwidth this device reaches at each size."""
@@ -121,8 +144,9 @@ def main():
     ap.add_argument("--decode-launch", choices=("graph", "direct"), default="graph",
                     help="replay one captured HIP graph per decode step (default) or launch the same "
                          "kernels one by one (profiler runs)")
-    ap.add_argument("--part", choices=("all", "gemv"), default="all",
-                    help="'gemv': only the GEMV roofline and copy legs (for counter passes)")
+    ap.add_argument("--part", choices=("all", "gemv", "gemm"), default="all",
+                    help="'gemv': only the GEMV roofline and copy legs (for counter passes); "
+                         "'gemm': only the config-2 Q8_0 GEMV/GEMM leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (asked for {args.gpus}); the hot path is "
@@ -134,6 +158,13 @@ def main():
 
     dev = Device(0)
     log(f"device: {dev.name()}")
+    if args.part == "gemm":
+        c2 = config2_q8(dev, 200)
+        for k, v in c2.items():
+            log(f"Q8_0 {k}: {v['us']:.2f} us, {v['gbs']:.0f} GB/s, {v['tflops']:.1f} TFLOP/s")
+        dev.close()
+        print(json.dumps({"config2": c2}), flush=True)
+        return
     if args.part == "gemv":
         gem = gemv_roofline(dev, args.gemv_iters)
         cp = copy_reference(dev, args.gemv_iters)
@@ -177,6 +208,9 @@ def main():
     cp = copy_reference(dev, args.gemv_iters)
     for k, v in cp.items():
         log(f"copy {k}: {v['us']:.2f} us, {v['gbs_rw']:.0f} GB/s read+write")
+    c2 = config2_q8(dev, 200)
+    for k, v in c2.items():
+        log(f"Q8_0 {k}: {v['us']:.2f} us, {v['gbs']:.0f} GB/s, {v['tflops']:.1f} TFLOP/s")
     g = gem["5632x2048"]
     dev.close()
 
@@ -218,6 +252,7 @@ def main():
             "decode_hbm_roofline_frac": round(tok_s * weights_per_token / (HBM_PEAK_GBS * 1e9), 4),
             "gemv_2048x5632": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in gem.items()},
             "copy_reference": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in cp.items()},
+            "config2_q8_0": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c2.items()},
         },
         "roofline": {
             "kernel": GEMV_KERNEL,

@@ -30,6 +30,35 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
     return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
+// GGUF payload -> f16 pairs.  A byte b placed under the high byte 0x64 is
+// the f16 1024 + b, so (1024 + q) - 1032 = q - 8 (Q4_0) and, after the xor
+// that offsets int8 by 128, (1024 + q + 128) - 1152 = q (Q8_0), both exact;
+// the multiply by the block scale d is then the one correctly rounded
+// product RNE_f16((q - 8) * d) / RNE_f16(q * d) of the reference's
+// dequantisation.  perm(X, Y, sel) takes byte i from sel byte i: 0-3 = Y's
+// bytes, 4-7 = X's.
+// Q4_0: bytes j..j+3 of the 16 payload bytes hold elements j..j+3 in their
+// low nibbles and j+16..j+19 in their high nibbles; out = (e0,e2) (e1,e3)
+// (e16,e18) (e17,e19) relative to j.
+__device__ __forceinline__ void q4_unpack(uint32_t w, h2 dd, h2 out[4]) {
+    const h2 bias = {(h16)-1032.0f, (h16)-1032.0f};
+    const uint32_t k = 0x64646464u;
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    out[0] = (as_h2(__builtin_amdgcn_perm(k, lo, 0x04020400u)) + bias) * dd;
+    out[1] = (as_h2(__builtin_amdgcn_perm(k, lo, 0x04030401u)) + bias) * dd;
+    out[2] = (as_h2(__builtin_amdgcn_perm(k, hi, 0x04020400u)) + bias) * dd;
+    out[3] = (as_h2(__builtin_amdgcn_perm(k, hi, 0x04030401u)) + bias) * dd;
+}
+
+// Q8_0: four int8 (e0..e3) -> (e0,e2) (e1,e3).
+__device__ __forceinline__ void q8_unpack(uint32_t w, h2 dd, h2 out[2]) {
+    const h2 bias = {(h16)-1152.0f, (h16)-1152.0f};
+    const uint32_t k = 0x64646464u;
+    const uint32_t v = w ^ 0x80808080u;
+    out[0] = (as_h2(__builtin_amdgcn_perm(k, v, 0x04020400u)) + bias) * dd;
+    out[1] = (as_h2(__builtin_amdgcn_perm(k, v, 0x04030401u)) + bias) * dd;
+}
+
 __device__ __forceinline__ float fdot2(h2 a, h2 b, float c) {
     return __builtin_amdgcn_fdot2(a, b, c, false);
 }

@@ -133,6 +133,9 @@ struct GemvArgs {
     uint16_t* x_out = nullptr;
     // EPI_ARGMAX: one (value, index) key per workgroup, gemv_norm_slots(N) of them
     unsigned long long* amax_slots = nullptr;
+    // GEMM split-K workspace (fp32 partials); none = no split
+    float* ws = nullptr;
+    size_t ws_bytes = 0;
 };
 enum GemvPro { PRO_NONE = 0, PRO_RMS = 1, PRO_LN = 2 };
 // Epilogues fused into the GEMV/GEMM store (each step rounds to f16 where
@@ -154,6 +157,7 @@ int gemv_norm_slots(int N);   // workgroups (= argmax keys) of the normalised GE
 tlhip_status launch_argmax_slots(hipStream_t s, const unsigned long long* slots, int n, int32_t* out,
                                  int32_t* token_log, int32_t* d_state);
 tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi);
+int gemm_splits(int M, int N, int K);   // split-K slices launch_gemm uses when given a workspace
 tlhip_status launch_repack(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks, void* qs,
                            uint16_t* d, int64_t nblocks, int64_t blocks_per_row, int to_gguf);
 tlhip_status launch_repack_rows(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks, void* qs,

@@ -248,8 +248,124 @@ __global__ __launch_bounds__(256) void attention64_kernel(AttnArgs a, int J_fixe
     }
 }
 
+// The same kernel for other even head dims D = 8 * EPL (Phi-2: 80): lane c
+// of a key's 8 lanes holds dims EPL*c .. EPL*c + EPL - 1, read as EPL/2
+// 4-byte words; one pass covers 32 keys; partial context rows are summed
+// in key-group order.
+template <int D>
+__global__ __launch_bounds__(256) void attention_dk_kernel(AttnArgs a, int J_fixed) {
+    constexpr int EPL = D / 8, NW = EPL / 2;
+    __shared__ float sc[ATT_MAX_J];
+    __shared__ float red[4];
+    __shared__ float part[32][D + 1];
+    const int s = blockIdx.x, h = blockIdx.y;
+    const int Hkv = a.Hkv;
+    const int kvh = h / (a.H / Hkv);
+    const int qs = a.q_stride ? a.q_stride : a.H * D;
+    const int os = a.out_stride ? a.out_stride : a.H * D;
+    const int tid = threadIdx.x, c = tid & 7, g = tid >> 3;
+    const size_t kstride = (size_t)Hkv * D;
+    const uint32_t* kbase = (const uint32_t*)(a.k + (size_t)kvh * D + EPL * c);
+    const uint32_t* vbase = (const uint32_t*)(a.v + (size_t)kvh * D + EPL * c);
+    const size_t wstride = kstride / 2;   // row stride in 4-byte words
+    float qf[EPL];
+    {
+        const uint32_t* qw = (const uint32_t*)(a.q + (size_t)s * qs + (size_t)h * D + EPL * c);
+#pragma unroll
+        for (int t = 0; t < NW; t++) {
+            const h2 p2 = as_h2(qw[t]);
+            qf[2 * t] = (float)p2[0];
+            qf[2 * t + 1] = (float)p2[1];
+        }
+    }
+    const int qpos = (a.d_pos ? *a.d_pos : a.q_pos0) + s;
+    const int J = min(a.d_pos ? qpos + 1 : J_fixed, ATT_MAX_J);
+    const int Jv = a.causal ? min(J, qpos + 1) : J;
+
+    float mx = -INFINITY;
+    for (int j0 = g; j0 < Jv; j0 += 32 * 4) {
+        uint32_t kw[4][NW];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int j = j0 + 32 * u;
+#pragma unroll
+            for (int t = 0; t < NW; t++) kw[u][t] = j < Jv ? kbase[(size_t)j * wstride + t] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = 0; t < NW; t++) {
+                const h2 k2 = as_h2(kw[u][t]);
+                acc += qf[2 * t] * (float)k2[0];
+                acc += qf[2 * t + 1] * (float)k2[1];
+            }
+            acc += __shfl_xor(acc, 1, 64);
+            acc += __shfl_xor(acc, 2, 64);
+            acc += __shfl_xor(acc, 4, 64);
+            const int j = j0 + 32 * u;
+            if (j < Jv) {
+                const float v = h2f(f2h(h2f(f2h(acc)) * a.scale_h));
+                if (c == 0) sc[j] = v;
+                if (isfinite(v)) mx = fmaxf(mx, v);
+            }
+        }
+    }
+    mx = bmax(mx, red);
+    if (!isfinite(mx)) mx = 0.0f;
+    float sum = 0.0f;
+    for (int j = tid; j < Jv; j += 256) {
+        const float v = sc[j];
+        const float e = isfinite(v) ? expf(v - mx) : 0.0f;
+        sc[j] = h2f(f2h(e));
+        sum += e;
+    }
+    sum = bsum(sum, red);
+    const bool degenerate = !(sum > 0.0f && isfinite(sum));
+    const int Jp = degenerate ? J : Jv;
+    const float uni = h2f(f2h(1.0f / (float)J));
+    for (int j = tid; j < Jp; j += 256) sc[j] = degenerate ? uni : h2f(f2h(sc[j] / sum));
+    __syncthreads();
+
+    float o[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; e++) o[e] = 0.0f;
+    for (int j0 = g; j0 < Jp; j0 += 32 * 4) {
+        uint32_t vw[4][NW];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int j = j0 + 32 * u;
+#pragma unroll
+            for (int t = 0; t < NW; t++) vw[u][t] = j < Jp ? vbase[(size_t)j * wstride + t] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int j = j0 + 32 * u;
+            if (j < Jp) {
+                const float pj = sc[j];
+#pragma unroll
+                for (int t = 0; t < NW; t++) {
+                    const h2 v2 = as_h2(vw[u][t]);
+                    o[2 * t] += pj * (float)v2[0];
+                    o[2 * t + 1] += pj * (float)v2[1];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; e++) part[g][EPL * c + e] = o[e];
+    __syncthreads();
+    if (tid < D) {
+        float t = part[0][tid];
+        for (int gg = 1; gg < 32; gg++) t += part[gg][tid];
+        a.out[(size_t)s * os + (size_t)h * D + tid] = f2h(t);
+    }
+}
+
 static void launch_attn_any(hipStream_t s, const AttnArgs& a, int J) {
     if (a.D == 64) hipLaunchKernelGGL(attention64_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, J);
+    else if (a.D == 80) hipLaunchKernelGGL(attention_dk_kernel<80>, dim3(a.S, a.H), dim3(256), 0, s, a, J);
+    else if (a.D == 128) hipLaunchKernelGGL(attention_dk_kernel<128>, dim3(a.S, a.H), dim3(256), 0, s, a, J);
     else hipLaunchKernelGGL(attention_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, J);
 }
 

@@ -190,13 +190,24 @@ __global__ void rope_kv_kernel(const uint16_t* __restrict__ qkv, int qkv_stride,
     const uint16_t* xr = row + (size_t)(is_k ? H + h : h) * D;
     uint16_t* yr = is_k ? kc + (size_t)pos * Hkv * D + (size_t)h * D : q_out + (size_t)s * H * D + (size_t)h * D;
     if (pe < half) {
-        int i0, i1;
-        rope_indices(layout, pe, half, i0, i1);
+        // layout 2: a pair-permuted projection (pair i in rows 2i, 2i+1)
+        // rotated into the half-rotation output positions (i, i + half)
+        int i0, i1, o0, o1;
+        if (layout == 2) {
+            i0 = 2 * pe;
+            i1 = 2 * pe + 1;
+            o0 = pe;
+            o1 = pe + half;
+        } else {
+            rope_indices(layout, pe, half, i0, i1);
+            o0 = i0;
+            o1 = i1;
+        }
         const float c = table[2 * ((size_t)pos * half + pe)], sn = table[2 * ((size_t)pos * half + pe) + 1];
         float r0, r1;
         rope_pair(h2f(xr[i0]), h2f(xr[i1]), c, sn, r0, r1);
-        yr[i0] = f2h(r0);
-        yr[i1] = f2h(r1);
+        yr[o0] = f2h(r0);
+        yr[o1] = f2h(r1);
     } else {
         const int d = rot + (pe - half);
         yr[d] = xr[d];

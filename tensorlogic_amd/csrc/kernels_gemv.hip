@@ -76,21 +76,6 @@ tlhip_status launch_repack(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks,
 // dequantisation to f16 (bit-exact with gguf.rs dequantize_q4_0 / q8_0)
 // one thread per block; 32 outputs written as 4 x 16 bytes
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void q4_unpack(uint32_t w, h2 dd, h2 out[4]) {
-    const h2 bias = {(h16)-1032.0f, (h16)-1032.0f};
-    out[0] = (as_h2((w & 0x000F000Fu) | 0x64006400u) + bias) * dd;          // e0, e2
-    out[1] = (as_h2(((w >> 8) & 0x000F000Fu) | 0x64006400u) + bias) * dd;   // e1, e3
-    out[2] = (as_h2(((w >> 4) & 0x000F000Fu) | 0x64006400u) + bias) * dd;   // e16, e18
-    out[3] = (as_h2(((w >> 12) & 0x000F000Fu) | 0x64006400u) + bias) * dd;  // e17, e19
-}
-
-__device__ __forceinline__ void q8_unpack(uint32_t w, h2 dd, h2 out[2]) {
-    const h2 bias = {(h16)-1152.0f, (h16)-1152.0f};
-    uint32_t v = w ^ 0x80808080u;
-    out[0] = (as_h2((v & 0x00FF00FFu) | 0x64006400u) + bias) * dd;          // e0, e2
-    out[1] = (as_h2(((v >> 8) & 0x00FF00FFu) | 0x64006400u) + bias) * dd;   // e1, e3
-}
-
 __global__ void dequant_q4_0_kernel(const uint8_t* __restrict__ qs, const uint16_t* __restrict__ d,
                                     uint16_t* __restrict__ out, int64_t nblocks) {
     int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;

@@ -20,6 +20,7 @@
 // the token, RoPE / cache writes / attention read pos, the argmax writes the
 // next token, advances pos and logs the token.  A decode step therefore has
 // no host inputs and is captured once as a HIP graph and replayed.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -62,6 +63,8 @@ struct tlhip_model_s {
     tlhip_tensor x = nullptr, xn = nullptr, qkv = nullptr, qrot = nullptr, att = nullptr, hmid = nullptr,
                  logits = nullptr;
     unsigned long long* d_amax = nullptr;   // per-workgroup greedy keys of the lm_head GEMV
+    float* ws = nullptr;          // split-K partials of the prefill GEMMs
+    size_t ws_bytes = 0;
     int32_t* d_state = nullptr;   // {token, pos, step}
     int32_t* d_tokens = nullptr;  // token log
     int32_t* d_ids = nullptr;     // prompt ids
@@ -140,6 +143,82 @@ tlhip_status place_rows(tlhip_ctx ctx, tlhip_gguf g, const std::string& name, in
     return st;
 }
 
+// Row order of a stacked [q | k | v] projection for the fused QKV + RoPE
+// epilogue: within each q and k head, rotary pair i (dims i and i + rot/2 of
+// the half-rotation layout) moves to rows 2i, 2i + 1; pass-through dims and
+// v keep their place.  perm[new_row] = source row.
+std::vector<int64_t> neox_pair_order(int64_t nq, int64_t nk, int64_t nv, int D, int rot) {
+    std::vector<int64_t> perm(nq + nk + nv);
+    for (int64_t r = 0; r < nq + nk + nv; r++) {
+        int64_t src = r;
+        if (r < nq + nk) {
+            const int64_t head0 = (r / D) * D;
+            const int e = (int)(r % D);
+            if (e < rot) src = head0 + (e / 2) + (e % 2) * (rot / 2);
+        }
+        perm[r] = src;
+    }
+    return perm;
+}
+
+// Uploads GGUF weight `name` [n, k] with its rows reordered by perm
+// (Q4_0 / Q8_0 / f16), through a host copy of the reordered block rows.
+tlhip_status load_rows_permuted(tlhip_ctx ctx, tlhip_gguf g, const std::string& name, int64_t n, int64_t k,
+                                const std::vector<int64_t>& perm, tlhip_tensor* out) {
+    uint32_t gt;
+    int nd;
+    int64_t dims[4];
+    const uint8_t* data;
+    size_t nbytes;
+    if (!gguf_lookup(g, name.c_str(), &gt, &nd, dims, &data, &nbytes))
+        return fail(TLHIP_ERR_LOAD, "tensor %s not found in GGUF", name.c_str());
+    if (nd != 2 || dims[0] != n || dims[1] != k || (int64_t)perm.size() != n)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "%s: [%lld, %lld], expected [%lld, %lld]", name.c_str(),
+                    (long long)dims[0], (long long)dims[1], (long long)n, (long long)k);
+    const tlhip_dtype dt = dtype_of(gt);
+    if (dt != TLHIP_Q4_0 && dt != TLHIP_Q8_0 && dt != TLHIP_F16)
+        return fail(TLHIP_ERR_DTYPE, "%s: GGUF type %u not supported by the runner", name.c_str(), gt);
+    const size_t rb = nbytes / (size_t)n;
+    std::vector<uint8_t> host(nbytes);
+    for (int64_t r = 0; r < n; r++) memcpy(host.data() + (size_t)r * rb, data + (size_t)perm[r] * rb, rb);
+    int64_t shp[2] = {n, k};
+    TLHIP_TRY(alloc_tensor(ctx, dt, 2, shp, out));
+    tlhip_status st = tlhip_tensor_upload(ctx, *out, host.data(), nbytes);
+    if (st == TLHIP_OK && hipStreamSynchronize(ctx->stream) != hipSuccess)
+        st = fail(TLHIP_ERR_DEVICE, "load %s", name.c_str());
+    if (st != TLHIP_OK) {
+        tlhip_tensor_free(*out);
+        *out = nullptr;
+    }
+    return st;
+}
+
+// A 1-D f16 vector with its entries reordered by perm.
+tlhip_status load_vec_permuted(tlhip_ctx ctx, tlhip_gguf g, const std::string& name,
+                               const std::vector<int64_t>& perm, tlhip_tensor* out) {
+    uint32_t gt;
+    int nd;
+    int64_t dims[4];
+    const uint8_t* data;
+    size_t nbytes;
+    if (!gguf_lookup(g, name.c_str(), &gt, &nd, dims, &data, &nbytes))
+        return fail(TLHIP_ERR_LOAD, "tensor %s not found in GGUF", name.c_str());
+    if (gt != 1 || nbytes != perm.size() * 2)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "%s: expected %zu f16 entries", name.c_str(), perm.size());
+    std::vector<uint16_t> host(perm.size());
+    for (size_t i = 0; i < perm.size(); i++) memcpy(&host[i], data + 2 * perm[i], 2);
+    int64_t shp[1] = {(int64_t)perm.size()};
+    TLHIP_TRY(alloc_tensor(ctx, TLHIP_F16, 1, shp, out));
+    tlhip_status st = tlhip_tensor_upload(ctx, *out, host.data(), host.size() * 2);
+    if (st == TLHIP_OK && hipStreamSynchronize(ctx->stream) != hipSuccess)
+        st = fail(TLHIP_ERR_DEVICE, "load %s", name.c_str());
+    if (st != TLHIP_OK) {
+        tlhip_tensor_free(*out);
+        *out = nullptr;
+    }
+    return st;
+}
+
 tlhip_status weight_dtype(tlhip_gguf g, const std::string& name, tlhip_dtype* dt) {
     uint32_t gt;
     int nd;
@@ -178,8 +257,10 @@ tlhip_status fused_weight(tlhip_ctx ctx, tlhip_gguf g, const std::vector<std::pa
 }
 
 tlhip_status linear_into(hipStream_t s, const Lin& l, const uint16_t* x, int M, uint16_t* y, int epi,
-                         const uint16_t* resid, int ldy = 0) {
+                         const uint16_t* resid, int ldy = 0, float* ws = nullptr, size_t ws_bytes = 0) {
     GemvArgs a;
+    a.ws = ws;
+    a.ws_bytes = ws_bytes;
     a.x = x;
     a.wq = l.w->data;
     a.wd = l.w->scales;
@@ -246,14 +327,16 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
         Layer& L = m->layers[li];
         uint16_t* kc = P(m->kv->k[li]);
         uint16_t* vc = P(m->kv->v[li]);
-        if (row1 && m->arch == 0) {
-            GemvArgs a = fused_norm_args(m, L.qkv, P(m->x), L.norm_w, nullptr);
+        if (row1) {
+            // norm + qkv (+ bias) + RoPE + cache write in one launch; phi2's
+            // q / k rows were loaded in rotary-pair order
+            GemvArgs a = fused_norm_args(m, L.qkv, P(m->x), L.norm_w, L.norm_b);
             embed_into(a, li);
             a.nq = H;
             a.nk = kvd;
             a.head_dim = D;
             a.rot = m->rot;
-            a.layout = 0;
+            a.layout = m->arch == 0 ? 0 : 1;
             a.pos0 = decode ? 0 : pos0;
             a.d_pos = d_pos;
             a.rope_tab = m->rope_tab;
@@ -262,17 +345,10 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
             a.vc = vc;
             TLHIP_TRY(launch_gemv(s, L.qkv.w->dtype, a, EPI_QKV_ROPE));
         } else {
-            if (row1) {
-                GemvArgs a = fused_norm_args(m, L.qkv, P(m->x), L.norm_w, L.norm_b);
-                embed_into(a, li);
-                a.y = P(m->qkv);
-                TLHIP_TRY(launch_gemv(s, L.qkv.w->dtype, a, L.qkv.b ? EPI_BIAS : EPI_STORE));
-            } else {
-                if (m->arch == 0) TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.norm_w), P(m->xn), S, H, m->eps));
-                else TLHIP_TRY(launch_layer_norm(s, P(m->x), P(L.norm_w), P(L.norm_b), P(m->xn), S, H, m->eps));
-                TLHIP_TRY(linear_into(s, L.qkv, P(m->xn), S, P(m->qkv), L.qkv.b ? EPI_BIAS : EPI_STORE, nullptr));
-            }
-            TLHIP_TRY(launch_rope_kv(s, P(m->qkv), qkv_w, S, NH, NKV, D, m->arch == 0 ? 0 : 1, m->rot,
+            if (m->arch == 0) TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.norm_w), P(m->xn), S, H, m->eps));
+            else TLHIP_TRY(launch_layer_norm(s, P(m->x), P(L.norm_w), P(L.norm_b), P(m->xn), S, H, m->eps));
+            TLHIP_TRY(linear_into(s, L.qkv, P(m->xn), S, P(m->qkv), L.qkv.b ? EPI_BIAS : EPI_STORE, nullptr, 0, m->ws, m->ws_bytes));
+            TLHIP_TRY(launch_rope_kv(s, P(m->qkv), qkv_w, S, NH, NKV, D, m->arch == 0 ? 0 : 2, m->rot,
                                      m->rope_tab, decode ? 0 : pos0, d_pos, P(m->qrot), kc, vc));
         }
         AttnArgs at;
@@ -295,16 +371,16 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
             TLHIP_TRY(launch_attention_j(s, at, pos0 + S));
         }
         if (m->arch == 0) {
-            TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_RESID, P(m->x)));
+            TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_RESID, P(m->x), 0, m->ws, m->ws_bytes));
             if (row1) {
                 GemvArgs a = fused_norm_args(m, L.gu, P(m->x), L.ffn_norm_w, nullptr);
                 a.y = P(m->hmid);
                 TLHIP_TRY(launch_gemv(s, L.gu.w->dtype, a, EPI_SWIGLU_PAIR));
             } else {
                 TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.ffn_norm_w), P(m->xn), S, H, m->eps));
-                TLHIP_TRY(linear_into(s, L.gu, P(m->xn), S, P(m->hmid), EPI_SWIGLU_PAIR, nullptr));
+                TLHIP_TRY(linear_into(s, L.gu, P(m->xn), S, P(m->hmid), EPI_SWIGLU_PAIR, nullptr, 0, m->ws, m->ws_bytes));
             }
-            TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_RESID, P(m->x)));
+            TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_RESID, P(m->x), 0, m->ws, m->ws_bytes));
         } else {
             // phi2: the MLP reads the same layer_norm output as attention
             if (row1) {
@@ -312,9 +388,9 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
                 a.y = P(m->hmid);
                 TLHIP_TRY(launch_gemv(s, L.up.w->dtype, a, EPI_BIAS_GELU));
             }
-            TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_BIAS_RESID, P(m->x)));
-            if (!row1) TLHIP_TRY(linear_into(s, L.up, P(m->xn), S, P(m->hmid), EPI_BIAS_GELU, nullptr));
-            TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_BIAS_RESID, P(m->x)));
+            TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes));
+            if (!row1) TLHIP_TRY(linear_into(s, L.up, P(m->xn), S, P(m->hmid), EPI_BIAS_GELU, nullptr, 0, m->ws, m->ws_bytes));
+            TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes));
         }
     }
     const uint16_t* last = P(m->x) + (size_t)(S - 1) * H;
@@ -524,6 +600,7 @@ tlhip_status tlhip_model_free(tlhip_model m) {
     tlhip_kvcache_free(m->kv);
     for (tlhip_tensor t : {m->x, m->xn, m->qkv, m->qrot, m->att, m->hmid, m->logits}) tlhip_tensor_free(t);
     if (m->d_amax) (void)hipFree(m->d_amax);
+    if (m->ws) (void)hipFree(m->ws);
     if (m->d_state) (void)hipFree(m->d_state);
     if (m->d_tokens) (void)hipFree(m->d_tokens);
     if (m->d_ids) (void)hipFree(m->d_ids);
@@ -599,8 +676,10 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
                 if ((st = fused_weight(ctx, g, {{p + "ffn_down.weight", H}}, I, false, &L.down.w)) != TLHIP_OK) break;
             } else {
                 if ((st = load_vec(ctx, g, p + "attn_norm.bias", H, &L.norm_b)) != TLHIP_OK) break;
-                if ((st = fused_weight(ctx, g, {{p + "attn_qkv.weight", H + 2 * kvd}}, H, false, &L.qkv.w)) != TLHIP_OK) break;
-                if ((st = load_vec(ctx, g, p + "attn_qkv.bias", H + 2 * kvd, &L.qkv.b)) != TLHIP_OK) break;
+                // q / k rows in rotary-pair order (see neox_pair_order)
+                const auto perm = neox_pair_order(H, kvd, kvd, m->head_dim, m->rot);
+                if ((st = load_rows_permuted(ctx, g, p + "attn_qkv.weight", H + 2 * kvd, H, perm, &L.qkv.w)) != TLHIP_OK) break;
+                if ((st = load_vec_permuted(ctx, g, p + "attn_qkv.bias", perm, &L.qkv.b)) != TLHIP_OK) break;
                 if ((st = fused_weight(ctx, g, {{p + "attn_output.weight", H}}, H, false, &L.o.w)) != TLHIP_OK) break;
                 if ((st = load_vec(ctx, g, p + "attn_output.bias", H, &L.o.b)) != TLHIP_OK) break;
                 if ((st = fused_weight(ctx, g, {{p + "ffn_up.weight", I}}, H, false, &L.up.w)) != TLHIP_OK) break;
@@ -625,6 +704,20 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
         if ((st = alloc_tensor(ctx, TLHIP_F16, 1, s_l, &m->logits)) != TLHIP_OK) break;
         hipError_t e = hipMalloc(&m->d_state, 4 * sizeof(int32_t));
         if (e == hipSuccess) e = hipMalloc(&m->d_amax, sizeof(unsigned long long) * gemv_norm_slots(m->vocab));
+        // split-K workspace: the largest partial set any prefill GEMM of this model uses
+        if (e == hipSuccess) {
+            const int64_t shapes[4][2] = {{H + 2 * kvd, H}, {H, H}, {arch == 0 ? 2 * I : I, H}, {H, I}};
+            size_t need = 0;
+            for (int rows = 5; rows <= (int)R; rows++)
+                for (auto& sh : shapes) {
+                    const int sp = gemm_splits(rows, (int)sh[0], (int)sh[1]);
+                    if (sp > 1) need = std::max(need, (size_t)sp * rows * sh[0] * sizeof(float));
+                }
+            if (need) {
+                e = hipMalloc(&m->ws, need);
+                m->ws_bytes = need;
+            }
+        }
         if (e == hipSuccess) e = hipMalloc(&m->d_tokens, sizeof(int32_t) * (max_ctx + 1));
         if (e == hipSuccess) e = hipMalloc(&m->d_ids, sizeof(int32_t) * R);
         if (e == hipSuccess) e = hipHostMalloc(&m->h_state, 4 * sizeof(int32_t), hipHostMallocDefault);
@@ -710,11 +803,13 @@ tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tenso
     for (int i = 0; i < n_w; i++) TLHIP_TRY(tlhip_linear(ctx, x, w[i], nullptr, y));   // checks + warm-up
     TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
     Lin l;
+    const bool gemm = x->shape[0] > 4;   // GEMMs go through tlhip_linear (split-K workspace)
     if (!per_launch) {
         TLHIP_CHECK_HIP(hipEventRecord(ctx->ev0, ctx->stream));
         for (int i = 0; i < iters; i++) {
             l.w = w[i % n_w];
-            TLHIP_TRY(linear_into(ctx->stream, l, P(x), (int)x->shape[0], P(y), EPI_STORE, nullptr));
+            if (gemm) TLHIP_TRY(tlhip_linear(ctx, x, l.w, nullptr, y));
+            else TLHIP_TRY(linear_into(ctx->stream, l, P(x), (int)x->shape[0], P(y), EPI_STORE, nullptr));
         }
         TLHIP_CHECK_HIP(hipEventRecord(ctx->ev1, ctx->stream));
         TLHIP_CHECK_HIP(hipEventSynchronize(ctx->ev1));
@@ -735,7 +830,9 @@ tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tenso
     for (int i = 0; i < iters && st == TLHIP_OK; i++) {
         l.w = w[i % n_w];
         if (hipEventRecord(ev[2 * i], ctx->stream) != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "hipEventRecord");
-        if (st == TLHIP_OK) st = linear_into(ctx->stream, l, P(x), (int)x->shape[0], P(y), EPI_STORE, nullptr);
+        if (st == TLHIP_OK)
+            st = gemm ? tlhip_linear(ctx, x, l.w, nullptr, y)
+                      : linear_into(ctx->stream, l, P(x), (int)x->shape[0], P(y), EPI_STORE, nullptr);
         if (st == TLHIP_OK && hipEventRecord(ev[2 * i + 1], ctx->stream) != hipSuccess)
             st = fail(TLHIP_ERR_DEVICE, "hipEventRecord");
     }

@@ -84,7 +84,21 @@ tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_t
         st = launch_gemv(ctx->stream, w->dtype, a, epi);
         if (st != TLHIP_OK) (void)hipGetLastError();
     }
-    if (st != TLHIP_OK) TLHIP_TRY(launch_gemm(ctx->stream, w->dtype, a, epi));
+    if (st == TLHIP_OK) return after_launch(ctx, "linear");
+    // MFMA GEMM; a split-K workspace from the stream-ordered pool when the
+    // output has too few tiles to fill the device
+    tlhip_tensor ws = nullptr;
+    const int sp = gemm_splits((int)M, (int)N, (int)K);
+    if (sp > 1) {
+        int64_t shp[1] = {(int64_t)sp * M * N};
+        if (alloc_tensor(ctx, TLHIP_F32, 1, shp, &ws) == TLHIP_OK) {
+            a.ws = (float*)ws->data;
+            a.ws_bytes = (size_t)sp * M * N * sizeof(float);
+        }
+    }
+    st = launch_gemm(ctx->stream, w->dtype, a, epi);
+    tlhip_tensor_free(ws);   // stream-ordered: returns to the pool after the GEMM
+    TLHIP_TRY(st);
     return after_launch(ctx, "linear");
 }
 

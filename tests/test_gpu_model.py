@@ -5,6 +5,7 @@ wins); the final logits within max-abs 2e-2 / rel-L2 1e-3.  Small models run
 the oracle live; the full TinyLlama-shape model is checked against the
 oracle's committed golden tokens (tests/golden/).
 """
+import base64
 import json
 import os
 
@@ -71,7 +72,7 @@ def test_long_prompt_chunked_prefill(dev, oracle, tmp_path):
 
 def _golden(name):
     p = os.path.join(GOLDEN, name)
-    if not os.path.exists(p):
+    if not os.path.exists(p) or os.path.getsize(p) == 0:
         pytest.skip(f"{name} not generated")
     with open(p) as f:
         return json.load(f)
@@ -81,6 +82,50 @@ def _ulp(v):
     """f16 spacing at |v|."""
     a = max(abs(float(v)), 2.0 ** -14)
     return 2.0 ** (np.floor(np.log2(a)) - 10)
+
+
+def _last_logits(g):
+    if "last_logits_f16_b64" in g:
+        return np.frombuffer(base64.b64decode(g["last_logits_f16_b64"]), "<f2").astype(np.float16)
+    return np.array(g["last_logits"], np.float16)
+
+
+def _teacher_forced(dev, path, arch, g, max_ctx):
+    """Decodes the oracle's own token stream on the device and checks every
+    step (see test_tinyllama_full_golden_tokens); returns the near-tie steps."""
+    prompt = np.array(g["prompt"], np.int32)
+    ref = np.array(g["tokens"], np.int32)
+    margins = np.array(g["margins"], np.float64)
+    key = next(k for k in g if k.startswith("top") and k.endswith("_ids"))
+    ids = np.array(g[key], np.int64)
+    vals = np.array(g[key.replace("_ids", "_logits")], np.float64)
+    n = g["n_decode"]
+    m = Model(dev, path, arch=arch, max_ctx=max_ctx)
+    worst_ulps, exempt, mism = 0.0, [], []
+    tok = m.prefill(prompt)
+    for step in range(n + 1):
+        if step:
+            tok = m.decode(int(ref[step - 1]))
+        lg = m.logits().astype(np.float64)
+        err = float(np.abs(lg[ids[step]] - vals[step]).max())
+        ulp = _ulp(vals[step][0])
+        worst_ulps = max(worst_ulps, err / ulp)
+        assert err <= 2e-2, f"step {step}: top logits off by {err:.3e}"
+        assert err <= 8 * ulp, f"step {step}: top logits off by {err / ulp:.1f} f16 ulps"
+        if margins[step] <= max(2 * err, ulp):
+            exempt.append(step)
+        elif tok != ref[step]:
+            mism.append((step, int(tok), int(ref[step]), float(margins[step])))
+    print(f"teacher-forced: worst top-k deviation {worst_ulps:.2f} ulp; near-tie steps {exempt}")
+    assert not mism, f"argmax differs at determined steps (step, device, oracle, margin): {mism}"
+    assert_close(m.logits(), _last_logits(g), what="final logits")
+    # free-running graph replay agrees up to the first near-tie
+    toks = m.generate(prompt, n, use_graph=True)
+    first = exempt[0] if exempt else n + 1
+    bad = np.nonzero(toks[:first] != ref[:first])[0]
+    assert bad.size == 0, f"free-running stream differs at step {bad[0]} before the first near-tie ({first})"
+    m.close()
+    return exempt
 
 
 def test_tinyllama_full_golden_tokens(dev, tmp_path):
@@ -101,38 +146,15 @@ def test_tinyllama_full_golden_tokens(dev, tmp_path):
         pytest.skip("golden file predates the per-step top-8 logits")
     path = str(tmp_path / "tinyllama.gguf")
     S.write_llama_gguf(path, seed=g["seed"], **S.TINYLLAMA_ARGS)
-    prompt = np.array(g["prompt"], np.int32)
-    ref = np.array(g["tokens"], np.int32)
-    margins = np.array(g["margins"], np.float64)
-    ids = np.array(g["top8_ids"], np.int64)
-    vals = np.array(g["top8_logits"], np.float64)
-    n = g["n_decode"]
-    m = Model(dev, path, arch=0, max_ctx=256)
+    _teacher_forced(dev, path, 0, g, 256)
 
-    # teacher-forced: step i sees exactly the oracle's context
-    worst_ulps, exempt, mism = 0.0, [], []
-    tok = m.prefill(prompt)
-    for step in range(n + 1):
-        if step:
-            tok = m.decode(int(ref[step - 1]))
-        lg = m.logits().astype(np.float64)
-        dev_top = np.abs(lg[ids[step]] - vals[step])
-        err = float(dev_top.max())
-        ulp = _ulp(vals[step][0])
-        worst_ulps = max(worst_ulps, err / ulp)
-        assert err <= 2e-2, f"step {step}: top-8 logits off by {err:.3e}"
-        assert err <= 8 * ulp, f"step {step}: top-8 logits off by {err / ulp:.1f} f16 ulps"
-        if margins[step] <= max(2 * err, ulp):
-            exempt.append(step)
-        elif tok != ref[step]:
-            mism.append((step, int(tok), int(ref[step]), float(margins[step])))
-    print(f"teacher-forced: worst top-8 deviation {worst_ulps:.2f} ulp; near-tie steps {exempt}")
-    assert not mism, f"argmax differs at determined steps (step, device, oracle, margin): {mism}"
-    assert_close(m.logits(), np.array(g["last_logits"], np.float16), what="final logits")
 
-    # free-running graph replay agrees up to the first near-tie
-    toks = m.generate(prompt, n, use_graph=True)
-    first = exempt[0] if exempt else n + 1
-    bad = np.nonzero(toks[:first] != ref[:first])[0]
-    assert bad.size == 0, f"free-running stream differs at step {bad[0]} before the first near-tie ({first})"
-    m.close()
+def test_phi2_full_golden_tokens(dev, tmp_path):
+    """Phi-2 shape (2.7B), Q8_0, 512-token prompt, 256 greedy steps (config 5):
+    the same teacher-forced check, through MFMA prefill of 512 rows and the
+    fused decode path (LayerNorm + fused QKV + half-rotation partial RoPE +
+    parallel GELU MLP)."""
+    g = _golden("phi2_q8_0_tokens.json")
+    path = str(tmp_path / "phi2.gguf")
+    S.write_phi2_gguf(path, seed=g["seed"], **S.PHI2_ARGS)
+    _teacher_forced(dev, path, 1, g, 800)
