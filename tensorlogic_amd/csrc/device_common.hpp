@@ -63,16 +63,51 @@ __device__ __forceinline__ float fdot2(h2 a, h2 b, float c) {
     return __builtin_amdgcn_fdot2(a, b, c, false);
 }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations (lgkmcnt) and meets the other waves, without the vmcnt(0) a
+// full __syncthreads() fence adds -- global loads issued before it (a
+// GEMV's weight rows) stay in flight.  The "memory" clobber keeps the
+// compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Cross-lane data movement within rows of 16 lanes by DPP (no LDS round
+// trip): quad_perm xor 1 (0xB1), quad_perm xor 2 (0x4E), row_half_mirror
+// (0x141: lane i <-> 7 - i of each 8), row_mirror (0x140: i <-> 15 - i).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each aligned group of 8 lanes, left in every lane of the group.
+// Every step adds a symmetric pair, so all lanes hold the same value.
+__device__ __forceinline__ float group8_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    return v;
+}
+
+// Sum over the 64-lane wave, the same value in every lane (fixed order:
+// quads, 8s and 16s by DPP, then the rows by two xor shuffles).
 template <int W>
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    static_assert(W == 64, "wave64 reduction");
+    v = group8_sum(v);
+    v += dpp_f<0x140>(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
     return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
     return v;
 }
 

@@ -172,9 +172,7 @@ __global__ __launch_bounds__(256) void attention64_kernel(AttnArgs a, int J_fixe
                 acc += qf[2 * t] * (float)k2[0];
                 acc += qf[2 * t + 1] * (float)k2[1];
             }
-            acc += __shfl_xor(acc, 1, 64);
-            acc += __shfl_xor(acc, 2, 64);
-            acc += __shfl_xor(acc, 4, 64);
+            acc = group8_sum(acc);
             const int j = j0 + 32 * u;
             if (j < Jv) {
                 const float v = h2f(f2h(h2f(f2h(acc)) * a.scale_h));
@@ -300,9 +298,7 @@ __global__ __launch_bounds__(256) void attention_dk_kernel(AttnArgs a, int J_fix
                 acc += qf[2 * t] * (float)k2[0];
                 acc += qf[2 * t + 1] * (float)k2[1];
             }
-            acc += __shfl_xor(acc, 1, 64);
-            acc += __shfl_xor(acc, 2, 64);
-            acc += __shfl_xor(acc, 4, 64);
+            acc = group8_sum(acc);
             const int j = j0 + 32 * u;
             if (j < Jv) {
                 const float v = h2f(f2h(h2f(f2h(acc)) * a.scale_h));

@@ -263,92 +263,128 @@ template <int WPB>
 __device__ __forceinline__ float wg_sum(float v, float* red) {
     v = wave_sum<64>(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
+    lds_barrier();
     float t = red[0];
 #pragma unroll
     for (int k = 1; k < WPB; k++) t += red[k];
-    __syncthreads();
+    lds_barrier();
     return t;
 }
 
 // Items (block b, quad v) are spread over the workgroup; each thread keeps
-// its (at most IPT) items' values in registers between the passes.
+// its (at most IPT) items' values in registers between the passes.  The
+// loads (NormStage::load) are issued before the weight rows: vector loads
+// retire in order, so the statistics can start while the weights are
+// still in flight.
 template <int WT, int NB, int WPB, int PRO>
-__device__ __forceinline__ void stage_norm(const GemvParams& p, const uint16_t* __restrict__ xsrc,
-                                           u4 (*xs)[NB * 64], float* red) {
-    constexpr int NT = WPB * 64;
-    constexpr int IPT = (NB * 256 + NT - 1) / NT;
-    const int nbr = p.K >> 5, items = nbr * 4;
-    float f[IPT][8];
-#pragma unroll
-    for (int k = 0; k < IPT; k++) {
-        const int it = threadIdx.x + k * NT;
-        if (it < items) load_quad<WT>(xsrc, it >> 2, it & 3, f[k]);
-        else
-#pragma unroll
-            for (int e = 0; e < 8; e++) f[k][e] = 0.0f;
+struct NormStage {
+    static constexpr int NT = WPB * 64;
+    static constexpr int IPT = (NB * 256 + NT - 1) / NT;
+    uint32_t xw[IPT][4], ww[IPT][4], bw[IPT][4];   // raw f16 pairs until finish()
+
+    __device__ __forceinline__ static void load_words(const uint16_t* __restrict__ src, int b, int v, uint32_t w[4]) {
+        if (WT == TLHIP_Q4_0) {
+            const uint2 lo = *(const uint2*)(src + (size_t)b * 32 + 4 * v);
+            const uint2 hi = *(const uint2*)(src + (size_t)b * 32 + 16 + 4 * v);
+            w[0] = lo.x; w[1] = lo.y; w[2] = hi.x; w[3] = hi.y;
+        } else {
+            const u4 t = *(const u4*)(src + (size_t)b * 32 + 8 * v);
+            w[0] = t[0]; w[1] = t[1]; w[2] = t[2]; w[3] = t[3];
+        }
     }
-    if (p.x_out && blockIdx.x == 0)   // the residual copy of an embedded row
+
+    __device__ __forceinline__ static void to_float(const uint32_t w[4], float f[8]) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const h2 h = as_h2(w[t]);
+            f[2 * t] = (float)h[0];
+            f[2 * t + 1] = (float)h[1];
+        }
+    }
+
+    __device__ __forceinline__ void load(const GemvParams& p, const uint16_t* __restrict__ xsrc) {
+        const int items = (p.K >> 5) * 4;
 #pragma unroll
         for (int k = 0; k < IPT; k++) {
             const int it = threadIdx.x + k * NT;
             if (it < items) {
-                const int b = it >> 2, v = it & 3;
+                load_words(xsrc, it >> 2, it & 3, xw[k]);
+                load_words(p.norm_w, it >> 2, it & 3, ww[k]);
+                if (PRO == PRO_LN) load_words(p.norm_b, it >> 2, it & 3, bw[k]);
+            } else {
 #pragma unroll
-                for (int e = 0; e < 8; e++) p.x_out[(size_t)b * 32 + quad_elem<WT>(v, e)] = f2h(f[k][e]);
+                for (int t = 0; t < 4; t++) xw[k][t] = 0u;
             }
         }
-    float mean = 0.0f, inv;
-    if (PRO == PRO_RMS) {
-        float ss = 0.0f;
+    }
+
+    __device__ __forceinline__ void finish(const GemvParams& p, u4 (*xs)[NB * 64], float* red) {
+        const int items = (p.K >> 5) * 4;
+        float f[IPT][8];
 #pragma unroll
-        for (int k = 0; k < IPT; k++)
+        for (int k = 0; k < IPT; k++) to_float(xw[k], f[k]);
+        if (p.x_out && blockIdx.x == 0)   // the residual copy of an embedded row
 #pragma unroll
-            for (int e = 0; e < 8; e++) ss += f[k][e] * f[k][e];
-        const float t = wg_sum<WPB>(ss, red);
-        inv = 1.0f / sqrtf(t / (float)p.K + p.eps);
-    } else {
-        float sm = 0.0f;
+            for (int k = 0; k < IPT; k++) {
+                const int it = threadIdx.x + k * NT;
+                if (it < items) {
+                    const int b = it >> 2, v = it & 3;
 #pragma unroll
-        for (int k = 0; k < IPT; k++)
+                    for (int e = 0; e < 8; e++) p.x_out[(size_t)b * 32 + quad_elem<WT>(v, e)] = f2h(f[k][e]);
+                }
+            }
+        float mean = 0.0f, inv;
+        if (PRO == PRO_RMS) {
+            float ss = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; e++) sm += f[k][e];
-        mean = wg_sum<WPB>(sm, red) / (float)p.K;
-        float q = 0.0f;
+            for (int k = 0; k < IPT; k++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) ss += f[k][e] * f[k][e];
+            const float t = wg_sum<WPB>(ss, red);
+            inv = 1.0f / sqrtf(t / (float)p.K + p.eps);
+        } else {
+            float sm = 0.0f;
+#pragma unroll
+            for (int k = 0; k < IPT; k++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) sm += f[k][e];
+            mean = wg_sum<WPB>(sm, red) / (float)p.K;
+            float q = 0.0f;
+#pragma unroll
+            for (int k = 0; k < IPT; k++) {
+                if (threadIdx.x + k * NT >= items) continue;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float d = f[k][e] - mean;
+                    q += d * d;
+                }
+            }
+            inv = 1.0f / sqrtf(wg_sum<WPB>(q, red) / (float)p.K + p.eps);
+        }
 #pragma unroll
         for (int k = 0; k < IPT; k++) {
-            if (threadIdx.x + k * NT >= items) continue;
+            const int it = threadIdx.x + k * NT;
+            if (it >= items) continue;
+            const int b = it >> 2, v = it & 3;
+            float w[8], bb[8];
+            to_float(ww[k], w);
+            if (PRO == PRO_LN) to_float(bw[k], bb);
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float d = f[k][e] - mean;
-                q += d * d;
-            }
+            for (int e = 0; e < 8; e++)
+                f[k][e] = PRO == PRO_RMS ? (f[k][e] * inv) * w[e] : (((f[k][e] - mean) * inv) * w[e]) + bb[e];
+            xs[v][b] = pack_quad<WT>(f[k]);
         }
-        inv = 1.0f / sqrtf(wg_sum<WPB>(q, red) / (float)p.K + p.eps);
+        lds_barrier();
     }
-#pragma unroll
-    for (int k = 0; k < IPT; k++) {
-        const int it = threadIdx.x + k * NT;
-        if (it >= items) continue;
-        const int b = it >> 2, v = it & 3;
-        float w[8], bb[8];
-        load_quad<WT>(p.norm_w, b, v, w);
-        if (PRO == PRO_LN) load_quad<WT>(p.norm_b, b, v, bb);
-#pragma unroll
-        for (int e = 0; e < 8; e++)
-            f[k][e] = PRO == PRO_RMS ? (f[k][e] * inv) * w[e] : (((f[k][e] - mean) * inv) * w[e]) + bb[e];
-        xs[v][b] = pack_quad<WT>(f[k]);
-    }
-    __syncthreads();
-}
+};
 
 // Weight payload of one 32-element block: Q4_0 1 x 16 B, Q8_0 2 x 16 B, F16 4 x 16 B.
 template <int WT> struct BlkLoads { static constexpr int n = WT == TLHIP_Q4_0 ? 1 : (WT == TLHIP_Q8_0 ? 2 : 4); };
 
 template <int WT>
-__device__ __forceinline__ float block_dot(const u4* q, uint16_t dbits, const uint32_t xc[16], float acc) {
+__device__ __forceinline__ float block_dot(const u4* q, uint32_t dbits, const uint32_t xc[16], float acc) {
     if (WT == TLHIP_Q4_0) {
-        h16 dh = __builtin_bit_cast(h16, dbits);
+        h16 dh = __builtin_bit_cast(h16, (uint16_t)dbits);
         h2 dd = {dh, dh};
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -358,7 +394,7 @@ __device__ __forceinline__ float block_dot(const u4* q, uint16_t dbits, const ui
             for (int j = 0; j < 4; j++) acc = fdot2(r[j], as_h2(xc[4 * t + j]), acc);
         }
     } else if (WT == TLHIP_Q8_0) {
-        h16 dh = __builtin_bit_cast(h16, dbits);
+        h16 dh = __builtin_bit_cast(h16, (uint16_t)dbits);
         h2 dd = {dh, dh};
 #pragma unroll
         for (int v = 0; v < 2; v++)
@@ -391,14 +427,14 @@ __device__ __forceinline__ float block_dot(const u4* q, uint16_t dbits, const ui
 // start of the kernel (QkvPre), so the tail makes no dependent loads.
 struct QkvPre {
     int pos;
-    uint16_t b0, b1;
+    uint32_t b0, b1;   // zero-extended f16 bits
     float c, sn;
 };
 
 __device__ __forceinline__ void qkv_rope_pre(const GemvParams& p, int row, int pos, QkvPre& q) {
     q.pos = pos;
-    q.b0 = p.bias ? p.bias[row] : 0;
-    q.b1 = p.bias ? p.bias[row + 1] : 0;
+    q.b0 = p.bias ? (uint32_t)p.bias[row] : 0u;
+    q.b1 = p.bias ? (uint32_t)p.bias[row + 1] : 0u;
     q.c = 1.0f;
     q.sn = 0.0f;
     const int D = p.head_dim;
@@ -415,8 +451,8 @@ __device__ __forceinline__ void qkv_rope_pre(const GemvParams& p, int row, int p
 __device__ __forceinline__ void qkv_rope_store(const GemvParams& p, int row, float a0, float a1, const QkvPre& q) {
     uint16_t r0 = f2h(a0), r1 = f2h(a1);
     if (p.bias) {
-        r0 = add_h(r0, q.b0);
-        r1 = add_h(r1, q.b1);
+        r0 = add_h(r0, (uint16_t)q.b0);
+        r1 = add_h(r1, (uint16_t)q.b1);
     }
     const int pos = q.pos;
     const int D = p.head_dim;
@@ -452,7 +488,7 @@ __device__ __forceinline__ void qkv_rope_store(const GemvParams& p, int row, flo
 // Loads of RI rows x NB blocks of the wave, all issued before any use.
 template <int WT, int NB, int RI>
 __device__ __forceinline__ void load_rows(const GemvParams& p, int row0, int lane, u4 (&q)[RI][NB][BlkLoads<WT>::n],
-                                          uint16_t (&ds)[RI][NB]) {
+                                          uint32_t (&ds)[RI][NB]) {
     constexpr int NL = BlkLoads<WT>::n;
     const int nbr = p.K >> 5;
     const size_t row_bytes = WT == TLHIP_Q4_0 ? (size_t)p.K / 2 : (WT == TLHIP_Q8_0 ? (size_t)p.K : (size_t)p.K * 2);
@@ -465,7 +501,7 @@ __device__ __forceinline__ void load_rows(const GemvParams& p, int row0, int lan
             const int b = min(lane + 64 * i, nbr - 1);
 #pragma unroll
             for (int l = 0; l < NL; l++) q[ri][i][l] = *(const u4*)(wr + (size_t)b * (16 * NL) + 16 * l);
-            ds[ri][i] = WT == TLHIP_F16 ? 0 : p.wd[(size_t)row * nbr + b];
+            ds[ri][i] = WT == TLHIP_F16 ? 0u : (uint32_t)p.wd[(size_t)row * nbr + b];
         }
     }
 }
@@ -473,9 +509,9 @@ __device__ __forceinline__ void load_rows(const GemvParams& p, int row0, int lan
 // Lane 0's bias / residual elements of the wave's rows, loaded right after
 // the weights so the epilogue makes no dependent loads.
 template <int RI, int MX>
-struct EpiPre {
-    uint16_t b[RI];
-    uint16_t r[RI][MX];
+struct EpiPre {   // zero-extended f16 bits (kept unpacked until the epilogue)
+    uint32_t b[RI];
+    uint32_t r[RI][MX];
 };
 
 template <int RI, int MX>
@@ -483,9 +519,9 @@ __device__ __forceinline__ void epi_preload(const GemvParams& p, int row0, EpiPr
 #pragma unroll
     for (int ri = 0; ri < RI; ri++) {
         const int row = min(row0 + ri, p.N - 1);
-        e.b[ri] = p.bias ? p.bias[row] : 0;
+        e.b[ri] = p.bias ? (uint32_t)p.bias[row] : 0u;
 #pragma unroll
-        for (int m = 0; m < MX; m++) e.r[ri][m] = (p.resid && m < p.M) ? p.resid[(size_t)m * p.N + row] : 0;
+        for (int m = 0; m < MX; m++) e.r[ri][m] = (p.resid && m < p.M) ? (uint32_t)p.resid[(size_t)m * p.N + row] : 0u;
     }
 }
 
@@ -510,7 +546,7 @@ __device__ __forceinline__ void store_rows(const GemvParams& p, int row0, const 
             if (row < p.N)
 #pragma unroll
                 for (int m = 0; m < MX; m++)
-                    if (m < p.M) p.y[(size_t)m * p.ldy + row] = epilogue_v(p.epi, acc[ri][m], e.b[ri], e.r[ri][m]);
+                    if (m < p.M) p.y[(size_t)m * p.ldy + row] = epilogue_v(p.epi, acc[ri][m], (uint16_t)e.b[ri], (uint16_t)e.r[ri][m]);
         }
     }
 }
@@ -542,7 +578,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     const int nbr = p.K >> 5;
     constexpr int NL = BlkLoads<WT>::n;
     u4 q[RI][NB][NL];
-    uint16_t ds[RI][NB];
+    uint32_t ds[RI][NB];   // scales zero-extended: no packing that would force an early wait
     load_rows<WT, NB, RI>(p, row0, lane, q, ds);
     EpiPre<RI, MX> pre;
     if (lane == 0) epi_preload<RI, MX>(p, row0, pre);
@@ -588,9 +624,12 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams p) {
     const int nbr = p.K >> 5;
     constexpr int NL = BlkLoads<WT>::n;
     u4 q[RI][NB][NL];
-    uint16_t ds[RI][NB];
+    uint32_t ds[RI][NB];   // scales zero-extended: no packing that would force an early wait
     // position first: the RoPE table loads depend on it
     const int pos = p.epi == EPI_QKV_ROPE ? p.pos0 + (p.d_pos ? *p.d_pos : 0) : 0;
+    const uint16_t* xsrc = p.embd ? p.embd + (size_t)(*p.d_token) * p.K : p.x;
+    NormStage<WT, NB, WPB, PRO> st;
+    st.load(p, xsrc);
     if (row0 < p.N) load_rows<WT, NB, RI>(p, row0, lane, q, ds);
     EpiPre<RI, 1> pre;
     QkvPre qp[RI / 2 > 0 ? RI / 2 : 1];
@@ -603,8 +642,7 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams p) {
             epi_preload<RI, 1>(p, row0, pre);
         }
     }
-    const uint16_t* xsrc = p.embd ? p.embd + (size_t)(*p.d_token) * p.K : p.x;
-    stage_norm<WT, NB, WPB, PRO>(p, xsrc, xs, red);
+    st.finish(p, xs, red);
 
     float acc[RI][1];
 #pragma unroll
@@ -645,7 +683,7 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams p) {
             const int row = row0 + ri;
             if (row < p.N) {
                 uint16_t r = f2h(acc[ri][0]);
-                if (p.bias) r = add_h(r, pre.b[ri]);
+                if (p.bias) r = add_h(r, (uint16_t)pre.b[ri]);
                 p.y[row] = r;
                 best = umax64(best, amax_key(r, row));
             }
