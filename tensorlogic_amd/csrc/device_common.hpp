@@ -89,6 +89,16 @@ __device__ __forceinline__ float group8_sum(float v) {
     return v;
 }
 
+// Sum over the lanes of a wave that share (lane & 7): lanes l, l+8, ...,
+// l+56, the same value in all eight (row_ror:8 within each row of 16, then
+// the rows by two xor shuffles).
+__device__ __forceinline__ float stride8_sum(float v) {
+    v += dpp_f<0x128>(v);   // row_ror:8
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
 // Sum over the 64-lane wave, the same value in every lane (fixed order:
 // quads, 8s and 16s by DPP, then the rows by two xor shuffles).
 template <int W>

@@ -108,7 +108,7 @@ constexpr int A64_UNR = 8;
 __global__ __launch_bounds__(256) void attention64_kernel(AttnArgs a, int J_fixed) {
     __shared__ float sc[ATT_MAX_J];
     __shared__ float red[4];
-    __shared__ float part[32][65];
+    __shared__ float part[4][64];
     const int s = blockIdx.x, h = blockIdx.y;
     const int Hkv = a.Hkv;
     const int kvh = h / (a.H / Hkv);
@@ -236,12 +236,15 @@ __global__ __launch_bounds__(256) void attention64_kernel(AttnArgs a, int J_fixe
             }
         }
     }
+    // the 8 key groups of each wave (lanes with the same c), then the 4 waves
 #pragma unroll
-    for (int e = 0; e < 8; e++) part[g][8 * c + e] = o[e];
-    __syncthreads();
+    for (int e = 0; e < 8; e++) o[e] = stride8_sum(o[e]);
+    if ((tid & 63) < 8)
+#pragma unroll
+        for (int e = 0; e < 8; e++) part[tid >> 6][8 * c + e] = o[e];
+    lds_barrier();
     if (tid < 64) {
-        float t = part[0][tid];
-        for (int gg = 1; gg < 32; gg++) t += part[gg][tid];
+        const float t = (part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]);
         a.out[(size_t)s * os + (size_t)h * 64 + tid] = f2h(t);
     }
 }

@@ -753,12 +753,12 @@ static bool launch_mx(hipStream_t s, const GemvParams& p, int nb, int ri) {
 
 // Normalised GEMV shapes: rows per wave and waves per workgroup chosen by
 // the measured optimum of the decoder's shapes on MI355X (more rows per
-// workgroup amortise the staging; tall matrices take 16-wave groups).
+// workgroup amortise the staging; tall matrices take 4 rows per wave).
 template <int WT, int NB, int PRO>
 static void launch_norm_shape(hipStream_t s, const GemvParams& p) {
     if (p.N >= 16384 && p.epi != EPI_QKV_ROPE && p.epi != EPI_SWIGLU_PAIR) {
-        const int wgs = (p.N + 63) / 64;   // 16 waves x 4 rows
-        hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 4, 16, PRO>), dim3(wgs), dim3(1024), 0, s, p);
+        const int wgs = (p.N + 31) / 32;   // 8 waves x 4 rows
+        hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 4, 8, PRO>), dim3(wgs), dim3(512), 0, s, p);
     } else if (p.N >= 8192) {
         const int wgs = (p.N + 15) / 16;   // 8 waves x 2 rows
         hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 2, 8, PRO>), dim3(wgs), dim3(512), 0, s, p);
@@ -784,7 +784,7 @@ static bool launch_norm(hipStream_t s, const GemvParams& p, int nb, int pro) {
 }
 
 int gemv_norm_slots(int N) {
-    if (N >= 16384) return (N + 63) / 64;
+    if (N >= 16384) return (N + 31) / 32;
     if (N >= 8192) return (N + 15) / 16;
     return (N + 7) / 8;
 }
