@@ -92,6 +92,38 @@ def config2_q8(dev, iters: int, copies: int = 24):
     return res
 
 
+def config3_attention(dev, iters: int = 20):
+    """Config 3 attention block: causal prefill over S = 46 and 2048 query
+    rows (32 query heads, 4 KV heads, head_dim 64, f16 K/V) and one decode
+    query against 2048 cached keys; hipEvents around back-to-back calls.
+    Algorithmic flops of causal prefill = 2 * 2 * H * D * S(S+1)/2 (QK^T and
+    P.V over the unmasked keys)."""
+    from tensorlogic_amd import Timer, attention
+    from tensorlogic_amd import synth as S
+    H, Hkv, D = 32, 4, 64
+    res = {}
+    for label, Sq, J, q0 in (("prefill_S46", 46, 46, 0), ("prefill_S2048", 2048, 2048, 0),
+                             ("decode_ctx2048", 1, 2048, 2047)):
+        q = dev.tensor(S.normal_f16(103, f"att_q{Sq}", (Sq, H, D)))
+        k = dev.tensor(S.normal_f16(103, f"att_k{J}", (J, Hkv, D)))
+        v = dev.tensor(S.normal_f16(103, f"att_v{J}", (J, Hkv, D)))
+        out = dev.empty((Sq, H, D))
+        for _ in range(3):
+            attention(q, k, v, q0, 0.125, True, out=out)
+        n = iters if Sq > 1 else 10 * iters
+        with Timer(dev) as t:
+            for _ in range(n):
+                attention(q, k, v, q0, 0.125, True, out=out)
+        us = t.ms * 1000.0 / n
+        keys = sum(min(J, q0 + s + 1) for s in range(Sq))
+        fl = 4.0 * H * D * keys
+        kv_bytes = 2 * 2 * J * Hkv * D
+        res[label] = dict(us=us, tflops=fl / us / 1e6, kv_gbs=kv_bytes / us / 1e3)
+        del q, k, v, out
+        dev.sync()
+    return res
+
+
 def copy_reference(dev, iters: int):
     """Plain copy kernel: 6.5 MB (the GEMV's size, 48 rotating sources) and
     1 GiB -- the streaming bandwidth this device reaches at each size."""
@@ -144,9 +176,10 @@ def main():
     ap.add_argument("--decode-launch", choices=("graph", "direct"), default="graph",
                     help="replay one captured HIP graph per decode step (default) or launch the same "
                          "kernels one by one (profiler runs)")
-    ap.add_argument("--part", choices=("all", "gemv", "gemm"), default="all",
+    ap.add_argument("--part", choices=("all", "gemv", "gemm", "attn"), default="all",
                     help="'gemv': only the GEMV roofline and copy legs (for counter passes); "
-                         "'gemm': only the config-2 Q8_0 GEMV/GEMM leg")
+                         "'gemm': only the config-2 Q8_0 GEMV/GEMM leg; 'attn': only the "
+                         "config-3 attention leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (asked for {args.gpus}); the hot path is "
@@ -164,6 +197,13 @@ def main():
             log(f"Q8_0 {k}: {v['us']:.2f} us, {v['gbs']:.0f} GB/s, {v['tflops']:.1f} TFLOP/s")
         dev.close()
         print(json.dumps({"config2": c2}), flush=True)
+        return
+    if args.part == "attn":
+        c3 = config3_attention(dev)
+        for k, v in c3.items():
+            log(f"attention {k}: {v['us']:.2f} us, {v['tflops']:.2f} TFLOP/s")
+        dev.close()
+        print(json.dumps({"config3": c3}), flush=True)
         return
     if args.part == "gemv":
         gem = gemv_roofline(dev, args.gemv_iters)
@@ -211,6 +251,9 @@ def main():
     c2 = config2_q8(dev, 200)
     for k, v in c2.items():
         log(f"Q8_0 {k}: {v['us']:.2f} us, {v['gbs']:.0f} GB/s, {v['tflops']:.1f} TFLOP/s")
+    c3 = config3_attention(dev)
+    for k, v in c3.items():
+        log(f"attention {k}: {v['us']:.2f} us, {v['tflops']:.2f} TFLOP/s")
     g = gem["5632x2048"]
     dev.close()
 
@@ -253,6 +296,7 @@ def main():
             "gemv_2048x5632": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in gem.items()},
             "copy_reference": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in cp.items()},
             "config2_q8_0": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c2.items()},
+            "config3_attention": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c3.items()},
         },
         "roofline": {
             "kernel": GEMV_KERNEL,

@@ -229,6 +229,11 @@ tlhip_status tlhip_bench_copy(tlhip_ctx ctx, size_t bytes, int n_buf, int iters,
  * context stream) and the 1 + n_decode tokens.                           */
 tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode,
                                 int use_graph, int32_t* tokens_out, float* prefill_ms, float* decode_ms);
+/* Event pair on the context stream around any sequence of asynchronous
+ * calls: timer_start records the first event; timer_stop records the
+ * second, waits for it and returns the elapsed ms.                       */
+tlhip_status tlhip_timer_start(tlhip_ctx ctx);
+tlhip_status tlhip_timer_stop(tlhip_ctx ctx, float* ms);
 
 #ifdef __cplusplus
 }

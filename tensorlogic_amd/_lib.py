@@ -91,6 +91,8 @@ SIGNATURES = {
     "tlhip_bench_linear": (_i, [_vp, _vp, C.POINTER(_vp), _i, _vp, _i, _i, C.POINTER(_f)]),
     "tlhip_bench_copy": (_i, [_vp, _sz, _i, _i, C.POINTER(_f)]),
     "tlhip_bench_decode": (_i, [_vp, _i32p, _i, _i, _i, _i32p, C.POINTER(_f), C.POINTER(_f)]),
+    "tlhip_timer_start": (_i, [_vp]),
+    "tlhip_timer_stop": (_i, [_vp, C.POINTER(_f)]),
 }
 
 _lib = None

@@ -205,6 +205,11 @@ tlhip_status launch_stream_copy(hipStream_t s, const void* src, void* dst, size_
 tlhip_status launch_transpose(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows, int cols);
 tlhip_status launch_attention(hipStream_t s, const AttnArgs& a);   // decode: J from *d_pos
 tlhip_status launch_attention_j(hipStream_t s, const AttnArgs& a, int J);
+// Prefill through the matrix cores when attention_mfma_ok(); vt is scratch
+// of attention_mfma_scratch() bytes (V transposed per KV head).
+bool attention_mfma_ok(const AttnArgs& a, int J);
+size_t attention_mfma_scratch(int J, int Hkv, int D);
+tlhip_status launch_attention_mfma(hipStream_t s, const AttnArgs& a, int J, uint16_t* vt);
 constexpr int kAttnMaxKeys = 8192;
 tlhip_status launch_copy_rows(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows,
                               int row_elems, int src_stride, int dst_stride, const int32_t* d_pos,

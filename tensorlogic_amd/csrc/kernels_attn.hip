@@ -361,6 +361,382 @@ __global__ __launch_bounds__(256) void attention_dk_kernel(AttnArgs a, int J_fix
     }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill attention on the matrix cores (S >= 32 query rows, head_dim a
+// multiple of 16 up to 128).  Same arithmetic and rounding points as the
+// kernels above -- f16 scores, f16 scale, masked keys skipped, exp in f32,
+// P = f16(f16(e) / sum), fp32 accumulation of P.V -- organised so the two
+// contractions run as v_mfma_f32_32x32x16_f16:
+//   S^T[key][query] = K . Q^T  (A = 32 keys x 16 dims from K rows, B = 32
+//                              queries x 16 dims from Q rows)
+//   O[query][d]     = P . V    (A = P straight from S^T's accumulators,
+//                              B = V^T rows from a transposed copy of V)
+// In S^T's accumulator layout lane l owns query l%32 and keys
+// 8(r/4) + 4(l/32) + r%4 (r = 0..15): the row statistics are per lane plus
+// one exchange with lane l^32, and registers 8t..8t+7 are exactly the
+// A operand of k-step t under the key order 16t + 8(i/4) + 4(l/32) + i%4,
+// which V^T is read in (two 4-key runs per lane).
+// Pass 1 over the key tiles keeps a running max and a rescaled sum of
+// exp(s - max); pass 2 recomputes the scores, forms P with the final max and
+// sum, and accumulates P.V.  Two waves own one head and a 32-row query tile
+// (causal: the pair of tiles t and n-1-t, so every workgroup does the same
+// work), each taking half of the key tiles; their row statistics meet in LDS
+// after pass 1 and the upper half's partial O is added by the lower half
+// after pass 2.  A workgroup holds four heads (two for head_dim 128), which
+// under GQA share their K/V head in L1/L2.
+// ---------------------------------------------------------------------------
+
+// V [J, Hkv, D] -> Vt [Hkv, D, Jp], zero for keys J..Jp-1 (Jp % 32 == 0).
+__global__ __launch_bounds__(256) void vt_transpose_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt,
+                                                         int J, int Jp, int Hkv, int D) {
+    __shared__ uint16_t tile[128][33];
+    const int j0 = blockIdx.x * 32, kvh = blockIdx.y;
+    const size_t kstride = (size_t)Hkv * D;
+    for (int d0 = 0; d0 < D; d0 += 128) {
+        const int dn = min(128, D - d0);
+        for (int i = threadIdx.x; i < 32 * dn; i += 256) {
+            const int jj = i / dn, d = i % dn, j = j0 + jj;
+            tile[d][jj] = j < J ? v[(size_t)j * kstride + (size_t)kvh * D + d0 + d] : (uint16_t)0;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < 32 * dn; i += 256) {
+            const int d = i / 32, jj = i % 32;
+            vt[((size_t)kvh * D + d0 + d) * Jp + j0 + jj] = tile[d][jj];
+        }
+        __syncthreads();
+    }
+}
+
+__device__ __forceinline__ h8 zero_h8() {
+    h8 z;
+#pragma unroll
+    for (int i = 0; i < 8; i++) z[i] = (h16)0.0f;
+    return z;
+}
+
+// The correctly rounded quotient a / b given r ~ 1/b (one residual
+// correction of the product; a in [0, 1], b >= 1 here).
+__device__ __forceinline__ float div_corr(float a, float b, float r) {
+    const float q = a * r;
+    return fmaf(fmaf(-b, q, a), r, q);
+}
+
+// Score of an excluded key: finite, so differences stay finite, and far
+// enough below any f16 score that its exponential is exactly 0.
+constexpr float FA_NEG = -1.0e30f;
+
+// e^x for x <= 0 to a few f32 ulps: the terms of the softmax denominator,
+// whose sum only needs f32-level relative accuracy.
+__device__ __forceinline__ float exp_sum(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.44269502162933349609375f);
+}
+
+// Running (max, sum) pairs combined: each sum rescaled to the common max.
+__device__ __forceinline__ float fa_merge(float m1, float s1, float m2, float s2, float m) {
+    return (m1 > FA_NEG ? s1 * exp_sum(m1 - m) : 0.0f) + (m2 > FA_NEG ? s2 * exp_sum(m2 - m) : 0.0f);
+}
+
+template <int D>
+struct FaWave {
+    static constexpr int KS = D / 16;          // k-steps of QK^T
+    static constexpr int NT = (D + 31) / 32;   // 32-wide output tiles of P.V
+
+    AttnArgs a;
+    const uint16_t* vt;
+    int J, Jp, h, kvh, lane, qs, os;
+    size_t kstride;
+
+    __device__ FaWave(const AttnArgs& a_, const uint16_t* vt_, int J_, int Jp_, int h_)
+        : a(a_), vt(vt_), J(J_), Jp(Jp_), h(h_) {
+        kvh = h / (a.H / a.Hkv);
+        lane = threadIdx.x & 63;
+        qs = a.q_stride ? a.q_stride : a.H * D;
+        os = a.out_stride ? a.out_stride : a.H * D;
+        kstride = (size_t)a.Hkv * D;
+    }
+
+    // K rows of tile kt (rows past J read row J-1: their scores are masked)
+    __device__ __forceinline__ void load_k(int kt, h8 (&kf)[KS]) const {
+        const int j = min(kt * 32 + (lane & 31), J - 1);
+        const uint16_t* kr = a.k + (size_t)j * kstride + (size_t)kvh * D + 8 * (lane >> 5);
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) kf[ks] = *(const h8*)(kr + 16 * ks);
+    }
+
+    // V^T operands of tile kt (columns past D read column D-1: their output
+    // columns are not stored; keys J..Jp-1 are zero in vt)
+    __device__ __forceinline__ void load_v(int kt, h8 (&vb)[NT][2]) const {
+        const int jb = kt * 32 + 4 * (lane >> 5);
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const int d = min(32 * n + (lane & 31), D - 1);
+            const uint16_t* vr = vt + ((size_t)kvh * D + d) * Jp + jb;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint2 lo = *(const uint2*)(vr + 16 * t);
+                const uint2 hi = *(const uint2*)(vr + 16 * t + 8);
+                const u4 w = {lo.x, lo.y, hi.x, hi.y};
+                vb[n][t] = __builtin_bit_cast(h8, w);
+            }
+        }
+    }
+
+    __device__ __forceinline__ f16v qk(const h8 (&qf)[KS], const h8 (&kf)[KS]) const {
+        f16v acc = {};
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks], qf[ks], acc, 0, 0, 0);
+        return acc;
+    }
+
+    // scores of key tile kt for this lane's query, as the reference stores
+    // them (f16 dot product, then the f16 product with the f16 scale);
+    // excluded keys (masked, past J, non-finite) come back as FA_NEG.
+    // FULL: every key of the tile is unmasked for every query of the wave.
+    template <bool FULL>
+    __device__ __forceinline__ void scores(int kt, const f16v& acc, int jlim, float (&sv)[16]) const {
+        const int jb = kt * 32 + 4 * (lane >> 5);
+        const h2 sc2 = {(h16)a.scale_h, (h16)a.scale_h};
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+            h2 x = {(h16)acc[r], (h16)acc[r + 1]};
+            x = x * sc2;
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const float v = (float)x[u];
+                bool ok = isfinite(v);
+                if (!FULL) ok = ok && jb + 8 * ((r + u) >> 2) + ((r + u) & 3) <= jlim;
+                sv[r + u] = ok ? v : FA_NEG;
+            }
+        }
+    }
+
+    // pass 1 over tiles [k0, k1): running max and rescaled sum of exp(s - max)
+    __device__ __forceinline__ void pass1(const h8 (&qf)[KS], int k0, int k1, int nfull, int jlim, float& mx,
+                                          float& sum) const {
+        mx = FA_NEG;
+        sum = 0.0f;
+        if (k0 >= k1) return;
+        // the QK^T product of tile kt+1 runs on the matrix core while the
+        // vector unit works on tile kt
+        h8 kf[KS];
+        load_k(k0, kf);
+        f16v acc = qk(qf, kf);
+        if (k0 + 1 < k1) load_k(k0 + 1, kf);
+        for (int kt = k0; kt < k1; kt++) {
+            f16v accn = acc;
+            if (kt + 1 < k1) accn = qk(qf, kf);
+            if (kt + 2 < k1) load_k(kt + 2, kf);
+            float sv[16];
+            if (kt < nfull) scores<true>(kt, acc, jlim, sv);
+            else scores<false>(kt, acc, jlim, sv);
+            acc = accn;
+            float mt = sv[0];
+#pragma unroll
+            for (int r = 1; r < 16; r++) mt = fmaxf(mt, sv[r]);
+            if (mt > mx) {
+                sum = sum * exp_sum(mx - mt);
+                mx = mt;
+            }
+            float es[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) es[r] = exp_sum(sv[r] - mx);
+            // pairwise, so the adds are not one dependent chain
+#pragma unroll
+            for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+                for (int r = 0; r < w; r++) es[r] += es[r + w];
+            if (mx > FA_NEG) sum += es[0];
+        }
+    }
+
+    // pass 2 over tiles [k0, k1): P = f16(f16(e) / sum) (DEG: rows with no
+    // finite score weight every key < J by f16(1/J)), O += P . V
+    template <bool DEG>
+    __device__ __forceinline__ void pass2(const h8 (&qf)[KS], int k0, int k1, int nfull, int jlim, float m,
+                                          float tot, bool deg, f16v (&o)[NT]) const {
+        if (k0 >= k1) return;
+        const float rt = 1.0f / tot;
+        const float uni = h2f(f2h(1.0f / (float)J));
+        // the QK^T product of tile kt+1 runs on the matrix core while the
+        // vector unit forms P of tile kt
+        h8 kf[KS];
+        load_k(k0, kf);
+        f16v acc = qk(qf, kf);
+        if (k0 + 1 < k1) load_k(k0 + 1, kf);
+        for (int kt = k0; kt < k1; kt++) {
+            h8 vb[NT][2];
+            load_v(kt, vb);
+            f16v accn = acc;
+            if (kt + 1 < k1) accn = qk(qf, kf);
+            if (kt + 2 < k1) load_k(kt + 2, kf);
+            float sv[16];
+            if (kt < nfull) scores<true>(kt, acc, jlim, sv);
+            else scores<false>(kt, acc, jlim, sv);
+            acc = accn;
+            // e = f16(exp(x)), x = s - max <= 0: 2^(x log2 e) on v_exp_f32,
+            // with the rounding error of the product x * f32(log2 e) and the
+            // tail of log2 e added back as a first-order term, so e stays
+            // within about an ulp of exp(x) before its f16 rounding.  Written
+            // stage by stage over the 16 scores, so 16 independent chains
+            // stand between dependent instructions.
+            constexpr float L1 = 1.44269502162933349609375f, L2 = 1.925963033500011e-8f;
+            constexpr float LN2 = 0.6931471805599453f;
+            float x[16], t[16], e[16], c[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) x[r] = sv[r] - m;
+#pragma unroll
+            for (int r = 0; r < 16; r++) t[r] = x[r] * L1;
+#pragma unroll
+            for (int r = 0; r < 16; r++) e[r] = __builtin_amdgcn_exp2f(t[r]);
+#pragma unroll
+            for (int r = 0; r < 16; r++) c[r] = fmaf(x[r], L2, fmaf(x[r], L1, -t[r]));
+            h8 pa[2];
+#pragma unroll
+            for (int r = 0; r < 16; r++) pa[r >> 3][r & 7] = (h16)fmaf(e[r] * LN2, c[r], e[r]);   // f16(exp(x))
+#pragma unroll
+            for (int r = 0; r < 16; r++) e[r] = (float)pa[r >> 3][r & 7];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                float pv = div_corr(e[r], tot, rt);
+                if (DEG) {
+                    const int j = kt * 32 + 4 * (lane >> 5) + 8 * (r >> 2) + (r & 3);
+                    pv = deg ? (j < J ? uni : 0.0f) : pv;
+                }
+                pa[r >> 3][r & 7] = (h16)pv;
+            }
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int t = 0; t < 2; t++) o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[t], vb[n][t], o[n], 0, 0, 0);
+        }
+    }
+
+    // Query tile qt, key half `half` of its tiles.  stm/sts: this head's
+    // [2][32] exchange of row statistics; ob: [NT][16][64] partial O of the
+    // upper half.  Two workgroup barriers, reached by every wave.
+    __device__ void run(int qt, int half, bool store, float* stm, float* sts, float* ob) const {
+        const int s0 = qt * 32;
+        const int myq = s0 + (lane & 31);
+        const int qpos = a.q_pos0 + myq;
+        const int last = min(s0 + 31, a.S - 1);
+        const int kend = a.causal ? min(J, a.q_pos0 + last + 1) : J;
+        const int nkt = (kend + 31) / 32;
+        const int jlim = a.causal ? min(J - 1, qpos) : J - 1;
+        // tiles below every query's limit need no mask test
+        const int lo_lim = a.causal ? min(J - 1, a.q_pos0 + s0) : J - 1;
+        const int nfull = (lo_lim + 1) / 32;
+        const int nh = (nkt + 1) / 2;
+
+        h8 qf[KS];
+        {
+            const uint16_t* qr = a.q + (size_t)min(myq, a.S - 1) * qs + (size_t)h * D + 8 * (lane >> 5);
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) qf[ks] = *(const h8*)(qr + 16 * ks);
+        }
+
+        float mx, sum;
+        pass1(qf, half ? nh : 0, half ? nkt : nh, nfull, jlim, mx, sum);
+        // the other 16 keys of every tile sit in lane l ^ 32, the other key
+        // half in the partner wave; both sides form the same sums
+        const float mo = __shfl_xor(mx, 32, 64), so = __shfl_xor(sum, 32, 64);
+        const float m1 = fmaxf(mx, mo);
+        const float t1 = fa_merge(mx, sum, mo, so, m1);
+        if (lane < 32) {
+            stm[half * 32 + lane] = m1;
+            sts[half * 32 + lane] = t1;
+        }
+        __syncthreads();
+        const float m2 = stm[(half ^ 1) * 32 + (lane & 31)], t2 = sts[(half ^ 1) * 32 + (lane & 31)];
+        const float m = fmaxf(m1, m2);
+        const float tot = fa_merge(m1, t1, m2, t2, m);
+        const bool deg = !(tot > 0.0f && isfinite(tot)) && myq < a.S;
+
+        f16v o[NT];
+#pragma unroll
+        for (int n = 0; n < NT; n++) o[n] = f16v{};
+        if (__any(deg)) {
+            const int nk = Jp / 32, nhd = (nk + 1) / 2;
+            pass2<true>(qf, half ? nhd : 0, half ? nk : nhd, 0, jlim, m, tot, deg, o);
+        } else {
+            pass2<false>(qf, half ? nh : 0, half ? nkt : nh, nfull, jlim, m, tot, false, o);
+        }
+
+        if (half) {
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) ob[(n * 16 + r) * 64 + lane] = o[n][r];
+        }
+        __syncthreads();
+        if (!half && store) {
+            // O accumulators: column d = 32n + l%32, rows 8(r/4) + 4(l/32) + r%4
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                const int d = 32 * n + (lane & 31);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = s0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    const float t = o[n][r] + ob[(n * 16 + r) * 64 + lane];
+                    if (row < a.S && d < D) a.out[(size_t)row * os + (size_t)h * D + d] = f2h(t);
+                }
+            }
+        }
+    }
+};
+
+// Heads per workgroup (each head = two waves, one per key half).
+template <int D>
+constexpr int fa_heads() { return D > 80 ? 2 : 4; }
+
+template <int D>
+__global__ __launch_bounds__(fa_heads<D>() * 128) void attention_mfma_kernel(AttnArgs a, const uint16_t* __restrict__ vt, int J,
+                                                             int Jp, int nqt) {
+    constexpr int HPW = fa_heads<D>(), NT = (D + 31) / 32;
+    __shared__ float stm[HPW][64], sts[HPW][64];
+    __shared__ float ob[HPW][NT * 16 * 64];
+    const int w = threadIdx.x >> 6, hw = w % HPW, half = w / HPW;
+    const int hh = blockIdx.y * HPW + hw;
+    const FaWave<D> fw(a, vt, J, Jp, min(hh, a.H - 1));
+    const bool store = hh < a.H;
+    if (a.causal) {
+        const int t0 = nqt - 1 - (int)blockIdx.x, t1 = blockIdx.x;
+        fw.run(t0, half, store, stm[hw], sts[hw], ob[hw]);
+        if (t1 < t0) fw.run(t1, half, store, stm[hw], sts[hw], ob[hw]);
+    } else {
+        fw.run(blockIdx.x, half, store, stm[hw], sts[hw], ob[hw]);
+    }
+}
+
+bool attention_mfma_ok(const AttnArgs& a, int J) {
+    const int qs = a.q_stride ? a.q_stride : a.H * a.D;
+    return a.S >= 128 && J >= 1 && (a.D == 64 || a.D == 80 || a.D == 128) && !a.d_pos && qs % 8 == 0 &&
+           ((uintptr_t)a.q % 16) == 0 && ((uintptr_t)a.k % 16) == 0;
+}
+
+size_t attention_mfma_scratch(int J, int Hkv, int D) {
+    return (size_t)Hkv * D * (size_t)((J + 31) / 32 * 32) * sizeof(uint16_t);
+}
+
+// Prefill over J keys through the matrix cores; vt holds
+// attention_mfma_scratch(J, Hkv, D) bytes.
+tlhip_status launch_attention_mfma(hipStream_t s, const AttnArgs& a, int J, uint16_t* vt) {
+    if (!attention_mfma_ok(a, J) || !vt)
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "attention: shape not on the matrix-core path");
+    if (a.Hkv <= 0 || a.H % a.Hkv) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: heads %d/%d", a.H, a.Hkv);
+    if (J > ATT_MAX_J) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: %d keys > %d", J, ATT_MAX_J);
+    const int Jp = (J + 31) / 32 * 32;
+    hipLaunchKernelGGL(vt_transpose_kernel, dim3(Jp / 32, a.Hkv), dim3(256), 0, s, a.v, vt, J, Jp, a.Hkv, a.D);
+    const int nqt = (a.S + 31) / 32;
+    const int gx = a.causal ? (nqt + 1) / 2 : nqt;
+    if (a.D == 64)
+        hipLaunchKernelGGL(attention_mfma_kernel<64>, dim3(gx, (a.H + 3) / 4), dim3(512), 0, s, a, vt, J, Jp, nqt);
+    else if (a.D == 80)
+        hipLaunchKernelGGL(attention_mfma_kernel<80>, dim3(gx, (a.H + 3) / 4), dim3(512), 0, s, a, vt, J, Jp, nqt);
+    else
+        hipLaunchKernelGGL(attention_mfma_kernel<128>, dim3(gx, (a.H + 1) / 2), dim3(256), 0, s, a, vt, J, Jp, nqt);
+    return TLHIP_OK;
+}
+
 static void launch_attn_any(hipStream_t s, const AttnArgs& a, int J) {
     if (a.D == 64) hipLaunchKernelGGL(attention64_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, J);
     else if (a.D == 80) hipLaunchKernelGGL(attention_dk_kernel<80>, dim3(a.S, a.H), dim3(256), 0, s, a, J);

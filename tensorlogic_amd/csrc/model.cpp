@@ -63,6 +63,7 @@ struct tlhip_model_s {
     tlhip_tensor x = nullptr, xn = nullptr, qkv = nullptr, qrot = nullptr, att = nullptr, hmid = nullptr,
                  logits = nullptr;
     unsigned long long* d_amax = nullptr;   // per-workgroup greedy keys of the lm_head GEMV
+    uint16_t* d_vt = nullptr;                // V transposed per KV head for matrix-core prefill attention
     float* ws = nullptr;          // split-K partials of the prefill GEMMs
     size_t ws_bytes = 0;
     int32_t* d_state = nullptr;   // {token, pos, step}
@@ -368,7 +369,8 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
             TLHIP_TRY(launch_attention(s, at));
         } else {
             at.q_pos0 = pos0;
-            TLHIP_TRY(launch_attention_j(s, at, pos0 + S));
+            if (attention_mfma_ok(at, pos0 + S)) TLHIP_TRY(launch_attention_mfma(s, at, pos0 + S, m->d_vt));
+            else TLHIP_TRY(launch_attention_j(s, at, pos0 + S));
         }
         if (m->arch == 0) {
             TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_RESID, P(m->x), 0, m->ws, m->ws_bytes));
@@ -600,6 +602,7 @@ tlhip_status tlhip_model_free(tlhip_model m) {
     tlhip_kvcache_free(m->kv);
     for (tlhip_tensor t : {m->x, m->xn, m->qkv, m->qrot, m->att, m->hmid, m->logits}) tlhip_tensor_free(t);
     if (m->d_amax) (void)hipFree(m->d_amax);
+    if (m->d_vt) (void)hipFree(m->d_vt);
     if (m->ws) (void)hipFree(m->ws);
     if (m->d_state) (void)hipFree(m->d_state);
     if (m->d_tokens) (void)hipFree(m->d_tokens);
@@ -704,6 +707,7 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
         if ((st = alloc_tensor(ctx, TLHIP_F16, 1, s_l, &m->logits)) != TLHIP_OK) break;
         hipError_t e = hipMalloc(&m->d_state, 4 * sizeof(int32_t));
         if (e == hipSuccess) e = hipMalloc(&m->d_amax, sizeof(unsigned long long) * gemv_norm_slots(m->vocab));
+        if (e == hipSuccess) e = hipMalloc(&m->d_vt, attention_mfma_scratch(m->max_ctx, m->n_kv, m->head_dim));
         // split-K workspace: the largest partial set any prefill GEMM of this model uses
         if (e == hipSuccess) {
             const int64_t shapes[4][2] = {{H + 2 * kvd, H}, {H, H}, {arch == 0 ? 2 * I : I, H}, {H, I}};
@@ -874,6 +878,21 @@ tlhip_status tlhip_bench_copy(tlhip_ctx ctx, size_t bytes, int n_buf, int iters,
     if (dst) (void)hipFree(dst);
     if (st == TLHIP_OK) *avg_us = ms * 1000.0f / (float)iters;
     return st;
+}
+
+tlhip_status tlhip_timer_start(tlhip_ctx ctx) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_CHECK_HIP(hipEventRecord(ctx->ev0, ctx->stream));
+    return TLHIP_OK;
+}
+
+tlhip_status tlhip_timer_stop(tlhip_ctx ctx, float* ms) {
+    TLHIP_TRY(check_ctx(ctx));
+    if (!ms) return fail(TLHIP_ERR_INVALID_ARGUMENT, "timer_stop: null output");
+    TLHIP_CHECK_HIP(hipEventRecord(ctx->ev1, ctx->stream));
+    TLHIP_CHECK_HIP(hipEventSynchronize(ctx->ev1));
+    TLHIP_CHECK_HIP(hipEventElapsedTime(ms, ctx->ev0, ctx->ev1));
+    return TLHIP_OK;
 }
 
 tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode, int use_graph,

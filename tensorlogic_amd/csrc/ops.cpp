@@ -340,7 +340,15 @@ tlhip_status tlhip_attention(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhi
     a.q_pos0 = q_pos0;
     a.causal = causal;
     a.scale_h = round_f16(scale);
-    TLHIP_TRY(launch_attention_j(ctx->stream, a, J));
+    if (attention_mfma_ok(a, J)) {
+        void* vt = nullptr;
+        TLHIP_CHECK_HIP(hipMallocAsync(&vt, attention_mfma_scratch(J, Hkv, D), ctx->stream));
+        const tlhip_status st = launch_attention_mfma(ctx->stream, a, J, (uint16_t*)vt);
+        (void)hipFreeAsync(vt, ctx->stream);
+        TLHIP_TRY(st);
+    } else {
+        TLHIP_TRY(launch_attention_j(ctx->stream, a, J));
+    }
     return after_launch(ctx, "attention");
 }
 

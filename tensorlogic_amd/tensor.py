@@ -249,10 +249,11 @@ def einsum(eq: str, a: Tensor, b: Tensor) -> Tensor:
 
 
 def attention(q: Tensor, k: Tensor, v: Tensor, q_pos0: int = 0, scale: float | None = None,
-              causal: bool = True) -> Tensor:
+              causal: bool = True, out: Tensor | None = None) -> Tensor:
     if scale is None:
         scale = 1.0 / np.sqrt(q.shape[2])
-    out = q.dev.empty(q.shape)
+    if out is None:
+        out = q.dev.empty(q.shape)
     call("tlhip_attention", q.dev.h, q.h, k.h, v.h, int(q_pos0), float(scale), int(causal), out.h)
     return out
 
@@ -399,6 +400,25 @@ def bench_linear(dev: Device, x: Tensor, ws: Sequence[Tensor], y: Tensor, iters:
     us = C.c_float()
     call("tlhip_bench_linear", dev.h, x.h, arr, len(ws), y.h, iters, int(per_launch), C.byref(us))
     return us.value
+
+
+class Timer:
+    """hipEvent pair on the device's stream around asynchronous calls:
+    ``with Timer(dev) as t: ...`` then ``t.ms``."""
+
+    def __init__(self, dev: Device):
+        self.dev, self.ms = dev, None
+
+    def __enter__(self):
+        call("tlhip_timer_start", self.dev.h)
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        if exc_type is None:
+            ms = C.c_float()
+            call("tlhip_timer_stop", self.dev.h, C.byref(ms))
+            self.ms = ms.value
+        return False
 
 
 def bench_copy(dev: Device, nbytes: int, n_buf: int, iters: int) -> float:

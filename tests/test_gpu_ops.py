@@ -238,16 +238,38 @@ def test_mask_and_einsums(dev, oracle):
     assert_close(fused, ref, what="fused attention")
 
 
-@pytest.mark.parametrize("Sq,J,H,Hkv,D,q0", [(1, 174, 32, 4, 64, 173), (46, 46, 32, 4, 64, 0),
-                                             (1, 768, 32, 32, 80, 767), (300, 300, 8, 4, 64, 0),
-                                             (2048, 2048, 4, 1, 64, 0)])
-def test_attention(dev, oracle, Sq, J, H, Hkv, D, q0):
+# S < 128 runs the one-workgroup-per-row kernels; S >= 128 the matrix-core
+# prefill kernel (two q-tiles per head pair of waves under causal masking,
+# key halves split between the waves, transposed V).
+@pytest.mark.parametrize("Sq,J,H,Hkv,D,q0,causal", [
+    (1, 174, 32, 4, 64, 173, True), (46, 46, 32, 4, 64, 0, True), (1, 768, 32, 32, 80, 767, True),
+    (31, 31, 4, 4, 64, 0, True), (64, 100, 8, 8, 80, 36, True), (97, 97, 8, 2, 128, 0, True),
+    (45, 77, 8, 4, 64, 0, False),
+    (128, 128, 4, 4, 64, 0, True), (300, 300, 8, 4, 64, 0, True), (2048, 2048, 4, 1, 64, 0, True),
+    (512, 512, 4, 4, 80, 0, True), (160, 200, 8, 8, 80, 40, True), (129, 129, 5, 1, 128, 0, True),
+    (200, 200, 6, 3, 64, 0, True), (128, 300, 4, 4, 80, 0, False), (250, 90, 4, 2, 128, 0, False)])
+def test_attention(dev, oracle, Sq, J, H, Hkv, D, q0, causal):
     q = S.normal_f16(11, "q", (Sq, H, D))
     k = S.normal_f16(11, "k", (J, Hkv, D))
     v = S.normal_f16(11, "v", (J, Hkv, D))
-    got = attention(dev.tensor(q), dev.tensor(k), dev.tensor(v), q0, 1 / np.sqrt(D), True).numpy()
-    ref = oracle.attention(q, k, v, q0, 1 / np.sqrt(D), True)
-    assert_close(got, ref, what=f"attention S={Sq} J={J}")
+    got = attention(dev.tensor(q), dev.tensor(k), dev.tensor(v), q0, 1 / np.sqrt(D), causal).numpy()
+    ref = oracle.attention(q, k, v, q0, 1 / np.sqrt(D), causal)
+    assert_close(got, ref, what=f"attention S={Sq} J={J} D={D} causal={causal}")
+
+
+@pytest.mark.parametrize("Sq", [8, 64, 160])
+def test_attention_degenerate_rows(dev, oracle, Sq):
+    """Rows whose every score overflows f16 take the reference softmax's
+    uniform 1/J weights (non-causal, so no -10000 masked scores exist)."""
+    H, Hkv, D, J = 4, 2, 64, 40
+    q = S.normal_f16(12, "q", (Sq, H, D))
+    q[::3] = np.float16(120.0)
+    k = np.abs(S.normal_f16(12, "k", (J, Hkv, D))) + np.float16(100.0)
+    v = S.normal_f16(12, "v", (J, Hkv, D))
+    got = attention(dev.tensor(q), dev.tensor(k), dev.tensor(v), 0, 0.125, False).numpy()
+    ref = oracle.attention(q, k, v, 0, 0.125, False)
+    assert np.isfinite(got).all()
+    assert_close(got, ref, what=f"degenerate attention S={Sq}")
 
 
 def test_embedding_and_argmax(dev, oracle):
