@@ -51,7 +51,9 @@ typedef enum {
     TLHIP_F32 = 1,
     TLHIP_I32 = 2,
     TLHIP_Q4_0 = 3,   /* GGUF Q4_0: 32-element blocks along K, 18 B/block */
-    TLHIP_Q8_0 = 4    /* GGUF Q8_0: 32-element blocks along K, 34 B/block */
+    TLHIP_Q8_0 = 4,   /* GGUF Q8_0: 32-element blocks along K, 34 B/block */
+    TLHIP_Q6_K = 5    /* GGUF Q6_K: 256-element super-blocks, 210 B each
+                         (dequantize_q6_k, gguf.rs:128-212)               */
 } tlhip_dtype;
 
 typedef enum {
@@ -83,7 +85,7 @@ tlhip_status tlhip_set_sync_every_op(tlhip_ctx ctx, int on);
 /* ---- tensors ------------------------------------------------------------- */
 /* MetalBuffer::new_uninit_pooled (metal_buffer.rs:213): device allocation
  * from the stream-ordered pool.  For Q4_0/Q8_0, ndim must be 2 and shape
- * [N, K] with K % 32 == 0.                                                 */
+ * [N, K] with K % 32 == 0; for Q6_K, K % 256 == 0.                        */
 tlhip_status tlhip_tensor_alloc(tlhip_ctx ctx, tlhip_dtype dtype, int ndim,
                                 const int64_t* shape, tlhip_tensor* out);
 /* MetalBuffer::from_slice (metal_buffer.rs:37) / Tensor::from_vec_gpu
@@ -117,8 +119,9 @@ tlhip_status tlhip_gguf_kv_u32(tlhip_gguf g, const char* key, uint32_t* v);
 tlhip_status tlhip_gguf_kv_f32(tlhip_gguf g, const char* key, float* v);
 
 /* ---- operators (Tensor methods / TL builtins) ---------------------------- */
-/* dequantize_q4_0 / dequantize_q8_0 (gguf.rs:22-112, mmap_gguf.rs:383-439)
- * on the device: q [N,K] packed -> out [N,K] f16, bit-exact.              */
+/* dequantize_q4_0 / dequantize_q8_0 / dequantize_q6_k (gguf.rs:22-212,
+ * mmap_gguf.rs:383-545) on the device: q [N,K] packed -> out [N,K] f16,
+ * bit-exact.                                                              */
 tlhip_status tlhip_dequantize(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor out_f16);
 /* linear(x, W[, b]) (builtin_math.rs:76-131) = matmul_transposed_b
  * (matmul.rs:241-458) then add(bias): y[M,N] = x[M,K] W[N,K]^T, fp32
@@ -151,7 +154,7 @@ tlhip_status tlhip_add(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tens
 tlhip_status tlhip_mul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y);
 /* tensor * scalar (mul_scalar): the scalar is rounded to f16 first.       */
 tlhip_status tlhip_mul_scalar(tlhip_ctx ctx, tlhip_tensor a, float s, tlhip_tensor y);
-/* embedding(table, ids) (builtin_nn.rs:627-812): table [V,H] F16/Q4_0/Q8_0,
+/* embedding(table, ids) (builtin_nn.rs:627-812): table [V,H] F16/Q4_0/Q8_0/Q6_K,
  * ids host int32[n] (bounds-checked on the host), out [n,H] f16.          */
 tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* ids, int n, tlhip_tensor out);
 /* apply_attention_mask(scores, mask) (masking.rs:36-51,147-165): where

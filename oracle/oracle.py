@@ -53,6 +53,7 @@ def _declare(L):
         "tlo_f2h_array": (None, [vp, vp, sz]),
         "tlo_dequant_q4_0": (None, [vp, sz, vp]),
         "tlo_dequant_q8_0": (None, [vp, sz, vp]),
+        "tlo_dequant_q6_k": (None, [vp, sz, vp]),
         "tlo_linear_f16": (None, [vp, vp, vp, i, i, i, i, vp]),
         "tlo_linear_q": (None, [vp, vp, i, vp, i, i, i, i, vp]),
         "tlo_rms_norm": (None, [vp, vp, i, i, f, vp]),
@@ -107,11 +108,13 @@ def f2h(x: np.ndarray) -> np.ndarray:
 
 
 def dequant(blocks: np.ndarray, gtype: int) -> np.ndarray:
+    """GGUF blocks (gtype 2 = Q4_0, 8 = Q8_0, 14 = Q6_K) -> f16 values."""
     blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
-    bb = 18 if gtype == 2 else 34
+    bb, per = {2: (18, 32), 8: (34, 32), 14: (210, 256)}[gtype]
     nb = blocks.size // bb
-    out = np.empty(nb * 32, np.float16)
-    (lib().tlo_dequant_q4_0 if gtype == 2 else lib().tlo_dequant_q8_0)(_p(blocks), nb, _p(out))
+    out = np.empty(nb * per, np.float16)
+    fn = {2: lib().tlo_dequant_q4_0, 8: lib().tlo_dequant_q8_0, 14: lib().tlo_dequant_q6_k}[gtype]
+    fn(_p(blocks), nb, _p(out))
     return out
 
 

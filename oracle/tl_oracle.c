@@ -122,6 +122,44 @@ void tlo_dequant_q8_0(const uint8_t* blocks, size_t nblocks, uint16_t* out) {
     }
 }
 
+/* Q6_K: 256-element super-blocks of 210 bytes, ql[128] qh[64] sc[16] d, as
+ * gguf.rs:128-212 / mmap_gguf.rs:457-545 walk them: for each 128-element
+ * half n and l < 32 the four values
+ *   q1 = ql[l]    low  | qh[l] bits 0-1 << 4   -> y[l]       scale sc[is]
+ *   q2 = ql[l+32] low  | qh[l] bits 2-3 << 4   -> y[l + 32]  scale sc[is + 2]
+ *   q3 = ql[l]    high | qh[l] bits 4-5 << 4   -> y[l + 64]  scale sc[is + 4]
+ *   q4 = ql[l+32] high | qh[l] bits 6-7 << 4   -> y[l + 96]  scale sc[is + 6]
+ * with is = l / 16, each value f16(d * sc * (q - 32)) in f32 (d * sc first),
+ * and ql += 64, qh += 32, sc += 8 per half.                                */
+void tlo_dequant_q6_k(const uint8_t* blocks, size_t nblocks, uint16_t* out) {
+    lut_init();
+    for (size_t b = 0; b < nblocks; b++) {
+        const uint8_t* blk = blocks + b * 210;
+        const uint8_t* ql = blk;
+        const uint8_t* qh = blk + 128;
+        const int8_t* sc = (const int8_t*)(blk + 192);
+        const float d = H2F((uint16_t)(blk[208] | (blk[209] << 8)));
+        uint16_t* y = out + b * 256;
+        for (int n = 0; n < 2; n++) {
+            for (int l = 0; l < 32; l++) {
+                const int is = l / 16;
+                const int q1 = (int)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                const int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                y[l] = tlo_f2h(d * (float)sc[is + 0] * (float)q1);
+                y[l + 32] = tlo_f2h(d * (float)sc[is + 2] * (float)q2);
+                y[l + 64] = tlo_f2h(d * (float)sc[is + 4] * (float)q3);
+                y[l + 96] = tlo_f2h(d * (float)sc[is + 6] * (float)q4);
+            }
+            y += 128;
+            ql += 64;
+            qh += 32;
+            sc += 8;
+        }
+    }
+}
+
 /* ======================================================================== */
 /* linear (matmul_transposed_b)                                             */
 /* ======================================================================== */
@@ -171,8 +209,10 @@ void tlo_linear_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
     free(wf);
 }
 
+/* nblocks counts 32-element units (Q6_K: eight per 210-byte super-block) */
 static void dequant_any(const uint8_t* blocks, int wtype, size_t nblocks, uint16_t* out) {
     if (wtype == 2) tlo_dequant_q4_0(blocks, nblocks, out);
+    else if (wtype == 14) tlo_dequant_q6_k(blocks, nblocks / 8, out);
     else tlo_dequant_q8_0(blocks, nblocks, out);
 }
 
@@ -690,6 +730,7 @@ static uint16_t* load_f16_vec(const tlo_gguf* g, const char* name, int64_t expec
     if (type == 1) memcpy(out, p, sizeof(uint16_t) * (size_t)n);
     else if (type == 0) { const float* f = (const float*)p; for (int64_t i = 0; i < n; i++) out[i] = tlo_f2h(f[i]); }
     else if (type == 2 || type == 8) dequant_any((const uint8_t*)p, type, (size_t)n / 32, out);
+    else if (type == 14 && n % 256 == 0) dequant_any((const uint8_t*)p, type, (size_t)n / 32, out);
     else { free(out); return NULL; }
     return out;
 }

@@ -48,6 +48,10 @@ void     tlo_f2h_array(const float* f, uint16_t* h, size_t n);
  *   src/model/formats/gguf.rs:22-53, mmap_gguf.rs:417-439                   */
 void tlo_dequant_q4_0(const uint8_t* blocks, size_t nblocks, uint16_t* out);
 void tlo_dequant_q8_0(const uint8_t* blocks, size_t nblocks, uint16_t* out);
+/* Q6_K super-block = ql[128] + qh[64] + int8 sc[16] + f16 d (210 bytes,
+ * 256 elements); value = f16(f32(d * sc) * (q6 - 32)), the f32 product exact.
+ *   src/model/formats/gguf.rs:128-212, mmap_gguf.rs:457-545               */
+void tlo_dequant_q6_k(const uint8_t* blocks, size_t nblocks, uint16_t* out);
 
 /* ---- linear / matmul_transposed_b ---------------------------------------
  * y[M,N] = x[M,K] . W[N,K]^T (+ bias[N]) ; f16 in, f16 out.
@@ -59,7 +63,8 @@ void tlo_dequant_q8_0(const uint8_t* blocks, size_t nblocks, uint16_t* out);
 void tlo_linear_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                     int M, int N, int K, int acc_mode, uint16_t* y);
 /* Same product with W given as packed GGUF blocks (dequantised row by row
- * exactly as tlo_dequant_*): wtype 2 = Q4_0, 8 = Q8_0 (GGUF type ids).     */
+ * exactly as tlo_dequant_*): wtype 2 = Q4_0, 8 = Q8_0, 14 = Q6_K (GGUF
+ * type ids).                                                              */
 void tlo_linear_q(const uint16_t* x, const uint8_t* wblocks, int wtype,
                   const uint16_t* bias, int M, int N, int K, int acc_mode,
                   uint16_t* y);

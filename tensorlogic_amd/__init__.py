@@ -5,10 +5,10 @@ this package holds the ctypes binding, a host-side mirror of the reference's
 tensor operator surface, the GGUF writer/reader and the seeded synthetic
 model generator.
 """
-from ._lib import F16, F32, I32, Q4_0, Q8_0, ROPE_INTERLEAVED, ROPE_NEOX, TLHipError  # noqa: F401
+from ._lib import F16, F32, I32, Q4_0, Q6_K, Q8_0, ROPE_INTERLEAVED, ROPE_NEOX, TLHipError  # noqa: F401
 from .tensor import (GGUF, Device, KVCache, Model, Tensor, Timer, attention, bench_copy, bench_linear,  # noqa: F401
                      einsum, embedding, temperature_sample)
 
 __all__ = ["Device", "Tensor", "KVCache", "GGUF", "Model", "TLHipError", "einsum", "attention",
-           "embedding", "temperature_sample", "bench_linear", "bench_copy", "Timer", "F16", "F32", "I32", "Q4_0", "Q8_0",
+           "embedding", "temperature_sample", "bench_linear", "bench_copy", "Timer", "F16", "F32", "I32", "Q4_0", "Q8_0", "Q6_K",
            "ROPE_INTERLEAVED", "ROPE_NEOX"]

@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtlhip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "tl_hip.h")
 
-F16, F32, I32, Q4_0, Q8_0 = 0, 1, 2, 3, 4
+F16, F32, I32, Q4_0, Q8_0, Q6_K = 0, 1, 2, 3, 4, 5
 ROPE_INTERLEAVED, ROPE_NEOX = 0, 1
 STATUS = {0: "OK", 1: "ShapeMismatch", 2: "InvalidDimension", 3: "InvalidOperation",
           4: "AllocationError", 5: "IndexOutOfBounds", 6: "LoadError", 7: "DeviceError",

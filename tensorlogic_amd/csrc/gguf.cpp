@@ -274,6 +274,7 @@ tlhip_status tlhip_gguf_load_tensor(tlhip_ctx ctx, tlhip_gguf g, const char* nam
         case 0: case 1: dt = TLHIP_F16; break;
         case 2: dt = TLHIP_Q4_0; break;
         case 8: dt = TLHIP_Q8_0; break;
+        case 14: dt = TLHIP_Q6_K; break;
         default: return fail(TLHIP_ERR_DTYPE, "tensor %s: GGUF type %u not supported on the device", name, ti->type);
     }
     if (is_quant(dt) && ti->ndim != 2)

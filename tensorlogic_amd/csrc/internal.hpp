@@ -82,9 +82,24 @@ inline int64_t numel(const tlhip_tensor_s* t) {
     return n;
 }
 inline int64_t last_dim(const tlhip_tensor_s* t) { return t->ndim ? t->shape[t->ndim - 1] : 1; }
-inline bool is_quant(tlhip_dtype d) { return d == TLHIP_Q4_0 || d == TLHIP_Q8_0; }
-inline size_t qs_row_bytes(tlhip_dtype d, int64_t K) { return d == TLHIP_Q4_0 ? (size_t)K / 2 : (size_t)K; }
-inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+inline bool is_quant(tlhip_dtype d) { return d == TLHIP_Q4_0 || d == TLHIP_Q8_0 || d == TLHIP_Q6_K; }
+__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+// Device layout of the packed types (rows of N, K along a row):
+//   Q4_0 / Q8_0: data = qs rows (K/2 or K bytes each, GGUF payload bytes in
+//     block order), then `scales` = f16 d [N][K/32];
+//   Q6_K: data = four planes, each 256-aligned: q4 [N][K/2] (per 32-element
+//     group: byte i = low 4 bits of elements i | i+16 << 4), q2 [N][K/4]
+//     (per group: byte b of word w holds the high 2 bits of elements
+//     16w + 4t + b at bits 2t..2t+1), sc [N][K/16] int8 (one per 16
+//     elements, natural order); `scales` = f16 d [N][K/256].
+inline size_t qs_row_bytes(tlhip_dtype d, int64_t K) { return d == TLHIP_Q8_0 ? (size_t)K : (size_t)K / 2; }
+__host__ __device__ inline size_t q6k_q2_offset(int64_t N, int64_t K) { return align256((size_t)N * K / 2); }
+__host__ __device__ inline size_t q6k_sc_offset(int64_t N, int64_t K) { return q6k_q2_offset(N, K) + align256((size_t)N * K / 4); }
+inline size_t quant_data_bytes(tlhip_dtype d, int64_t N, int64_t K) {
+    return d == TLHIP_Q6_K ? q6k_sc_offset(N, K) + align256((size_t)N * K / 16) : align256(qs_row_bytes(d, K) * (size_t)N);
+}
+inline int64_t quant_scale_count(tlhip_dtype d, int64_t N, int64_t K) { return N * (K / (d == TLHIP_Q6_K ? 256 : 32)); }
+inline int64_t quant_group(tlhip_dtype d) { return d == TLHIP_Q6_K ? 256 : 32; }
 size_t payload_bytes(tlhip_dtype d, const int64_t* shape, int ndim);
 std::string shape_str(const tlhip_tensor_s* t);
 
@@ -158,10 +173,11 @@ tlhip_status launch_argmax_slots(hipStream_t s, const unsigned long long* slots,
                                  int32_t* token_log, int32_t* d_state);
 tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi);
 int gemm_splits(int M, int N, int K);   // split-K slices launch_gemm uses when given a workspace
-tlhip_status launch_repack(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks, void* qs,
-                           uint16_t* d, int64_t nblocks, int64_t blocks_per_row, int to_gguf);
-tlhip_status launch_repack_rows(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks, void* qs,
-                                uint16_t* d, int64_t nblocks, int64_t bpr, int64_t dst_row0,
+// Rows 0..src_rows-1 of a GGUF block stream [src_rows, K] go to rows
+// dst_row0 + r * dst_step of a packed tensor of dst_rows rows (to_gguf = 1:
+// the reverse, packed tensor -> block stream).
+tlhip_status launch_repack_rows(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks, void* data,
+                                uint16_t* d, int64_t src_rows, int64_t K, int64_t dst_rows, int64_t dst_row0,
                                 int64_t dst_step, int to_gguf);
 tlhip_status launch_dequant(hipStream_t s, tlhip_dtype wt, const void* qs, const uint16_t* d,
                             uint16_t* out, int64_t N, int64_t K);
@@ -181,7 +197,7 @@ tlhip_status launch_mask(hipStream_t s, const uint16_t* sc, const uint16_t* mask
                          int64_t n, int64_t mask_period);
 tlhip_status launch_embedding(hipStream_t s, tlhip_dtype tt, const void* tq, const uint16_t* td,
                               const int32_t* ids, const int32_t* d_token, uint16_t* out, int n,
-                              int hidden);
+                              int hidden, int rows);
 tlhip_status launch_argmax(hipStream_t s, const uint16_t* x, int n, int32_t* out,
                            int32_t* token_log, int32_t* d_state);
 tlhip_status launch_scores(hipStream_t s, const uint16_t* q, const uint16_t* k, uint16_t* sc,

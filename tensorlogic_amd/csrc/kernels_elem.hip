@@ -344,13 +344,25 @@ tlhip_status launch_mask(hipStream_t s, const uint16_t* sc, const uint16_t* mask
 // ---------------------------------------------------------------------------
 __global__ void embedding_kernel(int tt, const uint8_t* __restrict__ tq, const uint16_t* __restrict__ td,
                                  const int32_t* __restrict__ ids, const int32_t* d_token,
-                                 uint16_t* __restrict__ out, int n, int hidden) {
+                                 uint16_t* __restrict__ out, int n, int hidden, int rows) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)n * hidden) return;
     const int s = (int)(i / hidden), c = (int)(i % hidden);
     const int id = d_token ? d_token[0] : ids[s];
     if (tt == TLHIP_F16) {
         out[i] = ((const uint16_t*)tq)[(size_t)id * hidden + c];
+        return;
+    }
+    if (tt == TLHIP_Q6_K) {
+        // planes of the packed Q6_K layout (see internal.hpp)
+        const int b = c / 32, e = c % 32;
+        const uint8_t* q2 = tq + q6k_q2_offset(rows, hidden);
+        const int8_t* sc = (const int8_t*)(tq + q6k_sc_offset(rows, hidden));
+        const uint8_t byte = tq[(size_t)id * (hidden / 2) + 16 * b + (e & 15)];
+        const int lo = e < 16 ? (byte & 15) : (byte >> 4);
+        const int hb = (q2[(size_t)id * (hidden / 4) + 8 * b + 4 * (e / 16) + (e % 4)] >> (2 * ((e % 16) / 4))) & 3;
+        const float ds = h2f(td[(size_t)id * (hidden / 256) + c / 256]) * (float)sc[(size_t)id * (hidden / 16) + c / 16];
+        out[i] = f2h(ds * (float)((lo | (hb << 4)) - 32));
         return;
     }
     const int nbr = hidden / 32, b = c / 32, e = c % 32;
@@ -367,11 +379,11 @@ __global__ void embedding_kernel(int tt, const uint8_t* __restrict__ tq, const u
 
 tlhip_status launch_embedding(hipStream_t s, tlhip_dtype tt, const void* tq, const uint16_t* td,
                               const int32_t* ids, const int32_t* d_token, uint16_t* out, int n,
-                              int hidden) {
+                              int hidden, int rows) {
     int64_t total = (int64_t)n * hidden;
     if (total <= 0) return TLHIP_OK;
     hipLaunchKernelGGL(embedding_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, (int)tt,
-                       (const uint8_t*)tq, td, ids, d_token, out, n, hidden);
+                       (const uint8_t*)tq, td, ids, d_token, out, n, hidden, rows);
     return TLHIP_OK;
 }
 

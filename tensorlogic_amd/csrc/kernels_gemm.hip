@@ -353,6 +353,8 @@ tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
     p.epi = epi;
     if (epi == EPI_QKV_ROPE || a.pro != PRO_NONE)
         return fail(TLHIP_ERR_INVALID_OPERATION, "gemm: fused normalisation / RoPE epilogue is GEMV-only");
+    if (wt != TLHIP_F16 && wt != TLHIP_Q4_0 && wt != TLHIP_Q8_0)
+        return fail(TLHIP_ERR_DTYPE, "gemm: weight dtype %d takes the dequantised f16 path", (int)wt);
     if (p.M <= 0 || p.N <= 0) return TLHIP_OK;
     if (p.K % 32 != 0) {
         if (wt != TLHIP_F16 || epi == EPI_SWIGLU_PAIR)

@@ -53,23 +53,95 @@ __global__ void repack_kernel(const uint8_t* __restrict__ blocks, uint8_t* __res
     }
 }
 
-tlhip_status launch_repack_rows(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks, void* qs,
-                                uint16_t* d, int64_t nblocks, int64_t bpr, int64_t dst_row0,
-                                int64_t dst_step, int to_gguf) {
-    if (nblocks <= 0) return TLHIP_OK;
-    dim3 grid((unsigned)((nblocks + 255) / 256));
-    if (wt == TLHIP_Q4_0)
-        hipLaunchKernelGGL((repack_kernel<18, 16>), grid, dim3(256), 0, s, blocks, (uint8_t*)qs, d,
-                           nblocks, bpr, dst_row0, dst_step, to_gguf);
-    else
-        hipLaunchKernelGGL((repack_kernel<34, 32>), grid, dim3(256), 0, s, blocks, (uint8_t*)qs, d,
-                           nblocks, bpr, dst_row0, dst_step, to_gguf);
-    return TLHIP_OK;
+// Q6_K: one thread per 32-element group g of a source row (super-block
+// g / 8, half n = (g % 8) / 4, quarter j = g % 4: elements 128n + 32j + l).
+// Element value code q = low 4 bits from nibble j / 2 of ql[64n + 32(j % 2)
+// + l], high 2 bits from bits 2j..2j+1 of qh[32n + l] (gguf.rs:170-190).
+// Download (to_gguf) rebuilds a super-block from its eight groups: the
+// threads of quarters 0/1 write the ql bytes they share with quarters 2/3,
+// quarter-0 threads the qh bytes, group-0 threads d.
+__global__ void repack_q6k_kernel(uint8_t* __restrict__ blocks, uint8_t* __restrict__ q4, uint8_t* __restrict__ q2,
+                                  int8_t* __restrict__ sc, uint16_t* __restrict__ d, int64_t src_rows, int64_t K,
+                                  int64_t dst_row0, int64_t dst_step, int to_gguf) {
+    const int64_t gpr = K / 32;   // groups per row
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= src_rows * gpr) return;
+    const int64_t r = t / gpr, g = t % gpr;
+    const int64_t dr = dst_row0 + r * dst_step;
+    uint8_t* blk = blocks + (r * (K / 256) + g / 8) * 210;
+    const int n = (int)(g % 8) / 4, j = (int)(g % 4);
+    uint8_t* ql = blk + 64 * n + 32 * (j % 2);
+    uint8_t* qh = blk + 128 + 32 * n;
+    int8_t* bsc = (int8_t*)(blk + 192) + 8 * n + 2 * j;
+    uint8_t* o4 = q4 + dr * (K / 2) + g * 16;
+    uint8_t* o2 = q2 + dr * (K / 4) + g * 8;
+    int8_t* osc = sc + dr * (K / 16) + 2 * g;
+    if (!to_gguf) {
+        uint8_t code[32];
+#pragma unroll
+        for (int l = 0; l < 32; l++) code[l] = (uint8_t)(((ql[l] >> (4 * (j / 2))) & 15) | (((qh[l] >> (2 * j)) & 3) << 4));
+#pragma unroll
+        for (int i = 0; i < 16; i++) o4[i] = (uint8_t)((code[i] & 15) | ((code[i + 16] & 15) << 4));
+#pragma unroll
+        for (int w = 0; w < 2; w++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                uint8_t v = 0;
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++) v |= (uint8_t)((code[16 * w + 4 * tt + b] >> 4) << (2 * tt));
+                o2[4 * w + b] = v;
+            }
+        osc[0] = bsc[0];
+        osc[1] = bsc[1];
+        if (g % 8 == 0) d[dr * (K / 256) + g / 8] = (uint16_t)(blk[208] | (blk[209] << 8));
+    } else {
+        // code of element l of group gg (same row) from the planes
+        auto code_of = [&](int64_t gg, int l) -> int {
+            const uint8_t* a4 = q4 + dr * (K / 2) + gg * 16;
+            const uint8_t* a2 = q2 + dr * (K / 4) + gg * 8;
+            const int lo = l < 16 ? (a4[l] & 15) : (a4[l - 16] >> 4);
+            const int w = l / 16, tt = (l % 16) / 4, b = l % 4;
+            return lo | (((a2[4 * w + b] >> (2 * tt)) & 3) << 4);
+        };
+        if (j < 2)
+            for (int l = 0; l < 32; l++) ql[l] = (uint8_t)(code_of(g, l) & 15) | (uint8_t)((code_of(g + 2, l) & 15) << 4);
+        if (j == 0)
+            for (int l = 0; l < 32; l++) {
+                uint8_t v = 0;
+                for (int jj = 0; jj < 4; jj++) v |= (uint8_t)((code_of(g + jj, l) >> 4) << (2 * jj));
+                qh[l] = v;
+            }
+        bsc[0] = osc[0];
+        bsc[1] = osc[1];
+        if (g % 8 == 0) {
+            const uint16_t dv = d[dr * (K / 256) + g / 8];
+            blk[208] = (uint8_t)(dv & 0xff);
+            blk[209] = (uint8_t)(dv >> 8);
+        }
+    }
 }
 
-tlhip_status launch_repack(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks, void* qs,
-                           uint16_t* d, int64_t nblocks, int64_t bpr, int to_gguf) {
-    return launch_repack_rows(s, wt, blocks, qs, d, nblocks, bpr, 0, 1, to_gguf);
+tlhip_status launch_repack_rows(hipStream_t s, tlhip_dtype wt, const uint8_t* blocks, void* data,
+                                uint16_t* d, int64_t src_rows, int64_t K, int64_t dst_rows, int64_t dst_row0,
+                                int64_t dst_step, int to_gguf) {
+    if (src_rows <= 0 || K <= 0) return TLHIP_OK;
+    if (wt == TLHIP_Q6_K) {
+        const int64_t n = src_rows * (K / 32);
+        uint8_t* base = (uint8_t*)data;
+        hipLaunchKernelGGL(repack_q6k_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (uint8_t*)blocks,
+                           base, base + q6k_q2_offset(dst_rows, K), (int8_t*)(base + q6k_sc_offset(dst_rows, K)), d,
+                           src_rows, K, dst_row0, dst_step, to_gguf);
+        return TLHIP_OK;
+    }
+    const int64_t nblocks = src_rows * (K / 32), bpr = K / 32;
+    dim3 grid((unsigned)((nblocks + 255) / 256));
+    if (wt == TLHIP_Q4_0)
+        hipLaunchKernelGGL((repack_kernel<18, 16>), grid, dim3(256), 0, s, blocks, (uint8_t*)data, d,
+                           nblocks, bpr, dst_row0, dst_step, to_gguf);
+    else
+        hipLaunchKernelGGL((repack_kernel<34, 32>), grid, dim3(256), 0, s, blocks, (uint8_t*)data, d,
+                           nblocks, bpr, dst_row0, dst_step, to_gguf);
+    return TLHIP_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -125,11 +197,66 @@ __global__ void dequant_q8_0_kernel(const uint8_t* __restrict__ qs, const uint16
     for (int i = 0; i < 4; i++) o[i] = u4{o32[4 * i], o32[4 * i + 1], o32[4 * i + 2], o32[4 * i + 3]};
 }
 
+// Q6_K group -> 16 f16 pairs in element order.  The six-bit codes u are
+// rebuilt four at a time as bytes (low nibbles from q4, bits 4-5 from q2),
+// placed under the f16 exponent byte 0x64 (1024 + u) and shifted by -1056
+// to u - 32, exactly; d * sc * (u - 32) needs at most 23 significant bits,
+// so one f32 product and one f16 rounding give the reference's value.
+// Pair order: out[2t], out[2t+1] = elements (4t, 4t+2), (4t+1, 4t+3) for
+// t < 4 (low nibbles), the same for elements 16.. in out[8..15].
+__device__ __forceinline__ void q6k_unpack(const u4& q4, uint32_t q2lo, uint32_t q2hi, float ds0, float ds1,
+                                           h2 (&out)[16]) {
+    const h2 bias = {(h16)-1056.0f, (h16)-1056.0f};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const uint32_t lo = (q4[t] & 0x0F0F0F0Fu) | (((q2lo >> (2 * t)) << 4) & 0x30303030u);
+        const uint32_t hi = ((q4[t] >> 4) & 0x0F0F0F0Fu) | (((q2hi >> (2 * t)) << 4) & 0x30303030u);
+        const h2 a0 = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04020400u)) + bias;
+        const h2 a1 = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030401u)) + bias;
+        const h2 b0 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04020400u)) + bias;
+        const h2 b1 = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030401u)) + bias;
+        out[2 * t] = h2{(h16)(ds0 * (float)a0[0]), (h16)(ds0 * (float)a0[1])};
+        out[2 * t + 1] = h2{(h16)(ds0 * (float)a1[0]), (h16)(ds0 * (float)a1[1])};
+        out[8 + 2 * t] = h2{(h16)(ds1 * (float)b0[0]), (h16)(ds1 * (float)b0[1])};
+        out[8 + 2 * t + 1] = h2{(h16)(ds1 * (float)b1[0]), (h16)(ds1 * (float)b1[1])};
+    }
+}
+
+// one thread per 32-element group; 32 outputs as 4 x 16 bytes
+__global__ void dequant_q6k_kernel(const uint8_t* __restrict__ q4, const uint8_t* __restrict__ q2,
+                                   const int8_t* __restrict__ sc, const uint16_t* __restrict__ d,
+                                   uint16_t* __restrict__ out, int64_t ngroups) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= ngroups) return;
+    const u4 q = *(const u4*)(q4 + g * 16);
+    const uint2 h = *(const uint2*)(q2 + g * 8);
+    const float dv = h2f(d[g / 8]);
+    h2 r[16];
+    q6k_unpack(q, h.x, h.y, dv * (float)sc[2 * g], dv * (float)sc[2 * g + 1], r);
+    uint32_t o32[16];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        o32[2 * t] = pack_lo(as_u32(r[2 * t]), as_u32(r[2 * t + 1]));       // (e4t, e4t+1)
+        o32[2 * t + 1] = pack_hi(as_u32(r[2 * t]), as_u32(r[2 * t + 1]));   // (e4t+2, e4t+3)
+        o32[8 + 2 * t] = pack_lo(as_u32(r[8 + 2 * t]), as_u32(r[8 + 2 * t + 1]));
+        o32[8 + 2 * t + 1] = pack_hi(as_u32(r[8 + 2 * t]), as_u32(r[8 + 2 * t + 1]));
+    }
+    u4* o = (u4*)(out + g * 32);
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = u4{o32[4 * i], o32[4 * i + 1], o32[4 * i + 2], o32[4 * i + 3]};
+}
+
 tlhip_status launch_dequant(hipStream_t s, tlhip_dtype wt, const void* qs, const uint16_t* d,
                             uint16_t* out, int64_t N, int64_t K) {
     int64_t nb = N * K / 32;
     if (nb <= 0) return TLHIP_OK;
     dim3 grid((unsigned)((nb + 255) / 256));
+    if (wt == TLHIP_Q6_K) {
+        const uint8_t* base = (const uint8_t*)qs;
+        hipLaunchKernelGGL(dequant_q6k_kernel, grid, dim3(256), 0, s, base, base + q6k_q2_offset(N, K),
+                           (const int8_t*)(base + q6k_sc_offset(N, K)), d, out, nb);
+        return TLHIP_OK;
+    }
     if (wt == TLHIP_Q4_0)
         hipLaunchKernelGGL(dequant_q4_0_kernel, grid, dim3(256), 0, s, (const uint8_t*)qs, d, out, nb);
     else
@@ -167,6 +294,10 @@ struct GemvParams {
     unsigned long long* amax_slots;
 };
 
+// Activation pair order of a weight type: Q6_K unpacks in the Q4_0 order.
+template <int WT>
+constexpr bool xo_nibble() { return WT == TLHIP_Q4_0 || WT == TLHIP_Q6_K; }
+
 // 32 consecutive f16 activations as 16 natural pairs xw[i] = (x2i, x2i+1).
 __device__ __forceinline__ void load_x32(const uint16_t* __restrict__ xb, uint32_t xw[16]) {
     const u4* p = (const u4*)xb;
@@ -184,7 +315,7 @@ __device__ __forceinline__ void load_x32(const uint16_t* __restrict__ xb, uint32
 //   F16  (16 pairs): natural pairs (x2i, x2i+1)
 template <int WT>
 __device__ __forceinline__ void order_x(const uint32_t xw[16], uint32_t xc[16]) {
-    if (WT == TLHIP_Q4_0) {
+    if (xo_nibble<WT>()) {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             xc[4 * t + 0] = pack_lo(xw[2 * t], xw[2 * t + 1]);
@@ -223,13 +354,13 @@ __device__ __forceinline__ void load_xchunk(const uint16_t* __restrict__ xb, uin
 // {8v..8v+7} for Q8_0 / f16.
 template <int WT>
 __device__ __forceinline__ int quad_elem(int v, int e) {
-    return WT == TLHIP_Q4_0 ? (e < 4 ? 4 * v + e : 12 + 4 * v + e) : 8 * v + e;
+    return xo_nibble<WT>() ? (e < 4 ? 4 * v + e : 12 + 4 * v + e) : 8 * v + e;
 }
 
 template <int WT>
 __device__ __forceinline__ void load_quad(const uint16_t* __restrict__ src, int b, int v, float f[8]) {
     uint32_t w[4];
-    if (WT == TLHIP_Q4_0) {
+    if (xo_nibble<WT>()) {
         const uint2 lo = *(const uint2*)(src + (size_t)b * 32 + 4 * v);
         const uint2 hi = *(const uint2*)(src + (size_t)b * 32 + 16 + 4 * v);
         w[0] = lo.x; w[1] = lo.y; w[2] = hi.x; w[3] = hi.y;
@@ -283,7 +414,7 @@ struct NormStage {
     uint32_t xw[IPT][4], ww[IPT][4], bw[IPT][4];   // raw f16 pairs until finish()
 
     __device__ __forceinline__ static void load_words(const uint16_t* __restrict__ src, int b, int v, uint32_t w[4]) {
-        if (WT == TLHIP_Q4_0) {
+        if (xo_nibble<WT>()) {
             const uint2 lo = *(const uint2*)(src + (size_t)b * 32 + 4 * v);
             const uint2 hi = *(const uint2*)(src + (size_t)b * 32 + 16 + 4 * v);
             w[0] = lo.x; w[1] = lo.y; w[2] = hi.x; w[3] = hi.y;
@@ -379,7 +510,12 @@ struct NormStage {
 };
 
 // Weight payload of one 32-element block: Q4_0 1 x 16 B, Q8_0 2 x 16 B, F16 4 x 16 B.
-template <int WT> struct BlkLoads { static constexpr int n = WT == TLHIP_Q4_0 ? 1 : (WT == TLHIP_Q8_0 ? 2 : 4); };
+// 16-byte words a lane holds per 32-element block: Q4_0 the 16 nibble bytes;
+// Q8_0 the 32 int8; f16 the 32 values; Q6_K the 16 q4 bytes, then
+// {q2 word 0, q2 word 1, sc pair | d << 16, 0}.
+template <int WT> struct BlkLoads {
+    static constexpr int n = WT == TLHIP_Q4_0 ? 1 : (WT == TLHIP_Q8_0 || WT == TLHIP_Q6_K ? 2 : 4);
+};
 
 template <int WT>
 __device__ __forceinline__ float block_dot(const u4* q, uint32_t dbits, const uint32_t xc[16], float acc) {
@@ -392,6 +528,18 @@ __device__ __forceinline__ float block_dot(const u4* q, uint32_t dbits, const ui
             q4_unpack(q[0][t], dd, r);
 #pragma unroll
             for (int j = 0; j < 4; j++) acc = fdot2(r[j], as_h2(xc[4 * t + j]), acc);
+        }
+    } else if (WT == TLHIP_Q6_K) {
+        const uint32_t sw = q[1][2];
+        const float dv = h2f((uint16_t)(sw >> 16));
+        h2 r[16];
+        q6k_unpack(q[0], q[1][0], q[1][1], dv * (float)(int8_t)(sw & 0xff), dv * (float)(int8_t)((sw >> 8) & 0xff), r);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            acc = fdot2(r[2 * t], as_h2(xc[4 * t + 0]), acc);
+            acc = fdot2(r[2 * t + 1], as_h2(xc[4 * t + 1]), acc);
+            acc = fdot2(r[8 + 2 * t], as_h2(xc[4 * t + 2]), acc);
+            acc = fdot2(r[8 + 2 * t + 1], as_h2(xc[4 * t + 3]), acc);
         }
     } else if (WT == TLHIP_Q8_0) {
         h16 dh = __builtin_bit_cast(h16, (uint16_t)dbits);
@@ -491,6 +639,25 @@ __device__ __forceinline__ void load_rows(const GemvParams& p, int row0, int lan
                                           uint32_t (&ds)[RI][NB]) {
     constexpr int NL = BlkLoads<WT>::n;
     const int nbr = p.K >> 5;
+    if (WT == TLHIP_Q6_K) {
+        const uint8_t* q2 = p.wq + q6k_q2_offset(p.N, p.K);
+        const uint8_t* sc = p.wq + q6k_sc_offset(p.N, p.K);
+#pragma unroll
+        for (int ri = 0; ri < RI; ri++) {
+            const int row = min(row0 + ri, p.N - 1);
+#pragma unroll
+            for (int i = 0; i < NB; i++) {
+                const int b = min(lane + 64 * i, nbr - 1);
+                q[ri][i][0] = *(const u4*)(p.wq + (size_t)row * (p.K / 2) + (size_t)b * 16);
+                const uint2 h = *(const uint2*)(q2 + (size_t)row * (p.K / 4) + (size_t)b * 8);
+                const uint32_t s2 = *(const uint16_t*)(sc + (size_t)row * (p.K / 16) + (size_t)b * 2);
+                const uint32_t dv = p.wd[(size_t)row * (p.K / 256) + b / 8];
+                q[ri][i][1] = u4{h.x, h.y, s2 | (dv << 16), 0u};
+                ds[ri][i] = 0u;
+            }
+        }
+        return;
+    }
     const size_t row_bytes = WT == TLHIP_Q4_0 ? (size_t)p.K / 2 : (WT == TLHIP_Q8_0 ? (size_t)p.K : (size_t)p.K * 2);
 #pragma unroll
     for (int ri = 0; ri < RI; ri++) {
@@ -839,9 +1006,12 @@ tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
     if (p.K % 32 == 0 && p.K > 0) {
         const int nbr = p.K / 32;
         const int nb = (nbr + 63) / 64;
-        if (normed) {
+        if (wt == TLHIP_Q6_K && p.K % 256 != 0) {
+            done = false;
+        } else if (normed) {
             if (wt == TLHIP_Q4_0) done = launch_norm<TLHIP_Q4_0>(s, p, nb, a.pro);
             else if (wt == TLHIP_Q8_0) done = launch_norm<TLHIP_Q8_0>(s, p, nb, a.pro);
+            else if (wt == TLHIP_Q6_K) done = launch_norm<TLHIP_Q6_K>(s, p, nb, a.pro);
             else done = launch_norm<TLHIP_F16>(s, p, nb, a.pro);
         } else {
             // two rows per wave: the measured optimum for the decoder's shapes
@@ -850,6 +1020,7 @@ tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
             if (pair_epi) ri = 2;
             if (wt == TLHIP_Q4_0) done = launch_mx<TLHIP_Q4_0>(s, p, nb, ri);
             else if (wt == TLHIP_Q8_0) done = launch_mx<TLHIP_Q8_0>(s, p, nb, ri);
+            else if (wt == TLHIP_Q6_K) done = launch_mx<TLHIP_Q6_K>(s, p, nb, ri);
             else done = launch_mx<TLHIP_F16>(s, p, nb, ri);
         }
     }

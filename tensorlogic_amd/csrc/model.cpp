@@ -91,6 +91,7 @@ tlhip_dtype dtype_of(uint32_t gt) {
         case 0: case 1: return TLHIP_F16;
         case 2: return TLHIP_Q4_0;
         case 8: return TLHIP_Q8_0;
+        case 14: return TLHIP_Q6_K;
         default: return (tlhip_dtype)-1;
     }
 }
@@ -130,8 +131,8 @@ tlhip_status place_rows(tlhip_ctx ctx, tlhip_gguf g, const std::string& name, in
     TLHIP_CHECK_HIP(hipMemcpyAsync(stage, data, nbytes, hipMemcpyHostToDevice, ctx->stream));
     tlhip_status st = TLHIP_OK;
     if (is_quant(dst->dtype)) {
-        st = launch_repack_rows(ctx->stream, dst->dtype, (const uint8_t*)stage, dst->data, dst->scales,
-                                n * k / 32, k / 32, dst_row0, step, 0);
+        st = launch_repack_rows(ctx->stream, dst->dtype, (const uint8_t*)stage, dst->data, dst->scales, n, k,
+                                dst->shape[0], dst_row0, step, 0);
     } else {
         const size_t rb = (size_t)k * 2;
         hipError_t e = hipMemcpy2DAsync((uint8_t*)dst->data + (size_t)dst_row0 * rb, rb * step, stage, rb, rb,
@@ -238,6 +239,11 @@ tlhip_status fused_weight(tlhip_ctx ctx, tlhip_gguf g, const std::vector<std::pa
                           int64_t k, bool interleave, tlhip_tensor* out) {
     tlhip_dtype dt;
     TLHIP_TRY(weight_dtype(g, parts[0].first, &dt));
+    // Q6_K (real Q4_0 checkpoints store output.weight so) runs through the
+    // decode GEMV only; the runner computes logits for one row at a time
+    if (dt == TLHIP_Q6_K && !(parts.size() == 1 && parts[0].first == "output.weight"))
+        return fail(TLHIP_ERR_DTYPE, "%s: Q6_K is supported for output.weight and token_embd.weight",
+                    parts[0].first.c_str());
     int64_t n = 0;
     for (auto& p : parts) n += p.second;
     int64_t shp[2] = {n, k};
@@ -315,7 +321,7 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
     const bool embd_fused = decode && m->embd->dtype == TLHIP_F16;
     if (!embd_fused)
         TLHIP_TRY(launch_embedding(s, m->embd->dtype, m->embd->data, m->embd->scales, ids_dev,
-                                   decode ? m->d_state : nullptr, P(m->x), S, H));
+                                   decode ? m->d_state : nullptr, P(m->x), S, H, m->vocab));
     auto embed_into = [&](GemvArgs& a, int li) {
         if (embd_fused && li == 0) {
             a.embd = P(m->embd);

@@ -42,7 +42,7 @@ tlhip_status tlhip_dequantize(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor out) {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(check_t(q, "dequantize"));
     TLHIP_TRY(f16_args("dequantize", {out}));
-    if (!is_quant(q->dtype)) return fail(TLHIP_ERR_DTYPE, "dequantize: input must be Q4_0 or Q8_0");
+    if (!is_quant(q->dtype)) return fail(TLHIP_ERR_DTYPE, "dequantize: input must be Q4_0, Q8_0 or Q6_K");
     if (out->ndim != 2 || out->shape[0] != q->shape[0] || out->shape[1] != q->shape[1])
         return fail(TLHIP_ERR_SHAPE_MISMATCH, "dequantize: %s -> %s", shape_str(q).c_str(), shape_str(out).c_str());
     TLHIP_TRY(launch_dequant(ctx->stream, q->dtype, q->data, q->scales, P(out), q->shape[0], q->shape[1]));
@@ -85,6 +85,22 @@ tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_t
         if (st != TLHIP_OK) (void)hipGetLastError();
     }
     if (st == TLHIP_OK) return after_launch(ctx, "linear");
+    // Q6_K weights reach the MFMA GEMM as their dequantised f16 copy (the
+    // reference's own representation), from the stream-ordered pool
+    tlhip_tensor wf = nullptr;
+    tlhip_dtype wt = w->dtype;
+    if (wt == TLHIP_Q6_K) {
+        int64_t shp[2] = {N, K};
+        TLHIP_TRY(alloc_tensor(ctx, TLHIP_F16, 2, shp, &wf));
+        st = launch_dequant(ctx->stream, TLHIP_Q6_K, w->data, w->scales, P(wf), N, K);
+        if (st != TLHIP_OK) {
+            tlhip_tensor_free(wf);
+            return st;
+        }
+        a.wq = wf->data;
+        a.wd = nullptr;
+        wt = TLHIP_F16;
+    }
     // MFMA GEMM; a split-K workspace from the stream-ordered pool when the
     // output has too few tiles to fill the device
     tlhip_tensor ws = nullptr;
@@ -96,8 +112,9 @@ tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_t
             a.ws_bytes = (size_t)sp * M * N * sizeof(float);
         }
     }
-    st = launch_gemm(ctx->stream, w->dtype, a, epi);
+    st = launch_gemm(ctx->stream, wt, a, epi);
     tlhip_tensor_free(ws);   // stream-ordered: returns to the pool after the GEMM
+    tlhip_tensor_free(wf);
     TLHIP_TRY(st);
     return after_launch(ctx, "linear");
 }
@@ -253,7 +270,7 @@ tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* i
     TLHIP_CHECK_HIP(hipMallocAsync(&d_ids, sizeof(int32_t) * n, ctx->stream));
     TLHIP_CHECK_HIP(hipMemcpyAsync(d_ids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, ctx->stream));
     tlhip_status st = launch_embedding(ctx->stream, table->dtype, table->data, table->scales, d_ids, nullptr, P(out),
-                                       n, (int)Hd);
+                                       n, (int)Hd, (int)V);
     (void)hipFreeAsync(d_ids, ctx->stream);
     // the host ids buffer must stay valid until the copy ran
     TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));

@@ -48,6 +48,7 @@ size_t payload_bytes(tlhip_dtype d, const int64_t* shape, int ndim) {
         case TLHIP_I32: return (size_t)n * 4;
         case TLHIP_Q4_0: return (size_t)n / 32 * 18;
         case TLHIP_Q8_0: return (size_t)n / 32 * 34;
+        case TLHIP_Q6_K: return (size_t)n / 256 * 210;
     }
     return 0;
 }
@@ -120,15 +121,15 @@ tlhip_status alloc_tensor(tlhip_ctx ctx, tlhip_dtype dtype, int ndim, const int6
         return fail(TLHIP_ERR_INVALID_DIMENSION, "rank %d not in 1..8", ndim);
     for (int i = 0; i < ndim; i++)
         if (shape[i] < 0) return fail(TLHIP_ERR_INVALID_DIMENSION, "negative dim %lld", (long long)shape[i]);
-    if ((int)dtype < 0 || (int)dtype > 4) return fail(TLHIP_ERR_INVALID_ARGUMENT, "bad dtype %d", (int)dtype);
+    if ((int)dtype < 0 || (int)dtype > 5) return fail(TLHIP_ERR_INVALID_ARGUMENT, "bad dtype %d", (int)dtype);
     size_t bytes = payload_bytes(dtype, shape, ndim);
     size_t qs_bytes = 0;
     if (is_quant(dtype)) {
-        if (ndim != 2 || shape[1] % 32 != 0)
-            return fail(TLHIP_ERR_INVALID_DIMENSION,
-                        "quantized tensors must be 2-D [N, K] with K %% 32 == 0");
-        qs_bytes = align256(qs_row_bytes(dtype, shape[1]) * (size_t)shape[0]);
-        bytes = qs_bytes + (size_t)shape[0] * (size_t)(shape[1] / 32) * 2;
+        if (ndim != 2 || shape[1] % quant_group(dtype) != 0)
+            return fail(TLHIP_ERR_INVALID_DIMENSION, "quantized tensors must be 2-D [N, K] with K %% %d == 0",
+                        (int)quant_group(dtype));
+        qs_bytes = quant_data_bytes(dtype, shape[0], shape[1]);
+        bytes = qs_bytes + (size_t)quant_scale_count(dtype, shape[0], shape[1]) * 2;
     }
     auto* t = new tlhip_tensor_s();
     t->ctx = ctx;
@@ -295,8 +296,8 @@ tlhip_status tlhip_tensor_upload(tlhip_ctx ctx, tlhip_tensor t, const void* host
     TLHIP_CHECK_HIP(hipMallocAsync(&stage, bytes, ctx->stream));
     TLHIP_CHECK_HIP(hipMemcpyAsync(stage, host, bytes, hipMemcpyHostToDevice, ctx->stream));
     int64_t N = t->shape[0], K = t->shape[1];
-    tlhip_status st = launch_repack(ctx->stream, t->dtype, (const uint8_t*)stage, t->data, t->scales,
-                                    N * K / 32, K / 32, 0);
+    tlhip_status st = launch_repack_rows(ctx->stream, t->dtype, (const uint8_t*)stage, t->data, t->scales,
+                                         N, K, N, 0, 1, 0);
     (void)hipFreeAsync(stage, ctx->stream);
     TLHIP_TRY(st);
     TLHIP_TRY(after_launch(ctx, "upload/repack"));
@@ -320,8 +321,8 @@ tlhip_status tlhip_tensor_download(tlhip_ctx ctx, tlhip_tensor t, void* host, si
     void* stage = nullptr;
     TLHIP_CHECK_HIP(hipMallocAsync(&stage, bytes, ctx->stream));
     int64_t N = t->shape[0], K = t->shape[1];
-    tlhip_status st = launch_repack(ctx->stream, t->dtype, (uint8_t*)stage, t->data, t->scales,
-                                    N * K / 32, K / 32, 1);
+    tlhip_status st = launch_repack_rows(ctx->stream, t->dtype, (uint8_t*)stage, t->data, t->scales,
+                                         N, K, N, 0, 1, 1);
     if (st == TLHIP_OK) {
         hipError_t e = hipMemcpyAsync(host, stage, bytes, hipMemcpyDeviceToHost, ctx->stream);
         if (e != hipSuccess) st = fail(TLHIP_ERR_DEVICE, "hipMemcpyAsync: %s", hipGetErrorString(e));

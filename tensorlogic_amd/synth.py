@@ -27,7 +27,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .gguf import GGML_F16, GGML_Q4_0, GGML_Q8_0, GGUFWriter
+from .gguf import GGML_F16, GGML_Q4_0, GGML_Q6_K, GGML_Q8_0, GGUFWriter
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
 _M1 = np.uint64(0xBF58476D1CE4E5B9)
@@ -120,6 +120,24 @@ def q8_0_blocks(seed: int, name: str, n: int, k: int, dlo: float = 1e-3, dhi: fl
     return blk.reshape(-1)
 
 
+def q6_k_blocks(seed: int, name: str, n: int, k: int, dlo: float = 2e-5, dhi: float = 1e-4,
+                smax: int = 100) -> np.ndarray:
+    """Packed GGUF Q6_K super-blocks (uint8, nblocks*210) for W[n, k]:
+    ql/qh random bytes, int8 scales uniform in [-smax, smax], f16 d."""
+    if k % 256:
+        raise ValueError("K must be a multiple of 256")
+    nb = n * k // 256
+    d = uniform_f16(seed, name, "d", nb, dlo, dhi)
+    qlh = random_bytes(seed, name, "q", nb * 192).reshape(nb, 192)
+    z = splitmix64(stream_key(seed, name, "sc"), nb * 16)
+    sc = ((((z >> np.uint64(32)) * np.uint64(2 * smax + 1)) >> np.uint64(32)).astype(np.int16) - smax).astype(np.int8)
+    blk = np.empty((nb, 210), dtype=np.uint8)
+    blk[:, 0:192] = qlh
+    blk[:, 192:208] = sc.view(np.uint8).reshape(nb, 16)
+    blk[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    return blk.reshape(-1)
+
+
 # ---------------------------------------------------------------------------
 # model files
 # ---------------------------------------------------------------------------
@@ -132,14 +150,18 @@ PHI2_ARGS = dict(n_layers=32, hidden=2560, inter=10240, n_heads=32, vocab=51200,
 def write_llama_gguf(path: str, seed: int, n_layers: int = 22, hidden: int = 2048,
                      inter: int = 5632, n_heads: int = 32, n_kv: int = 4, vocab: int = 32000,
                      eps: float = 1e-5, theta: float = 10000.0, ctx: int = 2048,
-                     qtype: int = GGML_Q4_0, norm_mean: float = 0.0) -> None:
+                     qtype: int = GGML_Q4_0, norm_mean: float = 0.0, out_qtype: int | None = None) -> None:
     """TinyLlama-architecture decoder with random-init weights.
 
-    Linear weights (incl. `output.weight`) are Q4_0 (or Q8_0), embeddings
-    f16 N(0, 0.02) and RMSNorm weights f16 N(norm_mean, 0.02) (the benchmark
-    configuration uses norm_mean 0).  Tensor names follow llama.cpp/GGUF.
+    Linear weights are Q4_0 (or Q8_0), `output.weight` the same unless
+    out_qtype says otherwise (GGML_Q6_K, as llama.cpp's Q4_0 checkpoints
+    store it), embeddings f16 N(0, 0.02) and RMSNorm weights f16
+    N(norm_mean, 0.02) (the benchmark configuration uses norm_mean 0).
+    Tensor names follow llama.cpp/GGUF.
     """
     qgen = q4_0_blocks if qtype == GGML_Q4_0 else q8_0_blocks
+    out_qtype = qtype if out_qtype is None else out_qtype
+    ogen = {GGML_Q4_0: q4_0_blocks, GGML_Q8_0: q8_0_blocks, GGML_Q6_K: q6_k_blocks}[out_qtype]
     hd = hidden // n_heads
     kvd = n_kv * hd
     w = GGUFWriter()
@@ -167,7 +189,7 @@ def write_llama_gguf(path: str, seed: int, n_layers: int = 22, hidden: int = 204
             w.add_tensor(p + nm + ".weight", qtype, (n, k), qgen(seed, p + nm + ".weight", n, k))
     w.add_tensor("output_norm.weight", GGML_F16, (hidden,),
                  normal_f16(seed, "output_norm.weight", (hidden,), norm_mean, 0.02))
-    w.add_tensor("output.weight", qtype, (vocab, hidden), qgen(seed, "output.weight", vocab, hidden))
+    w.add_tensor("output.weight", out_qtype, (vocab, hidden), ogen(seed, "output.weight", vocab, hidden))
     w.write(path)
 
 

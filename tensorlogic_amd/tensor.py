@@ -18,10 +18,10 @@ from typing import Sequence
 import numpy as np
 
 from . import _lib
-from ._lib import F16, Q4_0, Q8_0, ROPE_INTERLEAVED, ROPE_NEOX, TLHipError, call, lib
+from ._lib import F16, Q4_0, Q6_K, Q8_0, ROPE_INTERLEAVED, ROPE_NEOX, TLHipError, call, lib
 
 _vp = C.c_void_p
-_BLOCK_BYTES = {Q4_0: 18, Q8_0: 34}
+_BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q6_K: 210}
 
 
 def _shape_arr(shape):
@@ -66,7 +66,7 @@ class Device:
         return t
 
     def quantized(self, blocks: np.ndarray, shape, qtype: int) -> "Tensor":
-        """A packed Q4_0 / Q8_0 weight [N, K] from GGUF block bytes."""
+        """A packed Q4_0 / Q8_0 / Q6_K weight [N, K] from GGUF block bytes."""
         b = np.ascontiguousarray(blocks, dtype=np.uint8)
         t = self.empty(shape, qtype)
         call("tlhip_tensor_upload", self.h, t.h, b.ctypes.data_as(_vp), b.nbytes)

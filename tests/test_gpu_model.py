@@ -55,6 +55,15 @@ def test_tiny_llama_greedy(dev, oracle, tmp_path, qtype):
     _compare(dev, oracle, path, 0, prompt, 32)
 
 
+def test_tiny_llama_q6_k_lm_head(dev, oracle, tmp_path):
+    # llama.cpp Q4_0 checkpoints carry output.weight as Q6_K: the decode
+    # GEMV with the fused final norm and greedy keys runs on it directly
+    path = str(tmp_path / "tiny_llama_q6k.gguf")
+    S.write_llama_gguf(path, seed=24, out_qtype=S.GGML_Q6_K, **TINY_LLAMA)
+    prompt = S.token_ids(24, "prompt", 46, TINY_LLAMA["vocab"])
+    _compare(dev, oracle, path, 0, prompt, 32)
+
+
 def test_tiny_phi2_greedy(dev, oracle, tmp_path):
     path = str(tmp_path / "tiny_phi2.gguf")
     S.write_phi2_gguf(path, seed=22, **TINY_PHI2)

@@ -8,7 +8,7 @@ does).  Elementwise ops that evaluate exp/tanh are held to 1 f16 ulp.
 import numpy as np
 import pytest
 
-from tensorlogic_amd import F16, Q4_0, Q8_0, ROPE_INTERLEAVED, ROPE_NEOX, TLHipError
+from tensorlogic_amd import F16, Q4_0, Q6_K, Q8_0, ROPE_INTERLEAVED, ROPE_NEOX, TLHipError
 from tensorlogic_amd import synth as S
 from tensorlogic_amd.tensor import KVCache, attention, einsum, embedding, temperature_sample
 
@@ -72,6 +72,31 @@ def test_dequant_bit_exact(dev, oracle, qt, gen, shape):
     assert np.array_equal(got, ref)
 
 
+@pytest.mark.parametrize("shape", [(1, 256), (7, 768), (64, 2048), (1000, 2560)])
+def test_dequant_q6_k_bit_exact(dev, oracle, shape):
+    """Q6_K super-blocks (gguf.rs:128-212) re-laid out on the device: the
+    packed round trip returns the GGUF bytes and the device dequantisation is
+    the oracle's, bit for bit."""
+    blocks = S.q6_k_blocks(3, f"W6k{shape}", *shape)
+    w = dev.quantized(blocks, shape, Q6_K)
+    assert np.array_equal(w.numpy(), blocks), "packed round trip"
+    got = w.dequantize().numpy().view(np.uint16)
+    ref = oracle.dequant(blocks, 14).view(np.uint16).reshape(shape)
+    assert np.array_equal(got, ref)
+
+
+def test_q6_k_extreme_scales(dev, oracle):
+    # largest |sc|, both signs, every code, large and subnormal d
+    rng = np.random.default_rng(5)
+    blocks = S.q6_k_blocks(4, "W6kx", 4, 512, dlo=1e-7, dhi=8.0, smax=128)
+    blocks = blocks.reshape(-1, 210)
+    blocks[:, :192] = rng.integers(0, 256, (blocks.shape[0], 192), dtype=np.uint8)
+    blocks[0, 192:208] = np.array([-128, 127] * 8, np.int8).view(np.uint8)
+    blocks = blocks.reshape(-1)
+    got = dev.quantized(blocks, (4, 512), Q6_K).dequantize().numpy().view(np.uint16)
+    assert np.array_equal(got, oracle.dequant(blocks, 14).view(np.uint16).reshape(4, 512))
+
+
 def test_dequant_reference_known_answers(dev):
     # gguf.rs:622-718: Q8_0 scale 1 -> 0,1,2; two blocks scale 1/2 -> y[42] = 20;
     # Q4_0 scale 0.5, all nibbles 0xF -> 3.5 everywhere.
@@ -102,6 +127,20 @@ def test_linear_quant_gemv(dev, oracle, qt, M, N, K):
     y = dev.tensor(x).linear(w).numpy()
     ref = oracle.linear_q(x, blocks, 2 if qt == Q4_0 else 8, N)
     assert_close(y, ref, what=f"gemv {qt} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 32000, 2048), (3, 1000, 2560), (4, 512, 5632), (2, 77, 256),
+                                   (20, 300, 768)])
+def test_linear_q6_k(dev, oracle, M, N, K):
+    """Q6_K weights: the fused dequant-GEMV for M <= 4, the dequantised f16
+    copy through the MFMA GEMM above; fp32 accumulation of the reference's
+    f16 weights either way."""
+    blocks = S.q6_k_blocks(6, f"W6k{N}x{K}", N, K)
+    x = S.normal_f16(6, f"x6k{M}x{K}", (M, K))
+    w = dev.quantized(blocks, (N, K), Q6_K)
+    y = dev.tensor(x).linear(w).numpy()
+    ref = oracle.linear_q(x, blocks, 14, N)
+    assert_close(y, ref, what=f"q6_k linear {M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("qt", [Q4_0, Q8_0, F16])
@@ -285,6 +324,9 @@ def test_embedding_and_argmax(dev, oracle):
     blocks = S.q4_0_blocks(12, "tq", 320, 64)
     got = embedding(dev.quantized(blocks, (320, 64), Q4_0), ids).numpy()
     assert np.array_equal(got, oracle.dequant(blocks, 2).reshape(320, 64)[ids])
+    blocks = S.q6_k_blocks(12, "tq6", 320, 512)
+    got = embedding(dev.quantized(blocks, (320, 512), Q6_K), ids).numpy()
+    assert np.array_equal(got, oracle.dequant(blocks, 14).reshape(320, 512)[ids])
     # last-max tie-break (builtin_sampling.rs:170-176)
     logits = np.zeros(32000, np.float16)
     logits[[5, 17, 31000]] = 3.0

@@ -137,6 +137,61 @@ def test_dequant_q8_0_all_codes(oracle):
     assert np.array_equal(got.view(np.uint16), np.concatenate(ref).view(np.uint16))
 
 
+def q6k_block(d, sc, codes):
+    """One GGUF Q6_K super-block from 256 six-bit codes, written from the
+    block's element-index form: element e = 128 n + 32 j + l keeps its low
+    4 bits in nibble j // 2 of ql[64 n + 32 (j % 2) + l], its high 2 bits in
+    bits 2 j .. 2 j + 1 of qh[32 n + l], and its scale in sc[e // 16]."""
+    ql = np.zeros(128, np.uint8)
+    qh = np.zeros(64, np.uint8)
+    for e, q in enumerate(codes):
+        n, j, l = e // 128, (e % 128) // 32, e % 32
+        ql[64 * n + 32 * (j % 2) + l] |= (int(q) & 15) << (4 * (j // 2))
+        qh[32 * n + l] |= (int(q) >> 4) << (2 * j)
+    return np.concatenate([ql, qh, np.asarray(sc, np.int8).view(np.uint8),
+                           np.frombuffer(np.float16(d).tobytes(), np.uint8)])
+
+
+def test_dequant_q6_k_layout(oracle):
+    # distinct codes and distinct scales per 16-element group: a swapped
+    # nibble, bit pair, ql half or scale index fails here (no reference test
+    # covers Q6_K; gguf.rs:128-212 is the only statement of it)
+    codes = (np.arange(256) * 7 + 3) % 64
+    y = oracle.dequant(q6k_block(1.0, np.ones(16), codes), 14).astype(np.float32)
+    assert np.array_equal(y, codes.astype(np.float32) - 32.0)
+    sc = np.arange(1, 17) * np.where(np.arange(16) % 2, -1, 1)
+    y = oracle.dequant(q6k_block(0.5, sc, codes), 14).astype(np.float64)
+    assert np.array_equal(y, 0.5 * np.repeat(sc, 16) * (codes - 32.0))
+
+
+def test_dequant_q6_k_arithmetic(oracle):
+    # d * sc * (q - 32) needs at most 11 + 7 + 5 bits, so the reference's f32
+    # products are exact and the value is the correctly rounded f16 of the
+    # exact product -- checked in float64 over every code, both scale signs,
+    # and f16 scales from subnormal to the largest finite
+    rng = np.random.default_rng(3)
+    ds = h(np.concatenate([rng.uniform(2e-5, 1e-4, 40), rng.uniform(-2, 2, 20),
+                           [5.96e-8, 6.1e-5, 65504.0, -65504.0, 0.0]])).astype(np.float64)
+    blocks, ref = [], []
+    for d in ds:
+        sc = rng.integers(-128, 128, 16)
+        codes = np.concatenate([np.arange(64)] * 4)
+        rng.shuffle(codes)
+        blocks.append(q6k_block(d, sc, codes))
+        with np.errstate(over="ignore"):
+            ref.append((d * np.repeat(sc, 16) * (codes - 32.0)).astype(np.float16))
+    got = oracle.dequant(np.concatenate(blocks), 14)
+    assert np.array_equal(got.view(np.uint16), np.concatenate(ref).view(np.uint16))
+
+
+def test_dequant_q6_k_synthetic_rows(oracle):
+    # the seeded generator's blocks decode within the scale bounds it drew
+    from tensorlogic_amd import synth as S
+    blk = S.q6_k_blocks(9, "pin_q6k", 4, 512)
+    y = oracle.dequant(blk, 14).astype(np.float32)
+    assert y.size == 4 * 512 and np.isfinite(y).all() and np.abs(y).max() <= 1e-4 * 100 * 32 * 1.001
+
+
 # ---------------------------------------------------------------------------
 # linear = matmul_transposed_b (matmul.rs:241-311, unified.metal:4291-4348)
 # ---------------------------------------------------------------------------
