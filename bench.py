@@ -92,6 +92,24 @@ def config2_q8(dev, iters: int, copies: int = 24):
     return res
 
 
+def q6k_lm_head(dev, iters: int = 100, copies: int = 6):
+    """Q6_K GEMV at the TinyLlama lm_head shape (32000 x 2048, the type
+    llama.cpp Q4_0 checkpoints store output.weight in): 210 bytes per 256
+    weights, rotating copies past the 256 MB last-level cache."""
+    from tensorlogic_amd import Q6_K, bench_linear
+    from tensorlogic_amd import synth as S
+    N, K = 32000, 2048
+    blocks = S.q6_k_blocks(104, "bench_q6k_lm_head", N, K)
+    ws = [dev.quantized(blocks, (N, K), Q6_K) for _ in range(copies)]
+    x = dev.tensor(S.normal_f16(104, "bench_q6k_x", (1, K)))
+    y = dev.empty((1, N))
+    us = bench_linear(dev, x, ws, y, iters, per_launch=False)
+    byt = N * K // 256 * 210 + 2 * K + 2 * N
+    del ws
+    dev.sync()
+    return dict(us=us, bytes=byt, gbs=byt / us / 1e3)
+
+
 def config3_attention(dev, iters: int = 20):
     """Config 3 attention block: causal prefill over S = 46 and 2048 query
     rows (32 query heads, 4 KV heads, head_dim 64, f16 K/V) and one decode
@@ -239,6 +257,13 @@ def main():
     tok_s = args.steps / (decode_ms / 1000.0)
     log(f"prefill {n_prompt} tokens: {prefill_ms:.2f} ms; decode {args.steps} steps: {decode_ms:.2f} ms "
         f"= {tok_s:.1f} tok/s")
+    # the chat loop's own token choice: temperature_sample(logits, 0.8)
+    # (chat_demo_optimized.tl:204,239), drawn on the device inside the graph
+    m.set_sampling(0.8, seed=1)
+    m.generate(prompt, args.warmup, use_graph=use_graph)
+    _, _, dms_t = m.bench_decode(prompt, args.steps, use_graph=use_graph)
+    tok_s_t = args.steps / (dms_t / 1000.0)
+    log(f"decode with temperature 0.8: {tok_s_t:.1f} tok/s")
     m.close()
 
     gem = gemv_roofline(dev, args.gemv_iters)
@@ -254,6 +279,8 @@ def main():
     c3 = config3_attention(dev)
     for k, v in c3.items():
         log(f"attention {k}: {v['us']:.2f} us, {v['tflops']:.2f} TFLOP/s")
+    q6 = q6k_lm_head(dev)
+    log(f"Q6_K GEMV 32000x2048: {q6['us']:.2f} us, {q6['gbs']:.0f} GB/s")
     g = gem["5632x2048"]
     dev.close()
 
@@ -291,12 +318,14 @@ def main():
             "prefill_ms": round(prefill_ms, 3),
             "decode_launch": args.decode_launch,
             "decode_tokens": toks.tolist()[:8],
+            "decode_tok_s_temperature_0.8": round(tok_s_t, 2),
             "hbm_bytes_per_token": weights_per_token,
             "decode_hbm_roofline_frac": round(tok_s * weights_per_token / (HBM_PEAK_GBS * 1e9), 4),
             "gemv_2048x5632": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in gem.items()},
             "copy_reference": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in cp.items()},
             "config2_q8_0": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c2.items()},
             "config3_attention": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c3.items()},
+            "q6_k_gemv_32000x2048": {k: round(v, 3) for k, v in q6.items()},
         },
         "roofline": {
             "kernel": GEMV_KERNEL,

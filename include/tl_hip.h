@@ -174,6 +174,13 @@ tlhip_status tlhip_attention(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhi
 /* temperature_sample(logits, T<=1e-4) argmax (builtin_sampling.rs:170-176):
  * last maximum wins; logits [V] or [S,V] (last row).  Synchronous.        */
 tlhip_status tlhip_argmax(tlhip_ctx ctx, tlhip_tensor logits, int32_t* out);
+/* temperature_sample(logits, T) (builtin_sampling.rs:66-231): T <= 1e-4 is
+ * tlhip_argmax; otherwise softmax(x / T) and the inverse-CDF index of one
+ * uniform draw, V <= 2^20.  The reference draws from an unseeded
+ * thread_rng; here the draw is splitmix64(seed, counter), so a (seed,
+ * counter) pair always picks the same token.  Synchronous.                 */
+tlhip_status tlhip_temperature_sample(tlhip_ctx ctx, tlhip_tensor logits, float temperature, uint64_t seed,
+                                      uint64_t counter, int32_t* out);
 
 /* ---- KV cache (model::llama::Cache, llama.rs:50-114; KVCache builtins
  *      eval.rs:1247-1400), preallocated instead of concat-grown ----------- */
@@ -211,6 +218,11 @@ tlhip_status tlhip_model_generate(tlhip_model m, const int32_t* prompt, int n_pr
 tlhip_status tlhip_model_logits(tlhip_model m, uint16_t* host, size_t n);
 /* Architecture numbers: [n_layers, hidden, inter, n_heads, n_kv, head_dim, vocab, rot_dims]. */
 tlhip_status tlhip_model_dims(tlhip_model m, int32_t* dims8);
+/* The decode's token choice, temperature_sample(logits, T) as the chat
+ * loop calls it (chat_demo_optimized.tl:204,239; builtin_sampling.rs:
+ * 66-231): T <= 1e-4 greedy (the default), else a draw per step from
+ * splitmix64(seed, step) on the device, inside the replayed graph.        */
+tlhip_status tlhip_model_set_sampling(tlhip_model m, float temperature, uint64_t seed);
 
 /* ---- measurement helpers (hipEvent timing on the context's stream) ------ */
 /* Runs linear(x, w) `iters` times cycling over n_w weight tensors of equal

@@ -71,6 +71,8 @@ def _declare(L):
         "tlo_attention": (None, [vp, vp, vp, i, i, i, i, i, i, f, i, i, vp]),
         "tlo_embedding": (i, [vp, i, i, vp, i, vp]),
         "tlo_argmax_last": (i, [vp, i]),
+        "tlo_sample_temperature": (i, [vp, i, C.c_float, C.c_float]),
+        "tlo_sample_uniform": (C.c_float, [C.c_uint64, C.c_uint64]),
         "tlo_model_load": (vp, [C.c_char_p, i, i, i, i]),
         "tlo_model_free": (None, [vp]),
         "tlo_model_generate": (i, [vp, vp, i, i, vp, vp, vp]),
@@ -250,6 +252,15 @@ def embedding(table, ids) -> np.ndarray:
 def argmax_last(logits) -> int:
     logits = _h(logits).reshape(-1)
     return int(lib().tlo_argmax_last(_p(logits), logits.size))
+
+
+def sample_uniform(seed: int, counter: int) -> float:
+    return float(lib().tlo_sample_uniform(seed, counter))
+
+
+def sample_temperature(logits, temperature: float, r: float) -> int:
+    logits = _h(logits).reshape(-1)
+    return int(lib().tlo_sample_temperature(_p(logits), logits.size, temperature, r))
 
 
 class Model:

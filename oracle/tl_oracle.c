@@ -477,6 +477,38 @@ int tlo_embedding(const uint16_t* table, int vocab, int hidden,
     return 0;
 }
 
+int tlo_sample_temperature(const uint16_t* logits, int n, float temperature, float r) {
+    lut_init();
+    float* p = (float*)malloc(sizeof(float) * (size_t)n);
+    float mx = -INFINITY;
+    for (int i = 0; i < n; i++) {
+        p[i] = H2F(logits[i]) / temperature;
+        mx = fmaxf(mx, p[i]);   /* f32::max: a NaN operand loses */
+    }
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        p[i] = expf(p[i] - mx);
+        sum += p[i];
+    }
+    for (int i = 0; i < n; i++) p[i] /= sum;
+    float cum = 0.0f;
+    int idx = n - 1;
+    for (int i = 0; i < n; i++) {
+        cum += p[i];
+        if (r < cum) { idx = i; break; }
+    }
+    free(p);
+    return idx;
+}
+
+float tlo_sample_uniform(uint64_t seed, uint64_t counter) {
+    uint64_t z = seed + (counter + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (float)(z >> 40) * 0x1p-24f;
+}
+
 int tlo_argmax_last(const uint16_t* logits, int n) {
     lut_init();
     int best = 0;

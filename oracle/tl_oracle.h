@@ -142,6 +142,16 @@ int tlo_embedding(const uint16_t* table, int vocab, int hidden,
 /* temperature_sample(logits, T <= 1e-4) builtin_sampling.rs:170-176:
  * argmax with Iterator::max_by, i.e. the LAST of equal maxima wins.        */
 int tlo_argmax_last(const uint16_t* logits, int n);
+/* temperature_sample(logits, T > 1e-4) builtin_sampling.rs:178-215, for a
+ * given draw r in [0, 1): s = x / T, softmax with exp(s - max) summed in
+ * index order, p = e / sum, then the first index whose running sum of p
+ * (index order, f32) exceeds r, else n - 1.                               */
+int tlo_sample_temperature(const uint16_t* logits, int n, float temperature, float r);
+/* The draw for (seed, counter): the splitmix64 output of seed +
+ * (counter + 1) * 0x9E3779B97F4A7C15, top 24 bits * 2^-24.  (The reference
+ * draws from an unseeded rand::thread_rng; this generator makes runs
+ * repeatable and is what the device sampler uses.)                         */
+float tlo_sample_uniform(uint64_t seed, uint64_t counter);
 
 /* ---- GGUF reader (mmap_gguf.rs:187-379, spec-correct KV skipping) ------ */
 typedef struct tlo_gguf tlo_gguf;

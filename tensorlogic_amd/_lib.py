@@ -74,6 +74,7 @@ SIGNATURES = {
     "tlhip_einsum_context": (_i, [_vp, _vp, _vp, _vp]),
     "tlhip_attention": (_i, [_vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
     "tlhip_argmax": (_i, [_vp, _vp, _i32p]),
+    "tlhip_temperature_sample": (_i, [_vp, _vp, _f, C.c_uint64, C.c_uint64, _i32p]),
     "tlhip_kvcache_create": (_i, [_vp, _i, _i, _i, _i, C.POINTER(_vp)]),
     "tlhip_kvcache_free": (_i, [_vp]),
     "tlhip_kvcache_set": (_i, [_vp, _vp, _i, _vp, _vp]),
@@ -88,6 +89,7 @@ SIGNATURES = {
     "tlhip_model_generate": (_i, [_vp, _i32p, _i, _i, _i, _i32p]),
     "tlhip_model_logits": (_i, [_vp, C.POINTER(C.c_uint16), _sz]),
     "tlhip_model_dims": (_i, [_vp, _i32p]),
+    "tlhip_model_set_sampling": (_i, [_vp, _f, C.c_uint64]),
     "tlhip_bench_linear": (_i, [_vp, _vp, C.POINTER(_vp), _i, _vp, _i, _i, C.POINTER(_f)]),
     "tlhip_bench_copy": (_i, [_vp, _sz, _i, _i, C.POINTER(_f)]),
     "tlhip_bench_decode": (_i, [_vp, _i32p, _i, _i, _i, _i32p, C.POINTER(_f), C.POINTER(_f)]),

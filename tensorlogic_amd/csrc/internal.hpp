@@ -200,6 +200,12 @@ tlhip_status launch_embedding(hipStream_t s, tlhip_dtype tt, const void* tq, con
                               int hidden, int rows);
 tlhip_status launch_argmax(hipStream_t s, const uint16_t* x, int n, int32_t* out,
                            int32_t* token_log, int32_t* d_state);
+// temperature_sample with T > 1e-4 (draw from seed and counter
+// [+ d_state[2]]); scratch of sample_scratch_bytes(n); d_state / token_log
+// as launch_argmax.
+size_t sample_scratch_bytes(int n);
+tlhip_status launch_sample(hipStream_t s, const uint16_t* x, int n, float temperature, uint64_t seed,
+                           uint64_t counter, void* scratch, int32_t* out, int32_t* token_log, int32_t* d_state);
 tlhip_status launch_scores(hipStream_t s, const uint16_t* q, const uint16_t* k, uint16_t* sc,
                            int I, int J, int H, int Hkv, int D);
 tlhip_status launch_context(hipStream_t s, const uint16_t* p, const uint16_t* v, uint16_t* out,

@@ -461,6 +461,173 @@ tlhip_status launch_argmax(hipStream_t s, const uint16_t* x, int n, int32_t* out
     return TLHIP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// temperature_sample with T > 1e-4 (builtin_sampling.rs:178-215): s = x / T,
+// e = exp(s - max), p = e / sum(e), then the first index whose running sum
+// of p exceeds the draw r, else n - 1.  Two kernels:
+//   sample_stats: workgroup w owns the 1024-logit slice w and records its
+//     (max, sum of exp(s - slice max));
+//   sample_pick: one workgroup combines the slice statistics into the row
+//     max and sum, locates the slice whose probability mass holds r (slice
+//     masses in slice order), then forms p for that slice with the row max
+//     and sum and finds the first crossing with a workgroup scan in index
+//     order.
+// The draw is splitmix64(seed + (counter + 1) * golden)'s top 24 bits *
+// 2^-24, with counter += d_state[2] (the decode step) when the decode state
+// is given, so a replayed graph draws a fresh value per step.  Running sums
+// are f32 as in the reference, summed in slice order.
+// ---------------------------------------------------------------------------
+constexpr int SMP_SLICE = 1024;   // logits per slice
+constexpr int SMP_MAXW = 1024;    // slices: rows up to 1M logits
+
+__device__ __forceinline__ float sample_uniform(uint64_t seed, uint64_t counter) {
+    uint64_t z = seed + (counter + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (float)(z >> 40) * 0x1p-24f;
+}
+
+// max / sum over a workgroup of NW waves (partials in w_part[NW])
+template <int NW>
+__device__ __forceinline__ float wg_max(float v, float* w_part) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) w_part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = w_part[0];
+    for (int k = 1; k < NW; k++) m = fmaxf(m, w_part[k]);
+    __syncthreads();
+    return m;
+}
+
+template <int NW>
+__device__ __forceinline__ float wg_sum(float v, float* w_part) {
+    v = wave_sum<64>(v);
+    if ((threadIdx.x & 63) == 0) w_part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = w_part[0];
+    for (int k = 1; k < NW; k++) t += w_part[k];
+    __syncthreads();
+    return t;
+}
+
+// exclusive scan over a 1024-thread workgroup in thread order (wave scans,
+// then the wave totals in order); `total` = the sum of all
+__device__ __forceinline__ float wg_excl_scan(float v, float* wtot, float& total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    float inc = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float u = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += u;
+    }
+    if (lane == 63) wtot[w] = inc;
+    __syncthreads();
+    float before = 0.0f, t = 0.0f;
+    for (int k = 0; k < 16; k++) {
+        if (k < w) before += wtot[k];
+        t += wtot[k];
+    }
+    total = t;
+    __syncthreads();
+    return before + (inc - v);
+}
+
+__global__ __launch_bounds__(256) void sample_stats_kernel(const uint16_t* __restrict__ x, int n, float temperature,
+                                                           float2* __restrict__ stats) {
+    __shared__ float part[4];
+    const int i0 = blockIdx.x * SMP_SLICE;
+    float s[SMP_SLICE / 256];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < SMP_SLICE / 256; k++) {
+        const int i = i0 + threadIdx.x + 256 * k;
+        s[k] = i < n ? h2f(x[i]) / temperature : -INFINITY;
+        mx = fmaxf(mx, s[k]);   // as f32::max: a NaN operand loses
+    }
+    mx = wg_max<4>(mx, part);
+    float es = 0.0f;
+#pragma unroll
+    for (int k = 0; k < SMP_SLICE / 256; k++)
+        if (i0 + (int)threadIdx.x + 256 * k < n) es += expf(s[k] - mx);
+    es = wg_sum<4>(es, part);
+    if (threadIdx.x == 0) stats[blockIdx.x] = make_float2(mx, es);
+}
+
+__global__ __launch_bounds__(1024) void sample_pick_kernel(const uint16_t* __restrict__ x, int n, float temperature,
+                                                           uint64_t seed, uint64_t counter,
+                                                           const float2* __restrict__ stats, int32_t* out,
+                                                           int32_t* token_log, int32_t* d_state) {
+    __shared__ float wpart[16];
+    __shared__ int wmin[16];
+    __shared__ float sh_off;
+    __shared__ int sh_slice;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int nw = (n + SMP_SLICE - 1) / SMP_SLICE;
+    const float2 st = tid < nw ? stats[tid] : make_float2(-INFINITY, 0.0f);
+    const float m = wg_max<16>(st.x, wpart);
+    const float rs = (tid < nw && st.x > -INFINITY) ? st.y * expf(st.x - m) : 0.0f;
+    float sum;
+    const float r = sample_uniform(seed, counter + (d_state ? (uint64_t)d_state[2] : 0ull));
+    // slice masses rs / sum in slice order: the slice whose running mass
+    // first exceeds r
+    const float mass = rs;   // scaled by 1/sum below, after the total is known
+    float before = wg_excl_scan(mass, wpart, sum);
+    int cand = 0x7fffffff;
+    if (tid < nw && r < (before + mass) / sum) cand = tid;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) cand = min(cand, __shfl_xor(cand, off, 64));
+    if (lane == 0) wmin[w] = cand;
+    __syncthreads();
+    if (tid == 0) {
+        int c = wmin[0];
+        for (int k = 1; k < 16; k++) c = min(c, wmin[k]);
+        sh_slice = c == 0x7fffffff ? nw - 1 : c;
+    }
+    __syncthreads();
+    const int sl = sh_slice;
+    if (tid == sl) sh_off = before / sum;
+    __syncthreads();
+    // p for the slice with the row max and sum, running sum in index order
+    const int i = sl * SMP_SLICE + tid;
+    const float p = i < n ? expf(h2f(x[i]) / temperature - m) / sum : 0.0f;
+    float tot;
+    const float cum = sh_off + wg_excl_scan(p, wpart, tot) + p;
+    int found = (i < n && r < cum) ? i : 0x7fffffff;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) found = min(found, __shfl_xor(found, off, 64));
+    if (lane == 0) wmin[w] = found;
+    __syncthreads();
+    if (tid == 0) {
+        int f = wmin[0];
+        for (int k = 1; k < 16; k++) f = min(f, wmin[k]);
+        // past the slice's last logit by rounding: its last index (n - 1 at
+        // the row's end, as the reference's default)
+        const int tok = f == 0x7fffffff ? min(n, (sl + 1) * SMP_SLICE) - 1 : f;
+        if (out) out[0] = tok;
+        if (d_state) {
+            if (token_log) token_log[d_state[2]] = tok;
+            d_state[0] = tok;
+            d_state[1] += 1;
+            d_state[2] += 1;
+        }
+    }
+}
+
+size_t sample_scratch_bytes(int n) { return sizeof(float2) * (size_t)((n + SMP_SLICE - 1) / SMP_SLICE); }
+
+tlhip_status launch_sample(hipStream_t s, const uint16_t* x, int n, float temperature, uint64_t seed,
+                           uint64_t counter, void* scratch, int32_t* out, int32_t* token_log, int32_t* d_state) {
+    if (n <= 0) return fail(TLHIP_ERR_INVALID_DIMENSION, "temperature_sample of an empty tensor");
+    if (n > SMP_SLICE * SMP_MAXW) return fail(TLHIP_ERR_INVALID_DIMENSION, "temperature_sample: %d logits", n);
+    if (!(temperature > 0.0f)) return fail(TLHIP_ERR_INVALID_ARGUMENT, "temperature_sample: temperature %g", temperature);
+    const int nw = (n + SMP_SLICE - 1) / SMP_SLICE;
+    hipLaunchKernelGGL(sample_stats_kernel, dim3(nw), dim3(256), 0, s, x, n, temperature, (float2*)scratch);
+    hipLaunchKernelGGL(sample_pick_kernel, dim3(1), dim3(1024), 0, s, x, n, temperature, seed, counter,
+                       (const float2*)scratch, out, token_log, d_state);
+    return TLHIP_OK;
+}
+
 // Copies rows (e.g. KV-cache set/append): dst row (dst_row0 + *d_pos + r).
 __global__ void copy_rows_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
                                  int rows, int row_elems, int ss, int ds, const int32_t* d_pos,

@@ -64,6 +64,7 @@ struct tlhip_model_s {
                  logits = nullptr;
     unsigned long long* d_amax = nullptr;   // per-workgroup greedy keys of the lm_head GEMV
     uint16_t* d_vt = nullptr;                // V transposed per KV head for matrix-core prefill attention
+    void* d_sample = nullptr;                // per-slice statistics of the temperature sampler
     float* ws = nullptr;          // split-K partials of the prefill GEMMs
     size_t ws_bytes = 0;
     int32_t* d_state = nullptr;   // {token, pos, step}
@@ -72,6 +73,8 @@ struct tlhip_model_s {
     int32_t* h_state = nullptr;   // pinned
     const float* rope_tab = nullptr;
     int pos = 0;
+    float temperature = 0.0f;               // decode token choice: <= 1e-4 greedy, else sampled
+    uint64_t seed = 0;
     hipGraphExec_t gexec = nullptr;
     hipGraph_t graph = nullptr;
 };
@@ -410,7 +413,11 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
         a.amax_slots = m->d_amax;
         TLHIP_TRY(launch_gemv(s, m->out.w->dtype, a, EPI_ARGMAX));
     }
-    TLHIP_TRY(launch_argmax_slots(s, m->d_amax, gemv_norm_slots(m->vocab), nullptr, m->d_tokens, m->d_state));
+    if (m->temperature > 1e-4f)
+        TLHIP_TRY(launch_sample(s, P(m->logits), m->vocab, m->temperature, m->seed, 0, m->d_sample, nullptr, m->d_tokens,
+                                m->d_state));
+    else
+        TLHIP_TRY(launch_argmax_slots(s, m->d_amax, gemv_norm_slots(m->vocab), nullptr, m->d_tokens, m->d_state));
     return TLHIP_OK;
 }
 
@@ -609,6 +616,7 @@ tlhip_status tlhip_model_free(tlhip_model m) {
     for (tlhip_tensor t : {m->x, m->xn, m->qkv, m->qrot, m->att, m->hmid, m->logits}) tlhip_tensor_free(t);
     if (m->d_amax) (void)hipFree(m->d_amax);
     if (m->d_vt) (void)hipFree(m->d_vt);
+    if (m->d_sample) (void)hipFree(m->d_sample);
     if (m->ws) (void)hipFree(m->ws);
     if (m->d_state) (void)hipFree(m->d_state);
     if (m->d_tokens) (void)hipFree(m->d_tokens);
@@ -714,6 +722,7 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
         hipError_t e = hipMalloc(&m->d_state, 4 * sizeof(int32_t));
         if (e == hipSuccess) e = hipMalloc(&m->d_amax, sizeof(unsigned long long) * gemv_norm_slots(m->vocab));
         if (e == hipSuccess) e = hipMalloc(&m->d_vt, attention_mfma_scratch(m->max_ctx, m->n_kv, m->head_dim));
+        if (e == hipSuccess) e = hipMalloc(&m->d_sample, sample_scratch_bytes(m->vocab));
         // split-K workspace: the largest partial set any prefill GEMM of this model uses
         if (e == hipSuccess) {
             const int64_t shapes[4][2] = {{H + 2 * kvd, H}, {H, H}, {arch == 0 ? 2 * I : I, H}, {H, I}};
@@ -755,6 +764,22 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
 tlhip_status tlhip_model_reset(tlhip_model m) {
     if (!m) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null model");
     m->pos = 0;
+    return TLHIP_OK;
+}
+
+tlhip_status tlhip_model_set_sampling(tlhip_model m, float temperature, uint64_t seed) {
+    if (!m) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null model");
+    if (!(temperature >= 0.0f) || !std::isfinite(temperature))
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "temperature %g", temperature);
+    if (temperature == m->temperature && seed == m->seed) return TLHIP_OK;
+    // the decode graph holds the token-choice kernel: capture it again
+    TLHIP_CHECK_HIP(hipStreamSynchronize(m->ctx->stream));
+    if (m->gexec) (void)hipGraphExecDestroy(m->gexec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    m->gexec = nullptr;
+    m->graph = nullptr;
+    m->temperature = temperature;
+    m->seed = seed;
     return TLHIP_OK;
 }
 

@@ -386,4 +386,28 @@ tlhip_status tlhip_argmax(tlhip_ctx ctx, tlhip_tensor logits, int32_t* out) {
     return TLHIP_OK;
 }
 
+tlhip_status tlhip_temperature_sample(tlhip_ctx ctx, tlhip_tensor logits, float temperature, uint64_t seed,
+                                      uint64_t counter, int32_t* out) {
+    if (!(temperature > 1e-4f)) return tlhip_argmax(ctx, logits, out);
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("temperature_sample", {logits}));
+    if (!out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null output");
+    if (logits->ndim != 1 && logits->ndim != 2)
+        return fail(TLHIP_ERR_INVALID_DIMENSION, "temperature_sample() expects 1D or 2D logits tensor");
+    const int64_t V = last_dim(logits);
+    const int64_t rows = numel(logits) / (V ? V : 1);
+    if (V == 0 || rows == 0) return fail(TLHIP_ERR_INVALID_DIMENSION, "temperature_sample of an empty tensor");
+    const uint16_t* last = P(logits) + (size_t)(rows - 1) * V;
+    void* scratch = nullptr;
+    TLHIP_CHECK_HIP(hipMallocAsync(&scratch, sample_scratch_bytes((int)V), ctx->stream));
+    const tlhip_status st = launch_sample(ctx->stream, last, (int)V, temperature, seed, counter, scratch,
+                                          ctx->d_scratch_i32, nullptr, nullptr);
+    (void)hipFreeAsync(scratch, ctx->stream);
+    TLHIP_TRY(st);
+    TLHIP_CHECK_HIP(hipMemcpyAsync(ctx->h_pinned_i32, ctx->d_scratch_i32, 4, hipMemcpyDeviceToHost, ctx->stream));
+    TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
+    *out = ctx->h_pinned_i32[0];
+    return TLHIP_OK;
+}
+
 }  // extern "C"

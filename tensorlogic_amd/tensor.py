@@ -265,11 +265,16 @@ def embedding(table: Tensor, ids) -> Tensor:
     return out
 
 
-def temperature_sample(logits: Tensor, temperature: float) -> int:
-    """Greedy branch of temperature_sample (builtin_sampling.rs:170-176)."""
-    if temperature > 1e-4:
-        raise TLHipError(3, "only greedy sampling (temperature <= 1e-4) runs on the device")
-    return logits.argmax_last()
+def temperature_sample(logits: Tensor, temperature: float, seed: int = 0, counter: int = 0) -> int:
+    """temperature_sample(logits, T) (builtin_sampling.rs:66-231): greedy for
+    T <= 1e-4, else the inverse-CDF draw of softmax(x / T) for the uniform
+    value splitmix64(seed, counter) (the reference's thread_rng is unseeded)."""
+    if temperature <= 1e-4:
+        return logits.argmax_last()
+    out = C.c_int32()
+    call("tlhip_temperature_sample", logits.dev.h, logits.h, float(temperature), int(seed), int(counter),
+         C.byref(out))
+    return out.value
 
 
 class KVCache:
@@ -370,6 +375,11 @@ class Model:
         r = C.c_int32()
         call("tlhip_model_decode", self.h, int(token), C.byref(r))
         return r.value
+
+    def set_sampling(self, temperature: float, seed: int = 0):
+        """Token choice of prefill/decode: greedy for T <= 1e-4 (default),
+        else temperature_sample with the draw splitmix64(seed, step)."""
+        call("tlhip_model_set_sampling", self.h, float(temperature), int(seed))
 
     def generate(self, prompt, n_decode: int, use_graph: bool = True) -> np.ndarray:
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)

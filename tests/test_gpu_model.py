@@ -64,6 +64,37 @@ def test_tiny_llama_q6_k_lm_head(dev, oracle, tmp_path):
     _compare(dev, oracle, path, 0, prompt, 32)
 
 
+def test_tiny_llama_sampled_decode(dev, oracle, tmp_path):
+    """temperature_sample(logits, 0.8) as the chat loop's token choice
+    (chat_demo_optimized.tl:204,239): the replayed graph and direct launches
+    draw the same stream for a seed, another seed draws another, and the
+    prefill's token is the oracle sampler's pick for draw (seed, step 0)."""
+    path = str(tmp_path / "tiny_llama_sample.gguf")
+    S.write_llama_gguf(path, seed=25, **TINY_LLAMA)
+    prompt = S.token_ids(25, "prompt", 46, TINY_LLAMA["vocab"])
+    m = Model(dev, path, arch=0, max_ctx=128)
+    m.set_sampling(0.8, seed=77)
+    a = m.generate(prompt, 40, use_graph=True)
+    b = m.generate(prompt, 40, use_graph=False)
+    assert np.array_equal(a, b)
+    m.set_sampling(0.8, seed=78)
+    c = m.generate(prompt, 40, use_graph=True)
+    assert not np.array_equal(a, c)
+    m.set_sampling(0.0)
+    g = m.generate(prompt, 8, use_graph=True)
+    m.close()
+    om = oracle.Model(path, arch=0, max_ctx=128)
+    toks, _, _ = om.generate(prompt, 8)
+    om.close()
+    assert np.array_equal(g, toks), "greedy after sampling"
+    om = oracle.Model(path, arch=0, max_ctx=128)
+    _, lg = om.forward(np.asarray(prompt, np.int32), 0)
+    om.close()
+    r = oracle.sample_uniform(77, 0)
+    from test_gpu_ops import _sample_ok
+    assert a[0] == oracle.sample_temperature(lg, 0.8, r) or _sample_ok(lg.astype(np.float16), 0.8, r, int(a[0]))
+
+
 def test_tiny_phi2_greedy(dev, oracle, tmp_path):
     path = str(tmp_path / "tiny_phi2.gguf")
     S.write_phi2_gguf(path, seed=22, **TINY_PHI2)

@@ -432,3 +432,41 @@ def test_embedding_and_argmax(oracle):
     assert oracle.argmax_last(lg) == 31
     lg = S.normal_f16(41, "lg", (32000,))
     assert oracle.argmax_last(lg) == int(np.argmax(lg.astype(np.float32)))
+
+
+# ---------------------------------------------------------------------------
+# temperature_sample with T > 1e-4 (builtin_sampling.rs:178-215)
+# ---------------------------------------------------------------------------
+def test_sampler_known_answer_boundaries(oracle):
+    # softmax([1, 2, 3]) = [0.0900, 0.2447, 0.6652] (activations.rs:100-102
+    # quotes 0.0900, 0.2446, 0.6650): the inverse CDF switches at 0.0900 and
+    # 0.3348
+    lg = np.array([1, 2, 3], np.float16)
+    assert [oracle.sample_temperature(lg, 1.0, r) for r in (0.0, 0.0899, 0.0901, 0.3345, 0.3349, 0.99)] == \
+        [0, 0, 1, 1, 2, 2]
+    # T scales the logits before the softmax: T = 2 -> softmax([0.5, 1, 1.5])
+    assert oracle.sample_temperature(lg, 2.0, 0.18) == 0 and oracle.sample_temperature(lg, 2.0, 0.19) == 1
+
+
+def test_sampler_distribution(oracle):
+    # the inverse CDF over a grid of draws reproduces softmax(x / T) computed
+    # in float64 (a dropped scale, a wrong max shift or an off-by-one index
+    # shows as a frequency error far above the grid's 1/4096)
+    rng = np.random.default_rng(7)
+    lg = h(rng.normal(0, 2, 50))
+    for T in (0.5, 0.8, 1.7):
+        x = lg.astype(np.float64) / np.float64(np.float32(T))
+        p = np.exp(x - x.max())
+        p /= p.sum()
+        grid = (np.arange(4096) + 0.5) / 4096
+        toks = np.array([oracle.sample_temperature(lg, T, float(r)) for r in grid])
+        freq = np.bincount(toks, minlength=50) / 4096
+        assert np.abs(freq - p).max() < 2.0 / 4096 + 1e-6
+
+
+def test_sampler_uniform_is_splitmix64(oracle):
+    # splitmix64 seeded with 0 first returns 0xE220A8397B1DCDAF (Steele, Lea,
+    # Flood 2014); the draw is its top 24 bits
+    assert oracle.sample_uniform(0, 0) == 0xE220A8 / 2 ** 24
+    r = np.array([oracle.sample_uniform(11, c) for c in range(20000)])
+    assert r.min() >= 0.0 and r.max() < 1.0 and abs(r.mean() - 0.5) < 0.01
