@@ -95,6 +95,30 @@ def test_tiny_llama_sampled_decode(dev, oracle, tmp_path):
     assert a[0] == oracle.sample_temperature(lg, 0.8, r) or _sample_ok(lg.astype(np.float16), 0.8, r, int(a[0]))
 
 
+def test_tiny_llama_chat_turn(dev, tmp_path):
+    """The chat loop of chat_demo_optimized.tl:176-262 end to end on the
+    device: template -> tokens -> sampled decode (T = 0.8) -> text; the same
+    seed gives the same turn, and the ids are the graph's own stream cut at
+    the first EOS."""
+    from tensorlogic_amd import Tokenizer, chat, tinyllama_chat_prompt
+    from tensorlogic_amd.tokenizer import until_eos
+    from test_tokenizer import make_tokenizer_file
+    tok = Tokenizer.from_file(make_tokenizer_file(tmp_path / "tokenizer.json"))
+    path = str(tmp_path / "tiny_llama_chat.gguf")
+    S.write_llama_gguf(path, seed=26, **TINY_LLAMA)
+    m = Model(dev, path, arch=0, max_ctx=256)
+    text, ids = chat(m, tok, "You are a friendly and helpful AI assistant.",
+                     "Hello! Tell me a short fun fact about computers.", max_new_tokens=10, seed=4)
+    text2, ids2 = chat(m, tok, "You are a friendly and helpful AI assistant.",
+                       "Hello! Tell me a short fun fact about computers.", max_new_tokens=10, seed=4)
+    assert (text, ids) == (text2, ids2) and len(ids) <= 10 and all(0 <= i < TINY_LLAMA["vocab"] for i in ids)
+    prompt = tok.encode(tinyllama_chat_prompt("You are a friendly and helpful AI assistant.",
+                                              "Hello! Tell me a short fun fact about computers."), False)
+    m.set_sampling(0.8, 4)
+    assert ids == until_eos(m.generate(np.asarray(prompt, np.int32), 9)[:10], 2)
+    m.close()
+
+
 def test_tiny_phi2_greedy(dev, oracle, tmp_path):
     path = str(tmp_path / "tiny_phi2.gguf")
     S.write_phi2_gguf(path, seed=22, **TINY_PHI2)
