@@ -8,8 +8,9 @@
 // matmul does (unified.metal:4291-4348).  Output f16 with the same epilogues
 // as the GEMV (bias, residual add, SwiGLU on interleaved gate/up rows).
 //
-// Tile: 64 (M) x 64 (N) x 32 (K, one quant block) per 256-thread workgroup;
-// four waves in a 2 x 2 arrangement, each owning a 32 x 32 accumulator.
+// Three kernels: gemm_kernel (K % 64 != 0; 64 x 64 x 32 tiles), gemm2_kernel
+// (M <= 64: register-staged, two LDS buffers) and gemm_lds_kernel (M > 64:
+// 128 x 128 tiles, four LDS stages filled by direct global->LDS loads).
 #include "device_common.hpp"
 #include "internal.hpp"
 
@@ -285,6 +286,282 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmParams p, float* __restr
         }
 }
 
+// ---------------------------------------------------------------------------
+// Multi-stage MFMA dequant-GEMM (K % 64 == 0).  Workgroup tile BM x BN x 64,
+// 512 threads = 8 waves in a 2 (M) x 4 (N) grid, each wave (BM/2) x (BN/4) of
+// C in 32 x 32 v_mfma_f32_32x32x16_f16 tiles.  NS LDS stages are filled by
+// direct global->LDS loads (global_load_lds_dwordx4 / _dword, no VGPR
+// staging), so NS - 1 K steps are in flight while one is computed.  The LDS
+// keeps the GGUF payload as stored (Q4_0 nibbles, Q8_0 int8 or f16) plus the
+// block scales; each wave dequantises its B operand from LDS into registers
+// right before its MFMAs, with the same RNE_f16((q-8)*d) / RNE_f16(q*d) as
+// every other path.
+//
+// K order inside a 64-wide step: MFMA lane half h (lane / 32) carries the
+// elements 32h + 8t .. 32h + 8t + 7 at sub-step t = 0..3 (quant block h of
+// the step) for A and B alike, so every k is summed once in fp32.
+//
+// LDS rows are XOR-swizzled in 16-byte chunks so that the 32 rows a wave
+// reads at one chunk index fall in distinct banks: A / f16 B rows (128 B)
+// chunk c -> c ^ ((r >> 1) & 7); Q8_0 rows (64 B) c -> c ^ ((r >> 2) & 3); Q4_0 rows
+// (32 B) c -> c ^ ((r >> 3) & 1).  A direct load writes lane l's 16 (4) bytes
+// at LDS base + 16 l (4 l); each lane fetches the global chunk that the
+// swizzle puts in its slot.
+//
+// Workgroups are dispatched round-robin over the 8 XCDs (workgroup id mod
+// 8); the id -> tile map gives each XCD a contiguous run of tiles with the
+// M tiles of one N tile adjacent, so the BM-row tiles that share a weight
+// tile run on one XCD and read it through one L2.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void* gl_lds_t;
+
+template <int WT>
+struct GlRow {   // LDS bytes of one weight row per 64-wide K step
+    static constexpr int B = WT == TLHIP_F16 ? 128 : (WT == TLHIP_Q8_0 ? 64 : 32);
+};
+
+// direct loads of one LDS region of R bytes by 512 threads: 16-byte loads
+// when R is a multiple of 8 KB, else 4-byte loads (R multiple of 2 KB)
+template <int R>
+struct GlDma {
+    static constexpr int SZ = R % 8192 == 0 ? 16 : 4;
+    static constexpr int N = R / (512 * SZ);
+    static_assert(R % 2048 == 0, "region");
+};
+
+template <int WT, int BM, int BN, int NS>
+struct Gl {
+    static constexpr int A_BYTES = BM * 128;
+    static constexpr int B_BYTES = BN * GlRow<WT>::B;
+    static constexpr int S_BYTES = WT == TLHIP_F16 ? 0 : BN * 4;
+    static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+    static constexpr int VMC = GlDma<A_BYTES>::N + GlDma<B_BYTES>::N + (S_BYTES ? 1 : 0);
+    static_assert((NS - 2) * VMC < 64, "vmcnt range");
+    static_assert(BN / 8 <= 64, "scale rows per wave");
+};
+
+template <int N>
+__device__ __forceinline__ void gl_wait_vm() {   // s_waitcnt vmcnt(N), gfx9 encoding
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+template <int VMC, int K>
+__device__ __forceinline__ void gl_wait_stage(int ahead) {   // wait until <= ahead stages outstanding
+    if constexpr (K == 0) {
+        gl_wait_vm<0>();
+    } else {
+        if (ahead >= K) gl_wait_vm<K * VMC>();
+        else gl_wait_stage<VMC, K - 1>(ahead);
+    }
+}
+
+template <int SZ>
+__device__ __forceinline__ void gl_dma(const void* g, uint8_t* lds) {
+    if constexpr (SZ == 16) __builtin_amdgcn_global_load_lds(g, (gl_lds_t)lds, 16, 0, 0);
+    else __builtin_amdgcn_global_load_lds(g, (gl_lds_t)lds, 4, 0, 0);
+}
+
+// Four payload bytes -> two f16 pairs in element order (e0,e1) (e2,e3).
+__device__ __forceinline__ void q8_pairs(uint32_t w, h2 dd, uint32_t& p01, uint32_t& p23) {
+    const h2 bias = {(h16)-1152.0f, (h16)-1152.0f};
+    const uint32_t v = w ^ 0x80808080u;
+    p01 = as_u32((as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x04010400u)) + bias) * dd);
+    p23 = as_u32((as_h2(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u)) + bias) * dd);
+}
+__device__ __forceinline__ void q4_pairs(uint32_t nib, h2 dd, uint32_t& p01, uint32_t& p23) {
+    const h2 bias = {(h16)-1032.0f, (h16)-1032.0f};
+    p01 = as_u32((as_h2(__builtin_amdgcn_perm(0x64646464u, nib, 0x04010400u)) + bias) * dd);
+    p23 = as_u32((as_h2(__builtin_amdgcn_perm(0x64646464u, nib, 0x04030402u)) + bias) * dd);
+}
+
+__device__ __forceinline__ int gl_tile(int id, int T) {   // XCD-contiguous tile order
+    const int x = id & 7, s = id >> 3, q = T >> 3, r = T & 7;
+    return x * q + min(x, r) + s;
+}
+
+template <int WT, int BM, int BN, int NS>
+__global__ __launch_bounds__(512) void gemm_lds_kernel(GemmParams p, float* __restrict__ part, int mT, int nT, int splits) {
+    using L = Gl<WT, BM, BN, NS>;
+    constexpr int TM = BM / 64, TN = BN / 128;   // 32x32 tiles per wave
+    constexpr int WTN = BN / 4;                   // wave tile width
+    static_assert(TN >= 1 && BN % 128 == 0, "BN");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * L::STAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3, hh = lane >> 5, l32 = lane & 31;
+    const int T = mT * nT;
+    const int q = gl_tile((int)blockIdx.x, T * splits);
+    const int z = q / T, qt = q % T;
+    const int m0 = (qt % mT) * BM, n0 = (qt / mT) * BN;
+    const int nkt = p.K / 64;
+    const int kt0 = (int)((int64_t)nkt * z / splits), kt1 = (int)((int64_t)nkt * (z + 1) / splits);
+    const int nk = kt1 - kt0;
+    const int nbr = p.K >> 5;
+
+    using DA = GlDma<L::A_BYTES>;
+    using DB = GlDma<L::B_BYTES>;
+    const uint8_t* a_src[DA::N];
+#pragma unroll
+    for (int u = 0; u < DA::N; u++) {
+        const int P = (u * 8 + wave) * 64 * DA::SZ + lane * DA::SZ;
+        const int r = P >> 7, c = ((P >> 4) & 7) ^ ((r >> 1) & 7);
+        const int m = min(m0 + r, p.M - 1);
+        a_src[u] = (const uint8_t*)(p.x + (size_t)m * p.K + (size_t)kt0 * 64 + 8 * c) + (P & 15);
+    }
+    const uint8_t* b_src[DB::N];
+#pragma unroll
+    for (int u = 0; u < DB::N; u++) {
+        constexpr int RB = GlRow<WT>::B;
+        const int P = (u * 8 + wave) * 64 * DB::SZ + lane * DB::SZ;
+        const int r = P / RB, cp = (P % RB) >> 4, byte = P & 15;
+        const int n = min(n0 + r, p.N - 1);
+        if (WT == TLHIP_F16) {
+            b_src[u] = p.wq + ((size_t)n * p.K + (size_t)kt0 * 64 + 8 * (cp ^ ((r >> 1) & 7))) * 2 + byte;
+        } else if (WT == TLHIP_Q8_0) {
+            b_src[u] = p.wq + (size_t)n * p.K + (size_t)kt0 * 64 + 16 * (cp ^ ((r >> 2) & 3)) + byte;
+        } else {
+            b_src[u] = p.wq + (size_t)n * (p.K / 2) + (size_t)kt0 * 32 + 16 * (cp ^ ((r >> 3) & 1)) + byte;
+        }
+    }
+    // scales: wave w, lanes < BN/8 -> row w*BN/8 + lane, both blocks of the step (4 bytes)
+    constexpr int SR = BN / 8;
+    const bool s_lane = lane < SR;
+    const uint8_t* s_src = nullptr;
+    if (L::S_BYTES) {
+        const int n = min(n0 + wave * SR + (s_lane ? lane : 0), p.N - 1);
+        s_src = (const uint8_t*)(p.wd + (size_t)n * nbr + 2 * (size_t)kt0);
+    }
+    constexpr int B_STEP = GlRow<WT>::B == 128 ? 128 : GlRow<WT>::B;
+
+    auto issue = [&](int step, int s) {   // step = kt - kt0
+        uint8_t* st = smem + s * L::STAGE;
+#pragma unroll
+        for (int u = 0; u < DA::N; u++) gl_dma<DA::SZ>(a_src[u] + (size_t)step * 128, st + (u * 8 + wave) * 64 * DA::SZ);
+#pragma unroll
+        for (int u = 0; u < DB::N; u++)
+            gl_dma<DB::SZ>(b_src[u] + (size_t)step * B_STEP, st + L::A_BYTES + (u * 8 + wave) * 64 * DB::SZ);
+        if (L::S_BYTES && s_lane) gl_dma<4>(s_src + (size_t)step * 4, st + L::A_BYTES + L::B_BYTES + wave * SR * 4);
+    };
+
+    f16v acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = f16v{0};
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; s++)
+        if (s < nk) issue(s, s);
+
+    // per-lane LDS offsets inside a stage (constant over the K loop)
+    int a_off[TM][4], b_off[TN][4];
+#pragma unroll
+    for (int ii = 0; ii < TM; ii++) {
+        const int m = wm * (BM / 2) + 32 * ii + l32;
+#pragma unroll
+        for (int t = 0; t < 4; t++) a_off[ii][t] = 128 * m + 16 * ((4 * hh + t) ^ ((m >> 1) & 7));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int n = wn * WTN + 32 * j + l32;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            if (WT == TLHIP_F16) b_off[j][t] = L::A_BYTES + 128 * n + 16 * ((4 * hh + t) ^ ((n >> 1) & 7));
+            else if (WT == TLHIP_Q8_0) b_off[j][t] = t < 2 ? L::A_BYTES + 64 * n + 16 * ((2 * hh + t) ^ ((n >> 2) & 3))
+                                                           : L::A_BYTES + L::B_BYTES + 4 * n + 2 * hh;
+            else b_off[j][t] = t == 0 ? L::A_BYTES + 32 * n + 16 * (hh ^ ((n >> 3) & 1))
+                                      : L::A_BYTES + L::B_BYTES + 4 * n + 2 * hh;
+        }
+    }
+
+    for (int i = 0; i < nk; i++) {
+        gl_wait_stage<L::VMC, NS - 2>(min(nk - 1 - i, NS - 2));
+        lds_barrier();   // stage i landed for every wave; stage i-1 fully read
+        if (i + NS - 1 < nk) issue(i + NS - 1, (i + NS - 1) % NS);
+
+        const uint8_t* st = smem + (i % NS) * L::STAGE;
+        // all LDS reads of the step first, then dequantise, then the MFMAs
+        h8 aop[TM][4];
+#pragma unroll
+        for (int ii = 0; ii < TM; ii++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) aop[ii][t] = *(const h8*)(st + a_off[ii][t]);
+        h8 bop[TN][4];
+        if (WT == TLHIP_F16) {
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) bop[j][t] = *(const h8*)(st + b_off[j][t]);
+        } else if (WT == TLHIP_Q8_0) {
+            u4 raw[TN][2];
+            h16 dh[TN];
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                raw[j][0] = *(const u4*)(st + b_off[j][0]);
+                raw[j][1] = *(const u4*)(st + b_off[j][1]);
+                dh[j] = *(const h16*)(st + b_off[j][2]);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const h2 dd = {dh[j], dh[j]};
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    uint32_t o0, o1, o2, o3;
+                    q8_pairs(raw[j][t >> 1][2 * (t & 1)], dd, o0, o1);
+                    q8_pairs(raw[j][t >> 1][2 * (t & 1) + 1], dd, o2, o3);
+                    bop[j][t] = __builtin_bit_cast(h8, u4{o0, o1, o2, o3});
+                }
+            }
+        } else {
+            u4 raw[TN];
+            h16 dh[TN];
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                raw[j] = *(const u4*)(st + b_off[j][0]);
+                dh[j] = *(const h16*)(st + b_off[j][1]);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const h2 dd = {dh[j], dh[j]};
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    // t = 0/1: low nibbles of bytes 0-7 / 8-15; t = 2/3: high nibbles
+                    const uint32_t w0 = raw[j][2 * (t & 1)], w1 = raw[j][2 * (t & 1) + 1];
+                    const uint32_t n0w = t < 2 ? (w0 & 0x0F0F0F0Fu) : ((w0 >> 4) & 0x0F0F0F0Fu);
+                    const uint32_t n1w = t < 2 ? (w1 & 0x0F0F0F0Fu) : ((w1 >> 4) & 0x0F0F0F0Fu);
+                    uint32_t o0, o1, o2, o3;
+                    q4_pairs(n0w, dd, o0, o1);
+                    q4_pairs(n1w, dd, o2, o3);
+                    bop[j][t] = __builtin_bit_cast(h8, u4{o0, o1, o2, o3});
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int ii = 0; ii < TM; ii++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[ii][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(aop[ii][t], bop[j][t], acc[ii][j], 0, 0, 0);
+    }
+
+    // C layout: col = lane%32 (weight row n), row = 8*(r/4) + 4*(lane/32) + r%4 (activation row m)
+#pragma unroll
+    for (int ii = 0; ii < TM; ii++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn * WTN + 32 * j + l32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * (BM / 2) + 32 * ii + 8 * (r >> 2) + 4 * hh + (r & 3);
+                const float v = acc[ii][j][r];
+                if (part) {
+                    if (m < p.M && n < p.N) part[((size_t)z * p.M + m) * p.N + n] = v;
+                } else {
+                    gemm_store_one(p, m, n, v);
+                }
+            }
+        }
+}
+
 // Sum of the split-K partials in slice order, then the epilogue.
 __global__ void gemm_reduce_kernel(GemmParams p, const float* __restrict__ part, int splits) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -304,23 +581,34 @@ __global__ void gemm_reduce_kernel(GemmParams p, const float* __restrict__ part,
     }
 }
 
+constexpr int GL_BM = 128, GL_BN = 128, GL_NS = 4;
+
 template <int WT>
 static void launch_gemm2(hipStream_t s, const GemmParams& p, int splits, float* part) {
     if (p.M > 64) {
-        dim3 grid((unsigned)((p.N + 63) / 64), (unsigned)((p.M + 127) / 128), (unsigned)splits);
-        hipLaunchKernelGGL((gemm2_kernel<WT, 128, 64, 2, 2>), grid, dim3(256), 0, s, p, part);
+        const int mT = (p.M + GL_BM - 1) / GL_BM, nT = (p.N + GL_BN - 1) / GL_BN;
+        hipLaunchKernelGGL((gemm_lds_kernel<WT, GL_BM, GL_BN, GL_NS>), dim3((unsigned)(mT * nT * splits)), dim3(512), 0, s,
+                           p, part, mT, nT, splits);
     } else {
         dim3 grid((unsigned)((p.N + 63) / 64), (unsigned)((p.M + 63) / 64), (unsigned)splits);
         hipLaunchKernelGGL((gemm2_kernel<WT, 64, 64, 2, 2>), grid, dim3(256), 0, s, p, part);
     }
 }
 
-// split-K slices for a grid of `tiles` output tiles: enough workgroups to
-// cover the 256 CUs about once, at least 4 K steps per slice.
+// split-K slices.  M <= 64 (register-staged 64 x 64 tiles): enough
+// workgroups to cover the 256 CUs about once, at least 4 K steps per slice.
+// M > 64 (multi-stage 128 x 128 tiles, one workgroup per CU): up to 4
+// slices while the grid stays within 320 workgroups, at least 8 K steps
+// per slice.
 int gemm_splits(int M, int N, int K) {
     if (K % G2_BK) return 1;
-    const int tiles = ((N + 63) / 64) * (M > 64 ? (M + 127) / 128 : (M + 63) / 64);
     int sp = 1;
+    if (M > 64) {
+        const int tiles = ((N + GL_BN - 1) / GL_BN) * ((M + GL_BM - 1) / GL_BM);
+        while (sp < 4 && tiles * sp * 2 <= 320 && (K / G2_BK) / (sp * 2) >= 8) sp *= 2;
+        return sp;
+    }
+    const int tiles = ((N + 63) / 64) * ((M + 63) / 64);
     while (sp < 8 && tiles * sp * 2 <= 512 && (K / G2_BK) / (sp * 2) >= 4) sp *= 2;
     return sp;
 }

@@ -146,7 +146,7 @@ def test_linear_q6_k(dev, oracle, M, N, K):
 @pytest.mark.parametrize("qt", [Q4_0, Q8_0, F16])
 @pytest.mark.parametrize("M,N,K", [(46, 5632, 2048), (5, 64, 64), (64, 256, 512), (130, 96, 2048),
                                    (512, 512, 2048), (33, 100, 96), (17, 2048, 5632), (64, 130, 160),
-                                   (8, 40, 32)])
+                                   (8, 40, 32), (512, 2048, 5632), (200, 384, 1024), (65, 256, 128)])
 def test_linear_gemm(dev, oracle, qt, M, N, K):
     x = S.normal_f16(3, f"x{M}x{K}", (M, K))
     if qt == F16:
