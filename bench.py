@@ -11,7 +11,9 @@ on the runner's stream, inputs and weights resident in HBM.
 Alongside: the dominant kernel's roofline -- the Q4_0 dequant-GEMV at
 5632 x 2048 (6,503,424 algorithmic bytes per launch), launched back to back
 over 48 weight copies (312 MB, more than the 256 MB MALL) so the weights come
-from HBM, timed with hipEvents around the launches on the context stream --
+from HBM, timed with hipEvents around the launches on the context stream
+(plus the warm figure, one copy re-read from the caches, and the same kernel
+on 26 MB and 76 MB matrices) --
 and the CPU oracle's restatement of the reference CPU path timed on this host.
 `roofline.traffic` is the HBM bytes per launch the profiler counted for that
 kernel (FETCH_SIZE + WRITE_SIZE, scaled by the same counters on a plain copy
@@ -62,8 +64,32 @@ def gemv_roofline(dev, iters: int, copies: int = 48):
         y = dev.empty((1, N))
         us_stream = bench_linear(dev, x, ws, y, iters, per_launch=False)
         us_event = bench_linear(dev, x, ws, y, max(iters // 4, 16), per_launch=True)
+        # warm: one weight copy, re-read from the L2 / MALL every launch
+        us_warm = bench_linear(dev, x, ws[:1], y, iters, per_launch=False)
         algo = N * K // 32 * 18 + 2 * K + 2 * N
-        out[f"{N}x{K}"] = dict(stream_us=us_stream, event_us=us_event, bytes=algo, gbs=algo / us_stream / 1e3)
+        out[f"{N}x{K}"] = dict(stream_us=us_stream, event_us=us_event, bytes=algo, gbs=algo / us_stream / 1e3,
+                               warm_us=us_warm, warm_gbs=algo / us_warm / 1e3)
+        del ws
+        dev.sync()
+    return out
+
+
+def gemv_size_sweep(dev, iters: int = 100):
+    """The same Q4_0 GEMV kernel on larger matrices (K = 2048, cold weights:
+    rotating copies past the 256 MB MALL): how much of the small-matrix gap
+    to the HBM peak is the fixed per-launch latency rather than streaming."""
+    from tensorlogic_amd import Q4_0, bench_linear
+    from tensorlogic_amd import synth as S
+    out = {}
+    K = 2048
+    for N, copies in ((22528, 12), (65536, 5)):
+        blocks = S.q4_0_blocks(105, f"sweep_W{N}", N, K)
+        ws = [dev.quantized(blocks, (N, K), Q4_0) for _ in range(copies)]
+        x = dev.tensor(S.normal_f16(105, "sweep_x", (1, K)))
+        y = dev.empty((1, N))
+        us = bench_linear(dev, x, ws, y, iters, per_launch=False)
+        algo = N * K // 32 * 18 + 2 * K + 2 * N
+        out[f"{N}x{K}"] = dict(us=us, bytes=algo, gbs=algo / us / 1e3, frac=algo / us / 1e3 / HBM_PEAK_GBS)
         del ws
         dev.sync()
     return out
@@ -227,7 +253,7 @@ def main():
         gem = gemv_roofline(dev, args.gemv_iters)
         cp = copy_reference(dev, args.gemv_iters)
         for k, v in gem.items():
-            log(f"Q4_0 GEMV {k}: {v['stream_us']:.2f} us/launch, {v['gbs']:.0f} GB/s")
+            log(f"Q4_0 GEMV {k}: {v['stream_us']:.2f} us/launch, {v['gbs']:.0f} GB/s (warm {v['warm_us']:.2f} us)")
         for k, v in cp.items():
             log(f"copy {k}: {v['us']:.2f} us, {v['gbs_rw']:.0f} GB/s read+write")
         dev.close()
@@ -270,6 +296,9 @@ def main():
     for k, v in gem.items():
         log(f"Q4_0 GEMV {k}: {v['stream_us']:.2f} us/launch back to back ({v['event_us']:.2f} us with an "
             f"event pair per launch), {v['gbs']:.0f} GB/s ({v['gbs'] / HBM_PEAK_GBS:.1%} of peak)")
+    sweep = gemv_size_sweep(dev)
+    for k, v in sweep.items():
+        log(f"Q4_0 GEMV {k} (cold): {v['us']:.2f} us, {v['gbs']:.0f} GB/s ({v['frac']:.1%} of peak)")
     cp = copy_reference(dev, args.gemv_iters)
     for k, v in cp.items():
         log(f"copy {k}: {v['us']:.2f} us, {v['gbs_rw']:.0f} GB/s read+write")
@@ -322,6 +351,7 @@ def main():
             "hbm_bytes_per_token": weights_per_token,
             "decode_hbm_roofline_frac": round(tok_s * weights_per_token / (HBM_PEAK_GBS * 1e9), 4),
             "gemv_2048x5632": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in gem.items()},
+            "gemv_q4_0_size_sweep_k2048": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in sweep.items()},
             "copy_reference": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in cp.items()},
             "config2_q8_0": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c2.items()},
             "config3_attention": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c3.items()},

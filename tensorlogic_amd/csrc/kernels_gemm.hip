@@ -10,7 +10,8 @@
 //
 // Three kernels: gemm_kernel (K % 64 != 0; 64 x 64 x 32 tiles), gemm2_kernel
 // (M <= 64: register-staged, two LDS buffers) and gemm_lds_kernel (M > 64:
-// 128 x 128 tiles, four LDS stages filled by direct global->LDS loads).
+// 128 x 128 tiles, three or four LDS stages filled by direct global->LDS
+// loads).
 #include "device_common.hpp"
 #include "internal.hpp"
 
@@ -581,14 +582,20 @@ __global__ void gemm_reduce_kernel(GemmParams p, const float* __restrict__ part,
     }
 }
 
-constexpr int GL_BM = 128, GL_BN = 128, GL_NS = 4;
+
+constexpr int GL_BM = 128, GL_BN = 128;
 
 template <int WT>
 static void launch_gemm2(hipStream_t s, const GemmParams& p, int splits, float* part) {
     if (p.M > 64) {
+        // four stages (one workgroup per CU) while the grid fits the 256 CUs;
+        // beyond that three stages, so that two workgroups share a CU
         const int mT = (p.M + GL_BM - 1) / GL_BM, nT = (p.N + GL_BN - 1) / GL_BN;
-        hipLaunchKernelGGL((gemm_lds_kernel<WT, GL_BM, GL_BN, GL_NS>), dim3((unsigned)(mT * nT * splits)), dim3(512), 0, s,
-                           p, part, mT, nT, splits);
+        const unsigned grid = (unsigned)(mT * nT * splits);
+        if (grid > 256)
+            hipLaunchKernelGGL((gemm_lds_kernel<WT, GL_BM, GL_BN, 3>), dim3(grid), dim3(512), 0, s, p, part, mT, nT, splits);
+        else
+            hipLaunchKernelGGL((gemm_lds_kernel<WT, GL_BM, GL_BN, 4>), dim3(grid), dim3(512), 0, s, p, part, mT, nT, splits);
     } else {
         dim3 grid((unsigned)((p.N + 63) / 64), (unsigned)((p.M + 63) / 64), (unsigned)splits);
         hipLaunchKernelGGL((gemm2_kernel<WT, 64, 64, 2, 2>), grid, dim3(256), 0, s, p, part);
