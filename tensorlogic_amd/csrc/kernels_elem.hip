@@ -56,10 +56,59 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const uint16_t* __restric
     }
 }
 
+// The same with 16-byte accesses for n % 8 == 0, n <= 8 * 256 * NC: thread t
+// holds the 8-element chunks t, t+256, ... of its row in registers, so x and
+// w are read once, with every load issued before the reduction.
+template <int NC>
+__global__ __launch_bounds__(256) void rms_norm_vec_kernel(const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ w,
+                                                           uint16_t* __restrict__ y, int n, float eps) {
+    __shared__ float red[4];
+    const u4* xr = (const u4*)(x + (size_t)blockIdx.x * n);
+    const u4* wr = (const u4*)w;
+    u4* yr = (u4*)(y + (size_t)blockIdx.x * n);
+    const int nch = n >> 3;
+    u4 xv[NC], wv[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int i = threadIdx.x + 256 * c;
+        xv[c] = i < nch ? xr[i] : u4{0u, 0u, 0u, 0u};
+        wv[c] = i < nch ? wr[i] : u4{0u, 0u, 0u, 0u};
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const h2 v = as_h2(xv[c][k]);
+            s += (float)v[0] * (float)v[0];
+            s += (float)v[1] * (float)v[1];
+        }
+    s = block_sum256(s, red);
+    const float inv = 1.0f / sqrtf(s / (float)n + eps);
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int i = threadIdx.x + 256 * c;
+        if (i < nch) {
+            u4 o;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const h2 v = as_h2(xv[c][k]), g = as_h2(wv[c][k]);
+                o[k] = (uint32_t)f2h(((float)v[0] * inv) * (float)g[0]) | ((uint32_t)f2h(((float)v[1] * inv) * (float)g[1]) << 16);
+            }
+            yr[i] = o;
+        }
+    }
+}
+
 tlhip_status launch_rms_norm(hipStream_t s, const uint16_t* x, const uint16_t* w, uint16_t* y,
                              int rows, int n, float eps) {
     if (rows <= 0 || n <= 0) return TLHIP_OK;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, s, x, w, y, n, eps);
+    const bool vec = n % 8 == 0 && ((uintptr_t)x | (uintptr_t)w | (uintptr_t)y) % 16 == 0;
+    if (vec && n <= 2048) hipLaunchKernelGGL(rms_norm_vec_kernel<1>, dim3(rows), dim3(256), 0, s, x, w, y, n, eps);
+    else if (vec && n <= 4096) hipLaunchKernelGGL(rms_norm_vec_kernel<2>, dim3(rows), dim3(256), 0, s, x, w, y, n, eps);
+    else if (vec && n <= 8192) hipLaunchKernelGGL(rms_norm_vec_kernel<4>, dim3(rows), dim3(256), 0, s, x, w, y, n, eps);
+    else hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(256), 0, s, x, w, y, n, eps);
     return TLHIP_OK;
 }
 
@@ -94,10 +143,81 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const uint16_t* __restr
     }
 }
 
+// The same with 16-byte accesses (n % 8 == 0, n <= 8 * 256 * NC), the row
+// held in registers between the two reductions.
+template <int NC>
+__global__ __launch_bounds__(256) void layer_norm_vec_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ w,
+                                                             const uint16_t* __restrict__ b,
+                                                             uint16_t* __restrict__ y, int n, float eps) {
+    __shared__ float red[4];
+    const u4* xr = (const u4*)(x + (size_t)blockIdx.x * n);
+    u4* yr = (u4*)(y + (size_t)blockIdx.x * n);
+    const int nch = n >> 3;
+    u4 xv[NC], wv[NC], bv[NC];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int i = threadIdx.x + 256 * c;
+        const bool in = i < nch;
+        xv[c] = in ? xr[i] : u4{0u, 0u, 0u, 0u};
+        wv[c] = in && w ? ((const u4*)w)[i] : u4{0u, 0u, 0u, 0u};
+        bv[c] = in && b ? ((const u4*)b)[i] : u4{0u, 0u, 0u, 0u};
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const h2 v = as_h2(xv[c][k]);
+            s += (float)v[0];
+            s += (float)v[1];
+        }
+    s = block_sum256(s, red);
+    const float mean = s / (float)n;
+    float q = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+        if (threadIdx.x + 256 * c < nch)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const h2 v = as_h2(xv[c][k]);
+                const float d0 = (float)v[0] - mean, d1 = (float)v[1] - mean;
+                q += d0 * d0;
+                q += d1 * d1;
+            }
+    q = block_sum256(q, red);
+    const float inv_std = 1.0f / sqrtf(q / (float)n + eps);
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const int i = threadIdx.x + 256 * c;
+        if (i < nch) {
+            u4 o;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const h2 v = as_h2(xv[c][k]), g = as_h2(wv[c][k]), bb = as_h2(bv[c][k]);
+                float r[2];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    float t = ((float)v[e] - mean) * inv_std;
+                    if (w) t = t * (float)g[e];
+                    if (b) t = t + (float)bb[e];
+                    r[e] = t;
+                }
+                o[k] = (uint32_t)f2h(r[0]) | ((uint32_t)f2h(r[1]) << 16);
+            }
+            yr[i] = o;
+        }
+    }
+}
+
 tlhip_status launch_layer_norm(hipStream_t s, const uint16_t* x, const uint16_t* w,
                                const uint16_t* b, uint16_t* y, int rows, int n, float eps) {
     if (rows <= 0 || n <= 0) return TLHIP_OK;
-    hipLaunchKernelGGL(layer_norm_kernel, dim3(rows), dim3(256), 0, s, x, w, b, y, n, eps);
+    const bool vec = n % 8 == 0 && ((uintptr_t)x | (uintptr_t)w | (uintptr_t)b | (uintptr_t)y) % 16 == 0;
+    if (vec && n <= 2048) hipLaunchKernelGGL(layer_norm_vec_kernel<1>, dim3(rows), dim3(256), 0, s, x, w, b, y, n, eps);
+    else if (vec && n <= 4096) hipLaunchKernelGGL(layer_norm_vec_kernel<2>, dim3(rows), dim3(256), 0, s, x, w, b, y, n, eps);
+    else if (vec && n <= 8192) hipLaunchKernelGGL(layer_norm_vec_kernel<4>, dim3(rows), dim3(256), 0, s, x, w, b, y, n, eps);
+    else hipLaunchKernelGGL(layer_norm_kernel, dim3(rows), dim3(256), 0, s, x, w, b, y, n, eps);
     return TLHIP_OK;
 }
 

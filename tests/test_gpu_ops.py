@@ -162,6 +162,27 @@ def test_linear_gemm(dev, oracle, qt, M, N, K):
     assert_close(y, ref, what=f"gemm {qt} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("qt,M,N,K", [(Q8_0, 46, 5632, 2048), (Q4_0, 512, 2048, 5632), (F16, 33, 256, 4096)])
+def test_gemm_split_k_deterministic(dev, oracle, qt, M, N, K):
+    """Split-K GEMMs sum their fp32 slices in slice order: repeated calls
+    give identical bits (no order depends on scheduling)."""
+    x = S.normal_f16(7, f"xs{M}x{K}", (M, K))
+    if qt == F16:
+        wh = S.normal_f16(7, f"Ws{N}x{K}", (N, K), 0.0, 0.05)
+        w = dev.tensor(wh)
+        ref = oracle.linear(x, wh)
+    else:
+        gen = S.q4_0_blocks if qt == Q4_0 else S.q8_0_blocks
+        blocks = gen(7, f"Ws{N}x{K}", N, K)
+        w = dev.quantized(blocks, (N, K), qt)
+        ref = oracle.linear_q(x, blocks, 2 if qt == Q4_0 else 8, N)
+    tx = dev.tensor(x)
+    outs = [tx.linear(w).numpy() for _ in range(5)]
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint16), outs[0].view(np.uint16))
+    assert_close(outs[0], ref, what=f"split-K gemm {qt} {M}x{N}x{K}")
+
+
 def test_linear_bias_and_f16_odd_shapes(dev, oracle):
     # src/ops/tests.rs:248-377 uses a rectangular [50, 122] case
     x = S.normal_f16(4, "x", (3, 50))
@@ -190,7 +211,8 @@ def test_linear_shape_errors(dev):
 # ---------------------------------------------------------------------------
 # normalisation, RoPE, softmax, elementwise
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("rows,n", [(1, 2048), (46, 2048), (34, 2048), (3, 4), (5, 2560)])
+@pytest.mark.parametrize("rows,n", [(1, 2048), (46, 2048), (34, 2048), (3, 4), (5, 2560), (3, 24), (2, 6144),
+                                    (1, 8192), (2, 8200)])
 def test_rms_norm(dev, oracle, rows, n):
     x = S.normal_f16(5, "x", (rows, n))
     w = S.normal_f16(5, "w", (n,), 1.0, 0.02)
@@ -207,10 +229,11 @@ def test_rms_norm_known_answer(dev):
     assert np.allclose(got, np.array([1, 2, 3, 4]) / np.sqrt(7.5), atol=1e-3)
 
 
-def test_layer_norm(dev, oracle):
-    x = S.normal_f16(6, "x", (7, 2560), 0.3, 2.0)
-    w = S.normal_f16(6, "w", (2560,), 1.0, 0.1)
-    b = S.normal_f16(6, "b", (2560,), 0.0, 0.1)
+@pytest.mark.parametrize("rows,n", [(7, 2560), (46, 2048), (2, 24), (3, 100), (2, 8192), (1, 9000)])
+def test_layer_norm(dev, oracle, rows, n):
+    x = S.normal_f16(6, "x", (rows, n), 0.3, 2.0)
+    w = S.normal_f16(6, "w", (n,), 1.0, 0.1)
+    b = S.normal_f16(6, "b", (n,), 0.0, 0.1)
     got = dev.tensor(x).layer_norm(dev.tensor(w), dev.tensor(b), 1e-5).numpy()
     ref = oracle.layer_norm(x, w, b, 1e-5)
     assert ulp_diff(got, ref).max() <= 1
