@@ -118,6 +118,11 @@ size_t type_bytes(uint32_t type, uint64_t nelem, bool* ok) {
     }
 }
 
+
+}  // namespace
+
+namespace tlhip {
+
 // Round-to-nearest-even f32 -> f16 (host side, for F32 GGUF tensors).
 uint16_t f32_to_f16(float f) {
     uint32_t x;
@@ -138,9 +143,6 @@ uint16_t f32_to_f16(float f) {
     return (uint16_t)(sign | (r >> 13));
 }
 
-}  // namespace
-
-namespace tlhip {
 
 // Tensor lookup for the model loader: row-major dims, GGUF type id, data.
 bool gguf_lookup(tlhip_gguf g, const char* name, uint32_t* type, int* ndim, int64_t dims[4],

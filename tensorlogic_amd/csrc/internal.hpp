@@ -173,6 +173,7 @@ tlhip_status launch_argmax_slots(hipStream_t s, const unsigned long long* slots,
                                  int32_t* token_log, int32_t* d_state);
 tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi);
 int gemm_splits(int M, int N, int K);   // split-K slices launch_gemm uses when given a workspace
+uint16_t f32_to_f16(float f);            // host RNE rounding (F32 GGUF tensors)
 // Rows 0..src_rows-1 of a GGUF block stream [src_rows, K] go to rows
 // dst_row0 + r * dst_step of a packed tensor of dst_rows rows (to_gguf = 1:
 // the reverse, packed tensor -> block stream).

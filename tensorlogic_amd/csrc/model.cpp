@@ -128,7 +128,17 @@ tlhip_status place_rows(tlhip_ctx ctx, tlhip_gguf g, const std::string& name, in
                     (long long)dims[0], (long long)dims[1], (long long)n, (long long)k);
     if (dtype_of(gt) != dst->dtype)
         return fail(TLHIP_ERR_DTYPE, "%s: GGUF type %u differs from the fused tensor's dtype", name.c_str(), gt);
-    if (gt == 0) return fail(TLHIP_ERR_DTYPE, "%s: F32 linear weights are not supported by the runner", name.c_str());
+    // F32 weights are rounded to f16 (RNE) on the host, as the reference's
+    // loader stores them (gguf.rs: f32 -> f16 at load)
+    std::vector<uint16_t> h16;
+    if (gt == 0) {
+        const size_t ne = (size_t)n * k;
+        h16.resize(ne);
+        const float* f = (const float*)data;
+        for (size_t i = 0; i < ne; i++) h16[i] = f32_to_f16(f[i]);
+        data = (const uint8_t*)h16.data();
+        nbytes = ne * 2;
+    }
     void* stage = nullptr;
     TLHIP_CHECK_HIP(hipMallocAsync(&stage, nbytes, ctx->stream));
     TLHIP_CHECK_HIP(hipMemcpyAsync(stage, data, nbytes, hipMemcpyHostToDevice, ctx->stream));
@@ -183,6 +193,15 @@ tlhip_status load_rows_permuted(tlhip_ctx ctx, tlhip_gguf g, const std::string& 
     const tlhip_dtype dt = dtype_of(gt);
     if (dt != TLHIP_Q4_0 && dt != TLHIP_Q8_0 && dt != TLHIP_F16)
         return fail(TLHIP_ERR_DTYPE, "%s: GGUF type %u not supported by the runner", name.c_str(), gt);
+    std::vector<uint16_t> h16;
+    if (gt == 0) {   // F32 -> f16 (RNE) on the host
+        const size_t ne = (size_t)n * k;
+        h16.resize(ne);
+        const float* f = (const float*)data;
+        for (size_t i = 0; i < ne; i++) h16[i] = f32_to_f16(f[i]);
+        data = (const uint8_t*)h16.data();
+        nbytes = ne * 2;
+    }
     const size_t rb = nbytes / (size_t)n;
     std::vector<uint8_t> host(nbytes);
     for (int64_t r = 0; r < n; r++) memcpy(host.data() + (size_t)r * rb, data + (size_t)perm[r] * rb, rb);
@@ -208,10 +227,18 @@ tlhip_status load_vec_permuted(tlhip_ctx ctx, tlhip_gguf g, const std::string& n
     size_t nbytes;
     if (!gguf_lookup(g, name.c_str(), &gt, &nd, dims, &data, &nbytes))
         return fail(TLHIP_ERR_LOAD, "tensor %s not found in GGUF", name.c_str());
-    if (gt != 1 || nbytes != perm.size() * 2)
-        return fail(TLHIP_ERR_SHAPE_MISMATCH, "%s: expected %zu f16 entries", name.c_str(), perm.size());
+    if (!((gt == 1 && nbytes == perm.size() * 2) || (gt == 0 && nbytes == perm.size() * 4)))
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "%s: expected %zu f16 / f32 entries", name.c_str(), perm.size());
     std::vector<uint16_t> host(perm.size());
-    for (size_t i = 0; i < perm.size(); i++) memcpy(&host[i], data + 2 * perm[i], 2);
+    for (size_t i = 0; i < perm.size(); i++) {
+        if (gt == 1) {
+            memcpy(&host[i], data + 2 * perm[i], 2);
+        } else {
+            float f;
+            memcpy(&f, data + 4 * perm[i], 4);
+            host[i] = f32_to_f16(f);
+        }
+    }
     int64_t shp[1] = {(int64_t)perm.size()};
     TLHIP_TRY(alloc_tensor(ctx, TLHIP_F16, 1, shp, out));
     tlhip_status st = tlhip_tensor_upload(ctx, *out, host.data(), host.size() * 2);

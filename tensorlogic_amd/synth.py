@@ -27,7 +27,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .gguf import GGML_F16, GGML_Q4_0, GGML_Q6_K, GGML_Q8_0, GGUFWriter
+from .gguf import GGML_F16, GGML_F32, GGML_Q4_0, GGML_Q6_K, GGML_Q8_0, GGUFWriter
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
 _M1 = np.uint64(0xBF58476D1CE4E5B9)
@@ -81,6 +81,15 @@ def normal_f16(seed: int, name: str, shape, mean: float = 0.0, std: float = 1.0)
     u1, u2 = u[0::2], u[1::2]
     z = np.sqrt(-2.0 * np.log1p(-u1)) * np.cos(2.0 * np.pi * u2)
     return (mean + std * z).astype(np.float32).astype(np.float16).reshape(shape)
+
+
+def normal_f32(seed: int, name: str, shape, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    """The normal_f16 draw kept in f32 (values generally not f16-representable)."""
+    n = int(np.prod(shape))
+    u = uniform01(stream_key(seed, name, "normal"), 2 * n)
+    u1, u2 = u[0::2], u[1::2]
+    z = np.sqrt(-2.0 * np.log1p(-u1)) * np.cos(2.0 * np.pi * u2)
+    return (mean + std * z).astype(np.float32).reshape(shape)
 
 
 def random_bytes(seed: int, name: str, purpose: str, nbytes: int) -> np.ndarray:
@@ -153,15 +162,25 @@ def write_llama_gguf(path: str, seed: int, n_layers: int = 22, hidden: int = 204
                      qtype: int = GGML_Q4_0, norm_mean: float = 0.0, out_qtype: int | None = None) -> None:
     """TinyLlama-architecture decoder with random-init weights.
 
-    Linear weights are Q4_0 (or Q8_0), `output.weight` the same unless
-    out_qtype says otherwise (GGML_Q6_K, as llama.cpp's Q4_0 checkpoints
-    store it), embeddings f16 N(0, 0.02) and RMSNorm weights f16
-    N(norm_mean, 0.02) (the benchmark configuration uses norm_mean 0).
-    Tensor names follow llama.cpp/GGUF.
+    Linear weights are Q4_0 (or Q8_0, or unquantised F16 / F32 ~ N(0, 0.02);
+    the F32 values are not f16-representable, so loading them exercises
+    the RNE rounding to f16), `output.weight` the same unless out_qtype says
+    otherwise (GGML_Q6_K, as llama.cpp's Q4_0 checkpoints store it),
+    embeddings f16 N(0, 0.02) and RMSNorm weights f16 N(norm_mean, 0.02)
+    (the benchmark configuration uses norm_mean 0).  Tensor names follow
+    llama.cpp/GGUF.
     """
-    qgen = q4_0_blocks if qtype == GGML_Q4_0 else q8_0_blocks
+    def float_weights(gtype):
+        def gen(sd, name, n, k):
+            if gtype == GGML_F16:
+                return normal_f16(sd, name, (n, k), 0.0, 0.02)
+            return normal_f32(sd, name, (n, k), 0.0, 0.02)
+        return gen
+    qgen = {GGML_Q4_0: q4_0_blocks, GGML_Q8_0: q8_0_blocks, GGML_F16: float_weights(GGML_F16),
+            GGML_F32: float_weights(GGML_F32)}[qtype]
     out_qtype = qtype if out_qtype is None else out_qtype
-    ogen = {GGML_Q4_0: q4_0_blocks, GGML_Q8_0: q8_0_blocks, GGML_Q6_K: q6_k_blocks}[out_qtype]
+    ogen = {GGML_Q4_0: q4_0_blocks, GGML_Q8_0: q8_0_blocks, GGML_Q6_K: q6_k_blocks,
+            GGML_F16: float_weights(GGML_F16), GGML_F32: float_weights(GGML_F32)}[out_qtype]
     hd = hidden // n_heads
     kvd = n_kv * hd
     w = GGUFWriter()

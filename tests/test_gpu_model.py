@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from tensorlogic_amd import Model
-from tensorlogic_amd.gguf import GGML_Q4_0, GGML_Q8_0
+from tensorlogic_amd.gguf import GGML_F16, GGML_F32, GGML_Q4_0, GGML_Q8_0
 from tensorlogic_amd import synth as S
 
 from test_gpu_ops import assert_close
@@ -53,6 +53,17 @@ def test_tiny_llama_greedy(dev, oracle, tmp_path, qtype):
     S.write_llama_gguf(path, seed=21, qtype=qtype, **TINY_LLAMA)
     prompt = S.token_ids(21, "prompt", 46, TINY_LLAMA["vocab"])
     _compare(dev, oracle, path, 0, prompt, 32)
+
+
+@pytest.mark.parametrize("qtype", [GGML_F16, GGML_F32])
+def test_tiny_llama_float_weights(dev, oracle, tmp_path, qtype):
+    """Unquantised GGUF linear weights (the reference loads F32 and F16
+    tensors too, gguf.rs: F32 rounded to f16): f16 GEMV / GEMM paths, F32
+    rounded RNE on the host exactly as the oracle's loader does."""
+    path = str(tmp_path / f"tiny_llama_f{qtype}.gguf")
+    S.write_llama_gguf(path, seed=26, qtype=qtype, **TINY_LLAMA)
+    prompt = S.token_ids(26, "prompt", 46, TINY_LLAMA["vocab"])
+    _compare(dev, oracle, path, 0, prompt, 24)
 
 
 def test_tiny_llama_q6_k_lm_head(dev, oracle, tmp_path):
