@@ -168,6 +168,35 @@ def config3_attention(dev, iters: int = 20):
     return res
 
 
+def config5_phi2(dev, steps: int = 256, n_prompt: int = 512):
+    """Config 5: Phi-2-architecture decoder (2.7B, Q8_0 linear weights, random
+    init), 512-token prompt prefilled through the MFMA GEMM and attention,
+    then `steps` greedy decode steps (graph replay) against the growing KV
+    cache; hipEvents on the runner's stream."""
+    from tensorlogic_amd import Model
+    from tensorlogic_amd import synth as S
+    tmp = tempfile.mkdtemp(prefix="tlbench_phi2_")
+    path = os.path.join(tmp, "phi2_q8_0.gguf")
+    t0 = time.time()
+    S.write_phi2_gguf(path, seed=5, **S.PHI2_ARGS)
+    log(f"wrote synthetic Phi-2 Q8_0 GGUF ({os.path.getsize(path) / 1e9:.2f} GB) in {time.time() - t0:.1f} s")
+    prompt = S.token_ids(5, "prompt", n_prompt, S.PHI2_ARGS["vocab"])
+    try:
+        m = Model(dev, path, arch=1, max_ctx=n_prompt + steps + 8)
+        m.generate(prompt, 8)   # warm-up, captures the decode graph
+        dev.sync()
+        _, prefill_ms, decode_ms = m.bench_decode(prompt, steps)
+        m.close()
+    finally:
+        os.remove(path)
+        os.rmdir(tmp)
+    # Q8_0 weight bytes read per decode token: (32 x 78.64 M + 131.07 M lm_head) weights x 34/32 B
+    wbytes = (32 * (3 * 2560 * 2560 + 2560 * 2560 + 2 * 10240 * 2560) + 51200 * 2560) * 34 // 32
+    return dict(prefill_512_ms=prefill_ms, prefill_tok_s=n_prompt / (prefill_ms / 1000.0),
+                decode_tok_s=steps / (decode_ms / 1000.0), decode_ms_per_token=decode_ms / steps,
+                decode_hbm_gbs=wbytes * steps / (decode_ms / 1000.0) / 1e9)
+
+
 def copy_reference(dev, iters: int):
     """Plain copy kernel: 6.5 MB (the GEMV's size, 48 rotating sources) and
     1 GiB -- the streaming bandwidth this device reaches at each size."""
@@ -216,6 +245,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--gemv-iters", type=int, default=480)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-phi2", action="store_true", help="skip the config-5 Phi-2 leg")
     ap.add_argument("--model", default="", help="reuse an existing TinyLlama GGUF file")
     ap.add_argument("--decode-launch", choices=("graph", "direct"), default="graph",
                     help="replay one captured HIP graph per decode step (default) or launch the same "
@@ -310,6 +340,11 @@ def main():
         log(f"attention {k}: {v['us']:.2f} us, {v['tflops']:.2f} TFLOP/s")
     q6 = q6k_lm_head(dev)
     log(f"Q6_K GEMV 32000x2048: {q6['us']:.2f} us, {q6['gbs']:.0f} GB/s")
+    c5 = None
+    if not args.no_phi2:
+        c5 = config5_phi2(dev)
+        log(f"Phi-2 Q8_0: prefill 512 tokens {c5['prefill_512_ms']:.2f} ms, decode {c5['decode_tok_s']:.1f} tok/s "
+            f"({c5['decode_hbm_gbs']:.0f} GB/s of weights)")
     g = gem["5632x2048"]
     dev.close()
 
@@ -356,6 +391,7 @@ def main():
             "config2_q8_0": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c2.items()},
             "config3_attention": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c3.items()},
             "q6_k_gemv_32000x2048": {k: round(v, 3) for k, v in q6.items()},
+            "config5_phi2_q8_0": {k: round(v, 3) for k, v in c5.items()} if c5 else None,
         },
         "roofline": {
             "kernel": GEMV_KERNEL,

@@ -251,14 +251,58 @@ __global__ __launch_bounds__(256) void attention64_kernel(AttnArgs a, int J_fixe
 
 // The same kernel for other even head dims D = 8 * EPL (Phi-2: 80): lane c
 // of a key's 8 lanes holds dims EPL*c .. EPL*c + EPL - 1, read as EPL/2
-// 4-byte words; one pass covers 32 keys; partial context rows are summed
-// in key-group order.
+// 4-byte words; ADK_THREADS threads (8 lanes per key) cover 64 * ADK_UNR
+// keys per pass; the first 256 keys' K and V rows are loaded before the
+// decode position is read (as attention64_kernel), the rest of the first
+// pass right after, so up to 512 keys cost about one round trip to memory; the partial context rows are summed over the key
+// groups of a wave, then over the waves, in a fixed order.
+constexpr int ADK_UNR = 8, ADK_THREADS = 512;   // 64 key groups x 8 = 512 keys per pass
+
+// Workgroup max / sum over NWV waves in a fixed order.
+template <int NWV>
+__device__ __forceinline__ float block_max(float v, float* red) {
+    v = wave_max(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int k = 1; k < NWV; k++) t = fmaxf(t, red[k]);
+    return t;
+}
+template <int NWV>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum<64>(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int k = 1; k < NWV; k++) t += red[k];
+    return t;
+}
+
+// NW consecutive 4-byte words of one key row: 16-byte loads for each full
+// group of four (rows are only 4-byte aligned for D = 80; the loads do not
+// need more), single words for the rest -- 2 requests per lane for D = 80
+// instead of 5.
+template <int NW>
+__device__ __forceinline__ void load_row_words(const uint32_t* __restrict__ p, uint32_t (&w)[NW]) {
+#pragma unroll
+    for (int t = 0; t + 4 <= NW; t += 4) {
+        u4 v;
+        __builtin_memcpy(&v, p + t, 16);
+        w[t] = v[0]; w[t + 1] = v[1]; w[t + 2] = v[2]; w[t + 3] = v[3];
+    }
+#pragma unroll
+    for (int t = NW / 4 * 4; t < NW; t++) w[t] = p[t];
+}
 template <int D>
-__global__ __launch_bounds__(256) void attention_dk_kernel(AttnArgs a, int J_fixed) {
-    constexpr int EPL = D / 8, NW = EPL / 2;
+__global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, int J_fixed) {
+    constexpr int EPL = D / 8, NW = EPL / 2, U = ADK_UNR, NT = ADK_THREADS, NWV = NT / 64, NG = NT / 8;
     __shared__ float sc[ATT_MAX_J];
-    __shared__ float red[4];
-    __shared__ float part[32][D + 1];
+    __shared__ float red[NWV];
+    __shared__ float part[NWV][D];
     const int s = blockIdx.x, h = blockIdx.y;
     const int Hkv = a.Hkv;
     const int kvh = h / (a.H / Hkv);
@@ -269,6 +313,26 @@ __global__ __launch_bounds__(256) void attention_dk_kernel(AttnArgs a, int J_fix
     const uint32_t* kbase = (const uint32_t*)(a.k + (size_t)kvh * D + EPL * c);
     const uint32_t* vbase = (const uint32_t*)(a.v + (size_t)kvh * D + EPL * c);
     const size_t wstride = kstride / 2;   // row stride in 4-byte words
+    // Loads that do not depend on the decode position go out first: q, and
+    // the first pass of K and V rows (bounded by the rows allocated).
+    // (the first half of the pass before the decode position is known, the
+    // rest once it is, for the keys that exist)
+    const int kv_lim = a.kv_rows > 0 ? (a.d_pos ? a.kv_rows : min(a.kv_rows, J_fixed)) : min(J_fixed, ATT_MAX_J);
+    uint32_t k0[U][NW], v0[U][NW];
+#pragma unroll
+    for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int t = 0; t < NW; t++) k0[u][t] = v0[u][t] = 0u;
+#pragma unroll
+    for (int u = 0; u < U / 2; u++) {
+        const int j = g + NG * u;
+        if (j < kv_lim) load_row_words<NW>(kbase + (size_t)j * wstride, k0[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U / 2; u++) {
+        const int j = g + NG * u;
+        if (j < kv_lim) load_row_words<NW>(vbase + (size_t)j * wstride, v0[u]);
+    }
     float qf[EPL];
     {
         const uint32_t* qw = (const uint32_t*)(a.q + (size_t)s * qs + (size_t)h * D + EPL * c);
@@ -282,18 +346,37 @@ __global__ __launch_bounds__(256) void attention_dk_kernel(AttnArgs a, int J_fix
     const int qpos = (a.d_pos ? *a.d_pos : a.q_pos0) + s;
     const int J = min(a.d_pos ? qpos + 1 : J_fixed, ATT_MAX_J);
     const int Jv = a.causal ? min(J, qpos + 1) : J;
+#pragma unroll
+    for (int u = U / 2; u < U; u++) {
+        const int j = g + NG * u;
+        if (j < Jv && j < kv_lim) load_row_words<NW>(kbase + (size_t)j * wstride, k0[u]);
+    }
+#pragma unroll
+    for (int u = U / 2; u < U; u++) {
+        const int j = g + NG * u;
+        if (j < Jv && j < kv_lim) load_row_words<NW>(vbase + (size_t)j * wstride, v0[u]);
+    }
 
     float mx = -INFINITY;
-    for (int j0 = g; j0 < Jv; j0 += 32 * 4) {
-        uint32_t kw[4][NW];
+    for (int j0 = g; j0 < Jv; j0 += NG * U) {
+        uint32_t kw[U][NW];
+        if (j0 == g) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int j = j0 + 32 * u;
+            for (int u = 0; u < U; u++)
 #pragma unroll
-            for (int t = 0; t < NW; t++) kw[u][t] = j < Jv ? kbase[(size_t)j * wstride + t] : 0u;
+                for (int t = 0; t < NW; t++) kw[u][t] = k0[u][t];
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int j = j0 + NG * u;
+                if (j < Jv) load_row_words<NW>(kbase + (size_t)j * wstride, kw[u]);
+                else
+#pragma unroll
+                    for (int t = 0; t < NW; t++) kw[u][t] = 0u;
+            }
         }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < U; u++) {
             float acc = 0.0f;
 #pragma unroll
             for (int t = 0; t < NW; t++) {
@@ -302,7 +385,7 @@ __global__ __launch_bounds__(256) void attention_dk_kernel(AttnArgs a, int J_fix
                 acc += qf[2 * t + 1] * (float)k2[1];
             }
             acc = group8_sum(acc);
-            const int j = j0 + 32 * u;
+            const int j = j0 + NG * u;
             if (j < Jv) {
                 const float v = h2f(f2h(h2f(f2h(acc)) * a.scale_h));
                 if (c == 0) sc[j] = v;
@@ -310,36 +393,45 @@ __global__ __launch_bounds__(256) void attention_dk_kernel(AttnArgs a, int J_fix
             }
         }
     }
-    mx = bmax(mx, red);
+    mx = block_max<NWV>(mx, red);
     if (!isfinite(mx)) mx = 0.0f;
     float sum = 0.0f;
-    for (int j = tid; j < Jv; j += 256) {
+    for (int j = tid; j < Jv; j += NT) {
         const float v = sc[j];
         const float e = isfinite(v) ? expf(v - mx) : 0.0f;
         sc[j] = h2f(f2h(e));
         sum += e;
     }
-    sum = bsum(sum, red);
+    sum = block_sum<NWV>(sum, red);
     const bool degenerate = !(sum > 0.0f && isfinite(sum));
     const int Jp = degenerate ? J : Jv;
     const float uni = h2f(f2h(1.0f / (float)J));
-    for (int j = tid; j < Jp; j += 256) sc[j] = degenerate ? uni : h2f(f2h(sc[j] / sum));
+    for (int j = tid; j < Jp; j += NT) sc[j] = degenerate ? uni : h2f(f2h(sc[j] / sum));
     __syncthreads();
 
     float o[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; e++) o[e] = 0.0f;
-    for (int j0 = g; j0 < Jp; j0 += 32 * 4) {
-        uint32_t vw[4][NW];
+    for (int j0 = g; j0 < Jp; j0 += NG * U) {
+        uint32_t vw[U][NW];
+        if (j0 == g) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int j = j0 + 32 * u;
+            for (int u = 0; u < U; u++)
 #pragma unroll
-            for (int t = 0; t < NW; t++) vw[u][t] = j < Jp ? vbase[(size_t)j * wstride + t] : 0u;
+                for (int t = 0; t < NW; t++) vw[u][t] = v0[u][t];
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int j = j0 + NG * u;
+                if (j < Jp) load_row_words<NW>(vbase + (size_t)j * wstride, vw[u]);
+                else
+#pragma unroll
+                    for (int t = 0; t < NW; t++) vw[u][t] = 0u;
+            }
         }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int j = j0 + 32 * u;
+        for (int u = 0; u < U; u++) {
+            const int j = j0 + NG * u;
             if (j < Jp) {
                 const float pj = sc[j];
 #pragma unroll
@@ -351,12 +443,17 @@ __global__ __launch_bounds__(256) void attention_dk_kernel(AttnArgs a, int J_fix
             }
         }
     }
+    // the 8 key groups of each wave (lanes with the same c), then the waves
 #pragma unroll
-    for (int e = 0; e < EPL; e++) part[g][EPL * c + e] = o[e];
-    __syncthreads();
+    for (int e = 0; e < EPL; e++) o[e] = stride8_sum(o[e]);
+    if ((tid & 63) < 8)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) part[tid >> 6][EPL * c + e] = o[e];
+    lds_barrier();
     if (tid < D) {
         float t = part[0][tid];
-        for (int gg = 1; gg < 32; gg++) t += part[gg][tid];
+#pragma unroll
+        for (int wv = 1; wv < NWV; wv++) t += part[wv][tid];
         a.out[(size_t)s * os + (size_t)h * D + tid] = f2h(t);
     }
 }
@@ -739,8 +836,8 @@ tlhip_status launch_attention_mfma(hipStream_t s, const AttnArgs& a, int J, uint
 
 static void launch_attn_any(hipStream_t s, const AttnArgs& a, int J) {
     if (a.D == 64) hipLaunchKernelGGL(attention64_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, J);
-    else if (a.D == 80) hipLaunchKernelGGL(attention_dk_kernel<80>, dim3(a.S, a.H), dim3(256), 0, s, a, J);
-    else if (a.D == 128) hipLaunchKernelGGL(attention_dk_kernel<128>, dim3(a.S, a.H), dim3(256), 0, s, a, J);
+    else if (a.D == 80) hipLaunchKernelGGL(attention_dk_kernel<80>, dim3(a.S, a.H), dim3(ADK_THREADS), 0, s, a, J);
+    else if (a.D == 128) hipLaunchKernelGGL(attention_dk_kernel<128>, dim3(a.S, a.H), dim3(ADK_THREADS), 0, s, a, J);
     else hipLaunchKernelGGL(attention_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, J);
 }
 

@@ -310,7 +310,10 @@ def test_mask_and_einsums(dev, oracle):
     (45, 77, 8, 4, 64, 0, False),
     (128, 128, 4, 4, 64, 0, True), (300, 300, 8, 4, 64, 0, True), (2048, 2048, 4, 1, 64, 0, True),
     (512, 512, 4, 4, 80, 0, True), (160, 200, 8, 8, 80, 40, True), (129, 129, 5, 1, 128, 0, True),
-    (200, 200, 6, 3, 64, 0, True), (128, 300, 4, 4, 80, 0, False), (250, 90, 4, 2, 128, 0, False)])
+    (200, 200, 6, 3, 64, 0, True), (128, 300, 4, 4, 80, 0, False), (250, 90, 4, 2, 128, 0, False),
+    # single-row kernels for other head dims around their 256 / 512-key passes
+    (1, 100, 8, 8, 80, 99, True), (1, 300, 4, 4, 80, 299, True), (1, 513, 4, 2, 128, 512, True),
+    (3, 600, 4, 2, 80, 597, True), (2, 1100, 4, 4, 80, 0, False)])
 def test_attention(dev, oracle, Sq, J, H, Hkv, D, q0, causal):
     q = S.normal_f16(11, "q", (Sq, H, D))
     k = S.normal_f16(11, "k", (J, Hkv, D))
