@@ -96,168 +96,6 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, int J_fixed)
     }
 }
 
-// Head-dim-64 variant with the same arithmetic and storage points, laid out
-// for the memory system: a key is read by 8 lanes with one 16-byte load each
-// (a head's 128-byte K/V row in one coalesced access), 32 keys per pass, and
-// the loads of UNR passes are issued before their dot products so several
-// L2/HBM round trips overlap.  Scores: the 8 lanes' partial dot products are
-// combined with an xor tree.  Context: thread (g, c) accumulates dims
-// 8c..8c+7 over keys g, g+32, ...; the 32 partial rows are summed in g order.
-constexpr int A64_UNR = 8;
-
-__global__ __launch_bounds__(256) void attention64_kernel(AttnArgs a, int J_fixed) {
-    __shared__ float sc[ATT_MAX_J];
-    __shared__ float red[4];
-    __shared__ float part[4][64];
-    const int s = blockIdx.x, h = blockIdx.y;
-    const int Hkv = a.Hkv;
-    const int kvh = h / (a.H / Hkv);
-    const int qs = a.q_stride ? a.q_stride : a.H * 64;
-    const int os = a.out_stride ? a.out_stride : a.H * 64;
-    const int tid = threadIdx.x, c = tid & 7, g = tid >> 3;
-    const size_t kstride = (size_t)Hkv * 64;
-    const uint16_t* kbase = a.k + (size_t)kvh * 64 + 8 * c;
-    const uint16_t* vbase = a.v + (size_t)kvh * 64 + 8 * c;
-    // Loads that do not depend on the decode position go out first: q, and
-    // the first pass of K and V rows (bounded by the rows allocated, so
-    // every address is in bounds; rows past the key count are never used).
-    const u4 qv = *(const u4*)(a.q + (size_t)s * qs + (size_t)h * 64 + 8 * c);
-    const int kv_lim = a.kv_rows > 0 ? a.kv_rows : min(J_fixed, ATT_MAX_J);
-    u4 k0[A64_UNR], vv[A64_UNR];
-#pragma unroll
-    for (int u = 0; u < A64_UNR; u++) {
-        const int j = g + 32 * u;
-        k0[u] = j < kv_lim ? *(const u4*)(kbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int u = 0; u < A64_UNR; u++) {
-        const int j = g + 32 * u;
-        vv[u] = j < kv_lim ? *(const u4*)(vbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
-    }
-    const int qpos = (a.d_pos ? *a.d_pos : a.q_pos0) + s;
-    const int J = min(a.d_pos ? qpos + 1 : J_fixed, ATT_MAX_J);
-    const int Jv = a.causal ? min(J, qpos + 1) : J;
-
-    float qf[8];
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const h2 p2 = as_h2(qv[t]);
-        qf[2 * t] = (float)p2[0];
-        qf[2 * t + 1] = (float)p2[1];
-    }
-
-    // One pass covers 32 * A64_UNR keys; the first pass uses the rows loaded
-    // above.  When the unmasked row fits in that pass, the V rows loaded
-    // with it are used directly (one round trip to memory in all).
-    const bool one_pass = Jv <= 32 * A64_UNR;
-    float mx = -INFINITY;
-    for (int j0 = g; j0 < Jv; j0 += 32 * A64_UNR) {
-        u4 kv[A64_UNR];
-        if (j0 == g) {
-#pragma unroll
-            for (int u = 0; u < A64_UNR; u++) kv[u] = k0[u];
-        } else {
-#pragma unroll
-            for (int u = 0; u < A64_UNR; u++) {
-                const int j = j0 + 32 * u;
-                kv[u] = j < Jv ? *(const u4*)(kbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < A64_UNR; u++) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const h2 k2 = as_h2(kv[u][t]);
-                acc += qf[2 * t] * (float)k2[0];
-                acc += qf[2 * t + 1] * (float)k2[1];
-            }
-            acc = group8_sum(acc);
-            const int j = j0 + 32 * u;
-            if (j < Jv) {
-                const float v = h2f(f2h(h2f(f2h(acc)) * a.scale_h));
-                if (c == 0) sc[j] = v;
-                if (isfinite(v)) mx = fmaxf(mx, v);
-            }
-        }
-    }
-    mx = bmax(mx, red);   // (its barriers also publish sc[])
-    if (!isfinite(mx)) mx = 0.0f;
-    float sum = 0.0f;
-    for (int j = tid; j < Jv; j += 256) {
-        const float v = sc[j];
-        const float e = isfinite(v) ? expf(v - mx) : 0.0f;
-        sc[j] = h2f(f2h(e));
-        sum += e;
-    }
-    sum = bsum(sum, red);
-    const bool degenerate = !(sum > 0.0f && isfinite(sum));
-    const int Jp = degenerate ? J : Jv;
-    const float uni = h2f(f2h(1.0f / (float)J));
-    for (int j = tid; j < Jp; j += 256) sc[j] = degenerate ? uni : h2f(f2h(sc[j] / sum));
-    __syncthreads();
-
-    float o[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) o[e] = 0.0f;
-    if (one_pass && !degenerate) {
-#pragma unroll
-        for (int u = 0; u < A64_UNR; u++) {
-            const int j = g + 32 * u;
-            if (j < Jp) {
-                const float pj = sc[j];
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const h2 v2 = as_h2(vv[u][t]);
-                    o[2 * t] += pj * (float)v2[0];
-                    o[2 * t + 1] += pj * (float)v2[1];
-                }
-            }
-        }
-    } else {
-        for (int j0 = g; j0 < Jp; j0 += 32 * A64_UNR) {
-#pragma unroll
-            for (int u = 0; u < A64_UNR; u++) {
-                const int j = j0 + 32 * u;
-                vv[u] = j < Jp ? *(const u4*)(vbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
-            }
-#pragma unroll
-            for (int u = 0; u < A64_UNR; u++) {
-                const int j = j0 + 32 * u;
-                if (j < Jp) {
-                    const float pj = sc[j];
-#pragma unroll
-                    for (int t = 0; t < 4; t++) {
-                        const h2 v2 = as_h2(vv[u][t]);
-                        o[2 * t] += pj * (float)v2[0];
-                        o[2 * t + 1] += pj * (float)v2[1];
-                    }
-                }
-            }
-        }
-    }
-    // the 8 key groups of each wave (lanes with the same c), then the 4 waves
-#pragma unroll
-    for (int e = 0; e < 8; e++) o[e] = stride8_sum(o[e]);
-    if ((tid & 63) < 8)
-#pragma unroll
-        for (int e = 0; e < 8; e++) part[tid >> 6][8 * c + e] = o[e];
-    lds_barrier();
-    if (tid < 64) {
-        const float t = (part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]);
-        a.out[(size_t)s * os + (size_t)h * 64 + tid] = f2h(t);
-    }
-}
-
-// The same kernel for other even head dims D = 8 * EPL (Phi-2: 80): lane c
-// of a key's 8 lanes holds dims EPL*c .. EPL*c + EPL - 1, read as EPL/2
-// 4-byte words; ADK_THREADS threads (8 lanes per key) cover 64 * ADK_UNR
-// keys per pass; the first 256 keys' K and V rows are loaded before the
-// decode position is read (as attention64_kernel), the rest of the first
-// pass right after, so up to 512 keys cost about one round trip to memory; the partial context rows are summed over the key
-// groups of a wave, then over the waves, in a fixed order.
-constexpr int ADK_UNR = 8, ADK_THREADS = 512;   // 64 key groups x 8 = 512 keys per pass
-
 // Workgroup max / sum over NWV waves in a fixed order.
 template <int NWV>
 __device__ __forceinline__ float block_max(float v, float* red) {
@@ -281,6 +119,172 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     for (int k = 1; k < NWV; k++) t += red[k];
     return t;
 }
+
+// Head-dim-64 variant with the same arithmetic and storage points, laid out
+// for the memory system: a key is read by 8 lanes with one 16-byte load each
+// (a head's 128-byte K/V row in one coalesced access), 32 keys per pass, and
+// the loads of UNR passes are issued before their dot products so several
+// L2/HBM round trips overlap.  Scores: the 8 lanes' partial dot products are
+// combined with an xor tree.  Context: thread (g, c) accumulates dims
+// 8c..8c+7 over keys g, g+32, ...; the 32 partial rows are summed in g order.
+constexpr int A64_UNR = 8;
+
+template <int NT>
+__global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed) {
+    constexpr int NWV = NT / 64, NG = NT / 8;
+    __shared__ float sc[ATT_MAX_J];
+    __shared__ float red[NWV];
+    __shared__ float part[NWV][64];
+    const int s = blockIdx.x, h = blockIdx.y;
+    const int Hkv = a.Hkv;
+    const int kvh = h / (a.H / Hkv);
+    const int qs = a.q_stride ? a.q_stride : a.H * 64;
+    const int os = a.out_stride ? a.out_stride : a.H * 64;
+    const int tid = threadIdx.x, c = tid & 7, g = tid >> 3;
+    const size_t kstride = (size_t)Hkv * 64;
+    const uint16_t* kbase = a.k + (size_t)kvh * 64 + 8 * c;
+    const uint16_t* vbase = a.v + (size_t)kvh * 64 + 8 * c;
+    // Loads that do not depend on the decode position go out first: q, and
+    // the first pass of K and V rows (bounded by the rows allocated, so
+    // every address is in bounds; rows past the key count are never used).
+    const u4 qv = *(const u4*)(a.q + (size_t)s * qs + (size_t)h * 64 + 8 * c);
+    const int kv_lim = a.kv_rows > 0 ? (a.d_pos ? a.kv_rows : min(a.kv_rows, J_fixed)) : min(J_fixed, ATT_MAX_J);
+    u4 k0[A64_UNR], vv[A64_UNR];
+#pragma unroll
+    for (int u = 0; u < A64_UNR; u++) {
+        const int j = g + NG * u;
+        k0[u] = j < kv_lim ? *(const u4*)(kbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < A64_UNR; u++) {
+        const int j = g + NG * u;
+        vv[u] = j < kv_lim ? *(const u4*)(vbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
+    }
+    const int qpos = (a.d_pos ? *a.d_pos : a.q_pos0) + s;
+    const int J = min(a.d_pos ? qpos + 1 : J_fixed, ATT_MAX_J);
+    const int Jv = a.causal ? min(J, qpos + 1) : J;
+
+    float qf[8];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const h2 p2 = as_h2(qv[t]);
+        qf[2 * t] = (float)p2[0];
+        qf[2 * t + 1] = (float)p2[1];
+    }
+
+    // One pass covers NG * A64_UNR keys; the first pass uses the rows loaded
+    // above.  When the unmasked row fits in that pass, the V rows loaded
+    // with it are used directly (one round trip to memory in all).
+    const bool one_pass = Jv <= NG * A64_UNR;
+    float mx = -INFINITY;
+    for (int j0 = g; j0 < Jv; j0 += NG * A64_UNR) {
+        u4 kv[A64_UNR];
+        if (j0 == g) {
+#pragma unroll
+            for (int u = 0; u < A64_UNR; u++) kv[u] = k0[u];
+        } else {
+#pragma unroll
+            for (int u = 0; u < A64_UNR; u++) {
+                const int j = j0 + NG * u;
+                kv[u] = j < Jv ? *(const u4*)(kbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < A64_UNR; u++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const h2 k2 = as_h2(kv[u][t]);
+                acc += qf[2 * t] * (float)k2[0];
+                acc += qf[2 * t + 1] * (float)k2[1];
+            }
+            acc = group8_sum(acc);
+            const int j = j0 + NG * u;
+            if (j < Jv) {
+                const float v = h2f(f2h(h2f(f2h(acc)) * a.scale_h));
+                if (c == 0) sc[j] = v;
+                if (isfinite(v)) mx = fmaxf(mx, v);
+            }
+        }
+    }
+    mx = block_max<NWV>(mx, red);   // (its barriers also publish sc[])
+    if (!isfinite(mx)) mx = 0.0f;
+    float sum = 0.0f;
+    for (int j = tid; j < Jv; j += NT) {
+        const float v = sc[j];
+        const float e = isfinite(v) ? expf(v - mx) : 0.0f;
+        sc[j] = h2f(f2h(e));
+        sum += e;
+    }
+    sum = block_sum<NWV>(sum, red);
+    const bool degenerate = !(sum > 0.0f && isfinite(sum));
+    const int Jp = degenerate ? J : Jv;
+    const float uni = h2f(f2h(1.0f / (float)J));
+    for (int j = tid; j < Jp; j += NT) sc[j] = degenerate ? uni : h2f(f2h(sc[j] / sum));
+    __syncthreads();
+
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = 0.0f;
+    if (one_pass && !degenerate) {
+#pragma unroll
+        for (int u = 0; u < A64_UNR; u++) {
+            const int j = g + NG * u;
+            if (j < Jp) {
+                const float pj = sc[j];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const h2 v2 = as_h2(vv[u][t]);
+                    o[2 * t] += pj * (float)v2[0];
+                    o[2 * t + 1] += pj * (float)v2[1];
+                }
+            }
+        }
+    } else {
+        for (int j0 = g; j0 < Jp; j0 += NG * A64_UNR) {
+#pragma unroll
+            for (int u = 0; u < A64_UNR; u++) {
+                const int j = j0 + NG * u;
+                vv[u] = j < Jp ? *(const u4*)(vbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < A64_UNR; u++) {
+                const int j = j0 + NG * u;
+                if (j < Jp) {
+                    const float pj = sc[j];
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        const h2 v2 = as_h2(vv[u][t]);
+                        o[2 * t] += pj * (float)v2[0];
+                        o[2 * t + 1] += pj * (float)v2[1];
+                    }
+                }
+            }
+        }
+    }
+    // the 8 key groups of each wave (lanes with the same c), then the 4 waves
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = stride8_sum(o[e]);
+    if ((tid & 63) < 8)
+#pragma unroll
+        for (int e = 0; e < 8; e++) part[tid >> 6][8 * c + e] = o[e];
+    lds_barrier();
+    if (tid < 64) {
+        float t = part[0][tid];
+#pragma unroll
+        for (int wv = 1; wv < NWV; wv++) t += part[wv][tid];
+        a.out[(size_t)s * os + (size_t)h * 64 + tid] = f2h(t);
+    }
+}
+
+// The same kernel for other even head dims D = 8 * EPL (Phi-2: 80): lane c
+// of a key's 8 lanes holds dims EPL*c .. EPL*c + EPL - 1, read as EPL/2
+// 4-byte words; ADK_THREADS threads (8 lanes per key) cover 64 * ADK_UNR
+// keys per pass; the first 256 keys' K and V rows are loaded before the
+// decode position is read (as attention64_kernel), the rest of the first
+// pass right after, so up to 512 keys cost about one round trip to memory; the partial context rows are summed over the key
+// groups of a wave, then over the waves, in a fixed order.
+constexpr int ADK_UNR = 8, ADK_THREADS = 512;   // 64 key groups x 8 = 512 keys per pass
 
 // NW consecutive 4-byte words of one key row: 16-byte loads for each full
 // group of four (rows are only 4-byte aligned for D = 80; the loads do not
@@ -835,7 +839,10 @@ tlhip_status launch_attention_mfma(hipStream_t s, const AttnArgs& a, int J, uint
 }
 
 static void launch_attn_any(hipStream_t s, const AttnArgs& a, int J) {
-    if (a.D == 64) hipLaunchKernelGGL(attention64_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, J);
+    // a key count known at launch above one 256-key pass takes the 512-thread
+    // variant (512 keys per pass); decode (J read on the device) keeps 256
+    if (a.D == 64 && !a.d_pos && J > 256) hipLaunchKernelGGL(attention64_kernel<512>, dim3(a.S, a.H), dim3(512), 0, s, a, J);
+    else if (a.D == 64) hipLaunchKernelGGL(attention64_kernel<256>, dim3(a.S, a.H), dim3(256), 0, s, a, J);
     else if (a.D == 80) hipLaunchKernelGGL(attention_dk_kernel<80>, dim3(a.S, a.H), dim3(ADK_THREADS), 0, s, a, J);
     else if (a.D == 128) hipLaunchKernelGGL(attention_dk_kernel<128>, dim3(a.S, a.H), dim3(ADK_THREADS), 0, s, a, J);
     else hipLaunchKernelGGL(attention_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, J);
