@@ -219,23 +219,88 @@ def pmc_traffic():
     return int(m.group(1)) if m else None
 
 
-def cpu_baseline(path: str, prompt, threads: int = 1):
+def _host_cpu():
+    name = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return name, os.cpu_count(), len(os.sched_getaffinity(0))
+
+
+def _time_call(fn, min_s: float = 0.3):
+    """Seconds per call: repeats fn until min_s has passed (one call if slower)."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s:
+            return dt / n
+
+
+def cpu_ops(threads: int, big: bool):
+    """The oracle's restatement of the reference CPU ops at `threads` OpenMP
+    threads: Q4_0 dequantisation of config 1's W[2048 x 2048] (the reference
+    dequantises on load, one block after another: gguf.rs:68-112), and
+    matmul_cpu on the dequantised f16 weights with f16 accumulation
+    (matmul.rs:201-228) for config 1 (M = 1, 2048 x 2048 Q4_0) and config 2
+    (Q8_0 W[5632 x 2048] at M = 1 and 46, and 512 when `big`)."""
+    from oracle import oracle as O
+    from tensorlogic_amd import synth as S
+    O.set_threads(threads)
+    out = {}
+    w1 = S.q4_0_blocks(101, "bench_W2048x2048", 2048, 2048)
+    f1 = O.dequant(w1, 2).reshape(2048, 2048)
+    t = _time_call(lambda: O.dequant(w1, 2))
+    out["dequant_q4_0_2048x2048"] = dict(ms=t * 1e3, packed_mb_s=w1.size / t / 1e6,
+                                         f16_mb_s=f1.nbytes / t / 1e6)
+    x1 = S.normal_f16(101, "bench_x", (1, 2048))
+    t = _time_call(lambda: O.linear(x1, f1, acc=O.ACC_F16))
+    out["gemv_cfg1_2048x2048"] = dict(us=t * 1e6, gflops=2 * 2048 * 2048 / t / 1e9)
+    w2 = O.dequant(S.q8_0_blocks(102, "bench_q8_W5632x2048", 5632, 2048), 8).reshape(5632, 2048)
+    for M in ((1, 46, 512) if big else (1, 46)):
+        x = S.normal_f16(102, f"bench_q8_x{M}x2048", (M, 2048))
+        t = _time_call(lambda: O.linear(x, w2, acc=O.ACC_F16), min_s=0.3 if M == 1 else 0.0)
+        out[f"cfg2_M{M}_5632x2048"] = dict(ms=t * 1e3, gflops=2 * M * 5632 * 2048 / t / 1e9)
+    return out
+
+
+def cpu_baseline(path: str, prompt, omp_threads: int):
     """The oracle's restatement of the reference CPU path (dequantise on
     load, f16-accumulating matmul_cpu, rms_norm_cpu, ...) timing one
     decode-token forward pass of the full model, single-threaded like the
-    reference's CPU loops."""
+    reference's CPU loops (`value`), then the same pass on `omp_threads`
+    OpenMP threads, and the per-op figures of cpu_ops at both counts."""
     from oracle import oracle as O
+    cpu_name, nproc, affinity = _host_cpu()
     t0 = time.time()
-    m = O.Model(path, arch=0, max_ctx=64, acc=O.ACC_F16, n_threads=threads)
+    m = O.Model(path, arch=0, max_ctx=64, acc=O.ACC_F16, n_threads=1)
     load_s = time.time() - t0
+    O.set_threads(1)
     t0 = time.time()
     m.forward(np.asarray(prompt[:1], np.int32), 0)
     fwd_s = time.time() - t0
+    O.set_threads(omp_threads)
+    m.reset()
+    t0 = time.time()
+    m.forward(np.asarray(prompt[:1], np.int32), 0)
+    fwd_omp_s = time.time() - t0
     m.close()
-    return dict(value=1.0 / fwd_s, unit="tok/s", cores=threads, kind="port",
+    ops1 = cpu_ops(1, big=False)
+    opsn = cpu_ops(omp_threads, big=True)
+    O.set_threads(1)
+    r = lambda d: {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in d.items()}
+    return dict(value=1.0 / fwd_s, unit="tok/s", cores=1, kind="port",
                 sample=f"1 decode-token forward (position 0) of the full TinyLlama-shape Q4_0 model, "
                        f"f16 accumulation as matmul_cpu; {fwd_s:.1f} s/token, weights dequantised "
-                       f"to f16 at load ({load_s:.1f} s, not timed)")
+                       f"to f16 at load ({load_s:.1f} s, not timed)",
+                host=dict(cpu=cpu_name, nproc=nproc, affinity=affinity),
+                omp=dict(threads=omp_threads, tok_s=round(1.0 / fwd_omp_s, 4), ops=r(opsn)),
+                ops_1_thread=r(ops1))
 
 
 def main():
@@ -350,9 +415,11 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        log("CPU baseline (oracle, reference CPU arithmetic, 1 thread) ...")
-        cpu = cpu_baseline(path, prompt)
-        log(f"CPU baseline: {cpu['value']:.4f} tok/s")
+        omp_threads = min(16, len(os.sched_getaffinity(0)))
+        log(f"CPU baseline (oracle, reference CPU arithmetic, 1 and {omp_threads} threads) ...")
+        cpu = cpu_baseline(path, prompt, omp_threads)
+        log(f"CPU baseline: {cpu['value']:.4f} tok/s (1 thread), {cpu['omp']['tok_s']:.4f} tok/s "
+            f"({omp_threads} threads)")
     if not args.model:
         try:
             os.remove(path)

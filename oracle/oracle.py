@@ -47,6 +47,7 @@ _i32p = C.POINTER(C.c_int32)
 def _declare(L):
     sz, i, f, vp = C.c_size_t, C.c_int, C.c_float, C.c_void_p
     sig = {
+        "tlo_set_threads": (i, [i]),
         "tlo_h2f": (f, [C.c_uint16]),
         "tlo_f2h": (C.c_uint16, [f]),
         "tlo_h2f_array": (None, [vp, vp, sz]),
@@ -107,6 +108,12 @@ def f2h(x: np.ndarray) -> np.ndarray:
     out = np.empty(x.shape, np.uint16)
     lib().tlo_f2h_array(_p(x), _p(out), x.size)
     return out
+
+
+def set_threads(n: int) -> int:
+    """OpenMP threads for the oracle's loops (n <= 0: unchanged); returns the
+    count in force."""
+    return lib().tlo_set_threads(n)
 
 
 def dequant(blocks: np.ndarray, gtype: int) -> np.ndarray:

@@ -780,6 +780,16 @@ static int load_lin(const tlo_gguf* g, const char* name, const char* bname, int 
 
 static void free_lin(lin_t* l) { free(l->w); free(l->b); }
 
+int tlo_set_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+    return omp_get_max_threads();
+#else
+    (void)n;
+    return 1;
+#endif
+}
+
 tlo_model* tlo_model_load(const char* path, int arch, int max_ctx, int acc_mode, int n_threads) {
     lut_init();
 #ifdef _OPENMP

@@ -33,6 +33,10 @@ extern "C" {
 enum { TLO_ACC_F32 = 0, TLO_ACC_F16 = 1 };
 enum { TLO_ROPE_INTERLEAVED = 0, TLO_ROPE_NEOX = 1 };
 
+/* Number of OpenMP threads used by the loops below (the calling thread's
+ * setting; n <= 0 leaves it unchanged).  Returns the count now in force. */
+int      tlo_set_threads(int n);
+
 /* ---- binary16 <-> binary32 (the `half` 2.7.1 crate's from_f32/to_f32:
  *      RNE, subnormals kept, NaN kept quiet) --------------------------------*/
 float    tlo_h2f(uint16_t h);
