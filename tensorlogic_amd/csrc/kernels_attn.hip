@@ -96,30 +96,6 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, int J_fixed)
     }
 }
 
-// Workgroup max / sum over NWV waves in a fixed order.
-template <int NWV>
-__device__ __forceinline__ float block_max(float v, float* red) {
-    v = wave_max(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float t = red[0];
-#pragma unroll
-    for (int k = 1; k < NWV; k++) t = fmaxf(t, red[k]);
-    return t;
-}
-template <int NWV>
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    v = wave_sum<64>(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float t = red[0];
-#pragma unroll
-    for (int k = 1; k < NWV; k++) t += red[k];
-    return t;
-}
-
 // Head-dim-64 variant with the same arithmetic and storage points, laid out
 // for the memory system: a key is read by 8 lanes with one 16-byte load each
 // (a head's 128-byte K/V row in one coalesced access), 32 keys per pass, and

@@ -956,7 +956,7 @@ int gemv_norm_slots(int N) {
     return (N + 7) / 8;
 }
 
-tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi) {
+static GemvParams make_params(const GemvArgs& a, int epi) {
     GemvParams p = {};
     p.x = a.x;
     p.wq = (const uint8_t*)a.wq;
@@ -987,6 +987,11 @@ tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
     p.d_token = a.d_token;
     p.x_out = a.x_out;
     p.amax_slots = a.amax_slots;
+    return p;
+}
+
+tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi) {
+    const GemvParams p = make_params(a, epi);
     if (p.N <= 0 || p.M <= 0) return TLHIP_OK;
     const bool pair_epi = epi == EPI_SWIGLU_PAIR || epi == EPI_QKV_ROPE;
     if (pair_epi && (p.N % 2))
