@@ -735,20 +735,58 @@ __device__ __forceinline__ unsigned long long amax_key(uint16_t h, int idx) {
 __device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
 
 // NB: blocks per lane (ceil(K/32/64)); RI: rows per wave; MX: max activation
-// rows.  Activation chunks are loaded by every wave from global memory (L2).
+// rows.  M = 1: the workgroup stages the activation row once in LDS, in the
+// pair order of the unpacking (the layout of gemv_norm_kernel's staging,
+// without the normalisation), from loads issued before the weight rows --
+// vector loads retire in order, so the staging completes while the weights
+// are still in flight, and the row crosses the L2 -> CU path once per
+// workgroup instead of once per wave.  M > 1: every wave loads its
+// activation chunks from global memory (L2).
 template <int WT, int NB, int RI, int MX>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
+    __shared__ u4 xs[4][MX == 1 ? NB * 64 : 1];
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int row0 = wave * RI;
-    if (row0 >= p.N) return;
+    const bool active = row0 < p.N;   // (only the last workgroup has idle waves)
     const int nbr = p.K >> 5;
     constexpr int NL = BlkLoads<WT>::n;
+    uint32_t xw[MX == 1 ? NB : 1][4];
+    if constexpr (MX == 1) {
+        const int items = nbr * 4;
+#pragma unroll
+        for (int k = 0; k < NB; k++) {   // (clamped, unconditional: see load_rows below)
+            const int it = min((int)threadIdx.x + 256 * k, items - 1);
+            NormStage<WT, NB, 4, PRO_NONE>::load_words(p.x, it >> 2, it & 3, xw[k]);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // keep them ahead of the weight loads
+    } else if (!active) {
+        return;
+    }
+    // (unconditional: load_rows clamps rows into the matrix, and a load under
+    // a branch would make the staging below wait for every load)
     u4 q[RI][NB][NL];
     uint32_t ds[RI][NB];   // scales zero-extended: no packing that would force an early wait
     load_rows<WT, NB, RI>(p, row0, lane, q, ds);
     EpiPre<RI, MX> pre;
-    if (lane == 0) epi_preload<RI, MX>(p, row0, pre);
+    if constexpr (MX != 1) {
+        if (lane == 0) epi_preload<RI, MX>(p, row0, pre);
+    } else {
+        const int items = nbr * 4;
+#pragma unroll
+        for (int k = 0; k < NB; k++) {
+            const int it = threadIdx.x + 256 * k;
+            if (it < items) {
+                const uint32_t* w = xw[k];
+                xs[it & 3][it >> 2] = WT == TLHIP_F16 ? u4{w[0], w[1], w[2], w[3]}
+                                                      : u4{pack_lo(w[0], w[1]), pack_hi(w[0], w[1]),
+                                                           pack_lo(w[2], w[3]), pack_hi(w[2], w[3])};
+            }
+        }
+        if (lane == 0 && active) epi_preload<RI, MX>(p, row0, pre);
+        lds_barrier();
+        if (!active) return;
+    }
 
     float acc[RI][MX];
 #pragma unroll
@@ -763,7 +801,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
             for (int m = 0; m < MX; m++) {
                 if (m < p.M) {
                     uint32_t xc[16];
-                    load_xchunk<WT>(p.x + (size_t)m * p.K + (size_t)b * 32, xc);
+                    if constexpr (MX == 1) {
+#pragma unroll
+                        for (int v = 0; v < 4; v++) {
+                            const u4 t = xs[v][b];
+                            xc[4 * v] = t[0]; xc[4 * v + 1] = t[1]; xc[4 * v + 2] = t[2]; xc[4 * v + 3] = t[3];
+                        }
+                    } else {
+                        load_xchunk<WT>(p.x + (size_t)m * p.K + (size_t)b * 32, xc);
+                    }
 #pragma unroll
                     for (int ri = 0; ri < RI; ri++) acc[ri][m] = block_dot<WT>(q[ri][i], ds[ri][i], xc, acc[ri][m]);
                 }
