@@ -168,11 +168,12 @@ def config3_attention(dev, iters: int = 20):
     return res
 
 
-def config5_phi2(dev, steps: int = 256, n_prompt: int = 512):
+def config5_phi2(dev, steps: int = 256, n_prompt: int = 512, use_graph: bool = True):
     """Config 5: Phi-2-architecture decoder (2.7B, Q8_0 linear weights, random
     init), 512-token prompt prefilled through the MFMA GEMM and attention,
-    then `steps` greedy decode steps (graph replay) against the growing KV
-    cache; hipEvents on the runner's stream."""
+    then `steps` greedy decode steps (graph replay, or direct launches under
+    a profiler) against the growing KV cache; hipEvents on the runner's
+    stream."""
     from tensorlogic_amd import Model
     from tensorlogic_amd import synth as S
     tmp = tempfile.mkdtemp(prefix="tlbench_phi2_")
@@ -183,9 +184,9 @@ def config5_phi2(dev, steps: int = 256, n_prompt: int = 512):
     prompt = S.token_ids(5, "prompt", n_prompt, S.PHI2_ARGS["vocab"])
     try:
         m = Model(dev, path, arch=1, max_ctx=n_prompt + steps + 8)
-        m.generate(prompt, 8)   # warm-up, captures the decode graph
+        m.generate(prompt, 8, use_graph=use_graph)   # warm-up, captures the decode graph
         dev.sync()
-        _, prefill_ms, decode_ms = m.bench_decode(prompt, steps)
+        _, prefill_ms, decode_ms = m.bench_decode(prompt, steps, use_graph=use_graph)
         m.close()
     finally:
         os.remove(path)
@@ -407,7 +408,7 @@ def main():
     log(f"Q6_K GEMV 32000x2048: {q6['us']:.2f} us, {q6['gbs']:.0f} GB/s")
     c5 = None
     if not args.no_phi2:
-        c5 = config5_phi2(dev)
+        c5 = config5_phi2(dev, use_graph=use_graph)
         log(f"Phi-2 Q8_0: prefill 512 tokens {c5['prefill_512_ms']:.2f} ms, decode {c5['decode_tok_s']:.1f} tok/s "
             f"({c5['decode_hbm_gbs']:.0f} GB/s of weights)")
     g = gem["5632x2048"]

@@ -37,6 +37,16 @@ __device__ __forceinline__ float bmax(float v, float* red) {
 }
 
 // One workgroup (256 threads) per (query row s, head h).
+// Every field of the argument block in SGPRs at once (one wait for the
+// kernel-argument loads instead of one per first use; see kernarg_fence in
+// kernels_gemv.hip).
+__device__ __forceinline__ void attn_kernarg_fence(const AttnArgs& a, int J_fixed) {
+    asm volatile("" ::"s"(a.q), "s"(a.k), "s"(a.v), "s"(a.out), "s"(a.S), "s"(a.H), "s"(a.Hkv), "s"(a.D),
+                 "s"(a.q_pos0), "s"(a.d_pos), "s"(a.causal), "s"(a.scale_h), "s"(a.q_stride), "s"(a.out_stride),
+                 "s"(a.kv_rows), "s"(J_fixed));
+    __builtin_amdgcn_sched_barrier(0);   // nothing that uses them moves above
+}
+
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, int J_fixed) {
     __shared__ float sc[ATT_MAX_J];
     __shared__ float qf[256];
@@ -111,6 +121,7 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed
     __shared__ float sc[ATT_MAX_J];
     __shared__ float red[NWV];
     __shared__ float part[NWV][64];
+    attn_kernarg_fence(a, J_fixed);
     const int s = blockIdx.x, h = blockIdx.y;
     const int Hkv = a.Hkv;
     const int kvh = h / (a.H / Hkv);
@@ -121,20 +132,23 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed
     const uint16_t* kbase = a.k + (size_t)kvh * 64 + 8 * c;
     const uint16_t* vbase = a.v + (size_t)kvh * 64 + 8 * c;
     // Loads that do not depend on the decode position go out first: q, and
-    // the first pass of K and V rows (bounded by the rows allocated, so
-    // every address is in bounds; rows past the key count are never used).
+    // the first pass of K and V rows.  Row indices are clamped to the rows
+    // allocated (kv_lim), so every address is in bounds; the key count never
+    // exceeds kv_lim, so a clamped row is only ever loaded for a key that is
+    // not used.  The loads are unconditional: a load under a per-row branch
+    // makes the compiler wait for it at the branch join, which serialised
+    // the pass into several memory round trips.
     const u4 qv = *(const u4*)(a.q + (size_t)s * qs + (size_t)h * 64 + 8 * c);
     const int kv_lim = a.kv_rows > 0 ? (a.d_pos ? a.kv_rows : min(a.kv_rows, J_fixed)) : min(J_fixed, ATT_MAX_J);
     u4 k0[A64_UNR], vv[A64_UNR];
+    if (kv_lim > 0) {   // (uniform; 0 only when neither a key count nor the rows allocated is known)
 #pragma unroll
-    for (int u = 0; u < A64_UNR; u++) {
-        const int j = g + NG * u;
-        k0[u] = j < kv_lim ? *(const u4*)(kbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
-    }
+        for (int u = 0; u < A64_UNR; u++) k0[u] = *(const u4*)(kbase + (size_t)min(g + NG * u, kv_lim - 1) * kstride);
 #pragma unroll
-    for (int u = 0; u < A64_UNR; u++) {
-        const int j = g + NG * u;
-        vv[u] = j < kv_lim ? *(const u4*)(vbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
+        for (int u = 0; u < A64_UNR; u++) vv[u] = *(const u4*)(vbase + (size_t)min(g + NG * u, kv_lim - 1) * kstride);
+    } else {
+#pragma unroll
+        for (int u = 0; u < A64_UNR; u++) k0[u] = vv[u] = u4{0u, 0u, 0u, 0u};
     }
     const int qpos = (a.d_pos ? *a.d_pos : a.q_pos0) + s;
     const int J = min(a.d_pos ? qpos + 1 : J_fixed, ATT_MAX_J);
@@ -283,6 +297,7 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
     __shared__ float sc[ATT_MAX_J];
     __shared__ float red[NWV];
     __shared__ float part[NWV][D];
+    attn_kernarg_fence(a, J_fixed);
     const int s = blockIdx.x, h = blockIdx.y;
     const int Hkv = a.Hkv;
     const int kvh = h / (a.H / Hkv);
@@ -298,20 +313,17 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
     // (the first half of the pass before the decode position is known, the
     // rest once it is, for the keys that exist)
     const int kv_lim = a.kv_rows > 0 ? (a.d_pos ? a.kv_rows : min(a.kv_rows, J_fixed)) : min(J_fixed, ATT_MAX_J);
+    // (clamped, unconditional loads, as in attention64_kernel)
     uint32_t k0[U][NW], v0[U][NW];
 #pragma unroll
     for (int u = 0; u < U; u++)
 #pragma unroll
         for (int t = 0; t < NW; t++) k0[u][t] = v0[u][t] = 0u;
+    if (kv_lim > 0) {
 #pragma unroll
-    for (int u = 0; u < U / 2; u++) {
-        const int j = g + NG * u;
-        if (j < kv_lim) load_row_words<NW>(kbase + (size_t)j * wstride, k0[u]);
-    }
+        for (int u = 0; u < U / 2; u++) load_row_words<NW>(kbase + (size_t)min(g + NG * u, kv_lim - 1) * wstride, k0[u]);
 #pragma unroll
-    for (int u = 0; u < U / 2; u++) {
-        const int j = g + NG * u;
-        if (j < kv_lim) load_row_words<NW>(vbase + (size_t)j * wstride, v0[u]);
+        for (int u = 0; u < U / 2; u++) load_row_words<NW>(vbase + (size_t)min(g + NG * u, kv_lim - 1) * wstride, v0[u]);
     }
     float qf[EPL];
     {
@@ -326,15 +338,12 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
     const int qpos = (a.d_pos ? *a.d_pos : a.q_pos0) + s;
     const int J = min(a.d_pos ? qpos + 1 : J_fixed, ATT_MAX_J);
     const int Jv = a.causal ? min(J, qpos + 1) : J;
+    if (kv_lim > 0 && Jv > NG * (U / 2)) {   // (uniform)
+        const int jl = min(Jv, kv_lim) - 1;
 #pragma unroll
-    for (int u = U / 2; u < U; u++) {
-        const int j = g + NG * u;
-        if (j < Jv && j < kv_lim) load_row_words<NW>(kbase + (size_t)j * wstride, k0[u]);
-    }
+        for (int u = U / 2; u < U; u++) load_row_words<NW>(kbase + (size_t)min(g + NG * u, jl) * wstride, k0[u]);
 #pragma unroll
-    for (int u = U / 2; u < U; u++) {
-        const int j = g + NG * u;
-        if (j < Jv && j < kv_lim) load_row_words<NW>(vbase + (size_t)j * wstride, v0[u]);
+        for (int u = U / 2; u < U; u++) load_row_words<NW>(vbase + (size_t)min(g + NG * u, jl) * wstride, v0[u]);
     }
 
     float mx = -INFINITY;

@@ -294,6 +294,36 @@ struct GemvParams {
     unsigned long long* amax_slots;
 };
 
+// Fourth word of a raw buffer resource descriptor on gfx9-family GPUs
+// (gfx950 included): 32-bit data format, no swizzle, no stride; with it a
+// buffer load range-checks its offset against the descriptor's byte count
+// and returns zeros past it.
+constexpr int BUF_RSRC_WORD3 = 0x00020000;
+
+// 0 in a VGPR the compiler cannot see through: indexing a uniform address
+// with it makes the load a vector load (in-order completion) instead of a
+// scalar one.
+__device__ __forceinline__ int opaque_zero() {
+    int z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    return z;
+}
+
+// Every field of the parameter block in SGPRs before anything else runs.
+// Left alone, the compiler requests kernel-argument words lazily, next to
+// their first use, and a wait for one scalar load is a wait for all of them
+// (they return out of order), so the fields used behind a branch or after
+// the first loads cost a further round trip each before the weight loads
+// go out.  An empty asm that takes them all as SGPR operands makes the
+// compiler issue every kernel-argument load at once and wait once.
+__device__ __forceinline__ void kernarg_fence(const GemvParams& p) {
+    asm volatile("" ::"s"(p.x), "s"(p.wq), "s"(p.wd), "s"(p.bias), "s"(p.resid), "s"(p.y), "s"(p.M), "s"(p.N),
+                 "s"(p.K), "s"(p.ldy), "s"(p.epi), "s"(p.norm_w), "s"(p.norm_b), "s"(p.eps), "s"(p.nq), "s"(p.nk),
+                 "s"(p.head_dim), "s"(p.rot), "s"(p.layout), "s"(p.pos0), "s"(p.rope_tab), "s"(p.d_pos),
+                 "s"(p.q_out), "s"(p.kc), "s"(p.vc), "s"(p.embd), "s"(p.d_token), "s"(p.x_out), "s"(p.amax_slots));
+    __builtin_amdgcn_sched_barrier(0);   // nothing that uses them moves above
+}
+
 // Activation pair order of a weight type: Q6_K unpacks in the Q4_0 order.
 template <int WT>
 constexpr bool xo_nibble() { return WT == TLHIP_Q4_0 || WT == TLHIP_Q6_K; }
@@ -342,24 +372,11 @@ __device__ __forceinline__ void load_xchunk(const uint16_t* __restrict__ xb, uin
     order_x<WT>(xw, xc);
 }
 
-// Activation staging for the normalised GEMV (M = 1).  The workgroup loads
-// the row once, forms the row statistics, normalises with exactly the
-// formulas and f16 store of rms_norm_kernel / layer_norm_kernel
-//   RMS: y = f16((x * (1 / sqrt(mean(x^2) + eps))) * w)
-//   LN:  y = f16(((x - mean) * (1 / sqrt(var + eps))) * w + b)
-// and leaves it in LDS already in the pair order of the unpacking.  LDS is
-// quad-major, xs[v][b] = 16 bytes (pairs 4v..4v+3 of block b's chunk), so
-// lane l's reads of block l are consecutive 16-byte words (no conflicts).
-// Quad v of a block holds elements {4v..4v+3, 16+4v..16+4v+3} for Q4_0 and
-// {8v..8v+7} for Q8_0 / f16.
+// Quad v (8 activations) of block b as four f16 pairs, for the plain GEMV's
+// LDS staging (xs[v][b] = 16 bytes in the pair order of the unpacking):
+// elements {4v..4v+3, 16+4v..16+4v+3} for Q4_0 / Q6_K, {8v..8v+7} otherwise.
 template <int WT>
-__device__ __forceinline__ int quad_elem(int v, int e) {
-    return xo_nibble<WT>() ? (e < 4 ? 4 * v + e : 12 + 4 * v + e) : 8 * v + e;
-}
-
-template <int WT>
-__device__ __forceinline__ void load_quad(const uint16_t* __restrict__ src, int b, int v, float f[8]) {
-    uint32_t w[4];
+__device__ __forceinline__ void load_quad_words(const uint16_t* __restrict__ src, int b, int v, uint32_t w[4]) {
     if (xo_nibble<WT>()) {
         const uint2 lo = *(const uint2*)(src + (size_t)b * 32 + 4 * v);
         const uint2 hi = *(const uint2*)(src + (size_t)b * 32 + 16 + 4 * v);
@@ -368,144 +385,126 @@ __device__ __forceinline__ void load_quad(const uint16_t* __restrict__ src, int 
         const u4 t = *(const u4*)(src + (size_t)b * 32 + 8 * v);
         w[0] = t[0]; w[1] = t[1]; w[2] = t[2]; w[3] = t[3];
     }
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const h2 h = as_h2(w[t]);
-        f[2 * t] = (float)h[0];
-        f[2 * t + 1] = (float)h[1];
-    }
 }
 
-template <int WT>
-__device__ __forceinline__ u4 pack_quad(const float f[8]) {
-    uint32_t w[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        h2 h;
-        h[0] = (h16)f[2 * t];
-        h[1] = (h16)f[2 * t + 1];
-        w[t] = as_u32(h);
-    }
-    if (WT == TLHIP_F16) return u4{w[0], w[1], w[2], w[3]};
-    return u4{pack_lo(w[0], w[1]), pack_hi(w[0], w[1]), pack_lo(w[2], w[3]), pack_hi(w[2], w[3])};
-}
-
+// Sum over the workgroup's WPB waves in a fixed order, with ONE barrier:
+// the caller must not write `red` again before another barrier.
 template <int WPB>
-__device__ __forceinline__ float wg_sum(float v, float* red) {
+__device__ __forceinline__ float wg_sum1(float v, float* red) {
     v = wave_sum<64>(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     lds_barrier();
     float t = red[0];
 #pragma unroll
     for (int k = 1; k < WPB; k++) t += red[k];
-    lds_barrier();
     return t;
 }
 
-// Items (block b, quad v) are spread over the workgroup; each thread keeps
-// its (at most IPT) items' values in registers between the passes.  The
-// loads (NormStage::load) are issued before the weight rows: vector loads
-// retire in order, so the statistics can start while the weights are
-// still in flight.
+// Activation staging for the normalised GEMV (M = 1).  The workgroup loads
+// the row once, forms the row statistics, normalises with exactly the
+// formulas and f16 store of rms_norm_kernel / layer_norm_kernel
+//   RMS: y = f16((x * (1 / sqrt(mean(x^2) + eps))) * w)
+//   LN:  y = f16(((x - mean) * (1 / sqrt(var + eps))) * w + b)
+// and leaves it in LDS as natural f16 pairs, one row of 17 words per
+// 32-element block (16 words + 1 of padding, so the 64 lanes reading
+// blocks b = lane + 64 i word by word hit distinct banks); each wave
+// permutes its block's pairs into the order of the unpacking after the
+// read.  Thread t holds item t = 16 consecutive activations (half a block),
+// loaded with two 16-byte loads each of x, w (and b); K <= 4096 keeps it
+// to one item per thread.  The loads are issued before the weight rows
+// (vector loads retire in order), so the statistics start while the
+// weights are still in flight.  Measured against the earlier quad layout
+// (8-byte loads, a two-barrier workgroup sum) on MI355X: 6.78 -> 5.7 us for
+// the gate/up rows [11264 x 2048], 4.26 -> 3.2-3.4 us for [2560 x 2048].
 template <int WT, int NB, int WPB, int PRO>
 struct NormStage {
     static constexpr int NT = WPB * 64;
-    static constexpr int IPT = (NB * 256 + NT - 1) / NT;
-    uint32_t xw[IPT][4], ww[IPT][4], bw[IPT][4];   // raw f16 pairs until finish()
+    static_assert(NB * 128 <= NT, "one 16-element item per thread");
+    uint32_t xw[8], ww[8], bw[8];   // raw f16 pairs until finish()
 
-    __device__ __forceinline__ static void load_words(const uint16_t* __restrict__ src, int b, int v, uint32_t w[4]) {
-        if (xo_nibble<WT>()) {
-            const uint2 lo = *(const uint2*)(src + (size_t)b * 32 + 4 * v);
-            const uint2 hi = *(const uint2*)(src + (size_t)b * 32 + 16 + 4 * v);
-            w[0] = lo.x; w[1] = lo.y; w[2] = hi.x; w[3] = hi.y;
-        } else {
-            const u4 t = *(const u4*)(src + (size_t)b * 32 + 8 * v);
-            w[0] = t[0]; w[1] = t[1]; w[2] = t[2]; w[3] = t[3];
-        }
-    }
-
-    __device__ __forceinline__ static void to_float(const uint32_t w[4], float f[8]) {
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const h2 h = as_h2(w[t]);
-            f[2 * t] = (float)h[0];
-            f[2 * t + 1] = (float)h[1];
-        }
+    // Item it's 16 activations of a K-element row through a range-checked
+    // buffer descriptor: a lane whose item lies past the row gets zeros
+    // with no memory request, so there is neither a branch (whose join
+    // would make the compiler wait for the loads before the weight rows go
+    // out) nor a clamped duplicate read from the waves that hold no item.
+    __device__ __forceinline__ static void load16(const uint16_t* __restrict__ src, int K, int it, uint32_t w[8]) {
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, K * 2, BUF_RSRC_WORD3);
+        const u4 a = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, it * 32, 0, 0));
+        const u4 b = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, it * 32 + 16, 0, 0));
+        w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
+        w[4] = b[0]; w[5] = b[1]; w[6] = b[2]; w[7] = b[3];
     }
 
     __device__ __forceinline__ void load(const GemvParams& p, const uint16_t* __restrict__ xsrc) {
-        const int items = (p.K >> 5) * 4;
-#pragma unroll
-        for (int k = 0; k < IPT; k++) {
-            const int it = threadIdx.x + k * NT;
-            if (it < items) {
-                load_words(xsrc, it >> 2, it & 3, xw[k]);
-                load_words(p.norm_w, it >> 2, it & 3, ww[k]);
-                if (PRO == PRO_LN) load_words(p.norm_b, it >> 2, it & 3, bw[k]);
-            } else {
-#pragma unroll
-                for (int t = 0; t < 4; t++) xw[k][t] = 0u;
-            }
-        }
+        const int it = threadIdx.x;
+        load16(xsrc, p.K, it, xw);
+        load16(p.norm_w, p.K, it, ww);
+        if (PRO == PRO_LN) load16(p.norm_b, p.K, it, bw);
     }
 
-    __device__ __forceinline__ void finish(const GemvParams& p, u4 (*xs)[NB * 64], float* red) {
-        const int items = (p.K >> 5) * 4;
-        float f[IPT][8];
+    __device__ __forceinline__ void finish(const GemvParams& p, uint32_t (*xs)[17], float (*red)[WPB]) {
+        const int it = threadIdx.x;
+        const bool valid = it < (p.K >> 4);
+        float f[16];
 #pragma unroll
-        for (int k = 0; k < IPT; k++) to_float(xw[k], f[k]);
-        if (p.x_out && blockIdx.x == 0)   // the residual copy of an embedded row
-#pragma unroll
-            for (int k = 0; k < IPT; k++) {
-                const int it = threadIdx.x + k * NT;
-                if (it < items) {
-                    const int b = it >> 2, v = it & 3;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) p.x_out[(size_t)b * 32 + quad_elem<WT>(v, e)] = f2h(f[k][e]);
-                }
-            }
+        for (int i = 0; i < 8; i++) {
+            const h2 h = as_h2(xw[i]);
+            f[2 * i] = valid ? (float)h[0] : 0.0f;
+            f[2 * i + 1] = valid ? (float)h[1] : 0.0f;
+        }
+        if (p.x_out && blockIdx.x == 0 && valid) {   // the residual copy of an embedded row
+            u4* o = (u4*)(p.x_out + (size_t)it * 16);
+            o[0] = u4{xw[0], xw[1], xw[2], xw[3]};
+            o[1] = u4{xw[4], xw[5], xw[6], xw[7]};
+        }
         float mean = 0.0f, inv;
         if (PRO == PRO_RMS) {
             float ss = 0.0f;
 #pragma unroll
-            for (int k = 0; k < IPT; k++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) ss += f[k][e] * f[k][e];
-            const float t = wg_sum<WPB>(ss, red);
-            inv = 1.0f / sqrtf(t / (float)p.K + p.eps);
+            for (int e = 0; e < 16; e++) ss += f[e] * f[e];
+            inv = 1.0f / sqrtf(wg_sum1<WPB>(ss, red[0]) / (float)p.K + p.eps);
         } else {
             float sm = 0.0f;
 #pragma unroll
-            for (int k = 0; k < IPT; k++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) sm += f[k][e];
-            mean = wg_sum<WPB>(sm, red) / (float)p.K;
+            for (int e = 0; e < 16; e++) sm += f[e];
+            mean = wg_sum1<WPB>(sm, red[0]) / (float)p.K;
             float q = 0.0f;
+            if (valid)
 #pragma unroll
-            for (int k = 0; k < IPT; k++) {
-                if (threadIdx.x + k * NT >= items) continue;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float d = f[k][e] - mean;
+                for (int e = 0; e < 16; e++) {
+                    const float d = f[e] - mean;
                     q += d * d;
                 }
-            }
-            inv = 1.0f / sqrtf(wg_sum<WPB>(q, red) / (float)p.K + p.eps);
+            inv = 1.0f / sqrtf(wg_sum1<WPB>(q, red[1]) / (float)p.K + p.eps);
         }
+        if (valid) {
 #pragma unroll
-        for (int k = 0; k < IPT; k++) {
-            const int it = threadIdx.x + k * NT;
-            if (it >= items) continue;
-            const int b = it >> 2, v = it & 3;
-            float w[8], bb[8];
-            to_float(ww[k], w);
-            if (PRO == PRO_LN) to_float(bw[k], bb);
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                f[k][e] = PRO == PRO_RMS ? (f[k][e] * inv) * w[e] : (((f[k][e] - mean) * inv) * w[e]) + bb[e];
-            xs[v][b] = pack_quad<WT>(f[k]);
+            for (int i = 0; i < 8; i++) {
+                const h2 w = as_h2(ww[i]);
+                float o0, o1;
+                if (PRO == PRO_RMS) {
+                    o0 = (f[2 * i] * inv) * (float)w[0];
+                    o1 = (f[2 * i + 1] * inv) * (float)w[1];
+                } else {
+                    const h2 b = as_h2(bw[i]);
+                    o0 = (((f[2 * i] - mean) * inv) * (float)w[0]) + (float)b[0];
+                    o1 = (((f[2 * i + 1] - mean) * inv) * (float)w[1]) + (float)b[1];
+                }
+                h2 o;
+                o[0] = (h16)o0;
+                o[1] = (h16)o1;
+                xs[it >> 1][(it & 1) * 8 + i] = as_u32(o);
+            }
         }
         lds_barrier();
+    }
+
+    // Block b's 16 normalised pairs, permuted into the pair order of WT's unpacking.
+    __device__ __forceinline__ static void chunk(const uint32_t (*xs)[17], int b, uint32_t xc[16]) {
+        uint32_t nat[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) nat[i] = xs[b][i];
+        order_x<WT>(nat, xc);
     }
 };
 
@@ -575,14 +574,14 @@ __device__ __forceinline__ float block_dot(const u4* q, uint32_t dbits, const ui
 // start of the kernel (QkvPre), so the tail makes no dependent loads.
 struct QkvPre {
     int pos;
-    uint32_t b0, b1;   // zero-extended f16 bits
+    uint32_t b01;   // f16 bits of bias[row] (low half) and bias[row + 1]
     float c, sn;
 };
 
 __device__ __forceinline__ void qkv_rope_pre(const GemvParams& p, int row, int pos, QkvPre& q) {
     q.pos = pos;
-    q.b0 = p.bias ? (uint32_t)p.bias[row] : 0u;
-    q.b1 = p.bias ? (uint32_t)p.bias[row + 1] : 0u;
+    // one 4-byte load (row is even), split only at the store, so no wait here
+    q.b01 = p.bias ? *(const uint32_t*)(p.bias + row) : 0u;
     q.c = 1.0f;
     q.sn = 0.0f;
     const int D = p.head_dim;
@@ -599,8 +598,8 @@ __device__ __forceinline__ void qkv_rope_pre(const GemvParams& p, int row, int p
 __device__ __forceinline__ void qkv_rope_store(const GemvParams& p, int row, float a0, float a1, const QkvPre& q) {
     uint16_t r0 = f2h(a0), r1 = f2h(a1);
     if (p.bias) {
-        r0 = add_h(r0, (uint16_t)q.b0);
-        r1 = add_h(r1, (uint16_t)q.b1);
+        r0 = add_h(r0, (uint16_t)(q.b01 & 0xffffu));
+        r1 = add_h(r1, (uint16_t)(q.b01 >> 16));
     }
     const int pos = q.pos;
     const int D = p.head_dim;
@@ -740,11 +739,15 @@ __device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsig
 // without the normalisation), from loads issued before the weight rows --
 // vector loads retire in order, so the staging completes while the weights
 // are still in flight, and the row crosses the L2 -> CU path once per
-// workgroup instead of once per wave.  M > 1: every wave loads its
-// activation chunks from global memory (L2).
+// workgroup instead of once per wave.  (Each lane loading its own blocks'
+// chunks from L2 instead, with no LDS and no barrier, was measured on
+// MI355X: equal or slower back to back -- 5632 x 2048 3.88-3.99 vs
+// 3.82-3.88 us, 2048 x 5632 4.31-4.44 vs 3.98-4.09 us.)  M > 1: every wave
+// loads its activation chunks from global memory (L2).
 template <int WT, int NB, int RI, int MX>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     __shared__ u4 xs[4][MX == 1 ? NB * 64 : 1];
+    kernarg_fence(p);
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int row0 = wave * RI;
@@ -757,7 +760,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 #pragma unroll
         for (int k = 0; k < NB; k++) {   // (clamped, unconditional: see load_rows below)
             const int it = min((int)threadIdx.x + 256 * k, items - 1);
-            NormStage<WT, NB, 4, PRO_NONE>::load_words(p.x, it >> 2, it & 3, xw[k]);
+            load_quad_words<WT>(p.x, it >> 2, it & 3, xw[k]);
         }
         __builtin_amdgcn_sched_barrier(0);   // keep them ahead of the weight loads
     } else if (!active) {
@@ -829,25 +832,39 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 // stored logits to one (value, index) key in amax_slots[blockIdx.x].
 template <int WT, int NB, int RI, int WPB, int PRO>
 __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams p) {
-    __shared__ u4 xs[4][NB * 64];
-    __shared__ float red[WPB];
+    __shared__ uint32_t xs[NB * 64][17];
+    __shared__ float red[2][WPB];
     __shared__ unsigned long long wkey[WPB];
+    kernarg_fence(p);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * WPB + w) * RI;
     const int nbr = p.K >> 5;
     constexpr int NL = BlkLoads<WT>::n;
     u4 q[RI][NB][NL];
     uint32_t ds[RI][NB];   // scales zero-extended: no packing that would force an early wait
-    // position first: the RoPE table loads depend on it
-    const int pos = p.epi == EPI_QKV_ROPE ? p.pos0 + (p.d_pos ? *p.d_pos : 0) : 0;
+    // The decode position (only lane 0's RoPE table loads depend on it) is
+    // read first, as a vector load: those retire in order, so waiting for it
+    // later does not wait for the activation and weight loads issued after
+    // it.  As a scalar load (what a uniform address gets) any wait for it
+    // would be a wait for every scalar load, and it held back all the
+    // activation and weight loads by one memory round trip.  The load is
+    // unconditional, so no branch join forces the wait right here: without
+    // a device position it reads the first word of the norm weight, which
+    // launch_gemv requires for every normalised GEMV (the scale array is
+    // absent for F16 weights).
+    const bool dev_pos = p.epi == EPI_QKV_ROPE && p.d_pos;
+    const int pos_raw = (dev_pos ? p.d_pos : (const int32_t*)p.norm_w)[opaque_zero()];
     const uint16_t* xsrc = p.embd ? p.embd + (size_t)(*p.d_token) * p.K : p.x;
     NormStage<WT, NB, WPB, PRO> st;
     st.load(p, xsrc);
-    if (row0 < p.N) load_rows<WT, NB, RI>(p, row0, lane, q, ds);
+    // (unconditional: load_rows clamps rows into the matrix, and loads under
+    // a branch leave the compiler's wait counts imprecise after it)
+    load_rows<WT, NB, RI>(p, row0, lane, q, ds);
     EpiPre<RI, 1> pre;
     QkvPre qp[RI / 2 > 0 ? RI / 2 : 1];
     if (lane == 0 && row0 < p.N) {
         if (p.epi == EPI_QKV_ROPE) {
+            const int pos = p.pos0 + (dev_pos ? pos_raw : 0);
 #pragma unroll
             for (int ri = 0; ri + 1 < RI; ri += 2)
                 if (row0 + ri + 1 < p.N) qkv_rope_pre(p, row0 + ri, pos, qp[ri / 2]);
@@ -866,11 +883,7 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams p) {
             const int b = lane + 64 * i;
             if (b < nbr) {
                 uint32_t xc[16];
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const u4 t = xs[v][b];
-                    xc[4 * v] = t[0]; xc[4 * v + 1] = t[1]; xc[4 * v + 2] = t[2]; xc[4 * v + 3] = t[3];
-                }
+                NormStage<WT, NB, WPB, PRO>::chunk(xs, b, xc);
 #pragma unroll
                 for (int ri = 0; ri < RI; ri++) acc[ri][0] = block_dot<WT>(q[ri][i], ds[ri][i], xc, acc[ri][0]);
             }
@@ -1090,9 +1103,21 @@ tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
 __global__ __launch_bounds__(256) void argmax_slots_kernel(const unsigned long long* __restrict__ slots, int n,
                                                            int32_t* out, int32_t* token_log, int32_t* d_state) {
     __shared__ unsigned long long wk[4];
-    const int32_t step = d_state ? d_state[2] : 0;   // loaded with the keys, not after them
+    // the state words are read with the keys, not after them
+    const int32_t step = d_state ? d_state[2] : 0;
+    const int32_t pos = d_state ? d_state[1] : 0;
     unsigned long long b = 0ull;
-    for (int i = threadIdx.x; i < n; i += 256) b = umax64(b, slots[i]);
+    // 8 keys per thread per round, all loads issued before the first max
+    // (indices clamped to the last slot, a duplicate that cannot change the
+    // maximum): one memory round trip for up to 2048 slots, where a plain
+    // strided loop waits for each of its loads in turn
+    for (int base = 0; base < n; base += 256 * 8) {
+        unsigned long long v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = slots[min(base + (int)threadIdx.x + 256 * k, n - 1)];
+#pragma unroll
+        for (int k = 0; k < 8; k++) b = umax64(b, v[k]);
+    }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const uint32_t lo = __shfl_xor((uint32_t)b, off, 64), hi = __shfl_xor((uint32_t)(b >> 32), off, 64);
@@ -1107,7 +1132,7 @@ __global__ __launch_bounds__(256) void argmax_slots_kernel(const unsigned long l
         if (d_state) {
             if (token_log) token_log[step] = tok;
             d_state[0] = tok;
-            d_state[1] += 1;
+            d_state[1] = pos + 1;
             d_state[2] = step + 1;
         }
     }
