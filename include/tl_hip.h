@@ -160,6 +160,28 @@ tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* i
 /* apply_attention_mask(scores, mask) (masking.rs:36-51,147-165): where
  * mask == 0 the score becomes -10000.  mask broadcasts over leading dims. */
 tlhip_status tlhip_apply_attention_mask(tlhip_ctx ctx, tlhip_tensor scores, tlhip_tensor mask, tlhip_tensor y);
+/* causal_mask(n) (builtin_nn.rs:423-460, masking.rs:192-207): out [n, n]
+ * f16 = 1 where j <= i, else 0.                                          */
+tlhip_status tlhip_causal_mask(tlhip_ctx ctx, tlhip_tensor out);
+/* slice_last(x, axis) (builtin_tensor.rs:1949-1991, slice.rs:25-60): the
+ * last index of axis 0, y = x's shape without axis 0 ([1] for a 1-D x,
+ * where the reference returns a scalar).  axis != 0 -> InvalidOperation,
+ * as in the reference.  F16 / F32 / I32.                                 */
+tlhip_status tlhip_slice_last(tlhip_ctx ctx, tlhip_tensor x, int axis, tlhip_tensor y);
+/* broadcast_to(x, shape) (broadcast.rs:11-120, shape.rs:37-49): y's shape is
+ * the target; dims align from the right, an input dim of 1 repeats, else
+ * ShapeMismatch.  F16 / F32 / I32.                                        */
+tlhip_status tlhip_broadcast_to(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y);
+/* rope(x, cos, sin) (builtin_tensor.rs:569-597) = Tensor::rope_candle
+ * (rope.rs:18-65, rope_candle_f16 unified.metal:5122-5185): x [S, H, D],
+ * cos/sin [L >= S, D] f16; pair i of row s is rotated by cos[s, i] and
+ * sin[s, i] -- column i, as the reference's kernel indexes the table.    */
+tlhip_status tlhip_rope_cos_sin(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor cos_t, tlhip_tensor sin_t, tlhip_tensor y);
+/* precompute_rope_cos / _sin(head_dim, max_seq_len, base)
+ * (builtin_tensor.rs:610-700): out [max_seq_len, head_dim] f16, value of
+ * pair i at columns 2i and 2i+1.  Synchronous.                           */
+tlhip_status tlhip_precompute_rope(tlhip_ctx ctx, int head_dim, int max_seq_len, float base, int want_sin,
+                                   tlhip_tensor out);
 /* einsum("ihd,jhd->ihj") and einsum("ihj,jhd->ihd") (einsum.rs:653-886),
  * fp32 accumulation, f16 out.  K/V may carry fewer heads than Q (GQA:
  * head h reads h / (H/Hkv)), replacing broadcast_to + contiguous.         */

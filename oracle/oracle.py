@@ -71,6 +71,11 @@ def _declare(L):
         "tlo_gelu": (None, [vp, sz, vp]),
         "tlo_attention": (None, [vp, vp, vp, i, i, i, i, i, i, f, i, i, vp]),
         "tlo_embedding": (i, [vp, i, i, vp, i, vp]),
+        "tlo_causal_mask": (None, [i, vp]),
+        "tlo_slice_last": (i, [vp, vp, i, i, i, vp]),
+        "tlo_broadcast_to": (i, [vp, vp, i, vp, i, i, vp]),
+        "tlo_rope_cos_sin": (i, [vp, i, i, i, vp, vp, i, vp]),
+        "tlo_precompute_rope": (None, [i, i, f, i, vp]),
         "tlo_argmax_last": (i, [vp, i]),
         "tlo_sample_temperature": (i, [vp, i, C.c_float, C.c_float]),
         "tlo_sample_uniform": (C.c_float, [C.c_uint64, C.c_uint64]),
@@ -253,6 +258,52 @@ def embedding(table, ids) -> np.ndarray:
     out = np.empty((ids.size, Hd), np.float16)
     if lib().tlo_embedding(_p(table), V, Hd, _p(ids), ids.size, _p(out)) != 0:
         raise IndexError("token id out of range")
+    return out
+
+
+def causal_mask(n: int) -> np.ndarray:
+    out = np.empty((n, n), np.float16)
+    lib().tlo_causal_mask(n, _p(out))
+    return out
+
+
+def _shape_arr(shape) -> np.ndarray:
+    return np.ascontiguousarray(shape, dtype=np.int64)
+
+
+def slice_last(x, axis: int = 0) -> np.ndarray:
+    """Raises ValueError where the reference returns InvalidOperation."""
+    x = np.ascontiguousarray(x)
+    out = np.empty(x.shape[1:] if x.ndim > 1 else (1,), x.dtype)
+    shp = _shape_arr(x.shape)
+    if lib().tlo_slice_last(_p(x), _p(shp), x.ndim, axis, x.itemsize, _p(out)) != 0:
+        raise ValueError(f"slice_last: axis {axis} of a {x.ndim}-D tensor")
+    return out
+
+
+def broadcast_to(x, shape) -> np.ndarray:
+    """Raises ValueError where the reference returns ShapeMismatch."""
+    x = np.ascontiguousarray(x)
+    out = np.empty(tuple(shape), x.dtype)
+    xs, ts = _shape_arr(x.shape), _shape_arr(shape)
+    if lib().tlo_broadcast_to(_p(x), _p(xs), x.ndim, _p(ts), len(shape), x.itemsize, _p(out)) != 0:
+        raise ValueError(f"broadcast_to: {x.shape} -> {tuple(shape)}")
+    return out
+
+
+def rope_cos_sin(x, cos_t, sin_t) -> np.ndarray:
+    x, cos_t, sin_t = _h(x), _h(cos_t), _h(sin_t)
+    S, H, D = x.shape
+    y = np.empty_like(x)
+    if cos_t.shape != sin_t.shape or cos_t.ndim != 2 or cos_t.shape[1] != D or \
+            lib().tlo_rope_cos_sin(_p(x), S, H, D, _p(cos_t), _p(sin_t), cos_t.shape[0], _p(y)) != 0:
+        raise ValueError("rope(x, cos, sin): shapes")
+    return y
+
+
+def precompute_rope(head_dim: int, max_seq_len: int, base: float, want_sin: bool) -> np.ndarray:
+    out = np.empty((max_seq_len, head_dim), np.float16)
+    lib().tlo_precompute_rope(head_dim, max_seq_len, base, int(want_sin), _p(out))
     return out
 
 

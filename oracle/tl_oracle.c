@@ -464,6 +464,92 @@ void tlo_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
 }
 
 /* ======================================================================== */
+/* masks, slicing, broadcasting, table RoPE                                 */
+/* ======================================================================== */
+
+void tlo_causal_mask(int n, uint16_t* out) {
+    /* builtin_nn.rs:445-455: f16::ONE where j <= i, f16::ZERO otherwise */
+    for (int i = 0; i < n; i++)
+        for (int j = 0; j < n; j++) out[(size_t)i * n + j] = j <= i ? 0x3C00u : 0u;
+}
+
+int tlo_slice_last(const void* x, const int64_t* shape, int ndim, int axis, int elem, void* y) {
+    /* slice.rs:29-40: axis must exist and be 0 */
+    if (axis < 0 || axis >= ndim || axis != 0) return -1;
+    size_t inner = 1;
+    for (int i = 1; i < ndim; i++) inner *= (size_t)shape[i];
+    if (shape[0] <= 0) return -1;
+    memcpy(y, (const uint8_t*)x + (size_t)(shape[0] - 1) * inner * (size_t)elem, inner * (size_t)elem);
+    return 0;
+}
+
+int tlo_broadcast_to(const void* x, const int64_t* xshape, int xnd, const int64_t* tshape,
+                     int tnd, int elem, void* y) {
+    /* shape.rs:37-49: rank may not shrink; aligned from the right each input
+     * dim equals the target's or is 1 */
+    if (xnd > tnd || tnd > 8) return -1;
+    for (int k = 1; k <= xnd; k++) {
+        const int64_t a = xshape[xnd - k], b = tshape[tnd - k];
+        if (a != b && a != 1) return -1;
+    }
+    size_t total = 1;
+    for (int i = 0; i < tnd; i++) total *= (size_t)tshape[i];
+    int64_t xstride[8];
+    int64_t st = 1;
+    for (int i = xnd - 1; i >= 0; i--) { xstride[i] = st; st *= xshape[i]; }
+    const int rd = tnd - xnd;
+    for (size_t g = 0; g < total; g++) {
+        /* unified.metal:3788-3812: target multi-index, then each input dim of
+         * size 1 reads coordinate 0 */
+        size_t rem = g, src = 0;
+        for (int i = tnd - 1; i >= 0; i--) {
+            const size_t c = rem % (size_t)tshape[i];
+            rem /= (size_t)tshape[i];
+            if (i >= rd) {
+                const int xi = i - rd;
+                if (xshape[xi] != 1) src += c * (size_t)xstride[xi];
+            }
+        }
+        memcpy((uint8_t*)y + g * (size_t)elem, (const uint8_t*)x + src * (size_t)elem, (size_t)elem);
+    }
+    return 0;
+}
+
+int tlo_rope_cos_sin(const uint16_t* x, int S, int H, int D, const uint16_t* cos_t,
+                     const uint16_t* sin_t, int L, uint16_t* y) {
+    lut_init();
+    /* rope.rs:22-55: [S, H, D] input, [L >= S, D] tables */
+    if (S < 0 || H < 0 || D <= 0 || D % 2 || L < S) return -1;
+    for (int s = 0; s < S; s++)
+        for (int h = 0; h < H; h++) {
+            const uint16_t* xr = x + ((size_t)s * H + h) * D;
+            uint16_t* yr = y + ((size_t)s * H + h) * D;
+            for (int i = 0; i < D / 2; i++) {
+                /* unified.metal:5161-5178: cos_sin_idx = seq_idx * head_dim + pair */
+                const float c = H2F(cos_t[(size_t)s * D + i]), sn = H2F(sin_t[(size_t)s * D + i]);
+                const float x0 = H2F(xr[2 * i]), x1 = H2F(xr[2 * i + 1]);
+                const float a = x0 * c, b = x1 * sn;
+                const float e = x0 * sn, f = x1 * c;
+                yr[2 * i] = tlo_f2h(a - b);
+                yr[2 * i + 1] = tlo_f2h(e + f);
+            }
+        }
+    return 0;
+}
+
+void tlo_precompute_rope(int D, int L, float base, int want_sin, uint16_t* out) {
+    for (int pos = 0; pos < L; pos++)
+        for (int i = 0; i < D / 2; i++) {
+            /* builtin_tensor.rs:664-682 */
+            const float theta = 1.0f / powf(base, (float)(2 * i) / (float)D);
+            const float ang = (float)pos * theta;
+            const uint16_t v = tlo_f2h(want_sin ? sinf(ang) : cosf(ang));
+            out[(size_t)pos * D + 2 * i] = v;
+            out[(size_t)pos * D + 2 * i + 1] = v;
+        }
+}
+
+/* ======================================================================== */
 /* gather / sampling                                                        */
 /* ======================================================================== */
 

@@ -138,6 +138,38 @@ void tlo_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                    int S, int J, int H, int Hkv, int D, int q_pos0,
                    float scale, int causal, int acc_mode, uint16_t* out);
 
+/* ---- masks, slicing, broadcasting, table RoPE ---------------------------
+ * causal_mask builtin_nn.rs:423-460 / Tensor::causal_mask masking.rs:192-207:
+ * [n, n] f16, 1 where j <= i, else 0.                                      */
+void tlo_causal_mask(int n, uint16_t* out);
+/* Tensor::slice_last slice.rs:25-60 (slice_last_axis0_f16 unified.metal):
+ * the last index of axis 0, x [d0, d1, ...] -> [d1, ...] (a 1-D input gives
+ * its last element).  Only axis 0 is supported, as in the reference.
+ * elem = element bytes.  Returns 0, or -1 for an axis the reference rejects
+ * (InvalidOperation).                                                      */
+int tlo_slice_last(const void* x, const int64_t* shape, int ndim, int axis, int elem, void* y);
+/* Tensor::broadcast_to broadcast.rs:11-30 + broadcast_f16 unified.metal:
+ * 3769-3815, TensorShape::can_broadcast_to shape.rs:37-49: dims aligned from
+ * the right; an input dim of 1 repeats.  Returns 0, or -1 when the shapes
+ * do not broadcast (ShapeMismatch).                                        */
+int tlo_broadcast_to(const void* x, const int64_t* xshape, int xnd, const int64_t* tshape,
+                     int tnd, int elem, void* y);
+/* rope(x, cos, sin) = Tensor::rope_candle rope.rs:18-65 + rope_candle_f16
+ * unified.metal:5122-5185: x [S, H, D] f16, cos/sin [L >= S, D] f16; pair
+ * i of row s (elements 2i, 2i+1) is rotated by cos[s, i] / sin[s, i] --
+ * column i, not 2i, exactly as the Metal kernel indexes the table (with
+ * the duplicated tables of precompute_rope_*, pair i therefore turns by
+ * the frequency of pair i/2).  f32 products, each rounded, f16 stores.
+ * Returns 0, or -1 for the shapes rope_candle rejects (InvalidOperation)
+ * and for odd D.                                                           */
+int tlo_rope_cos_sin(const uint16_t* x, int S, int H, int D, const uint16_t* cos_t,
+                     const uint16_t* sin_t, int L, uint16_t* y);
+/* precompute_rope_cos / precompute_rope_sin builtin_tensor.rs:610-700:
+ * theta_i = 1 / base^(2i/D) (f32 powf), angle = pos * theta_i (f32), each
+ * value stored twice (columns 2i and 2i+1) in an f32 [L, D] table, then
+ * converted to f16.  want_sin selects the table.                           */
+void tlo_precompute_rope(int D, int L, float base, int want_sin, uint16_t* out);
+
 /* ---- gather / sampling ----------------------------------------------------
  * embedding builtin_nn.rs:627-812 (+ unified.metal:658-676): row copy.
  * Returns 0, or -1 when an id is out of range (the builtin's bounds check).*/

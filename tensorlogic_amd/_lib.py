@@ -70,6 +70,11 @@ SIGNATURES = {
     "tlhip_mul_scalar": (_i, [_vp, _vp, _f, _vp]),
     "tlhip_embedding": (_i, [_vp, _vp, _i32p, _i, _vp]),
     "tlhip_apply_attention_mask": (_i, [_vp, _vp, _vp, _vp]),
+    "tlhip_causal_mask": (_i, [_vp, _vp]),
+    "tlhip_slice_last": (_i, [_vp, _vp, _i, _vp]),
+    "tlhip_broadcast_to": (_i, [_vp, _vp, _vp]),
+    "tlhip_rope_cos_sin": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "tlhip_precompute_rope": (_i, [_vp, _i, _i, _f, _i, _vp]),
     "tlhip_einsum_scores": (_i, [_vp, _vp, _vp, _vp]),
     "tlhip_einsum_context": (_i, [_vp, _vp, _vp, _vp]),
     "tlhip_attention": (_i, [_vp, _vp, _vp, _vp, _i, _f, _i, _vp]),

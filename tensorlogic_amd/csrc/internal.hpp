@@ -194,6 +194,17 @@ enum EwOp { EW_SIGMOID = 0, EW_SILU = 1, EW_GELU = 2, EW_ADD = 3, EW_MUL = 4, EW
             EW_SILU_MUL = 6 };
 tlhip_status launch_elementwise(hipStream_t s, int op, const uint16_t* a, const uint16_t* b,
                                 uint16_t* y, int64_t n, int64_t b_period, float scalar);
+tlhip_status launch_causal_mask(hipStream_t s, uint16_t* out, int64_t n);
+// broadcast_to: target dims and, per target dim, the input stride (0 where
+// the input has size 1 or no dim)
+struct BcastDims {
+    int nd = 0;
+    int64_t shape[8] = {};
+    int64_t xstride[8] = {};
+};
+tlhip_status launch_broadcast(hipStream_t s, const void* x, void* y, int elem, const BcastDims& b);
+tlhip_status launch_rope_cs(hipStream_t s, const uint16_t* x, const uint16_t* ct, const uint16_t* st, uint16_t* y,
+                            int S, int H, int D);
 tlhip_status launch_mask(hipStream_t s, const uint16_t* sc, const uint16_t* mask, uint16_t* y,
                          int64_t n, int64_t mask_period);
 tlhip_status launch_embedding(hipStream_t s, tlhip_dtype tt, const void* tq, const uint16_t* td,

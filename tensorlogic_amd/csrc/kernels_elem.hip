@@ -457,6 +457,94 @@ tlhip_status launch_mask(hipStream_t s, const uint16_t* sc, const uint16_t* mask
 }
 
 // ---------------------------------------------------------------------------
+// causal_mask(n) (builtin_nn.rs:423-460, Tensor::causal_mask masking.rs:
+// 192-207): [n, n] f16, 1 where j <= i.  Eight elements per thread, one
+// 16-byte store where the group lies inside the matrix.
+// ---------------------------------------------------------------------------
+__global__ void causal_mask_kernel(uint16_t* __restrict__ out, int64_t n) {
+    const int64_t total = n * n;
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (i0 >= total) return;
+    uint16_t v[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int64_t i = i0 + e;
+        v[e] = (i < total && i % n <= i / n) ? (uint16_t)0x3C00u : (uint16_t)0u;
+    }
+    if (i0 + 8 <= total && (i0 & 7) == 0) {
+        *(u4*)(out + i0) = u4{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16),
+                              (uint32_t)v[4] | ((uint32_t)v[5] << 16), (uint32_t)v[6] | ((uint32_t)v[7] << 16)};
+    } else {
+        for (int e = 0; e < 8 && i0 + e < total; e++) out[i0 + e] = v[e];
+    }
+}
+
+tlhip_status launch_causal_mask(hipStream_t s, uint16_t* out, int64_t n) {
+    const int64_t groups = (n * n + 7) / 8;
+    if (groups <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(causal_mask_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, out, n);
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// broadcast_to (broadcast.rs:11-120, broadcast_f16 unified.metal:3769-3815):
+// target element g reads the input element whose coordinates are g's,
+// aligned from the right, with coordinate 0 on the input's size-1 dims
+// (stride 0 below).  One thread per output element, 2- or 4-byte elements.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void broadcast_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t total, BcastDims b) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= total) return;
+    int64_t rem = g, src = 0;
+    for (int i = b.nd - 1; i >= 0; i--) {
+        const int64_t c = rem % b.shape[i];
+        rem /= b.shape[i];
+        src += c * b.xstride[i];
+    }
+    y[g] = x[src];
+}
+
+tlhip_status launch_broadcast(hipStream_t s, const void* x, void* y, int elem, const BcastDims& b) {
+    int64_t total = 1;
+    for (int i = 0; i < b.nd; i++) total *= b.shape[i];
+    if (total <= 0) return TLHIP_OK;
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (elem == 2) hipLaunchKernelGGL(broadcast_kernel<uint16_t>, grid, dim3(256), 0, s, (const uint16_t*)x, (uint16_t*)y, total, b);
+    else hipLaunchKernelGGL(broadcast_kernel<uint32_t>, grid, dim3(256), 0, s, (const uint32_t*)x, (uint32_t*)y, total, b);
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// rope(x, cos, sin) = Tensor::rope_candle (rope.rs:18-65, rope_candle_f16
+// unified.metal:5122-5185): x [S, H, D], tables [L >= S, D]; pair i of row
+// s is rotated by cos[s, i] / sin[s, i] (column i, as the Metal kernel
+// indexes the table), f32 products each rounded, f16 stores.  One thread
+// per pair, both elements written by it.
+// ---------------------------------------------------------------------------
+__global__ void rope_cs_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ ct,
+                               const uint16_t* __restrict__ st, uint16_t* __restrict__ y, int S, int H, int D) {
+    const int64_t half = D / 2;
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= (int64_t)S * H * half) return;
+    const int64_t i = p % half, sh = p / half, s = sh / H;
+    const float c = h2f(ct[s * D + i]), sn = h2f(st[s * D + i]);
+    const uint32_t xw = *(const uint32_t*)(x + sh * D + 2 * i);
+    const float x0 = h2f((uint16_t)(xw & 0xffffu)), x1 = h2f((uint16_t)(xw >> 16));
+    const float r0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
+    const float r1 = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, c));
+    *(uint32_t*)(y + sh * D + 2 * i) = (uint32_t)f2h(r0) | ((uint32_t)f2h(r1) << 16);
+}
+
+tlhip_status launch_rope_cs(hipStream_t s, const uint16_t* x, const uint16_t* ct, const uint16_t* st, uint16_t* y,
+                            int S, int H, int D) {
+    const int64_t pairs = (int64_t)S * H * (D / 2);
+    if (pairs <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(rope_cs_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s, x, ct, st, y, S, H, D);
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
 // embedding (builtin_nn.rs:627-812, embedding_lookup_f16 unified.metal:
 // 658-676): out[s, :] = table[id_s, :]; quantized tables are dequantised
 // row by row (bit-exact with gguf.rs).  ids come from a device array, or in

@@ -4,6 +4,7 @@
 // when a check fails.
 #include <cmath>
 #include <cstring>
+#include <vector>
 
 #include "internal.hpp"
 
@@ -292,6 +293,123 @@ tlhip_status tlhip_apply_attention_mask(tlhip_ctx ctx, tlhip_tensor sc, tlhip_te
                     shape_str(mask).c_str());
     TLHIP_TRY(launch_mask(ctx->stream, P(sc), P(mask), P(y), numel(sc), period));
     return after_launch(ctx, "apply_attention_mask");
+}
+
+// causal_mask(n) (builtin_nn.rs:423-460): out must be [n, n] f16.
+tlhip_status tlhip_causal_mask(tlhip_ctx ctx, tlhip_tensor out) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("causal_mask", {out}));
+    if (out->ndim != 2 || out->shape[0] != out->shape[1])
+        return fail(TLHIP_ERR_INVALID_DIMENSION, "causal_mask: output must be [n, n], got %s", shape_str(out).c_str());
+    TLHIP_TRY(launch_causal_mask(ctx->stream, P(out), out->shape[0]));
+    return after_launch(ctx, "causal_mask");
+}
+
+static int elem_bytes(tlhip_dtype d) { return d == TLHIP_F16 ? 2 : (d == TLHIP_F32 || d == TLHIP_I32) ? 4 : 0; }
+
+// slice_last(x, axis) (builtin_tensor.rs:1949-1991, slice.rs:25-60): the
+// last index of axis 0; y is x's shape without axis 0 ([1] for a 1-D x,
+// where the reference returns a scalar).
+tlhip_status tlhip_slice_last(tlhip_ctx ctx, tlhip_tensor x, int axis, tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(check_t(x, "slice_last"));
+    TLHIP_TRY(check_t(y, "slice_last"));
+    const int eb = elem_bytes(x->dtype);
+    if (!eb || y->dtype != x->dtype) return fail(TLHIP_ERR_DTYPE, "slice_last: dtypes %d -> %d", (int)x->dtype, (int)y->dtype);
+    if (axis < 0 || axis >= x->ndim)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "slice_last() axis %d out of bounds for %dD tensor", axis, x->ndim);
+    if (axis != 0)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "slice_last() currently only supports axis=0, got axis=%d", axis);
+    const bool ok = x->ndim == 1 ? (y->ndim == 1 && y->shape[0] == 1)
+                                 : (y->ndim == x->ndim - 1 &&
+                                    memcmp(y->shape, x->shape + 1, sizeof(int64_t) * (x->ndim - 1)) == 0);
+    if (!ok) return fail(TLHIP_ERR_SHAPE_MISMATCH, "slice_last: %s -> %s", shape_str(x).c_str(), shape_str(y).c_str());
+    if (x->shape[0] <= 0) return fail(TLHIP_ERR_INVALID_DIMENSION, "slice_last: empty axis 0");
+    const size_t inner = (size_t)numel(y) * eb;
+    if (inner)
+        TLHIP_CHECK_HIP(hipMemcpyAsync(y->data, (const uint8_t*)x->data + (size_t)(x->shape[0] - 1) * inner, inner,
+                                       hipMemcpyDeviceToDevice, ctx->stream));
+    return after_launch(ctx, "slice_last");
+}
+
+// broadcast_to(x, shape) (broadcast.rs:11-120, shape.rs:37-49): y's shape is
+// the target; dims align from the right and an input dim of 1 repeats.  An
+// equal shape is a copy (the reference returns the tensor itself).
+tlhip_status tlhip_broadcast_to(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(check_t(x, "broadcast_to"));
+    TLHIP_TRY(check_t(y, "broadcast_to"));
+    const int eb = elem_bytes(x->dtype);
+    if (!eb || y->dtype != x->dtype) return fail(TLHIP_ERR_DTYPE, "broadcast_to: dtypes %d -> %d", (int)x->dtype, (int)y->dtype);
+    bool ok = x->ndim <= y->ndim;
+    for (int k = 1; ok && k <= x->ndim; k++) {
+        const int64_t a = x->shape[x->ndim - k], b = y->shape[y->ndim - k];
+        ok = a == b || a == 1;
+    }
+    if (!ok) return fail(TLHIP_ERR_SHAPE_MISMATCH, "broadcast_to: expected %s, actual %s", shape_str(y).c_str(),
+                         shape_str(x).c_str());
+    BcastDims b;
+    b.nd = y->ndim;
+    const int rd = y->ndim - x->ndim;
+    int64_t st = 1;
+    for (int i = y->ndim - 1; i >= 0; i--) {
+        b.shape[i] = y->shape[i];
+        if (i >= rd) {
+            const int64_t xd = x->shape[i - rd];
+            b.xstride[i] = xd == 1 ? 0 : st;
+            st *= xd;
+        }
+    }
+    TLHIP_TRY(launch_broadcast(ctx->stream, x->data, y->data, eb, b));
+    return after_launch(ctx, "broadcast_to");
+}
+
+// rope(x, cos, sin) = Tensor::rope_candle (builtin_tensor.rs:569-597,
+// rope.rs:18-65): x [S, H, D], cos/sin [L >= S, D] f16.
+tlhip_status tlhip_rope_cos_sin(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor cos_t, tlhip_tensor sin_t, tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("rope(x, cos, sin)", {x, cos_t, sin_t, y}));
+    if (x->ndim != 3)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "rope_candle requires 3D tensor [seq_len, n_heads, head_dim], got %dD",
+                    x->ndim);
+    if (cos_t->ndim != 2 || sin_t->ndim != 2)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "cos/sin must be 2D [max_seq_len, head_dim], got cos: %dD, sin: %dD",
+                    cos_t->ndim, sin_t->ndim);
+    const int64_t S = x->shape[0], H = x->shape[1], D = x->shape[2];
+    if (cos_t->shape[1] != D || sin_t->shape[1] != D)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "cos/sin last dim must be head_dim = %lld", (long long)D);
+    if (cos_t->shape[0] < S || sin_t->shape[0] < S)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "cos/sin first dim must be >= seq_len = %lld", (long long)S);
+    if (D % 2) return fail(TLHIP_ERR_INVALID_DIMENSION, "rope(x, cos, sin): head_dim %lld is odd", (long long)D);
+    TLHIP_TRY(same_shape(x, y, "rope(x, cos, sin)"));
+    if (S * H * D > INT32_MAX) return fail(TLHIP_ERR_INVALID_DIMENSION, "rope(x, cos, sin): tensor too large");
+    TLHIP_TRY(launch_rope_cs(ctx->stream, P(x), P(cos_t), P(sin_t), P(y), (int)S, (int)H, (int)D));
+    return after_launch(ctx, "rope(x, cos, sin)");
+}
+
+// precompute_rope_cos / precompute_rope_sin (builtin_tensor.rs:610-700):
+// computed on the host in f32 as the reference does, each value stored in
+// columns 2i and 2i+1, converted to f16 and uploaded; out [max_seq_len,
+// head_dim] f16.  Synchronous (the host table is freed on return).
+tlhip_status tlhip_precompute_rope(tlhip_ctx ctx, int head_dim, int max_seq_len, float base, int want_sin,
+                                   tlhip_tensor out) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(f16_args("precompute_rope", {out}));
+    if (head_dim <= 0 || head_dim % 2)
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "head_dim must be even, got %d", head_dim);
+    if (max_seq_len < 0 || out->ndim != 2 || out->shape[0] != max_seq_len || out->shape[1] != head_dim)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "precompute_rope: output %s for [%d, %d]", shape_str(out).c_str(),
+                    max_seq_len, head_dim);
+    std::vector<_Float16> tab((size_t)max_seq_len * head_dim);
+    for (int pos = 0; pos < max_seq_len; pos++)
+        for (int i = 0; i < head_dim / 2; i++) {
+            const float theta = 1.0f / powf(base, (float)(2 * i) / (float)head_dim);
+            const float ang = (float)pos * theta;
+            const _Float16 v = (_Float16)(want_sin ? sinf(ang) : cosf(ang));
+            tab[(size_t)pos * head_dim + 2 * i] = v;
+            tab[(size_t)pos * head_dim + 2 * i + 1] = v;
+        }
+    return tlhip_tensor_upload(ctx, out, tab.data(), tab.size() * sizeof(_Float16));
 }
 
 static tlhip_status qkv_dims(tlhip_tensor q, tlhip_tensor k, const char* nm, int* H, int* Hkv, int* D) {

@@ -18,7 +18,7 @@ from typing import Sequence
 import numpy as np
 
 from . import _lib
-from ._lib import F16, Q4_0, Q6_K, Q8_0, ROPE_INTERLEAVED, ROPE_NEOX, TLHipError, call, lib
+from ._lib import F16, F32, I32, Q4_0, Q6_K, Q8_0, ROPE_INTERLEAVED, ROPE_NEOX, TLHipError, call, lib
 
 _vp = C.c_void_p
 _BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q6_K: 210}
@@ -26,6 +26,9 @@ _BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q6_K: 210}
 
 def _shape_arr(shape):
     return (C.c_int64 * len(shape))(*[int(s) for s in shape])
+
+
+_NP_DTYPE = {F16: np.float16, F32: np.float32, I32: np.int32}
 
 
 class Device:
@@ -58,10 +61,11 @@ class Device:
         call("tlhip_tensor_alloc", self.h, dtype, len(shape), _shape_arr(shape), C.byref(h))
         return Tensor(self, h)
 
-    def tensor(self, arr) -> "Tensor":
-        """Tensor::from_vec_gpu: upload an f16 array (float arrays are rounded RNE)."""
-        a = np.ascontiguousarray(arr, dtype=np.float16)
-        t = self.empty(a.shape if a.ndim else (1,))
+    def tensor(self, arr, dtype: int = F16) -> "Tensor":
+        """Tensor::from_vec_gpu: upload an array as F16 (float arrays are
+        rounded RNE), F32 or I32."""
+        a = np.ascontiguousarray(arr, dtype=_NP_DTYPE[dtype])
+        t = self.empty(a.shape if a.ndim else (1,), dtype)
         call("tlhip_tensor_upload", self.h, t.h, a.ctypes.data_as(_vp), a.nbytes)
         return t
 
@@ -114,7 +118,7 @@ class Tensor:
         if dt in _BLOCK_BYTES:
             out = np.empty(self.nbytes(), np.uint8)
         else:
-            out = np.empty(shape, np.float16)
+            out = np.empty(shape, _NP_DTYPE[dt])
         call("tlhip_tensor_download", self.dev.h, self.h, out.ctypes.data_as(_vp), out.nbytes)
         return out
 
@@ -223,6 +227,26 @@ class Tensor:
     def __mul__(self, other):
         return self.mul_scalar(other) if isinstance(other, (int, float)) else self.mul(other)
 
+    def slice_last(self, axis: int = 0) -> "Tensor":
+        """Tensor::slice_last (slice.rs:25-60): last index of axis 0; a 1-D
+        tensor gives shape [1] (the reference's scalar)."""
+        shape = self.shape
+        out = self.dev.empty(shape[1:] if len(shape) > 1 else (1,), self.dtype)
+        call("tlhip_slice_last", self.dev.h, self.h, int(axis), out.h)
+        return out
+
+    def broadcast_to(self, shape) -> "Tensor":
+        """Tensor::broadcast_to (broadcast.rs:11-120)."""
+        out = self.dev.empty(tuple(shape), self.dtype)
+        call("tlhip_broadcast_to", self.dev.h, self.h, out.h)
+        return out
+
+    def rope_candle(self, cos: "Tensor", sin: "Tensor") -> "Tensor":
+        """rope(x, cos, sin) = Tensor::rope_candle (rope.rs:18-65)."""
+        out = self._new(self.shape)
+        call("tlhip_rope_cos_sin", self.dev.h, self.h, cos.h, sin.h, out.h)
+        return out
+
     def apply_attention_mask(self, mask: "Tensor") -> "Tensor":
         out = self._new(self.shape)
         call("tlhip_apply_attention_mask", self.dev.h, self.h, mask.h, out.h)
@@ -255,6 +279,27 @@ def attention(q: Tensor, k: Tensor, v: Tensor, q_pos0: int = 0, scale: float | N
     if out is None:
         out = q.dev.empty(q.shape)
     call("tlhip_attention", q.dev.h, q.h, k.h, v.h, int(q_pos0), float(scale), int(causal), out.h)
+    return out
+
+
+def causal_mask(dev: Device, n: int) -> Tensor:
+    """causal_mask(n) (builtin_nn.rs:423-460): [n, n], 1 where j <= i."""
+    out = dev.empty((n, n))
+    call("tlhip_causal_mask", dev.h, out.h)
+    return out
+
+
+def precompute_rope_cos(dev: Device, head_dim: int, max_seq_len: int, base: float = 10000.0) -> Tensor:
+    """precompute_rope_cos (builtin_tensor.rs:610-700): [max_seq_len, head_dim] f16."""
+    out = dev.empty((max_seq_len, head_dim))
+    call("tlhip_precompute_rope", dev.h, int(head_dim), int(max_seq_len), float(base), 0, out.h)
+    return out
+
+
+def precompute_rope_sin(dev: Device, head_dim: int, max_seq_len: int, base: float = 10000.0) -> Tensor:
+    """precompute_rope_sin (builtin_tensor.rs:610-700): [max_seq_len, head_dim] f16."""
+    out = dev.empty((max_seq_len, head_dim))
+    call("tlhip_precompute_rope", dev.h, int(head_dim), int(max_seq_len), float(base), 1, out.h)
     return out
 
 
