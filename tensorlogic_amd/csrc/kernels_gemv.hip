@@ -405,106 +405,140 @@ __device__ __forceinline__ float wg_sum1(float v, float* red) {
 // formulas and f16 store of rms_norm_kernel / layer_norm_kernel
 //   RMS: y = f16((x * (1 / sqrt(mean(x^2) + eps))) * w)
 //   LN:  y = f16(((x - mean) * (1 / sqrt(var + eps))) * w + b)
-// and leaves it in LDS as natural f16 pairs, one row of 17 words per
-// 32-element block (16 words + 1 of padding, so the 64 lanes reading
-// blocks b = lane + 64 i word by word hit distinct banks); each wave
-// permutes its block's pairs into the order of the unpacking after the
-// read.  Thread t holds item t = 16 consecutive activations (half a block),
-// loaded with two 16-byte loads each of x, w (and b); K <= 4096 keeps it
-// to one item per thread.  The loads are issued before the weight rows
-// (vector loads retire in order), so the statistics start while the
-// weights are still in flight.  Measured against the earlier quad layout
-// (8-byte loads, a two-barrier workgroup sum) on MI355X: 6.78 -> 5.7 us for
-// the gate/up rows [11264 x 2048], 4.26 -> 3.2-3.4 us for [2560 x 2048].
+// and leaves it in LDS already in the pair order of the unpacking.  LDS is
+// quad-major, xs[v][b] = 16 bytes (pairs 4v..4v+3 of block b's chunk), so
+// lane l's reads of block l are consecutive 16-byte words (no conflicts).
+// Quad v of a block holds elements {4v..4v+3, 16+4v..16+4v+3} for Q4_0 /
+// Q6_K and {8v..8v+7} for Q8_0 / f16; thread t holds quads t, t + NT, ...
+// (8 activations each, so the loads and the statistics spread over four
+// waves of a K = 2048 row).  The loads go through range-checked buffer
+// descriptors: a quad past the row reads zeros with no memory request, so
+// there is neither a branch (whose join would make the compiler wait for
+// the loads before the weight rows go out) nor a duplicate read.  They are
+// issued before the weight rows (vector loads retire in order), so the
+// statistics start while the weights are still in flight.
+template <int WT>
+__device__ __forceinline__ int quad_elem(int v, int e) {
+    return xo_nibble<WT>() ? (e < 4 ? 4 * v + e : 12 + 4 * v + e) : 8 * v + e;
+}
+
+template <int WT>
+__device__ __forceinline__ u4 pack_quad(const float f[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        h2 h;
+        h[0] = (h16)f[2 * t];
+        h[1] = (h16)f[2 * t + 1];
+        w[t] = as_u32(h);
+    }
+    if (WT == TLHIP_F16) return u4{w[0], w[1], w[2], w[3]};
+    return u4{pack_lo(w[0], w[1]), pack_hi(w[0], w[1]), pack_lo(w[2], w[3]), pack_hi(w[2], w[3])};
+}
+
 template <int WT, int NB, int WPB, int PRO>
 struct NormStage {
     static constexpr int NT = WPB * 64;
-    static_assert(NB * 128 <= NT, "one 16-element item per thread");
-    uint32_t xw[8], ww[8], bw[8];   // raw f16 pairs until finish()
+    static constexpr int IPT = (NB * 256 + NT - 1) / NT;
+    uint32_t xw[IPT][4], ww[IPT][4], bw[IPT][4];   // raw f16 pairs until finish()
 
-    // Item it's 16 activations of a K-element row through a range-checked
-    // buffer descriptor: a lane whose item lies past the row gets zeros
-    // with no memory request, so there is neither a branch (whose join
-    // would make the compiler wait for the loads before the weight rows go
-    // out) nor a clamped duplicate read from the waves that hold no item.
-    __device__ __forceinline__ static void load16(const uint16_t* __restrict__ src, int K, int it, uint32_t w[8]) {
+    __device__ __forceinline__ static void load_buf(const uint16_t* __restrict__ src, int K, int it, uint32_t w[4]) {
         const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, K * 2, BUF_RSRC_WORD3);
-        const u4 a = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, it * 32, 0, 0));
-        const u4 b = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, it * 32 + 16, 0, 0));
-        w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
-        w[4] = b[0]; w[5] = b[1]; w[6] = b[2]; w[7] = b[3];
+        const int b = it >> 2, v = it & 3;
+        if (xo_nibble<WT>()) {
+            const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (b * 32 + 4 * v) * 2, 0, 0));
+            const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (b * 32 + 16 + 4 * v) * 2, 0, 0));
+            w[0] = lo.x; w[1] = lo.y; w[2] = hi.x; w[3] = hi.y;
+        } else {
+            const u4 t = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, (b * 32 + 8 * v) * 2, 0, 0));
+            w[0] = t[0]; w[1] = t[1]; w[2] = t[2]; w[3] = t[3];
+        }
+    }
+
+    __device__ __forceinline__ static void to_float(const uint32_t w[4], float f[8]) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const h2 h = as_h2(w[t]);
+            f[2 * t] = (float)h[0];
+            f[2 * t + 1] = (float)h[1];
+        }
     }
 
     __device__ __forceinline__ void load(const GemvParams& p, const uint16_t* __restrict__ xsrc) {
-        const int it = threadIdx.x;
-        load16(xsrc, p.K, it, xw);
-        load16(p.norm_w, p.K, it, ww);
-        if (PRO == PRO_LN) load16(p.norm_b, p.K, it, bw);
+#pragma unroll
+        for (int k = 0; k < IPT; k++) {
+            const int it = threadIdx.x + k * NT;
+            load_buf(xsrc, p.K, it, xw[k]);
+            load_buf(p.norm_w, p.K, it, ww[k]);
+            if (PRO == PRO_LN) load_buf(p.norm_b, p.K, it, bw[k]);
+        }
     }
 
-    __device__ __forceinline__ void finish(const GemvParams& p, uint32_t (*xs)[17], float (*red)[WPB]) {
-        const int it = threadIdx.x;
-        const bool valid = it < (p.K >> 4);
-        float f[16];
+    __device__ __forceinline__ void finish(const GemvParams& p, u4 (*xs)[NB * 64], float (*red)[WPB]) {
+        const int items = (p.K >> 5) * 4;
+        float f[IPT][8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const h2 h = as_h2(xw[i]);
-            f[2 * i] = valid ? (float)h[0] : 0.0f;
-            f[2 * i + 1] = valid ? (float)h[1] : 0.0f;
-        }
-        if (p.x_out && blockIdx.x == 0 && valid) {   // the residual copy of an embedded row
-            u4* o = (u4*)(p.x_out + (size_t)it * 16);
-            o[0] = u4{xw[0], xw[1], xw[2], xw[3]};
-            o[1] = u4{xw[4], xw[5], xw[6], xw[7]};
-        }
+        for (int k = 0; k < IPT; k++) to_float(xw[k], f[k]);   // (quads past the row read zeros)
+        if (p.x_out && blockIdx.x == 0)   // the residual copy of an embedded row
+#pragma unroll
+            for (int k = 0; k < IPT; k++) {
+                const int it = threadIdx.x + k * NT;
+                if (it < items) {
+                    const int b = it >> 2, v = it & 3;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) p.x_out[(size_t)b * 32 + quad_elem<WT>(v, e)] = f2h(f[k][e]);
+                }
+            }
         float mean = 0.0f, inv;
         if (PRO == PRO_RMS) {
             float ss = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 16; e++) ss += f[e] * f[e];
+            for (int k = 0; k < IPT; k++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) ss += f[k][e] * f[k][e];
             inv = 1.0f / sqrtf(wg_sum1<WPB>(ss, red[0]) / (float)p.K + p.eps);
         } else {
             float sm = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 16; e++) sm += f[e];
+            for (int k = 0; k < IPT; k++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) sm += f[k][e];
             mean = wg_sum1<WPB>(sm, red[0]) / (float)p.K;
             float q = 0.0f;
-            if (valid)
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const float d = f[e] - mean;
+            for (int k = 0; k < IPT; k++) {
+                if ((int)threadIdx.x + k * NT >= items) continue;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float d = f[k][e] - mean;
                     q += d * d;
                 }
+            }
             inv = 1.0f / sqrtf(wg_sum1<WPB>(q, red[1]) / (float)p.K + p.eps);
         }
-        if (valid) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const h2 w = as_h2(ww[i]);
-                float o0, o1;
-                if (PRO == PRO_RMS) {
-                    o0 = (f[2 * i] * inv) * (float)w[0];
-                    o1 = (f[2 * i + 1] * inv) * (float)w[1];
-                } else {
-                    const h2 b = as_h2(bw[i]);
-                    o0 = (((f[2 * i] - mean) * inv) * (float)w[0]) + (float)b[0];
-                    o1 = (((f[2 * i + 1] - mean) * inv) * (float)w[1]) + (float)b[1];
-                }
-                h2 o;
-                o[0] = (h16)o0;
-                o[1] = (h16)o1;
-                xs[it >> 1][(it & 1) * 8 + i] = as_u32(o);
-            }
+        for (int k = 0; k < IPT; k++) {
+            const int it = threadIdx.x + k * NT;
+            if (it >= items) continue;
+            const int b = it >> 2, v = it & 3;
+            float w[8], bb[8];
+            to_float(ww[k], w);
+            if (PRO == PRO_LN) to_float(bw[k], bb);
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                f[k][e] = PRO == PRO_RMS ? (f[k][e] * inv) * w[e] : (((f[k][e] - mean) * inv) * w[e]) + bb[e];
+            xs[v][b] = pack_quad<WT>(f[k]);
         }
         lds_barrier();
     }
 
-    // Block b's 16 normalised pairs, permuted into the pair order of WT's unpacking.
-    __device__ __forceinline__ static void chunk(const uint32_t (*xs)[17], int b, uint32_t xc[16]) {
-        uint32_t nat[16];
+    // Block b's 16 normalised pairs, already in the pair order of WT's unpacking.
+    __device__ __forceinline__ static void chunk(const u4 (*xs)[NB * 64], int b, uint32_t xc[16]) {
 #pragma unroll
-        for (int i = 0; i < 16; i++) nat[i] = xs[b][i];
-        order_x<WT>(nat, xc);
+        for (int v = 0; v < 4; v++) {
+            const u4 t = xs[v][b];
+            xc[4 * v] = t[0]; xc[4 * v + 1] = t[1]; xc[4 * v + 2] = t[2]; xc[4 * v + 3] = t[3];
+        }
     }
 };
 
@@ -832,7 +866,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
 // stored logits to one (value, index) key in amax_slots[blockIdx.x].
 template <int WT, int NB, int RI, int WPB, int PRO>
 __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams p) {
-    __shared__ uint32_t xs[NB * 64][17];
+    __shared__ u4 xs[4][NB * 64];
     __shared__ float red[2][WPB];
     __shared__ unsigned long long wkey[WPB];
     kernarg_fence(p);
