@@ -145,6 +145,30 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     return t;
 }
 
+// Single-barrier workgroup max / sum: the caller must not write `red` again
+// before another barrier (use one array per reduction).  The barrier also
+// publishes every LDS write made before the call.
+template <int NWV>
+__device__ __forceinline__ float block_max1(float v, float* red) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int k = 1; k < NWV; k++) t = fmaxf(t, red[k]);
+    return t;
+}
+template <int NWV>
+__device__ __forceinline__ float block_sum1(float v, float* red) {
+    v = wave_sum<64>(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int k = 1; k < NWV; k++) t += red[k];
+    return t;
+}
+
 // sigmoid as the reference CPU path computes it (activations.rs:252-266):
 // f32 1 / (1 + exp(-x)), then stored f16.
 __device__ __forceinline__ uint16_t sigmoid_h(uint16_t x) {

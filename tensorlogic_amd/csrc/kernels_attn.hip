@@ -119,7 +119,7 @@ template <int NT>
 __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed) {
     constexpr int NWV = NT / 64, NG = NT / 8;
     __shared__ float sc[ATT_MAX_J];
-    __shared__ float red[NWV];
+    __shared__ float red[2][NWV];
     __shared__ float part[NWV][64];
     attn_kernarg_fence(a, J_fixed);
     const int s = blockIdx.x, h = blockIdx.y;
@@ -197,7 +197,7 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed
             }
         }
     }
-    mx = block_max<NWV>(mx, red);   // (its barriers also publish sc[])
+    mx = block_max1<NWV>(mx, red[0]);   // (its barrier also publishes sc[])
     if (!isfinite(mx)) mx = 0.0f;
     float sum = 0.0f;
     for (int j = tid; j < Jv; j += NT) {
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed
         sc[j] = h2f(f2h(e));
         sum += e;
     }
-    sum = block_sum<NWV>(sum, red);
+    sum = block_sum1<NWV>(sum, red[1]);
     const bool degenerate = !(sum > 0.0f && isfinite(sum));
     const int Jp = degenerate ? J : Jv;
     const float uni = h2f(f2h(1.0f / (float)J));
@@ -295,7 +295,7 @@ template <int D>
 __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, int J_fixed) {
     constexpr int EPL = D / 8, NW = EPL / 2, U = ADK_UNR, NT = ADK_THREADS, NWV = NT / 64, NG = NT / 8;
     __shared__ float sc[ATT_MAX_J];
-    __shared__ float red[NWV];
+    __shared__ float red[2][NWV];
     __shared__ float part[NWV][D];
     attn_kernarg_fence(a, J_fixed);
     const int s = blockIdx.x, h = blockIdx.y;
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
             }
         }
     }
-    mx = block_max<NWV>(mx, red);
+    mx = block_max1<NWV>(mx, red[0]);
     if (!isfinite(mx)) mx = 0.0f;
     float sum = 0.0f;
     for (int j = tid; j < Jv; j += NT) {
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
         sc[j] = h2f(f2h(e));
         sum += e;
     }
-    sum = block_sum<NWV>(sum, red);
+    sum = block_sum1<NWV>(sum, red[1]);
     const bool degenerate = !(sum > 0.0f && isfinite(sum));
     const int Jp = degenerate ? J : Jv;
     const float uni = h2f(f2h(1.0f / (float)J));
