@@ -243,6 +243,12 @@ tlhip_status launch_attention_j(hipStream_t s, const AttnArgs& a, int J);
 // of attention_mfma_scratch() bytes (V transposed per KV head).
 bool attention_mfma_ok(const AttnArgs& a, int J);
 size_t attention_mfma_scratch(int J, int Hkv, int D);
+// Decode attention split over key chunks (head dims 80 / 128, caches of more
+// than 512 rows, position read on the device); scratch of
+// attention_split_scratch() bytes.
+bool attention_split_ok(const AttnArgs& a);
+size_t attention_split_scratch(int H, int kv_rows, int D);
+tlhip_status launch_attention_split(hipStream_t s, const AttnArgs& a, float* scratch);
 tlhip_status launch_attention_mfma(hipStream_t s, const AttnArgs& a, int J, uint16_t* vt);
 constexpr int kAttnMaxKeys = 8192;
 tlhip_status launch_copy_rows(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows,

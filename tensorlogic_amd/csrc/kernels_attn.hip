@@ -448,6 +448,202 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
 }
 
 // ---------------------------------------------------------------------------
+// Decode attention split over key chunks (head dims 80 / 128, long caches).
+// One workgroup per head streams every K/V row of the head through one CU
+// (~17 GB/s per CU for Phi-2's 5 KB-strided rows); here each head's keys
+// are cut into AS_CH-key chunks handled by separate workgroups, keeping the
+// rounding points of attention_dk_kernel:
+//   1 asplit_scores : s_j = f16(f16(q.k_j) * scale) (same lane order as the
+//                     one-workgroup kernel, so the same values) and each
+//                     chunk's max over finite scores
+//   2 asplit_exp    : global max from the chunk maxima (0 when none is
+//                     finite), e_j = f16(exp(s_j - max)) (0 for non-finite
+//                     s_j), chunk sums of the unrounded exp
+//   3 asplit_pv     : global sum in chunk order, P_j = f16(e_j / sum) (the
+//                     uniform f16(1/J) when the sum is not a positive finite
+//                     number), fp32 P.V partials per chunk
+//   4 asplit_combine: the partials summed in chunk order, f16 out.
+// Only the order of the fp32 sums differs from the one-workgroup kernel.
+// Decode only (one query row, causal, position read on the device); rows
+// are read at min(j, kv_rows - 1), inside the allocation.
+constexpr int AS_CH = 128, AS_NT = 256, AS_NG = AS_NT / 8, AS_U = AS_CH / AS_NG;
+
+struct SplitBufs {
+    float* e;      // [H][kv_rows] scores, then f16-rounded exp values
+    float* mx;     // [H][nch] chunk maxima
+    float* sum;    // [H][nch] chunk sums
+    float* o;      // [H][nch][D] P.V partials
+    int nch;
+};
+
+__device__ __forceinline__ int asplit_keys(const AttnArgs& a) {
+    return min(*a.d_pos + 1, a.kv_rows);
+}
+
+template <int D>
+__global__ __launch_bounds__(AS_NT) void asplit_scores_kernel(AttnArgs a, SplitBufs b) {
+    constexpr int EPL = D / 8, NW = EPL / 2, NWV = AS_NT / 64;
+    __shared__ float red[NWV];
+    const int ch = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, c = tid & 7, g = tid >> 3;
+    const int kvh = h / (a.H / a.Hkv);
+    const size_t wstride = (size_t)a.Hkv * D / 2;
+    const uint32_t* kbase = (const uint32_t*)(a.k + (size_t)kvh * D + EPL * c);
+    const int j0 = ch * AS_CH;
+    uint32_t kw[AS_U][NW];
+#pragma unroll
+    for (int u = 0; u < AS_U; u++) load_row_words<NW>(kbase + (size_t)min(j0 + g + AS_NG * u, a.kv_rows - 1) * wstride, kw[u]);
+    float qf[EPL];
+    {
+        const uint32_t* qw = (const uint32_t*)(a.q + (size_t)h * D + EPL * c);
+#pragma unroll
+        for (int t = 0; t < NW; t++) {
+            const h2 p2 = as_h2(qw[t]);
+            qf[2 * t] = (float)p2[0];
+            qf[2 * t + 1] = (float)p2[1];
+        }
+    }
+    const int J = asplit_keys(a);
+    if (j0 >= J) return;   // (uniform: chunk past the keys)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < AS_U; u++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NW; t++) {
+            const h2 k2 = as_h2(kw[u][t]);
+            acc += qf[2 * t] * (float)k2[0];
+            acc += qf[2 * t + 1] * (float)k2[1];
+        }
+        acc = group8_sum(acc);
+        const int j = j0 + g + AS_NG * u;
+        if (j < J) {
+            const float v = h2f(f2h(h2f(f2h(acc)) * a.scale_h));
+            if (c == 0) b.e[(size_t)h * a.kv_rows + j] = v;
+            if (isfinite(v)) mx = fmaxf(mx, v);
+        }
+    }
+    mx = block_max1<NWV>(mx, red);
+    if (tid == 0) b.mx[(size_t)h * b.nch + ch] = mx;
+}
+
+template <int D>
+__global__ __launch_bounds__(AS_NT) void asplit_exp_kernel(AttnArgs a, SplitBufs b) {
+    constexpr int NWV = AS_NT / 64;
+    __shared__ float red[NWV];
+    const int ch = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const int J = asplit_keys(a);
+    const int nc = (J + AS_CH - 1) / AS_CH;
+    if (ch >= nc) return;
+    float gmax = -INFINITY;
+    for (int k = 0; k < nc; k++) gmax = fmaxf(gmax, b.mx[(size_t)h * b.nch + k]);
+    if (!isfinite(gmax)) gmax = 0.0f;
+    float sum = 0.0f;
+    const int j = ch * AS_CH + tid;
+    if (tid < AS_CH && j < J) {
+        float* ep = b.e + (size_t)h * a.kv_rows + j;
+        const float v = *ep;
+        const float e = isfinite(v) ? expf(v - gmax) : 0.0f;
+        *ep = h2f(f2h(e));
+        sum = e;
+    }
+    sum = block_sum1<NWV>(sum, red);
+    if (tid == 0) b.sum[(size_t)h * b.nch + ch] = sum;
+}
+
+template <int D>
+__global__ __launch_bounds__(AS_NT) void asplit_pv_kernel(AttnArgs a, SplitBufs b) {
+    constexpr int EPL = D / 8, NW = EPL / 2, NWV = AS_NT / 64;
+    __shared__ float part[NWV][D];
+    const int ch = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, c = tid & 7, g = tid >> 3;
+    const int kvh = h / (a.H / a.Hkv);
+    const size_t wstride = (size_t)a.Hkv * D / 2;
+    const uint32_t* vbase = (const uint32_t*)(a.v + (size_t)kvh * D + EPL * c);
+    const int j0 = ch * AS_CH;
+    uint32_t vw[AS_U][NW];
+#pragma unroll
+    for (int u = 0; u < AS_U; u++) load_row_words<NW>(vbase + (size_t)min(j0 + g + AS_NG * u, a.kv_rows - 1) * wstride, vw[u]);
+    const int J = asplit_keys(a);
+    const int nc = (J + AS_CH - 1) / AS_CH;
+    if (ch >= nc) return;
+    float gsum = 0.0f;
+    for (int k = 0; k < nc; k++) gsum += b.sum[(size_t)h * b.nch + k];
+    const bool degenerate = !(gsum > 0.0f && isfinite(gsum));
+    const float uni = h2f(f2h(1.0f / (float)J));
+    float o[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; e++) o[e] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < AS_U; u++) {
+        const int j = j0 + g + AS_NG * u;
+        if (j < J) {
+            const float pj = degenerate ? uni : h2f(f2h(b.e[(size_t)h * a.kv_rows + j] / gsum));
+#pragma unroll
+            for (int t = 0; t < NW; t++) {
+                const h2 v2 = as_h2(vw[u][t]);
+                o[2 * t] += pj * (float)v2[0];
+                o[2 * t + 1] += pj * (float)v2[1];
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; e++) o[e] = stride8_sum(o[e]);
+    if ((tid & 63) < 8)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) part[tid >> 6][EPL * c + e] = o[e];
+    lds_barrier();
+    if (tid < D) {
+        float t = part[0][tid];
+#pragma unroll
+        for (int wv = 1; wv < NWV; wv++) t += part[wv][tid];
+        b.o[((size_t)h * b.nch + ch) * D + tid] = t;
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(D) void asplit_combine_kernel(AttnArgs a, SplitBufs b) {
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int J = asplit_keys(a);
+    const int nc = (J + AS_CH - 1) / AS_CH;
+    float t = 0.0f;
+    for (int k = 0; k < nc; k++) t += b.o[((size_t)h * b.nch + k) * D + tid];
+    a.out[(size_t)h * D + tid] = f2h(t);   // (one query row)
+}
+
+bool attention_split_ok(const AttnArgs& a) {
+    return a.d_pos && a.S == 1 && a.causal && (a.D == 80 || a.D == 128) && a.kv_rows > 512 && a.Hkv > 0 &&
+           a.H % a.Hkv == 0;
+}
+
+size_t attention_split_scratch(int H, int kv_rows, int D) {
+    const size_t nch = (size_t)(kv_rows + AS_CH - 1) / AS_CH;
+    return ((size_t)H * kv_rows + 2 * (size_t)H * nch + (size_t)H * nch * D) * sizeof(float);
+}
+
+tlhip_status launch_attention_split(hipStream_t s, const AttnArgs& a, float* scratch) {
+    if (!attention_split_ok(a) || !scratch)
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "attention: split decode path needs a device position, S = 1, D 80/128");
+    SplitBufs b;
+    b.nch = (a.kv_rows + AS_CH - 1) / AS_CH;
+    b.e = scratch;
+    b.mx = b.e + (size_t)a.H * a.kv_rows;
+    b.sum = b.mx + (size_t)a.H * b.nch;
+    b.o = b.sum + (size_t)a.H * b.nch;
+    const dim3 grid((unsigned)b.nch, (unsigned)a.H);
+    if (a.D == 80) {
+        hipLaunchKernelGGL(asplit_scores_kernel<80>, grid, dim3(AS_NT), 0, s, a, b);
+        hipLaunchKernelGGL(asplit_exp_kernel<80>, grid, dim3(AS_NT), 0, s, a, b);
+        hipLaunchKernelGGL(asplit_pv_kernel<80>, grid, dim3(AS_NT), 0, s, a, b);
+        hipLaunchKernelGGL(asplit_combine_kernel<80>, dim3((unsigned)a.H), dim3(80), 0, s, a, b);
+    } else {
+        hipLaunchKernelGGL(asplit_scores_kernel<128>, grid, dim3(AS_NT), 0, s, a, b);
+        hipLaunchKernelGGL(asplit_exp_kernel<128>, grid, dim3(AS_NT), 0, s, a, b);
+        hipLaunchKernelGGL(asplit_pv_kernel<128>, grid, dim3(AS_NT), 0, s, a, b);
+        hipLaunchKernelGGL(asplit_combine_kernel<128>, dim3((unsigned)a.H), dim3(128), 0, s, a, b);
+    }
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
 // Prefill attention on the matrix cores (S >= 32 query rows, head_dim a
 // multiple of 16 up to 128).  Same arithmetic and rounding points as the
 // kernels above -- f16 scores, f16 scale, masked keys skipped, exp in f32,

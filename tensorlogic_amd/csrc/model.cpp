@@ -64,6 +64,7 @@ struct tlhip_model_s {
                  logits = nullptr;
     unsigned long long* d_amax = nullptr;   // per-workgroup greedy keys of the lm_head GEMV
     uint16_t* d_vt = nullptr;                // V transposed per KV head for matrix-core prefill attention
+    float* d_asplit = nullptr;               // decode attention split over key chunks (long caches)
     void* d_sample = nullptr;                // per-slice statistics of the temperature sampler
     float* ws = nullptr;          // split-K partials of the prefill GEMMs
     size_t ws_bytes = 0;
@@ -402,7 +403,8 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
         at.scale_h = (float)(_Float16)(1.0f / sqrtf((float)D));
         if (decode) {
             at.d_pos = d_pos;
-            TLHIP_TRY(launch_attention(s, at));
+            if (m->d_asplit && attention_split_ok(at)) TLHIP_TRY(launch_attention_split(s, at, m->d_asplit));
+            else TLHIP_TRY(launch_attention(s, at));
         } else {
             at.q_pos0 = pos0;
             if (attention_mfma_ok(at, pos0 + S)) TLHIP_TRY(launch_attention_mfma(s, at, pos0 + S, m->d_vt));
@@ -643,6 +645,7 @@ tlhip_status tlhip_model_free(tlhip_model m) {
     for (tlhip_tensor t : {m->x, m->xn, m->qkv, m->qrot, m->att, m->hmid, m->logits}) tlhip_tensor_free(t);
     if (m->d_amax) (void)hipFree(m->d_amax);
     if (m->d_vt) (void)hipFree(m->d_vt);
+    if (m->d_asplit) (void)hipFree(m->d_asplit);
     if (m->d_sample) (void)hipFree(m->d_sample);
     if (m->ws) (void)hipFree(m->ws);
     if (m->d_state) (void)hipFree(m->d_state);
@@ -749,6 +752,17 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
         hipError_t e = hipMalloc(&m->d_state, 4 * sizeof(int32_t));
         if (e == hipSuccess) e = hipMalloc(&m->d_amax, sizeof(unsigned long long) * gemv_norm_slots(m->vocab));
         if (e == hipSuccess) e = hipMalloc(&m->d_vt, attention_mfma_scratch(m->max_ctx, m->n_kv, m->head_dim));
+        {
+            AttnArgs probe;
+            probe.d_pos = (const int32_t*)m->d_state;
+            probe.S = 1;
+            probe.H = m->n_heads;
+            probe.Hkv = m->n_kv;
+            probe.D = m->head_dim;
+            probe.kv_rows = m->max_ctx;
+            if (e == hipSuccess && attention_split_ok(probe))
+                e = hipMalloc(&m->d_asplit, attention_split_scratch(m->n_heads, m->max_ctx, m->head_dim));
+        }
         if (e == hipSuccess) e = hipMalloc(&m->d_sample, sample_scratch_bytes(m->vocab));
         // split-K workspace: the largest partial set any prefill GEMM of this model uses
         if (e == hipSuccess) {
