@@ -454,24 +454,25 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
 // are cut into AS_CH-key chunks handled by separate workgroups, keeping the
 // rounding points of attention_dk_kernel:
 //   1 asplit_scores : s_j = f16(f16(q.k_j) * scale) (same lane order as the
-//                     one-workgroup kernel, so the same values) and each
-//                     chunk's max over finite scores
-//   2 asplit_exp    : global max from the chunk maxima (0 when none is
-//                     finite), e_j = f16(exp(s_j - max)) (0 for non-finite
-//                     s_j), chunk sums of the unrounded exp
-//   3 asplit_pv     : global sum in chunk order, P_j = f16(e_j / sum) (the
-//                     uniform f16(1/J) when the sum is not a positive finite
-//                     number), fp32 P.V partials per chunk
-//   4 asplit_combine: the partials summed in chunk order, f16 out.
-// Only the order of the fp32 sums differs from the one-workgroup kernel.
+//                     one-workgroup kernel, so the same values), each
+//                     chunk's max m_c over finite scores and its sum of
+//                     exp(s_j - m_c)
+//   2 asplit_pv     : global max M = max m_c (0 when none is finite), global
+//                     sum = sum_c sum_c * exp(m_c - M) in chunk order (the
+//                     reference's sum of exp(s_j - M), re-associated: ~1e-7
+//                     relative), e_j = f16(exp(s_j - M)) (0 for non-finite
+//                     s_j), P_j = f16(e_j / sum) (the uniform f16(1/J) when
+//                     the sum is not a positive finite number), fp32 P.V
+//                     partials per chunk
+//   3 asplit_combine: the partials summed in chunk order, f16 out.
 // Decode only (one query row, causal, position read on the device); rows
 // are read at min(j, kv_rows - 1), inside the allocation.
 constexpr int AS_CH = 128, AS_NT = 256, AS_NG = AS_NT / 8, AS_U = AS_CH / AS_NG;
 
 struct SplitBufs {
-    float* e;      // [H][kv_rows] scores, then f16-rounded exp values
+    float* e;      // [H][kv_rows] scores
     float* mx;     // [H][nch] chunk maxima
-    float* sum;    // [H][nch] chunk sums
+    float* sum;    // [H][nch] chunk sums of exp(s - chunk max)
     float* o;      // [H][nch][D] P.V partials
     int nch;
 };
@@ -483,7 +484,7 @@ __device__ __forceinline__ int asplit_keys(const AttnArgs& a) {
 template <int D>
 __global__ __launch_bounds__(AS_NT) void asplit_scores_kernel(AttnArgs a, SplitBufs b) {
     constexpr int EPL = D / 8, NW = EPL / 2, NWV = AS_NT / 64;
-    __shared__ float red[NWV];
+    __shared__ float red[2][NWV];
     const int ch = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, c = tid & 7, g = tid >> 3;
     const int kvh = h / (a.H / a.Hkv);
     const size_t wstride = (size_t)a.Hkv * D / 2;
@@ -504,7 +505,7 @@ __global__ __launch_bounds__(AS_NT) void asplit_scores_kernel(AttnArgs a, SplitB
     }
     const int J = asplit_keys(a);
     if (j0 >= J) return;   // (uniform: chunk past the keys)
-    float mx = -INFINITY;
+    float mx = -INFINITY, sv[AS_U];
 #pragma unroll
     for (int u = 0; u < AS_U; u++) {
         float acc = 0.0f;
@@ -516,38 +517,28 @@ __global__ __launch_bounds__(AS_NT) void asplit_scores_kernel(AttnArgs a, SplitB
         }
         acc = group8_sum(acc);
         const int j = j0 + g + AS_NG * u;
+        sv[u] = -INFINITY;
         if (j < J) {
             const float v = h2f(f2h(h2f(f2h(acc)) * a.scale_h));
             if (c == 0) b.e[(size_t)h * a.kv_rows + j] = v;
-            if (isfinite(v)) mx = fmaxf(mx, v);
+            if (isfinite(v)) {
+                mx = fmaxf(mx, v);
+                sv[u] = v;
+            }
         }
     }
-    mx = block_max1<NWV>(mx, red);
-    if (tid == 0) b.mx[(size_t)h * b.nch + ch] = mx;
-}
-
-template <int D>
-__global__ __launch_bounds__(AS_NT) void asplit_exp_kernel(AttnArgs a, SplitBufs b) {
-    constexpr int NWV = AS_NT / 64;
-    __shared__ float red[NWV];
-    const int ch = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-    const int J = asplit_keys(a);
-    const int nc = (J + AS_CH - 1) / AS_CH;
-    if (ch >= nc) return;
-    float gmax = -INFINITY;
-    for (int k = 0; k < nc; k++) gmax = fmaxf(gmax, b.mx[(size_t)h * b.nch + k]);
-    if (!isfinite(gmax)) gmax = 0.0f;
-    float sum = 0.0f;
-    const int j = ch * AS_CH + tid;
-    if (tid < AS_CH && j < J) {
-        float* ep = b.e + (size_t)h * a.kv_rows + j;
-        const float v = *ep;
-        const float e = isfinite(v) ? expf(v - gmax) : 0.0f;
-        *ep = h2f(f2h(e));
-        sum = e;
+    mx = block_max1<NWV>(mx, red[0]);
+    // the chunk's sum of exp(s - chunk max), one term per key (lane c = 0)
+    float se = 0.0f;
+    if (c == 0 && isfinite(mx))
+#pragma unroll
+        for (int u = 0; u < AS_U; u++)
+            if (isfinite(sv[u])) se += expf(sv[u] - mx);
+    se = block_sum1<NWV>(se, red[1]);
+    if (tid == 0) {
+        b.mx[(size_t)h * b.nch + ch] = mx;
+        b.sum[(size_t)h * b.nch + ch] = se;
     }
-    sum = block_sum1<NWV>(sum, red);
-    if (tid == 0) b.sum[(size_t)h * b.nch + ch] = sum;
 }
 
 template <int D>
@@ -565,8 +556,14 @@ __global__ __launch_bounds__(AS_NT) void asplit_pv_kernel(AttnArgs a, SplitBufs 
     const int J = asplit_keys(a);
     const int nc = (J + AS_CH - 1) / AS_CH;
     if (ch >= nc) return;
+    float gmax = -INFINITY;
+    for (int k = 0; k < nc; k++) gmax = fmaxf(gmax, b.mx[(size_t)h * b.nch + k]);
+    if (!isfinite(gmax)) gmax = 0.0f;
     float gsum = 0.0f;
-    for (int k = 0; k < nc; k++) gsum += b.sum[(size_t)h * b.nch + k];
+    for (int k = 0; k < nc; k++) {
+        const float mk = b.mx[(size_t)h * b.nch + k];
+        if (isfinite(mk)) gsum += b.sum[(size_t)h * b.nch + k] * expf(mk - gmax);
+    }
     const bool degenerate = !(gsum > 0.0f && isfinite(gsum));
     const float uni = h2f(f2h(1.0f / (float)J));
     float o[EPL];
@@ -576,7 +573,9 @@ __global__ __launch_bounds__(AS_NT) void asplit_pv_kernel(AttnArgs a, SplitBufs 
     for (int u = 0; u < AS_U; u++) {
         const int j = j0 + g + AS_NG * u;
         if (j < J) {
-            const float pj = degenerate ? uni : h2f(f2h(b.e[(size_t)h * a.kv_rows + j] / gsum));
+            const float sj = b.e[(size_t)h * a.kv_rows + j];
+            const float ej = isfinite(sj) ? h2f(f2h(expf(sj - gmax))) : 0.0f;
+            const float pj = degenerate ? uni : h2f(f2h(ej / gsum));
 #pragma unroll
             for (int t = 0; t < NW; t++) {
                 const h2 v2 = as_h2(vw[u][t]);
@@ -631,12 +630,10 @@ tlhip_status launch_attention_split(hipStream_t s, const AttnArgs& a, float* scr
     const dim3 grid((unsigned)b.nch, (unsigned)a.H);
     if (a.D == 80) {
         hipLaunchKernelGGL(asplit_scores_kernel<80>, grid, dim3(AS_NT), 0, s, a, b);
-        hipLaunchKernelGGL(asplit_exp_kernel<80>, grid, dim3(AS_NT), 0, s, a, b);
         hipLaunchKernelGGL(asplit_pv_kernel<80>, grid, dim3(AS_NT), 0, s, a, b);
         hipLaunchKernelGGL(asplit_combine_kernel<80>, dim3((unsigned)a.H), dim3(80), 0, s, a, b);
     } else {
         hipLaunchKernelGGL(asplit_scores_kernel<128>, grid, dim3(AS_NT), 0, s, a, b);
-        hipLaunchKernelGGL(asplit_exp_kernel<128>, grid, dim3(AS_NT), 0, s, a, b);
         hipLaunchKernelGGL(asplit_pv_kernel<128>, grid, dim3(AS_NT), 0, s, a, b);
         hipLaunchKernelGGL(asplit_combine_kernel<128>, dim3((unsigned)a.H), dim3(128), 0, s, a, b);
     }
