@@ -121,30 +121,6 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// Workgroup max / sum over NWV waves in a fixed order.
-template <int NWV>
-__device__ __forceinline__ float block_max(float v, float* red) {
-    v = wave_max(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float t = red[0];
-#pragma unroll
-    for (int k = 1; k < NWV; k++) t = fmaxf(t, red[k]);
-    return t;
-}
-template <int NWV>
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    v = wave_sum<64>(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float t = red[0];
-#pragma unroll
-    for (int k = 1; k < NWV; k++) t += red[k];
-    return t;
-}
-
 // Single-barrier workgroup max / sum: the caller must not write `red` again
 // before another barrier (use one array per reduction).  The barrier also
 // publishes every LDS write made before the call.
