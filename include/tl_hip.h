@@ -219,6 +219,16 @@ tlhip_status tlhip_kvcache_append(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlh
  * storage; later appends do not change the view's length).               */
 tlhip_status tlhip_kvcache_get(tlhip_kvcache c, int layer, int which_v, tlhip_tensor* out);
 int tlhip_kvcache_len(tlhip_kvcache c, int layer);
+/* Attention against a cache layer after cache.append -- the TL program's
+ * get_k / get_v followed by einsum, scale, causal mask, softmax, einsum
+ * (chat_demo_with_kvcache.tl, einsum.rs:653-886, masking.rs:147-165,
+ * activations.rs:107-230): q [S, H, D] are the queries of the cache's last
+ * S positions (len - S .. len - 1), causal; out [S, H, D].  _decode takes
+ * the single new row (S = 1).  Same kernels and bars as tlhip_attention. */
+tlhip_status tlhip_attention_prefill(tlhip_ctx ctx, tlhip_tensor q, tlhip_kvcache c, int layer, float scale,
+                                     tlhip_tensor out);
+tlhip_status tlhip_attention_decode(tlhip_ctx ctx, tlhip_tensor q, tlhip_kvcache c, int layer, float scale,
+                                    tlhip_tensor out);
 
 /* ---- decoder runner (the op sequence of debug/chat_demo_with_kvcache.tl,
  *      fused; arch 0 = llama/TinyLlama, 1 = phi2) ------------------------- */

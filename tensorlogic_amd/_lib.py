@@ -71,6 +71,8 @@ SIGNATURES = {
     "tlhip_embedding": (_i, [_vp, _vp, _i32p, _i, _vp]),
     "tlhip_apply_attention_mask": (_i, [_vp, _vp, _vp, _vp]),
     "tlhip_causal_mask": (_i, [_vp, _vp]),
+    "tlhip_attention_prefill": (_i, [_vp, _vp, _vp, _i, _f, _vp]),
+    "tlhip_attention_decode": (_i, [_vp, _vp, _vp, _i, _f, _vp]),
     "tlhip_slice_last": (_i, [_vp, _vp, _i, _vp]),
     "tlhip_broadcast_to": (_i, [_vp, _vp, _vp]),
     "tlhip_rope_cos_sin": (_i, [_vp, _vp, _vp, _vp, _vp]),

@@ -619,6 +619,36 @@ int tlhip_kvcache_len(tlhip_kvcache c, int layer) {
     return c->len[layer];
 }
 
+// Attention of S query rows against a KV cache layer after cache.append (the
+// TL program's get_k / get_v + einsum / mask / softmax / einsum sequence):
+// the queries are the cache's last S positions, len - S .. len - 1, causal.
+tlhip_status tlhip_attention_prefill(tlhip_ctx ctx, tlhip_tensor q, tlhip_kvcache c, int layer, float scale,
+                                     tlhip_tensor out) {
+    if (!c || layer < 0 || layer >= c->n_layers) return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "kvcache layer %d", layer);
+    TLHIP_TRY(check_t(q, "attention_prefill"));
+    if (q->ndim != 3) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention_prefill: q must be [S, H, D]");
+    const int len = c->len[layer];
+    const int64_t S = q->shape[0];
+    if (S < 1 || S > len)
+        return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: %lld query rows for a cache of %d rows", (long long)S, len);
+    tlhip_tensor k = nullptr, v = nullptr;
+    TLHIP_TRY(tlhip_kvcache_get(c, layer, 0, &k));
+    tlhip_status st = tlhip_kvcache_get(c, layer, 1, &v);
+    if (st == TLHIP_OK) st = tlhip_attention(ctx, q, k, v, len - (int)S, scale, 1, out);
+    (void)tlhip_tensor_free(k);
+    if (v) (void)tlhip_tensor_free(v);
+    return st;
+}
+
+// One decode row: q [1, H, D] at the cache's last position.
+tlhip_status tlhip_attention_decode(tlhip_ctx ctx, tlhip_tensor q, tlhip_kvcache c, int layer, float scale,
+                                    tlhip_tensor out) {
+    TLHIP_TRY(check_t(q, "attention_decode"));
+    if (q->ndim != 3 || q->shape[0] != 1)
+        return fail(TLHIP_ERR_INVALID_DIMENSION, "attention_decode: q must be [1, H, D], got %s", shape_str(q).c_str());
+    return tlhip_attention_prefill(ctx, q, c, layer, scale, out);
+}
+
 // ---------------------------------------------------------------------------
 // model
 // ---------------------------------------------------------------------------

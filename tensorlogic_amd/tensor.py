@@ -356,6 +356,15 @@ class KVCache:
     def len(self, layer: int) -> int:
         return lib().tlhip_kvcache_len(self.h, layer)
 
+    def attention(self, q: Tensor, layer: int, scale: float) -> Tensor:
+        """Causal attention of q [S, H, D] -- the queries of the layer's last S
+        positions -- against the cached K/V (get_k/get_v + the einsum /
+        mask / softmax sequence); S = 1 is the decode step."""
+        out = self.dev.empty(q.shape)
+        fn = "tlhip_attention_decode" if q.shape[0] == 1 else "tlhip_attention_prefill"
+        call(fn, self.dev.h, q.h, self.h, int(layer), float(scale), out.h)
+        return out
+
 
 class GGUF:
     def __init__(self, path: str):

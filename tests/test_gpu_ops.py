@@ -407,6 +407,33 @@ def test_temperature_sample_distribution(dev):
     assert np.abs(freq - p).max() < 5 * np.sqrt(p.max() * (1 - p.max()) / n)
 
 
+@pytest.mark.parametrize("H,Hkv,D", [(32, 4, 64), (4, 4, 80)])
+def test_kvcache_attention(dev, oracle, H, Hkv, D):
+    """The TL cache flow: set a 46-row prompt, attend it (prefill), append one
+    row at a time and attend each (decode); every output equals the oracle's
+    attention of the same queries at positions len - S .. len - 1."""
+    c = KVCache(dev, 1, 64, Hkv, D)
+    k0, v0 = S.normal_f16(14, "ck0", (46, Hkv, D)), S.normal_f16(14, "cv0", (46, Hkv, D))
+    q0 = S.normal_f16(14, "cq0", (46, H, D))
+    c.set(0, dev.tensor(k0), dev.tensor(v0))
+    scale = 1 / np.sqrt(D)
+    got = c.attention(dev.tensor(q0), 0, scale).numpy()
+    assert_close(got, oracle.attention(q0, k0, v0, 0, scale, True), what="cache prefill")
+    ks, vs = [k0], [v0]
+    for t in range(3):
+        k1, v1 = S.normal_f16(15 + t, "ck", (1, Hkv, D)), S.normal_f16(15 + t, "cv", (1, Hkv, D))
+        q1 = S.normal_f16(15 + t, "cq", (1, H, D))
+        c.append(0, dev.tensor(k1), dev.tensor(v1))
+        ks.append(k1)
+        vs.append(v1)
+        got = c.attention(dev.tensor(q1), 0, scale).numpy()
+        kk, vv = np.concatenate(ks), np.concatenate(vs)
+        assert_close(got, oracle.attention(q1, kk, vv, kk.shape[0] - 1, scale, True), what=f"cache decode {t}")
+    with pytest.raises(TLHipError) as e:   # more query rows than the cache holds
+        c.attention(dev.tensor(S.normal_f16(16, "cqx", (60, H, D))), 0, scale)
+    assert e.value.kind == "InvalidDimension"
+
+
 def test_kvcache(dev):
     c = KVCache(dev, 2, 16, 4, 8)
     k1, v1 = S.normal_f16(13, "k1", (5, 4, 8)), S.normal_f16(13, "v1", (5, 4, 8))
