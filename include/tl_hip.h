@@ -128,6 +128,17 @@ tlhip_status tlhip_dequantize(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor out_f1
  * accumulation, f16 out.  W may be F16, Q4_0 or Q8_0; M <= 4 uses the
  * fused dequant-GEMV, larger M the MFMA dequant-GEMM.  bias may be NULL.  */
 tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y);
+/* linear(x, W[, b]) exactly as tlhip_linear (same checks, kernels and bits),
+ * but allocating nothing: no counterpart in the reference.  It is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The split-K
+ * partials of the MFMA GEMM live in a 16 MiB device array that each GPU holds
+ * from library load to process end (partials beyond it -> AllocationError;
+ * the library's split policy needs at most 10.5 MB).  A Q6_K weight with
+ * M > 4 needs a dequantised f16 copy and is refused (InvalidOperation).  All
+ * calls on one GPU share that array: calls overlapping in time on one GPU
+ * (several contexts or threads) race and must be serialised by the caller. */
+tlhip_status tlhip_linear_noalloc(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y);
 /* matmul(a, b) (builtin_math.rs:39, matmul.rs:52-197): c[M,N] = a[M,K] b[K,N]. */
 tlhip_status tlhip_matmul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor c);
 /* rms_norm(x, w[, eps]) (builtin_nn.rs:44-103, normalization.rs:42-250)

@@ -56,6 +56,7 @@ SIGNATURES = {
     "tlhip_gguf_kv_f32": (_i, [_vp, C.c_char_p, C.POINTER(_f)]),
     "tlhip_dequantize": (_i, [_vp, _vp, _vp]),
     "tlhip_linear": (_i, [_vp, _vp, _vp, _vp, _vp]),
+    "tlhip_linear_noalloc": (_i, [_vp, _vp, _vp, _vp, _vp]),
     "tlhip_matmul": (_i, [_vp, _vp, _vp, _vp]),
     "tlhip_rms_norm": (_i, [_vp, _vp, _vp, _f, _vp]),
     "tlhip_layer_norm": (_i, [_vp, _vp, _vp, _vp, _f, _vp]),

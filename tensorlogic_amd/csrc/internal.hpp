@@ -113,6 +113,16 @@ tlhip_status after_launch(tlhip_ctx ctx, const char* op);
 tlhip_status alloc_tensor(tlhip_ctx ctx, tlhip_dtype dtype, int ndim, const int64_t* shape,
                           tlhip_tensor* out);
 
+// linear(x, W[, b]) behind tlhip_linear (fixed_ws = nullptr: split-K
+// partials and the Q6_K f16 copy come from the stream-ordered pool) and
+// tlhip_linear_noalloc (fixed_ws = a workspace of fixed_ws_bytes that the
+// caller owns; nothing is allocated, Q6_K with M > 4 is refused).
+tlhip_status linear_impl(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y,
+                         float* fixed_ws, size_t fixed_ws_bytes);
+// Once per device, with that device current (tlhip_init): resolves the
+// device address of the no-allocation entry point's workspace.
+tlhip_status noalloc_setup(int device);
+
 // RoPE cos/sin table for (theta, rot_dims) covering positions [0, need_pos).
 tlhip_status rope_table(tlhip_ctx ctx, float theta, int rot_dims, int need_pos, const float** dev);
 

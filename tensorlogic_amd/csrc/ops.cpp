@@ -51,6 +51,15 @@ tlhip_status tlhip_dequantize(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor out) {
 }
 
 tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y) {
+    return linear_impl(ctx, x, w, bias, y, nullptr, 0);
+}
+
+}  // extern "C"
+
+namespace tlhip {
+
+tlhip_status linear_impl(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y,
+                         float* fixed_ws, size_t fixed_ws_bytes) {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("linear", {x, y}));
     TLHIP_TRY(check_t(w, "linear weight"));
@@ -86,10 +95,15 @@ tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_t
         if (st != TLHIP_OK) (void)hipGetLastError();
     }
     if (st == TLHIP_OK) return after_launch(ctx, "linear");
+    const bool no_alloc = fixed_ws != nullptr;
     // Q6_K weights reach the MFMA GEMM as their dequantised f16 copy (the
     // reference's own representation), from the stream-ordered pool
     tlhip_tensor wf = nullptr;
     tlhip_dtype wt = w->dtype;
+    if (wt == TLHIP_Q6_K && no_alloc)
+        return fail(TLHIP_ERR_INVALID_OPERATION,
+                    "linear_noalloc: a Q6_K weight with M = %lld > 4 needs a dequantised f16 copy, which "
+                    "this entry point cannot allocate (use tlhip_linear)", (long long)M);
     if (wt == TLHIP_Q6_K) {
         int64_t shp[2] = {N, K};
         TLHIP_TRY(alloc_tensor(ctx, TLHIP_F16, 2, shp, &wf));
@@ -106,11 +120,21 @@ tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_t
     // output has too few tiles to fill the device
     tlhip_tensor ws = nullptr;
     const int sp = gemm_splits((int)M, (int)N, (int)K);
-    if (sp > 1) {
+    const size_t need = (size_t)sp * M * N * sizeof(float);
+    if (sp > 1 && no_alloc) {
+        // the caller's fixed workspace: the same split as the pool path, so
+        // the same kernels and the same bits
+        if (need > fixed_ws_bytes)
+            return fail(TLHIP_ERR_ALLOCATION,
+                        "linear_noalloc: split-K partials of %zu bytes for [%lld x %lld] exceed the fixed "
+                        "workspace of %zu bytes", need, (long long)M, (long long)N, fixed_ws_bytes);
+        a.ws = fixed_ws;
+        a.ws_bytes = need;
+    } else if (sp > 1) {
         int64_t shp[1] = {(int64_t)sp * M * N};
         if (alloc_tensor(ctx, TLHIP_F32, 1, shp, &ws) == TLHIP_OK) {
             a.ws = (float*)ws->data;
-            a.ws_bytes = (size_t)sp * M * N * sizeof(float);
+            a.ws_bytes = need;
         }
     }
     st = launch_gemm(ctx->stream, wt, a, epi);
@@ -119,6 +143,10 @@ tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_t
     TLHIP_TRY(st);
     return after_launch(ctx, "linear");
 }
+
+}  // namespace tlhip
+
+extern "C" {
 
 tlhip_status tlhip_matmul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor c) {
     TLHIP_TRY(check_ctx(ctx));

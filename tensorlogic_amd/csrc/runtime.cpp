@@ -216,6 +216,8 @@ tlhip_status tlhip_init(int device, tlhip_ctx* out) {
     if (device < 0) device = 0;
     if (device >= n) return fail(TLHIP_ERR_DEVICE, "device %d out of range (%d devices)", device, n);
     TLHIP_CHECK_HIP(hipSetDevice(device));
+    // the no-allocation entry point's workspace address on this device
+    TLHIP_TRY(noalloc_setup(device));
     auto* c = new tlhip_ctx_s();
     c->device = device;
     hipError_t e1 = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
