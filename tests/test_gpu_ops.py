@@ -146,7 +146,9 @@ def test_linear_q6_k(dev, oracle, M, N, K):
 @pytest.mark.parametrize("qt", [Q4_0, Q8_0, F16])
 @pytest.mark.parametrize("M,N,K", [(46, 5632, 2048), (5, 64, 64), (64, 256, 512), (130, 96, 2048),
                                    (512, 512, 2048), (33, 100, 96), (17, 2048, 5632), (64, 130, 160),
-                                   (8, 40, 32), (512, 2048, 5632), (200, 384, 1024), (65, 256, 128)])
+                                   (8, 40, 32), (512, 2048, 5632), (200, 384, 1024), (65, 256, 128),
+                                   # config 2's remaining cells: M = 46 on W_down, M = 512 on W_up/gate
+                                   (46, 2048, 5632), (512, 5632, 2048)])
 def test_linear_gemm(dev, oracle, qt, M, N, K):
     x = S.normal_f16(3, f"x{M}x{K}", (M, K))
     if qt == F16:
@@ -212,7 +214,7 @@ def test_linear_shape_errors(dev):
 # normalisation, RoPE, softmax, elementwise
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("rows,n", [(1, 2048), (46, 2048), (34, 2048), (3, 4), (5, 2560), (3, 24), (2, 6144),
-                                    (1, 8192), (2, 8200)])
+                                    (1, 8192), (2, 8200), (2048, 2048)])
 def test_rms_norm(dev, oracle, rows, n):
     x = S.normal_f16(5, "x", (rows, n))
     w = S.normal_f16(5, "w", (n,), 1.0, 0.02)
@@ -243,7 +245,9 @@ def test_layer_norm(dev, oracle, rows, n):
 @pytest.mark.parametrize("S_,H,D,off,layout,rot", [
     (3, 2, 8, 0, ROPE_INTERLEAVED, 0),       # test_shader_mathematical_correctness.rs:66-101
     (46, 32, 64, 0, ROPE_INTERLEAVED, 0), (1, 32, 64, 34, ROPE_INTERLEAVED, 0),
-    (2048, 4, 64, 0, ROPE_NEOX, 0), (5, 32, 80, 511, ROPE_NEOX, 32)])
+    (2048, 4, 64, 0, ROPE_NEOX, 0), (5, 32, 80, 511, ROPE_NEOX, 32),
+    # config 3 at S = 2048: Q [2048, 32, 64] in both layouts, K [2048, 4, 64]
+    (2048, 32, 64, 0, ROPE_INTERLEAVED, 0), (2048, 32, 64, 0, ROPE_NEOX, 0), (2048, 4, 64, 0, ROPE_INTERLEAVED, 0)])
 def test_rope(dev, oracle, S_, H, D, off, layout, rot):
     if (S_, H, D) == (3, 2, 8):
         x = np.sin(0.1 * np.arange(S_ * H * D)).astype(np.float16).reshape(S_, H, D)
@@ -313,7 +317,9 @@ def test_mask_and_einsums(dev, oracle):
     (200, 200, 6, 3, 64, 0, True), (128, 300, 4, 4, 80, 0, False), (250, 90, 4, 2, 128, 0, False),
     # single-row kernels for other head dims around their 256 / 512-key passes
     (1, 100, 8, 8, 80, 99, True), (1, 300, 4, 4, 80, 299, True), (1, 513, 4, 2, 128, 512, True),
-    (3, 600, 4, 2, 80, 597, True), (2, 1100, 4, 4, 80, 0, False)])
+    (3, 600, 4, 2, 80, 597, True), (2, 1100, 4, 4, 80, 0, False),
+    # config 3 at its head layout: 32 query / 4 KV heads (GQA group 8), D = 64
+    (2048, 2048, 32, 4, 64, 0, True), (1, 2048, 32, 4, 64, 2047, True), (256, 1024, 32, 4, 64, 768, True)])
 def test_attention(dev, oracle, Sq, J, H, Hkv, D, q0, causal):
     q = S.normal_f16(11, "q", (Sq, H, D))
     k = S.normal_f16(11, "k", (J, Hkv, D))
@@ -432,6 +438,37 @@ def test_kvcache_attention(dev, oracle, H, Hkv, D):
     with pytest.raises(TLHipError) as e:   # more query rows than the cache holds
         c.attention(dev.tensor(S.normal_f16(16, "cqx", (60, H, D))), 0, scale)
     assert e.value.kind == "InvalidDimension"
+
+
+@pytest.mark.parametrize("H,Hkv,D", [(32, 32, 80), (8, 2, 128), (32, 4, 64)])
+def test_kvcache_attention_long(dev, oracle, H, Hkv, D):
+    """A cache filled in two prompt chunks of 300 rows (the second chunk's
+    causal prefill attends from q_pos0 = 300 through the matrix-core kernel),
+    then decode rows past 600 keys: for head dims 80 and 128 the one-row
+    kernel takes several 256 / 512-key passes with the key count known on the
+    host.  Every output equals the oracle's attention at the same positions."""
+    c = KVCache(dev, 1, 640, Hkv, D)
+    scale = 1 / np.sqrt(D)
+    ks, vs = [], []
+    for chunk in range(2):
+        k0 = S.normal_f16(60 + chunk, "lk", (300, Hkv, D))
+        v0 = S.normal_f16(60 + chunk, "lv", (300, Hkv, D))
+        q0 = S.normal_f16(60 + chunk, "lq", (300, H, D))
+        c.append(0, dev.tensor(k0), dev.tensor(v0))
+        ks.append(k0)
+        vs.append(v0)
+        kk, vv = np.concatenate(ks), np.concatenate(vs)
+        got = c.attention(dev.tensor(q0), 0, scale).numpy()
+        assert_close(got, oracle.attention(q0, kk, vv, 300 * chunk, scale, True), what=f"chunk {chunk}")
+    for t in range(3):
+        k1, v1 = S.normal_f16(70 + t, "lk1", (1, Hkv, D)), S.normal_f16(70 + t, "lv1", (1, Hkv, D))
+        q1 = S.normal_f16(70 + t, "lq1", (1, H, D))
+        c.append(0, dev.tensor(k1), dev.tensor(v1))
+        ks.append(k1)
+        vs.append(v1)
+        kk, vv = np.concatenate(ks), np.concatenate(vs)
+        got = c.attention(dev.tensor(q1), 0, scale).numpy()
+        assert_close(got, oracle.attention(q1, kk, vv, kk.shape[0] - 1, scale, True), what=f"decode {t}")
 
 
 def test_kvcache(dev):
