@@ -198,6 +198,35 @@ def config5_phi2(dev, steps: int = 256, n_prompt: int = 512, use_graph: bool = T
                 decode_hbm_gbs=wbytes * steps / (decode_ms / 1000.0) / 1e9)
 
 
+def op_by_op_decode(dev, path: str, prompt, steps: int, warmup: int = 2):
+    """debug/chat_demo_with_kvcache.tl run unchanged, one tlhip_* call per TL
+    builtin (tensorlogic_amd.program: ~37 calls per layer, no fusion, no
+    graph), greedy, at the program's literal semantics; wall-clock seconds
+    per decode token from Python over the C ABI, the per-token argmax read
+    back as the program's temperature_sample does.  Returns tok/s and the
+    token ids (for comparison with the fused runner in literal mode)."""
+    from tensorlogic_amd import temperature_sample
+    from tensorlogic_amd.program import ChatDemoKVCache
+    prog = ChatDemoKVCache(dev, path, max_ctx=len(prompt) + steps + warmup + 4)
+    t0 = time.perf_counter()
+    tok = temperature_sample(prog.prefill(prompt), 0.0)
+    prefill_s = time.perf_counter() - t0
+    toks = [tok]
+    for _ in range(warmup):
+        tok = temperature_sample(prog.decode(tok), 0.0)
+        toks.append(tok)
+    dev.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = temperature_sample(prog.decode(tok), 0.0)
+        toks.append(tok)
+    dev.sync()
+    dt = time.perf_counter() - t0
+    del prog
+    return dict(tok_s=steps / dt, ms_per_token=dt * 1e3 / steps, prefill_ms=prefill_s * 1e3,
+                steps=steps), toks
+
+
 def copy_reference(dev, iters: int):
     """Plain copy kernel: 6.5 MB (the GEMV's size, 48 rotating sources) and
     1 GiB -- the streaming bandwidth this device reaches at each size."""
@@ -386,7 +415,22 @@ def main():
     _, _, dms_t = m.bench_decode(prompt, args.steps, use_graph=use_graph)
     tok_s_t = args.steps / (dms_t / 1000.0)
     log(f"decode with temperature 0.8: {tok_s_t:.1f} tok/s")
+    # the program's literal semantics (decode rows rotated as position 0,
+    # rms_norm eps 1e-6) in the fused runner, then the same program op by op
+    m.set_sampling(0.0)
+    m.set_program_semantics(True)
+    m.generate(prompt, args.warmup, use_graph=use_graph)
+    lit_toks, _, dms_lit = m.bench_decode(prompt, args.steps, use_graph=use_graph)
+    tok_s_lit = args.steps / (dms_lit / 1000.0)
+    m.set_program_semantics(False)
     m.close()
+    log(f"decode, program semantics (fused runner): {tok_s_lit:.1f} tok/s")
+    obo_steps = min(args.steps, 16)
+    obo, obo_toks = op_by_op_decode(dev, path, prompt, obo_steps)
+    n_cmp = min(len(obo_toks), len(lit_toks))
+    obo_match = obo_toks[:n_cmp] == lit_toks.tolist()[:n_cmp]
+    log(f"decode, program op by op through the C ABI: {obo['tok_s']:.1f} tok/s "
+        f"({obo['ms_per_token']:.2f} ms/token); tokens equal to the fused runner's: {obo_match}")
 
     gem = gemv_roofline(dev, args.gemv_iters)
     for k, v in gem.items():
@@ -451,6 +495,11 @@ def main():
             "decode_launch": args.decode_launch,
             "decode_tokens": toks.tolist()[:8],
             "decode_tok_s_temperature_0.8": round(tok_s_t, 2),
+            "decode_tok_s_program_semantics_fused": round(tok_s_lit, 2),
+            "decode_op_by_op": dict({k: round(v, 3) for k, v in obo.items()},
+                                    what="debug/chat_demo_with_kvcache.tl one tlhip_* call per TL builtin from "
+                                         "Python (literal semantics, greedy, wall clock)",
+                                    tokens_equal_fused_literal=obo_match),
             "hbm_bytes_per_token": weights_per_token,
             "decode_hbm_roofline_frac": round(tok_s * weights_per_token / (HBM_PEAK_GBS * 1e9), 4),
             "gemv_2048x5632": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in gem.items()},

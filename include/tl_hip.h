@@ -218,11 +218,14 @@ tlhip_status tlhip_temperature_sample(tlhip_ctx ctx, tlhip_tensor logits, float 
 /* ---- KV cache (model::llama::Cache, llama.rs:50-114; KVCache builtins
  *      eval.rs:1247-1400), preallocated instead of concat-grown ----------- */
 typedef struct tlhip_kvcache_s* tlhip_kvcache;
-/* KVCache::new_f16(n_layers) with room for max_ctx rows of [Hkv, D].      */
+/* KVCache::new_f16(n_layers) with room for max_ctx rows of [Hkv, D];
+ * max_ctx <= 8192, the most keys the attention entry points read
+ * (InvalidDimension beyond).                                              */
 tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads,
                                   int head_dim, tlhip_kvcache* out);
 tlhip_status tlhip_kvcache_free(tlhip_kvcache c);
-/* cache.set(layer, K, V): replaces the layer's contents with K,V [S,Hkv,D]. */
+/* cache.set(layer, K, V): replaces the layer's contents with K,V [S,Hkv,D]
+ * (K and V of the same shape, else ShapeMismatch).                       */
 tlhip_status tlhip_kvcache_set(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v);
 /* cache.append(layer, K, V): appends S rows. */
 tlhip_status tlhip_kvcache_append(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v);
@@ -259,6 +262,16 @@ tlhip_status tlhip_model_generate(tlhip_model m, const int32_t* prompt, int n_pr
                                   int n_decode, int use_graph, int32_t* tokens_out);
 /* Copies the last computed logits row (f16, vocab entries) to host.       */
 tlhip_status tlhip_model_logits(tlhip_model m, uint16_t* host, size_t n);
+/* Op semantics of the TL program the runner stands for (llama only).
+ * literal = 0 (default): RoPE at each token's absolute position, as
+ * rope(x, offset) allows (builtin_tensor.rs:514-556), and RMSNorm at the
+ * GGUF file's eps (llama.attention.layer_norm_rms_epsilon).  literal = 1:
+ * debug/chat_demo_with_kvcache.tl as written -- rope(x) with no offset in
+ * its decode loop (:236,244) rotates every decode row as position 0, and
+ * rms_norm(x, w) uses the builtin default eps 1e-6 (builtin_nn.rs:84-92);
+ * prompt rows rotate at their positions either way.  Phi-2 ->
+ * InvalidOperation.                                                       */
+tlhip_status tlhip_model_set_program_semantics(tlhip_model m, int literal);
 /* Architecture numbers: [n_layers, hidden, inter, n_heads, n_kv, head_dim, vocab, rot_dims]. */
 tlhip_status tlhip_model_dims(tlhip_model m, int32_t* dims8);
 /* The decode's token choice, temperature_sample(logits, T) as the chat

@@ -47,6 +47,17 @@ _i32p = C.POINTER(C.c_int32)
 def _declare(L):
     sz, i, f, vp = C.c_size_t, C.c_int, C.c_float, C.c_void_p
     sig = {
+        "tlo_gguf_open": (vp, [C.c_char_p]),
+        "tlo_gguf_close": (None, [vp]),
+        "tlo_gguf_n_tensors": (i, [vp]),
+        "tlo_gguf_tensor_name": (C.c_char_p, [vp, i]),
+        "tlo_gguf_tensor": (vp, [vp, C.c_char_p, C.POINTER(i), C.POINTER(i), C.POINTER(C.c_int64),
+                                 C.POINTER(sz)]),
+        "tlo_gguf_kv_u32": (i, [vp, C.c_char_p, C.POINTER(C.c_uint32)]),
+        "tlo_gguf_kv_f32": (i, [vp, C.c_char_p, C.POINTER(C.c_float)]),
+        "tlo_einsum_scores": (None, [vp, vp, i, i, i, i, i, vp]),
+        "tlo_einsum_context": (None, [vp, vp, i, i, i, i, i, i, vp]),
+        "tlo_apply_attention_mask": (None, [vp, vp, sz, vp]),
         "tlo_set_threads": (i, [i]),
         "tlo_h2f": (f, [C.c_uint16]),
         "tlo_f2h": (C.c_uint16, [f]),
@@ -84,6 +95,7 @@ def _declare(L):
         "tlo_model_generate": (i, [vp, vp, i, i, vp, vp, vp]),
         "tlo_model_forward": (i, [vp, vp, i, i, vp, vp]),
         "tlo_model_reset": (None, [vp]),
+        "tlo_model_set_program_semantics": (i, [vp, i]),
         "tlo_model_vocab": (i, [vp]),
         "tlo_model_hidden": (i, [vp]),
     }
@@ -251,6 +263,38 @@ def attention(q, k, v, q_pos0=0, scale=None, causal=True, acc=ACC_F32) -> np.nda
     return out
 
 
+def einsum_scores(q, k) -> np.ndarray:
+    """einsum("ihd,jhd->ihj", q [I,H,D], k [J,Hkv,D]) with the GQA mapping
+    (tlo_einsum_scores)."""
+    q, k = _h(q), _h(k)
+    I, H, D = q.shape
+    J, Hkv, _ = k.shape
+    out = np.empty((I, H, J), np.float16)
+    lib().tlo_einsum_scores(_p(q), _p(k), I, J, H, Hkv, D, _p(out))
+    return out
+
+
+def einsum_context(p, v, acc=ACC_F32) -> np.ndarray:
+    """einsum("ihj,jhd->ihd", p [I,H,J], v [J,Hkv,D]) (tlo_einsum_context)."""
+    p, v = _h(p), _h(v)
+    I, H, J = p.shape
+    _, Hkv, D = v.shape
+    out = np.empty((I, H, D), np.float16)
+    lib().tlo_einsum_context(_p(p), _p(v), I, J, H, Hkv, D, acc, _p(out))
+    return out
+
+
+def apply_attention_mask(scores, mask) -> np.ndarray:
+    """apply_attention_mask (tlo_apply_attention_mask): same shapes, as the
+    reference requires (masking.rs:36-43)."""
+    scores, mask = _h(scores), _h(mask)
+    if scores.shape != mask.shape:
+        raise ValueError(f"apply_attention_mask: {scores.shape} vs {mask.shape}")
+    out = np.empty_like(scores)
+    lib().tlo_apply_attention_mask(_p(scores), _p(mask), scores.size, _p(out))
+    return out
+
+
 def embedding(table, ids) -> np.ndarray:
     table = _h(table)
     ids = np.ascontiguousarray(ids, dtype=np.int32)
@@ -321,6 +365,44 @@ def sample_temperature(logits, temperature: float, r: float) -> int:
     return int(lib().tlo_sample_temperature(_p(logits), logits.size, temperature, r))
 
 
+class GGUF:
+    """The oracle's GGUF reader (tlo_gguf_open, tl_oracle.h): None-checked
+    open, tensor table, metadata and each tensor's raw bytes."""
+
+    def __init__(self, path: str):
+        self.h = lib().tlo_gguf_open(path.encode())
+        if not self.h:
+            raise ValueError(f"oracle GGUF reader rejected {path}")
+
+    def close(self):
+        if self.h:
+            lib().tlo_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def names(self):
+        return [lib().tlo_gguf_tensor_name(self.h, i).decode() for i in range(lib().tlo_gguf_n_tensors(self.h))]
+
+    def kv_u32(self, key: str):
+        v = C.c_uint32()
+        return v.value if lib().tlo_gguf_kv_u32(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def kv_f32(self, key: str):
+        v = C.c_float()
+        return v.value if lib().tlo_gguf_kv_f32(self.h, key.encode(), C.byref(v)) == 0 else None
+
+    def tensor(self, name: str):
+        """(gguf type, row-major dims, raw bytes) of one tensor."""
+        t, nd, nb = C.c_int(), C.c_int(), C.c_size_t()
+        dims = (C.c_int64 * 4)()
+        p = lib().tlo_gguf_tensor(self.h, name.encode(), C.byref(t), C.byref(nd), dims, C.byref(nb))
+        if not p:
+            raise KeyError(name)
+        return t.value, tuple(dims[i] for i in range(nd.value)), C.string_at(p, nb.value)
+
+
 class Model:
     """The oracle's decoder (tlo_model_*): arch 0 = llama, 1 = phi2."""
 
@@ -361,3 +443,10 @@ class Model:
 
     def reset(self):
         lib().tlo_model_reset(self.h)
+
+    def set_program_semantics(self, literal: bool):
+        """debug/chat_demo_with_kvcache.tl as written (decode rows rotated at
+        position 0, rms_norm eps 1e-6) or the default (absolute positions,
+        the file's eps); see tlo_model_set_program_semantics."""
+        if lib().tlo_model_set_program_semantics(self.h, int(literal)) != 0:
+            raise ValueError("program semantics are defined for llama models only")

@@ -463,6 +463,52 @@ void tlo_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
     }
 }
 
+void tlo_einsum_scores(const uint16_t* q, const uint16_t* k, int I, int J, int H, int Hkv, int D,
+                       uint16_t* out) {
+    lut_init();
+    const int group = H / Hkv;
+    #pragma omp parallel for schedule(static) collapse(2)
+    for (int i = 0; i < I; i++) {
+        for (int h = 0; h < H; h++) {
+            const uint16_t* qr = q + ((size_t)i * H + h) * D;
+            for (int j = 0; j < J; j++) {
+                const uint16_t* kr = k + ((size_t)j * Hkv + h / group) * D;
+                float acc = 0.0f;
+                for (int d = 0; d < D; d++) acc += H2F(qr[d]) * H2F(kr[d]);
+                out[((size_t)i * H + h) * J + j] = tlo_f2h(acc);
+            }
+        }
+    }
+}
+
+void tlo_einsum_context(const uint16_t* p, const uint16_t* v, int I, int J, int H, int Hkv, int D,
+                        int acc_mode, uint16_t* out) {
+    lut_init();
+    const int group = H / Hkv;
+    #pragma omp parallel for schedule(static) collapse(2)
+    for (int i = 0; i < I; i++) {
+        for (int h = 0; h < H; h++) {
+            const uint16_t* pr = p + ((size_t)i * H + h) * J;
+            for (int d = 0; d < D; d++) {
+                float a = 0.0f;
+                uint16_t ah = 0;
+                for (int j = 0; j < J; j++) {
+                    const float vv = H2F(v[((size_t)j * Hkv + h / group) * D + d]);
+                    if (acc_mode == TLO_ACC_F16) ah = tlo_f2h(H2F(ah) + H2F(tlo_f2h(H2F(pr[j]) * vv)));
+                    else a += H2F(pr[j]) * vv;
+                }
+                out[((size_t)i * H + h) * D + d] = acc_mode == TLO_ACC_F16 ? ah : tlo_f2h(a);
+            }
+        }
+    }
+}
+
+void tlo_apply_attention_mask(const uint16_t* scores, const uint16_t* mask, size_t n, uint16_t* out) {
+    lut_init();
+    const uint16_t masked = tlo_f2h(-10000.0f);
+    for (size_t i = 0; i < n; i++) out[i] = H2F(mask[i]) == 0.0f ? masked : scores[i];
+}
+
 /* ======================================================================== */
 /* masks, slicing, broadcasting, table RoPE                                 */
 /* ======================================================================== */
@@ -741,18 +787,31 @@ tlo_gguf* tlo_gguf_open(const char* path) {
         if (r.err || nd < 1 || nd > 4) goto fail;
         int64_t raw[4];
         uint64_t nelem = 1;
-        for (uint32_t d = 0; d < nd; d++) { raw[d] = (int64_t)rd_uint(&r, 8); nelem *= (uint64_t)raw[d]; }
+        for (uint32_t d = 0; d < nd; d++) {
+            raw[d] = (int64_t)rd_uint(&r, 8);
+            /* element counts past 2^48 fit no mappable file; the bound keeps
+             * gguf_type_bytes' products in range */
+            if (raw[d] < 0 || __builtin_mul_overflow(nelem, (uint64_t)raw[d], &nelem) ||
+                nelem > ((uint64_t)1 << 48)) goto fail;
+        }
         ti->ndim = (int)nd;
         for (uint32_t d = 0; d < nd; d++) ti->dims[d] = raw[nd - 1 - d];
         ti->type = (int)rd_uint(&r, 4);
         ti->offset = rd_uint(&r, 8);
         if (r.err) goto fail;
         ti->nbytes = gguf_type_bytes(ti->type, nelem);
+        /* quantized tensors hold whole blocks (Q4_0 / Q8_0: 32, Q6_K: 256) */
+        if ((ti->type == 2 || ti->type == 8) && nelem % 32) goto fail;
+        if (ti->type == 14 && nelem % 256) goto fail;
     }
     if (alignment == 0) alignment = 32;
     g->data_off = (r.off + alignment - 1) / alignment * alignment;
+    if (g->data_off > size) goto fail;
     for (int i = 0; i < g->n_tensors; i++) {
-        if (g->data_off + g->infos[i].offset + g->infos[i].nbytes > size) goto fail;
+        /* [offset, offset + nbytes) inside the data section, compared as
+         * differences so that no sum wraps */
+        const size_t avail = size - g->data_off;
+        if (g->infos[i].offset > avail || g->infos[i].nbytes > avail - g->infos[i].offset) goto fail;
     }
     return g;
 fail:
@@ -830,6 +889,8 @@ struct tlo_model {
     int arch, n_layers, hidden, inter, n_heads, n_kv, head_dim, vocab, rot_dims, max_ctx;
     float eps, theta;
     int acc_mode;
+    int literal;             /* tlo_model_set_program_semantics */
+    float gguf_eps;          /* eps read from the file */
     int pos;                 /* tokens already in the cache */
     uint16_t* embd;          /* [vocab, hidden] f16 */
     uint16_t *out_norm_w, *out_norm_b;
@@ -906,6 +967,7 @@ tlo_model* tlo_model_load(const char* path, int arch, int max_ctx, int acc_mode,
     m->head_dim = m->hidden / m->n_heads;
     snprintf(key, sizeof key, "%s.%s", a, arch == 0 ? "attention.layer_norm_rms_epsilon" : "attention.layer_norm_epsilon");
     m->eps = tlo_gguf_kv_f32(g, key, &f) ? 1e-5f : f;
+    m->gguf_eps = m->eps;
     snprintf(key, sizeof key, "%s.rope.freq_base", a);
     m->theta = tlo_gguf_kv_f32(g, key, &f) ? 10000.0f : f;
     snprintf(key, sizeof key, "%s.rope.dimension_count", a);
@@ -1012,6 +1074,9 @@ int tlo_model_forward(tlo_model* m, const int32_t* ids, int n, int pos0,
     int rc = tlo_embedding(m->embd, m->vocab, H, ids, n, x);
     if (rc) goto done;
     float scale = 1.0f / sqrtf((float)D);
+    /* rotation offset: literal program semantics rotate a decode row (one
+     * token after the prompt) at position 0, prompt rows at pos0 + s */
+    const int rope_off = (m->literal && n == 1 && pos0 > 0) ? 0 : pos0;
     for (int li = 0; li < m->n_layers; li++) {
         layer_t* L = &m->layers[li];
         uint16_t* kdst = L->kc + (size_t)pos0 * kvd;
@@ -1021,8 +1086,8 @@ int tlo_model_forward(tlo_model* m, const int32_t* ids, int n, int pos0,
             run_lin(m, &L->q, xn, n, q);
             run_lin(m, &L->k, xn, n, kk);
             run_lin(m, &L->v, xn, n, vv);
-            tlo_rope(q, n, NH, D, pos0, m->theta, TLO_ROPE_INTERLEAVED, D, qr);
-            tlo_rope(kk, n, NKV, D, pos0, m->theta, TLO_ROPE_INTERLEAVED, D, kdst);
+            tlo_rope(q, n, NH, D, rope_off, m->theta, TLO_ROPE_INTERLEAVED, D, qr);
+            tlo_rope(kk, n, NKV, D, rope_off, m->theta, TLO_ROPE_INTERLEAVED, D, kdst);
             memcpy(vdst, vv, sizeof(uint16_t) * (size_t)n * kvd);
             tlo_attention(qr, L->kc, L->vc, n, pos0 + n, NH, NKV, D, pos0, scale, 1, m->acc_mode, att);
             run_lin(m, &L->o, att, n, ao);
@@ -1072,6 +1137,13 @@ static float top_margin(const uint16_t* logits, int n, int best) {
     float b = H2F(logits[best]), second = -INFINITY;
     for (int i = 0; i < n; i++) if (i != best) { float v = H2F(logits[i]); if (v > second) second = v; }
     return b - second;
+}
+
+int tlo_model_set_program_semantics(tlo_model* m, int literal) {
+    if (!m || m->arch != 0) return -1;
+    m->literal = literal != 0;
+    m->eps = m->literal ? 1e-6f : m->gguf_eps;
+    return 0;
 }
 
 int tlo_model_generate(tlo_model* m, const int32_t* prompt, int n_prompt,

@@ -137,6 +137,20 @@ void tlo_gelu(const uint16_t* x, size_t n, uint16_t* y);
 void tlo_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                    int S, int J, int H, int Hkv, int D, int q_pos0,
                    float scale, int causal, int acc_mode, uint16_t* out);
+/* The same steps one builtin at a time, as a TL program calls them:
+ * einsum("ihd,jhd->ihj", q [I,H,D], k [J,Hkv,D]) -> [I,H,J], f32 acc, f16
+ * store (einsum.rs:653-686, unified.metal:2524-2560); einsum("ihj,jhd->ihd",
+ * p [I,H,J], v [J,Hkv,D]) -> [I,H,D], accumulation per acc_mode
+ * (unified.metal:2646-2684).  Head h of q / p reads KV head h / (H/Hkv), the
+ * broadcast_to + contiguous expansion of the programs.                     */
+void tlo_einsum_scores(const uint16_t* q, const uint16_t* k, int I, int J, int H, int Hkv, int D,
+                       uint16_t* out);
+void tlo_einsum_context(const uint16_t* p, const uint16_t* v, int I, int J, int H, int Hkv, int D,
+                        int acc_mode, uint16_t* out);
+/* apply_attention_mask(scores, mask) (masking.rs:36-51,147-165,
+ * unified.metal:4474-4489): scores and mask of the same n elements; where
+ * the mask value equals 0 the score becomes f16(-10000), else it is kept.  */
+void tlo_apply_attention_mask(const uint16_t* scores, const uint16_t* mask, size_t n, uint16_t* out);
 
 /* ---- masks, slicing, broadcasting, table RoPE ---------------------------
  * causal_mask builtin_nn.rs:423-460 / Tensor::causal_mask masking.rs:192-207:
@@ -230,6 +244,14 @@ int tlo_model_generate(tlo_model* m, const int32_t* prompt, int n_prompt,
 int tlo_model_forward(tlo_model* m, const int32_t* ids, int n, int pos0,
                       uint16_t* hidden_out, uint16_t* logits_out);
 void tlo_model_reset(tlo_model* m);
+/* literal = 1: the op semantics of debug/chat_demo_with_kvcache.tl as
+ * written -- rope(x) without an offset, so a single-token forward after the
+ * prompt (the decode loop, :236,244) rotates its q and k at position 0
+ * (builtin_tensor.rs:531-546) while prompt rows rotate at 0..S-1, and
+ * rms_norm(x, w) at the builtin default eps 1e-6 (builtin_nn.rs:84-92).
+ * literal = 0 (default): each row at its absolute position, eps from the
+ * GGUF file.  llama only; returns -1 for phi2.                             */
+int  tlo_model_set_program_semantics(tlo_model* m, int literal);
 int  tlo_model_vocab(const tlo_model* m);
 int  tlo_model_hidden(const tlo_model* m);
 

@@ -98,6 +98,7 @@ SIGNATURES = {
     "tlhip_model_logits": (_i, [_vp, C.POINTER(C.c_uint16), _sz]),
     "tlhip_model_dims": (_i, [_vp, _i32p]),
     "tlhip_model_set_sampling": (_i, [_vp, _f, C.c_uint64]),
+    "tlhip_model_set_program_semantics": (_i, [_vp, _i]),
     "tlhip_bench_linear": (_i, [_vp, _vp, C.POINTER(_vp), _i, _vp, _i, _i, C.POINTER(_f)]),
     "tlhip_bench_copy": (_i, [_vp, _sz, _i, _i, C.POINTER(_f)]),
     "tlhip_bench_decode": (_i, [_vp, _i32p, _i, _i, _i, _i32p, C.POINTER(_f), C.POINTER(_f)]),

@@ -212,7 +212,10 @@ tlhip_status tlhip_gguf_open(const char* path, tlhip_gguf* out) {
         for (uint32_t d = 0; d < nd; d++) {
             raw[d] = (int64_t)r.u(8);
             if (raw[d] < 0 || raw[d] > (int64_t)1 << 40) return bad("bad tensor dim");
-            nelem *= (uint64_t)raw[d];
+            // element counts beyond 2^48 cannot fit any file this parser maps;
+            // bounding them keeps type_bytes' products (<= 4 * nelem) in range
+            if (__builtin_mul_overflow(nelem, (uint64_t)raw[d], &nelem) || nelem > ((uint64_t)1 << 48))
+                return bad("tensor element count overflows");
         }
         ti.ndim = (int)nd;
         for (uint32_t d = 0; d < nd; d++) ti.dims[d] = raw[nd - 1 - d];
@@ -226,8 +229,12 @@ tlhip_status tlhip_gguf_open(const char* path, tlhip_gguf* out) {
     }
     if (alignment == 0 || (alignment & (alignment - 1))) return bad("bad general.alignment");
     g->data_off = (r.off + alignment - 1) / alignment * alignment;
+    if (g->data_off > size) return bad("tensor data exceeds file");
+    // each tensor's [offset, offset + nbytes) must lie inside the data section;
+    // compared as differences so that no sum can wrap
+    const size_t data_bytes = size - g->data_off;
     for (auto& ti : g->infos)
-        if (g->data_off + ti.offset + ti.nbytes > size) return bad("tensor data exceeds file");
+        if (ti.offset > data_bytes || ti.nbytes > data_bytes - ti.offset) return bad("tensor data exceeds file");
     *out = g;
     return TLHIP_OK;
 }

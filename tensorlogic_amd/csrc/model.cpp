@@ -11,10 +11,13 @@
 //     cache write -> attention -> GEMV[o]+bias+residual ;
 //     GEMV[up]+bias+gelu -> GEMV[down]+bias+residual
 //   then final norm -> GEMV[lm_head] -> greedy argmax on the device.
-// RoPE is applied at each token's absolute position (the reference's demo
-// calls rope() without an offset in its decode loop, which rotates every new
-// token as position 0; the runner passes the position as rope(x, offset)
-// allows, builtin_tensor.rs:514-556).
+// RoPE is applied at each token's absolute position and RMSNorm takes the
+// GGUF file's eps by default: the reference's demo calls rope() without an
+// offset in its decode loop, which rotates every new token as position 0,
+// and rms_norm(x, w) at the builtin default 1e-6; the runner passes the
+// position as rope(x, offset) allows (builtin_tensor.rs:514-556) and the
+// model's own eps.  tlhip_model_set_program_semantics selects the program's
+// literal choices instead.
 //
 // Decode state lives on the device: {token, pos, step}.  The embedding reads
 // the token, RoPE / cache writes / attention read pos, the argmax writes the
@@ -55,6 +58,9 @@ struct tlhip_model_s {
     int n_layers = 0, hidden = 0, inter = 0, n_heads = 0, n_kv = 0, head_dim = 0, vocab = 0, rot = 0;
     int max_ctx = 0, max_rows = 0;
     float eps = 1e-5f, theta = 10000.0f;
+    float gguf_eps = 1e-5f;                 // eps read from the file
+    int literal = 0;                        // tlhip_model_set_program_semantics
+    float* rope_id = nullptr;               // identity rotation table (every position = position 0)
     tlhip_tensor embd = nullptr, out_norm_w = nullptr, out_norm_b = nullptr;
     Lin out;
     std::vector<Layer> layers;
@@ -377,7 +383,9 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
             a.layout = m->arch == 0 ? 0 : 1;
             a.pos0 = decode ? 0 : pos0;
             a.d_pos = d_pos;
-            a.rope_tab = m->rope_tab;
+            // the program as written rotates a decode row as position 0:
+            // cos 1, sin 0 at every cache row
+            a.rope_tab = decode && m->literal ? m->rope_id : m->rope_tab;
             a.q_out = P(m->qrot);
             a.kc = kc;
             a.vc = vc;
@@ -536,6 +544,11 @@ tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int 
     *out = nullptr;
     if (n_layers <= 0 || max_ctx <= 0 || n_kv_heads <= 0 || head_dim <= 0)
         return fail(TLHIP_ERR_INVALID_DIMENSION, "kvcache: bad sizes");
+    // the attention entry points read at most kAttnMaxKeys keys: a longer
+    // cache could be appended past what it can attend
+    if (max_ctx > kAttnMaxKeys)
+        return fail(TLHIP_ERR_INVALID_DIMENSION, "kvcache: max_ctx %d > %d keys, the most attention reads", max_ctx,
+                    kAttnMaxKeys);
     auto* c = new tlhip_kvcache_s();
     c->ctx = ctx;
     c->n_layers = n_layers;
@@ -576,7 +589,10 @@ static tlhip_status kv_write(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_te
     TLHIP_TRY(check_dtype(k, TLHIP_F16, "kvcache"));
     TLHIP_TRY(check_dtype(v, TLHIP_F16, "kvcache"));
     const int64_t row = (int64_t)c->n_kv * c->head_dim;
-    if (k->ndim < 1 || numel(k) % row != 0 || numel(v) != numel(k) || last_dim(k) != c->head_dim)
+    // K and V must have the same shape: same element count alone would let a
+    // V of another layout (e.g. [S, D, Hkv]) be stored as if it were [S, Hkv, D]
+    const bool same = k->ndim == v->ndim && memcmp(k->shape, v->shape, sizeof(int64_t) * k->ndim) == 0;
+    if (k->ndim < 1 || numel(k) % row != 0 || !same || last_dim(k) != c->head_dim)
         return fail(TLHIP_ERR_SHAPE_MISMATCH, "kvcache: K %s / V %s for rows of [%d, %d]", shape_str(k).c_str(),
                     shape_str(v).c_str(), c->n_kv, c->head_dim);
     const int S = (int)(numel(k) / row);
@@ -679,6 +695,7 @@ tlhip_status tlhip_model_free(tlhip_model m) {
     if (m->d_sample) (void)hipFree(m->d_sample);
     if (m->ws) (void)hipFree(m->ws);
     if (m->d_state) (void)hipFree(m->d_state);
+    if (m->rope_id) (void)hipFree(m->rope_id);
     if (m->d_tokens) (void)hipFree(m->d_tokens);
     if (m->d_ids) (void)hipFree(m->d_ids);
     if (m->h_state) (void)hipHostFree(m->h_state);
@@ -721,6 +738,7 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
         float f;
         if (tlhip_gguf_kv_f32(g, (a + (arch == 0 ? "attention.layer_norm_rms_epsilon" : "attention.layer_norm_epsilon")).c_str(), &f) == TLHIP_OK)
             m->eps = f;
+        m->gguf_eps = m->eps;
         if (tlhip_gguf_kv_f32(g, (a + "rope.freq_base").c_str(), &f) == TLHIP_OK) m->theta = f;
         uint32_t u;
         m->rot = tlhip_gguf_kv_u32(g, (a + "rope.dimension_count").c_str(), &u) == TLHIP_OK ? (int)u : m->head_dim;
@@ -851,6 +869,33 @@ tlhip_status tlhip_model_set_sampling(tlhip_model m, float temperature, uint64_t
     m->graph = nullptr;
     m->temperature = temperature;
     m->seed = seed;
+    return TLHIP_OK;
+}
+
+tlhip_status tlhip_model_set_program_semantics(tlhip_model m, int literal) {
+    if (!m) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null model");
+    if (m->arch != 0)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "program semantics are defined for the llama program only");
+    literal = literal != 0;
+    if (literal == m->literal) return TLHIP_OK;
+    // eps and the rotation table are arguments of the captured decode kernels
+    TLHIP_CHECK_HIP(hipStreamSynchronize(m->ctx->stream));
+    if (m->gexec) (void)hipGraphExecDestroy(m->gexec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    m->gexec = nullptr;
+    m->graph = nullptr;
+    if (literal && !m->rope_id) {
+        // [max_ctx][rot/2] (cos, sin) = (1, 0): the table of position 0 at every row
+        std::vector<float> h((size_t)m->max_ctx * (m->rot / 2) * 2);
+        for (size_t i = 0; i < h.size(); i += 2) {
+            h[i] = 1.0f;
+            h[i + 1] = 0.0f;
+        }
+        TLHIP_CHECK_HIP(hipMalloc(&m->rope_id, h.size() * sizeof(float)));
+        TLHIP_CHECK_HIP(hipMemcpy(m->rope_id, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice));
+    }
+    m->literal = literal;
+    m->eps = literal ? 1e-6f : m->gguf_eps;
     return TLHIP_OK;
 }
 

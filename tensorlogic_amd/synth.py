@@ -102,13 +102,27 @@ def token_ids(seed: int, name: str, n: int, vocab: int) -> np.ndarray:
     return (((z >> np.uint64(32)) * np.uint64(vocab)) >> np.uint64(32)).astype(np.int32)
 
 
-def q4_0_blocks(seed: int, name: str, n: int, k: int, dlo: float = 1e-3, dhi: float = 2e-2) -> np.ndarray:
-    """Packed GGUF Q4_0 blocks (uint8, nblocks*18) for W[n, k]."""
+def q4_0_blocks(seed: int, name: str, n: int, k: int, dlo: float = 1e-3, dhi: float = 2e-2,
+                zero_mean: bool = False) -> np.ndarray:
+    """Packed GGUF Q4_0 blocks (uint8, nblocks*18) for W[n, k].
+
+    Codes are uniform in 0..15 (the benchmark configuration), so the
+    dequantised weights (q - 8) * d have mean -d/2.  zero_mean draws codes
+    uniform in 1..15 instead ((z >> 32) * 15 >> 32, plus 1; element j of a
+    block in the low nibble of byte j, element j + 16 in its high nibble):
+    weights symmetric about 0, as a trained model's are, so that a deep stack
+    with unit RMSNorm gains does not amplify the activations' common mode."""
     if k % 32:
         raise ValueError("K must be a multiple of 32")
     nb = n * k // 32
     d = uniform_f16(seed, name, "d", nb, dlo, dhi)
-    qs = random_bytes(seed, name, "q", nb * 16).reshape(nb, 16)
+    if zero_mean:
+        z = splitmix64(stream_key(seed, name, "q15"), nb * 32)
+        c = ((((z >> np.uint64(32)) * np.uint64(15)) >> np.uint64(32)) + np.uint64(1)).astype(np.uint8)
+        c = c.reshape(nb, 32)
+        qs = (c[:, :16] | (c[:, 16:] << np.uint8(4))).astype(np.uint8)
+    else:
+        qs = random_bytes(seed, name, "q", nb * 16).reshape(nb, 16)
     blk = np.empty((nb, 18), dtype=np.uint8)
     blk[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
     blk[:, 2:] = qs
@@ -159,7 +173,8 @@ PHI2_ARGS = dict(n_layers=32, hidden=2560, inter=10240, n_heads=32, vocab=51200,
 def write_llama_gguf(path: str, seed: int, n_layers: int = 22, hidden: int = 2048,
                      inter: int = 5632, n_heads: int = 32, n_kv: int = 4, vocab: int = 32000,
                      eps: float = 1e-5, theta: float = 10000.0, ctx: int = 2048,
-                     qtype: int = GGML_Q4_0, norm_mean: float = 0.0, out_qtype: int | None = None) -> None:
+                     qtype: int = GGML_Q4_0, norm_mean: float = 0.0, out_qtype: int | None = None,
+                     zero_mean: bool = False) -> None:
     """TinyLlama-architecture decoder with random-init weights.
 
     Linear weights are Q4_0 (or Q8_0, or unquantised F16 / F32 ~ N(0, 0.02);
@@ -167,8 +182,10 @@ def write_llama_gguf(path: str, seed: int, n_layers: int = 22, hidden: int = 204
     the RNE rounding to f16), `output.weight` the same unless out_qtype says
     otherwise (GGML_Q6_K, as llama.cpp's Q4_0 checkpoints store it),
     embeddings f16 N(0, 0.02) and RMSNorm weights f16 N(norm_mean, 0.02)
-    (the benchmark configuration uses norm_mean 0).  Tensor names follow
-    llama.cpp/GGUF.
+    (the benchmark configuration uses norm_mean 0).  zero_mean draws the
+    Q4_0 codes symmetric about 8 (see q4_0_blocks); with it, norm_mean 1
+    gives a full-depth model whose logits have real top-2 margins.  Tensor
+    names follow llama.cpp/GGUF.
     """
     def float_weights(gtype):
         def gen(sd, name, n, k):
@@ -176,10 +193,12 @@ def write_llama_gguf(path: str, seed: int, n_layers: int = 22, hidden: int = 204
                 return normal_f16(sd, name, (n, k), 0.0, 0.02)
             return normal_f32(sd, name, (n, k), 0.0, 0.02)
         return gen
-    qgen = {GGML_Q4_0: q4_0_blocks, GGML_Q8_0: q8_0_blocks, GGML_F16: float_weights(GGML_F16),
+    def q4(sd, name, n, k):
+        return q4_0_blocks(sd, name, n, k, zero_mean=zero_mean)
+    qgen = {GGML_Q4_0: q4, GGML_Q8_0: q8_0_blocks, GGML_F16: float_weights(GGML_F16),
             GGML_F32: float_weights(GGML_F32)}[qtype]
     out_qtype = qtype if out_qtype is None else out_qtype
-    ogen = {GGML_Q4_0: q4_0_blocks, GGML_Q8_0: q8_0_blocks, GGML_Q6_K: q6_k_blocks,
+    ogen = {GGML_Q4_0: q4, GGML_Q8_0: q8_0_blocks, GGML_Q6_K: q6_k_blocks,
             GGML_F16: float_weights(GGML_F16), GGML_F32: float_weights(GGML_F32)}[out_qtype]
     hd = hidden // n_heads
     kvd = n_kv * hd

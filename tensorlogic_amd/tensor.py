@@ -435,6 +435,12 @@ class Model:
         else temperature_sample with the draw splitmix64(seed, step)."""
         call("tlhip_model_set_sampling", self.h, float(temperature), int(seed))
 
+    def set_program_semantics(self, literal: bool):
+        """debug/chat_demo_with_kvcache.tl as written (decode rows rotated as
+        position 0, rms_norm eps 1e-6) or the default (absolute positions,
+        the file's eps); llama only."""
+        call("tlhip_model_set_program_semantics", self.h, int(literal))
+
     def generate(self, prompt, n_decode: int, use_graph: bool = True) -> np.ndarray:
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)
         out = np.empty(n_decode + 1, np.int32)

@@ -482,3 +482,15 @@ def test_kvcache(dev):
     assert np.array_equal(c.get_v(1).numpy(), np.concatenate([v1, v2]))
     with pytest.raises(TLHipError):
         c.append(1, dev.tensor(np.zeros((11, 4, 8), np.float16)), dev.tensor(np.zeros((11, 4, 8), np.float16)))
+    # V with K's element count but another layout is refused, and nothing is written
+    with pytest.raises(TLHipError) as e:
+        c.append(1, dev.tensor(k2), dev.tensor(v2.reshape(1, 8, 4)))
+    assert e.value.kind == "ShapeMismatch" and c.len(1) == 6
+
+
+def test_kvcache_limits(dev):
+    # a cache longer than attention can read is refused at creation
+    with pytest.raises(TLHipError) as e:
+        KVCache(dev, 1, 8193, 4, 64)
+    assert e.value.kind == "InvalidDimension"
+    KVCache(dev, 1, 8192, 4, 64)

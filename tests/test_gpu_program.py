@@ -1,0 +1,96 @@
+"""debug/chat_demo_with_kvcache.tl run unchanged through the per-op boundary.
+
+tensorlogic_amd.program.ChatDemoKVCache issues one tlhip_* call per TL
+builtin of the program (embedding, rms_norm, linear, reshape, rope,
+KVCache.set/append/get_k/get_v, broadcast_to, einsum, * 0.125, causal_mask,
+apply_attention_mask, softmax, sigmoid, *, +, slice_last,
+temperature_sample).  Its greedy tokens must equal those of
+oracle/program.py -- the same statements composed from the CPU oracle's
+one-builtin functions, pinned bit for bit against the oracle's decoder in
+test_oracle_program.py -- at every step, free-running, and its final logits
+must be within the linear bars.  The program's semantics are its literal
+ones (rope(x) with no offset in decode, rms_norm eps 1e-6); the absolute-
+position variant is checked as well.  The fused runner in its literal mode
+(tlhip_model_set_program_semantics) must produce the same stream.
+"""
+import numpy as np
+import pytest
+
+from oracle.program import ChatDemoKVCache as OracleProgram
+from tensorlogic_amd import Model
+from tensorlogic_amd import synth as S
+from tensorlogic_amd.gguf import GGML_Q4_0
+from tensorlogic_amd.program import ChatDemoKVCache
+
+from test_gpu_ops import assert_close
+
+pytestmark = pytest.mark.gpu
+
+# llama shape with head_dim 64 (the program's literal * 0.125); RMSNorm
+# weights 1 + N(0, 0.02) and Q4_0 codes symmetric about 8, so that the logits
+# have real top-2 margins.  Seeds 47 and 51: the oracle's smallest top-2
+# margin over the 25 greedy steps is >= 8 f16 ulps of the top logit in both
+# semantics (a random model has steps whose margin is under one ulp, where
+# two summation orders may pick different ids; those seeds are not used).
+SMALL = dict(n_layers=2, hidden=256, inter=512, n_heads=4, n_kv=2, vocab=1000)
+
+
+def _model(tmp_path, seed):
+    p = str(tmp_path / f"prog_{seed}.gguf")
+    S.write_llama_gguf(p, seed=seed, qtype=GGML_Q4_0, norm_mean=1.0, zero_mean=True, **SMALL)
+    return p
+
+
+@pytest.mark.parametrize("seed", [47, 51])
+@pytest.mark.parametrize("rope_mode,eps", [("program", 1e-6), ("absolute", 1e-5)])
+def test_program_op_by_op_equals_oracle(dev, oracle, tmp_path, seed, rope_mode, eps):
+    path = _model(tmp_path, seed)
+    prompt = S.token_ids(seed, "prompt", 30, SMALL["vocab"])
+    n = 24
+    ref_toks, margins, ref_logits = OracleProgram(path, rope_mode, eps).generate(prompt, n)
+    prog = ChatDemoKVCache(dev, path, max_ctx=64, rope_mode=rope_mode, eps=eps)
+    toks = prog.generate(prompt, n)
+    bad = np.nonzero(toks != ref_toks)[0]
+    assert bad.size == 0, (f"first mismatch at step {bad[0]}: {toks[bad[0]]} vs {ref_toks[bad[0]]} "
+                           f"(oracle margin {margins[bad[0]]:.3g})")
+    assert_close(prog.last_logits.numpy()[0], ref_logits, what="final logits")
+    print(f"{rope_mode}: {len(set(ref_toks.tolist()))} distinct ids, min top-2 margin {margins.min():.3g}")
+
+
+def test_fused_runner_literal_semantics(dev, oracle, tmp_path):
+    """The fused, graph-replayed runner in literal mode reproduces the
+    program's stream (oracle decoder in the same mode, and the op-by-op
+    device run), with direct launches and with graph replay; switching back
+    restores the default semantics."""
+    path = _model(tmp_path, 47)
+    prompt = S.token_ids(47, "prompt", 30, SMALL["vocab"])
+    n = 24
+    om = oracle.Model(path, arch=0, max_ctx=64)
+    om.set_program_semantics(True)
+    ref_lit, _, ref_lit_logits = om.generate(prompt, n)
+    om.set_program_semantics(False)
+    ref_abs, _, _ = om.generate(prompt, n)
+    om.close()
+    assert not np.array_equal(ref_lit, ref_abs), "the two semantics should give different streams"
+    m = Model(dev, path, arch=0, max_ctx=64)
+    m.set_program_semantics(True)
+    for use_graph in (False, True):
+        toks = m.generate(prompt, n, use_graph=use_graph)
+        assert np.array_equal(toks, ref_lit), f"graph={use_graph}: {toks.tolist()} vs {ref_lit.tolist()}"
+        assert_close(m.logits(), ref_lit_logits, what="final logits")
+    m.set_program_semantics(False)
+    assert np.array_equal(m.generate(prompt, n, use_graph=True), ref_abs)
+    m.close()
+    prog = ChatDemoKVCache(dev, path, max_ctx=64)
+    assert np.array_equal(prog.generate(prompt, n), ref_lit)
+
+
+def test_program_semantics_llama_only(dev, tmp_path):
+    from tensorlogic_amd import TLHipError
+    p = str(tmp_path / "phi.gguf")
+    S.write_phi2_gguf(p, seed=43, n_layers=1, hidden=128, inter=256, n_heads=2, vocab=64, rot=32)
+    m = Model(dev, p, arch=1, max_ctx=16)
+    with pytest.raises(TLHipError) as e:
+        m.set_program_semantics(True)
+    assert e.value.kind == "InvalidOperation"
+    m.close()

@@ -69,8 +69,10 @@ def _s(b: str) -> bytes:
     return struct.pack("<Q", len(e)) + e
 
 
-def raw_gguf(kvs, tensors, version=3, align=32, magic=0x46554747, truncate=None):
-    """Hand-built GGUF: kvs = [(key, type, payload_bytes)], tensors = [(name, dims_rowmajor, gtype, data)]."""
+def raw_gguf(kvs, tensors, version=3, align=32, magic=0x46554747, truncate=None, header_offsets=None):
+    """Hand-built GGUF: kvs = [(key, type, payload_bytes)], tensors = [(name, dims_rowmajor, gtype, data)].
+    header_offsets, when given, replaces the tensor offsets written in the
+    tensor table (the data is still laid out at the true offsets)."""
     head = struct.pack("<IIQQ", magic, version, len(tensors), len(kvs))
     for k, t, payload in kvs:
         head += _s(k) + struct.pack("<I", t) + payload
@@ -79,11 +81,11 @@ def raw_gguf(kvs, tensors, version=3, align=32, magic=0x46554747, truncate=None)
         offs.append(off)
         off += len(data)
         off = (off + align - 1) // align * align
-    for (name, dims, gt, _), o in zip(tensors, offs):
+    for i, ((name, dims, gt, _), o) in enumerate(zip(tensors, offs)):
         head += _s(name) + struct.pack("<I", len(dims))
         for d in reversed(dims):
             head += struct.pack("<Q", d)
-        head += struct.pack("<IQ", gt, o)
+        head += struct.pack("<IQ", gt, header_offsets[i] if header_offsets else o)
     head += b"\0" * ((-len(head)) % align)
     body = b""
     for (_, _, _, data), o in zip(tensors, offs):
@@ -116,7 +118,7 @@ def open_c(path):
     return st, g
 
 
-def test_gguf_every_kv_type_and_tensor_table(tmp_path):
+def test_gguf_every_kv_type_and_tensor_table(tmp_path, oracle):
     q4 = S.q4_0_blocks(50, "w", 4, 64)
     emb = S.normal_f16(50, "e", (3, 8))
     p = str(tmp_path / "all.gguf")
@@ -137,6 +139,15 @@ def test_gguf_every_kv_type_and_tensor_table(tmp_path):
     assert r.kv["a.u16"] == 700 and r.kv["a.arr_str"] == ["x", "yz"] and r.kv["a.f64"] == 0.25
     assert r.tensors["w"].shape == (4, 64) and np.array_equal(r.raw("w"), q4)
     assert np.array_equal(r.raw("e").view(np.float16).reshape(3, 8), emb)
+    # and so does the oracle's own reader (tlo_gguf_open), which every
+    # oracle model and golden fixture is loaded through
+    og = oracle.GGUF(p)
+    assert sorted(og.names()) == ["e", "w"]
+    assert og.kv_u32("llama.block_count") == 22 and og.kv_f32("llama.rope.freq_base") == 10000.0
+    assert og.kv_u32("missing.key") is None
+    assert og.tensor("w") == (GGML_Q4_0, (4, 64), q4.tobytes())
+    assert og.tensor("e") == (GGML_F16, (3, 8), emb.tobytes())
+    og.close()
 
 
 def test_gguf_general_alignment_is_honoured(tmp_path):
@@ -153,8 +164,9 @@ def test_gguf_general_alignment_is_honoured(tmp_path):
 
 
 @pytest.mark.parametrize("case", ["magic", "version", "truncated_header", "data_past_eof",
-                                  "bad_kv_type", "bad_q_shape", "missing_file"])
-def test_gguf_malformed_is_a_load_error(tmp_path, case):
+                                  "bad_kv_type", "bad_q_shape", "missing_file", "huge_offset",
+                                  "offset_past_eof", "dim_overflow", "dim_overflow_to_zero"])
+def test_gguf_malformed_is_a_load_error(tmp_path, oracle, case):
     q8 = S.q8_0_blocks(52, "w", 2, 64).tobytes()
     t = [("w", (2, 64), GGML_Q8_0, q8)]
     p = str(tmp_path / f"{case}.gguf")
@@ -170,11 +182,21 @@ def test_gguf_malformed_is_a_load_error(tmp_path, case):
         blob = raw_gguf([("x", 99, b"\0" * 8)], t)
     elif case == "bad_q_shape":                     # 48 elements is not a whole number of Q8_0 blocks
         blob = raw_gguf([], [("w", (1, 48), GGML_Q8_0, q8[:51])])
+    elif case == "huge_offset":                     # data_off + offset + nbytes wraps past 2^64
+        blob = raw_gguf([], t, header_offsets=[(1 << 64) - 64])
+    elif case == "offset_past_eof":                 # offset alone beyond the file
+        blob = raw_gguf([], t, header_offsets=[1 << 40])
+    elif case == "dim_overflow":                    # 2^40 x 2^40 elements: the count wraps 64 bits
+        blob = raw_gguf([], [("w", (1 << 40, 1 << 40), GGML_Q8_0, q8)])
+    elif case == "dim_overflow_to_zero":            # 2^32 * 2^32 * 2^32 wraps to 0 elements, 0 bytes
+        blob = raw_gguf([], [("w", (1 << 32, 1 << 32, 1 << 32), GGML_Q8_0, q8)])
     if case != "missing_file":
         open(p, "wb").write(blob)
     st, g = open_c(p)
     assert st == 6, (case, st)                       # TLHIP_ERR_LOAD (TensorError::LoadError)
     assert b"LoadError" in L.lib().tlhip_last_error()
+    with pytest.raises(ValueError):                  # the oracle's reader refuses the same files
+        oracle.GGUF(p)
 
 
 def test_writer_reader_round_trip_and_reference_parseable_types(tmp_path):

@@ -172,3 +172,76 @@ def test_rope_cos_sin_rejects_bad_shapes(oracle):
         oracle.rope_cos_sin(x, h(np.ones((4, 6))), h(np.zeros((4, 6))))   # table width != head_dim
     with pytest.raises(ValueError):
         oracle.rope_cos_sin(h(np.zeros((4, 2, 7))), h(np.ones((4, 7))), h(np.zeros((4, 7))))   # odd head_dim
+
+
+# ---------------------------------------------------------------------------
+# einsum("ihd,jhd->ihj"), einsum("ihj,jhd->ihd"), apply_attention_mask: the
+# attention steps one builtin at a time, as debug/chat_demo_with_kvcache.tl
+# calls them
+# ---------------------------------------------------------------------------
+def test_einsum_known_answers(oracle):
+    # tests/test_einsum_f16_comprehensive.rs:45-89: q [2,1,2], k [3,1,2]
+    q = h([[[1, 2]], [[3, 4]]])
+    k = h([[[1, 0]], [[0, 1]], [[1, 1]]])
+    assert np.array_equal(oracle.einsum_scores(q, k), h([[[1, 2, 3]], [[3, 4, 7]]]))
+    # :92-135: attn [2,1,3], v [3,1,2] -> [[0.7, 0.5]], [[0.7, 0.8]] (within 1e-2)
+    p = h([[[0.5, 0.3, 0.2]], [[0.2, 0.3, 0.5]]])
+    for acc in (oracle.ACC_F32, oracle.ACC_F16):
+        out = oracle.einsum_context(p, k, acc).astype(np.float32)
+        assert out.shape == (2, 1, 2)
+        assert np.allclose(out, [[[0.7, 0.5]], [[0.7, 0.8]]], atol=1e-2)
+
+
+@pytest.mark.parametrize("I,J,H,Hkv,D", [(5, 9, 8, 2, 16), (1, 40, 4, 4, 64), (7, 7, 6, 3, 80)])
+def test_einsum_vs_float64(oracle, I, J, H, Hkv, D):
+    """Against float64 with the expansion written out as the programs do it
+    (K reshaped to [J, Hkv, 1, D] and broadcast to [J, Hkv, H/Hkv, D]): a
+    transposed operand or the wrong KV head for a query head fails."""
+    q = S.normal_f16(80, "eq", (I, H, D))
+    k = S.normal_f16(80, "ek", (J, Hkv, D))
+    v = S.normal_f16(80, "ev", (J, Hkv, D))
+    kx = np.broadcast_to(k[:, :, None, :], (J, Hkv, H // Hkv, D)).reshape(J, H, D).astype(np.float64)
+    vx = np.broadcast_to(v[:, :, None, :], (J, Hkv, H // Hkv, D)).reshape(J, H, D).astype(np.float64)
+    sc = oracle.einsum_scores(q, k)
+    ref = np.einsum("ihd,jhd->ihj", q.astype(np.float64), kx)
+    # one f32 sum of D products, one f16 rounding: within one f16 ulp
+    assert np.all(np.abs(sc.astype(np.float64) - ref) <= np.maximum(2.0 ** -24, np.abs(ref) * 2.0 ** -10))
+    p = oracle.softmax(sc)
+    ctx = oracle.einsum_context(p, v)
+    ref = np.einsum("ihj,jhd->ihd", p.astype(np.float64), vx)
+    assert np.all(np.abs(ctx.astype(np.float64) - ref) <= np.maximum(2.0 ** -24, np.abs(ref) * 2.0 ** -10))
+
+
+def test_apply_attention_mask_known_answers(oracle):
+    # tests/test_attention_mask.rs:267-292, :296-319, :323-343, :347-373
+    assert np.array_equal(oracle.apply_attention_mask(h([[1, 2], [3, 4]]), h([[1, 0], [1, 1]])),
+                          h([[1, -10000], [3, 4]]))
+    assert np.array_equal(oracle.apply_attention_mask(h([[1, 2, 3]]), h([[1, 1, 1]])), h([[1, 2, 3]]))
+    assert np.all(oracle.apply_attention_mask(h([[1, 2], [3, 4]]), np.zeros((2, 2), np.float16)) == -10000)
+    got = oracle.apply_attention_mask(np.ones((4, 4), np.float16), oracle.causal_mask(4))
+    assert np.array_equal(got, np.where(np.tril(np.ones((4, 4))) == 1, 1.0, -10000.0).astype(np.float16))
+    with pytest.raises(ValueError):            # the reference requires equal shapes (masking.rs:36-43)
+        oracle.apply_attention_mask(h([[1, 2]]), h([[1], [1]]))
+
+
+@pytest.mark.parametrize("acc", [0, 1])
+@pytest.mark.parametrize("S_,H,Hkv,D,q0", [(12, 8, 2, 64, 0), (1, 8, 2, 64, 11), (30, 4, 4, 16, 0)])
+def test_einsum_program_composition_is_the_fused_oracle(oracle, acc, S_, H, Hkv, D, q0):
+    """The program's steps -- einsum, * 0.125, apply_attention_mask with a
+    causal_mask broadcast over heads (all ones for the single decode row),
+    softmax, einsum -- composed from the one-builtin functions equal
+    tlo_attention (pinned against float64 in test_oracle_pinning.py) bit
+    for bit."""
+    J = q0 + S_
+    q = S.normal_f16(81, "cq", (S_, H, D))
+    k = S.normal_f16(81, "ck", (J, Hkv, D))
+    v = S.normal_f16(81, "cv", (J, Hkv, D))
+    sc = oracle.mul_scalar(oracle.einsum_scores(q, k), 0.125)
+    if S_ == J:
+        mask = np.broadcast_to(oracle.causal_mask(S_).reshape(S_, 1, S_), (S_, H, S_))
+    else:   # decode: causal_mask(1) broadcast to [1, H, J] (chat_demo_with_kvcache.tl:265-268)
+        mask = np.broadcast_to(oracle.causal_mask(1).reshape(1, 1, 1), (1, H, J))
+    p = oracle.softmax(oracle.apply_attention_mask(sc, np.ascontiguousarray(mask)))
+    out = oracle.einsum_context(p, v, acc)
+    fused = oracle.attention(q, k, v, q0, 0.125, True, acc)
+    assert np.array_equal(out.view(np.uint16), fused.view(np.uint16))
