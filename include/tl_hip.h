@@ -125,8 +125,11 @@ tlhip_status tlhip_gguf_kv_f32(tlhip_gguf g, const char* key, float* v);
 tlhip_status tlhip_dequantize(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor out_f16);
 /* linear(x, W[, b]) (builtin_math.rs:76-131) = matmul_transposed_b
  * (matmul.rs:241-458) then add(bias): y[M,N] = x[M,K] W[N,K]^T, fp32
- * accumulation, f16 out.  W may be F16, Q4_0 or Q8_0; M <= 4 uses the
- * fused dequant-GEMV, larger M the MFMA dequant-GEMM.  bias may be NULL.  */
+ * accumulation, f16 out.  W may be F16, Q4_0, Q8_0 or Q6_K; M <= 4 uses
+ * the fused dequant-GEMV, larger M the MFMA dequant-GEMM (a Q6_K weight
+ * keeps the dequantised f16 copy that GEMM reads, 2 bytes per weight, from
+ * its first use with M > 4 until it is freed or re-uploaded).  bias may be
+ * NULL.                                                                   */
 tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y);
 /* linear(x, W[, b]) exactly as tlhip_linear (same checks, kernels and bits),
  * but allocating nothing: no counterpart in the reference.  It is for

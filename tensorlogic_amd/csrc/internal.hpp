@@ -59,6 +59,9 @@ struct tlhip_ctx_s {
     bool sync_every_op = false;
     std::vector<tlhip::RopeTable> rope_tables;
     int32_t* d_scratch_i32 = nullptr;   // small scratch for argmax results
+    uint32_t* d_tile_flags = nullptr;   // skinny GEMM split counters (zero between launches)
+    float* d_ws = nullptr;              // linear's split-K partials, grown on demand
+    size_t ws_bytes = 0;
     int32_t* h_pinned_i32 = nullptr;    // pinned host mirror
 };
 
@@ -72,6 +75,9 @@ struct tlhip_tensor_s {
     uint16_t* scales = nullptr; // Q types: f16 scales [N][K/32]
     size_t alloc_bytes = 0;
     tlhip_tensor base = nullptr;  // owner when this is a view
+    // Q6_K: the dequantised f16 weight the MFMA GEMM reads (linear with
+    // M > 4), made on first use, dropped on upload, freed with the tensor
+    tlhip_tensor f16_copy = nullptr;
 };
 
 namespace tlhip {
@@ -161,7 +167,13 @@ struct GemvArgs {
     // GEMM split-K workspace (fp32 partials); none = no split
     float* ws = nullptr;
     size_t ws_bytes = 0;
+    // arrival counters of the skinny GEMM's K split (SK_MAX_TILES_SPLIT of
+    // them, zero between launches); none = no split across workgroups
+    uint32_t* tile_flags = nullptr;
 };
+// weight-row tiles up to which the skinny GEMM splits K over workgroups (and
+// so the counters a context holds for it)
+constexpr int SK_MAX_TILES_SPLIT = 128;
 enum GemvPro { PRO_NONE = 0, PRO_RMS = 1, PRO_LN = 2 };
 // Epilogues fused into the GEMV/GEMM store (each step rounds to f16 where
 // the reference's separate op would store f16):
@@ -182,7 +194,8 @@ int gemv_norm_slots(int N);   // workgroups (= argmax keys) of the normalised GE
 tlhip_status launch_argmax_slots(hipStream_t s, const unsigned long long* slots, int n, int32_t* out,
                                  int32_t* token_log, int32_t* d_state);
 tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi);
-int gemm_splits(int M, int N, int K);   // split-K slices launch_gemm uses when given a workspace
+int gemm_splits(int M, int N, int K, int wt);   // split-K slices launch_gemm uses when given a workspace
+                                                // (wt < 0: any weight type, the largest count)
 uint16_t f32_to_f16(float f);            // host RNE rounding (F32 GGUF tensors)
 // Rows 0..src_rows-1 of a GGUF block stream [src_rows, K] go to rows
 // dst_row0 + r * dst_step of a packed tensor of dst_rows rows (to_gguf = 1:

@@ -12,6 +12,8 @@
 // (M <= 64: register-staged, two LDS buffers) and gemm_lds_kernel (M > 64:
 // 128 x 128 tiles, three or four LDS stages filled by direct global->LDS
 // loads).
+#include <type_traits>
+
 #include "device_common.hpp"
 #include "internal.hpp"
 
@@ -25,6 +27,11 @@ struct GemmParams {
     const uint16_t* resid;
     uint16_t* y;
     int M, N, K, ldy, epi;
+    // skinny GEMM split over K: fp32 partials [splits][M][N] and one arrival
+    // counter per 32-row tile (zero between launches)
+    float* part = nullptr;
+    uint32_t* flags = nullptr;
+    int splits = 1;
 };
 
 constexpr int GBM = 64, GBN = 64, GBK = 32, GPAD = 8;
@@ -379,6 +386,359 @@ __device__ __forceinline__ int gl_tile(int id, int T) {   // XCD-contiguous tile
     return x * q + min(x, r) + s;
 }
 
+// ---------------------------------------------------------------------------
+// Skinny dequant-GEMM (4 < M <= 64, K % 64 == 0) on v_mfma_f32_16x16x32_f16:
+// one launch, no workspace.  Every workgroup reads all of x (M x K) and its
+// own weight rows once; both streams enter the CU as whole 64-byte pieces,
+// because the vector L1 handles a load one piece per lane-run of adjacent
+// addresses: an MFMA operand read straight from a row-major matrix (one row
+// per lane) costs one L1 access per lane, here one per 64 bytes.
+//
+// A workgroup (4 waves) owns SK_ROWS = 32 weight rows as two 16-row tiles;
+// wave w takes K part w (K / 64 steps of 64 k split into 4 ranges) for both
+// tiles.  Each wave streams its part through a private ring of L::ST LDS
+// stages with buffer loads to LDS (16 bytes per lane, adjacent lanes on
+// adjacent bytes; the 16-byte pieces of a row XOR-swizzled by row so the
+// operand reads below spread over the banks), then reads the operands of
+// sub-step t = 0, 1 in the natural 16 x 16 x 32 layout -- lane l (tile row /
+// column l % 16, group g = l / 16) holds k = 64 q + 32 t + 8 g + i:
+//   A (activation row 16 mt + l % 16): 16 bytes;
+//   B (weight row): f16 16 bytes; Q8_0 8 bytes of block 2q + t; Q4_0 8
+//   bytes of block 2q + t (low nibbles for g < 2, high for g >= 2), with the
+//   block's scale,
+// dequantised with the correctly rounded RNE_f16((q - 8) d) / RNE_f16(q d)
+// of every other path.  Ring stages past the wave's range are filled from
+// offsets outside the buffers (no memory access) and never read, so every
+// stage has the same number of loads and the waits are fixed counts.  The
+// four K parts' fp32 accumulators meet in LDS and are added in a fixed order
+// (part 0 + 1 + 2 + 3) before the epilogue.
+//
+// When the weight rows give fewer than ~128 workgroups, K is also split over
+// p.splits workgroups per tile (block b: tile b / splits, K slice
+// b % splits).  Each writes its fp32 tile to p.part and counts itself in on
+// the tile's counter; the last to arrive adds the slices in slice order --
+// the same bits whichever arrives last -- applies the epilogue and resets
+// the counter to zero for the next launch, so no second kernel runs.  C layout of a 16 x 16 tile:
+// lane l holds column (weight row) l % 16 and activation rows 4 (l / 16) + r.
+// ---------------------------------------------------------------------------
+constexpr int SK_ROWS = 32, SK_KP = 4;   // weight rows, K parts (waves)
+constexpr int SK_LDS = 160 * 1024 - 1024;   // LDS the rings may take
+constexpr int SK_MAX_SPLITS = 8;
+constexpr uint32_t SK_OOB = 0x80000000u;            // a buffer offset past every tensor
+
+template <int WT, int MT>
+struct SkL {   // LDS bytes of one stage (one 64-k step) of one wave
+    static constexpr int X = MT * 16 * 128;   // activation rows, 128 bytes each
+    static constexpr int WROW = WT == TLHIP_F16 ? 128 : (WT == TLHIP_Q8_0 ? 64 : 32);
+    static constexpr int W = SK_ROWS * WROW;
+    static constexpr int S = WT == TLHIP_F16 ? 0 : 256;   // 32 rows x 2 scales (+ the unused upper half)
+    static constexpr int STAGE = X + W + S;
+    static constexpr int NX = X / 1024, NW = W / 1024, NS = S ? 1 : 0;
+    static constexpr int C = NX + NW + NS;   // loads per stage
+    // stages per wave: as many as the LDS holds (the deeper the ring, the
+    // fewer memory round trips a wave's part takes), at most 6
+    static constexpr int ST = SK_LDS / (SK_KP * STAGE) < 6 ? SK_LDS / (SK_KP * STAGE) : 6;
+    static_assert(X % 1024 == 0 && W % 1024 == 0, "1 KB loads");
+    static_assert(ST >= 2 && (ST - 1) * C < 64, "stages, vmcnt range");
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// Buffer load to LDS at wave-uniform LDS byte address lds (+ 16 or 4 bytes
+// per lane), written as assembly: the compiler then neither tracks these
+// LDS writes (it would wait for every one of them before any LDS read) nor
+// counts them, and the kernel waits for them itself with sk_wait_vm.  M0
+// holds the LDS address (one wait state between its write and the load);
+// the compiler uses M0 for nothing else in the kernels that call this.
+template <int SZ>
+__device__ __forceinline__ void sk_dma(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t off) {
+    if constexpr (SZ == 16)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(off), "s"(r)
+                     : "memory");
+    else
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(off), "s"(r)
+                     : "memory");
+}
+template <int N>
+__device__ __forceinline__ void sk_wait_vm() {   // a compiler barrier for memory, unlike the builtin
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int WT, int MT>
+__global__ __launch_bounds__(64 * SK_KP) void gemm_skinny_kernel(GemmParams p) {
+    using L = SkL<WT, MT>;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[SK_KP * L::ST * L::STAGE];
+    const int lane = threadIdx.x & 63;
+    const int kp = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);   // wave-uniform
+    const int nl = lane & 15, g = lane >> 4;
+    const int tile = (int)blockIdx.x / p.splits, z = (int)blockIdx.x % p.splits;
+    const int n0 = tile * SK_ROWS;
+    const int nq = p.K >> 6;
+    const int za = nq * z / p.splits, nz = nq * (z + 1) / p.splits - za;   // this workgroup's K slice (steps)
+    const int qa = za + nz * kp / SK_KP, qb = za + nz * (kp + 1) / SK_KP;
+    uint8_t* const ring = smem + kp * L::ST * L::STAGE;
+    const uint32_t ring_lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(gl_lds_t)ring);
+    const uint32_t K = (uint32_t)p.K;
+
+    constexpr uint32_t WSTEP = WT == TLHIP_F16 ? 128u : (WT == TLHIP_Q8_0 ? 64u : 32u);   // weight bytes per row and step
+    const uint32_t wrow = WT == TLHIP_F16 ? 2u * K : (WT == TLHIP_Q8_0 ? K : K / 2u);
+    const __amdgpu_buffer_rsrc_t rx = sk_rsrc(p.x, (uint32_t)p.M * K * 2u);
+    const __amdgpu_buffer_rsrc_t rw = sk_rsrc(p.wq, (uint32_t)p.N * wrow);
+    const __amdgpu_buffer_rsrc_t rd = sk_rsrc(WT == TLHIP_F16 ? (const void*)p.wq : (const void*)p.wd,
+                                              WT == TLHIP_F16 ? 0u : (uint32_t)p.N * (K / 32u) * 2u);
+
+    // source byte offsets (step 0) of this lane's 16 bytes in each load:
+    // LDS piece P = 64 u + lane of the region, rows of 8 (x, f16 weights),
+    // 4 (Q8_0) or 2 (Q4_0) pieces
+    uint32_t xsrc[L::NX], wsrc[L::NW], dsrc = SK_OOB;
+#pragma unroll
+    for (int u = 0; u < L::NX; u++) {
+        const int P = 64 * u + lane, r = P >> 3, c = (P & 7) ^ (r & 7);
+        xsrc[u] = r < p.M ? (uint32_t)r * K * 2u + 16u * c : SK_OOB;
+    }
+#pragma unroll
+    for (int u = 0; u < L::NW; u++) {
+        const int P = 64 * u + lane;
+        int n, c;
+        if (WT == TLHIP_F16) { n = P >> 3; c = (P & 7) ^ (n & 7); }
+        else if (WT == TLHIP_Q8_0) { n = P >> 2; c = (P & 3) ^ ((n >> 1) & 3); }
+        else { n = P >> 1; c = (P & 1) ^ ((n >> 2) & 1); }
+        wsrc[u] = n0 + n < p.N ? (uint32_t)(n0 + n) * wrow + 16u * c : SK_OOB;
+    }
+    if (L::NS && lane < SK_ROWS && n0 + lane < p.N) dsrc = (uint32_t)(n0 + lane) * (K / 32u) * 2u;
+
+    // operand offsets inside a stage
+    int xrd[MT][2], wrd[2][2], drd[2];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int r = 16 * mt + nl, c = 4 * t + g;
+            xrd[mt][t] = r * 128 + 16 * (c ^ (r & 7));
+        }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int n = 16 * j + nl;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            if (WT == TLHIP_F16) wrd[j][t] = L::X + n * 128 + 16 * ((4 * t + g) ^ (n & 7));
+            else if (WT == TLHIP_Q8_0) wrd[j][t] = L::X + n * 64 + 16 * ((2 * t + (g >> 1)) ^ ((n >> 1) & 3)) + 8 * (g & 1);
+            else wrd[j][t] = L::X + n * 32 + 16 * (t ^ ((n >> 2) & 1)) + 8 * (g & 1);
+        }
+        drd[j] = L::X + L::W + 4 * n;
+    }
+
+    // one stage's loads: step q into stage st (past the range: offsets
+    // outside the buffers, no memory access)
+    auto issue = [&](int q, int st) {
+        const uint32_t oob = q < qb ? 0u : SK_OOB;
+        const uint32_t base = ring_lds + (uint32_t)(st * L::STAGE);
+#pragma unroll
+        for (int u = 0; u < L::NX; u++) sk_dma<16>(rx, base + 1024u * u, (xsrc[u] + (uint32_t)q * 128u) | oob);
+#pragma unroll
+        for (int u = 0; u < L::NW; u++) sk_dma<16>(rw, base + L::X + 1024u * u, (wsrc[u] + (uint32_t)q * WSTEP) | oob);
+        if constexpr (L::NS > 0) sk_dma<4>(rd, base + L::X + L::W, (dsrc + (uint32_t)q * 4u) | oob);
+    };
+
+    f4 acc[2][MT];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[j][mt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll
+    for (int st = 0; st < L::ST; st++) issue(qa + st, st);
+    int st = 0;
+    for (int q = qa; q < qb; q++) {
+        sk_wait_vm<(L::ST - 1) * L::C>();   // this step's stage has landed (loads complete in order)
+        const uint8_t* base = ring + st * L::STAGE;
+        h8 a[MT][2], b[2][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) a[mt][t] = *(const h8*)(base + xrd[mt][t]);
+        if constexpr (WT == TLHIP_F16) {
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int t = 0; t < 2; t++) b[j][t] = *(const h8*)(base + wrd[j][t]);
+        } else {
+            uint2 w[2][2];
+            uint32_t d[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+#pragma unroll
+                for (int t = 0; t < 2; t++) w[j][t] = *(const uint2*)(base + wrd[j][t]);
+                d[j] = *(const uint32_t*)(base + drd[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const h16 dh = __builtin_bit_cast(h16, (uint16_t)(t ? d[j] >> 16 : d[j] & 0xFFFFu));
+                    const h2 dd = {dh, dh};
+                    uint32_t o0, o1, o2, o3;
+                    if constexpr (WT == TLHIP_Q8_0) {
+                        q8_pairs(w[j][t].x, dd, o0, o1);
+                        q8_pairs(w[j][t].y, dd, o2, o3);
+                    } else {
+                        const int sh = (g >> 1) * 4;   // groups 2, 3 take the high nibbles
+                        q4_pairs((w[j][t].x >> sh) & 0x0F0F0F0Fu, dd, o0, o1);
+                        q4_pairs((w[j][t].y >> sh) & 0x0F0F0F0Fu, dd, o2, o3);
+                    }
+                    b[j][t] = __builtin_bit_cast(h8, u4{o0, o1, o2, o3});
+                }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][t], b[j][t], acc[j][mt], 0, 0, 0);
+        // the stage's reads have returned before its refill is issued
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        issue(q + L::ST, st);
+        __builtin_amdgcn_sched_barrier(0);
+        st = st + 1 == L::ST ? 0 : st + 1;
+    }
+
+    // every part's partial tiles to LDS (over the ring, once every wave's
+    // loads have landed); wave w then reduces (tile, row tile) pairs w and
+    // w + 4 in part order and applies the epilogue
+    sk_wait_vm<0>();
+    __syncthreads();
+    float (*red)[2][MT * 4][64] = (float (*)[2][MT * 4][64])smem;
+    static_assert(sizeof(float) * SK_KP * 2 * MT * 4 * 64 <= sizeof(smem), "reduction fits the ring");
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[kp][j][mt * 4 + r][lane] = acc[j][mt][r];
+    const bool use_b = p.epi == EPI_BIAS || p.epi == EPI_BIAS_RESID || p.epi == EPI_BIAS_GELU;
+    const bool use_r = p.epi == EPI_RESID || p.epi == EPI_BIAS_RESID;
+    constexpr int NP = (2 * MT + SK_KP - 1) / SK_KP;   // pairs per wave
+    uint32_t bv[NP], rv[NP][4];
+#pragma unroll
+    for (int i = 0; i < NP; i++) {   // epilogue operands loaded before the barrier
+        const int pr = kp + SK_KP * i, j = pr & 1, mt = pr >> 1;
+        const int n = min(n0 + 16 * j + nl, p.N - 1);
+        bv[i] = use_b && mt < MT ? (uint32_t)p.bias[n] : 0u;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            rv[i][r] = use_r && mt < MT ? (uint32_t)p.resid[(size_t)min(16 * mt + 4 * g + r, p.M - 1) * p.N + n] : 0u;
+    }
+    __syncthreads();
+    float vs[NP][4];
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const int pr = kp + SK_KP * i, j = pr & 1, mt = pr >> 1;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float v = 0.0f;
+            if (mt < MT) {
+                v = red[0][j][mt * 4 + r][lane];
+#pragma unroll
+                for (int u = 1; u < SK_KP; u++) v += red[u][j][mt * 4 + r][lane];
+            }
+            vs[i][r] = v;
+        }
+    }
+    if (p.splits > 1) {
+        // This slice's tile to the partials; the last slice to arrive sums
+        // them.  Partials and counter are written and read as device-scope
+        // relaxed atomics, which go past this XCD's L2 to the memory every
+        // XCD sees; waiting for the stores to complete before the count
+        // orders them.  (Device-scope fences would instead write back and
+        // invalidate the whole L2, which the other workgroups on the XCD
+        // are streaming through.)
+        __shared__ int sk_last;
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int pr = kp + SK_KP * i, j = pr & 1, mt = pr >> 1;
+            const int ncol = n0 + 16 * j + nl;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = 16 * mt + 4 * g + r;
+                if (mt < MT && m < p.M && ncol < p.N)
+                    __hip_atomic_store(p.part + ((size_t)z * p.M + m) * p.N + ncol, vs[i][r], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0)
+            sk_last = __hip_atomic_fetch_add(p.flags + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      (uint32_t)(p.splits - 1);
+        __syncthreads();
+        if (!sk_last) return;
+        if (threadIdx.x == 0) __hip_atomic_store(p.flags + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int pr = kp + SK_KP * i, j = pr & 1, mt = pr >> 1;
+            const int ncol = min(n0 + 16 * j + nl, p.N - 1);
+            float t[4][SK_MAX_SPLITS];   // every slice's value loaded before the in-order sum
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = min(16 * mt + 4 * g + r, p.M - 1);
+#pragma unroll
+                for (int zz = 0; zz < SK_MAX_SPLITS; zz++)
+                    t[r][zz] = mt < MT && zz < p.splits
+                                   ? __hip_atomic_load(p.part + ((size_t)zz * p.M + m) * p.N + ncol, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float v = t[r][0];
+#pragma unroll
+                for (int zz = 1; zz < SK_MAX_SPLITS; zz++) v += t[r][zz];
+                vs[i][r] = v;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        const int pr = kp + SK_KP * i, j = pr & 1, mt = pr >> 1;
+        if (mt >= MT) break;
+        const int ncol = n0 + 16 * j + nl;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float v = vs[i][r];
+            const int m = 16 * mt + 4 * g + r;
+            if (p.epi == EPI_SWIGLU_PAIR) {
+                const float up = __shfl_down(v, 1, 64);
+                if (m < p.M && ncol + 1 < p.N && (ncol & 1) == 0)
+                    p.y[(size_t)m * p.ldy + ncol / 2] = swiglu_h(f2h(v), f2h(up));
+            } else if (m < p.M && ncol < p.N) {
+                p.y[(size_t)m * p.ldy + ncol] = epilogue_v(p.epi, v, (uint16_t)bv[i], (uint16_t)rv[i][r]);
+            }
+        }
+    }
+}
+
+bool gemm_skinny_ok(int M, int N, int K, int wt) {
+    // byte offsets of the buffer loads are 32-bit, the padding offset
+    // SK_OOB above every tensor
+    const uint64_t wrow = wt == TLHIP_F16 ? 2ull * K : (wt == TLHIP_Q4_0 ? K / 2ull : (uint64_t)K);
+    return M > 4 && M <= 64 && K % 64 == 0 && (wt == TLHIP_F16 || wt == TLHIP_Q8_0 || wt == TLHIP_Q4_0) &&
+           (uint64_t)N * wrow < SK_OOB && 2ull * M * K < SK_OOB;
+}
+
+template <int WT>
+static void launch_skinny(hipStream_t s, const GemmParams& p) {
+    const dim3 grid((unsigned)((p.N + SK_ROWS - 1) / SK_ROWS * p.splits));
+    switch ((p.M + 15) / 16) {
+        case 1: hipLaunchKernelGGL((gemm_skinny_kernel<WT, 1>), grid, dim3(64 * SK_KP), 0, s, p); break;
+        case 2: hipLaunchKernelGGL((gemm_skinny_kernel<WT, 2>), grid, dim3(64 * SK_KP), 0, s, p); break;
+        case 3: hipLaunchKernelGGL((gemm_skinny_kernel<WT, 3>), grid, dim3(64 * SK_KP), 0, s, p); break;
+        default: hipLaunchKernelGGL((gemm_skinny_kernel<WT, 4>), grid, dim3(64 * SK_KP), 0, s, p); break;
+    }
+}
+
 template <int WT, int BM, int BN, int NS>
 __global__ __launch_bounds__(512) void gemm_lds_kernel(GemmParams p, float* __restrict__ part, int mT, int nT, int splits) {
     using L = Gl<WT, BM, BN, NS>;
@@ -607,7 +967,20 @@ static void launch_gemm2(hipStream_t s, const GemmParams& p, int splits, float* 
 // M > 64 (multi-stage 128 x 128 tiles, one workgroup per CU): up to 4
 // slices while the grid stays within 320 workgroups, at least 8 K steps
 // per slice.
-int gemm_splits(int M, int N, int K) {
+int gemm_splits(int M, int N, int K, int wt) {
+    if (wt < 0) {   // any weight type: the largest count any of them takes
+        int sp = 1;
+        for (int t : {(int)TLHIP_F16, (int)TLHIP_Q8_0, (int)TLHIP_Q4_0, (int)TLHIP_Q6_K}) sp = std::max(sp, gemm_splits(M, N, K, t));
+        return sp;
+    }
+    if (gemm_skinny_ok(M, N, K, wt)) {
+        // skinny: slices until about 256 workgroups, each slice at least
+        // one 64-k step per wave
+        const int tiles = (N + SK_ROWS - 1) / SK_ROWS;
+        int sp = 1;
+        while (sp < SK_MAX_SPLITS && tiles * (sp + 1) <= 256 && (K / 64) / (sp + 1) >= SK_KP) sp++;
+        return tiles <= SK_MAX_TILES_SPLIT ? sp : 1;
+    }
     if (K % G2_BK) return 1;
     int sp = 1;
     if (M > 64) {
@@ -658,8 +1031,22 @@ tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
         hipLaunchKernelGGL(gemm_naive_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p);
         return TLHIP_OK;
     }
+    if (gemm_skinny_ok(p.M, p.N, p.K, wt)) {
+        // K split over workgroups only with a workspace for the partials and
+        // the per-tile counters
+        const int sp = gemm_splits(p.M, p.N, p.K, wt);
+        if (sp > 1 && a.ws && a.tile_flags && (size_t)sp * p.M * p.N * sizeof(float) <= a.ws_bytes) {
+            p.splits = sp;
+            p.part = a.ws;
+            p.flags = a.tile_flags;
+        }
+        if (wt == TLHIP_Q4_0) launch_skinny<TLHIP_Q4_0>(s, p);
+        else if (wt == TLHIP_Q8_0) launch_skinny<TLHIP_Q8_0>(s, p);
+        else launch_skinny<TLHIP_F16>(s, p);
+        return TLHIP_OK;
+    }
     if (p.K % G2_BK == 0) {
-        int splits = a.ws ? gemm_splits(p.M, p.N, p.K) : 1;
+        int splits = a.ws ? gemm_splits(p.M, p.N, p.K, wt) : 1;
         if ((size_t)splits * p.M * p.N * sizeof(float) > a.ws_bytes) splits = 1;
         float* part = splits > 1 ? a.ws : nullptr;
         if (wt == TLHIP_Q4_0) launch_gemm2<TLHIP_Q4_0>(s, p, splits, part);

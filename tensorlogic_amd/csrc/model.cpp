@@ -301,10 +301,12 @@ tlhip_status fused_weight(tlhip_ctx ctx, tlhip_gguf g, const std::vector<std::pa
 }
 
 tlhip_status linear_into(hipStream_t s, const Lin& l, const uint16_t* x, int M, uint16_t* y, int epi,
-                         const uint16_t* resid, int ldy = 0, float* ws = nullptr, size_t ws_bytes = 0) {
+                         const uint16_t* resid, int ldy = 0, float* ws = nullptr, size_t ws_bytes = 0,
+                         uint32_t* tile_flags = nullptr) {
     GemvArgs a;
     a.ws = ws;
     a.ws_bytes = ws_bytes;
+    a.tile_flags = tile_flags;
     a.x = x;
     a.wq = l.w->data;
     a.wd = l.w->scales;
@@ -393,7 +395,7 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
         } else {
             if (m->arch == 0) TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.norm_w), P(m->xn), S, H, m->eps));
             else TLHIP_TRY(launch_layer_norm(s, P(m->x), P(L.norm_w), P(L.norm_b), P(m->xn), S, H, m->eps));
-            TLHIP_TRY(linear_into(s, L.qkv, P(m->xn), S, P(m->qkv), L.qkv.b ? EPI_BIAS : EPI_STORE, nullptr, 0, m->ws, m->ws_bytes));
+            TLHIP_TRY(linear_into(s, L.qkv, P(m->xn), S, P(m->qkv), L.qkv.b ? EPI_BIAS : EPI_STORE, nullptr, 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
             TLHIP_TRY(launch_rope_kv(s, P(m->qkv), qkv_w, S, NH, NKV, D, m->arch == 0 ? 0 : 2, m->rot,
                                      m->rope_tab, decode ? 0 : pos0, d_pos, P(m->qrot), kc, vc));
         }
@@ -419,16 +421,16 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
             else TLHIP_TRY(launch_attention_j(s, at, pos0 + S));
         }
         if (m->arch == 0) {
-            TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_RESID, P(m->x), 0, m->ws, m->ws_bytes));
+            TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_RESID, P(m->x), 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
             if (row1) {
                 GemvArgs a = fused_norm_args(m, L.gu, P(m->x), L.ffn_norm_w, nullptr);
                 a.y = P(m->hmid);
                 TLHIP_TRY(launch_gemv(s, L.gu.w->dtype, a, EPI_SWIGLU_PAIR));
             } else {
                 TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.ffn_norm_w), P(m->xn), S, H, m->eps));
-                TLHIP_TRY(linear_into(s, L.gu, P(m->xn), S, P(m->hmid), EPI_SWIGLU_PAIR, nullptr, 0, m->ws, m->ws_bytes));
+                TLHIP_TRY(linear_into(s, L.gu, P(m->xn), S, P(m->hmid), EPI_SWIGLU_PAIR, nullptr, 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
             }
-            TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_RESID, P(m->x), 0, m->ws, m->ws_bytes));
+            TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_RESID, P(m->x), 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
         } else {
             // phi2: the MLP reads the same layer_norm output as attention
             if (row1) {
@@ -436,9 +438,9 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
                 a.y = P(m->hmid);
                 TLHIP_TRY(launch_gemv(s, L.up.w->dtype, a, EPI_BIAS_GELU));
             }
-            TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes));
-            if (!row1) TLHIP_TRY(linear_into(s, L.up, P(m->xn), S, P(m->hmid), EPI_BIAS_GELU, nullptr, 0, m->ws, m->ws_bytes));
-            TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes));
+            TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
+            if (!row1) TLHIP_TRY(linear_into(s, L.up, P(m->xn), S, P(m->hmid), EPI_BIAS_GELU, nullptr, 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
+            TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
         }
     }
     const uint16_t* last = P(m->x) + (size_t)(S - 1) * H;
@@ -623,6 +625,7 @@ tlhip_status tlhip_kvcache_get(tlhip_kvcache c, int layer, int which_v, tlhip_te
     auto* view = new tlhip_tensor_s();
     *view = *src;
     view->refcount = 1;
+    view->f16_copy = nullptr;
     view->shape[0] = shp[0];
     view->base = src;
     src->refcount++;
@@ -818,7 +821,7 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
             size_t need = 0;
             for (int rows = 5; rows <= (int)R; rows++)
                 for (auto& sh : shapes) {
-                    const int sp = gemm_splits(rows, (int)sh[0], (int)sh[1]);
+                    const int sp = gemm_splits(rows, (int)sh[0], (int)sh[1], -1);
                     if (sp > 1) need = std::max(need, (size_t)sp * rows * sh[0] * sizeof(float));
                 }
             if (need) {

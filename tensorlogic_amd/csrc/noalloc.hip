@@ -11,10 +11,12 @@
 // name, to kernels.
 //
 // The split is the one tlhip_linear picks (gemm_splits), so both entry points
-// run the same kernels and produce the same bits.  Every partial the reduce
+// run the same kernels and produce the same bits.  Every partial a reduction
 // reads is written by the GEMM of the same call (each slice covers every
 // output element of its tiles), so the contents a previous call left behind
-// never matter and nothing is cleared.  All calls on one GPU share the array:
+// never matter and nothing is cleared.  The skinny GEMM's arrival counters
+// live in the context (allocated by tlhip_init) and every launch leaves them
+// at zero.  All calls on one GPU share the array:
 // calls that overlap in time on one GPU (two contexts' streams, two host
 // threads) race on it and must be serialised by the caller.
 #include <mutex>
@@ -25,7 +27,8 @@ namespace {
 
 // Largest split-K partial set gemm_splits can ask for: M > 64 keeps at most
 // 320 / 2 = 160 tiles of 128 x 128 per split product (sp * M * N <= 160 *
-// 16384 floats = 10.5 MB); M <= 64 at most 256 tiles of 64 x 64 (4 MiB).
+// 16384 floats = 10.5 MB); M <= 64 splits only up to 128 tiles of 32 rows,
+// at most 8 slices (8 * 64 * 4096 floats = 8 MiB).
 constexpr size_t kScratchBytes = 16u << 20;
 constexpr int kMaxDevices = 64;
 

@@ -85,6 +85,7 @@ tlhip_status linear_impl(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_te
     a.wd = w->scales;
     a.bias = bias ? P(bias) : nullptr;
     a.y = P(y);
+    a.tile_flags = ctx->d_tile_flags;
     a.M = (int)M;
     a.N = (int)N;
     a.K = (int)K;
@@ -97,29 +98,33 @@ tlhip_status linear_impl(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_te
     if (st == TLHIP_OK) return after_launch(ctx, "linear");
     const bool no_alloc = fixed_ws != nullptr;
     // Q6_K weights reach the MFMA GEMM as their dequantised f16 copy (the
-    // reference's own representation), from the stream-ordered pool
-    tlhip_tensor wf = nullptr;
+    // reference's own representation), made once per weight tensor on its
+    // first use here and kept with it
     tlhip_dtype wt = w->dtype;
     if (wt == TLHIP_Q6_K && no_alloc)
         return fail(TLHIP_ERR_INVALID_OPERATION,
                     "linear_noalloc: a Q6_K weight with M = %lld > 4 needs a dequantised f16 copy, which "
                     "this entry point cannot allocate (use tlhip_linear)", (long long)M);
     if (wt == TLHIP_Q6_K) {
-        int64_t shp[2] = {N, K};
-        TLHIP_TRY(alloc_tensor(ctx, TLHIP_F16, 2, shp, &wf));
-        st = launch_dequant(ctx->stream, TLHIP_Q6_K, w->data, w->scales, P(wf), N, K);
-        if (st != TLHIP_OK) {
-            tlhip_tensor_free(wf);
-            return st;
+        if (!w->f16_copy) {
+            tlhip_tensor wf = nullptr;
+            int64_t shp[2] = {N, K};
+            TLHIP_TRY(alloc_tensor(ctx, TLHIP_F16, 2, shp, &wf));
+            st = launch_dequant(ctx->stream, TLHIP_Q6_K, w->data, w->scales, P(wf), N, K);
+            if (st != TLHIP_OK) {
+                tlhip_tensor_free(wf);
+                return st;
+            }
+            w->f16_copy = wf;
         }
-        a.wq = wf->data;
+        a.wq = w->f16_copy->data;
         a.wd = nullptr;
         wt = TLHIP_F16;
     }
-    // MFMA GEMM; a split-K workspace from the stream-ordered pool when the
-    // output has too few tiles to fill the device
-    tlhip_tensor ws = nullptr;
-    const int sp = gemm_splits((int)M, (int)N, (int)K);
+    // MFMA GEMM; a split-K workspace when the output has too few tiles to
+    // fill the device: the context's, grown (stream-ordered) when a call
+    // needs more, so steady-state calls allocate nothing
+    const int sp = gemm_splits((int)M, (int)N, (int)K, (int)wt);
     const size_t need = (size_t)sp * M * N * sizeof(float);
     if (sp > 1 && no_alloc) {
         // the caller's fixed workspace: the same split as the pool path, so
@@ -131,16 +136,22 @@ tlhip_status linear_impl(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_te
         a.ws = fixed_ws;
         a.ws_bytes = need;
     } else if (sp > 1) {
-        int64_t shp[1] = {(int64_t)sp * M * N};
-        if (alloc_tensor(ctx, TLHIP_F32, 1, shp, &ws) == TLHIP_OK) {
-            a.ws = (float*)ws->data;
+        if (need > ctx->ws_bytes) {
+            void* grown = nullptr;
+            if (hipMallocAsync(&grown, need, ctx->stream) == hipSuccess) {
+                if (ctx->d_ws) (void)hipFreeAsync(ctx->d_ws, ctx->stream);   // after the GEMMs that used it
+                ctx->d_ws = (float*)grown;
+                ctx->ws_bytes = need;
+            } else {
+                (void)hipGetLastError();   // no workspace: the GEMM runs unsplit
+            }
+        }
+        if (need <= ctx->ws_bytes) {
+            a.ws = ctx->d_ws;
             a.ws_bytes = need;
         }
     }
-    st = launch_gemm(ctx->stream, wt, a, epi);
-    tlhip_tensor_free(ws);   // stream-ordered: returns to the pool after the GEMM
-    tlhip_tensor_free(wf);
-    TLHIP_TRY(st);
+    TLHIP_TRY(launch_gemm(ctx->stream, wt, a, epi));
     return after_launch(ctx, "linear");
 }
 

@@ -78,6 +78,11 @@ void ctx_release(tlhip_ctx ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     for (auto& r : ctx->rope_tables) (void)hipFree(r.dev);
     (void)hipFree(ctx->d_scratch_i32);
+    (void)hipFree(ctx->d_tile_flags);
+    if (ctx->d_ws) {
+        (void)hipFreeAsync(ctx->d_ws, ctx->stream);
+        (void)hipStreamSynchronize(ctx->stream);
+    }
     (void)hipHostFree(ctx->h_pinned_i32);
     (void)hipEventDestroy(ctx->ev0);
     (void)hipEventDestroy(ctx->ev1);
@@ -228,6 +233,8 @@ tlhip_status tlhip_init(int device, tlhip_ctx* out) {
     TLHIP_CHECK_HIP(hipEventCreate(&c->ev0));
     TLHIP_CHECK_HIP(hipEventCreate(&c->ev1));
     TLHIP_CHECK_HIP(hipMalloc(&c->d_scratch_i32, 256 * sizeof(int32_t)));
+    TLHIP_CHECK_HIP(hipMalloc(&c->d_tile_flags, SK_MAX_TILES_SPLIT * sizeof(uint32_t)));
+    TLHIP_CHECK_HIP(hipMemset(c->d_tile_flags, 0, SK_MAX_TILES_SPLIT * sizeof(uint32_t)));
     TLHIP_CHECK_HIP(hipHostMalloc(&c->h_pinned_i32, 256 * sizeof(int32_t), hipHostMallocDefault));
     // Keep freed pool memory cached in the pool instead of returning it to
     // the driver at every synchronisation.
@@ -293,6 +300,11 @@ tlhip_status tlhip_tensor_upload(tlhip_ctx ctx, tlhip_tensor t, const void* host
         TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
         return TLHIP_OK;
     }
+    // new contents: a dequantised copy made from the old ones is stale
+    if (t->f16_copy) {
+        tlhip_tensor_free(t->f16_copy);
+        t->f16_copy = nullptr;
+    }
     // Packed GGUF blocks -> staging -> structure-of-arrays repack on device.
     void* stage = nullptr;
     TLHIP_CHECK_HIP(hipMallocAsync(&stage, bytes, ctx->stream));
@@ -346,6 +358,7 @@ tlhip_status tlhip_tensor_free(tlhip_tensor t) {
     if (t->base) {
         tlhip_tensor_free(t->base);
     } else if (t->data) {
+        if (t->f16_copy) tlhip_tensor_free(t->f16_copy);
         (void)hipSetDevice(t->ctx->device);
         (void)hipFreeAsync(t->data, t->ctx->stream);
         ctx_release(t->ctx);
@@ -379,6 +392,7 @@ tlhip_status tlhip_tensor_reshape(tlhip_tensor t, int ndim, const int64_t* shape
     auto* v = new tlhip_tensor_s();
     *v = *t;
     v->refcount = 1;
+    v->f16_copy = nullptr;
     v->ndim = ndim;
     for (int i = 0; i < 8; i++) v->shape[i] = i < ndim ? shape[i] : 0;
     tlhip_tensor owner = t->base ? t->base : t;

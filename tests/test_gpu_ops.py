@@ -143,12 +143,38 @@ def test_linear_q6_k(dev, oracle, M, N, K):
     assert_close(y, ref, what=f"q6_k linear {M}x{N}x{K}")
 
 
+def test_linear_q6_k_copy_follows_upload(dev, oracle):
+    """The f16 copy a Q6_K weight keeps for the GEMM (M > 4) is made once,
+    gives the same bits on the next call, and is replaced when the weight's
+    contents are uploaded again."""
+    M, N, K = 12, 200, 512
+    b1 = S.q6_k_blocks(8, "W6c1", N, K)
+    b2 = S.q6_k_blocks(8, "W6c2", N, K)
+    x = S.normal_f16(8, "x6c", (M, K))
+    w = dev.quantized(b1, (N, K), Q6_K)
+    tx = dev.tensor(x)
+    y1 = tx.linear(w).numpy()
+    assert np.array_equal(tx.linear(w).numpy().view(np.uint16), y1.view(np.uint16))
+    assert_close(y1, oracle.linear_q(x, b1, 14, N), what="q6_k first contents")
+    from tensorlogic_amd._lib import call
+    import ctypes as C
+    bb = np.ascontiguousarray(b2)
+    call("tlhip_tensor_upload", dev.h, w.h, bb.ctypes.data_as(C.c_void_p), bb.nbytes)
+    assert_close(tx.linear(w).numpy(), oracle.linear_q(x, b2, 14, N), what="q6_k after re-upload")
+
+
 @pytest.mark.parametrize("qt", [Q4_0, Q8_0, F16])
 @pytest.mark.parametrize("M,N,K", [(46, 5632, 2048), (5, 64, 64), (64, 256, 512), (130, 96, 2048),
                                    (512, 512, 2048), (33, 100, 96), (17, 2048, 5632), (64, 130, 160),
                                    (8, 40, 32), (512, 2048, 5632), (200, 384, 1024), (65, 256, 128),
                                    # config 2's remaining cells: M = 46 on W_down, M = 512 on W_up/gate
-                                   (46, 2048, 5632), (512, 5632, 2048)])
+                                   (46, 2048, 5632), (512, 5632, 2048),
+                                   # skinny path (M <= 64, K % 64 == 0): ragged N, one to four
+                                   # 16-row M tiles, K parts of unequal length; up to 128 tiles of
+                                   # 32 rows also split K over workgroups (2 to 5 slices here)
+                                   (7, 77, 256), (20, 300, 768), (63, 1000, 384), (5, 2048, 2048),
+                                   (48, 2560, 2048), (33, 11264, 2048), (9, 500, 320), (12, 640, 1472),
+                                   (64, 4096, 2048)])
 def test_linear_gemm(dev, oracle, qt, M, N, K):
     x = S.normal_f16(3, f"x{M}x{K}", (M, K))
     if qt == F16:
@@ -164,10 +190,13 @@ def test_linear_gemm(dev, oracle, qt, M, N, K):
     assert_close(y, ref, what=f"gemm {qt} {M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("qt,M,N,K", [(Q8_0, 46, 5632, 2048), (Q4_0, 512, 2048, 5632), (F16, 33, 256, 4096)])
+@pytest.mark.parametrize("qt,M,N,K", [(Q8_0, 46, 5632, 2048), (Q4_0, 512, 2048, 5632), (F16, 33, 256, 4096),
+                                      (Q4_0, 46, 2048, 5632), (F16, 12, 640, 1472)])
 def test_gemm_split_k_deterministic(dev, oracle, qt, M, N, K):
     """Split-K GEMMs sum their fp32 slices in slice order: repeated calls
-    give identical bits (no order depends on scheduling)."""
+    give identical bits (no order depends on scheduling).  The skinny
+    GEMM's split (the last workgroup of a tile to arrive adds the slices)
+    also resets its arrival counters: every repeat is correct."""
     x = S.normal_f16(7, f"xs{M}x{K}", (M, K))
     if qt == F16:
         wh = S.normal_f16(7, f"Ws{N}x{K}", (N, K), 0.0, 0.05)

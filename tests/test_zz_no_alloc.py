@@ -32,8 +32,9 @@ def _linear_pair(dev, oracle, qt, M, N, K, seed):
     return y_na.numpy(), y_ref.numpy(), ref
 
 
-# (qt, M, N, K): split-K GEMMs of both kernels (M <= 64: 2 and 8 slices;
-# M > 64: 2 slices), then a smaller call reusing the array, then a GEMV
+# (qt, M, N, K): split-K GEMMs of both kernels (M <= 64: the skinny GEMM,
+# unsplit at 176 weight-row tiles, 4 and 8 slices at 64 and 8 tiles; M > 64:
+# 2 slices), then a smaller call reusing the array, then a GEMV
 @pytest.mark.parametrize("calls", [
     [(Q8_0, 46, 5632, 2048), (Q8_0, 20, 2048, 2048)],
     [(Q4_0, 512, 2048, 2048), (Q4_0, 130, 256, 2048)],
@@ -47,8 +48,9 @@ def test_linear_noalloc_matches_linear(dev, oracle, calls):
 
 
 def test_linear_noalloc_with_bias_repeated(dev, oracle):
-    """Bias epilogue through the split-K reduce (8 slices), twice in a row on
-    the same tensors: the second call reads only what it wrote itself.  The
+    """Bias epilogue through the skinny GEMM's split (8 slices), twice in a
+    row on the same tensors: the second call reads only what it wrote
+    itself.  The
     activations are N(0, 0.25) so that outputs stay below 8, where the bias
     add's second f16 rounding is within the 2e-2 bar."""
     M, N, K = 33, 512, 4096
