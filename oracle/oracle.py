@@ -18,7 +18,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
-ACC_F32, ACC_F16 = 0, 1
+ACC_F32, ACC_F16, ACC_F32_REV = 0, 1, 2   # ACC_F32_REV: fp32 sums in descending order
 ROPE_INTERLEAVED, ROPE_NEOX = 0, 1
 
 _lib = None

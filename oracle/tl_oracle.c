@@ -172,6 +172,13 @@ static float dot_f32acc(const float* a, const float* b, int K) {
     return s;
 }
 
+/* TLO_ACC_F32_REV: the same sum in descending k -- a second fp32 order */
+static float dot_f32acc_rev(const float* a, const float* b, int K) {
+    float s = 0.0f;
+    for (int k = K - 1; k >= 0; k--) s += a[k] * b[k];
+    return s;
+}
+
 /* f16 accumulation: matmul_cpu (matmul.rs:201-228), `sum += a * b` on
  * half::f16 -- the product is rounded to f16, then the sum is.             */
 static uint16_t dot_f16acc(const float* a, const float* b, int K) {
@@ -189,8 +196,9 @@ static void linear_rows_f32w(const float* xf, const float* wf, const uint16_t* b
     for (int n = 0; n < N; n++) {
         const float* wr = wf + (size_t)n * K;
         for (int m = 0; m < M; m++) {
-            uint16_t r = (acc_mode == TLO_ACC_F16) ? dot_f16acc(xf + (size_t)m * K, wr, K)
-                                                   : tlo_f2h(dot_f32acc(xf + (size_t)m * K, wr, K));
+            uint16_t r = (acc_mode == TLO_ACC_F16)       ? dot_f16acc(xf + (size_t)m * K, wr, K)
+                         : (acc_mode == TLO_ACC_F32_REV) ? tlo_f2h(dot_f32acc_rev(xf + (size_t)m * K, wr, K))
+                                                         : tlo_f2h(dot_f32acc(xf + (size_t)m * K, wr, K));
             if (bias) r = tlo_f2h(H2F(r) + H2F(bias[n]));
             y[(size_t)m * N + n] = r;
         }
@@ -432,7 +440,10 @@ void tlo_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                 for (int j = 0; j < J; j++) {
                     const uint16_t* kr = k + ((size_t)j * Hkv + kvh) * D;
                     float acc = 0.0f;
-                    for (int d = 0; d < D; d++) acc += qf[d] * H2F(kr[d]);
+                    if (acc_mode == TLO_ACC_F32_REV)
+                        for (int d = D - 1; d >= 0; d--) acc += qf[d] * H2F(kr[d]);
+                    else
+                        for (int d = 0; d < D; d++) acc += qf[d] * H2F(kr[d]);
                     uint16_t sv = tlo_f2h(acc);                 /* einsum store  */
                     sv = tlo_f2h(H2F(sv) * scale_h);            /* scores * c    */
                     if (causal && j > qpos) sv = tlo_f2h(-10000.0f);  /* mask */
@@ -448,6 +459,11 @@ void tlo_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                             a = tlo_f2h(H2F(a) + H2F(pr));
                         }
                         orow[d] = a;
+                    } else if (acc_mode == TLO_ACC_F32_REV) {
+                        float a = 0.0f;
+                        for (int j = J - 1; j >= 0; j--)
+                            a += H2F(p[j]) * H2F(v[((size_t)j * Hkv + kvh) * D + d]);
+                        orow[d] = tlo_f2h(a);
                     } else {
                         float a = 0.0f;
                         for (int j = 0; j < J; j++)

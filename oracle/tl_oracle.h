@@ -16,7 +16,11 @@
  *                  where the reference stores f16 (the parity oracle);
  *   TLO_ACC_F16 -- the reference CPU loops' own f16 accumulation
  *                  (src/ops/matmul.rs:201-228, unified.metal:2646-2684),
- *                  used only as the timed CPU baseline.
+ *                  used only as the timed CPU baseline;
+ *   TLO_ACC_F32_REV -- TLO_ACC_F32 with the linear and attention (scores
+ *                  and context) sums taken in descending order: a second, equally valid
+ *                  fp32 order, used only to measure how far a model's
+ *                  outputs move between two fp32 summation orders.
  *
  * Pinning of each function is recorded in tests/ (test_oracle_*.py).
  */
@@ -30,7 +34,7 @@
 extern "C" {
 #endif
 
-enum { TLO_ACC_F32 = 0, TLO_ACC_F16 = 1 };
+enum { TLO_ACC_F32 = 0, TLO_ACC_F16 = 1, TLO_ACC_F32_REV = 2 };
 enum { TLO_ROPE_INTERLEAVED = 0, TLO_ROPE_NEOX = 1 };
 
 /* Number of OpenMP threads used by the loops below (the calling thread's

@@ -32,6 +32,7 @@ struct GemmParams {
     float* part = nullptr;
     uint32_t* flags = nullptr;
     int splits = 1;
+    int mtiles = 1;   // skinny GEMM: workgroups along M
 };
 
 constexpr int GBM = 64, GBN = 64, GBK = 32, GPAD = 8;
@@ -388,16 +389,21 @@ __device__ __forceinline__ int gl_tile(int id, int T) {   // XCD-contiguous tile
 
 // ---------------------------------------------------------------------------
 // Skinny dequant-GEMM (4 < M <= 64, K % 64 == 0) on v_mfma_f32_16x16x32_f16:
-// one launch, no workspace.  Every workgroup reads all of x (M x K) and its
-// own weight rows once; both streams enter the CU as whole 64-byte pieces,
+// one launch, no workspace by default.  A workgroup reads its activation
+// rows and weight rows once; both enter the CU as whole 64-byte pieces,
 // because the vector L1 handles a load one piece per lane-run of adjacent
 // addresses: an MFMA operand read straight from a row-major matrix (one row
-// per lane) costs one L1 access per lane, here one per 64 bytes.
+// per lane) costs one L1 access per lane, here one per 64 bytes.  What
+// bounds it is the bytes each CU takes in: the activation rows (which every
+// workgroup of the same rows re-reads) plus its own weight rows.  The host
+// plan (sk_plan) picks per shape how many 16-row M tiles a workgroup covers
+// (MT) and how many 16-row weight tiles (NT), so that the largest per-CU
+// byte count is smallest.
 //
-// A workgroup (4 waves) owns SK_ROWS = 32 weight rows as two 16-row tiles;
-// wave w takes K part w (K / 64 steps of 64 k split into 4 ranges) for both
-// tiles.  Each wave streams its part through a private ring of L::ST LDS
-// stages with buffer loads to LDS (16 bytes per lane, adjacent lanes on
+// A workgroup (4 waves) owns MT x 16 activation rows and 16 NT weight rows;
+// wave w takes K part w (the workgroup's 64-k steps split into 4 ranges) for
+// all of them.  Each wave streams its part through a private ring of L::ST
+// LDS stages with buffer loads to LDS (16 bytes per lane, adjacent lanes on
 // adjacent bytes; the 16-byte pieces of a row XOR-swizzled by row so the
 // operand reads below spread over the banks), then reads the operands of
 // sub-step t = 0, 1 in the natural 16 x 16 x 32 layout -- lane l (tile row /
@@ -407,39 +413,44 @@ __device__ __forceinline__ int gl_tile(int id, int T) {   // XCD-contiguous tile
 //   bytes of block 2q + t (low nibbles for g < 2, high for g >= 2), with the
 //   block's scale,
 // dequantised with the correctly rounded RNE_f16((q - 8) d) / RNE_f16(q d)
-// of every other path.  Ring stages past the wave's range are filled from
-// offsets outside the buffers (no memory access) and never read, so every
-// stage has the same number of loads and the waits are fixed counts.  The
-// four K parts' fp32 accumulators meet in LDS and are added in a fixed order
-// (part 0 + 1 + 2 + 3) before the epilogue.
+// of every other path.  A wave issues only the stages of its own range and
+// waits for a stage with the exact count of loads issued after it.  Rows
+// past M and weight rows past N are read from offsets outside the buffers
+// (zeros, no memory access).  The four K parts' fp32 accumulators meet in
+// LDS and are added in a fixed order (part 0 + 1 + 2 + 3) before the
+// epilogue.  C layout of a 16 x 16 tile: lane l holds column (weight row)
+// l % 16 and activation rows 4 (l / 16) + r.
 //
-// When the weight rows give fewer than ~128 workgroups, K is also split over
-// p.splits workgroups per tile (block b: tile b / splits, K slice
+// K may also be split over p.splits workgroups per tile (block b: slice
 // b % splits).  Each writes its fp32 tile to p.part and counts itself in on
 // the tile's counter; the last to arrive adds the slices in slice order --
 // the same bits whichever arrives last -- applies the epilogue and resets
-// the counter to zero for the next launch, so no second kernel runs.  C layout of a 16 x 16 tile:
-// lane l holds column (weight row) l % 16 and activation rows 4 (l / 16) + r.
+// the counter to zero for the next launch, so no second kernel runs.  The
+// exchange costs a few microseconds of memory round trips, so the plan
+// splits only where that pays.  Every choice but the split leaves each
+// output's summation order, and so its bits, unchanged.
 // ---------------------------------------------------------------------------
-constexpr int SK_ROWS = 32, SK_KP = 4;   // weight rows, K parts (waves)
 constexpr int SK_LDS = 160 * 1024 - 1024;   // LDS the rings may take
+constexpr uint32_t SK_OOB = 0x80000000u;    // a buffer offset past every tensor
 constexpr int SK_MAX_SPLITS = 8;
-constexpr uint32_t SK_OOB = 0x80000000u;            // a buffer offset past every tensor
 
-template <int WT, int MT>
+template <int WT, int MT, int NT, int KP>
 struct SkL {   // LDS bytes of one stage (one 64-k step) of one wave
+    static constexpr int ROWS = 16 * NT;      // weight rows per workgroup
     static constexpr int X = MT * 16 * 128;   // activation rows, 128 bytes each
     static constexpr int WROW = WT == TLHIP_F16 ? 128 : (WT == TLHIP_Q8_0 ? 64 : 32);
-    static constexpr int W = SK_ROWS * WROW;
-    static constexpr int S = WT == TLHIP_F16 ? 0 : 256;   // 32 rows x 2 scales (+ the unused upper half)
+    static constexpr int W = ROWS * WROW;
+    static constexpr int S = WT == TLHIP_F16 ? 0 : 256;   // ROWS x 2 scales, one 4-byte load per lane
     static constexpr int STAGE = X + W + S;
     static constexpr int NX = X / 1024, NW = W / 1024, NS = S ? 1 : 0;
     static constexpr int C = NX + NW + NS;   // loads per stage
     // stages per wave: as many as the LDS holds (the deeper the ring, the
-    // fewer memory round trips a wave's part takes), at most 6
-    static constexpr int ST = SK_LDS / (SK_KP * STAGE) < 6 ? SK_LDS / (SK_KP * STAGE) : 6;
-    static_assert(X % 1024 == 0 && W % 1024 == 0, "1 KB loads");
-    static_assert(ST >= 2 && (ST - 1) * C < 64, "stages, vmcnt range");
+    // fewer memory round trips a wave's part takes), at most 6; a shape with
+    // fewer than 2 is not launched (sk_plan)
+    static constexpr int ST0 = SK_LDS / (KP * STAGE);
+    static constexpr int ST = ST0 < 6 ? ST0 : 6;
+    static constexpr bool OK = ST >= 2 && (ST - 1) * C < 64;
+    static_assert(X % 1024 == 0 && W % 1024 == 0 && ROWS * 4 <= 256, "load shapes");
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const void* base, uint32_t bytes) {
@@ -464,19 +475,48 @@ template <int N>
 __device__ __forceinline__ void sk_wait_vm() {   // a compiler barrier for memory, unlike the builtin
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// wait until at most `ahead` stages of C loads each are outstanding
+template <int C, int K>
+__device__ __forceinline__ void sk_wait_stages(int ahead) {
+    if constexpr (K == 0) {
+        sk_wait_vm<0>();
+    } else {
+        if (ahead >= K) sk_wait_vm<K * C>();
+        else sk_wait_stages<C, K - 1>(ahead);
+    }
+}
 
-template <int WT, int MT>
-__global__ __launch_bounds__(64 * SK_KP) void gemm_skinny_kernel(GemmParams p) {
-    using L = SkL<WT, MT>;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[SK_KP * L::ST * L::STAGE];
+// Operand layout of one 64-k step (the k order inside an MFMA is free as
+// long as both operands follow it).  Lane l = (column / row l % 16, group
+// g = l / 16) holds at sub-step t the 8 elements k = 64 q + 8 c + i of its
+// activation row, c = sk_piece(g, t), and of its weight row:
+//   f16:  c = 4t + g, 16 bytes per sub-step;
+//   Q8_0: c = 4(g/2) + 2(g%2) + t -- 16 bytes of block 2q + g/2 (elements
+//         16(g%2) .. +15) give both sub-steps;
+//   Q4_0: c = 4(g/2) + 2t + g%2 -- 8 bytes of block 2q + g/2 (bytes
+//         8(g%2) .. +7) give both: low nibbles (elements 8(g%2) .. +7) at
+//         t = 0, high nibbles (elements 16 + 8(g%2) .. +7) at t = 1;
+// each block dequantised with its scale as RNE_f16((q - 8) d) / RNE_f16(q d).
+template <int WT>
+__device__ __forceinline__ int sk_piece(int g, int t) {
+    if constexpr (WT == TLHIP_F16) return 4 * t + g;
+    else if constexpr (WT == TLHIP_Q8_0) return 4 * (g >> 1) + 2 * (g & 1) + t;
+    else return 4 * (g >> 1) + 2 * t + (g & 1);
+}
+
+template <int WT, int MT, int NT, int KP>
+__global__ __launch_bounds__(64 * KP) void gemm_skinny_kernel(GemmParams p) {
+    using L = SkL<WT, MT, NT, KP>;
+    static_assert(L::OK, "ring");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[KP * L::ST * L::STAGE];
     const int lane = threadIdx.x & 63;
     const int kp = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);   // wave-uniform
     const int nl = lane & 15, g = lane >> 4;
-    const int tile = (int)blockIdx.x / p.splits, z = (int)blockIdx.x % p.splits;
-    const int n0 = tile * SK_ROWS;
+    const int z = (int)blockIdx.x % p.splits, mn = (int)blockIdx.x / p.splits;   // K slice, (M tile, N tile)
+    const int m0 = mn % p.mtiles * 16 * MT, n0 = mn / p.mtiles * L::ROWS;
     const int nq = p.K >> 6;
     const int za = nq * z / p.splits, nz = nq * (z + 1) / p.splits - za;   // this workgroup's K slice (steps)
-    const int qa = za + nz * kp / SK_KP, qb = za + nz * (kp + 1) / SK_KP;
+    const int qa = za + nz * kp / KP, nst = za + nz * (kp + 1) / KP - qa;
     uint8_t* const ring = smem + kp * L::ST * L::STAGE;
     const uint32_t ring_lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(gl_lds_t)ring);
     const uint32_t K = (uint32_t)p.K;
@@ -490,12 +530,12 @@ __global__ __launch_bounds__(64 * SK_KP) void gemm_skinny_kernel(GemmParams p) {
 
     // source byte offsets (step 0) of this lane's 16 bytes in each load:
     // LDS piece P = 64 u + lane of the region, rows of 8 (x, f16 weights),
-    // 4 (Q8_0) or 2 (Q4_0) pieces
+    // 4 (Q8_0) or 2 (Q4_0) pieces, XOR-swizzled by row
     uint32_t xsrc[L::NX], wsrc[L::NW], dsrc = SK_OOB;
 #pragma unroll
     for (int u = 0; u < L::NX; u++) {
         const int P = 64 * u + lane, r = P >> 3, c = (P & 7) ^ (r & 7);
-        xsrc[u] = r < p.M ? (uint32_t)r * K * 2u + 16u * c : SK_OOB;
+        xsrc[u] = m0 + r < p.M ? (uint32_t)(m0 + r) * K * 2u + 16u * c : SK_OOB;
     }
 #pragma unroll
     for (int u = 0; u < L::NW; u++) {
@@ -506,143 +546,150 @@ __global__ __launch_bounds__(64 * SK_KP) void gemm_skinny_kernel(GemmParams p) {
         else { n = P >> 1; c = (P & 1) ^ ((n >> 2) & 1); }
         wsrc[u] = n0 + n < p.N ? (uint32_t)(n0 + n) * wrow + 16u * c : SK_OOB;
     }
-    if (L::NS && lane < SK_ROWS && n0 + lane < p.N) dsrc = (uint32_t)(n0 + lane) * (K / 32u) * 2u;
+    if (L::NS && lane < L::ROWS && n0 + lane < p.N) dsrc = (uint32_t)(n0 + lane) * (K / 32u) * 2u;
 
     // operand offsets inside a stage
-    int xrd[MT][2], wrd[2][2], drd[2];
+    int xrd[MT][2], wrd[NT][2], drd[NT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            const int r = 16 * mt + nl, c = 4 * t + g;
-            xrd[mt][t] = r * 128 + 16 * (c ^ (r & 7));
+            const int r = 16 * mt + nl;
+            xrd[mt][t] = r * 128 + 16 * (sk_piece<WT>(g, t) ^ (r & 7));
         }
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
+    for (int j = 0; j < NT; j++) {
         const int n = 16 * j + nl;
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             if (WT == TLHIP_F16) wrd[j][t] = L::X + n * 128 + 16 * ((4 * t + g) ^ (n & 7));
-            else if (WT == TLHIP_Q8_0) wrd[j][t] = L::X + n * 64 + 16 * ((2 * t + (g >> 1)) ^ ((n >> 1) & 3)) + 8 * (g & 1);
-            else wrd[j][t] = L::X + n * 32 + 16 * (t ^ ((n >> 2) & 1)) + 8 * (g & 1);
+            else if (WT == TLHIP_Q8_0) wrd[j][t] = L::X + n * 64 + 16 * ((2 * (g >> 1) + (g & 1)) ^ ((n >> 1) & 3));
+            else wrd[j][t] = L::X + n * 32 + 16 * ((g >> 1) ^ ((n >> 2) & 1)) + 8 * (g & 1);
         }
-        drd[j] = L::X + L::W + 4 * n;
+        drd[j] = L::X + L::W + 4 * n + 2 * (g >> 1);   // this lane's block's scale
     }
 
-    // one stage's loads: step q into stage st (past the range: offsets
-    // outside the buffers, no memory access)
+    // one stage's loads: step q into stage st
     auto issue = [&](int q, int st) {
-        const uint32_t oob = q < qb ? 0u : SK_OOB;
         const uint32_t base = ring_lds + (uint32_t)(st * L::STAGE);
 #pragma unroll
-        for (int u = 0; u < L::NX; u++) sk_dma<16>(rx, base + 1024u * u, (xsrc[u] + (uint32_t)q * 128u) | oob);
+        for (int u = 0; u < L::NX; u++) sk_dma<16>(rx, base + 1024u * u, xsrc[u] + (uint32_t)q * 128u);
 #pragma unroll
-        for (int u = 0; u < L::NW; u++) sk_dma<16>(rw, base + L::X + 1024u * u, (wsrc[u] + (uint32_t)q * WSTEP) | oob);
-        if constexpr (L::NS > 0) sk_dma<4>(rd, base + L::X + L::W, (dsrc + (uint32_t)q * 4u) | oob);
+        for (int u = 0; u < L::NW; u++) sk_dma<16>(rw, base + L::X + 1024u * u, wsrc[u] + (uint32_t)q * WSTEP);
+        if constexpr (L::NS > 0) sk_dma<4>(rd, base + L::X + L::W, dsrc + (uint32_t)q * 4u);
     };
 
-    f4 acc[2][MT];
+    f4 acc[NT][MT];
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < NT; j++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[j][mt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-#pragma unroll
-    for (int st = 0; st < L::ST; st++) issue(qa + st, st);
-    int st = 0;
-    for (int q = qa; q < qb; q++) {
-        sk_wait_vm<(L::ST - 1) * L::C>();   // this step's stage has landed (loads complete in order)
+    // the operands of one stage and its MFMAs
+    auto compute = [&](int st) {
         const uint8_t* base = ring + st * L::STAGE;
-        h8 a[MT][2], b[2][2];
+        h8 a[MT][2], b[NT][2];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int t = 0; t < 2; t++) a[mt][t] = *(const h8*)(base + xrd[mt][t]);
         if constexpr (WT == TLHIP_F16) {
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < NT; j++)
 #pragma unroll
                 for (int t = 0; t < 2; t++) b[j][t] = *(const h8*)(base + wrd[j][t]);
         } else {
-            uint2 w[2][2];
-            uint32_t d[2];
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-#pragma unroll
-                for (int t = 0; t < 2; t++) w[j][t] = *(const uint2*)(base + wrd[j][t]);
-                d[j] = *(const uint32_t*)(base + drd[j]);
-            }
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-#pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    const h16 dh = __builtin_bit_cast(h16, (uint16_t)(t ? d[j] >> 16 : d[j] & 0xFFFFu));
-                    const h2 dd = {dh, dh};
-                    uint32_t o0, o1, o2, o3;
-                    if constexpr (WT == TLHIP_Q8_0) {
-                        q8_pairs(w[j][t].x, dd, o0, o1);
-                        q8_pairs(w[j][t].y, dd, o2, o3);
-                    } else {
-                        const int sh = (g >> 1) * 4;   // groups 2, 3 take the high nibbles
-                        q4_pairs((w[j][t].x >> sh) & 0x0F0F0F0Fu, dd, o0, o1);
-                        q4_pairs((w[j][t].y >> sh) & 0x0F0F0F0Fu, dd, o2, o3);
-                    }
-                    b[j][t] = __builtin_bit_cast(h8, u4{o0, o1, o2, o3});
+            for (int j = 0; j < NT; j++) {
+                const h16 dh = *(const h16*)(base + drd[j]);
+                const h2 dd = {dh, dh};
+                uint32_t o[8];
+                if constexpr (WT == TLHIP_Q8_0) {
+                    const u4 w = *(const u4*)(base + wrd[j][0]);   // 16 elements: t = 0 bytes 0-7, t = 1 bytes 8-15
+                    q8_pairs(w[0], dd, o[0], o[1]);
+                    q8_pairs(w[1], dd, o[2], o[3]);
+                    q8_pairs(w[2], dd, o[4], o[5]);
+                    q8_pairs(w[3], dd, o[6], o[7]);
+                } else {
+                    const uint2 w = *(const uint2*)(base + wrd[j][0]);   // low nibbles t = 0, high nibbles t = 1
+                    q4_pairs(w.x & 0x0F0F0F0Fu, dd, o[0], o[1]);
+                    q4_pairs(w.y & 0x0F0F0F0Fu, dd, o[2], o[3]);
+                    q4_pairs((w.x >> 4) & 0x0F0F0F0Fu, dd, o[4], o[5]);
+                    q4_pairs((w.y >> 4) & 0x0F0F0F0Fu, dd, o[6], o[7]);
                 }
+                b[j][0] = __builtin_bit_cast(h8, u4{o[0], o[1], o[2], o[3]});
+                b[j][1] = __builtin_bit_cast(h8, u4{o[4], o[5], o[6], o[7]});
+            }
         }
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+                for (int j = 0; j < NT; j++)
                     acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt][t], b[j][t], acc[j][mt], 0, 0, 0);
+    };
+
+#pragma unroll
+    for (int st = 0; st < L::ST; st++)
+        if (st < nst) issue(qa + st, st);
+    // steady state: every step refills its stage, so L::ST - 1 stages are
+    // always in flight after it; then the last L::ST - 1 steps (fewer if the
+    // part is short) drain the ring
+    int st = 0, i = 0;
+    for (; i + L::ST < nst; i++) {
+        sk_wait_vm<(L::ST - 1) * L::C>();   // this step's stage has landed (loads complete in order)
+        compute(st);
         // the stage's reads have returned before its refill is issued
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        issue(q + L::ST, st);
+        issue(qa + i + L::ST, st);
         __builtin_amdgcn_sched_barrier(0);
         st = st + 1 == L::ST ? 0 : st + 1;
     }
+    for (; i < nst; i++) {
+        sk_wait_stages<L::C, L::ST - 1>(nst - 1 - i);
+        compute(st);
+        st = st + 1 == L::ST ? 0 : st + 1;
+    }
 
-    // every part's partial tiles to LDS (over the ring, once every wave's
-    // loads have landed); wave w then reduces (tile, row tile) pairs w and
-    // w + 4 in part order and applies the epilogue
-    sk_wait_vm<0>();
+    // every part's partial tiles to LDS (over the rings: every wave's loads
+    // have landed); wave w then reduces (weight tile, M tile) pairs w,
+    // w + KP, ... in part order and applies the epilogue
     __syncthreads();
-    float (*red)[2][MT * 4][64] = (float (*)[2][MT * 4][64])smem;
-    static_assert(sizeof(float) * SK_KP * 2 * MT * 4 * 64 <= sizeof(smem), "reduction fits the ring");
+    float (*red)[NT][MT * 4][64] = (float (*)[NT][MT * 4][64])smem;
+    static_assert(sizeof(float) * KP * NT * MT * 4 * 64 <= sizeof(smem), "reduction fits the rings");
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < NT; j++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) red[kp][j][mt * 4 + r][lane] = acc[j][mt][r];
     const bool use_b = p.epi == EPI_BIAS || p.epi == EPI_BIAS_RESID || p.epi == EPI_BIAS_GELU;
     const bool use_r = p.epi == EPI_RESID || p.epi == EPI_BIAS_RESID;
-    constexpr int NP = (2 * MT + SK_KP - 1) / SK_KP;   // pairs per wave
+    constexpr int NP = (NT * MT + KP - 1) / KP;   // pairs per wave
     uint32_t bv[NP], rv[NP][4];
 #pragma unroll
     for (int i = 0; i < NP; i++) {   // epilogue operands loaded before the barrier
-        const int pr = kp + SK_KP * i, j = pr & 1, mt = pr >> 1;
+        const int pr = kp + KP * i, j = pr % NT, mt = pr / NT;
         const int n = min(n0 + 16 * j + nl, p.N - 1);
         bv[i] = use_b && mt < MT ? (uint32_t)p.bias[n] : 0u;
 #pragma unroll
         for (int r = 0; r < 4; r++)
-            rv[i][r] = use_r && mt < MT ? (uint32_t)p.resid[(size_t)min(16 * mt + 4 * g + r, p.M - 1) * p.N + n] : 0u;
+            rv[i][r] = use_r && mt < MT ? (uint32_t)p.resid[(size_t)min(m0 + 16 * mt + 4 * g + r, p.M - 1) * p.N + n] : 0u;
     }
     __syncthreads();
     float vs[NP][4];
 #pragma unroll
     for (int i = 0; i < NP; i++) {
-        const int pr = kp + SK_KP * i, j = pr & 1, mt = pr >> 1;
+        const int pr = kp + KP * i, j = pr % NT, mt = pr / NT;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             float v = 0.0f;
             if (mt < MT) {
                 v = red[0][j][mt * 4 + r][lane];
 #pragma unroll
-                for (int u = 1; u < SK_KP; u++) v += red[u][j][mt * 4 + r][lane];
+                for (int u = 1; u < KP; u++) v += red[u][j][mt * 4 + r][lane];
             }
             vs[i][r] = v;
         }
@@ -658,11 +705,11 @@ __global__ __launch_bounds__(64 * SK_KP) void gemm_skinny_kernel(GemmParams p) {
         __shared__ int sk_last;
 #pragma unroll
         for (int i = 0; i < NP; i++) {
-            const int pr = kp + SK_KP * i, j = pr & 1, mt = pr >> 1;
+            const int pr = kp + KP * i, j = pr % NT, mt = pr / NT;
             const int ncol = n0 + 16 * j + nl;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = 16 * mt + 4 * g + r;
+                const int m = m0 + 16 * mt + 4 * g + r;
                 if (mt < MT && m < p.M && ncol < p.N)
                     __hip_atomic_store(p.part + ((size_t)z * p.M + m) * p.N + ncol, vs[i][r], __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
@@ -671,19 +718,19 @@ __global__ __launch_bounds__(64 * SK_KP) void gemm_skinny_kernel(GemmParams p) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (threadIdx.x == 0)
-            sk_last = __hip_atomic_fetch_add(p.flags + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            sk_last = __hip_atomic_fetch_add(p.flags + mn, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                       (uint32_t)(p.splits - 1);
         __syncthreads();
         if (!sk_last) return;
-        if (threadIdx.x == 0) __hip_atomic_store(p.flags + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) __hip_atomic_store(p.flags + mn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
         for (int i = 0; i < NP; i++) {
-            const int pr = kp + SK_KP * i, j = pr & 1, mt = pr >> 1;
+            const int pr = kp + KP * i, j = pr % NT, mt = pr / NT;
             const int ncol = min(n0 + 16 * j + nl, p.N - 1);
             float t[4][SK_MAX_SPLITS];   // every slice's value loaded before the in-order sum
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = min(16 * mt + 4 * g + r, p.M - 1);
+                const int m = min(m0 + 16 * mt + 4 * g + r, p.M - 1);
 #pragma unroll
                 for (int zz = 0; zz < SK_MAX_SPLITS; zz++)
                     t[r][zz] = mt < MT && zz < p.splits
@@ -702,13 +749,13 @@ __global__ __launch_bounds__(64 * SK_KP) void gemm_skinny_kernel(GemmParams p) {
     }
 #pragma unroll
     for (int i = 0; i < NP; i++) {
-        const int pr = kp + SK_KP * i, j = pr & 1, mt = pr >> 1;
+        const int pr = kp + KP * i, j = pr % NT, mt = pr / NT;
         if (mt >= MT) break;
         const int ncol = n0 + 16 * j + nl;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const float v = vs[i][r];
-            const int m = 16 * mt + 4 * g + r;
+            const int m = m0 + 16 * mt + 4 * g + r;
             if (p.epi == EPI_SWIGLU_PAIR) {
                 const float up = __shfl_down(v, 1, 64);
                 if (m < p.M && ncol + 1 < p.N && (ncol & 1) == 0)
@@ -728,14 +775,78 @@ bool gemm_skinny_ok(int M, int N, int K, int wt) {
            (uint64_t)N * wrow < SK_OOB && 2ull * M * K < SK_OOB;
 }
 
+// The skinny GEMM's launch shape for (M, N, K, weight type): M tiles per
+// workgroup, weight tiles per workgroup, K slices.  A cost model of the
+// measured kernel: a workgroup takes its bytes in at about 50 GB/s, plus
+// 2.5 us of fixed time per round of workgroups (one workgroup per CU: the
+// rings fill the LDS), plus 4 us for the exchange of a K split.
+// The skinny GEMM's launch shape for (M, N, K, weight type): M tiles per
+// workgroup (mt), 16-row weight tiles per workgroup (nt), waves (K parts)
+// per workgroup (kp) and K slices.  A cost model of the measured kernel: a
+// workgroup takes its bytes in at about 50 GB/s, plus 2.5 us of fixed time
+// per round of workgroups (one workgroup per CU: the rings fill the LDS),
+// plus 4 us for the exchange of a K split.  Eight waves (two per SIMD, so
+// one's dequantisation overlaps the other's MFMAs and waits) wherever the
+// LDS still holds a two-stage ring for each.
+struct SkPlan {
+    int mt = 1, nt = 2, kp = 4, mtiles = 1, splits = 1;
+};
+static int sk_stage_bytes(int wt, int mt, int nt) {
+    const int wrow = wt == TLHIP_F16 ? 128 : (wt == TLHIP_Q8_0 ? 64 : 32);
+    return mt * 16 * 128 + 16 * nt * wrow + (wt == TLHIP_F16 ? 0 : 256);
+}
+static SkPlan sk_plan(int M, int N, int K, int wt) {
+    const double bpe = wt == TLHIP_F16 ? 2.0 : (wt == TLHIP_Q8_0 ? 34.0 / 32 : 18.0 / 32);
+    const int mt16 = (M + 15) / 16;
+    SkPlan best;
+    double best_us = 1e30;
+    for (int nt : {2, 4})
+        for (int mt = 1; mt <= mt16; mt++) {
+            const int kp = SK_LDS / (8 * sk_stage_bytes(wt, mt, nt)) >= 2 ? 8 : 4;
+            for (int sp = 1; sp <= SK_MAX_SPLITS; sp *= 2) {
+                const int mtiles = (mt16 + mt - 1) / mt, ntiles = (N + 16 * nt - 1) / (16 * nt);
+                if (sp > 1 && ((K / 64) / sp < kp || mtiles * ntiles > SK_MAX_TILES_SPLIT)) continue;
+                const long wgs = (long)mtiles * ntiles * sp;
+                const double rounds = (double)((wgs + 255) / 256);
+                const double bytes = (std::min(16 * mt, M) * 2.0 + 16 * nt * bpe) * K / sp;
+                const double us = rounds * (bytes / 50e3 + 2.5) + (sp > 1 ? 4.0 : 0.0);
+                if (us < best_us - 1e-9) {
+                    best_us = us;
+                    best.mt = mt;
+                    best.nt = nt;
+                    best.kp = kp;
+                    best.mtiles = mtiles;
+                    best.splits = sp;
+                }
+            }
+        }
+    return best;
+}
+
+template <int WT, int MT, int NT, int KP>
+static void launch_skinny_one(hipStream_t s, const GemmParams& p) {
+    if constexpr (SkL<WT, MT, NT, KP>::OK) {
+        const dim3 grid((unsigned)(p.mtiles * ((p.N + 16 * NT - 1) / (16 * NT)) * p.splits));
+        hipLaunchKernelGGL((gemm_skinny_kernel<WT, MT, NT, KP>), grid, dim3(64 * KP), 0, s, p);
+    }
+}
+template <int WT, int NT, int KP>
+static void launch_skinny_mt(hipStream_t s, const GemmParams& p, int mt) {
+    switch (mt) {
+        case 1: launch_skinny_one<WT, 1, NT, KP>(s, p); break;
+        case 2: launch_skinny_one<WT, 2, NT, KP>(s, p); break;
+        case 3: launch_skinny_one<WT, 3, NT, KP>(s, p); break;
+        default: launch_skinny_one<WT, 4, NT, KP>(s, p); break;
+    }
+}
 template <int WT>
-static void launch_skinny(hipStream_t s, const GemmParams& p) {
-    const dim3 grid((unsigned)((p.N + SK_ROWS - 1) / SK_ROWS * p.splits));
-    switch ((p.M + 15) / 16) {
-        case 1: hipLaunchKernelGGL((gemm_skinny_kernel<WT, 1>), grid, dim3(64 * SK_KP), 0, s, p); break;
-        case 2: hipLaunchKernelGGL((gemm_skinny_kernel<WT, 2>), grid, dim3(64 * SK_KP), 0, s, p); break;
-        case 3: hipLaunchKernelGGL((gemm_skinny_kernel<WT, 3>), grid, dim3(64 * SK_KP), 0, s, p); break;
-        default: hipLaunchKernelGGL((gemm_skinny_kernel<WT, 4>), grid, dim3(64 * SK_KP), 0, s, p); break;
+static void launch_skinny(hipStream_t s, const GemmParams& p, const SkPlan& pl) {
+    if (pl.nt == 4) {
+        if (pl.kp == 8) launch_skinny_mt<WT, 4, 8>(s, p, pl.mt);
+        else launch_skinny_mt<WT, 4, 4>(s, p, pl.mt);
+    } else {
+        if (pl.kp == 8) launch_skinny_mt<WT, 2, 8>(s, p, pl.mt);
+        else launch_skinny_mt<WT, 2, 4>(s, p, pl.mt);
     }
 }
 
@@ -973,14 +1084,7 @@ int gemm_splits(int M, int N, int K, int wt) {
         for (int t : {(int)TLHIP_F16, (int)TLHIP_Q8_0, (int)TLHIP_Q4_0, (int)TLHIP_Q6_K}) sp = std::max(sp, gemm_splits(M, N, K, t));
         return sp;
     }
-    if (gemm_skinny_ok(M, N, K, wt)) {
-        // skinny: slices until about 256 workgroups, each slice at least
-        // one 64-k step per wave
-        const int tiles = (N + SK_ROWS - 1) / SK_ROWS;
-        int sp = 1;
-        while (sp < SK_MAX_SPLITS && tiles * (sp + 1) <= 256 && (K / 64) / (sp + 1) >= SK_KP) sp++;
-        return tiles <= SK_MAX_TILES_SPLIT ? sp : 1;
-    }
+    if (gemm_skinny_ok(M, N, K, wt)) return sk_plan(M, N, K, wt).splits;
     if (K % G2_BK) return 1;
     int sp = 1;
     if (M > 64) {
@@ -1034,15 +1138,16 @@ tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
     if (gemm_skinny_ok(p.M, p.N, p.K, wt)) {
         // K split over workgroups only with a workspace for the partials and
         // the per-tile counters
-        const int sp = gemm_splits(p.M, p.N, p.K, wt);
-        if (sp > 1 && a.ws && a.tile_flags && (size_t)sp * p.M * p.N * sizeof(float) <= a.ws_bytes) {
-            p.splits = sp;
+        const SkPlan pl = sk_plan(p.M, p.N, p.K, wt);
+        p.mtiles = pl.mtiles;
+        if (pl.splits > 1 && a.ws && a.tile_flags && (size_t)pl.splits * p.M * p.N * sizeof(float) <= a.ws_bytes) {
+            p.splits = pl.splits;
             p.part = a.ws;
             p.flags = a.tile_flags;
         }
-        if (wt == TLHIP_Q4_0) launch_skinny<TLHIP_Q4_0>(s, p);
-        else if (wt == TLHIP_Q8_0) launch_skinny<TLHIP_Q8_0>(s, p);
-        else launch_skinny<TLHIP_F16>(s, p);
+        if (wt == TLHIP_Q4_0) launch_skinny<TLHIP_Q4_0>(s, p, pl);
+        else if (wt == TLHIP_Q8_0) launch_skinny<TLHIP_Q8_0>(s, p, pl);
+        else launch_skinny<TLHIP_F16>(s, p, pl);
         return TLHIP_OK;
     }
     if (p.K % G2_BK == 0) {

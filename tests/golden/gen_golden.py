@@ -10,6 +10,13 @@ tinyllama_q4_0_tokens.json -- config 4: the TinyLlama-1.1B-shape Q4_0 model
     that must reproduce the greedy stream) and the final logits (f16
     values).  The GPU test regenerates the same file from the seed and
     compares.
+tinyllama_q4_0_margins_tokens.json -- the config-4 architecture with real
+    logit margins (RMSNorm weights 1 + N(0, 0.02), zero-mean Q4_0 codes;
+    see tinyllama_margins_tokens), recorded the same way plus each step's
+    top-2 margin in f16 ulps, and the same model run by the oracle with
+    every fp32 sum taken in descending order (ACC_F32_REV): its per-step
+    top-8 deviation teacher-forced and its free-running greedy stream -- how
+    far a second, equally valid fp32 summation order moves this model.
 phi2_q8_0_tokens.json -- config 5: the Phi-2-shape Q8_0 model of
     write_phi2_gguf(seed=5), 512-token prompt token_ids(5, "prompt", 512,
     51200), 256 greedy decode steps, recorded the same way.
@@ -43,6 +50,7 @@ def synth_checksums():
     draws = {
         "q4_0_blocks(1,'W',64,256)": S.q4_0_blocks(1, "W", 64, 256).tobytes(),
         "q8_0_blocks(1,'W',64,256)": S.q8_0_blocks(1, "W", 64, 256).tobytes(),
+        "q4_0_blocks(1,'W',64,256,zero_mean)": S.q4_0_blocks(1, "W", 64, 256, zero_mean=True).tobytes(),
         "normal_f16(1,'x',(4,2048))": S.normal_f16(1, "x", (4, 2048)).tobytes(),
         "token_ids(4,'prompt',46,32000)": S.token_ids(4, "prompt", 46, 32000).tobytes(),
     }
@@ -88,6 +96,51 @@ def tinyllama_tokens(n_decode=128, seed=4):
     return {"config": "TinyLlama-1.1B shape, Q4_0 linear weights, seed 4", "seed": seed, **rec}
 
 
+def reordered_oracle(path, prompt, rec, n_decode, top=8):
+    """The oracle with every fp32 sum in descending order (ACC_F32_REV) on
+    the same model: per-step deviation of its top-k logits from rec's, in
+    f16 ulps of the top logit, on rec's own token stream (teacher-forced),
+    and its free-running greedy stream."""
+    ids = np.array(rec[f"top{top}_ids"], np.int64)
+    vals = np.array(rec[f"top{top}_logits"], np.float64)
+    toks = np.array(rec["tokens"], np.int32)
+    m = O.Model(path, arch=0, max_ctx=256, acc=O.ACC_F32_REV)
+    dev = []
+    _, lg = m.forward(prompt, 0)
+    for step in range(n_decode + 1):
+        ulp = 2.0 ** (np.floor(np.log2(max(abs(vals[step][0]), 2.0 ** -14))) - 10)
+        dev.append(float(np.abs(lg.astype(np.float64)[ids[step]] - vals[step]).max() / ulp))
+        if step < n_decode:
+            _, lg = m.forward(np.array([toks[step]], np.int32), len(prompt) + step)
+    m.reset()
+    rtoks, _, _ = m.generate(prompt, n_decode)
+    m.close()
+    bad = np.nonzero(rtoks != toks)[0]
+    return {"reorder_dev_ulps": dev, "reorder_tokens": rtoks.tolist(),
+            "reorder_first_divergence": int(bad[0]) if bad.size else n_decode + 1}
+
+
+def tinyllama_margins_tokens(n_decode=128, seed=8):
+    """Config-4 shape (22 layers, 2048 / 5632, 32 / 4 heads, vocab 32000),
+    Q4_0, with RMSNorm weights 1 + N(0, 0.02) and Q4_0 codes symmetric about
+    8 (synth.write_llama_gguf(zero_mean=True)): logits of a few units, so
+    the greedy stream is diverse and its top-2 margins are real.  The seed
+    is the one of seeds 5..16 whose smallest margin over the 129 steps,
+    in f16 ulps of the top logit, comes latest and is largest."""
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "tinyllama_margins.gguf")
+        S.write_llama_gguf(path, seed=seed, norm_mean=1.0, zero_mean=True, **S.TINYLLAMA_ARGS)
+        prompt = S.token_ids(seed, "prompt", 46, S.TINYLLAMA_ARGS["vocab"])
+        rec = record_tokens(path, 0, prompt, n_decode, 256)
+        rec.update(reordered_oracle(path, prompt, rec, n_decode))
+    top = np.array(rec["top8_logits"], np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(top[:, 0]), 2.0 ** -14))) - 10)
+    rec["margin_ulps"] = [float(v) for v in (top[:, 0] - top[:, 1]) / ulp]
+    rec["min_margin_ulps"] = float(min(rec["margin_ulps"]))
+    return {"config": "TinyLlama-1.1B shape, Q4_0 (codes 1..15), RMSNorm weights 1 + N(0, 0.02), seed "
+                      f"{seed}", "seed": seed, **rec}
+
+
 def phi2_tokens(n_decode=256, seed=5):
     with tempfile.TemporaryDirectory() as td:
         path = os.path.join(td, "phi2.gguf")
@@ -103,6 +156,7 @@ def main():
     a = ap.parse_args()
     jobs = {"synth_checksums.json": synth_checksums,
             "tinyllama_q4_0_tokens.json": tinyllama_tokens,
+            "tinyllama_q4_0_margins_tokens.json": tinyllama_margins_tokens,
             "phi2_q8_0_tokens.json": phi2_tokens}
     for name, fn in jobs.items():
         if a.only and a.only != name:
