@@ -243,6 +243,30 @@ def test_linear_f16_accumulation_is_matmul_cpu(oracle):
     assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
 
 
+def test_linear_reversed_fp32_order(oracle):
+    # ACC_F32_REV sums k in descending order: on integer-valued inputs every
+    # partial sum is exact, so both orders agree bit for bit; on random
+    # inputs both stay within 1 ulp of the float64 product and differ
+    # somewhere (an order-insensitive implementation would not), and a
+    # reversed attention matches the forward one within the same bound
+    x = (S.token_ids(33, "xi", 3 * 64, 7).reshape(3, 64) - 3).astype(np.float16)
+    w = (S.token_ids(33, "wi", 5 * 64, 5).reshape(5, 64) - 2).astype(np.float16)
+    assert np.array_equal(oracle.linear(x, w, acc=oracle.ACC_F32_REV).view(np.uint16),
+                          oracle.linear(x, w).view(np.uint16))
+    x = S.normal_f16(33, "x", (16, 2048))
+    w = S.normal_f16(33, "w", (64, 2048), 0.0, 0.2)
+    fwd, rev = oracle.linear(x, w), oracle.linear(x, w, acc=oracle.ACC_F32_REV)
+    ref = (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float16)
+    assert ulps(fwd, ref).max() <= 1 and ulps(rev, ref).max() <= 1
+    assert not np.array_equal(fwd.view(np.uint16), rev.view(np.uint16))
+    q = S.normal_f16(33, "q", (4, 8, 64))
+    k = S.normal_f16(33, "k", (40, 2, 64))
+    v = S.normal_f16(33, "v", (40, 2, 64))
+    a = oracle.attention(q, k, v, 36, 0.125, True)
+    b = oracle.attention(q, k, v, 36, 0.125, True, acc=oracle.ACC_F32_REV)
+    assert ulps(a, b).max() <= 2
+
+
 # ---------------------------------------------------------------------------
 # RMSNorm (normalization.rs:199-250, unified.metal:1785-1831)
 # ---------------------------------------------------------------------------
