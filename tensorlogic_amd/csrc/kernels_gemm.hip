@@ -322,7 +322,6 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmParams p, float* __restr
 // M tiles of one N tile adjacent, so the BM-row tiles that share a weight
 // tile run on one XCD and read it through one L2.
 // ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void* gl_lds_t;
 
 template <int WT>
 struct GlRow {   // LDS bytes of one weight row per 64-wide K step
@@ -453,28 +452,6 @@ struct SkL {   // LDS bytes of one stage (one 64-k step) of one wave
     static_assert(X % 1024 == 0 && W % 1024 == 0 && ROWS * 4 <= 256, "load shapes");
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-// Buffer load to LDS at wave-uniform LDS byte address lds (+ 16 or 4 bytes
-// per lane), written as assembly: the compiler then neither tracks these
-// LDS writes (it would wait for every one of them before any LDS read) nor
-// counts them, and the kernel waits for them itself with sk_wait_vm.  M0
-// holds the LDS address (one wait state between its write and the load);
-// the compiler uses M0 for nothing else in the kernels that call this.
-template <int SZ>
-__device__ __forceinline__ void sk_dma(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t off) {
-    if constexpr (SZ == 16)
-        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(off), "s"(r)
-                     : "memory");
-    else
-        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(lds), "v"(off), "s"(r)
-                     : "memory");
-}
-template <int N>
-__device__ __forceinline__ void sk_wait_vm() {   // a compiler barrier for memory, unlike the builtin
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 // wait until at most `ahead` stages of C loads each are outstanding
 template <int C, int K>
 __device__ __forceinline__ void sk_wait_stages(int ahead) {
