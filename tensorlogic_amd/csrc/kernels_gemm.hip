@@ -33,6 +33,13 @@ struct GemmParams {
     uint32_t* flags = nullptr;
     int splits = 1;
     int mtiles = 1;   // skinny GEMM: workgroups along M
+    // skinny GEMM, EPI_QKV_ROPE: columns [0, nq) are q, [nq, nq + nk) k, the
+    // rest v; row m is position pos0 + m (as the GEMV's fused epilogue)
+    int nq = 0, nk = 0, head_dim = 0, rot = 0, layout = 0, pos0 = 0;
+    const float* rope_tab = nullptr;
+    uint16_t* q_out = nullptr;
+    uint16_t* kc = nullptr;
+    uint16_t* vc = nullptr;
 };
 
 constexpr int GBM = 64, GBN = 64, GBK = 32, GPAD = 8;
@@ -556,6 +563,39 @@ __global__ __launch_bounds__(64 * KP) void gemm_skinny_kernel(GemmParams p) {
         if constexpr (L::NS > 0) sk_dma<4>(rd, base + L::X + L::W, dsrc + (uint32_t)q * 4u);
     };
 
+    const bool rope = p.epi == EPI_QKV_ROPE;
+    const bool use_b = p.epi == EPI_BIAS || p.epi == EPI_BIAS_RESID || p.epi == EPI_BIAS_GELU || (rope && p.bias);
+    const bool use_r = p.epi == EPI_RESID || p.epi == EPI_BIAS_RESID;
+    constexpr int NP = (NT * MT + KP - 1) / KP;   // pairs per wave
+    uint32_t bv[NP], rv[NP][4];
+    float rc[NP][4], rsn[NP][4];   // EPI_QKV_ROPE: the rotation of this lane's column pair at each row
+#pragma unroll
+    for (int i = 0; i < NP; i++) {   // epilogue operands, loaded while the K loop runs
+        const int pr = kp + KP * i, j = pr % NT, mt = pr / NT;
+        const int n = min(n0 + 16 * j + nl, p.N - 1);
+        bv[i] = use_b && mt < MT ? (uint32_t)p.bias[n] : 0u;
+        // EPI_QKV_ROPE: this column pair's place in its head (one division
+        // per column, not per row)
+        int re = -1;
+        if (rope && mt < MT) {
+            const int ne = n & ~1, D = p.head_dim;
+            re = ne < p.nq ? ne % D : (ne < p.nq + p.nk ? (ne - p.nq) % D : -1);
+            if (re >= p.rot) re = -1;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = min(m0 + 16 * mt + 4 * g + r, p.M - 1);
+            rv[i][r] = use_r && mt < MT ? (uint32_t)p.resid[(size_t)m * p.N + n] : 0u;
+            rc[i][r] = 1.0f;
+            rsn[i][r] = 0.0f;
+            if (re >= 0) {
+                const size_t ti = 2 * ((size_t)(p.pos0 + m) * (p.rot >> 1) + (re >> 1));
+                rc[i][r] = p.rope_tab[ti];
+                rsn[i][r] = p.rope_tab[ti + 1];
+            }
+        }
+    }
+
     f4 acc[NT][MT];
 #pragma unroll
     for (int j = 0; j < NT; j++)
@@ -642,19 +682,6 @@ __global__ __launch_bounds__(64 * KP) void gemm_skinny_kernel(GemmParams p) {
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) red[kp][j][mt * 4 + r][lane] = acc[j][mt][r];
-    const bool use_b = p.epi == EPI_BIAS || p.epi == EPI_BIAS_RESID || p.epi == EPI_BIAS_GELU;
-    const bool use_r = p.epi == EPI_RESID || p.epi == EPI_BIAS_RESID;
-    constexpr int NP = (NT * MT + KP - 1) / KP;   // pairs per wave
-    uint32_t bv[NP], rv[NP][4];
-#pragma unroll
-    for (int i = 0; i < NP; i++) {   // epilogue operands loaded before the barrier
-        const int pr = kp + KP * i, j = pr % NT, mt = pr / NT;
-        const int n = min(n0 + 16 * j + nl, p.N - 1);
-        bv[i] = use_b && mt < MT ? (uint32_t)p.bias[n] : 0u;
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-            rv[i][r] = use_r && mt < MT ? (uint32_t)p.resid[(size_t)min(m0 + 16 * mt + 4 * g + r, p.M - 1) * p.N + n] : 0u;
-    }
     __syncthreads();
     float vs[NP][4];
 #pragma unroll
@@ -729,11 +756,54 @@ __global__ __launch_bounds__(64 * KP) void gemm_skinny_kernel(GemmParams p) {
         const int pr = kp + KP * i, j = pr % NT, mt = pr / NT;
         if (mt >= MT) break;
         const int ncol = n0 + 16 * j + nl;
+        // EPI_QKV_ROPE: destination of this column pair (per column, not per row)
+        int sect = 0, hoff = 0, e = 0;
+        if (rope) {
+            const int D = p.head_dim;
+            if (ncol < p.nq) {
+                hoff = ncol / D * D;
+                e = ncol - hoff;
+            } else if (ncol < p.nq + p.nk) {
+                sect = 1;
+                hoff = (ncol - p.nq) / D * D;
+                e = ncol - p.nq - hoff;
+            } else {
+                sect = 2;
+                hoff = ncol - p.nq - p.nk;
+            }
+        }
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const float v = vs[i][r];
             const int m = m0 + 16 * mt + 4 * g + r;
-            if (p.epi == EPI_SWIGLU_PAIR) {
+            if (rope) {
+                // the f16 projection (plus bias) of this column and of its
+                // pair partner (column ^ 1, the neighbouring lane), rotated
+                // and stored as the GEMV's fused epilogue does
+                uint16_t x = f2h(v);
+                if (p.bias) x = add_h(x, (uint16_t)bv[i]);
+                const uint32_t xo = (uint32_t)__shfl_xor((int)x, 1, 64);
+                if ((ncol & 1) == 0 && m < p.M && ncol + 1 < p.N) {
+                    const int pos = p.pos0 + m;
+                    if (sect == 2) {
+                        p.vc[(size_t)pos * p.nk + hoff] = x;
+                        p.vc[(size_t)pos * p.nk + hoff + 1] = (uint16_t)xo;
+                        continue;
+                    }
+                    uint16_t* dst = sect ? p.kc + (size_t)pos * p.nk + hoff : p.q_out + (size_t)m * p.nq + hoff;
+                    if (e < p.rot) {
+                        const int half = p.rot >> 1, ip = e >> 1;
+                        const float x0 = h2f(x), x1 = h2f((uint16_t)xo), c = rc[i][r], sn = rsn[i][r];
+                        const float o0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
+                        const float o1 = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, c));
+                        dst[p.layout ? ip : 2 * ip] = f2h(o0);
+                        dst[p.layout ? ip + half : 2 * ip + 1] = f2h(o1);
+                    } else {
+                        dst[e] = x;
+                        dst[e + 1] = (uint16_t)xo;
+                    }
+                }
+            } else if (p.epi == EPI_SWIGLU_PAIR) {
                 const float up = __shfl_down(v, 1, 64);
                 if (m < p.M && ncol + 1 < p.N && (ncol & 1) == 0)
                     p.y[(size_t)m * p.ldy + ncol / 2] = swiglu_h(f2h(v), f2h(up));
@@ -1100,8 +1170,24 @@ tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
     p.K = a.K;
     p.ldy = a.ldy ? a.ldy : (epi == EPI_SWIGLU_PAIR ? a.N / 2 : a.N);
     p.epi = epi;
-    if (epi == EPI_QKV_ROPE || a.pro != PRO_NONE)
-        return fail(TLHIP_ERR_INVALID_OPERATION, "gemm: fused normalisation / RoPE epilogue is GEMV-only");
+    if (a.pro != PRO_NONE)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "gemm: the fused normalisation prologue is GEMV-only");
+    if (epi == EPI_QKV_ROPE) {
+        if (!gemm_skinny_ok(p.M, p.N, p.K, wt) || a.d_pos || !a.rope_tab || !a.q_out || !a.kc || !a.vc ||
+            a.head_dim <= 0 || a.head_dim % 2 || a.rot % 2 || a.rot > a.head_dim || a.nq % a.head_dim ||
+            a.nk % a.head_dim || a.nq + 2 * a.nk != p.N)
+            return fail(TLHIP_ERR_INVALID_OPERATION, "gemm: the RoPE epilogue needs the skinny GEMM and a q/k/v layout");
+        p.nq = a.nq;
+        p.nk = a.nk;
+        p.head_dim = a.head_dim;
+        p.rot = a.rot;
+        p.layout = a.layout;
+        p.pos0 = a.pos0;
+        p.rope_tab = a.rope_tab;
+        p.q_out = a.q_out;
+        p.kc = a.kc;
+        p.vc = a.vc;
+    }
     if (wt != TLHIP_F16 && wt != TLHIP_Q4_0 && wt != TLHIP_Q8_0)
         return fail(TLHIP_ERR_DTYPE, "gemm: weight dtype %d takes the dequantised f16 path", (int)wt);
     if (p.M <= 0 || p.N <= 0) return TLHIP_OK;

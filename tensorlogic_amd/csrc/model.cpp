@@ -395,9 +395,36 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
         } else {
             if (m->arch == 0) TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.norm_w), P(m->xn), S, H, m->eps));
             else TLHIP_TRY(launch_layer_norm(s, P(m->x), P(L.norm_w), P(L.norm_b), P(m->xn), S, H, m->eps));
-            TLHIP_TRY(linear_into(s, L.qkv, P(m->xn), S, P(m->qkv), L.qkv.b ? EPI_BIAS : EPI_STORE, nullptr, 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
-            TLHIP_TRY(launch_rope_kv(s, P(m->qkv), qkv_w, S, NH, NKV, D, m->arch == 0 ? 0 : 2, m->rot,
-                                     m->rope_tab, decode ? 0 : pos0, d_pos, P(m->qrot), kc, vc));
+            if (!decode && gemm_skinny_ok(S, qkv_w, H, L.qkv.w->dtype)) {
+                // qkv (+ bias) + RoPE + cache write in the GEMM's epilogue
+                GemvArgs a;
+                a.x = P(m->xn);
+                a.wq = L.qkv.w->data;
+                a.wd = L.qkv.w->scales;
+                a.bias = L.qkv.b ? P(L.qkv.b) : nullptr;
+                a.y = P(m->qkv);
+                a.M = S;
+                a.N = qkv_w;
+                a.K = H;
+                a.ws = m->ws;
+                a.ws_bytes = m->ws_bytes;
+                a.tile_flags = m->ctx->d_tile_flags;
+                a.nq = H;
+                a.nk = kvd;
+                a.head_dim = D;
+                a.rot = m->rot;
+                a.layout = m->arch == 0 ? 0 : 1;
+                a.pos0 = pos0;
+                a.rope_tab = m->rope_tab;
+                a.q_out = P(m->qrot);
+                a.kc = kc;
+                a.vc = vc;
+                TLHIP_TRY(launch_gemm(s, L.qkv.w->dtype, a, EPI_QKV_ROPE));
+            } else {
+                TLHIP_TRY(linear_into(s, L.qkv, P(m->xn), S, P(m->qkv), L.qkv.b ? EPI_BIAS : EPI_STORE, nullptr, 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
+                TLHIP_TRY(launch_rope_kv(s, P(m->qkv), qkv_w, S, NH, NKV, D, m->arch == 0 ? 0 : 2, m->rot,
+                                         m->rope_tab, decode ? 0 : pos0, d_pos, P(m->qrot), kc, vc));
+            }
         }
         AttnArgs at;
         at.q = P(m->qrot);
