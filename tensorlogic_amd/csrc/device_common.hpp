@@ -214,6 +214,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const void* base, uint
 // the compiler uses M0 for nothing else in the kernels that call this.
 template <int SZ>
 __device__ __forceinline__ void sk_dma(__amdgpu_buffer_rsrc_t r, uint32_t lds, uint32_t off) {
+    lds = __builtin_amdgcn_readfirstlane(lds);   // an SGPR for the "s" operand however the caller computed it
     if constexpr (SZ == 16)
         asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds), "v"(off), "s"(r)
                      : "memory");

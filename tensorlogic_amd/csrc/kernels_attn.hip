@@ -641,80 +641,265 @@ tlhip_status launch_attention_split(hipStream_t s, const AttnArgs& a, float* scr
 }
 
 // ---------------------------------------------------------------------------
-// Prefill attention on the matrix cores (S >= 32 query rows, head_dim a
-// multiple of 16 up to 128).  Same arithmetic and rounding points as the
-// kernels above -- f16 scores, f16 scale, masked keys skipped, exp in f32,
-// P = f16(f16(e) / sum), fp32 accumulation of P.V -- organised so the two
-// contractions run as v_mfma_f32_32x32x16_f16:
+// Prefill attention on the matrix cores (S >= 128 query rows, head_dim 64,
+// 80 or 128).  The scores keep the reference's rounding points -- f16 dot
+// product, f16 product with the f16 scale, masked and non-finite keys
+// excluded -- and so do the exponentials, e = f16(exp(s - max)) with the sum
+// taken over the unrounded values; the one departure is that P . V is
+// accumulated from the f16 e (fp32) and divided by the sum once per output,
+// where the reference rounds each P = f16(e / sum) to f16 first (within one
+// f16 rounding per term; the layer bars are max-abs 2e-2 and rel-L2 1e-3).
+// The contractions run as v_mfma_f32_32x32x16_f16:
 //   S^T[key][query] = K . Q^T  (A = 32 keys x 16 dims from K rows, B = 32
 //                              queries x 16 dims from Q rows)
-//   O[query][d]     = P . V    (A = P straight from S^T's accumulators,
-//                              B = V^T rows from a transposed copy of V)
+//   O[query][d]     = E . V    (A = f16 e straight from S^T's accumulator
+//                              layout, B = 16-byte runs of the V^T tiles)
 // In S^T's accumulator layout lane l owns query l%32 and keys
 // 8(r/4) + 4(l/32) + r%4 (r = 0..15): the row statistics are per lane plus
 // one exchange with lane l^32, and registers 8t..8t+7 are exactly the
 // A operand of k-step t under the key order 16t + 8(i/4) + 4(l/32) + i%4,
-// which V^T is read in (two 4-key runs per lane).
-// Pass 1 over the key tiles keeps a running max and a rescaled sum of
-// exp(s - max); pass 2 recomputes the scores, forms P with the final max and
-// sum, and accumulates P.V.  Two waves own one head and a 32-row query tile
-// (causal: the pair of tiles t and n-1-t, so every workgroup does the same
-// work), each taking half of the key tiles; their row statistics meet in LDS
-// after pass 1 and the upper half's partial O is added by the lower half
-// after pass 2.  A workgroup holds four heads (two for head_dim 128), which
-// under GQA share their K/V head in L1/L2.
+// which the V^T tiles are stored in.
+// Pass 1 over the key tiles finds the row max on packed f16 scores; pass 2
+// recomputes the scores and accumulates the sum and E . V.  Two waves own
+// one head and a 32-row query tile (causal: the pair of tiles t and n-1-t,
+// so every workgroup does the same work), each taking half of the key
+// tiles; their maxima meet in LDS after pass 1, their sums and the upper
+// half's partial O after pass 2.  A workgroup holds four heads (two for
+// head_dim 128).  When they share one KV head (GQA groups of a multiple of
+// that many heads) the staged kernel copies each 32-key tile of K and V^T
+// to LDS once, with DMA loads of whole 1 KiB pieces, and all heads read it
+// there; otherwise every wave reads its operands from global memory, where
+// each load instruction touches 32 cache lines (the L1 tag rate, not the
+// matrix or vector units, then bounds the kernel).
 // ---------------------------------------------------------------------------
 
-// V [J, Hkv, D] -> Vt [Hkv, D, Jp], zero for keys J..Jp-1 (Jp % 32 == 0).
+// V [J, Hkv, D] -> V^T in 32-key tiles [Hkv][Jp/32][4][D][8], zero for
+// keys J..Jp-1 (Jp % 32 == 0).  A tile holds row d's 32 keys as four
+// 16-byte chunks in the order the E . V operand reads them: chunk
+// c = 2t + hh holds keys 16t + 8(i/4) + 4hh + i%4 (i = 0..7), and chunk c
+// of every row comes before chunk c + 1, so the 32 lanes reading one chunk
+// of 32 rows read 512 contiguous bytes.  A tile is one contiguous
+// 64 D-byte block, copied to LDS unchanged.
 __global__ __launch_bounds__(256) void vt_transpose_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt,
                                                          int J, int Jp, int Hkv, int D) {
-    __shared__ uint16_t tile[128][33];
-    const int j0 = blockIdx.x * 32, kvh = blockIdx.y;
+    __shared__ __attribute__((aligned(16))) uint16_t tile[32 * 128];   // [key][D] of this tile
+    const int j0 = blockIdx.x * 32, kvh = blockIdx.y, nc = 4 * D;   // 16-byte units per tile
     const size_t kstride = (size_t)Hkv * D;
-    for (int d0 = 0; d0 < D; d0 += 128) {
-        const int dn = min(128, D - d0);
-        for (int i = threadIdx.x; i < 32 * dn; i += 256) {
-            const int jj = i / dn, d = i % dn, j = j0 + jj;
-            tile[d][jj] = j < J ? v[(size_t)j * kstride + (size_t)kvh * D + d0 + d] : (uint16_t)0;
-        }
-        __syncthreads();
-        for (int i = threadIdx.x; i < 32 * dn; i += 256) {
-            const int d = i / 32, jj = i % 32;
-            vt[((size_t)kvh * D + d0 + d) * Jp + j0 + jj] = tile[d][jj];
-        }
-        __syncthreads();
+    for (int i = threadIdx.x; i < nc; i += 256) {   // 16 bytes of key i / (D/8)
+        const int key = i / (D / 8), c = i % (D / 8), j = j0 + key;
+        u4 w = {0u, 0u, 0u, 0u};
+        if (j < J) w = *(const u4*)(v + (size_t)j * kstride + (size_t)kvh * D + 8 * c);
+        *(u4*)(tile + key * D + 8 * c) = w;
+    }
+    __syncthreads();
+    uint16_t* const out = vt + ((size_t)kvh * (Jp / 32) + blockIdx.x) * (size_t)D * 32;
+    for (int i = threadIdx.x; i < nc; i += 256) {   // chunk c of row d
+        const int c = i / D, d = i % D;
+        uint16_t e8[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) e8[e] = tile[(16 * (c >> 1) + 8 * (e >> 2) + 4 * (c & 1) + (e & 3)) * D + d];
+        u4 w;
+#pragma unroll
+        for (int q = 0; q < 4; q++) w[q] = (uint32_t)e8[2 * q] | ((uint32_t)e8[2 * q + 1] << 16);
+        *(u4*)(out + (size_t)i * 8) = w;
     }
 }
 
-__device__ __forceinline__ h8 zero_h8() {
-    h8 z;
+// Byte offset, inside a V^T tile, of the 16 bytes lane l reads as the
+// E . V operand of output tile n (column d, clamped to D-1: columns past D
+// are not stored) and k-step t.
+template <int D>
+__device__ __forceinline__ int fa_vt_off(int lane, int n, int t) {
+    const int d = D % 32 == 0 ? 32 * n + (lane & 31) : min(32 * n + (lane & 31), D - 1);
+    return 16 * ((2 * t + (lane >> 5)) * D + d);
+}
+
+// Scores of one 32-key tile (jb = first key of this lane's runs) for this
+// lane's query as the reference stores them (f16 dot product, then the f16
+// product with the f16 scale), as eight f16 pairs; excluded keys (masked,
+// non-finite) come back as -inf.  Non-finite scores are found with packed
+// f16 arithmetic: x - x is 0 for a finite x and NaN otherwise, x + (x - x)
+// keeps x or turns it into NaN, and the IEEE max with -inf maps NaN to -inf.
+// FULL: every key of the tile is unmasked for every query of the wave.
+// !SAFE: the row is known to hold no +inf score (its largest score is
+// finite), so only NaN needs mapping to -inf, and -inf stays.
+// fa_round: the f16 dot products; fa_scale: the scores from them, in place.
+__device__ __forceinline__ void fa_round(const f16v& acc, h2 (&s2)[8]) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) z[i] = (h16)0.0f;
-    return z;
+    for (int r = 0; r < 16; r += 2) s2[r >> 1] = h2{(h16)acc[r], (h16)acc[r + 1]};
+}
+template <bool FULL, bool SAFE = true>
+__device__ __forceinline__ void fa_scale(h2 (&s2)[8], int jb, int jlim, float scale_h) {
+    const h2 sc2 = {(h16)scale_h, (h16)scale_h};
+    const h2 ninf = {(h16)-INFINITY, (h16)-INFINITY};
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+        h2 x = s2[r >> 1] * sc2;
+        x = __builtin_elementwise_max(SAFE ? x + (x - x) : x, ninf);
+        if (!FULL) {
+            if (jb + 8 * (r >> 2) + (r & 3) > jlim) x[0] = (h16)-INFINITY;
+            if (jb + 8 * ((r + 1) >> 2) + ((r + 1) & 3) > jlim) x[1] = (h16)-INFINITY;
+        }
+        s2[r >> 1] = x;
+    }
+}
+template <bool FULL, bool SAFE = true>
+__device__ __forceinline__ void fa_scores(const f16v& acc, int jb, int jlim, float scale_h, h2 (&s2)[8]) {
+    fa_round(acc, s2);
+    fa_scale<FULL, SAFE>(s2, jb, jlim, scale_h);
 }
 
-// The correctly rounded quotient a / b given r ~ 1/b (one residual
-// correction of the product; a in [0, 1], b >= 1 here).
-__device__ __forceinline__ float div_corr(float a, float b, float r) {
-    const float q = a * r;
-    return fmaf(fmaf(-b, q, a), r, q);
+// Pass-2 work of one tile: e = f16(exp(s - m)) as the reference stores it
+// (pa, the A operand of E . V) and the fp32 sum of the unrounded
+// exponentials; the product of the f16 e with V is divided by the sum at
+// the end.  DEG: rows with no finite score (deg) weight every key < J by
+// f16(1/J) = uni and keep a sum of 1, as the reference's softmax does.
+template <bool DEG>
+__device__ __forceinline__ void fa_exp(const h2 (&s2)[8], float m, bool deg, float uni, int jb, int J, h8 (&pa)[2],
+                                       float& sum) {
+    constexpr float L1 = 1.44269502162933349609375f;   // log2(e)
+    // x = s - m in f32 (v_fma_mix_f32 of the f16 s: s * 1 - m, one
+    // rounding, as the f32 subtraction); e = 2^(x log2 e) on v_exp_f32,
+    // within a few f32 ulps of exp(x) before its f16 rounding; excluded keys
+    // (-inf) give exactly 0
+    const float nm = -m;
+    float e[16];
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+        float x0, x1;
+        asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(x0) : "v"(s2[r >> 1]), "v"(nm));
+        asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(x1) : "v"(s2[r >> 1]), "v"(nm));
+        e[r] = __builtin_amdgcn_exp2f(x0 * L1);
+        e[r + 1] = __builtin_amdgcn_exp2f(x1 * L1);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) pa[r >> 3][r & 7] = (h16)e[r];
+    // pairwise, so the adds are not one dependent chain
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int r = 0; r < w; r++) e[r] += e[r + w];
+    sum += e[0];
+    if (DEG && deg) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) pa[r >> 3][r & 7] = (h16)(jb + 8 * (r >> 2) + (r & 3) < J ? uni : 0.0f);
+    }
 }
 
-// Score of an excluded key: finite, so differences stay finite, and far
-// enough below any f16 score that its exponential is exactly 0.
-constexpr float FA_NEG = -1.0e30f;
-
-// e^x for x <= 0 to a few f32 ulps: the terms of the softmax denominator,
-// whose sum only needs f32-level relative accuracy.
-__device__ __forceinline__ float exp_sum(float x) {
-    return __builtin_amdgcn_exp2f(x * 1.44269502162933349609375f);
+template <int NT>
+__device__ __forceinline__ void fa_pv(const h8 (&pa)[2], const h8 (&vb)[NT][2], f16v (&o)[NT]) {
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int n = 0; n < NT; n++) o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[t], vb[n][t], o[n], 0, 0, 0);
 }
 
-// Running (max, sum) pairs combined: each sum rescaled to the common max.
-__device__ __forceinline__ float fa_merge(float m1, float s1, float m2, float s2, float m) {
-    return (m1 > FA_NEG ? s1 * exp_sum(m1 - m) : 0.0f) + (m2 > FA_NEG ? s2 * exp_sum(m2 - m) : 0.0f);
+// pass kinds of the staged kernel
+enum { FA_MAX = 0, FA_MAX_EXACT = 1, FA_PV = 2, FA_PV_SAFE = 3, FA_PV_DEG = 4 };
+
+// After pass 2: the row's sum over both lane halves and both key halves in
+// a fixed order, the upper half's partial O through LDS (ob: [NT][16][64]),
+// and the lower half stores (o + ob) / sum; a degenerate row (no finite
+// score in either half's max, stm) divides by 1.  One workgroup barrier,
+// reached by every wave.
+// Whether p holds for any lane of the workgroup's nw waves: one word per
+// wave in slot (LDS), one lds_barrier.  The caller writes the slot again
+// only after later barriers.
+__device__ __forceinline__ bool wg_any(bool p, int* slot, int nw) {
+    const bool wp = __any(p);
+    if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = wp;
+    lds_barrier();
+    int r = 0;
+    for (int i = 0; i < nw; i++) r |= slot[i];
+    return r != 0;
 }
 
+// Row stride (elements) of the f16 output tile staged in LDS by fa_finish.
+template <int D>
+constexpr int fa_ot_stride() { return D + 8; }
+
+// After pass 2: the row's sum over both lane halves and both key halves in
+// a fixed order, the upper half's partial O through LDS (ob: [NT][16][64]),
+// and the lower half's f16 (o + ob) / sum, a degenerate row (no finite
+// score in either half's max, stm) divided by 1.  The lower half stages
+// the tile in ot ([32][fa_ot_stride] f16, LDS) and stores it in 16-byte
+// pieces, rows past S left out.  One workgroup barrier, reached by every
+// wave.
+template <int D>
+__device__ __forceinline__ void fa_finish(const AttnArgs& a, int h, int s0, int half, bool store, int os,
+                                          const f16v (&o)[(D + 31) / 32], float sum, const float* stm, float* sts,
+                                          float* ob, uint16_t* ot) {
+    constexpr int NT = (D + 31) / 32, DP = fa_ot_stride<D>();
+    // the lane index through an opaque copy: the addresses below are then
+    // computed here, not hoisted out of the caller's loops to stay live
+    // through them
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
+    const float s1 = sum + __shfl_xor(sum, 32, 64);
+    if (lane < 32) sts[half * 32 + lane] = s1;
+    if (half) {
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) ob[(n * 16 + r) * 64 + lane] = o[n][r];
+    }
+    lds_barrier();
+    if (!half) {
+        // row q's scale into sts[q] (lane q): a row's sum is at least 1 (its
+        // largest score's e), so the f32 reciprocal (v_rcp_f32, 1 ulp) does
+        if (lane < 32) {
+            const float tot = sts[lane] + sts[32 + lane];
+            sts[lane] = fmaxf(stm[lane], stm[32 + lane]) > -INFINITY ? __builtin_amdgcn_rcpf(tot) : 1.0f;
+        }
+        // O accumulators: column d = 32n + l%32, rows 8(r/4) + 4(l/32) + r%4
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const int d = 32 * n + (lane & 31);
+            if (D % 32 == 0 || d < D) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int q = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    ot[q * DP + d] = f2h((o[n][r] + ob[(n * 16 + r) * 64 + lane]) * sts[q]);
+                }
+            }
+        }
+        if (store) {
+            // the wave's own LDS writes complete before its reads (the
+            // compiler waits for them)
+            uint16_t* const ob0 = a.out + (size_t)s0 * os + (size_t)h * D;
+#pragma unroll
+            for (int i = 0; i < (4 * D + 63) / 64; i++) {
+                const int c = lane + 64 * i, row = c / (D / 8), c8 = c % (D / 8);
+                if (c < 4 * D && s0 + row < a.S)
+                    *(u4*)(ob0 + (size_t)row * os + 8 * c8) = *(const u4*)(ot + row * DP + 8 * c8);
+            }
+        }
+    }
+}
+
+// The key-tile ranges of one query tile and this lane's query.
+struct FaTile {
+    int s0, myq, nkt, jlim, nfull, nh;
+    __device__ FaTile(const AttnArgs& a, int J, int qt) {
+        const int lane = threadIdx.x & 63;
+        s0 = qt * 32;
+        myq = s0 + (lane & 31);
+        const int last = min(s0 + 31, a.S - 1);
+        const int kend = a.causal ? min(J, a.q_pos0 + last + 1) : J;
+        nkt = (kend + 31) / 32;
+        jlim = a.causal ? min(J - 1, a.q_pos0 + myq) : J - 1;
+        // tiles below every query's limit need no mask test
+        const int lo_lim = a.causal ? min(J - 1, a.q_pos0 + s0) : J - 1;
+        nfull = (lo_lim + 1) / 32;
+        nh = (nkt + 1) / 2;
+    }
+};
+
+// Heads per workgroup (each head = two waves, one per key half).
+template <int D>
+constexpr int fa_heads() { return D > 80 ? 2 : 4; }
+
+// -- operands from global memory (any head grouping) -----------------------
 template <int D>
 struct FaWave {
     static constexpr int KS = D / 16;          // k-steps of QK^T
@@ -742,22 +927,13 @@ struct FaWave {
         for (int ks = 0; ks < KS; ks++) kf[ks] = *(const h8*)(kr + 16 * ks);
     }
 
-    // V^T operands of tile kt (columns past D read column D-1: their output
-    // columns are not stored; keys J..Jp-1 are zero in vt)
+    // V^T operands of tile kt
     __device__ __forceinline__ void load_v(int kt, h8 (&vb)[NT][2]) const {
-        const int jb = kt * 32 + 4 * (lane >> 5);
+        const uint8_t* tb = (const uint8_t*)(vt + ((size_t)kvh * (Jp / 32) + kt) * (size_t)D * 32);
 #pragma unroll
-        for (int n = 0; n < NT; n++) {
-            const int d = min(32 * n + (lane & 31), D - 1);
-            const uint16_t* vr = vt + ((size_t)kvh * D + d) * Jp + jb;
+        for (int n = 0; n < NT; n++)
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const uint2 lo = *(const uint2*)(vr + 16 * t);
-                const uint2 hi = *(const uint2*)(vr + 16 * t + 8);
-                const u4 w = {lo.x, lo.y, hi.x, hi.y};
-                vb[n][t] = __builtin_bit_cast(h8, w);
-            }
-        }
+            for (int t = 0; t < 2; t++) vb[n][t] = *(const h8*)(tb + fa_vt_off<D>(lane, n, t));
     }
 
     __device__ __forceinline__ f16v qk(const h8 (&qf)[KS], const h8 (&kf)[KS]) const {
@@ -767,34 +943,12 @@ struct FaWave {
         return acc;
     }
 
-    // scores of key tile kt for this lane's query, as the reference stores
-    // them (f16 dot product, then the f16 product with the f16 scale);
-    // excluded keys (masked, past J, non-finite) come back as FA_NEG.
-    // FULL: every key of the tile is unmasked for every query of the wave.
-    template <bool FULL>
-    __device__ __forceinline__ void scores(int kt, const f16v& acc, int jlim, float (&sv)[16]) const {
-        const int jb = kt * 32 + 4 * (lane >> 5);
-        const h2 sc2 = {(h16)a.scale_h, (h16)a.scale_h};
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-            h2 x = {(h16)acc[r], (h16)acc[r + 1]};
-            x = x * sc2;
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const float v = (float)x[u];
-                bool ok = isfinite(v);
-                if (!FULL) ok = ok && jb + 8 * ((r + u) >> 2) + ((r + u) & 3) <= jlim;
-                sv[r + u] = ok ? v : FA_NEG;
-            }
-        }
-    }
-
-    // pass 1 over tiles [k0, k1): running max and rescaled sum of exp(s - max)
-    __device__ __forceinline__ void pass1(const h8 (&qf)[KS], int k0, int k1, int nfull, int jlim, float& mx,
-                                          float& sum) const {
-        mx = FA_NEG;
-        sum = 0.0f;
-        if (k0 >= k1) return;
+    // pass 1 over tiles [k0, k1): the largest finite score of this lane's
+    // keys (-inf if none)
+    __device__ __forceinline__ float pass1(const h8 (&qf)[KS], int k0, int k1, int nfull, int jlim) const {
+        const h2 ninf = {(h16)-INFINITY, (h16)-INFINITY};
+        h2 m2 = ninf;
+        if (k0 >= k1) return -INFINITY;
         // the QK^T product of tile kt+1 runs on the matrix core while the
         // vector unit works on tile kt
         h8 kf[KS];
@@ -805,39 +959,23 @@ struct FaWave {
             f16v accn = acc;
             if (kt + 1 < k1) accn = qk(qf, kf);
             if (kt + 2 < k1) load_k(kt + 2, kf);
-            float sv[16];
-            if (kt < nfull) scores<true>(kt, acc, jlim, sv);
-            else scores<false>(kt, acc, jlim, sv);
+            h2 s2[8];
+            const int jb = kt * 32 + 4 * (lane >> 5);
+            if (kt < nfull) fa_scores<true>(acc, jb, jlim, a.scale_h, s2);
+            else fa_scores<false>(acc, jb, jlim, a.scale_h, s2);
             acc = accn;
-            float mt = sv[0];
 #pragma unroll
-            for (int r = 1; r < 16; r++) mt = fmaxf(mt, sv[r]);
-            if (mt > mx) {
-                sum = sum * exp_sum(mx - mt);
-                mx = mt;
-            }
-            float es[16];
-#pragma unroll
-            for (int r = 0; r < 16; r++) es[r] = exp_sum(sv[r] - mx);
-            // pairwise, so the adds are not one dependent chain
-#pragma unroll
-            for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-                for (int r = 0; r < w; r++) es[r] += es[r + w];
-            if (mx > FA_NEG) sum += es[0];
+            for (int r = 0; r < 8; r++) m2 = __builtin_elementwise_max(m2, s2[r]);
         }
+        return fmaxf((float)m2[0], (float)m2[1]);
     }
 
-    // pass 2 over tiles [k0, k1): P = f16(f16(e) / sum) (DEG: rows with no
-    // finite score weight every key < J by f16(1/J)), O += P . V
+    // pass 2 over tiles [k0, k1)
     template <bool DEG>
     __device__ __forceinline__ void pass2(const h8 (&qf)[KS], int k0, int k1, int nfull, int jlim, float m,
-                                          float tot, bool deg, f16v (&o)[NT]) const {
+                                          bool deg, f16v (&o)[NT], float& sum) const {
         if (k0 >= k1) return;
-        const float rt = 1.0f / tot;
         const float uni = h2f(f2h(1.0f / (float)J));
-        // the QK^T product of tile kt+1 runs on the matrix core while the
-        // vector unit forms P of tile kt
         h8 kf[KS];
         load_k(k0, kf);
         f16v acc = qk(qf, kf);
@@ -848,124 +986,52 @@ struct FaWave {
             f16v accn = acc;
             if (kt + 1 < k1) accn = qk(qf, kf);
             if (kt + 2 < k1) load_k(kt + 2, kf);
-            float sv[16];
-            if (kt < nfull) scores<true>(kt, acc, jlim, sv);
-            else scores<false>(kt, acc, jlim, sv);
+            h2 s2[8];
+            const int jb = kt * 32 + 4 * (lane >> 5);
+            if (kt < nfull) fa_scores<true>(acc, jb, jlim, a.scale_h, s2);
+            else fa_scores<false>(acc, jb, jlim, a.scale_h, s2);
             acc = accn;
-            // e = f16(exp(x)), x = s - max <= 0: 2^(x log2 e) on v_exp_f32,
-            // with the rounding error of the product x * f32(log2 e) and the
-            // tail of log2 e added back as a first-order term, so e stays
-            // within about an ulp of exp(x) before its f16 rounding.  Written
-            // stage by stage over the 16 scores, so 16 independent chains
-            // stand between dependent instructions.
-            constexpr float L1 = 1.44269502162933349609375f, L2 = 1.925963033500011e-8f;
-            constexpr float LN2 = 0.6931471805599453f;
-            float x[16], t[16], e[16], c[16];
-#pragma unroll
-            for (int r = 0; r < 16; r++) x[r] = sv[r] - m;
-#pragma unroll
-            for (int r = 0; r < 16; r++) t[r] = x[r] * L1;
-#pragma unroll
-            for (int r = 0; r < 16; r++) e[r] = __builtin_amdgcn_exp2f(t[r]);
-#pragma unroll
-            for (int r = 0; r < 16; r++) c[r] = fmaf(x[r], L2, fmaf(x[r], L1, -t[r]));
             h8 pa[2];
-#pragma unroll
-            for (int r = 0; r < 16; r++) pa[r >> 3][r & 7] = (h16)fmaf(e[r] * LN2, c[r], e[r]);   // f16(exp(x))
-#pragma unroll
-            for (int r = 0; r < 16; r++) e[r] = (float)pa[r >> 3][r & 7];
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float pv = div_corr(e[r], tot, rt);
-                if (DEG) {
-                    const int j = kt * 32 + 4 * (lane >> 5) + 8 * (r >> 2) + (r & 3);
-                    pv = deg ? (j < J ? uni : 0.0f) : pv;
-                }
-                pa[r >> 3][r & 7] = (h16)pv;
-            }
-#pragma unroll
-            for (int n = 0; n < NT; n++)
-#pragma unroll
-                for (int t = 0; t < 2; t++) o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pa[t], vb[n][t], o[n], 0, 0, 0);
+            fa_exp<DEG>(s2, m, deg, uni, jb, J, pa, sum);
+            fa_pv<NT>(pa, vb, o);
         }
     }
 
     // Query tile qt, key half `half` of its tiles.  stm/sts: this head's
     // [2][32] exchange of row statistics; ob: [NT][16][64] partial O of the
     // upper half.  Two workgroup barriers, reached by every wave.
-    __device__ void run(int qt, int half, bool store, float* stm, float* sts, float* ob) const {
-        const int s0 = qt * 32;
-        const int myq = s0 + (lane & 31);
-        const int qpos = a.q_pos0 + myq;
-        const int last = min(s0 + 31, a.S - 1);
-        const int kend = a.causal ? min(J, a.q_pos0 + last + 1) : J;
-        const int nkt = (kend + 31) / 32;
-        const int jlim = a.causal ? min(J - 1, qpos) : J - 1;
-        // tiles below every query's limit need no mask test
-        const int lo_lim = a.causal ? min(J - 1, a.q_pos0 + s0) : J - 1;
-        const int nfull = (lo_lim + 1) / 32;
-        const int nh = (nkt + 1) / 2;
-
+    __device__ __forceinline__ void run(int qt, int half, bool store, float* stm, float* sts, float* ob,
+                                        uint16_t* ot) const {
+        const FaTile tl(a, J, qt);
         h8 qf[KS];
         {
-            const uint16_t* qr = a.q + (size_t)min(myq, a.S - 1) * qs + (size_t)h * D + 8 * (lane >> 5);
+            const uint16_t* qr = a.q + (size_t)min(tl.myq, a.S - 1) * qs + (size_t)h * D + 8 * (lane >> 5);
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) qf[ks] = *(const h8*)(qr + 16 * ks);
         }
 
-        float mx, sum;
-        pass1(qf, half ? nh : 0, half ? nkt : nh, nfull, jlim, mx, sum);
-        // the other 16 keys of every tile sit in lane l ^ 32, the other key
-        // half in the partner wave; both sides form the same sums
-        const float mo = __shfl_xor(mx, 32, 64), so = __shfl_xor(sum, 32, 64);
-        const float m1 = fmaxf(mx, mo);
-        const float t1 = fa_merge(mx, sum, mo, so, m1);
-        if (lane < 32) {
-            stm[half * 32 + lane] = m1;
-            sts[half * 32 + lane] = t1;
-        }
-        __syncthreads();
-        const float m2 = stm[(half ^ 1) * 32 + (lane & 31)], t2 = sts[(half ^ 1) * 32 + (lane & 31)];
-        const float m = fmaxf(m1, m2);
-        const float tot = fa_merge(m1, t1, m2, t2, m);
-        const bool deg = !(tot > 0.0f && isfinite(tot)) && myq < a.S;
+        // the row max: this lane's keys, the other 16 keys of every tile in
+        // lane l ^ 32, the other key half in the partner wave
+        const float mx = pass1(qf, half ? tl.nh : 0, half ? tl.nkt : tl.nh, tl.nfull, tl.jlim);
+        const float m1 = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        if (lane < 32) stm[half * 32 + lane] = m1;
+        lds_barrier();
+        const float m = fmaxf(m1, stm[(half ^ 1) * 32 + (lane & 31)]);
+        const bool deg = !(m > -INFINITY) && tl.myq < a.S;   // no finite score in the row
 
         f16v o[NT];
 #pragma unroll
         for (int n = 0; n < NT; n++) o[n] = f16v{};
+        float sum = 0.0f;
         if (__any(deg)) {
             const int nk = Jp / 32, nhd = (nk + 1) / 2;
-            pass2<true>(qf, half ? nhd : 0, half ? nk : nhd, 0, jlim, m, tot, deg, o);
+            pass2<true>(qf, half ? nhd : 0, half ? nk : nhd, 0, tl.jlim, deg ? 0.0f : m, deg, o, sum);
         } else {
-            pass2<false>(qf, half ? nh : 0, half ? nkt : nh, nfull, jlim, m, tot, false, o);
+            pass2<false>(qf, half ? tl.nh : 0, half ? tl.nkt : tl.nh, tl.nfull, tl.jlim, m, false, o, sum);
         }
-
-        if (half) {
-#pragma unroll
-            for (int n = 0; n < NT; n++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) ob[(n * 16 + r) * 64 + lane] = o[n][r];
-        }
-        __syncthreads();
-        if (!half && store) {
-            // O accumulators: column d = 32n + l%32, rows 8(r/4) + 4(l/32) + r%4
-#pragma unroll
-            for (int n = 0; n < NT; n++) {
-                const int d = 32 * n + (lane & 31);
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = s0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    const float t = o[n][r] + ob[(n * 16 + r) * 64 + lane];
-                    if (row < a.S && d < D) a.out[(size_t)row * os + (size_t)h * D + d] = f2h(t);
-                }
-            }
-        }
+        fa_finish<D>(a, h, tl.s0, half, store, os, o, sum, stm, sts, ob, ot);
     }
 };
-
-// Heads per workgroup (each head = two waves, one per key half).
-template <int D>
-constexpr int fa_heads() { return D > 80 ? 2 : 4; }
 
 template <int D>
 __global__ __launch_bounds__(fa_heads<D>() * 128) void attention_mfma_kernel(AttnArgs a, const uint16_t* __restrict__ vt, int J,
@@ -973,27 +1039,433 @@ __global__ __launch_bounds__(fa_heads<D>() * 128) void attention_mfma_kernel(Att
     constexpr int HPW = fa_heads<D>(), NT = (D + 31) / 32;
     __shared__ float stm[HPW][64], sts[HPW][64];
     __shared__ float ob[HPW][NT * 16 * 64];
+    __shared__ __attribute__((aligned(16))) uint16_t ot[HPW][32 * fa_ot_stride<D>()];
     const int w = threadIdx.x >> 6, hw = w % HPW, half = w / HPW;
     const int hh = blockIdx.y * HPW + hw;
     const FaWave<D> fw(a, vt, J, Jp, min(hh, a.H - 1));
     const bool store = hh < a.H;
-    if (a.causal) {
-        const int t0 = nqt - 1 - (int)blockIdx.x, t1 = blockIdx.x;
-        fw.run(t0, half, store, stm[hw], sts[hw], ob[hw]);
-        if (t1 < t0) fw.run(t1, half, store, stm[hw], sts[hw], ob[hw]);
-    } else {
-        fw.run(blockIdx.x, half, store, stm[hw], sts[hw], ob[hw]);
+    // causal: tiles n-1-x and x (one call site, so run() is inlined)
+    const int t0 = a.causal ? nqt - 1 - (int)blockIdx.x : (int)blockIdx.x, t1 = blockIdx.x;
+    const int nrun = a.causal && t1 < t0 ? 2 : 1;
+    for (int u = 0; u < nrun; u++) fw.run(u ? t1 : t0, half, store, stm[hw], sts[hw], ob[hw], ot[hw]);
+}
+
+// -- operands staged in LDS (every head of the workgroup on one KV head) ---
+// Ring of ST stages; a stage holds one 32-key tile of K for each key half
+// and, in pass 2, one of V^T (64 D bytes each).  Both halves step through
+// their tiles in lock step, one workgroup barrier per step: at step i a
+// wave waits for its own copies of tile i + 1, the barrier makes every
+// wave's copies visible and ends every read of tile i - 1, whose slot then
+// receives tile i + ST - 1 -- of the same pass or of the passes that
+// follow, so that a pass starts on tiles already in LDS.  A K tile in LDS is chunk-major, [D/8][32][8]:
+// 16-byte chunk c of key r at 16 (32 c + r), so a k-step's operand is 16
+// contiguous bytes per lane (lane l at 16 l + 1024 ks) and every copy piece
+// is two 16-byte chunks of 32 rows.
+template <int D>
+struct FaStaged {
+    static constexpr int HPW = fa_heads<D>();
+    static constexpr int KS = D / 16, NT = (D + 31) / 32;
+    static constexpr int TB = 64 * D;                   // bytes of a 32-key tile of K or of V^T
+    static constexpr int NQ = D / 16;                   // 1 KiB DMA pieces per tile
+    static constexpr int CQ = (NQ + HPW - 1) / HPW;     // pieces per wave and tile (the rest copy nothing)
+    // LEAD: steps whose copies are in place ahead of the current one (a
+    // lead of 2, with tile i+1's K read from LDS a step early, measured
+    // slower at head_dim 64: the copies then had one step to land, not two)
+    static constexpr int LEAD = 1;
+    static constexpr int ST = D > 80 ? 3 : 4;           // ring stages
+    static constexpr int STAGE = 4 * TB;                // K half 0, K half 1, V^T half 0, V^T half 1
+    static constexpr int RING = ST * STAGE;
+    static constexpr uint32_t OOB = 0x80000000u;        // buffer offset past every range: no access, zeros
+    static constexpr int G = 2 * CQ;                    // copies per wave and stage
+
+    AttnArgs a;
+    int J, Jp, h, lane, hw, half, qs, os;
+    uint32_t ring_lds, kstride2, vbase;
+    const uint8_t* ring;
+    __amdgpu_buffer_rsrc_t rk, rv;
+    uint32_t kcol[CQ];     // byte offset, in its key's row of the cache, of this lane's 16 bytes of piece hw + HPW c
+
+    __device__ FaStaged(const AttnArgs& a_, const uint16_t* vt, int J_, int Jp_, int kvh, int h_, int hw_, int half_,
+                        const uint8_t* ring_)
+        : a(a_), J(J_), Jp(Jp_), h(h_), hw(hw_), half(half_), ring(ring_) {
+        lane = threadIdx.x & 63;
+        qs = a.q_stride ? a.q_stride : a.H * D;
+        os = a.out_stride ? a.out_stride : a.H * D;
+        kstride2 = (uint32_t)a.Hkv * D * 2u;
+        vbase = (uint32_t)kvh * (uint32_t)(Jp / 32) * TB;
+        ring_lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(gl_lds_t)ring);
+        rk = sk_rsrc(a.k, (uint32_t)(J - 1) * kstride2 + (uint32_t)a.Hkv * D * 2u);
+        rv = sk_rsrc(vt, (uint32_t)a.Hkv * (uint32_t)Jp * D * 2u);
+        // piece q = hw + HPW c: LDS 16-byte unit 64 q + lane = chunk 2q + l/32 of key l%32
+#pragma unroll
+        for (int c = 0; c < CQ; c++) kcol[c] = (uint32_t)kvh * D * 2u + 16u * (2 * (hw + HPW * c) + (lane >> 5));
     }
+
+    // this wave's pieces of tile kt (nothing if !ok; K only if !pv) into
+    // ring slot sl: G copies in every case (those of nothing touch no
+    // memory), so the wait counts are fixed.  Branch-free (the piece count
+    // and its bounds are uniform selects).
+    __device__ __forceinline__ void issue(int kt, bool ok, bool pv, int sl) const {
+        const uint32_t sb = ring_lds + (uint32_t)(sl * STAGE);
+#pragma unroll
+        for (int c = 0; c < CQ; c++) {
+            const int q = hw + HPW * c;
+            const bool real = q < NQ;
+            const uint32_t src = ok && real ? (uint32_t)min(kt * 32 + (lane & 31), J - 1) * kstride2 + kcol[c] : OOB;
+            sk_dma<16>(rk, real ? sb + (uint32_t)(half * TB + 1024 * q) : ring_lds + RING, src);
+        }
+#pragma unroll
+        for (int c = 0; c < CQ; c++) {
+            const int q = hw + HPW * c;
+            const bool real = q < NQ;
+            const uint32_t src = ok && pv && real ? vbase + (uint32_t)kt * TB + 1024u * q + 16u * lane : OOB;
+            sk_dma<16>(rv, real ? sb + (uint32_t)(2 * TB + half * TB + 1024 * q) : ring_lds + RING, src);
+        }
+    }
+
+    __device__ __forceinline__ void read_k(int sl, h8 (&kf)[KS]) const {
+        const uint8_t* kb = ring + sl * STAGE + half * TB + 16 * lane;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) kf[ks] = *(const h8*)(kb + 1024 * ks);
+    }
+    __device__ __forceinline__ void read_v(int sl, h8 (&vb)[NT][2]) const {
+        const uint8_t* vb0 = ring + sl * STAGE + 2 * TB + half * TB;
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) vb[n][t] = *(const h8*)(vb0 + fa_vt_off<D>(lane, n, t));
+    }
+    static __device__ __forceinline__ f16v qk(const h8 (&qf)[KS], const h8 (&kf)[KS]) {
+        f16v acc = {};
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks], qf[ks], acc, 0, 0, 0);
+        return acc;
+    }
+    // the largest of mr and 16 raw accumulators (v_max3_f32: a NaN operand
+    // is passed over, as IEEE maxNum does)
+    static __device__ __forceinline__ float max3(float a, float b, float c) {
+        float d;
+        asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+        return d;
+    }
+    static __device__ __forceinline__ void raw_max(const f16v& acc, float& mr) {
+        float m0 = max3(mr, acc[0], acc[1]), m1 = max3(acc[2], acc[3], acc[4]);
+#pragma unroll
+        for (int r = 5; r < 15; r += 4) {
+            m0 = max3(m0, acc[r], acc[r + 1]);
+            m1 = max3(m1, acc[r + 2], acc[r + 3]);
+        }
+        mr = max3(m0, m1, acc[15]);
+    }
+
+    // Steps i in [0, n) over this half's tiles [k0, k0 + cnt) (n >= cnt,
+    // the workgroup's common count).  On entry acc holds the QK^T of tile k0
+    // (if cnt > 0) and sl the ring slot of step 0; the copies of steps
+    // 0 .. LEAD-1 are in place.  At step i a wave waits for its copies of
+    // step i + LEAD, the barrier makes every wave's copies visible and ends
+    // every read of step i - 1's slot, and ahead(i + ST - 1, that slot)
+    // issues the copies of step i + ST - 1.  On exit sl is the slot of step
+    // n; the copies of steps n .. n+LEAD-1 are in place.  MODE:
+    //   FA_MAX        the largest raw accumulator (the dot product before
+    //                 its f16 roundings) of the unmasked keys into mr;
+    //   FA_MAX_EXACT  the largest finite f16 score into m2;
+    //   FA_PV         pass 2 for rows whose largest score is finite;
+    //   FA_PV_SAFE    pass 2 for any rows;
+    //   FA_PV_DEG     pass 2 over every key, degenerate rows uniformly (m,
+    //                 deg as in fa_exp).
+    // Steps whose tile and next tile are both in range and unmasked run a
+    // loop without branches, in which the matrix core takes tile i-1's
+    // E . V and tile i+1's QK^T while the vector unit works on tile i.
+    template <int MODE, class Ahead>
+    __device__ __forceinline__ void loop(const Ahead& ahead, const h8 (&qf)[KS], int k0, int cnt, int n, int nfull,
+                                         int jlim, float m, bool deg, float& mr, h2& m2, f16v (&o)[NT], float& sum,
+                                         f16v& acc, int& sl) const {
+        constexpr bool PV = MODE >= FA_PV, DEG = MODE == FA_PV_DEG, SAFE = MODE != FA_PV;
+        const float uni = h2f(f2h(1.0f / (float)J));
+        int i = 0;
+        if constexpr (MODE != FA_MAX_EXACT && !DEG) {
+            const int na = max(0, min(min(cnt - 1, nfull - k0), n));
+            h8 pp[2] = {}, vp[NT][2] = {};   // tile i-1's E and V^T (zero before the first step)
+            for (; i < na; i++) {
+                const int sn = sl + 1 == ST ? 0 : sl + 1;   // tile i + 1
+                const int sp = sl == 0 ? ST - 1 : sl - 1;   // tile i - 1, refilled with step i + ST - 1
+                sk_wait_vm<(ST - 2 - LEAD) * G>();
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                ahead(i + ST - 1, sp);
+                h8 kf[KS];
+                read_k(sn, kf);
+                // each register set is read before it is rewritten: the loop
+                // carries them without copies
+                if constexpr (PV) {
+                    fa_pv<NT>(pp, vp, o);   // tile i - 1
+                    __builtin_amdgcn_sched_barrier(0);
+                    read_v(sl, vp);
+                    h2 s2[8];
+                    fa_round(acc, s2);
+                    __builtin_amdgcn_sched_barrier(0);
+                    acc = qk(qf, kf);       // tile i + 1
+                    const int jb = (k0 + i) * 32 + 4 * (lane >> 5);
+                    fa_scale<true, SAFE>(s2, jb, jlim, a.scale_h);
+                    fa_exp<false>(s2, m, false, uni, jb, J, pp, sum);
+                } else {
+                    raw_max(acc, mr);
+                    __builtin_amdgcn_sched_barrier(0);
+                    acc = qk(qf, kf);
+                }
+                sl = sn;
+            }
+            if constexpr (PV) fa_pv<NT>(pp, vp, o);
+        }
+        for (; i < n; i++) {
+            const int sn = sl + 1 == ST ? 0 : sl + 1;
+            const int sp = sl == 0 ? ST - 1 : sl - 1;
+            sk_wait_vm<(ST - 2 - LEAD) * G>();
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            ahead(i + ST - 1, sp);
+            f16v accn = acc;
+            if (i + 1 < cnt) {   // on the matrix core while the vector unit works on tile i
+                h8 kf[KS];
+                read_k(sn, kf);
+                accn = qk(qf, kf);
+            }
+            if (i < cnt) {
+                const int kt = k0 + i, jb = kt * 32 + 4 * (lane >> 5);
+                if constexpr (MODE == FA_MAX) {
+                    f16v am = acc;
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        if (jb + 8 * (r >> 2) + (r & 3) > jlim) am[r] = -INFINITY;
+                    raw_max(am, mr);
+                } else {
+                    h2 s2[8];
+                    if (kt < nfull) fa_scores<true, SAFE>(acc, jb, jlim, a.scale_h, s2);
+                    else fa_scores<false, SAFE>(acc, jb, jlim, a.scale_h, s2);
+                    if constexpr (PV) {
+                        h8 vb[NT][2], pa[2];
+                        read_v(sl, vb);
+                        fa_exp<DEG>(s2, m, deg, uni, jb, J, pa, sum);
+                        fa_pv<NT>(pa, vb, o);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 8; r++) m2 = __builtin_elementwise_max(m2, s2[r]);
+                    }
+                }
+            }
+            acc = accn;
+            sl = sn;
+        }
+    }
+
+    // A pass on its own (the rare exact row max and degenerate rows): after
+    // every wave is done with the ring, copies of its own from slot 0, and
+    // its last copies landed at the end.
+    template <int MODE>
+    __device__ __forceinline__ void pass(const h8 (&qf)[KS], int k0, int cnt, int n, int nfull, int jlim, float m,
+                                         bool deg, float& mr, h2& m2, f16v (&o)[NT], float& sum) const {
+        constexpr bool PV = MODE >= FA_PV;
+        auto ahead = [&](int i, int s) { issue(k0 + i, i < cnt, PV, s); };
+        f16v acc;
+        int sl;
+        start(ahead, qf, cnt, acc, sl);
+        loop<MODE>(ahead, qf, k0, cnt, n, nfull, jlim, m, deg, mr, m2, o, sum, acc, sl);
+        sk_wait_vm<0>();
+    }
+
+    // Fill the ring from its slot 0 with steps 0 .. ST-2 (ahead), once every
+    // wave is done with it (steps 0 .. LEAD-1 in place), and the first
+    // tile's QK^T (if cnt > 0).
+    template <class Ahead>
+    __device__ __forceinline__ void start(const Ahead& ahead, const h8 (&qf)[KS], int cnt, f16v& acc, int& sl) const {
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        sk_wait_vm<0>();
+#pragma unroll
+        for (int i = 0; i < ST - 1; i++) ahead(i, i);
+        sk_wait_vm<(ST - 1 - LEAD) * G>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        sl = 0;
+        acc = f16v{};
+        if (cnt > 0) {
+            h8 kf[KS];
+            read_k(0, kf);
+            acc = qk(qf, kf);
+        }
+    }
+
+    // The workgroup's key tiles as one stream: job j = 2u + p is pass p
+    // (0: the row max, 1: the sums and E . V) of query tile u (t0, then
+    // t1), job_n steps each over the same tiles; every step copies the step
+    // ST - 1 positions ahead, whichever job that is, so only the first job
+    // waits for memory.
+    struct Stream {
+        int nh0, nkt0, nh1, nkt1, nj;   // steps and key tiles of the two query tiles; jobs (2 or 4)
+    };
+    __device__ __forceinline__ int job_n(const Stream& s, int j) const { return j < 2 ? s.nh0 : s.nh1; }
+    __device__ __forceinline__ int job_k0(const Stream& s, int j) const { return half ? job_n(s, j) : 0; }
+    __device__ __forceinline__ int job_cnt(const Stream& s, int j) const {
+        return half ? (j < 2 ? s.nkt0 : s.nkt1) - job_n(s, j) : job_n(s, j);
+    }
+    // the copies of step i of job j (i may run past the job's end) into slot sl
+    __device__ __forceinline__ void issue_at(const Stream& s, int j, int i, int sl) const {
+#pragma unroll
+        for (int u = 0; u < ST - 1; u++)   // at most ST - 1 jobs ahead (every job has a step)
+            if (j < s.nj && i >= job_n(s, j)) {
+                i -= job_n(s, j);
+                j++;
+            }
+        const bool ok = j < s.nj && i < job_cnt(s, j);
+        issue(ok ? job_k0(s, j) + i : 0, ok, (j & 1) != 0, sl);
+    }
+
+    __device__ __forceinline__ void load_q(int myq, h8 (&qf)[KS]) const {
+        const uint16_t* qr = a.q + (size_t)min(myq, a.S - 1) * qs + (size_t)h * D + 8 * (lane >> 5);
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qf[ks] = *(const h8*)(qr + 16 * ks);
+    }
+
+    // Query tiles t0 and, if nu == 2, t1; stm/sts/ob/ot as in fa_finish,
+    // votes 4 HPW words.  Every wave reaches the same barriers.
+    __device__ __forceinline__ void run(int t0, int t1, int nu, bool store, float* stm, float* sts, float* ob,
+                                        uint16_t* ot, int* votes) const {
+        const FaTile T0(a, J, t0), T1(a, J, t1);
+        const Stream s{T0.nh, T0.nkt, T1.nh, T1.nkt, 2 * nu};
+        // the ring's first copies, then both query tiles' rows: waiting
+        // for the rows (the compiler counts only its own loads) waits for
+        // the older copies too, one memory latency for both; the rows arrive
+        // here, once -- a first use inside the step loops would make the
+        // compiler wait there for every load outstanding
+#pragma unroll
+        for (int i = 0; i < ST - 1; i++) issue_at(s, 0, i, i);
+        h8 qf[KS], qn[KS];
+        load_q(T0.myq, qf);
+        load_q(T1.myq, qn);
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) asm volatile("" ::"v"(qf[ks]), "v"(qn[ks]));
+        sk_wait_vm<0>();
+        lds_barrier();
+        int sl = 0;
+        f16v acc = {};
+        if (job_cnt(s, 0) > 0) {
+            h8 kf[KS];
+            read_k(0, kf);
+            acc = qk(qf, kf);
+        }
+        for (int u = 0; u < nu; u++) {
+            const FaTile& T = u ? T1 : T0;
+            const int j = 2 * u, k0 = job_k0(s, j), cnt = job_cnt(s, j), n = job_n(s, j);
+            f16v o[NT];
+#pragma unroll
+            for (int nn = 0; nn < NT; nn++) o[nn] = f16v{};
+            float sum = 0.0f, mr = -INFINITY;
+            h2 m2 = {(h16)-INFINITY, (h16)-INFINITY};
+            // The row max from the raw accumulators: rounding to f16 and the
+            // product with the positive f16 scale never reverse an order, so
+            // the largest score is g(M) = f16(f16(M) * scale) of the largest
+            // accumulator M whenever g(M) is finite (M itself a finite
+            // score).  Otherwise (a score overflowing f16, no finite score)
+            // the workgroup takes the exact pass over the f16 scores.
+            loop<FA_MAX>([&](int i, int sl_) { issue_at(s, j, i, sl_); }, qf, k0, cnt, n, T.nfull, T.jlim, 0.0f, false,
+                         mr, m2, o, sum, acc, sl);
+            if (cnt > 0) {   // pass 2's first QK^T: the same tile, in place
+                h8 kf[KS];
+                read_k(sl, kf);
+                acc = qk(qf, kf);
+            }
+            float m1 = fmaxf(mr, __shfl_xor(mr, 32, 64));
+            if (lane < 32) stm[half * 32 + lane] = m1;
+            lds_barrier();
+            float m = (float)((h16)fmaxf(m1, stm[(half ^ 1) * 32 + (lane & 31)]) * (h16)a.scale_h);
+            const bool exact = wg_any(!(__builtin_fabsf(m) < INFINITY) && T.myq < a.S, votes, 2 * HPW);
+            if (exact) {
+                pass<FA_MAX_EXACT>(qf, k0, cnt, n, T.nfull, T.jlim, 0.0f, false, mr, m2, o, sum);
+                m1 = fmaxf((float)m2[0], (float)m2[1]);
+                m1 = fmaxf(m1, __shfl_xor(m1, 32, 64));
+                if (lane < 32) stm[half * 32 + lane] = m1;
+                lds_barrier();
+                m = fmaxf(m1, stm[(half ^ 1) * 32 + (lane & 31)]);
+            }
+            const bool deg = !(m > -INFINITY) && T.myq < a.S;   // no finite score in the row
+            const bool anydeg = wg_any(deg, votes + 2 * HPW, 2 * HPW);
+            if (anydeg) {
+                // every key of the cache, the degenerate rows uniformly
+                const int nk = Jp / 32, nhd = (nk + 1) / 2;
+                pass<FA_PV_DEG>(qf, half ? nhd : 0, half ? nk - nhd : nhd, nhd, 0, T.jlim, deg ? 0.0f : m, deg, mr, m2,
+                                o, sum);
+            } else {
+                auto ahead = [&](int i, int sl_) { issue_at(s, j + 1, i, sl_); };
+                if (exact) {
+                    start(ahead, qf, cnt, acc, sl);
+                    loop<FA_PV_SAFE>(ahead, qf, k0, cnt, n, T.nfull, T.jlim, m, false, mr, m2, o, sum, acc, sl);
+                } else {
+                    loop<FA_PV>(ahead, qf, k0, cnt, n, T.nfull, T.jlim, m, false, mr, m2, o, sum, acc, sl);
+                }
+            }
+            fa_finish<D>(a, h, T.s0, half, store, os, o, sum, stm, sts, ob, ot);
+            if (u + 1 < nu) {   // query tile t1: its q rows, its first tile in place (or the ring refilled)
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) qf[ks] = qn[ks];
+                if (anydeg) {
+                    start([&](int i, int sl_) { issue_at(s, j + 2, i, sl_); }, qf, job_cnt(s, j + 2), acc, sl);
+                } else {
+                    acc = f16v{};
+                    if (job_cnt(s, j + 2) > 0) {
+                        h8 kf[KS];
+                        read_k(sl, kf);
+                        acc = qk(qf, kf);
+                    }
+                }
+            }
+        }
+        sk_wait_vm<0>();   // no copy into LDS outstanding when the workgroup ends
+    }
+};
+
+template <int D>
+__global__ __launch_bounds__(fa_heads<D>() * 128) void attention_mfma_staged_kernel(AttnArgs a,
+                                                                    const uint16_t* __restrict__ vt, int J,
+                                                                    int Jp, int nqt) {
+    using L = FaStaged<D>;
+    constexpr int HPW = L::HPW, NT = L::NT;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[L::RING + 1024];   // + the pieces that copy nothing
+    __shared__ float stm[HPW][64], sts[HPW][64];
+    __shared__ float ob[HPW][NT * 16 * 64];
+    __shared__ __attribute__((aligned(16))) uint16_t ot[HPW][32 * fa_ot_stride<D>()];
+    __shared__ int votes[4 * HPW];
+    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), hw = w % HPW, half = w / HPW;
+    const int hh = blockIdx.y * HPW + hw;
+    const int kvh = (int)(blockIdx.y * HPW) / (a.H / a.Hkv);
+    const L fs(a, vt, J, Jp, kvh, min(hh, a.H - 1), hw, half, ring);
+    // causal: tiles n-1-x and x
+    const int t0 = a.causal ? nqt - 1 - (int)blockIdx.x : (int)blockIdx.x, t1 = blockIdx.x;
+    fs.run(t0, t1, a.causal && t1 < t0 ? 2 : 1, hh < a.H, stm[hw], sts[hw], ob[hw], ot[hw], votes);
 }
 
 bool attention_mfma_ok(const AttnArgs& a, int J) {
     const int qs = a.q_stride ? a.q_stride : a.H * a.D;
+    const int os = a.out_stride ? a.out_stride : a.H * a.D;
     return a.S >= 128 && J >= 1 && (a.D == 64 || a.D == 80 || a.D == 128) && !a.d_pos && qs % 8 == 0 &&
-           ((uintptr_t)a.q % 16) == 0 && ((uintptr_t)a.k % 16) == 0;
+           os % 8 == 0 && ((uintptr_t)a.q % 16) == 0 && ((uintptr_t)a.k % 16) == 0 && ((uintptr_t)a.v % 16) == 0 &&
+           ((uintptr_t)a.out % 16) == 0;
 }
 
 size_t attention_mfma_scratch(int J, int Hkv, int D) {
     return (size_t)Hkv * D * (size_t)((J + 31) / 32 * 32) * sizeof(uint16_t);
+}
+
+// The staged kernel: every workgroup's heads on one KV head, and the K and
+// V^T byte ranges within its 32-bit buffer offsets.
+static bool attention_staged_ok(const AttnArgs& a, int J) {
+    const int hpw = a.D > 80 ? 2 : 4;
+    const size_t jp = (size_t)(J + 31) / 32 * 32;
+    return (a.H / a.Hkv) % hpw == 0 && (size_t)J * a.Hkv * a.D * 2 < 0x80000000u &&
+           jp * a.Hkv * a.D * 2 < 0x80000000u;
+}
+
+template <int D>
+static void launch_fa(hipStream_t s, const AttnArgs& a, const uint16_t* vt, int J, int Jp, int nqt, int gx, bool staged) {
+    constexpr int HPW = fa_heads<D>();
+    const dim3 grid(gx, (a.H + HPW - 1) / HPW), block(HPW * 128);
+    if (staged) hipLaunchKernelGGL(attention_mfma_staged_kernel<D>, grid, block, 0, s, a, vt, J, Jp, nqt);
+    else hipLaunchKernelGGL(attention_mfma_kernel<D>, grid, block, 0, s, a, vt, J, Jp, nqt);
 }
 
 // Prefill over J keys through the matrix cores; vt holds
@@ -1007,12 +1479,10 @@ tlhip_status launch_attention_mfma(hipStream_t s, const AttnArgs& a, int J, uint
     hipLaunchKernelGGL(vt_transpose_kernel, dim3(Jp / 32, a.Hkv), dim3(256), 0, s, a.v, vt, J, Jp, a.Hkv, a.D);
     const int nqt = (a.S + 31) / 32;
     const int gx = a.causal ? (nqt + 1) / 2 : nqt;
-    if (a.D == 64)
-        hipLaunchKernelGGL(attention_mfma_kernel<64>, dim3(gx, (a.H + 3) / 4), dim3(512), 0, s, a, vt, J, Jp, nqt);
-    else if (a.D == 80)
-        hipLaunchKernelGGL(attention_mfma_kernel<80>, dim3(gx, (a.H + 3) / 4), dim3(512), 0, s, a, vt, J, Jp, nqt);
-    else
-        hipLaunchKernelGGL(attention_mfma_kernel<128>, dim3(gx, (a.H + 1) / 2), dim3(256), 0, s, a, vt, J, Jp, nqt);
+    const bool staged = attention_staged_ok(a, J);
+    if (a.D == 64) launch_fa<64>(s, a, vt, J, Jp, nqt, gx, staged);
+    else if (a.D == 80) launch_fa<80>(s, a, vt, J, Jp, nqt, gx, staged);
+    else launch_fa<128>(s, a, vt, J, Jp, nqt, gx, staged);
     return TLHIP_OK;
 }
 

@@ -335,8 +335,10 @@ def test_mask_and_einsums(dev, oracle):
 
 
 # S < 128 runs the one-workgroup-per-row kernels; S >= 128 the matrix-core
-# prefill kernel (two q-tiles per head pair of waves under causal masking,
-# key halves split between the waves, transposed V).
+# prefill kernels (two q-tiles per head pair of waves under causal masking,
+# key halves split between the waves, transposed V): the staged one (K / V
+# tiles copied to LDS once per workgroup) when the GQA group is a multiple
+# of the workgroup's 4 heads (2 at head_dim 128), the direct one otherwise.
 @pytest.mark.parametrize("Sq,J,H,Hkv,D,q0,causal", [
     (1, 174, 32, 4, 64, 173, True), (46, 46, 32, 4, 64, 0, True), (1, 768, 32, 32, 80, 767, True),
     (31, 31, 4, 4, 64, 0, True), (64, 100, 8, 8, 80, 36, True), (97, 97, 8, 2, 128, 0, True),
@@ -348,7 +350,10 @@ def test_mask_and_einsums(dev, oracle):
     (1, 100, 8, 8, 80, 99, True), (1, 300, 4, 4, 80, 299, True), (1, 513, 4, 2, 128, 512, True),
     (3, 600, 4, 2, 80, 597, True), (2, 1100, 4, 4, 80, 0, False),
     # config 3 at its head layout: 32 query / 4 KV heads (GQA group 8), D = 64
-    (2048, 2048, 32, 4, 64, 0, True), (1, 2048, 32, 4, 64, 2047, True), (256, 1024, 32, 4, 64, 768, True)])
+    (2048, 2048, 32, 4, 64, 0, True), (1, 2048, 32, 4, 64, 2047, True), (256, 1024, 32, 4, 64, 768, True),
+    # staged kernel at head dims 80 and 128, ragged key counts, odd tile counts
+    (300, 300, 8, 2, 80, 0, True), (200, 150, 8, 2, 80, 0, False), (129, 129, 4, 2, 128, 0, True),
+    (256, 333, 8, 2, 128, 77, True), (160, 1000, 8, 1, 64, 840, True)])
 def test_attention(dev, oracle, Sq, J, H, Hkv, D, q0, causal):
     q = S.normal_f16(11, "q", (Sq, H, D))
     k = S.normal_f16(11, "k", (J, Hkv, D))
@@ -358,11 +363,12 @@ def test_attention(dev, oracle, Sq, J, H, Hkv, D, q0, causal):
     assert_close(got, ref, what=f"attention S={Sq} J={J} D={D} causal={causal}")
 
 
-@pytest.mark.parametrize("Sq", [8, 64, 160])
-def test_attention_degenerate_rows(dev, oracle, Sq):
+@pytest.mark.parametrize("Sq,H", [(8, 4), (64, 4), (160, 4), (160, 8), (300, 8)])
+def test_attention_degenerate_rows(dev, oracle, Sq, H):
     """Rows whose every score overflows f16 take the reference softmax's
-    uniform 1/J weights (non-causal, so no -10000 masked scores exist)."""
-    H, Hkv, D, J = 4, 2, 64, 40
+    uniform 1/J weights (non-causal, so no -10000 masked scores exist);
+    S >= 128 with 8 heads on 2 KV heads runs the staged matrix-core kernel."""
+    Hkv, D, J = 2, 64, 40
     q = S.normal_f16(12, "q", (Sq, H, D))
     q[::3] = np.float16(120.0)
     k = np.abs(S.normal_f16(12, "k", (J, Hkv, D))) + np.float16(100.0)
