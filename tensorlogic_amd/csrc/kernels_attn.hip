@@ -1163,9 +1163,10 @@ struct FaStaged {
     // (if cnt > 0) and sl the ring slot of step 0; the copies of steps
     // 0 .. LEAD-1 are in place.  At step i a wave waits for its copies of
     // step i + LEAD, the barrier makes every wave's copies visible and ends
-    // every read of step i - 1's slot, and ahead(i + ST - 1, that slot)
-    // issues the copies of step i + ST - 1.  On exit sl is the slot of step
-    // n; the copies of steps n .. n+LEAD-1 are in place.  MODE:
+    // every read of step i - 1's slot, and ahead(that slot) issues the
+    // copies of step i + ST - 1 (ahead keeps its own position).  On exit sl
+    // is the slot of step n; the copies of steps n .. n+LEAD-1 are in
+    // place.  MODE:
     //   FA_MAX        the largest raw accumulator (the dot product before
     //                 its f16 roundings) of the unmasked keys into mr;
     //   FA_MAX_EXACT  the largest finite f16 score into m2;
@@ -1191,7 +1192,7 @@ struct FaStaged {
                 const int sp = sl == 0 ? ST - 1 : sl - 1;   // tile i - 1, refilled with step i + ST - 1
                 sk_wait_vm<(ST - 2 - LEAD) * G>();
                 asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-                ahead(i + ST - 1, sp);
+                ahead(sp);
                 h8 kf[KS];
                 read_k(sn, kf);
                 // each register set is read before it is rewritten: the loop
@@ -1221,7 +1222,7 @@ struct FaStaged {
             const int sp = sl == 0 ? ST - 1 : sl - 1;
             sk_wait_vm<(ST - 2 - LEAD) * G>();
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            ahead(i + ST - 1, sp);
+            ahead(sp);
             f16v accn = acc;
             if (i + 1 < cnt) {   // on the matrix core while the vector unit works on tile i
                 h8 kf[KS];
@@ -1263,7 +1264,11 @@ struct FaStaged {
     __device__ __forceinline__ void pass(const h8 (&qf)[KS], int k0, int cnt, int n, int nfull, int jlim, float m,
                                          bool deg, float& mr, h2& m2, f16v (&o)[NT], float& sum) const {
         constexpr bool PV = MODE >= FA_PV;
-        auto ahead = [&](int i, int s) { issue(k0 + i, i < cnt, PV, s); };
+        int pos = 0;
+        auto ahead = [&](int s) {
+            issue(k0 + pos, pos < cnt, PV, s);
+            pos++;
+        };
         f16v acc;
         int sl;
         start(ahead, qf, cnt, acc, sl);
@@ -1279,7 +1284,7 @@ struct FaStaged {
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         sk_wait_vm<0>();
 #pragma unroll
-        for (int i = 0; i < ST - 1; i++) ahead(i, i);
+        for (int i = 0; i < ST - 1; i++) ahead(i);
         sk_wait_vm<(ST - 1 - LEAD) * G>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         sl = 0;
@@ -1304,16 +1309,19 @@ struct FaStaged {
     __device__ __forceinline__ int job_cnt(const Stream& s, int j) const {
         return half ? (j < 2 ? s.nkt0 : s.nkt1) - job_n(s, j) : job_n(s, j);
     }
-    // the copies of step i of job j (i may run past the job's end) into slot sl
-    __device__ __forceinline__ void issue_at(const Stream& s, int j, int i, int sl) const {
-#pragma unroll
-        for (int u = 0; u < ST - 1; u++)   // at most ST - 1 jobs ahead (every job has a step)
-            if (j < s.nj && i >= job_n(s, j)) {
-                i -= job_n(s, j);
-                j++;
-            }
-        const bool ok = j < s.nj && i < job_cnt(s, j);
-        issue(ok ? job_k0(s, j) + i : 0, ok, (j & 1) != 0, sl);
+    // A position of the stream: step i of job j (past the last job: copies
+    // of nothing).
+    struct Cursor {
+        int j, i;
+    };
+    // the copies at c into slot sl; c one step on (every job has a step)
+    __device__ __forceinline__ void issue_next(const Stream& s, Cursor& c, int sl) const {
+        const bool ok = c.j < s.nj && c.i < job_cnt(s, c.j);
+        issue(ok ? job_k0(s, c.j) + c.i : 0, ok, (c.j & 1) != 0, sl);
+        if (++c.i >= job_n(s, c.j)) {
+            c.i = 0;
+            c.j++;
+        }
     }
 
     __device__ __forceinline__ void load_q(int myq, h8 (&qf)[KS]) const {
@@ -1333,8 +1341,10 @@ struct FaStaged {
         // the older copies too, one memory latency for both; the rows arrive
         // here, once -- a first use inside the step loops would make the
         // compiler wait there for every load outstanding
+        Cursor cur{0, 0};
+        auto ahead = [&](int sl_) { issue_next(s, cur, sl_); };
 #pragma unroll
-        for (int i = 0; i < ST - 1; i++) issue_at(s, 0, i, i);
+        for (int i = 0; i < ST - 1; i++) ahead(i);
         h8 qf[KS], qn[KS];
         load_q(T0.myq, qf);
         load_q(T1.myq, qn);
@@ -1363,8 +1373,7 @@ struct FaStaged {
             // accumulator M whenever g(M) is finite (M itself a finite
             // score).  Otherwise (a score overflowing f16, no finite score)
             // the workgroup takes the exact pass over the f16 scores.
-            loop<FA_MAX>([&](int i, int sl_) { issue_at(s, j, i, sl_); }, qf, k0, cnt, n, T.nfull, T.jlim, 0.0f, false,
-                         mr, m2, o, sum, acc, sl);
+            loop<FA_MAX>(ahead, qf, k0, cnt, n, T.nfull, T.jlim, 0.0f, false, mr, m2, o, sum, acc, sl);
             if (cnt > 0) {   // pass 2's first QK^T: the same tile, in place
                 h8 kf[KS];
                 read_k(sl, kf);
@@ -1391,8 +1400,8 @@ struct FaStaged {
                 pass<FA_PV_DEG>(qf, half ? nhd : 0, half ? nk - nhd : nhd, nhd, 0, T.jlim, deg ? 0.0f : m, deg, mr, m2,
                                 o, sum);
             } else {
-                auto ahead = [&](int i, int sl_) { issue_at(s, j + 1, i, sl_); };
-                if (exact) {
+                if (exact) {   // the ring refilled from pass 2's first step
+                    cur = Cursor{j + 1, 0};
                     start(ahead, qf, cnt, acc, sl);
                     loop<FA_PV_SAFE>(ahead, qf, k0, cnt, n, T.nfull, T.jlim, m, false, mr, m2, o, sum, acc, sl);
                 } else {
@@ -1404,7 +1413,8 @@ struct FaStaged {
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++) qf[ks] = qn[ks];
                 if (anydeg) {
-                    start([&](int i, int sl_) { issue_at(s, j + 2, i, sl_); }, qf, job_cnt(s, j + 2), acc, sl);
+                    cur = Cursor{j + 2, 0};
+                    start(ahead, qf, job_cnt(s, j + 2), acc, sl);
                 } else {
                     acc = f16v{};
                     if (job_cnt(s, j + 2) > 0) {
