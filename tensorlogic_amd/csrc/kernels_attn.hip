@@ -115,10 +115,14 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a, int J_fixed)
 // 8c..8c+7 over keys g, g+32, ...; the 32 partial rows are summed in g order.
 constexpr int A64_UNR = 8;
 
-template <int NT>
+// JMAX: keys the score row holds; below ATT_MAX_J only for a key count
+// known at launch (no d_pos) of at most JMAX -- the smaller row lets more
+// workgroups share a CU.  UNR: K / V rows per key group and pass (fewer
+// registers, so more workgroups per CU, for short rows).
+template <int NT, int JMAX = ATT_MAX_J, int UNR = A64_UNR>
 __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed) {
     constexpr int NWV = NT / 64, NG = NT / 8;
-    __shared__ float sc[ATT_MAX_J];
+    __shared__ float sc[JMAX];
     __shared__ float red[2][NWV];
     __shared__ float part[NWV][64];
     attn_kernarg_fence(a, J_fixed);
@@ -139,19 +143,19 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed
     // makes the compiler wait for it at the branch join, which serialised
     // the pass into several memory round trips.
     const u4 qv = *(const u4*)(a.q + (size_t)s * qs + (size_t)h * 64 + 8 * c);
-    const int kv_lim = a.kv_rows > 0 ? (a.d_pos ? a.kv_rows : min(a.kv_rows, J_fixed)) : min(J_fixed, ATT_MAX_J);
-    u4 k0[A64_UNR], vv[A64_UNR];
+    const int kv_lim = a.kv_rows > 0 ? (a.d_pos ? a.kv_rows : min(a.kv_rows, J_fixed)) : min(J_fixed, JMAX);
+    u4 k0[UNR], vv[UNR];
     if (kv_lim > 0) {   // (uniform; 0 only when neither a key count nor the rows allocated is known)
 #pragma unroll
-        for (int u = 0; u < A64_UNR; u++) k0[u] = *(const u4*)(kbase + (size_t)min(g + NG * u, kv_lim - 1) * kstride);
+        for (int u = 0; u < UNR; u++) k0[u] = *(const u4*)(kbase + (size_t)min(g + NG * u, kv_lim - 1) * kstride);
 #pragma unroll
-        for (int u = 0; u < A64_UNR; u++) vv[u] = *(const u4*)(vbase + (size_t)min(g + NG * u, kv_lim - 1) * kstride);
+        for (int u = 0; u < UNR; u++) vv[u] = *(const u4*)(vbase + (size_t)min(g + NG * u, kv_lim - 1) * kstride);
     } else {
 #pragma unroll
-        for (int u = 0; u < A64_UNR; u++) k0[u] = vv[u] = u4{0u, 0u, 0u, 0u};
+        for (int u = 0; u < UNR; u++) k0[u] = vv[u] = u4{0u, 0u, 0u, 0u};
     }
     const int qpos = (a.d_pos ? *a.d_pos : a.q_pos0) + s;
-    const int J = min(a.d_pos ? qpos + 1 : J_fixed, ATT_MAX_J);
+    const int J = min(a.d_pos ? qpos + 1 : J_fixed, JMAX);
     const int Jv = a.causal ? min(J, qpos + 1) : J;
 
     float qf[8];
@@ -162,25 +166,25 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed
         qf[2 * t + 1] = (float)p2[1];
     }
 
-    // One pass covers NG * A64_UNR keys; the first pass uses the rows loaded
+    // One pass covers NG * UNR keys; the first pass uses the rows loaded
     // above.  When the unmasked row fits in that pass, the V rows loaded
     // with it are used directly (one round trip to memory in all).
-    const bool one_pass = Jv <= NG * A64_UNR;
+    const bool one_pass = Jv <= NG * UNR;
     float mx = -INFINITY;
-    for (int j0 = g; j0 < Jv; j0 += NG * A64_UNR) {
-        u4 kv[A64_UNR];
+    for (int j0 = g; j0 < Jv; j0 += NG * UNR) {
+        u4 kv[UNR];
         if (j0 == g) {
 #pragma unroll
-            for (int u = 0; u < A64_UNR; u++) kv[u] = k0[u];
+            for (int u = 0; u < UNR; u++) kv[u] = k0[u];
         } else {
 #pragma unroll
-            for (int u = 0; u < A64_UNR; u++) {
+            for (int u = 0; u < UNR; u++) {
                 const int j = j0 + NG * u;
                 kv[u] = j < Jv ? *(const u4*)(kbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
             }
         }
 #pragma unroll
-        for (int u = 0; u < A64_UNR; u++) {
+        for (int u = 0; u < UNR; u++) {
             float acc = 0.0f;
 #pragma unroll
             for (int t = 0; t < 4; t++) {
@@ -218,7 +222,7 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed
     for (int e = 0; e < 8; e++) o[e] = 0.0f;
     if (one_pass && !degenerate) {
 #pragma unroll
-        for (int u = 0; u < A64_UNR; u++) {
+        for (int u = 0; u < UNR; u++) {
             const int j = g + NG * u;
             if (j < Jp) {
                 const float pj = sc[j];
@@ -231,14 +235,14 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed
             }
         }
     } else {
-        for (int j0 = g; j0 < Jp; j0 += NG * A64_UNR) {
+        for (int j0 = g; j0 < Jp; j0 += NG * UNR) {
 #pragma unroll
-            for (int u = 0; u < A64_UNR; u++) {
+            for (int u = 0; u < UNR; u++) {
                 const int j = j0 + NG * u;
                 vv[u] = j < Jp ? *(const u4*)(vbase + (size_t)j * kstride) : u4{0u, 0u, 0u, 0u};
             }
 #pragma unroll
-            for (int u = 0; u < A64_UNR; u++) {
+            for (int u = 0; u < UNR; u++) {
                 const int j = j0 + NG * u;
                 if (j < Jp) {
                     const float pj = sc[j];
@@ -291,10 +295,10 @@ __device__ __forceinline__ void load_row_words(const uint32_t* __restrict__ p, u
 #pragma unroll
     for (int t = NW / 4 * 4; t < NW; t++) w[t] = p[t];
 }
-template <int D>
+template <int D, int JMAX = ATT_MAX_J>   // JMAX as in attention64_kernel
 __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, int J_fixed) {
     constexpr int EPL = D / 8, NW = EPL / 2, U = ADK_UNR, NT = ADK_THREADS, NWV = NT / 64, NG = NT / 8;
-    __shared__ float sc[ATT_MAX_J];
+    __shared__ float sc[JMAX];
     __shared__ float red[2][NWV];
     __shared__ float part[NWV][D];
     attn_kernarg_fence(a, J_fixed);
@@ -312,7 +316,7 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
     // the first pass of K and V rows (bounded by the rows allocated).
     // (the first half of the pass before the decode position is known, the
     // rest once it is, for the keys that exist)
-    const int kv_lim = a.kv_rows > 0 ? (a.d_pos ? a.kv_rows : min(a.kv_rows, J_fixed)) : min(J_fixed, ATT_MAX_J);
+    const int kv_lim = a.kv_rows > 0 ? (a.d_pos ? a.kv_rows : min(a.kv_rows, J_fixed)) : min(J_fixed, JMAX);
     // (clamped, unconditional loads, as in attention64_kernel)
     uint32_t k0[U][NW], v0[U][NW];
 #pragma unroll
@@ -336,7 +340,7 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
         }
     }
     const int qpos = (a.d_pos ? *a.d_pos : a.q_pos0) + s;
-    const int J = min(a.d_pos ? qpos + 1 : J_fixed, ATT_MAX_J);
+    const int J = min(a.d_pos ? qpos + 1 : J_fixed, JMAX);
     const int Jv = a.causal ? min(J, qpos + 1) : J;
     if (kv_lim > 0 && Jv > NG * (U / 2)) {   // (uniform)
         const int jl = min(Jv, kv_lim) - 1;
@@ -1498,12 +1502,27 @@ tlhip_status launch_attention_mfma(hipStream_t s, const AttnArgs& a, int J, uint
 
 static void launch_attn_any(hipStream_t s, const AttnArgs& a, int J) {
     // a key count known at launch above one 256-key pass takes the 512-thread
-    // variant (512 keys per pass); decode (J read on the device) keeps 256
-    if (a.D == 64 && !a.d_pos && J > 256) hipLaunchKernelGGL(attention64_kernel<512>, dim3(a.S, a.H), dim3(512), 0, s, a, J);
-    else if (a.D == 64) hipLaunchKernelGGL(attention64_kernel<256>, dim3(a.S, a.H), dim3(256), 0, s, a, J);
-    else if (a.D == 80) hipLaunchKernelGGL(attention_dk_kernel<80>, dim3(a.S, a.H), dim3(ADK_THREADS), 0, s, a, J);
-    else if (a.D == 128) hipLaunchKernelGGL(attention_dk_kernel<128>, dim3(a.S, a.H), dim3(ADK_THREADS), 0, s, a, J);
-    else hipLaunchKernelGGL(attention_kernel, dim3(a.S, a.H), dim3(256), 0, s, a, J);
+    // variant (512 keys per pass); decode (J read on the device) keeps 256.
+    // A key count known at launch of at most 512 takes a 2 KiB score row
+    // instead of the 32 KiB one, so more workgroups share a CU.
+    const bool small = !a.d_pos && J <= 512;
+    const dim3 g(a.S, a.H);
+    if (a.D == 64 && !a.d_pos && J > 256) {
+        if (small) hipLaunchKernelGGL((attention64_kernel<512, 512>), g, dim3(512), 0, s, a, J);
+        else hipLaunchKernelGGL(attention64_kernel<512>, g, dim3(512), 0, s, a, J);
+    } else if (a.D == 64) {
+        if (small && J <= 64) hipLaunchKernelGGL((attention64_kernel<256, 64, 2>), g, dim3(256), 0, s, a, J);
+        else if (small) hipLaunchKernelGGL((attention64_kernel<256, 512>), g, dim3(256), 0, s, a, J);
+        else hipLaunchKernelGGL(attention64_kernel<256>, g, dim3(256), 0, s, a, J);
+    } else if (a.D == 80) {
+        if (small) hipLaunchKernelGGL((attention_dk_kernel<80, 512>), g, dim3(ADK_THREADS), 0, s, a, J);
+        else hipLaunchKernelGGL(attention_dk_kernel<80>, g, dim3(ADK_THREADS), 0, s, a, J);
+    } else if (a.D == 128) {
+        if (small) hipLaunchKernelGGL((attention_dk_kernel<128, 512>), g, dim3(ADK_THREADS), 0, s, a, J);
+        else hipLaunchKernelGGL(attention_dk_kernel<128>, g, dim3(ADK_THREADS), 0, s, a, J);
+    } else {
+        hipLaunchKernelGGL(attention_kernel, g, dim3(256), 0, s, a, J);
+    }
 }
 
 tlhip_status launch_attention(hipStream_t s, const AttnArgs& a) {

@@ -823,18 +823,19 @@ bool gemm_skinny_ok(int M, int N, int K, int wt) {
 }
 
 // The skinny GEMM's launch shape for (M, N, K, weight type): M tiles per
-// workgroup, weight tiles per workgroup, K slices.  A cost model of the
-// measured kernel: a workgroup takes its bytes in at about 50 GB/s, plus
-// 2.5 us of fixed time per round of workgroups (one workgroup per CU: the
-// rings fill the LDS), plus 4 us for the exchange of a K split.
-// The skinny GEMM's launch shape for (M, N, K, weight type): M tiles per
 // workgroup (mt), 16-row weight tiles per workgroup (nt), waves (K parts)
-// per workgroup (kp) and K slices.  A cost model of the measured kernel: a
-// workgroup takes its bytes in at about 50 GB/s, plus 2.5 us of fixed time
-// per round of workgroups (one workgroup per CU: the rings fill the LDS),
-// plus 4 us for the exchange of a K split.  Eight waves (two per SIMD, so
-// one's dequantisation overlaps the other's MFMAs and waits) wherever the
-// LDS still holds a two-stage ring for each.
+// per workgroup (kp) and K slices.  A cost model fitted to the measured
+// kernel (M = 46, cold weights): a workgroup takes its activation bytes in
+// at about 50 GB/s (they are in L2: every weight tile reads them again) and
+// its weight bytes at about 25 GB/s, plus 2.5 us of fixed time per round of
+// workgroups (one workgroup per CU: the rings fill the LDS), plus 2.5 us
+// for the exchange of a K split.  Where the weight tiles alone fill the
+// device, splitting K with every row in one workgroup moves fewer bytes
+// per CU (Q4_0 [2048 x 5632]: 13.8 -> 11.0 us; Q8_0: 15.7 -> 12.1 us).
+// Eight waves (two per SIMD, so one's dequantisation overlaps the other's
+// MFMAs and waits) wherever the LDS still holds a two-stage ring for each:
+// four measured slower at every shape tried, so they are taken only when
+// nothing else fits; a split leaves each wave at least two 64-k steps.
 struct SkPlan {
     int mt = 1, nt = 2, kp = 4, mtiles = 1, splits = 1;
 };
@@ -846,27 +847,32 @@ static SkPlan sk_plan(int M, int N, int K, int wt) {
     const double bpe = wt == TLHIP_F16 ? 2.0 : (wt == TLHIP_Q8_0 ? 34.0 / 32 : 18.0 / 32);
     const int mt16 = (M + 15) / 16;
     SkPlan best;
-    double best_us = 1e30;
-    for (int nt : {2, 4})
-        for (int mt = 1; mt <= mt16; mt++) {
-            const int kp = SK_LDS / (8 * sk_stage_bytes(wt, mt, nt)) >= 2 ? 8 : 4;
-            for (int sp = 1; sp <= SK_MAX_SPLITS; sp *= 2) {
-                const int mtiles = (mt16 + mt - 1) / mt, ntiles = (N + 16 * nt - 1) / (16 * nt);
-                if (sp > 1 && ((K / 64) / sp < kp || mtiles * ntiles > SK_MAX_TILES_SPLIT)) continue;
-                const long wgs = (long)mtiles * ntiles * sp;
-                const double rounds = (double)((wgs + 255) / 256);
-                const double bytes = (std::min(16 * mt, M) * 2.0 + 16 * nt * bpe) * K / sp;
-                const double us = rounds * (bytes / 50e3 + 2.5) + (sp > 1 ? 4.0 : 0.0);
-                if (us < best_us - 1e-9) {
-                    best_us = us;
-                    best.mt = mt;
-                    best.nt = nt;
-                    best.kp = kp;
-                    best.mtiles = mtiles;
-                    best.splits = sp;
+    for (int allow4 = 0; allow4 < 2; allow4++) {
+        double best_us = 1e30;
+        for (int nt : {2, 4})
+            for (int mt = 1; mt <= mt16; mt++) {
+                const int sb = sk_stage_bytes(wt, mt, nt);
+                const int kp = SK_LDS / (8 * sb) >= 2 ? 8 : 4;
+                if ((kp == 4 && !allow4) || SK_LDS / (kp * sb) < 2) continue;
+                for (int sp = 1; sp <= SK_MAX_SPLITS; sp *= 2) {
+                    const int mtiles = (mt16 + mt - 1) / mt, ntiles = (N + 16 * nt - 1) / (16 * nt);
+                    if (sp > 1 && ((K / 64) / sp < 2 * kp || mtiles * ntiles > SK_MAX_TILES_SPLIT)) continue;
+                    const long wgs = (long)mtiles * ntiles * sp;
+                    const double rounds = (double)((wgs + 255) / 256);
+                    const double bx = std::min(16 * mt, M) * 2.0 * K / sp, bw = 16 * nt * bpe * K / sp;
+                    const double us = rounds * (bx / 50e3 + bw / 25e3 + 2.5) + (sp > 1 ? 2.5 : 0.0);
+                    if (us < best_us - 1e-9) {
+                        best_us = us;
+                        best.mt = mt;
+                        best.nt = nt;
+                        best.kp = kp;
+                        best.mtiles = mtiles;
+                        best.splits = sp;
+                    }
                 }
             }
-        }
+        if (best_us < 1e30) break;
+    }
     return best;
 }
 
