@@ -706,6 +706,61 @@ __device__ __forceinline__ void load_rows(const GemvParams& p, int row0, int lan
     }
 }
 
+// load_rows through range-checked buffer loads.  row0 must be wave-uniform:
+// every row base is then a scalar address (one descriptor per row and
+// stream, built by the scalar unit), each lane's offset is a 32-bit
+// multiple of its block index, and a block past the row (lane + 64 i >=
+// K / 32) reads zero bytes and a zero scale -- a zero weight -- with no
+// memory request and no clamp.  Rows past N are clamped to the last row.
+// What this saves is the per-lane 64-bit address arithmetic load_rows
+// issues before its first weight load; on MI355X that delay, repeated for
+// every wave a SIMD holds, cost 0.2-0.3 us of a 4 us GEMV.
+template <int WT, int NB, int RI>
+__device__ __forceinline__ void load_rows_buf(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
+                                              u4 (&q)[RI][NB][BlkLoads<WT>::n], uint32_t (&ds)[RI][NB]) {
+    constexpr int NL = BlkLoads<WT>::n;
+    const int nbr = K >> 5;
+    if (WT == TLHIP_Q6_K) {
+        const uint8_t* q2 = wq + q6k_q2_offset(N, K);
+        const uint8_t* sc = wq + q6k_sc_offset(N, K);
+#pragma unroll
+        for (int ri = 0; ri < RI; ri++) {
+            const size_t row = (size_t)min(row0 + ri, N - 1);
+            const __amdgpu_buffer_rsrc_t r4 = __builtin_amdgcn_make_buffer_rsrc((void*)(wq + row * (K / 2)), (short)0, K / 2, BUF_RSRC_WORD3);
+            const __amdgpu_buffer_rsrc_t r2 = __builtin_amdgcn_make_buffer_rsrc((void*)(q2 + row * (K / 4)), (short)0, K / 4, BUF_RSRC_WORD3);
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)(sc + row * (K / 16)), (short)0, K / 16, BUF_RSRC_WORD3);
+            const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)(wd + row * (K / 256)), (short)0, K / 128, BUF_RSRC_WORD3);
+#pragma unroll
+            for (int i = 0; i < NB; i++) {
+                const int b = lane + 64 * i;
+                q[ri][i][0] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r4, b * 16, 0, 0));
+                const uint2 h = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r2, b * 8, 0, 0));
+                const uint32_t s2 = __builtin_amdgcn_raw_buffer_load_b16(rs, b * 2, 0, 0);
+                const uint32_t dv = __builtin_amdgcn_raw_buffer_load_b16(rd, (b >> 3) * 2, 0, 0);
+                q[ri][i][1] = u4{h.x, h.y, s2 | (dv << 16), 0u};
+                ds[ri][i] = 0u;
+            }
+        }
+        return;
+    }
+    const int row_bytes = WT == TLHIP_Q4_0 ? K / 2 : (WT == TLHIP_Q8_0 ? K : K * 2);
+#pragma unroll
+    for (int ri = 0; ri < RI; ri++) {
+        const size_t row = (size_t)min(row0 + ri, N - 1);
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)(wq + row * row_bytes), (short)0, row_bytes, BUF_RSRC_WORD3);
+        const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)(wd + row * nbr), (short)0,
+                                                                            WT == TLHIP_F16 ? 0 : nbr * 2, BUF_RSRC_WORD3);
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int b = lane + 64 * i;
+#pragma unroll
+            for (int l = 0; l < NL; l++)
+                q[ri][i][l] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rq, b * (16 * NL) + 16 * l, 0, 0));
+            ds[ri][i] = WT == TLHIP_F16 ? 0u : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rd, b * 2, 0, 0);
+        }
+    }
+}
+
 // Lane 0's bias / residual elements of the wave's rows, loaded right after
 // the weights so the epilogue makes no dependent loads.
 template <int RI, int MX>
@@ -860,6 +915,108 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvParams p) {
     if (lane == 0) store_rows<RI, MX>(p, row0, acc, pre);
 }
 
+// Activation quad `it` (block it / 4, quad it % 4) of a row through a
+// range-checked buffer descriptor of the row: a quad past the row reads
+// zeros with no memory request.  Pair order of gemv_kernel's staging.
+template <int WT>
+__device__ __forceinline__ void load_quad_buf(__amdgpu_buffer_rsrc_t r, int it, uint32_t w[4]) {
+    const int b = it >> 2, v = it & 3;
+    if (xo_nibble<WT>()) {
+        const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (b * 32 + 4 * v) * 2, 0, 0));
+        const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (b * 32 + 16 + 4 * v) * 2, 0, 0));
+        w[0] = lo.x; w[1] = lo.y; w[2] = hi.x; w[3] = hi.y;
+    } else {
+        const u4 t = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, (b * 32 + 8 * v) * 2, 0, 0));
+        w[0] = t[0]; w[1] = t[1]; w[2] = t[2]; w[3] = t[3];
+    }
+}
+
+// Plain GEMV of one activation row (M = 1) with the single-row epilogues
+// (STORE, BIAS, RESID, BIAS_RESID, BIAS_GELU): the decoder's output and
+// down projections and linear() on one row.  The arithmetic is
+// gemv_kernel's, bit for bit (same block dots, same lane partial sums, same
+// wave reduction); what differs is how the loads are addressed.  Its
+// parameter block holds only what these epilogues read, fetched as the
+// code first needs it; the wave's rows are scalar (the wave index is read
+// through readfirstlane), and every load is a range-checked buffer load
+// (load_rows_buf, load_quad_buf): the weight loads go out after a handful
+// of scalar instructions instead of gemv_kernel's per-lane 64-bit address
+// arithmetic, and blocks or quads past the row read zeros (zero weights,
+// zero activations) so the dot needs no bounds branch.
+struct Gemv1Params {
+    const uint16_t* x;
+    const uint8_t* wq;
+    const uint16_t* wd;
+    const uint16_t* bias;
+    const uint16_t* resid;
+    uint16_t* y;
+    int N, K, epi;
+};
+
+template <int WT, int NB, int RI>
+__global__ __launch_bounds__(256) void gemv_m1_kernel(Gemv1Params p) {
+    __shared__ u4 xs[4][NB * 64];
+    constexpr int NL = BlkLoads<WT>::n;
+    const int lane = threadIdx.x & 63;
+    const int row0 = ((int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6)) * RI;
+    uint32_t xw[NB][4];
+    {
+        const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, (short)0, p.K * 2, BUF_RSRC_WORD3);
+#pragma unroll
+        for (int k = 0; k < NB; k++) load_quad_buf<WT>(rx, (int)threadIdx.x + 256 * k, xw[k]);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // the activation loads go out first
+    u4 q[RI][NB][NL];
+    uint32_t ds[RI][NB];
+    load_rows_buf<WT, NB, RI>(p.wq, p.wd, p.N, p.K, row0, lane, q, ds);
+    // the epilogue's f16 operands: one per row, the same address in every
+    // lane; an absent operand is never loaded (the branch is uniform)
+    uint32_t eb[RI], er[RI];
+#pragma unroll
+    for (int ri = 0; ri < RI; ri++) eb[ri] = er[ri] = 0u;
+    if (p.bias) {
+        const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)p.bias, (short)0, p.N * 2, BUF_RSRC_WORD3);
+#pragma unroll
+        for (int ri = 0; ri < RI; ri++) eb[ri] = __builtin_amdgcn_raw_buffer_load_b16(rb, 0, (row0 + ri) * 2, 0);
+    }
+    if (p.resid) {
+        const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc((void*)p.resid, (short)0, p.N * 2, BUF_RSRC_WORD3);
+#pragma unroll
+        for (int ri = 0; ri < RI; ri++) er[ri] = __builtin_amdgcn_raw_buffer_load_b16(rr, 0, (row0 + ri) * 2, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < NB; k++) {
+        const int it = threadIdx.x + 256 * k;
+        const uint32_t* w = xw[k];
+        xs[it & 3][it >> 2] = WT == TLHIP_F16 ? u4{w[0], w[1], w[2], w[3]}
+                                              : u4{pack_lo(w[0], w[1]), pack_hi(w[0], w[1]), pack_lo(w[2], w[3]), pack_hi(w[2], w[3])};
+    }
+    lds_barrier();
+    if (row0 >= p.N) return;   // (uniform: only the last workgroup has idle waves)
+    float acc[RI];
+#pragma unroll
+    for (int ri = 0; ri < RI; ri++) acc[ri] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        const int b = lane + 64 * i;
+        uint32_t xc[16];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const u4 t = xs[v][b];
+            xc[4 * v] = t[0]; xc[4 * v + 1] = t[1]; xc[4 * v + 2] = t[2]; xc[4 * v + 3] = t[3];
+        }
+#pragma unroll
+        for (int ri = 0; ri < RI; ri++) acc[ri] = block_dot<WT>(q[ri][i], ds[ri][i], xc, acc[ri]);
+    }
+#pragma unroll
+    for (int ri = 0; ri < RI; ri++) acc[ri] = wave_sum<64>(acc[ri]);
+    if (lane == 0) {
+#pragma unroll
+        for (int ri = 0; ri < RI; ri++)
+            if (row0 + ri < p.N) p.y[row0 + ri] = epilogue_v(p.epi, acc[ri], (uint16_t)eb[ri], (uint16_t)er[ri]);
+    }
+}
+
 // Normalised GEMV (M = 1): norm(x) staged once per workgroup in LDS (the
 // weight loads are issued first, so they are in flight during it), then
 // the same block dots.  EPI_ARGMAX additionally reduces the workgroup's
@@ -1003,6 +1160,28 @@ static bool launch_nb(hipStream_t s, const GemvParams& p, int nb, int ri) {
     }
 }
 
+template <int WT, int NB>
+static void launch_m1_ri(hipStream_t s, const Gemv1Params& p, int ri) {
+    const int waves = (p.N + ri - 1) / ri;
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    if (ri == 2) hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, 2>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, 1>), grid, dim3(256), 0, s, p);
+}
+
+template <int WT>
+static bool launch_m1(hipStream_t s, const GemvParams& g, int nb, int ri) {
+    const Gemv1Params p = {g.x, g.wq, g.wd, g.bias, g.resid, g.y, g.N, g.K, g.epi};
+    switch (nb) {
+        case 1: launch_m1_ri<WT, 1>(s, p, ri); return true;
+        case 2: launch_m1_ri<WT, 2>(s, p, ri); return true;
+        case 3: launch_m1_ri<WT, 3>(s, p, ri); return true;
+        case 4: launch_m1_ri<WT, 4>(s, p, ri); return true;
+        case 5: case 6: launch_m1_ri<WT, 6>(s, p, ri); return true;
+        case 7: case 8: launch_m1_ri<WT, 8>(s, p, ri); return true;
+        default: return false;
+    }
+}
+
 template <int WT>
 static bool launch_mx(hipStream_t s, const GemvParams& p, int nb, int ri) {
     if (p.M == 1) return launch_nb<WT, 1>(s, p, nb, ri);
@@ -1116,7 +1295,12 @@ tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
             // (5632 x 2048 and 2048 x 5632); paired epilogues need it anyway
             int ri = p.N >= 1024 ? 2 : 1;
             if (pair_epi) ri = 2;
-            if (wt == TLHIP_Q4_0) done = launch_mx<TLHIP_Q4_0>(s, p, nb, ri);
+            if (p.M == 1 && !pair_epi) {   // single-row epilogues: the compact M = 1 kernel
+                if (wt == TLHIP_Q4_0) done = launch_m1<TLHIP_Q4_0>(s, p, nb, ri);
+                else if (wt == TLHIP_Q8_0) done = launch_m1<TLHIP_Q8_0>(s, p, nb, ri);
+                else if (wt == TLHIP_Q6_K) done = launch_m1<TLHIP_Q6_K>(s, p, nb, ri);
+                else done = launch_m1<TLHIP_F16>(s, p, nb, ri);
+            } else if (wt == TLHIP_Q4_0) done = launch_mx<TLHIP_Q4_0>(s, p, nb, ri);
             else if (wt == TLHIP_Q8_0) done = launch_mx<TLHIP_Q8_0>(s, p, nb, ri);
             else if (wt == TLHIP_Q6_K) done = launch_mx<TLHIP_Q6_K>(s, p, nb, ri);
             else done = launch_mx<TLHIP_F16>(s, p, nb, ri);

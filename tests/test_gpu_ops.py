@@ -224,6 +224,27 @@ def test_linear_bias_and_f16_odd_shapes(dev, oracle):
         assert_close(got, oracle.linear(x[:M], w, b), what=f"f16 linear M={M}")
 
 
+@pytest.mark.parametrize("qt", [Q4_0, Q8_0, F16])
+@pytest.mark.parametrize("N,K", [(37, 96), (1025, 2048), (300, 5632), (2, 32)])
+def test_linear_one_row_bias(dev, oracle, qt, N, K):
+    """One activation row with a bias: the compact M = 1 GEMV (rows per wave
+    1 or 2, blocks past the row read as zero weights: K = 96 and 5632 leave
+    lanes without a block, K = 32 all but one)."""
+    x = S.normal_f16(9, f"x1b{K}", (1, K))
+    b = S.normal_f16(9, f"b1b{N}", (N,))
+    if qt == F16:
+        wh = S.normal_f16(9, f"W1b{N}x{K}", (N, K), 0.0, 0.05)
+        w = dev.tensor(wh)
+        ref = oracle.linear(x, wh, b)
+    else:
+        gen = S.q4_0_blocks if qt == Q4_0 else S.q8_0_blocks
+        blocks = gen(9, f"W1b{N}x{K}", N, K)
+        w = dev.quantized(blocks, (N, K), qt)
+        ref = oracle.linear_q(x, blocks, 2 if qt == Q4_0 else 8, N, b)
+    got = dev.tensor(x).linear(w, dev.tensor(b)).numpy()
+    assert_close(got, ref, what=f"one-row linear + bias {qt} {N}x{K}")
+
+
 def test_matmul_known_answer(dev):
     # tests/test_gpu_operations.rs:81-94: [[1,2],[3,4]] @ [[5,6],[7,8]]
     a = dev.tensor(np.array([[1, 2], [3, 4]], np.float16))
