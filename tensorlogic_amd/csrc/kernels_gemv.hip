@@ -1027,8 +1027,8 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams p) {
     __shared__ float red[2][WPB];
     __shared__ unsigned long long wkey[WPB];
     kernarg_fence(p);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * WPB + w) * RI;
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int row0 = (blockIdx.x * WPB + w) * RI;   // wave-uniform (load_rows_buf)
     const int nbr = p.K >> 5;
     constexpr int NL = BlkLoads<WT>::n;
     u4 q[RI][NB][NL];
@@ -1045,12 +1045,15 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams p) {
     // absent for F16 weights).
     const bool dev_pos = p.epi == EPI_QKV_ROPE && p.d_pos;
     const int pos_raw = (dev_pos ? p.d_pos : (const int32_t*)p.norm_w)[opaque_zero()];
-    const uint16_t* xsrc = p.embd ? p.embd + (size_t)(*p.d_token) * p.K : p.x;
+    // (the token is uniform: read through readfirstlane, the row address
+    // stays scalar and the staging loads take one buffer descriptor instead
+    // of a loop over the lanes' distinct descriptors)
+    const uint16_t* xsrc = p.embd ? p.embd + (size_t)__builtin_amdgcn_readfirstlane(*p.d_token) * p.K : p.x;
     NormStage<WT, NB, WPB, PRO> st;
     st.load(p, xsrc);
-    // (unconditional: load_rows clamps rows into the matrix, and loads under
-    // a branch leave the compiler's wait counts imprecise after it)
-    load_rows<WT, NB, RI>(p, row0, lane, q, ds);
+    // (unconditional: rows are clamped into the matrix, and loads under a
+    // branch leave the compiler's wait counts imprecise after it)
+    load_rows_buf<WT, NB, RI>(p.wq, p.wd, p.N, p.K, row0, lane, q, ds);
     EpiPre<RI, 1> pre;
     QkvPre qp[RI / 2 > 0 ? RI / 2 : 1];
     if (lane == 0 && row0 < p.N) {
