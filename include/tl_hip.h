@@ -210,6 +210,17 @@ tlhip_status tlhip_attention(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhi
 /* temperature_sample(logits, T<=1e-4) argmax (builtin_sampling.rs:170-176):
  * last maximum wins; logits [V] or [S,V] (last row).  Synchronous.        */
 tlhip_status tlhip_argmax(tlhip_ctx ctx, tlhip_tensor logits, int32_t* out);
+/* argmax(x[, dim[, keepdim]]) = Tensor::argmax(dim, keepdim) (reduce.rs:585-668;
+ * builtin_tensor.rs:1438-1490): index of the FIRST largest value (a strict '>'
+ * scan; NaN never wins, and neither does -inf along a dim), stored in x's own
+ * dtype (f16 or f32) as the reference's T::from_f64(index).  dim < 0: the
+ * whole tensor, y of shape [1] (keepdim: [1] * rank); else y has x's shape
+ * without dim (keepdim: dim of size 1), reducing the only dim without keepdim
+ * is a shape error as in the reference, and output element o is the line
+ * whose kept coordinates are o's digits with the first kept dim least
+ * significant (the reference's own index order).  The builtin's integer
+ * result (no dim, no keepdim) is y's one element.                         */
+tlhip_status tlhip_tensor_argmax(tlhip_ctx ctx, tlhip_tensor x, int dim, int keepdim, tlhip_tensor y);
 /* temperature_sample(logits, T) (builtin_sampling.rs:66-231): T <= 1e-4 is
  * tlhip_argmax; otherwise softmax(x / T) and the inverse-CDF index of one
  * uniform draw, V <= 2^20.  The reference draws from an unseeded

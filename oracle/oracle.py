@@ -84,6 +84,7 @@ def _declare(L):
         "tlo_embedding": (i, [vp, i, i, vp, i, vp]),
         "tlo_causal_mask": (None, [i, vp]),
         "tlo_slice_last": (i, [vp, vp, i, i, i, vp]),
+        "tlo_tensor_argmax": (C.c_int64, [vp, vp, i, i, vp]),
         "tlo_broadcast_to": (i, [vp, vp, i, vp, i, i, vp]),
         "tlo_rope_cos_sin": (i, [vp, i, i, i, vp, vp, i, vp]),
         "tlo_precompute_rope": (None, [i, i, f, i, vp]),
@@ -323,6 +324,32 @@ def slice_last(x, axis: int = 0) -> np.ndarray:
     if lib().tlo_slice_last(_p(x), _p(shp), x.ndim, axis, x.itemsize, _p(out)) != 0:
         raise ValueError(f"slice_last: axis {axis} of a {x.ndim}-D tensor")
     return out
+
+
+def tensor_argmax(x, dim=None, keepdim=False) -> np.ndarray:
+    """Tensor::argmax(dim, keepdim) on an f16 (uint16 bits or float16) or f32
+    array: the result tensor the reference builds, in x's dtype (indices
+    converted with T::from_f64, so f16 indices above 2048 are rounded).
+    Raises ValueError where the reference returns an error."""
+    x = np.ascontiguousarray(x)
+    if x.dtype == np.uint16:
+        x = x.view(np.float16)
+    xd = np.ascontiguousarray(x, dtype=np.float64)
+    shp = _shape_arr(x.shape)
+    n_out = 1 if dim is None else int(np.prod([s for i, s in enumerate(x.shape) if i != dim], dtype=np.int64))
+    idx = np.zeros(max(n_out, 1), np.int64)
+    got = lib().tlo_tensor_argmax(_p(xd), _p(shp), x.ndim, -1 if dim is None else dim, _p(idx))
+    if got < 0:
+        raise ValueError(f"argmax: dim {dim} of a {x.ndim}-D tensor (or an empty tensor)")
+    if dim is None:
+        out_shape = (1,) * x.ndim if keepdim else (1,)
+    else:
+        out_shape = tuple((1 if i == dim else s) for i, s in enumerate(x.shape) if keepdim or i != dim)
+        if not out_shape:
+            # Tensor::from_vec(1 value, shape []) fails: a shape without dims
+            # has numel 0 (tensor_creation.rs:111-118, shape.rs:28-34)
+            raise ValueError("argmax: every dim reduced without keepdim (ShapeMismatch)")
+    return idx[:got].astype(np.float64).astype(x.dtype).reshape(out_shape)
 
 
 def broadcast_to(x, shape) -> np.ndarray:

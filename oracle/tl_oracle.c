@@ -545,6 +545,54 @@ int tlo_slice_last(const void* x, const int64_t* shape, int ndim, int axis, int 
     return 0;
 }
 
+int64_t tlo_tensor_argmax(const double* x, const int64_t* shape, int ndim, int dim, int64_t* idx) {
+    size_t total = 1;
+    for (int i = 0; i < ndim; i++) total *= (size_t)shape[i];
+    if (dim < 0) {
+        /* reduce.rs:589-598 */
+        if (total == 0) return -1;
+        int64_t best = 0;
+        double mv = x[0];
+        for (size_t i = 1; i < total; i++)
+            if (x[i] > mv) {
+                mv = x[i];
+                best = (int64_t)i;
+            }
+        idx[0] = best;
+        return 1;
+    }
+    if (dim >= ndim || ndim > 8) return -1;
+    /* reduce.rs:621-668 */
+    int64_t strides[8];
+    strides[ndim - 1] = 1;
+    for (int i = ndim - 2; i >= 0; i--) strides[i] = strides[i + 1] * shape[i + 1];
+    size_t out_n = 1;
+    for (int i = 0; i < ndim; i++)
+        if (i != dim) out_n *= (size_t)shape[i];
+    for (size_t o = 0; o < out_n; o++) {
+        int64_t coords[8] = {0};
+        size_t rem = o;
+        for (int i = 0; i < ndim; i++)
+            if (i != dim) {
+                coords[i] = (int64_t)(rem % (size_t)shape[i]);
+                rem /= (size_t)shape[i];
+            }
+        int64_t best = 0;
+        double mv = -INFINITY;
+        for (int64_t d = 0; d < shape[dim]; d++) {
+            coords[dim] = d;
+            int64_t lin = 0;
+            for (int i = 0; i < ndim; i++) lin += coords[i] * strides[i];
+            if (x[lin] > mv) {
+                mv = x[lin];
+                best = d;
+            }
+        }
+        idx[o] = best;
+    }
+    return (int64_t)out_n;
+}
+
 int tlo_broadcast_to(const void* x, const int64_t* xshape, int xnd, const int64_t* tshape,
                      int tnd, int elem, void* y) {
     /* shape.rs:37-49: rank may not shrink; aligned from the right each input

@@ -166,6 +166,21 @@ void tlo_causal_mask(int n, uint16_t* out);
  * elem = element bytes.  Returns 0, or -1 for an axis the reference rejects
  * (InvalidOperation).                                                      */
 int tlo_slice_last(const void* x, const int64_t* shape, int ndim, int axis, int elem, void* y);
+/* Tensor::argmax(dim, keepdim) reduce.rs:585-658 (the argmax() builtin,
+ * builtin_tensor.rs:1438-1490), on values already widened to double (exact
+ * for f16 and f32 inputs).  dim < 0: the whole tensor, scanned in order from
+ * element 0 with a strict '>' against element 0's value (reduce.rs:589-598)
+ * -- the first maximum wins and a NaN at element 0 keeps index 0.  dim >= 0:
+ * each output element o scans its line from a running maximum of -inf with
+ * a strict '>' (reduce.rs:644-668), so the first maximum wins and NaN and
+ * -inf never do.  Output element o's line has the non-reduced coordinates
+ * of o taken digit by digit with the FIRST non-reduced dim least significant
+ * (reduce.rs:649-657), as the reference computes them; its output is
+ * row-major in the kept dims, so for two or more kept dims larger than one
+ * the lines land in the transposed order.  idx receives the indices (one per
+ * output element; 1 for dim < 0).  Returns the output element count, or -1
+ * for dim >= ndim (InvalidDimension) or an empty input with dim < 0.      */
+int64_t tlo_tensor_argmax(const double* x, const int64_t* shape, int ndim, int dim, int64_t* idx);
 /* Tensor::broadcast_to broadcast.rs:11-30 + broadcast_f16 unified.metal:
  * 3769-3815, TensorShape::can_broadcast_to shape.rs:37-49: dims aligned from
  * the right; an input dim of 1 repeats.  Returns 0, or -1 when the shapes

@@ -214,6 +214,8 @@ tlhip_status launch_rope(hipStream_t s, const uint16_t* x, uint16_t* y, int S, i
                          int64_t batch, int offset, const int32_t* d_pos, int layout,
                          int rot_dims, const float* table, int x_row_stride, int y_row_stride);
 tlhip_status launch_softmax(hipStream_t s, const uint16_t* x, uint16_t* y, int64_t rows, int n);
+tlhip_status launch_tensor_argmax(hipStream_t s, tlhip_dtype dt, const void* x, void* y, const int64_t* shape, int nd,
+                                  int dim);   // dim < 0: whole tensor; y: one element per line
 enum EwOp { EW_SIGMOID = 0, EW_SILU = 1, EW_GELU = 2, EW_ADD = 3, EW_MUL = 4, EW_MUL_SCALAR = 5,
             EW_SILU_MUL = 6 };
 tlhip_status launch_elementwise(hipStream_t s, int op, const uint16_t* a, const uint16_t* b,

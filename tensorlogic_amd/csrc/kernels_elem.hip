@@ -487,6 +487,113 @@ tlhip_status launch_causal_mask(hipStream_t s, uint16_t* out, int64_t n) {
 }
 
 // ---------------------------------------------------------------------------
+// Tensor::argmax(dim, keepdim) (reduce.rs:585-668, the argmax() builtin):
+// one workgroup per output element.  The reference scans its line in order
+// with a strict '>' (from element 0's value for the whole tensor, from -inf
+// along a dim), so the result is the first index of the line's largest
+// value, a NaN never wins, and along a dim neither does -inf (index 0 when
+// nothing beats the start; for the whole tensor, also when element 0 is
+// NaN).  Here every thread scans a strided part of the line and keeps the
+// largest key (order-preserving image of the value << 32 | ~index: larger
+// value first, then smaller index), -0 counted as +0; the keys meet in a
+// workgroup maximum, which no scan order changes.  Line o starts at the
+// coordinates the reference derives from o (first kept dim least
+// significant, reduce.rs:649-657).  The index is stored as T::from_f64(i)
+// in the input's type (f16: rounded to nearest even above 2048).
+// ---------------------------------------------------------------------------
+struct ArgmaxDims {
+    int64_t shape[8];
+    int64_t stride[8];
+    int nd, dim;          // dim < 0: the whole tensor
+    int64_t line, lstride;
+};
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int64_t i) {
+    if (!(v > -INFINITY)) return 0ull;   // NaN and -inf never win a '>' against -inf
+    if (v == 0.0f) v = 0.0f;             // -0 == +0
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (0xffffffffu - (uint32_t)i);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void tensor_argmax_kernel(const T* __restrict__ x, T* __restrict__ y, ArgmaxDims d) {
+    __shared__ unsigned long long wk[4];
+    int64_t base = 0;
+    if (d.dim >= 0) {
+        int64_t rem = blockIdx.x;
+        for (int i = 0; i < d.nd; i++)
+            if (i != d.dim) {
+                base += (rem % d.shape[i]) * d.stride[i];
+                rem /= d.shape[i];
+            }
+    }
+    auto val = [&](int64_t i) -> float {
+        if constexpr (sizeof(T) == 2) return h2f(x[base + i * d.lstride]);
+        else return x[base + i * d.lstride];
+    };
+    unsigned long long best = 0ull;
+    for (int64_t i = threadIdx.x; i < d.line; i += 256) {
+        const unsigned long long k = argmax_key(val(i), i);
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)best, off), hi = __shfl_xor((uint32_t)(best >> 32), off);
+        const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = wk[0];
+        for (int w = 1; w < 4; w++) b = wk[w] > b ? wk[w] : b;
+        int64_t idx = b ? (int64_t)(0xffffffffu - (uint32_t)b) : 0;
+        if (d.dim < 0 && !(val(0) == val(0))) idx = 0;   // a NaN start is never beaten
+        const float f = (float)idx;                        // exact below 2^24
+        if constexpr (sizeof(T) == 2) y[blockIdx.x] = f2h(f);
+        else y[blockIdx.x] = f;
+    }
+}
+
+tlhip_status launch_tensor_argmax(hipStream_t s, tlhip_dtype dt, const void* x, void* y, const int64_t* shape, int nd,
+                                  int dim) {
+    if (nd > 8) return fail(TLHIP_ERR_INVALID_DIMENSION, "argmax: rank %d > 8", nd);
+    ArgmaxDims d = {};
+    d.nd = nd;
+    d.dim = dim;
+    int64_t total = 1, st = 1;
+    for (int i = nd - 1; i >= 0; i--) {
+        d.shape[i] = shape[i];
+        d.stride[i] = st;
+        st *= shape[i];
+    }
+    total = st;
+    int64_t outs = 1;
+    if (dim < 0) {
+        d.line = total;
+        d.lstride = 1;
+    } else {
+        d.line = shape[dim];
+        d.lstride = d.stride[dim];
+        outs = total / (shape[dim] ? shape[dim] : 1);
+        if (shape[dim] == 0) {   // every line is empty: all outputs index 0
+            outs = 1;
+            for (int i = 0; i < nd; i++)
+                if (i != dim) outs *= shape[i];
+        }
+    }
+    if (d.line >= 0xffffffffll) return fail(TLHIP_ERR_INVALID_DIMENSION, "argmax: line of %lld elements", (long long)d.line);
+    if (outs <= 0) return TLHIP_OK;
+    if (outs > 0x7fffffffll) return fail(TLHIP_ERR_INVALID_DIMENSION, "argmax: %lld outputs", (long long)outs);
+    if (dt == TLHIP_F16)
+        hipLaunchKernelGGL(tensor_argmax_kernel<uint16_t>, dim3((unsigned)outs), dim3(256), 0, s, (const uint16_t*)x, (uint16_t*)y, d);
+    else
+        hipLaunchKernelGGL(tensor_argmax_kernel<float>, dim3((unsigned)outs), dim3(256), 0, s, (const float*)x, (float*)y, d);
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
 // broadcast_to (broadcast.rs:11-120, broadcast_f16 unified.metal:3769-3815):
 // target element g reads the input element whose coordinates are g's,
 // aligned from the right, with coordinate 0 on the input's size-1 dims

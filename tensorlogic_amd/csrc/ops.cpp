@@ -526,6 +526,37 @@ tlhip_status tlhip_attention(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhi
     return after_launch(ctx, "attention");
 }
 
+tlhip_status tlhip_tensor_argmax(tlhip_ctx ctx, tlhip_tensor x, int dim, int keepdim, tlhip_tensor y) {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(check_t(x, "argmax"));
+    TLHIP_TRY(check_t(y, "argmax"));
+    if (x->dtype != TLHIP_F16 && x->dtype != TLHIP_F32)
+        return fail(TLHIP_ERR_DTYPE, "argmax: input must be f16 or f32 (dtype %d)", (int)x->dtype);
+    if (y->dtype != x->dtype) return fail(TLHIP_ERR_DTYPE, "argmax: result dtype %d != input dtype %d", (int)y->dtype, (int)x->dtype);
+    if (dim >= x->ndim) return fail(TLHIP_ERR_INVALID_DIMENSION, "Invalid dimension: %d", dim);
+    if (x->ndim > 8) return fail(TLHIP_ERR_INVALID_DIMENSION, "argmax: rank %d > 8", x->ndim);
+    // result shape (reduce.rs:600-606, 625-636): the whole tensor -> [1]
+    // ([1] * rank with keepdim); a dim -> the other dims (that dim as 1 with
+    // keepdim).  Reducing the only dim without keepdim leaves no dims, which
+    // the reference's Tensor::from_vec rejects (a dimensionless shape has
+    // numel 0, tensor_creation.rs:111-118).
+    std::vector<int64_t> want;
+    if (dim < 0) {
+        if (numel(x) == 0) return fail(TLHIP_ERR_INVALID_OPERATION, "argmax of an empty tensor");
+        want.assign(keepdim ? x->ndim : 1, 1);
+    } else {
+        for (int i = 0; i < x->ndim; i++)
+            if (i != dim) want.push_back(x->shape[i]);
+            else if (keepdim) want.push_back(1);
+        if (want.empty()) return fail(TLHIP_ERR_SHAPE_MISMATCH, "argmax: no dims left (expected [0], got [1])");
+    }
+    if ((int)want.size() != y->ndim || memcmp(want.data(), y->shape, sizeof(int64_t) * want.size()) != 0)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "argmax: result shape %s for %s along dim %d", shape_str(y).c_str(),
+                    shape_str(x).c_str(), dim);
+    TLHIP_TRY(launch_tensor_argmax(ctx->stream, x->dtype, x->data, y->data, x->shape, x->ndim, dim < 0 ? -1 : dim));
+    return after_launch(ctx, "argmax");
+}
+
 tlhip_status tlhip_argmax(tlhip_ctx ctx, tlhip_tensor logits, int32_t* out) {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("argmax", {logits}));

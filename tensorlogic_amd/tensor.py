@@ -257,6 +257,23 @@ class Tensor:
         call("tlhip_argmax", self.dev.h, self.h, C.byref(r))
         return r.value
 
+    def argmax(self, dim: int | None = None, keepdim: bool = False) -> "int | Tensor":
+        """The argmax() builtin (builtin_tensor.rs:1438-1490) over
+        Tensor::argmax (reduce.rs:585-668): with neither dim nor keepdim the
+        index as an integer, read back from the reference's result tensor
+        (so an f16 index above 2048 comes back rounded, as there); otherwise
+        the result tensor in this tensor's dtype."""
+        shape = self.shape
+        if dim is None:
+            out_shape = (1,) * len(shape) if keepdim else (1,)
+        else:
+            out_shape = tuple(1 if i == dim else s for i, s in enumerate(shape) if keepdim or i != dim) or (1,)
+        out = self.dev.empty(out_shape, self.dtype)
+        call("tlhip_tensor_argmax", self.dev.h, self.h, -1 if dim is None else int(dim), int(bool(keepdim)), out.h)
+        if dim is None and not keepdim:
+            return int(out.numpy().astype(np.float64)[0])
+        return out
+
 
 def einsum(eq: str, a: Tensor, b: Tensor) -> Tensor:
     """The two attention einsums the TL programs use (einsum.rs:653-886)."""

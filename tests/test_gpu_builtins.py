@@ -110,3 +110,68 @@ def test_rope_cos_sin_errors(dev):
         dev.tensor(np.zeros((4, 8), np.float16)).rope_candle(dev.tensor(np.ones((4, 8), np.float16)),
                                                             dev.tensor(np.ones((4, 8), np.float16)))
     assert e.value.kind == "InvalidOperation"
+
+
+# ---------------------------------------------------------------------------
+# argmax() builtin (Tensor::argmax, reduce.rs:585-668): indices are small
+# integers stored in the input dtype, so the bar is bit-exact.
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape,dim,keepdim", [((5,), None, False), ((5,), None, True), ((2, 3), 1, False),
+                                               ((2, 3), 1, True), ((2, 3), 0, False), ((6, 9), None, True),
+                                               ((4, 3, 5), 0, False), ((4, 3, 5), 1, True), ((4, 3, 5), 2, False),
+                                               ((2, 3, 4, 5), 2, False), ((64, 32000), 1, False),
+                                               ((3, 5000), None, False), ((2, 70000), 1, False),
+                                               ((300, 7), 0, True), ((1, 1), 0, False)])
+@pytest.mark.parametrize("dtype", [F16, F32])
+def test_tensor_argmax(dev, oracle, shape, dim, keepdim, dtype):
+    np_t = np.float16 if dtype == F16 else np.float32
+    rng = np.random.default_rng(int(np.prod(shape)) % 1000 + (dim or 0))
+    x = rng.integers(-40, 41, size=shape).astype(np_t)   # ties everywhere
+    flat = x.reshape(-1)
+    flat[rng.integers(0, flat.size, size=max(1, flat.size // 50))] = np.nan
+    flat[rng.integers(0, flat.size, size=max(1, flat.size // 50))] = -np.inf
+    flat[rng.integers(0, flat.size, size=max(1, flat.size // 50))] = np.float16(-0.0)
+    if dim is None and flat.size > 2:
+        flat[0] = 1.0   # (a NaN at element 0 has a test of its own)
+    t = dev.tensor(x, dtype)
+    got = t.argmax(dim, keepdim)
+    want = oracle.tensor_argmax(x, dim, keepdim)
+    if dim is None and not keepdim:
+        assert got == int(want[0])
+    else:
+        g = got.numpy()
+        assert g.shape == want.shape and g.dtype == want.dtype
+        assert np.array_equal(bits(g), bits(want))
+
+
+def test_tensor_argmax_specials(dev, oracle):
+    inf, nan = np.inf, np.nan
+    for arr, dim in (([nan, 5, 7], None), ([[nan, 5, 7], [-inf, -inf, nan], [-inf, -3, -inf]], 1),
+                     ([-0.0, 0.0, -1], None), ([[1, 4, 4, 2]], 1)):
+        for dt, np_t in ((F16, np.float16), (F32, np.float32)):
+            x = np.array(arr, np_t)
+            got = dev.tensor(x, dt).argmax(dim, True)
+            want = oracle.tensor_argmax(x, dim, True)
+            assert np.array_equal(bits(got.numpy()), bits(want)), (arr, dim, dt)
+    # f16 indices above 2048 round to nearest even, as T::from_f64 does
+    x = np.zeros((1, 4000), np.float16)
+    x[0, 3003] = 1
+    assert dev.tensor(x).argmax() == 3004
+    assert dev.tensor(x.astype(np.float32), F32).argmax() == 3003
+
+
+def test_tensor_argmax_errors(dev):
+    from tensorlogic_amd._lib import call
+    t = dev.tensor(np.ones((2, 3), np.float16))
+    with pytest.raises(TLHipError) as e:
+        t.argmax(10)
+    assert e.value.kind == "InvalidDimension"
+    with pytest.raises(TLHipError) as e:
+        dev.tensor(np.ones(4, np.float16)).argmax(0)
+    assert e.value.kind == "ShapeMismatch"
+    with pytest.raises(TLHipError) as e:   # a result of the wrong shape
+        call("tlhip_tensor_argmax", dev.h, t.h, 1, 0, dev.empty((3,)).h)
+    assert e.value.kind == "ShapeMismatch"
+    with pytest.raises(TLHipError) as e:
+        dev.tensor(np.ones((2, 3), np.int32), I32).argmax()
+    assert e.value.kind == "DtypeError"

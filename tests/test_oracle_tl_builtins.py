@@ -245,3 +245,65 @@ def test_einsum_program_composition_is_the_fused_oracle(oracle, acc, S_, H, Hkv,
     out = oracle.einsum_context(p, v, acc)
     fused = oracle.attention(q, k, v, q0, 0.125, True, acc)
     assert np.array_equal(out.view(np.uint16), fused.view(np.uint16))
+
+
+# ---------------------------------------------------------------------------
+# argmax (Tensor::argmax, reduce.rs:585-668)
+# ---------------------------------------------------------------------------
+def test_argmax_reference_known_answers(oracle):
+    # tests/test_reduce_ops.rs:385-398, 418-441, 463-482, 519-525
+    assert oracle.tensor_argmax(h([3, 7, 2, 9, 1])).tolist() == [3.0]
+    assert oracle.tensor_argmax(h([[1, 5, 3], [9, 2, 7]]), 1).tolist() == [1.0, 0.0]
+    assert oracle.tensor_argmax(h([[1, 5], [9, 2]]), 1, True).shape == (2, 1)
+    with pytest.raises(ValueError):
+        oracle.tensor_argmax(h(np.ones((2, 3))), 10)
+
+
+def test_argmax_first_maximum_and_specials(oracle):
+    inf, nan = np.inf, np.nan
+    # ties: the first index; -0 and +0 are equal; NaN never beats anything
+    assert oracle.tensor_argmax(h([1, 4, 4, 2])).tolist() == [1.0]
+    assert oracle.tensor_argmax(h([-0.0, 0.0, -1])).tolist() == [0.0]
+    assert oracle.tensor_argmax(h([1, nan, 3, nan])).tolist() == [2.0]
+    # the whole-tensor scan starts from element 0's value: a NaN there is never beaten
+    assert oracle.tensor_argmax(h([nan, 5, 7])).tolist() == [0.0]
+    # along a dim the scan starts from -inf: NaN and -inf never win, index 0 if nothing does
+    assert oracle.tensor_argmax(h([[nan, 5, 7], [-inf, -inf, nan], [-inf, -3, -inf]]), 1).tolist() == [2.0, 0.0, 1.0]
+    assert oracle.tensor_argmax(np.array([-inf, -inf], np.float32)).tolist() == [0.0]
+    # the index is stored as T::from_f64: f16 rounds to nearest even above 2048
+    x = np.zeros(4000, np.float16)
+    for i, want in ((2049, 2048.0), (3001, 3000.0), (3003, 3004.0), (2047, 2047.0)):
+        x[:] = 0
+        x[i] = 1
+        assert oracle.tensor_argmax(x).tolist() == [want]
+        assert oracle.tensor_argmax(x.astype(np.float32)).tolist() == [float(i)]
+    # reducing the only dim without keepdim: the reference's from_vec([i], []) fails
+    with pytest.raises(ValueError):
+        oracle.tensor_argmax(h([1, 2]), 0)
+    assert oracle.tensor_argmax(h([1, 2]), 0, True).tolist() == [1.0]
+
+
+@pytest.mark.parametrize("shape,dim", [((17,), None), ((6, 9), None), ((6, 9), 0), ((6, 9), 1), ((1, 40), 1),
+                                       ((4, 3, 5), 0), ((4, 3, 5), 1), ((4, 3, 5), 2), ((2, 3, 4, 5), 2),
+                                       ((3, 1, 4), 2), ((5, 2, 3), None)])
+@pytest.mark.parametrize("dt", [np.float16, np.float32])
+def test_argmax_matches_numpy(oracle, shape, dim, dt):
+    """numpy's argmax also returns the first maximum (no NaNs here; -inf
+    entries and all--inf lines included).  The reference lays the results
+    out with the first kept dim varying fastest, i.e. numpy's result array
+    with its axes reversed, flattened, in the kept dims' shape."""
+    rng = np.random.default_rng(len(shape) * 10 + (dim or 0))
+    x = rng.integers(-4, 5, size=shape).astype(dt)   # many ties
+    x[x == -4] = -np.inf
+    if dim is not None and x.ndim > 1:
+        first = [slice(None)] * x.ndim
+        first[0 if dim else -1] = 0
+        x[tuple(first)] = -np.inf   # some lines with nothing above -inf
+    got = oracle.tensor_argmax(x, dim)
+    if dim is None:
+        want = np.array([np.argmax(x.ravel())], np.float64)
+    else:
+        r = np.argmax(x, axis=dim)
+        want = r.transpose(tuple(reversed(range(r.ndim)))).ravel().reshape(r.shape)
+    assert got.shape == want.shape
+    assert np.array_equal(got.astype(np.float64), want.astype(dt).astype(np.float64))
