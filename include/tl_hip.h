@@ -233,8 +233,10 @@ tlhip_status tlhip_temperature_sample(tlhip_ctx ctx, tlhip_tensor logits, float 
  *      eval.rs:1247-1400), preallocated instead of concat-grown ----------- */
 typedef struct tlhip_kvcache_s* tlhip_kvcache;
 /* KVCache::new_f16(n_layers) with room for max_ctx rows of [Hkv, D];
- * max_ctx <= 8192, the most keys the attention entry points read
- * (InvalidDimension beyond).                                              */
+ * max_ctx <= 65536, the most keys the attention entry points read
+ * (InvalidDimension beyond).  The reference grows its cache without a cap
+ * (llama.rs:87-88); past 8192 keys a single query row is attended in key
+ * chunks and several rows on the matrix cores (head dims 64 / 80 / 128).  */
 tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads,
                                   int head_dim, tlhip_kvcache* out);
 tlhip_status tlhip_kvcache_free(tlhip_kvcache c);

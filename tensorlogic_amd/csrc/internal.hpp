@@ -275,8 +275,14 @@ size_t attention_mfma_scratch(int J, int Hkv, int D);
 bool attention_split_ok(const AttnArgs& a);
 size_t attention_split_scratch(int H, int kv_rows, int D);
 tlhip_status launch_attention_split(hipStream_t s, const AttnArgs& a, float* scratch);
+// The same split for one query row over J keys known at launch (no device
+// position; kv_rows is taken as J); scratch of attention_split_scratch(H, J, D).
+bool attention_split_j_ok(const AttnArgs& a, int J);
+tlhip_status launch_attention_split_j(hipStream_t s, const AttnArgs& a, int J, float* scratch);
 tlhip_status launch_attention_mfma(hipStream_t s, const AttnArgs& a, int J, uint16_t* vt);
-constexpr int kAttnMaxKeys = 8192;
+constexpr int kAttnRowKeys = 8192;    // keys the one-workgroup kernels hold in their LDS score row
+constexpr int kAttnMaxKeys = 65536;   // keys any attention entry point reads (longer rows take the
+                                      // key-chunked split for one query row, the matrix cores for more)
 tlhip_status launch_copy_rows(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows,
                               int row_elems, int src_stride, int dst_stride, const int32_t* d_pos,
                               int dst_row0);

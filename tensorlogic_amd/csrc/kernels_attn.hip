@@ -19,7 +19,7 @@
 
 namespace tlhip {
 
-constexpr int ATT_MAX_J = 8192;   // keys held in LDS by the single-pass kernel
+constexpr int ATT_MAX_J = kAttnRowKeys;   // keys held in LDS by the single-pass kernel
 
 __device__ __forceinline__ float bsum(float v, float* red) {
     v = wave_sum<64>(v);
@@ -469,8 +469,10 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
 //                     the sum is not a positive finite number), fp32 P.V
 //                     partials per chunk
 //   3 asplit_combine: the partials summed in chunk order, f16 out.
-// Decode only (one query row, causal, position read on the device); rows
-// are read at min(j, kv_rows - 1), inside the allocation.
+// One query row: the decode step (causal, position read on the device) or
+// a single row over a key count known at launch, which is also how a row
+// attends more keys than the one-workgroup kernels' LDS score row holds
+// (ATT_MAX_J).  Rows are read at min(j, kv_rows - 1), inside the allocation.
 constexpr int AS_CH = 128, AS_NT = 256, AS_NG = AS_NT / 8, AS_U = AS_CH / AS_NG;
 
 struct SplitBufs {
@@ -479,10 +481,11 @@ struct SplitBufs {
     float* sum;    // [H][nch] chunk sums of exp(s - chunk max)
     float* o;      // [H][nch][D] P.V partials
     int nch;
+    int keys;      // keys attended when no device position is given
 };
 
-__device__ __forceinline__ int asplit_keys(const AttnArgs& a) {
-    return min(*a.d_pos + 1, a.kv_rows);
+__device__ __forceinline__ int asplit_keys(const AttnArgs& a, const SplitBufs& b) {
+    return a.d_pos ? min(*a.d_pos + 1, a.kv_rows) : b.keys;
 }
 
 template <int D>
@@ -507,7 +510,7 @@ __global__ __launch_bounds__(AS_NT) void asplit_scores_kernel(AttnArgs a, SplitB
             qf[2 * t + 1] = (float)p2[1];
         }
     }
-    const int J = asplit_keys(a);
+    const int J = asplit_keys(a, b);
     if (j0 >= J) return;   // (uniform: chunk past the keys)
     float mx = -INFINITY, sv[AS_U];
 #pragma unroll
@@ -557,7 +560,7 @@ __global__ __launch_bounds__(AS_NT) void asplit_pv_kernel(AttnArgs a, SplitBufs 
     uint32_t vw[AS_U][NW];
 #pragma unroll
     for (int u = 0; u < AS_U; u++) load_row_words<NW>(vbase + (size_t)min(j0 + g + AS_NG * u, a.kv_rows - 1) * wstride, vw[u]);
-    const int J = asplit_keys(a);
+    const int J = asplit_keys(a, b);
     const int nc = (J + AS_CH - 1) / AS_CH;
     if (ch >= nc) return;
     float gmax = -INFINITY;
@@ -605,16 +608,25 @@ __global__ __launch_bounds__(AS_NT) void asplit_pv_kernel(AttnArgs a, SplitBufs 
 template <int D>
 __global__ __launch_bounds__(D) void asplit_combine_kernel(AttnArgs a, SplitBufs b) {
     const int h = blockIdx.x, tid = threadIdx.x;
-    const int J = asplit_keys(a);
+    const int J = asplit_keys(a, b);
     const int nc = (J + AS_CH - 1) / AS_CH;
     float t = 0.0f;
     for (int k = 0; k < nc; k++) t += b.o[((size_t)h * b.nch + k) * D + tid];
     a.out[(size_t)h * D + tid] = f2h(t);   // (one query row)
 }
 
+// Decode: head dims 80 / 128 from caches of more than 512 rows (one
+// workgroup per head streams too few bytes per CU there); head dim 64 only
+// past the one-workgroup kernel's score row.
 bool attention_split_ok(const AttnArgs& a) {
-    return a.d_pos && a.S == 1 && a.causal && (a.D == 80 || a.D == 128) && a.kv_rows > 512 && a.Hkv > 0 &&
-           a.H % a.Hkv == 0;
+    if (!(a.d_pos && a.S == 1 && a.causal && a.Hkv > 0 && a.H % a.Hkv == 0)) return false;
+    return ((a.D == 80 || a.D == 128) && a.kv_rows > 512) || (a.D == 64 && a.kv_rows > ATT_MAX_J);
+}
+
+// One row over J keys known at launch.
+bool attention_split_j_ok(const AttnArgs& a, int J) {
+    return !a.d_pos && a.S == 1 && J >= 1 && (a.D == 64 || a.D == 80 || a.D == 128) && a.Hkv > 0 &&
+           a.H % a.Hkv == 0 && (!a.causal || a.q_pos0 < J);
 }
 
 size_t attention_split_scratch(int H, int kv_rows, int D) {
@@ -622,17 +634,18 @@ size_t attention_split_scratch(int H, int kv_rows, int D) {
     return ((size_t)H * kv_rows + 2 * (size_t)H * nch + (size_t)H * nch * D) * sizeof(float);
 }
 
-tlhip_status launch_attention_split(hipStream_t s, const AttnArgs& a, float* scratch) {
-    if (!attention_split_ok(a) || !scratch)
-        return fail(TLHIP_ERR_INVALID_ARGUMENT, "attention: split decode path needs a device position, S = 1, D 80/128");
-    SplitBufs b;
+static tlhip_status launch_split(hipStream_t s, const AttnArgs& a, SplitBufs b, float* scratch) {
     b.nch = (a.kv_rows + AS_CH - 1) / AS_CH;
     b.e = scratch;
     b.mx = b.e + (size_t)a.H * a.kv_rows;
     b.sum = b.mx + (size_t)a.H * b.nch;
     b.o = b.sum + (size_t)a.H * b.nch;
     const dim3 grid((unsigned)b.nch, (unsigned)a.H);
-    if (a.D == 80) {
+    if (a.D == 64) {
+        hipLaunchKernelGGL(asplit_scores_kernel<64>, grid, dim3(AS_NT), 0, s, a, b);
+        hipLaunchKernelGGL(asplit_pv_kernel<64>, grid, dim3(AS_NT), 0, s, a, b);
+        hipLaunchKernelGGL(asplit_combine_kernel<64>, dim3((unsigned)a.H), dim3(64), 0, s, a, b);
+    } else if (a.D == 80) {
         hipLaunchKernelGGL(asplit_scores_kernel<80>, grid, dim3(AS_NT), 0, s, a, b);
         hipLaunchKernelGGL(asplit_pv_kernel<80>, grid, dim3(AS_NT), 0, s, a, b);
         hipLaunchKernelGGL(asplit_combine_kernel<80>, dim3((unsigned)a.H), dim3(80), 0, s, a, b);
@@ -642,6 +655,24 @@ tlhip_status launch_attention_split(hipStream_t s, const AttnArgs& a, float* scr
         hipLaunchKernelGGL(asplit_combine_kernel<128>, dim3((unsigned)a.H), dim3(128), 0, s, a, b);
     }
     return TLHIP_OK;
+}
+
+tlhip_status launch_attention_split(hipStream_t s, const AttnArgs& a, float* scratch) {
+    if (!attention_split_ok(a) || !scratch)
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "attention: split decode path needs a device position, S = 1, D 64/80/128");
+    SplitBufs b = {};
+    return launch_split(s, a, b, scratch);
+}
+
+// One row over J keys; scratch holds attention_split_scratch(H, J, D) bytes.
+tlhip_status launch_attention_split_j(hipStream_t s, const AttnArgs& a, int J, float* scratch) {
+    if (!attention_split_j_ok(a, J) || !scratch)
+        return fail(TLHIP_ERR_INVALID_ARGUMENT, "attention: split path needs one query row and D 64/80/128");
+    AttnArgs r = a;
+    r.kv_rows = J;   // rows in k / v
+    SplitBufs b = {};
+    b.keys = a.causal ? min(J, a.q_pos0 + 1) : J;
+    return launch_split(s, r, b, scratch);
 }
 
 // ---------------------------------------------------------------------------
@@ -1453,10 +1484,14 @@ __global__ __launch_bounds__(fa_heads<D>() * 128) void attention_mfma_staged_ker
     fs.run(t0, t1, a.causal && t1 < t0 ? 2 : 1, hh < a.H, stm[hw], sts[hw], ob[hw], ot[hw], votes);
 }
 
+// S >= 128 query rows; fewer take the matrix cores only past the
+// one-workgroup kernels' score row (more than ATT_MAX_J keys), where those
+// kernels cannot run.
 bool attention_mfma_ok(const AttnArgs& a, int J) {
     const int qs = a.q_stride ? a.q_stride : a.H * a.D;
     const int os = a.out_stride ? a.out_stride : a.H * a.D;
-    return a.S >= 128 && J >= 1 && (a.D == 64 || a.D == 80 || a.D == 128) && !a.d_pos && qs % 8 == 0 &&
+    return (a.S >= 128 || (a.S >= 2 && J > ATT_MAX_J)) && J >= 1 && (a.D == 64 || a.D == 80 || a.D == 128) &&
+           !a.d_pos && qs % 8 == 0 &&
            os % 8 == 0 && ((uintptr_t)a.q % 16) == 0 && ((uintptr_t)a.k % 16) == 0 && ((uintptr_t)a.v % 16) == 0 &&
            ((uintptr_t)a.out % 16) == 0;
 }
@@ -1488,7 +1523,6 @@ tlhip_status launch_attention_mfma(hipStream_t s, const AttnArgs& a, int J, uint
     if (!attention_mfma_ok(a, J) || !vt)
         return fail(TLHIP_ERR_INVALID_ARGUMENT, "attention: shape not on the matrix-core path");
     if (a.Hkv <= 0 || a.H % a.Hkv) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: heads %d/%d", a.H, a.Hkv);
-    if (J > ATT_MAX_J) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: %d keys > %d", J, ATT_MAX_J);
     const int Jp = (J + 31) / 32 * 32;
     hipLaunchKernelGGL(vt_transpose_kernel, dim3(Jp / 32, a.Hkv), dim3(256), 0, s, a.v, vt, J, Jp, a.Hkv, a.D);
     const int nqt = (a.S + 31) / 32;

@@ -445,6 +445,8 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
         } else {
             at.q_pos0 = pos0;
             if (attention_mfma_ok(at, pos0 + S)) TLHIP_TRY(launch_attention_mfma(s, at, pos0 + S, m->d_vt));
+            else if (pos0 + S > kAttnRowKeys && m->d_asplit && attention_split_j_ok(at, pos0 + S))
+                TLHIP_TRY(launch_attention_split_j(s, at, pos0 + S, m->d_asplit));   // one row past the score row
             else TLHIP_TRY(launch_attention_j(s, at, pos0 + S));
         }
         if (m->arch == 0) {
@@ -765,6 +767,13 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
             break;
         }
         m->head_dim = m->hidden / m->n_heads;
+        if (max_ctx > kAttnRowKeys && m->head_dim != 64 && m->head_dim != 80 && m->head_dim != 128) {
+            // past the one-workgroup kernels' score row, attention takes the
+            // key-chunked and matrix-core paths, which cover these head dims
+            st = fail(TLHIP_ERR_INVALID_DIMENSION, "max_ctx %d > %d needs head_dim 64, 80 or 128 (got %d)", max_ctx,
+                      kAttnRowKeys, m->head_dim);
+            break;
+        }
         float f;
         if (tlhip_gguf_kv_f32(g, (a + (arch == 0 ? "attention.layer_norm_rms_epsilon" : "attention.layer_norm_epsilon")).c_str(), &f) == TLHIP_OK)
             m->eps = f;

@@ -520,6 +520,17 @@ tlhip_status tlhip_attention(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhi
         const tlhip_status st = launch_attention_mfma(ctx->stream, a, J, (uint16_t*)vt);
         (void)hipFreeAsync(vt, ctx->stream);
         TLHIP_TRY(st);
+    } else if (J > kAttnRowKeys && attention_split_j_ok(a, J)) {
+        // one row past the one-workgroup kernels' score row: key-chunked
+        void* sc = nullptr;
+        TLHIP_CHECK_HIP(hipMallocAsync(&sc, attention_split_scratch(H, J, D), ctx->stream));
+        const tlhip_status st = launch_attention_split_j(ctx->stream, a, J, (float*)sc);
+        (void)hipFreeAsync(sc, ctx->stream);
+        TLHIP_TRY(st);
+    } else if (J > kAttnRowKeys) {
+        return fail(TLHIP_ERR_INVALID_DIMENSION,
+                    "attention: %d keys needs head_dim 64/80/128 and 16-byte aligned rows (more than %d keys)", J,
+                    kAttnRowKeys);
     } else {
         TLHIP_TRY(launch_attention_j(ctx->stream, a, J));
     }

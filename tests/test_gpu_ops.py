@@ -384,6 +384,58 @@ def test_attention(dev, oracle, Sq, J, H, Hkv, D, q0, causal):
     assert_close(got, ref, what=f"attention S={Sq} J={J} D={D} causal={causal}")
 
 
+@pytest.mark.parametrize("Sq,J,H,Hkv,D,causal", [
+    # one row past the one-workgroup kernels' 8,192-key score row: key-chunked split
+    (1, 8193, 8, 2, 64, True), (1, 10000, 32, 4, 64, True), (1, 9000, 4, 4, 80, False), (1, 12345, 8, 2, 128, True),
+    # several rows: the matrix-core path, which has no key cap of its own
+    (2, 8200, 8, 2, 64, True), (46, 10000, 32, 4, 64, True), (130, 9000, 8, 8, 80, True), (5, 8500, 4, 2, 128, False)])
+def test_attention_past_8192_keys(dev, oracle, Sq, J, H, Hkv, D, causal):
+    """Context beyond 8,192 keys (the reference materialises its scores and
+    has no cap): queries at the last Sq positions of J keys."""
+    q = S.normal_f16(31, f"lq{J}", (Sq, H, D))
+    k = S.normal_f16(31, f"lk{J}", (J, Hkv, D))
+    v = S.normal_f16(31, f"lv{J}", (J, Hkv, D))
+    q0 = J - Sq
+    got = attention(dev.tensor(q), dev.tensor(k), dev.tensor(v), q0, 1 / np.sqrt(D), causal).numpy()
+    ref = oracle.attention(q, k, v, q0, 1 / np.sqrt(D), causal)
+    assert_close(got, ref, what=f"attention S={Sq} J={J} D={D} causal={causal}")
+
+
+def test_kvcache_past_8192_keys(dev, oracle):
+    """A KV cache of 9,000 rows: decode rows appended past 8,192 keys attend
+    the whole cache through the key-chunked path."""
+    H, Hkv, D = 8, 2, 64
+    c = KVCache(dev, 1, 9000, Hkv, D)
+    k0, v0 = S.normal_f16(33, "xk0", (8990, Hkv, D)), S.normal_f16(33, "xv0", (8990, Hkv, D))
+    c.set(0, dev.tensor(k0), dev.tensor(v0))
+    ks, vs = [k0], [v0]
+    scale = 1 / np.sqrt(D)
+    for t in range(2):
+        k1, v1 = S.normal_f16(34 + t, "xk", (1, Hkv, D)), S.normal_f16(34 + t, "xv", (1, Hkv, D))
+        q1 = S.normal_f16(34 + t, "xq", (1, H, D))
+        c.append(0, dev.tensor(k1), dev.tensor(v1))
+        ks.append(k1)
+        vs.append(v1)
+        kk, vv = np.concatenate(ks), np.concatenate(vs)
+        got = c.attention(dev.tensor(q1), 0, scale).numpy()
+        assert_close(got, oracle.attention(q1, kk, vv, kk.shape[0] - 1, scale, True), what=f"long cache decode {t}")
+
+
+def test_attention_key_count_limit(dev):
+    """More keys than any entry point reads, and a head dim the long-row paths
+    do not cover, are shape errors (no silent truncation)."""
+    q = dev.tensor(np.zeros((1, 2, 64), np.float16))
+    kv = dev.empty((65537, 1, 64))
+    with pytest.raises(TLHipError) as e:
+        attention(q, kv, kv, 65536)
+    assert e.value.kind == "InvalidDimension"
+    q96 = dev.tensor(np.zeros((1, 2, 96), np.float16))
+    kv96 = dev.empty((9000, 1, 96))
+    with pytest.raises(TLHipError) as e:
+        attention(q96, kv96, kv96, 8999)
+    assert e.value.kind == "InvalidDimension"
+
+
 @pytest.mark.parametrize("Sq,H", [(8, 4), (64, 4), (160, 4), (160, 8), (300, 8)])
 def test_attention_degenerate_rows(dev, oracle, Sq, H):
     """Rows whose every score overflows f16 take the reference softmax's
@@ -545,8 +597,8 @@ def test_kvcache(dev):
 
 
 def test_kvcache_limits(dev):
-    # a cache longer than attention can read is refused at creation
+    # a cache longer than attention can read (65,536 keys) is refused at creation
     with pytest.raises(TLHipError) as e:
-        KVCache(dev, 1, 8193, 4, 64)
+        KVCache(dev, 1, 65537, 1, 64)
     assert e.value.kind == "InvalidDimension"
-    KVCache(dev, 1, 8192, 4, 64)
+    KVCache(dev, 1, 65536, 1, 64)
