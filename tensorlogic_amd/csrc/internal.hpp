@@ -119,6 +119,7 @@ tlhip_status after_launch(tlhip_ctx ctx, const char* op);
 tlhip_status alloc_tensor(tlhip_ctx ctx, tlhip_dtype dtype, int ndim, const int64_t* shape,
                           tlhip_tensor* out);
 
+float* ctx_workspace(tlhip_ctx ctx, size_t need);   // the context's grown device workspace (null: none)
 // linear(x, W[, b]) behind tlhip_linear (fixed_ws = nullptr: split-K
 // partials and the Q6_K f16 copy come from the stream-ordered pool) and
 // tlhip_linear_noalloc (fixed_ws = a workspace of fixed_ws_bytes that the

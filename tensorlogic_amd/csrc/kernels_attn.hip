@@ -462,9 +462,9 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
 //                     chunk's max m_c over finite scores and its sum of
 //                     exp(s_j - m_c)
 //   2 asplit_pv     : global max M = max m_c (0 when none is finite), global
-//                     sum = sum_c sum_c * exp(m_c - M) in chunk order (the
-//                     reference's sum of exp(s_j - M), re-associated: ~1e-7
-//                     relative), e_j = f16(exp(s_j - M)) (0 for non-finite
+//                     sum = sum_c sum_c * exp(m_c - M) in a fixed tree order
+//                     (the reference's sum of exp(s_j - M), re-associated:
+//                     ~1e-7 relative), e_j = f16(exp(s_j - M)) (0 for non-finite
 //                     s_j), P_j = f16(e_j / sum) (the uniform f16(1/J) when
 //                     the sum is not a positive finite number), fp32 P.V
 //                     partials per chunk
@@ -552,6 +552,7 @@ template <int D>
 __global__ __launch_bounds__(AS_NT) void asplit_pv_kernel(AttnArgs a, SplitBufs b) {
     constexpr int EPL = D / 8, NW = EPL / 2, NWV = AS_NT / 64;
     __shared__ float part[NWV][D];
+    __shared__ float red[2][NWV];
     const int ch = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, c = tid & 7, g = tid >> 3;
     const int kvh = h / (a.H / a.Hkv);
     const size_t wstride = (size_t)a.Hkv * D / 2;
@@ -563,14 +564,19 @@ __global__ __launch_bounds__(AS_NT) void asplit_pv_kernel(AttnArgs a, SplitBufs 
     const int J = asplit_keys(a, b);
     const int nc = (J + AS_CH - 1) / AS_CH;
     if (ch >= nc) return;
+    // the chunk statistics, loaded by every thread at once (a loop of
+    // dependent loads over the chunks cost one L2 round trip per chunk), then
+    // combined in a fixed tree order
     float gmax = -INFINITY;
-    for (int k = 0; k < nc; k++) gmax = fmaxf(gmax, b.mx[(size_t)h * b.nch + k]);
+    for (int k = tid; k < nc; k += AS_NT) gmax = fmaxf(gmax, b.mx[(size_t)h * b.nch + k]);
+    gmax = block_max1<NWV>(gmax, red[0]);
     if (!isfinite(gmax)) gmax = 0.0f;
     float gsum = 0.0f;
-    for (int k = 0; k < nc; k++) {
+    for (int k = tid; k < nc; k += AS_NT) {
         const float mk = b.mx[(size_t)h * b.nch + k];
         if (isfinite(mk)) gsum += b.sum[(size_t)h * b.nch + k] * expf(mk - gmax);
     }
+    gsum = block_sum1<NWV>(gsum, red[1]);
     const bool degenerate = !(gsum > 0.0f && isfinite(gsum));
     const float uni = h2f(f2h(1.0f / (float)J));
     float o[EPL];
@@ -610,8 +616,18 @@ __global__ __launch_bounds__(D) void asplit_combine_kernel(AttnArgs a, SplitBufs
     const int h = blockIdx.x, tid = threadIdx.x;
     const int J = asplit_keys(a, b);
     const int nc = (J + AS_CH - 1) / AS_CH;
+    // chunk order, 16 loads in flight at a time
+    const float* po = b.o + (size_t)h * b.nch * D + tid;
     float t = 0.0f;
-    for (int k = 0; k < nc; k++) t += b.o[((size_t)h * b.nch + k) * D + tid];
+    int k = 0;
+    for (; k + 16 <= nc; k += 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = po[(size_t)(k + u) * D];
+#pragma unroll
+        for (int u = 0; u < 16; u++) t += v[u];
+    }
+    for (; k < nc; k++) t += po[(size_t)k * D];
     a.out[(size_t)h * D + tid] = f2h(t);   // (one query row)
 }
 

@@ -58,6 +58,24 @@ tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_t
 
 namespace tlhip {
 
+// The context's device workspace (split-K partials, attention scratch),
+// grown stream-ordered when a call needs more, so steady-state calls
+// allocate nothing; null when it cannot grow.  Calls on the context's
+// stream use it one after another.
+float* ctx_workspace(tlhip_ctx ctx, size_t need) {
+    if (need > ctx->ws_bytes) {
+        void* grown = nullptr;
+        if (hipMallocAsync(&grown, need, ctx->stream) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        if (ctx->d_ws) (void)hipFreeAsync(ctx->d_ws, ctx->stream);   // after the calls that used it
+        ctx->d_ws = (float*)grown;
+        ctx->ws_bytes = need;
+    }
+    return ctx->d_ws;
+}
+
 tlhip_status linear_impl(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y,
                          float* fixed_ws, size_t fixed_ws_bytes) {
     TLHIP_TRY(check_ctx(ctx));
@@ -136,18 +154,8 @@ tlhip_status linear_impl(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_te
         a.ws = fixed_ws;
         a.ws_bytes = need;
     } else if (sp > 1) {
-        if (need > ctx->ws_bytes) {
-            void* grown = nullptr;
-            if (hipMallocAsync(&grown, need, ctx->stream) == hipSuccess) {
-                if (ctx->d_ws) (void)hipFreeAsync(ctx->d_ws, ctx->stream);   // after the GEMMs that used it
-                ctx->d_ws = (float*)grown;
-                ctx->ws_bytes = need;
-            } else {
-                (void)hipGetLastError();   // no workspace: the GEMM runs unsplit
-            }
-        }
-        if (need <= ctx->ws_bytes) {
-            a.ws = ctx->d_ws;
+        if (float* ws = ctx_workspace(ctx, need)) {   // (none: the GEMM runs unsplit)
+            a.ws = ws;
             a.ws_bytes = need;
         }
     }
@@ -515,18 +523,18 @@ tlhip_status tlhip_attention(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhi
     a.causal = causal;
     a.scale_h = round_f16(scale);
     if (attention_mfma_ok(a, J)) {
-        void* vt = nullptr;
-        TLHIP_CHECK_HIP(hipMallocAsync(&vt, attention_mfma_scratch(J, Hkv, D), ctx->stream));
-        const tlhip_status st = launch_attention_mfma(ctx->stream, a, J, (uint16_t*)vt);
-        (void)hipFreeAsync(vt, ctx->stream);
-        TLHIP_TRY(st);
-    } else if (J > kAttnRowKeys && attention_split_j_ok(a, J)) {
-        // one row past the one-workgroup kernels' score row: key-chunked
-        void* sc = nullptr;
-        TLHIP_CHECK_HIP(hipMallocAsync(&sc, attention_split_scratch(H, J, D), ctx->stream));
-        const tlhip_status st = launch_attention_split_j(ctx->stream, a, J, (float*)sc);
-        (void)hipFreeAsync(sc, ctx->stream);
-        TLHIP_TRY(st);
+        float* vt = ctx_workspace(ctx, attention_mfma_scratch(J, Hkv, D));
+        if (!vt) return fail(TLHIP_ERR_ALLOCATION, "attention: no workspace for V^T (%zu bytes)", attention_mfma_scratch(J, Hkv, D));
+        TLHIP_TRY(launch_attention_mfma(ctx->stream, a, J, (uint16_t*)vt));
+    } else if (attention_split_j_ok(a, J) && (J > kAttnRowKeys || J > (D == 64 ? 1024 : 512))) {
+        // one row over many keys: key-chunked (more workgroups than the one
+        // per head of the one-row kernels; measured faster on MI355X past
+        // ~1,024 keys at head dim 64 and ~512 at 80 / 128), and the only path
+        // past their score row
+        float* sc = ctx_workspace(ctx, attention_split_scratch(H, J, D));
+        if (sc) TLHIP_TRY(launch_attention_split_j(ctx->stream, a, J, sc));
+        else if (J > kAttnRowKeys) return fail(TLHIP_ERR_ALLOCATION, "attention: no workspace for the key chunks");
+        else TLHIP_TRY(launch_attention_j(ctx->stream, a, J));
     } else if (J > kAttnRowKeys) {
         return fail(TLHIP_ERR_INVALID_DIMENSION,
                     "attention: %d keys needs head_dim 64/80/128 and 16-byte aligned rows (more than %d keys)", J,
