@@ -129,7 +129,11 @@ tlhip_status tlhip_dequantize(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor out_f1
  * the fused dequant-GEMV, larger M the MFMA dequant-GEMM (a Q6_K weight
  * keeps the dequantised f16 copy that GEMM reads, 2 bytes per weight, from
  * its first use with M > 4 until it is freed or re-uploaded).  bias may be
- * NULL.                                                                   */
+ * NULL.  The TensorF32 arm (builtin_math.rs:121-175): x, W, bias and y all
+ * F32, each output the sum of the reference's f32 kernel
+ * (matmul_transposed_b_tiled_32x32_f32, unified.metal:4409-4461: k in
+ * order, one fused multiply-add per term, zero terms to a multiple of 32)
+ * plus the bias; f16 mixed with f32 is a DtypeError.                      */
 tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y);
 /* linear(x, W[, b]) exactly as tlhip_linear (same checks, kernels and bits),
  * but allocating nothing: no counterpart in the reference.  It is for
@@ -239,6 +243,12 @@ typedef struct tlhip_kvcache_s* tlhip_kvcache;
  * chunks and several rows on the matrix cores (head dims 64 / 80 / 128).  */
 tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads,
                                   int head_dim, tlhip_kvcache* out);
+/* KVCache::new_f32(n_layers) (eval.rs:942; set / append / get_k / get_v at
+ * eval.rs:1302,1422,1506,1582): the same cache holding f32 rows; its set /
+ * append take f32 K, V and get returns f32 views.  The attention entry
+ * points below are f16 (a DtypeError on an f32 cache).                    */
+tlhip_status tlhip_kvcache_create_f32(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads,
+                                      int head_dim, tlhip_kvcache* out);
 tlhip_status tlhip_kvcache_free(tlhip_kvcache c);
 /* cache.set(layer, K, V): replaces the layer's contents with K,V [S,Hkv,D]
  * (K and V of the same shape, else ShapeMismatch).                       */

@@ -84,6 +84,7 @@ def _declare(L):
         "tlo_embedding": (i, [vp, i, i, vp, i, vp]),
         "tlo_causal_mask": (None, [i, vp]),
         "tlo_slice_last": (i, [vp, vp, i, i, i, vp]),
+        "tlo_linear_f32": (None, [vp, vp, vp, i, i, i, vp]),
         "tlo_tensor_argmax": (C.c_int64, [vp, vp, i, i, vp]),
         "tlo_broadcast_to": (i, [vp, vp, i, vp, i, i, vp]),
         "tlo_rope_cos_sin": (i, [vp, i, i, i, vp, vp, i, vp]),
@@ -151,6 +152,18 @@ def linear(x, w, bias=None, acc=ACC_F32) -> np.ndarray:
     N = w.shape[0]
     y = np.empty((M, N), np.float16)
     lib().tlo_linear_f16(_p(x), _p(w), _p(_h(bias)) if bias is not None else None, M, N, K, acc, _p(y))
+    return y
+
+
+def linear_f32(x, w, bias=None) -> np.ndarray:
+    """linear() on f32 operands: the reference f32 kernel's fused sums."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    M, K = x.shape
+    N = w.shape[0]
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    y = np.empty((M, N), np.float32)
+    lib().tlo_linear_f32(_p(x), _p(w), _p(b) if b is not None else None, M, N, K, _p(y))
     return y
 
 

@@ -205,6 +205,20 @@ static void linear_rows_f32w(const float* xf, const float* wf, const uint16_t* b
     }
 }
 
+void tlo_linear_f32(const float* x, const float* w, const float* bias, int M, int N, int K, float* y) {
+    const int kp = (K + 31) / 32 * 32;   /* the kernel's 32-wide tiles, zero-padded */
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            float sum = 0.0f;
+            for (int k = 0; k < kp; k++) {
+                const float a = k < K ? x[(size_t)m * K + k] : 0.0f;
+                const float b = k < K ? w[(size_t)n * K + k] : 0.0f;
+                sum = fmaf(a, b, sum);
+            }
+            y[(size_t)m * N + n] = bias ? sum + bias[n] : sum;
+        }
+}
+
 void tlo_linear_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                     int M, int N, int K, int acc_mode, uint16_t* y) {
     lut_init();

@@ -68,6 +68,14 @@ void tlo_dequant_q6_k(const uint8_t* blocks, size_t nblocks, uint16_t* out);
  *   CPU: matmul.rs:293-297 -> matmul_cpu matmul.rs:201-228 (f16 accumulate)
  * Bias, when given, is a separate f16 add of the stored product
  *   (builtin_math.rs:76-131: linear(x, W, b) = add(matmul, b)).            */
+/* linear() on TensorF32 operands (builtin_math.rs:121-175) =
+ * matmul_transposed_b_tiled_32x32_f32 (unified.metal:4409-4461) + add(bias):
+ * y[m][n] = (sum over k = 0 .. ceil32(K) - 1, from +0, of fmaf(x[m][k],
+ * w[n][k], sum), zero terms past K) + bias[n].  The one fused multiply-add
+ * per term is the contraction Metal's default fast math makes of the
+ * kernel's `sum += A * B`; the reference's CPU branch (matmul.rs:201-228)
+ * rounds the product and the sum separately.  bias may be NULL.            */
+void tlo_linear_f32(const float* x, const float* w, const float* bias, int M, int N, int K, float* y);
 void tlo_linear_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                     int M, int N, int K, int acc_mode, uint16_t* y);
 /* Same product with W given as packed GGUF blocks (dequantised row by row

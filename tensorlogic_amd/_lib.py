@@ -85,6 +85,7 @@ SIGNATURES = {
     "tlhip_tensor_argmax": (_i, [_vp, _vp, _i, _i, _vp]),
     "tlhip_temperature_sample": (_i, [_vp, _vp, _f, C.c_uint64, C.c_uint64, _i32p]),
     "tlhip_kvcache_create": (_i, [_vp, _i, _i, _i, _i, C.POINTER(_vp)]),
+    "tlhip_kvcache_create_f32": (_i, [_vp, _i, _i, _i, _i, C.POINTER(_vp)]),
     "tlhip_kvcache_free": (_i, [_vp]),
     "tlhip_kvcache_set": (_i, [_vp, _vp, _i, _vp, _vp]),
     "tlhip_kvcache_append": (_i, [_vp, _vp, _i, _vp, _vp]),

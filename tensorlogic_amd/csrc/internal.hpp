@@ -195,6 +195,9 @@ int gemv_norm_slots(int N);   // workgroups (= argmax keys) of the normalised GE
 tlhip_status launch_argmax_slots(hipStream_t s, const unsigned long long* slots, int n, int32_t* out,
                                  int32_t* token_log, int32_t* d_state);
 tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int epi);
+// y[M,N] = x[M,K] . w[N,K]^T (+ bias[N]) on f32 tensors (linear()'s TensorF32 arm)
+tlhip_status launch_linear_f32(hipStream_t s, const float* x, const float* w, const float* bias, float* y, int M, int N,
+                               int K);
 bool gemm_skinny_ok(int M, int N, int K, int wt);   // the skinny M <= 64 GEMM takes the shape (and EPI_QKV_ROPE)
 int gemm_splits(int M, int N, int K, int wt);   // split-K slices launch_gemm uses when given a workspace
                                                 // (wt < 0: any weight type, the largest count)

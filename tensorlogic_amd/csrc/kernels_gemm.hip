@@ -1240,4 +1240,75 @@ tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
     return TLHIP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// linear() on f32 tensors (the TensorF32 arm, builtin_math.rs:121-175:
+// x.matmul_transposed_b(w), then result.add(bias)).  Every output is the
+// reference kernel's sum (matmul_transposed_b_tiled_32x32_f32,
+// unified.metal:4409-4461): k in order from +0, one fused multiply-add per
+// term (the contraction Metal's default fast math makes of `sum += a * b`),
+// the row padded with zero terms to a multiple of 32 as its tiles are; the
+// bias is a separate f32 add.  A workgroup of 256 threads computes a 64 x 64
+// tile, 4 x 4 outputs per thread, from 64 x 32 slices of x and w staged
+// k-major in LDS.  Not on the decode path (the LLM programs are f16): plain
+// VALU arithmetic, no MFMA (v_mfma_f32_*_xf32 would change the sums' order).
+// ---------------------------------------------------------------------------
+constexpr int LF_BM = 64, LF_BN = 64, LF_BK = 32;
+
+__global__ __launch_bounds__(256) void linear_f32_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                         const float* __restrict__ bias, float* __restrict__ y, int M,
+                                                         int N, int K) {
+    __shared__ float as[LF_BK][LF_BM + 4];
+    __shared__ float bs[LF_BK][LF_BN + 4];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int m0 = blockIdx.y * LF_BM, n0 = blockIdx.x * LF_BN;
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
+    const int kp = (K + LF_BK - 1) / LF_BK * LF_BK;   // zero terms up to a multiple of 32
+    for (int k0 = 0; k0 < kp; k0 += LF_BK) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {   // 64 rows x 32 k of each operand, 8 per thread
+            const int idx = tid + 256 * i, r = idx >> 5, c = idx & 31;
+            const int k = k0 + c;
+            as[c][r] = (m0 + r < M && k < K) ? x[(size_t)(m0 + r) * K + k] : 0.0f;
+            bs[c][r] = (n0 + r < N && k < K) ? w[(size_t)(n0 + r) * K + k] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll 8
+        for (int kk = 0; kk < LF_BK; kk++) {
+            float a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) a[i] = as[kk][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; j++) b[j] = bs[kk][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int m = m0 + ty * 4 + i;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int n = n0 + tx * 4 + j;
+            if (n < N) y[(size_t)m * N + n] = bias ? acc[i][j] + bias[n] : acc[i][j];
+        }
+    }
+}
+
+tlhip_status launch_linear_f32(hipStream_t s, const float* x, const float* w, const float* bias, float* y, int M, int N,
+                               int K) {
+    if (M <= 0 || N <= 0) return TLHIP_OK;
+    const dim3 grid((unsigned)((N + LF_BN - 1) / LF_BN), (unsigned)((M + LF_BM - 1) / LF_BM));
+    if (grid.y > 65535) return fail(TLHIP_ERR_INVALID_DIMENSION, "linear f32: %d rows", M);
+    hipLaunchKernelGGL(linear_f32_kernel, grid, dim3(256), 0, s, x, w, bias, y, M, N, K);
+    return TLHIP_OK;
+}
+
 }  // namespace tlhip

@@ -33,6 +33,7 @@ using namespace tlhip;
 
 struct tlhip_kvcache_s {
     tlhip_ctx ctx = nullptr;
+    tlhip_dtype dtype = TLHIP_F16;   // KVCache::new_f16 / new_f32
     int n_layers = 0, max_ctx = 0, n_kv = 0, head_dim = 0;
     std::vector<tlhip_tensor> k, v;
     std::vector<int> len;
@@ -568,8 +569,8 @@ extern "C" {
 // ---------------------------------------------------------------------------
 // KV cache
 // ---------------------------------------------------------------------------
-tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads, int head_dim,
-                                  tlhip_kvcache* out) {
+static tlhip_status kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads, int head_dim,
+                                   tlhip_dtype dtype, tlhip_kvcache* out) {
     TLHIP_TRY(check_ctx(ctx));
     if (!out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null output");
     *out = nullptr;
@@ -582,6 +583,7 @@ tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int 
                     kAttnMaxKeys);
     auto* c = new tlhip_kvcache_s();
     c->ctx = ctx;
+    c->dtype = dtype;
     c->n_layers = n_layers;
     c->max_ctx = max_ctx;
     c->n_kv = n_kv_heads;
@@ -590,8 +592,8 @@ tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int 
     int64_t shp[3] = {max_ctx, n_kv_heads, head_dim};
     for (int i = 0; i < n_layers; i++) {
         tlhip_tensor k = nullptr, v = nullptr;
-        tlhip_status st = alloc_tensor(ctx, TLHIP_F16, 3, shp, &k);
-        if (st == TLHIP_OK) st = alloc_tensor(ctx, TLHIP_F16, 3, shp, &v);
+        tlhip_status st = alloc_tensor(ctx, dtype, 3, shp, &k);
+        if (st == TLHIP_OK) st = alloc_tensor(ctx, dtype, 3, shp, &v);
         if (st != TLHIP_OK) {
             tlhip_tensor_free(k);
             tlhip_kvcache_free(c);
@@ -602,6 +604,16 @@ tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int 
     }
     *out = c;
     return TLHIP_OK;
+}
+
+tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads, int head_dim,
+                                  tlhip_kvcache* out) {
+    return kvcache_create(ctx, n_layers, max_ctx, n_kv_heads, head_dim, TLHIP_F16, out);
+}
+
+tlhip_status tlhip_kvcache_create_f32(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads, int head_dim,
+                                      tlhip_kvcache* out) {
+    return kvcache_create(ctx, n_layers, max_ctx, n_kv_heads, head_dim, TLHIP_F32, out);
 }
 
 tlhip_status tlhip_kvcache_free(tlhip_kvcache c) {
@@ -617,8 +629,8 @@ static tlhip_status kv_write(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_te
     if (!c || layer < 0 || layer >= c->n_layers) return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "kvcache layer %d", layer);
     TLHIP_TRY(check_t(k, "kvcache K"));
     TLHIP_TRY(check_t(v, "kvcache V"));
-    TLHIP_TRY(check_dtype(k, TLHIP_F16, "kvcache"));
-    TLHIP_TRY(check_dtype(v, TLHIP_F16, "kvcache"));
+    TLHIP_TRY(check_dtype(k, c->dtype, "kvcache"));
+    TLHIP_TRY(check_dtype(v, c->dtype, "kvcache"));
     const int64_t row = (int64_t)c->n_kv * c->head_dim;
     // K and V must have the same shape: same element count alone would let a
     // V of another layout (e.g. [S, D, Hkv]) be stored as if it were [S, Hkv, D]
@@ -630,8 +642,10 @@ static tlhip_status kv_write(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_te
     const int start = append ? c->len[layer] : 0;
     if (start + S > c->max_ctx)
         return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "kvcache: %d + %d rows > %d", start, S, c->max_ctx);
-    TLHIP_TRY(launch_copy_rows(ctx->stream, P(k), P(c->k[layer]), S, (int)row, (int)row, (int)row, nullptr, start));
-    TLHIP_TRY(launch_copy_rows(ctx->stream, P(v), P(c->v[layer]), S, (int)row, (int)row, (int)row, nullptr, start));
+    // (rows copied as 16-bit units: an f32 row is twice as many)
+    const int ru = (int)row * (c->dtype == TLHIP_F32 ? 2 : 1);
+    TLHIP_TRY(launch_copy_rows(ctx->stream, P(k), P(c->k[layer]), S, ru, ru, ru, nullptr, start));
+    TLHIP_TRY(launch_copy_rows(ctx->stream, P(v), P(c->v[layer]), S, ru, ru, ru, nullptr, start));
     c->len[layer] = start + S;
     return after_launch(ctx, append ? "kvcache_append" : "kvcache_set");
 }

@@ -76,9 +76,35 @@ float* ctx_workspace(tlhip_ctx ctx, size_t need) {
     return ctx->d_ws;
 }
 
+// linear() on TensorF32 operands (builtin_math.rs:121-175): x [M, K], w [N, K],
+// bias [N] and y [M, N] all f32; a mix of f16 and f32 is the reference's
+// TypeError (a dtype error here).
+static tlhip_status linear_f32(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y) {
+    TLHIP_TRY(check_t(w, "linear weight"));
+    TLHIP_TRY(check_t(y, "linear output"));
+    if (w->dtype != TLHIP_F32 || y->dtype != TLHIP_F32 || (bias && bias->dtype != TLHIP_F32))
+        return fail(TLHIP_ERR_DTYPE, "linear(): f32 input needs f32 weight, bias and output");
+    if (x->ndim != 2 || w->ndim != 2)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "matmul_transposed_b requires 2D tensors");
+    const int64_t M = x->shape[0], K = x->shape[1], N = w->shape[0];
+    if (w->shape[1] != K)
+        return fail(TLHIP_ERR_INVALID_OPERATION, "matmul_transposed_b shape mismatch: [%lld, %lld] @ [%lld, %lld].T",
+                    (long long)M, (long long)K, (long long)N, (long long)w->shape[1]);
+    if (y->ndim != 2 || y->shape[0] != M || y->shape[1] != N)
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "linear: output %s for [%lld, %lld]", shape_str(y).c_str(),
+                    (long long)M, (long long)N);
+    if (bias && (bias->ndim != 1 || bias->shape[0] != N))
+        return fail(TLHIP_ERR_SHAPE_MISMATCH, "linear: bias %s for %lld outputs", shape_str(bias).c_str(), (long long)N);
+    if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return fail(TLHIP_ERR_INVALID_DIMENSION, "linear: too large");
+    TLHIP_TRY(launch_linear_f32(ctx->stream, (const float*)x->data, (const float*)w->data,
+                                bias ? (const float*)bias->data : nullptr, (float*)y->data, (int)M, (int)N, (int)K));
+    return after_launch(ctx, "linear");
+}
+
 tlhip_status linear_impl(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y,
                          float* fixed_ws, size_t fixed_ws_bytes) {
     TLHIP_TRY(check_ctx(ctx));
+    if (x && check_t(x, "linear") == TLHIP_OK && x->dtype == TLHIP_F32) return linear_f32(ctx, x, w, bias, y);
     TLHIP_TRY(f16_args("linear", {x, y}));
     TLHIP_TRY(check_t(w, "linear weight"));
     if (w->dtype != TLHIP_F16 && !is_quant(w->dtype))

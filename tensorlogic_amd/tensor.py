@@ -141,9 +141,11 @@ class Tensor:
         return self.linear(w)
 
     def linear(self, w: "Tensor", bias: "Tensor | None" = None) -> "Tensor":
+        """linear(x, W[, b]) (builtin_math.rs:76-175): f16 (W f16 or quantized)
+        or, all operands F32, the TensorF32 arm; the output has x's dtype."""
         M = self.shape[0] if len(self.shape) == 2 else -1
         N = w.shape[0]
-        out = self._new((max(M, 0), N)) if M >= 0 else self._new((1, N))
+        out = self.dev.empty((max(M, 0), N) if M >= 0 else (1, N), F32 if self.dtype == F32 else F16)
         call("tlhip_linear", self.dev.h, self.h, w.h, bias.h if bias is not None else None, out.h)
         return out
 
@@ -340,12 +342,15 @@ def temperature_sample(logits: Tensor, temperature: float, seed: int = 0, counte
 
 
 class KVCache:
-    """KVCache::new_f16 with a preallocated device buffer per layer."""
+    """KVCache::new_f16 (or, dtype F32, KVCache::new_f32) with a
+    preallocated device buffer per layer."""
 
-    def __init__(self, dev: Device, n_layers: int, max_ctx: int, n_kv_heads: int, head_dim: int):
+    def __init__(self, dev: Device, n_layers: int, max_ctx: int, n_kv_heads: int, head_dim: int,
+                 dtype: int = F16):
         self.dev = dev
         h = _vp()
-        call("tlhip_kvcache_create", dev.h, n_layers, max_ctx, n_kv_heads, head_dim, C.byref(h))
+        fn = "tlhip_kvcache_create_f32" if dtype == F32 else "tlhip_kvcache_create"
+        call(fn, dev.h, n_layers, max_ctx, n_kv_heads, head_dim, C.byref(h))
         self.h = h
 
     def __del__(self):

@@ -245,6 +245,54 @@ def test_linear_one_row_bias(dev, oracle, qt, N, K):
     assert_close(got, ref, what=f"one-row linear + bias {qt} {N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K,with_bias", [(1, 64, 64, False), (3, 100, 37, True), (46, 256, 2048, True),
+                                             (130, 96, 200, False), (64, 65, 33, True), (1, 2048, 5632, False)])
+def test_linear_f32(dev, oracle, M, N, K, with_bias):
+    """linear() on TensorF32 operands: the reference f32 kernel's fused sums
+    in k order and the separate bias add, bit for bit."""
+    from tensorlogic_amd import F32
+    rng = np.random.default_rng(M * 7 + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (0.05 * rng.standard_normal((N, K))).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32) if with_bias else None
+    got = dev.tensor(x, F32).linear(dev.tensor(w, F32), dev.tensor(b, F32) if with_bias else None).numpy()
+    want = oracle.linear_f32(x, w, b)
+    assert got.dtype == np.float32
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_linear_f32_dtype_mix_is_an_error(dev):
+    from tensorlogic_amd import F32
+    x32 = dev.tensor(np.ones((2, 32), np.float32), F32)
+    with pytest.raises(TLHipError) as e:
+        x32.linear(dev.tensor(np.ones((4, 32), np.float16)))
+    assert e.value.kind == "DtypeError"
+    with pytest.raises(TLHipError) as e:
+        x32.linear(dev.tensor(np.ones((4, 31), np.float32), F32))
+    assert e.value.kind == "InvalidOperation"
+
+
+def test_kvcache_f32(dev):
+    """KVCache::new_f32: set / append / get_k / get_v on f32 rows, bit for
+    bit; an f16 row is refused, and so is attention over the f32 cache."""
+    from tensorlogic_amd import F32
+    c = KVCache(dev, 2, 16, 2, 8, dtype=F32)
+    rng = np.random.default_rng(3)
+    k0, v0 = rng.standard_normal((5, 2, 8)).astype(np.float32), rng.standard_normal((5, 2, 8)).astype(np.float32)
+    k1, v1 = rng.standard_normal((2, 2, 8)).astype(np.float32), rng.standard_normal((2, 2, 8)).astype(np.float32)
+    c.set(1, dev.tensor(k0, F32), dev.tensor(v0, F32))
+    c.append(1, dev.tensor(k1, F32), dev.tensor(v1, F32))
+    gk, gv = c.get_k(1).numpy(), c.get_v(1).numpy()
+    assert gk.dtype == np.float32 and gk.shape == (7, 2, 8)
+    assert np.array_equal(gk, np.concatenate([k0, k1])) and np.array_equal(gv, np.concatenate([v0, v1]))
+    with pytest.raises(TLHipError) as e:
+        c.append(1, dev.tensor(k1), dev.tensor(v1))
+    assert e.value.kind == "DtypeError"
+    with pytest.raises(TLHipError) as e:
+        c.attention(dev.tensor(rng.standard_normal((1, 4, 8)).astype(np.float32), F32), 1, 0.35)
+    assert e.value.kind == "DtypeError"
+
+
 def test_matmul_known_answer(dev):
     # tests/test_gpu_operations.rs:81-94: [[1,2],[3,4]] @ [[5,6],[7,8]]
     a = dev.tensor(np.array([[1, 2], [3, 4]], np.float16))

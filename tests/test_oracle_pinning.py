@@ -267,6 +267,42 @@ def test_linear_reversed_fp32_order(oracle):
     assert ulps(a, b).max() <= 2
 
 
+def test_linear_f32_fused_sums(oracle):
+    """linear() on f32 operands: one fused multiply-add per term in k order
+    over the kernel's zero-padded 32-wide tiles, then the bias add.
+    (1) Small integers: every product and partial sum is exact, so the result
+    is numpy's integer matmul whatever the order or fusion -- a transposed
+    operand, a dropped term or a wrong bias index fails.  (2) Values on a
+    2^-12 grid in [-4, 4]: products need up to 29 bits, so a separately
+    rounded product and a fused one differ, while a float64 running sum of
+    f32 partials plus the exact product is exact, and rounding it to f32
+    once per step is the fused multiply-add -- the oracle equals that
+    emulation bit for bit and differs somewhere from the unfused order."""
+    rng = np.random.default_rng(41)
+    xi = rng.integers(-7, 8, size=(5, 37)).astype(np.float32)
+    wi = rng.integers(-7, 8, size=(9, 37)).astype(np.float32)
+    bi = rng.integers(-50, 51, size=9).astype(np.float32)
+    want = (xi.astype(np.int64) @ wi.astype(np.int64).T + bi.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(oracle.linear_f32(xi, wi, bi), want)
+    assert np.array_equal(oracle.linear_f32(xi, wi), (xi.astype(np.int64) @ wi.astype(np.int64).T).astype(np.float32))
+    x = (rng.integers(-2 ** 14, 2 ** 14, size=(4, 45)) * 2.0 ** -12).astype(np.float32)
+    w = (rng.integers(-2 ** 14, 2 ** 14, size=(6, 45)) * 2.0 ** -12).astype(np.float32)
+    got = oracle.linear_f32(x, w)
+    fused = np.zeros((4, 6), np.float32)
+    unfused = np.zeros((4, 6), np.float32)
+    for m in range(4):
+        for n in range(6):
+            sf = su = np.float32(0.0)
+            for k in range(64):   # 45 terms padded to two 32-wide tiles
+                a = float(x[m, k]) if k < 45 else 0.0
+                b = float(w[n, k]) if k < 45 else 0.0
+                sf = np.float32(float(sf) + a * b)
+                su = np.float32(su + np.float32(a * b))
+            fused[m, n], unfused[m, n] = sf, su
+    assert np.array_equal(got.view(np.uint32), fused.view(np.uint32))
+    assert not np.array_equal(fused.view(np.uint32), unfused.view(np.uint32))
+
+
 # ---------------------------------------------------------------------------
 # RMSNorm (normalization.rs:199-250, unified.metal:1785-1831)
 # ---------------------------------------------------------------------------
