@@ -261,6 +261,22 @@ def _host_cpu():
     return name, os.cpu_count(), len(os.sched_getaffinity(0))
 
 
+def _child_processes() -> list:
+    """Live child processes of this one (from /proc): bench.py starts none
+    of its own -- the CPU leg's OpenMP pool is threads, and the oracle's
+    `make` runs only when liboracle.so is missing and is waited for -- so
+    this is the evidence, reported in the JSON line, that nothing it started
+    outlives it."""
+    kids = []
+    try:
+        for task in os.listdir(f"/proc/{os.getpid()}/task"):
+            with open(f"/proc/{os.getpid()}/task/{task}/children") as f:
+                kids += [int(p) for p in f.read().split()]
+    except OSError:
+        return []
+    return sorted(set(kids))
+
+
 def _time_call(fn, min_s: float = 0.3):
     """Seconds per call: repeats fn until min_s has passed (one call if slower)."""
     n, t0 = 0, time.perf_counter()
@@ -473,6 +489,9 @@ def main():
             pass
 
     weights_per_token = 544997376 + 36864000
+    kids = _child_processes()
+    if kids:
+        log(f"child processes still running at the end: {kids}")
     result = {
         "metric": "decode tok/s TinyLlama-1.1B-shape Q4_0 @1 GPU; Q4_0 GEMV HBM GB/s (% peak)",
         "value": round(tok_s, 2),
@@ -520,6 +539,7 @@ def main():
             "traffic": pmc_traffic(),
         },
         "cpu_baseline": cpu,
+        "child_processes_at_exit": len(kids),
     }
     print(json.dumps(result), flush=True)
 
