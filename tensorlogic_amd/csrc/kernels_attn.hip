@@ -126,7 +126,12 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed
     __shared__ float red[2][NWV];
     __shared__ float part[NWV][64];
     attn_kernarg_fence(a, J_fixed);
-    const int s = blockIdx.x, h = blockIdx.y;
+    const int s = blockIdx.x;
+    // One query row: workgroup i runs on XCD i % 8, so heads are dealt out
+    // XCD-major (XCD x takes heads x * H/8 .. x * H/8 + H/8 - 1) and the
+    // query heads that share a KV head read its rows through one or two
+    // L2s instead of all eight.
+    const int h = (gridDim.x == 1 && (a.H & 7) == 0) ? (blockIdx.y & 7) * (a.H >> 3) + (blockIdx.y >> 3) : blockIdx.y;
     const int Hkv = a.Hkv;
     const int kvh = h / (a.H / Hkv);
     const int qs = a.q_stride ? a.q_stride : a.H * 64;
