@@ -38,7 +38,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-GEMV_KERNEL = "gemv_m1_kernel<3, 1, 2> (Q4_0 fused dequant-GEMV, one activation row, 2 rows per wave)"
+GEMV_KERNEL = "gemv_m1_kernel<3, 1, 2, 0> (Q4_0 fused dequant-GEMV, one activation row, 2 rows per wave, plain-store epilogue)"
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_q4_0_5632x2048_pmc.txt")
 
 

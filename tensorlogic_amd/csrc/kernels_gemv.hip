@@ -280,6 +280,7 @@ static void launch_m1_ri(hipStream_t s, const Gemv1Params& p, int ri) {
 template <int WT>
 static bool launch_m1(hipStream_t s, const GemvParams& g, int nb, int ri) {
     const Gemv1Params p = {g.x, g.wq, g.wd, g.bias, g.resid, g.y, g.N, g.K, g.epi};
+    if (launch_m1_epi(s, (tlhip_dtype)WT, p, nb, ri)) return true;
     switch (nb) {
         case 1: launch_m1_ri<WT, 1>(s, p, ri); return true;
         case 2: launch_m1_ri<WT, 2>(s, p, ri); return true;

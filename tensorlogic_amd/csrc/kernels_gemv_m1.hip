@@ -1,0 +1,55 @@
+// kernels_gemv_m1.hip -- the single-row GEMV (M = 1, two rows per wave)
+// instantiated for each plain epilogue (gemv_device.hpp: gemv_m1_kernel with
+// EPI >= 0).  In a source of their own so that they compile in parallel with
+// the generic instantiations in kernels_gemv.hip.
+#include "gemv_device.hpp"
+
+namespace tlhip {
+
+template <int WT, int NB>
+static bool launch_m1_epi_nb(hipStream_t s, const Gemv1Params& p) {
+    const dim3 grid((unsigned)(((p.N + 1) / 2 + 3) / 4)), block(256);
+    const bool b = p.bias != nullptr, r = p.resid != nullptr;
+    switch (p.epi) {
+        case EPI_STORE: hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, 2, EPI_STORE>), grid, block, 0, s, p); return true;
+        case EPI_BIAS:
+            if (!b) return false;
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, 2, EPI_BIAS>), grid, block, 0, s, p);
+            return true;
+        case EPI_RESID:
+            if (!r) return false;
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, 2, EPI_RESID>), grid, block, 0, s, p);
+            return true;
+        case EPI_BIAS_RESID:
+            if (!b || !r) return false;
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, 2, EPI_BIAS_RESID>), grid, block, 0, s, p);
+            return true;
+        default: return false;
+    }
+}
+
+template <int WT>
+static bool launch_m1_epi_wt(hipStream_t s, const Gemv1Params& p, int nb) {
+    switch (nb) {   // the block counts launch_m1 rounds to
+        case 1: return launch_m1_epi_nb<WT, 1>(s, p);
+        case 2: return launch_m1_epi_nb<WT, 2>(s, p);
+        case 3: return launch_m1_epi_nb<WT, 3>(s, p);
+        case 4: return launch_m1_epi_nb<WT, 4>(s, p);
+        case 5: case 6: return launch_m1_epi_nb<WT, 6>(s, p);
+        case 7: case 8: return launch_m1_epi_nb<WT, 8>(s, p);
+        default: return false;
+    }
+}
+
+bool launch_m1_epi(hipStream_t s, tlhip_dtype wt, const Gemv1Params& p, int nb, int ri) {
+    if (ri != 2) return false;
+    switch (wt) {
+        case TLHIP_Q4_0: return launch_m1_epi_wt<TLHIP_Q4_0>(s, p, nb);
+        case TLHIP_Q8_0: return launch_m1_epi_wt<TLHIP_Q8_0>(s, p, nb);
+        case TLHIP_Q6_K: return launch_m1_epi_wt<TLHIP_Q6_K>(s, p, nb);
+        case TLHIP_F16: return launch_m1_epi_wt<TLHIP_F16>(s, p, nb);
+        default: return false;
+    }
+}
+
+}  // namespace tlhip
