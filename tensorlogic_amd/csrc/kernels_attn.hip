@@ -119,19 +119,48 @@ constexpr int A64_UNR = 8;
 // known at launch (no d_pos) of at most JMAX -- the smaller row lets more
 // workgroups share a CU.  UNR: K / V rows per key group and pass (fewer
 // registers, so more workgroups per CU, for short rows).
-template <int NT, int JMAX = ATT_MAX_J, int UNR = A64_UNR>
-__global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs a, int J_fixed) {
+// DEC: the decode step's launch (one query row, position read from d_pos,
+// causal, default row strides, the cache's allocated rows known) with those
+// facts as constants, so the compiler drops the other cases' code.
+__device__ __forceinline__ AttnArgs attn_dec_view(const AttnArgs& k) {
+    AttnArgs a;
+    a.q = k.q;
+    a.k = k.k;
+    a.v = k.v;
+    a.out = k.out;
+    a.S = 1;
+    a.H = k.H;
+    a.Hkv = k.Hkv;
+    a.D = 64;
+    a.q_pos0 = 0;
+    a.d_pos = k.d_pos;
+    a.causal = 1;
+    a.scale_h = k.scale_h;
+    a.q_stride = 0;
+    a.out_stride = 0;
+    a.kv_rows = k.kv_rows;
+    return a;
+}
+
+template <int NT, int JMAX = ATT_MAX_J, int UNR = A64_UNR, bool DEC = false>
+__global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs ak, int J_fixed) {
     constexpr int NWV = NT / 64, NG = NT / 8;
     __shared__ float sc[JMAX];
     __shared__ float red[2][NWV];
     __shared__ float part[NWV][64];
+    const AttnArgs a = DEC ? attn_dec_view(ak) : ak;
+    if constexpr (DEC) {   // (the launch checks both)
+        J_fixed = 0;
+        __builtin_assume(a.d_pos != nullptr);
+        __builtin_assume(a.kv_rows > 0);
+    }
     attn_kernarg_fence(a, J_fixed);
-    const int s = blockIdx.x;
+    const int s = DEC ? 0 : (int)blockIdx.x;
     // One query row: workgroup i runs on XCD i % 8, so heads are dealt out
     // XCD-major (XCD x takes heads x * H/8 .. x * H/8 + H/8 - 1) and the
     // query heads that share a KV head read its rows through one or two
     // L2s instead of all eight.
-    const int h = (gridDim.x == 1 && (a.H & 7) == 0) ? (blockIdx.y & 7) * (a.H >> 3) + (blockIdx.y >> 3) : blockIdx.y;
+    const int h = ((DEC || gridDim.x == 1) && (a.H & 7) == 0) ? (blockIdx.y & 7) * (a.H >> 3) + (blockIdx.y >> 3) : blockIdx.y;
     const int Hkv = a.Hkv;
     const int kvh = h / (a.H / Hkv);
     const int qs = a.q_stride ? a.q_stride : a.H * 64;
@@ -1566,7 +1595,9 @@ static void launch_attn_any(hipStream_t s, const AttnArgs& a, int J) {
         if (small) hipLaunchKernelGGL((attention64_kernel<512, 512>), g, dim3(512), 0, s, a, J);
         else hipLaunchKernelGGL(attention64_kernel<512>, g, dim3(512), 0, s, a, J);
     } else if (a.D == 64) {
-        if (small && J <= 64) hipLaunchKernelGGL((attention64_kernel<256, 64, 2>), g, dim3(256), 0, s, a, J);
+        if (a.d_pos && a.S == 1 && a.causal && !a.q_stride && !a.out_stride && a.kv_rows > 0)
+            hipLaunchKernelGGL((attention64_kernel<256, ATT_MAX_J, A64_UNR, true>), g, dim3(256), 0, s, a, J);
+        else if (small && J <= 64) hipLaunchKernelGGL((attention64_kernel<256, 64, 2>), g, dim3(256), 0, s, a, J);
         else if (small) hipLaunchKernelGGL((attention64_kernel<256, 512>), g, dim3(256), 0, s, a, J);
         else hipLaunchKernelGGL(attention64_kernel<256>, g, dim3(256), 0, s, a, J);
     } else if (a.D == 80) {
