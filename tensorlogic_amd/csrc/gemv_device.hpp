@@ -985,9 +985,10 @@ static void launch_norm_shape(hipStream_t s, const GemvParams& p) {
     }
 }
 
-// The single-row GEMV at two rows per wave, specialised on its epilogue
-// (kernels_gemv_m1.hip): plain store, bias, residual, bias + residual, each
-// only when the pointers it reads are present.  false: not specialised.
+// The single-row GEMV from 1024 rows (two rows per wave up to K = 4096, one
+// beyond), specialised on its epilogue (kernels_gemv_m1.hip): plain store,
+// bias, residual, bias + residual, each only when the pointers it reads are
+// present.  false: not specialised.
 bool launch_m1_epi(hipStream_t s, tlhip_dtype wt, const Gemv1Params& p, int nb, int ri);
 
 // The normalised GEMV of a decode step, specialised on its epilogue

@@ -395,10 +395,15 @@ tlhip_status launch_gemv(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
             int ri = p.N >= 1024 ? 2 : 1;
             if (pair_epi) ri = 2;
             if (p.M == 1 && !pair_epi) {   // single-row epilogues: the compact M = 1 kernel
-                if (wt == TLHIP_Q4_0) done = launch_m1<TLHIP_Q4_0>(s, p, nb, ri);
-                else if (wt == TLHIP_Q8_0) done = launch_m1<TLHIP_Q8_0>(s, p, nb, ri);
-                else if (wt == TLHIP_Q6_K) done = launch_m1<TLHIP_Q6_K>(s, p, nb, ri);
-                else done = launch_m1<TLHIP_F16>(s, p, nb, ri);
+                // one row per wave once a row takes three or more 64-block
+                // passes (measured on MI355X, Q4_0 under graph replay:
+                // [2560 x 10240] 7.96 -> 6.66 us, [2048 x 5632] 3.93 -> 3.87 us;
+                // at K = 2048 two rows per wave stay faster, 2.58 vs 2.72 us)
+                const int ri1 = nb >= 3 ? 1 : ri;
+                if (wt == TLHIP_Q4_0) done = launch_m1<TLHIP_Q4_0>(s, p, nb, ri1);
+                else if (wt == TLHIP_Q8_0) done = launch_m1<TLHIP_Q8_0>(s, p, nb, ri1);
+                else if (wt == TLHIP_Q6_K) done = launch_m1<TLHIP_Q6_K>(s, p, nb, ri1);
+                else done = launch_m1<TLHIP_F16>(s, p, nb, ri1);
             } else if (wt == TLHIP_Q4_0) done = launch_mx<TLHIP_Q4_0>(s, p, nb, ri);
             else if (wt == TLHIP_Q8_0) done = launch_mx<TLHIP_Q8_0>(s, p, nb, ri);
             else if (wt == TLHIP_Q6_K) done = launch_mx<TLHIP_Q6_K>(s, p, nb, ri);

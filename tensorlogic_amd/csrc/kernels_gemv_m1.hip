@@ -1,4 +1,4 @@
-// kernels_gemv_m1.hip -- the single-row GEMV (M = 1, two rows per wave)
+// kernels_gemv_m1.hip -- the single-row GEMV (M = 1, from 1024 rows)
 // instantiated for each plain epilogue (gemv_device.hpp: gemv_m1_kernel with
 // EPI >= 0).  In a source of their own so that they compile in parallel with
 // the generic instantiations in kernels_gemv.hip.
@@ -6,48 +6,55 @@
 
 namespace tlhip {
 
-template <int WT, int NB>
+template <int WT, int NB, int RI>
 static bool launch_m1_epi_nb(hipStream_t s, const Gemv1Params& p) {
-    const dim3 grid((unsigned)(((p.N + 1) / 2 + 3) / 4)), block(256);
+    const dim3 grid((unsigned)(((p.N + RI - 1) / RI + 3) / 4)), block(256);
     const bool b = p.bias != nullptr, r = p.resid != nullptr;
     switch (p.epi) {
-        case EPI_STORE: hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, 2, EPI_STORE>), grid, block, 0, s, p); return true;
+        case EPI_STORE: hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_STORE>), grid, block, 0, s, p); return true;
         case EPI_BIAS:
             if (!b) return false;
-            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, 2, EPI_BIAS>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS>), grid, block, 0, s, p);
             return true;
         case EPI_RESID:
             if (!r) return false;
-            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, 2, EPI_RESID>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_RESID>), grid, block, 0, s, p);
             return true;
         case EPI_BIAS_RESID:
             if (!b || !r) return false;
-            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, 2, EPI_BIAS_RESID>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS_RESID>), grid, block, 0, s, p);
             return true;
         default: return false;
     }
 }
 
+// Two rows per wave up to two 64-block passes per row, one row per wave
+// beyond (the shapes launch_m1 picks for M = 1 from 1024 rows).
 template <int WT>
-static bool launch_m1_epi_wt(hipStream_t s, const Gemv1Params& p, int nb) {
+static bool launch_m1_epi_wt(hipStream_t s, const Gemv1Params& p, int nb, int ri) {
+    if (ri == 2) {
+        switch (nb) {
+            case 1: return launch_m1_epi_nb<WT, 1, 2>(s, p);
+            case 2: return launch_m1_epi_nb<WT, 2, 2>(s, p);
+            default: return false;
+        }
+    }
     switch (nb) {   // the block counts launch_m1 rounds to
-        case 1: return launch_m1_epi_nb<WT, 1>(s, p);
-        case 2: return launch_m1_epi_nb<WT, 2>(s, p);
-        case 3: return launch_m1_epi_nb<WT, 3>(s, p);
-        case 4: return launch_m1_epi_nb<WT, 4>(s, p);
-        case 5: case 6: return launch_m1_epi_nb<WT, 6>(s, p);
-        case 7: case 8: return launch_m1_epi_nb<WT, 8>(s, p);
+        case 3: return launch_m1_epi_nb<WT, 3, 1>(s, p);
+        case 4: return launch_m1_epi_nb<WT, 4, 1>(s, p);
+        case 5: case 6: return launch_m1_epi_nb<WT, 6, 1>(s, p);
+        case 7: case 8: return launch_m1_epi_nb<WT, 8, 1>(s, p);
         default: return false;
     }
 }
 
 bool launch_m1_epi(hipStream_t s, tlhip_dtype wt, const Gemv1Params& p, int nb, int ri) {
-    if (ri != 2) return false;
+    if (p.N < 1024) return false;
     switch (wt) {
-        case TLHIP_Q4_0: return launch_m1_epi_wt<TLHIP_Q4_0>(s, p, nb);
-        case TLHIP_Q8_0: return launch_m1_epi_wt<TLHIP_Q8_0>(s, p, nb);
-        case TLHIP_Q6_K: return launch_m1_epi_wt<TLHIP_Q6_K>(s, p, nb);
-        case TLHIP_F16: return launch_m1_epi_wt<TLHIP_F16>(s, p, nb);
+        case TLHIP_Q4_0: return launch_m1_epi_wt<TLHIP_Q4_0>(s, p, nb, ri);
+        case TLHIP_Q8_0: return launch_m1_epi_wt<TLHIP_Q8_0>(s, p, nb, ri);
+        case TLHIP_Q6_K: return launch_m1_epi_wt<TLHIP_Q6_K>(s, p, nb, ri);
+        case TLHIP_F16: return launch_m1_epi_wt<TLHIP_F16>(s, p, nb, ri);
         default: return false;
     }
 }
