@@ -225,11 +225,14 @@ def test_linear_bias_and_f16_odd_shapes(dev, oracle):
 
 
 @pytest.mark.parametrize("qt", [Q4_0, Q8_0, F16])
-@pytest.mark.parametrize("N,K", [(37, 96), (1025, 2048), (300, 5632), (2, 32)])
+@pytest.mark.parametrize("N,K", [(37, 96), (1025, 2048), (300, 5632), (2, 32), (1030, 5632)])
 def test_linear_one_row_bias(dev, oracle, qt, N, K):
     """One activation row with a bias: the compact M = 1 GEMV (rows per wave
     1 or 2, blocks past the row read as zero weights: K = 96 and 5632 leave
-    lanes without a block, K = 32 all but one)."""
+    lanes without a block, K = 32 all but one); from 1024 rows the
+    epilogue-specialised instantiations, two rows per wave at K = 2048 and
+    one at K = 5632 (three 64-block passes), with idle waves in the last
+    workgroup at N = 1030."""
     x = S.normal_f16(9, f"x1b{K}", (1, K))
     b = S.normal_f16(9, f"b1b{N}", (N,))
     if qt == F16:
