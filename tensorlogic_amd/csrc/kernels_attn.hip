@@ -507,7 +507,18 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
 // a single row over a key count known at launch, which is also how a row
 // attends more keys than the one-workgroup kernels' LDS score row holds
 // (ATT_MAX_J).  Rows are read at min(j, kv_rows - 1), inside the allocation.
-constexpr int AS_CH = 128, AS_NT = 256, AS_NG = AS_NT / 8, AS_U = AS_CH / AS_NG;
+constexpr int AS_CH = 128;
+// NT threads per chunk workgroup: NT / 8 key groups of 8 lanes, each
+// holding AS_CH / (NT / 8) of the chunk's K / V rows.  512 threads (2 rows
+// per key group) up to 2048 cache rows, 256 (4 rows) beyond: measured on
+// MI355X, one row over 2048 keys 10.35 -> 10.04 us (head dim 64) and 11.03
+// -> 10.69 us (80) with 512, Phi-2 decode 696.7 -> 714.2 tok/s (same
+// tokens), but 8192 keys 16.3 -> 19.7 us (64).
+constexpr int AS_NT_ROWS = 2048;
+template <int NT>
+struct As {
+    static constexpr int NG = NT / 8, U = AS_CH / NG, NWV = NT / 64;
+};
 
 struct SplitBufs {
     float* e;      // [H][kv_rows] scores
@@ -522,9 +533,9 @@ __device__ __forceinline__ int asplit_keys(const AttnArgs& a, const SplitBufs& b
     return a.d_pos ? min(*a.d_pos + 1, a.kv_rows) : b.keys;
 }
 
-template <int D>
-__global__ __launch_bounds__(AS_NT) void asplit_scores_kernel(AttnArgs a, SplitBufs b) {
-    constexpr int EPL = D / 8, NW = EPL / 2, NWV = AS_NT / 64;
+template <int D, int NT>
+__global__ __launch_bounds__(NT) void asplit_scores_kernel(AttnArgs a, SplitBufs b) {
+    constexpr int EPL = D / 8, NW = EPL / 2, NWV = As<NT>::NWV, AS_NG = As<NT>::NG, AS_U = As<NT>::U;
     __shared__ float red[2][NWV];
     const int ch = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, c = tid & 7, g = tid >> 3;
     const int kvh = h / (a.H / a.Hkv);
@@ -582,9 +593,9 @@ __global__ __launch_bounds__(AS_NT) void asplit_scores_kernel(AttnArgs a, SplitB
     }
 }
 
-template <int D>
-__global__ __launch_bounds__(AS_NT) void asplit_pv_kernel(AttnArgs a, SplitBufs b) {
-    constexpr int EPL = D / 8, NW = EPL / 2, NWV = AS_NT / 64;
+template <int D, int NT>
+__global__ __launch_bounds__(NT) void asplit_pv_kernel(AttnArgs a, SplitBufs b) {
+    constexpr int EPL = D / 8, NW = EPL / 2, NWV = As<NT>::NWV, AS_NG = As<NT>::NG, AS_U = As<NT>::U;
     __shared__ float part[NWV][D];
     __shared__ float red[2][NWV];
     const int ch = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, c = tid & 7, g = tid >> 3;
@@ -602,11 +613,11 @@ __global__ __launch_bounds__(AS_NT) void asplit_pv_kernel(AttnArgs a, SplitBufs 
     // dependent loads over the chunks cost one L2 round trip per chunk), then
     // combined in a fixed tree order
     float gmax = -INFINITY;
-    for (int k = tid; k < nc; k += AS_NT) gmax = fmaxf(gmax, b.mx[(size_t)h * b.nch + k]);
+    for (int k = tid; k < nc; k += NT) gmax = fmaxf(gmax, b.mx[(size_t)h * b.nch + k]);
     gmax = block_max1<NWV>(gmax, red[0]);
     if (!isfinite(gmax)) gmax = 0.0f;
     float gsum = 0.0f;
-    for (int k = tid; k < nc; k += AS_NT) {
+    for (int k = tid; k < nc; k += NT) {
         const float mk = b.mx[(size_t)h * b.nch + k];
         if (isfinite(mk)) gsum += b.sum[(size_t)h * b.nch + k] * expf(mk - gmax);
     }
@@ -684,6 +695,23 @@ size_t attention_split_scratch(int H, int kv_rows, int D) {
     return ((size_t)H * kv_rows + 2 * (size_t)H * nch + (size_t)H * nch * D) * sizeof(float);
 }
 
+template <int NT>
+static void launch_split_kernels(hipStream_t s, const AttnArgs& a, const SplitBufs& b, dim3 grid) {
+    if (a.D == 64) {
+        hipLaunchKernelGGL((asplit_scores_kernel<64, NT>), grid, dim3(NT), 0, s, a, b);
+        hipLaunchKernelGGL((asplit_pv_kernel<64, NT>), grid, dim3(NT), 0, s, a, b);
+        hipLaunchKernelGGL(asplit_combine_kernel<64>, dim3((unsigned)a.H), dim3(64), 0, s, a, b);
+    } else if (a.D == 80) {
+        hipLaunchKernelGGL((asplit_scores_kernel<80, NT>), grid, dim3(NT), 0, s, a, b);
+        hipLaunchKernelGGL((asplit_pv_kernel<80, NT>), grid, dim3(NT), 0, s, a, b);
+        hipLaunchKernelGGL(asplit_combine_kernel<80>, dim3((unsigned)a.H), dim3(80), 0, s, a, b);
+    } else {
+        hipLaunchKernelGGL((asplit_scores_kernel<128, NT>), grid, dim3(NT), 0, s, a, b);
+        hipLaunchKernelGGL((asplit_pv_kernel<128, NT>), grid, dim3(NT), 0, s, a, b);
+        hipLaunchKernelGGL(asplit_combine_kernel<128>, dim3((unsigned)a.H), dim3(128), 0, s, a, b);
+    }
+}
+
 static tlhip_status launch_split(hipStream_t s, const AttnArgs& a, SplitBufs b, float* scratch) {
     b.nch = (a.kv_rows + AS_CH - 1) / AS_CH;
     b.e = scratch;
@@ -691,19 +719,8 @@ static tlhip_status launch_split(hipStream_t s, const AttnArgs& a, SplitBufs b, 
     b.sum = b.mx + (size_t)a.H * b.nch;
     b.o = b.sum + (size_t)a.H * b.nch;
     const dim3 grid((unsigned)b.nch, (unsigned)a.H);
-    if (a.D == 64) {
-        hipLaunchKernelGGL(asplit_scores_kernel<64>, grid, dim3(AS_NT), 0, s, a, b);
-        hipLaunchKernelGGL(asplit_pv_kernel<64>, grid, dim3(AS_NT), 0, s, a, b);
-        hipLaunchKernelGGL(asplit_combine_kernel<64>, dim3((unsigned)a.H), dim3(64), 0, s, a, b);
-    } else if (a.D == 80) {
-        hipLaunchKernelGGL(asplit_scores_kernel<80>, grid, dim3(AS_NT), 0, s, a, b);
-        hipLaunchKernelGGL(asplit_pv_kernel<80>, grid, dim3(AS_NT), 0, s, a, b);
-        hipLaunchKernelGGL(asplit_combine_kernel<80>, dim3((unsigned)a.H), dim3(80), 0, s, a, b);
-    } else {
-        hipLaunchKernelGGL(asplit_scores_kernel<128>, grid, dim3(AS_NT), 0, s, a, b);
-        hipLaunchKernelGGL(asplit_pv_kernel<128>, grid, dim3(AS_NT), 0, s, a, b);
-        hipLaunchKernelGGL(asplit_combine_kernel<128>, dim3((unsigned)a.H), dim3(128), 0, s, a, b);
-    }
+    if (a.kv_rows <= AS_NT_ROWS) launch_split_kernels<512>(s, a, b, grid);
+    else launch_split_kernels<256>(s, a, b, grid);
     return TLHIP_OK;
 }
 
