@@ -368,7 +368,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (asked for {args.gpus}); the hot path is "
-              "single-GPU by design, see DESIGN.md for how it would shard", file=sys.stderr)
+              "single-GPU by design: one process drives one GPU's share of a model, and no "
+              "multi-GPU figure is produced", file=sys.stderr)
         sys.exit(2)
 
     from tensorlogic_amd import Device, Model
