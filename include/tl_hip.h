@@ -139,14 +139,19 @@ tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_t
  * but allocating nothing: no counterpart in the reference.  It is for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  The split-K
- * partials of the MFMA GEMM live in a 16 MiB device array that each GPU holds
+ * partials of the MFMA GEMM live in a 20 MiB device array that each GPU holds
  * from library load to process end (partials beyond it -> AllocationError;
- * the library's split policy needs at most 10.5 MB).  A Q6_K weight with
+ * the library's split policy needs at most 20 MiB: 320 tiles of 128 x 128
+ * fp32 over all slices, e.g. [512 x 10240] @ [2560 x 10240]^T in 4 slices).
+ * Its device address is resolved by tlhip_init, or on the first call if that
+ * failed (a failure is reported by this call only).  A Q6_K weight with
  * M > 4 needs a dequantised f16 copy and is refused (InvalidOperation).  All
  * calls on one GPU share that array: calls overlapping in time on one GPU
  * (several contexts or threads) race and must be serialised by the caller. */
 tlhip_status tlhip_linear_noalloc(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y);
-/* matmul(a, b) (builtin_math.rs:39, matmul.rs:52-197): c[M,N] = a[M,K] b[K,N]. */
+/* matmul(a, b) (builtin_math.rs:36-60, matmul.rs:22-197): c[M,N] = a[M,K] b[K,N],
+ * all f16 or all f32 (a mix: DtypeError); rank != 2 or an inner-dimension
+ * mismatch: InvalidOperation, as Tensor::matmul returns. */
 tlhip_status tlhip_matmul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor c);
 /* rms_norm(x, w[, eps]) (builtin_nn.rs:44-103, normalization.rs:42-250)
  * over the last dim.                                                       */

@@ -164,7 +164,7 @@ bool gguf_lookup(tlhip_gguf g, const char* name, uint32_t* type, int* ndim, int6
 
 extern "C" {
 
-tlhip_status tlhip_gguf_open(const char* path, tlhip_gguf* out) {
+tlhip_status tlhip_gguf_open(const char* path, tlhip_gguf* out) try {
     if (!path || !out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     *out = nullptr;
     int fd = open(path, O_RDONLY);
@@ -190,6 +190,11 @@ tlhip_status tlhip_gguf_open(const char* path, tlhip_gguf* out) {
     if (version < 2 || version > 3) return bad("unsupported GGUF version (expected 2 or 3)");
     uint64_t nt = r.u(8), nkv = r.u(8);
     if (r.err || nt > (1u << 24) || nkv > (1u << 24)) return bad("corrupt tensor/KV counts");
+    // every KV pair takes at least 13 bytes (key length, type, a one-byte
+    // value) and every tensor info 32 (name length, rank, one dim, type,
+    // offset): counts the file cannot hold are refused before any container
+    // is sized by them
+    if (nkv * 13 + nt * 32 > size - r.off) return bad("tensor/KV counts exceed the file");
     uint64_t alignment = 32;
     for (uint64_t i = 0; i < nkv; i++) {
         std::string key = r.str();
@@ -237,39 +242,39 @@ tlhip_status tlhip_gguf_open(const char* path, tlhip_gguf* out) {
         if (ti.offset > data_bytes || ti.nbytes > data_bytes - ti.offset) return bad("tensor data exceeds file");
     *out = g;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_gguf_close(tlhip_gguf g) {
+tlhip_status tlhip_gguf_close(tlhip_gguf g) try {
     if (!g) return TLHIP_OK;
     if (g->map) munmap(g->map, g->size);
     delete g;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-int tlhip_gguf_n_tensors(tlhip_gguf g) { return g ? (int)g->infos.size() : 0; }
+int tlhip_gguf_n_tensors(tlhip_gguf g) try { return g ? (int)g->infos.size() : 0; } TLHIP_CATCH_VALUE(0)
 
-const char* tlhip_gguf_tensor_name(tlhip_gguf g, int i) {
+const char* tlhip_gguf_tensor_name(tlhip_gguf g, int i) try {
     if (!g || i < 0 || i >= (int)g->infos.size()) return nullptr;
     return g->infos[i].name.c_str();
-}
+} TLHIP_CATCH_VALUE(nullptr)
 
-tlhip_status tlhip_gguf_kv_u32(tlhip_gguf g, const char* key, uint32_t* v) {
+tlhip_status tlhip_gguf_kv_u32(tlhip_gguf g, const char* key, uint32_t* v) try {
     if (!g || !key || !v) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     auto it = g->kv.find(key);
     if (it == g->kv.end()) return fail(TLHIP_ERR_LOAD, "GGUF key %s not found", key);
     *v = (uint32_t)it->second.u;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_gguf_kv_f32(tlhip_gguf g, const char* key, float* v) {
+tlhip_status tlhip_gguf_kv_f32(tlhip_gguf g, const char* key, float* v) try {
     if (!g || !key || !v) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     auto it = g->kv.find(key);
     if (it == g->kv.end()) return fail(TLHIP_ERR_LOAD, "GGUF key %s not found", key);
     *v = (float)it->second.f;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_gguf_load_tensor(tlhip_ctx ctx, tlhip_gguf g, const char* name, tlhip_tensor* out) {
+tlhip_status tlhip_gguf_load_tensor(tlhip_ctx ctx, tlhip_gguf g, const char* name, tlhip_tensor* out) try {
     TLHIP_TRY(check_ctx(ctx));
     if (!g || !name || !out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     *out = nullptr;
@@ -309,6 +314,6 @@ tlhip_status tlhip_gguf_load_tensor(tlhip_ctx ctx, tlhip_gguf g, const char* nam
     }
     *out = t;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
 }  // extern "C"

@@ -34,6 +34,21 @@ tlhip_status fail(tlhip_status st, const char* fmt, ...) __attribute__((format(p
                                  hipGetErrorString(e_));                               \
     } while (0)
 
+tlhip_status abi_exception() noexcept;
+
+// Handler of a function-try-block around an exported function's body:
+// any host exception becomes a status (see abi_exception).
+#define TLHIP_CATCH_STATUS \
+    catch (...) {          \
+        return ::tlhip::abi_exception(); \
+    }
+// The same for exported functions that return a value: the value on error.
+#define TLHIP_CATCH_VALUE(v)             \
+    catch (...) {                        \
+        (void)::tlhip::abi_exception();  \
+        return v;                        \
+    }
+
 #define TLHIP_TRY(expr)                                 \
     do {                                                \
         tlhip_status s_ = (expr);                       \
@@ -175,6 +190,10 @@ struct GemvArgs {
 // weight-row tiles up to which the skinny GEMM splits K over workgroups (and
 // so the counters a context holds for it)
 constexpr int SK_MAX_TILES_SPLIT = 128;
+// arrival counters of the key-chunked decode attention, one per head, after
+// the skinny GEMM's in the context's counter array (zero between launches)
+constexpr int ATTN_SPLIT_MAX_HEADS = 1024;
+constexpr int CTX_FLAG_WORDS = SK_MAX_TILES_SPLIT + ATTN_SPLIT_MAX_HEADS;
 enum GemvPro { PRO_NONE = 0, PRO_RMS = 1, PRO_LN = 2 };
 // Epilogues fused into the GEMV/GEMM store (each step rounds to f16 where
 // the reference's separate op would store f16):
@@ -199,6 +218,14 @@ tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
 tlhip_status launch_linear_f32(hipStream_t s, const float* x, const float* w, const float* bias, float* y, int M, int N,
                                int K);
 bool gemm_skinny_ok(int M, int N, int K, int wt);   // the skinny M <= 64 GEMM takes the shape (and EPI_QKV_ROPE)
+// Split-K partials (fp32) of any count gemm_splits picks stay within
+// GEMM_SPLIT_PARTIALS_MAX bytes: M > 64 keeps tiles x slices <= GEMM_SPLIT_TILE_CAP
+// tiles of 128 x 128 (20 MiB); the skinny GEMM (5 <= M <= 64) splits at most
+// SK_MAX_TILES_SPLIT tiles (N <= 8192 at 64 rows) into 8 slices (16 MiB); the
+// other M <= 64 shapes keep tiles x slices <= 512 tiles of 64 x 64 (8 MiB).
+// kernels_gemm.hip ties these figures to its tile constants by static_assert.
+constexpr int GEMM_SPLIT_TILE_CAP = 320;
+constexpr size_t GEMM_SPLIT_PARTIALS_MAX = (size_t)GEMM_SPLIT_TILE_CAP * 128 * 128 * sizeof(float);
 int gemm_splits(int M, int N, int K, int wt);   // split-K slices launch_gemm uses when given a workspace
                                                 // (wt < 0: any weight type, the largest count)
 uint16_t f32_to_f16(float f);            // host RNE rounding (F32 GGUF tensors)
@@ -264,9 +291,11 @@ struct AttnArgs {
     float scale_h = 0.125f;       // f16-rounded scale
     int q_stride = 0, out_stride = 0;  // row strides (elements); 0 = H*D
     int kv_rows = 0;              // rows allocated in k / v (bounds early loads); 0 = J
+    uint32_t* head_flags = nullptr;  // key-chunked decode: the context's per-head counters
 };
 tlhip_status launch_stream_copy(hipStream_t s, const void* src, void* dst, size_t bytes);
 tlhip_status launch_transpose(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows, int cols);
+tlhip_status launch_transpose_f32(hipStream_t s, const float* src, float* dst, int rows, int cols);
 tlhip_status launch_attention(hipStream_t s, const AttnArgs& a);   // decode: J from *d_pos
 tlhip_status launch_attention_j(hipStream_t s, const AttnArgs& a, int J);
 // Prefill through the matrix cores when attention_mfma_ok(); vt is scratch

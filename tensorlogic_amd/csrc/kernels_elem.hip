@@ -981,9 +981,9 @@ tlhip_status launch_stream_copy(hipStream_t s, const void* src, void* dst, size_
 }
 
 // dst[c, r] = src[r, c] for a row-major [rows, cols] f16 matrix.
-__global__ void transpose_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst, int rows,
-                                 int cols) {
-    __shared__ uint16_t tile[32][33];
+template <typename T>
+__global__ void transpose_kernel(const T* __restrict__ src, T* __restrict__ dst, int rows, int cols) {
+    __shared__ T tile[32][33];
     const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
     const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 256 threads: 32 x 8
     for (int i = ty; i < 32; i += 8) {
@@ -997,11 +997,21 @@ __global__ void transpose_kernel(const uint16_t* __restrict__ src, uint16_t* __r
     }
 }
 
-tlhip_status launch_transpose(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows, int cols) {
+template <typename T>
+static tlhip_status launch_transpose_t(hipStream_t s, const T* src, T* dst, int rows, int cols) {
     if (rows <= 0 || cols <= 0) return TLHIP_OK;
-    hipLaunchKernelGGL(transpose_kernel, dim3((cols + 31) / 32, (rows + 31) / 32), dim3(256), 0, s, src, dst,
-                       rows, cols);
+    const unsigned gy = (unsigned)((rows + 31) / 32);
+    if (gy > 65535u) return fail(TLHIP_ERR_INVALID_DIMENSION, "transpose: %d rows exceed the launch grid", rows);
+    hipLaunchKernelGGL(transpose_kernel<T>, dim3((cols + 31) / 32, gy), dim3(256), 0, s, src, dst, rows, cols);
     return TLHIP_OK;
+}
+
+tlhip_status launch_transpose(hipStream_t s, const uint16_t* src, uint16_t* dst, int rows, int cols) {
+    return launch_transpose_t(s, src, dst, rows, cols);
+}
+
+tlhip_status launch_transpose_f32(hipStream_t s, const float* src, float* dst, int rows, int cols) {
+    return launch_transpose_t(s, src, dst, rows, cols);
 }
 
 }  // namespace tlhip

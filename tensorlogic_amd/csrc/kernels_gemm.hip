@@ -1131,6 +1131,12 @@ static void launch_gemm2(hipStream_t s, const GemmParams& p, int splits, float* 
 // M > 64 (multi-stage 128 x 128 tiles, one workgroup per CU): up to 4
 // slices while the grid stays within 320 workgroups, at least 8 K steps
 // per slice.
+// The bound GEMM_SPLIT_PARTIALS_MAX states for each branch below (the fixed
+// workspace of the no-allocation entry point is sized by it).
+static_assert((size_t)GEMM_SPLIT_TILE_CAP * GL_BM * GL_BN * sizeof(float) <= GEMM_SPLIT_PARTIALS_MAX, "M > 64 split");
+static_assert((size_t)SK_MAX_SPLITS * 64 * (SK_MAX_TILES_SPLIT * 16 * 4) * sizeof(float) <= GEMM_SPLIT_PARTIALS_MAX,
+              "skinny split (64 rows, N <= SK_MAX_TILES_SPLIT tiles of 16 x 4 weight rows)");
+static_assert((size_t)512 * 64 * 64 * sizeof(float) <= GEMM_SPLIT_PARTIALS_MAX, "M <= 64 split");
 int gemm_splits(int M, int N, int K, int wt) {
     if (wt < 0) {   // any weight type: the largest count any of them takes
         int sp = 1;
@@ -1142,7 +1148,7 @@ int gemm_splits(int M, int N, int K, int wt) {
     int sp = 1;
     if (M > 64) {
         const int tiles = ((N + GL_BN - 1) / GL_BN) * ((M + GL_BM - 1) / GL_BM);
-        while (sp < 4 && tiles * sp * 2 <= 320 && (K / G2_BK) / (sp * 2) >= 8) sp *= 2;
+        while (sp < 4 && tiles * sp * 2 <= GEMM_SPLIT_TILE_CAP && (K / G2_BK) / (sp * 2) >= 8) sp *= 2;
         return sp;
     }
     const int tiles = ((N + 63) / 64) * ((M + 63) / 64);

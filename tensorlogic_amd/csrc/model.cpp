@@ -439,6 +439,7 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
         at.causal = 1;
         at.kv_rows = m->max_ctx;
         at.scale_h = (float)(_Float16)(1.0f / sqrtf((float)D));
+        at.head_flags = m->ctx->d_tile_flags + SK_MAX_TILES_SPLIT;
         if (decode) {
             at.d_pos = d_pos;
             if (m->d_asplit && attention_split_ok(at)) TLHIP_TRY(launch_attention_split(s, at, m->d_asplit));
@@ -607,22 +608,22 @@ static tlhip_status kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int
 }
 
 tlhip_status tlhip_kvcache_create(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads, int head_dim,
-                                  tlhip_kvcache* out) {
+                                  tlhip_kvcache* out) try {
     return kvcache_create(ctx, n_layers, max_ctx, n_kv_heads, head_dim, TLHIP_F16, out);
-}
+} TLHIP_CATCH_STATUS
 
 tlhip_status tlhip_kvcache_create_f32(tlhip_ctx ctx, int n_layers, int max_ctx, int n_kv_heads, int head_dim,
-                                      tlhip_kvcache* out) {
+                                      tlhip_kvcache* out) try {
     return kvcache_create(ctx, n_layers, max_ctx, n_kv_heads, head_dim, TLHIP_F32, out);
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_kvcache_free(tlhip_kvcache c) {
+tlhip_status tlhip_kvcache_free(tlhip_kvcache c) try {
     if (!c) return TLHIP_OK;
     for (auto t : c->k) tlhip_tensor_free(t);
     for (auto t : c->v) tlhip_tensor_free(t);
     delete c;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
 static tlhip_status kv_write(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v, bool append) {
     TLHIP_TRY(check_ctx(ctx));
@@ -650,15 +651,15 @@ static tlhip_status kv_write(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_te
     return after_launch(ctx, append ? "kvcache_append" : "kvcache_set");
 }
 
-tlhip_status tlhip_kvcache_set(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v) {
+tlhip_status tlhip_kvcache_set(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v) try {
     return kv_write(ctx, c, layer, k, v, false);
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_kvcache_append(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v) {
+tlhip_status tlhip_kvcache_append(tlhip_ctx ctx, tlhip_kvcache c, int layer, tlhip_tensor k, tlhip_tensor v) try {
     return kv_write(ctx, c, layer, k, v, true);
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_kvcache_get(tlhip_kvcache c, int layer, int which_v, tlhip_tensor* out) {
+tlhip_status tlhip_kvcache_get(tlhip_kvcache c, int layer, int which_v, tlhip_tensor* out) try {
     if (!c || !out || layer < 0 || layer >= c->n_layers)
         return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "kvcache layer %d", layer);
     if (c->len[layer] == 0) return fail(TLHIP_ERR_INVALID_OPERATION, "kvcache layer %d is empty", layer);
@@ -674,18 +675,18 @@ tlhip_status tlhip_kvcache_get(tlhip_kvcache c, int layer, int which_v, tlhip_te
     src->refcount++;
     *out = view;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-int tlhip_kvcache_len(tlhip_kvcache c, int layer) {
+int tlhip_kvcache_len(tlhip_kvcache c, int layer) try {
     if (!c || layer < 0 || layer >= c->n_layers) return -1;
     return c->len[layer];
-}
+} TLHIP_CATCH_VALUE(-1)
 
 // Attention of S query rows against a KV cache layer after cache.append (the
 // TL program's get_k / get_v + einsum / mask / softmax / einsum sequence):
 // the queries are the cache's last S positions, len - S .. len - 1, causal.
 tlhip_status tlhip_attention_prefill(tlhip_ctx ctx, tlhip_tensor q, tlhip_kvcache c, int layer, float scale,
-                                     tlhip_tensor out) {
+                                     tlhip_tensor out) try {
     if (!c || layer < 0 || layer >= c->n_layers) return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "kvcache layer %d", layer);
     TLHIP_TRY(check_t(q, "attention_prefill"));
     if (q->ndim != 3) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention_prefill: q must be [S, H, D]");
@@ -700,21 +701,21 @@ tlhip_status tlhip_attention_prefill(tlhip_ctx ctx, tlhip_tensor q, tlhip_kvcach
     (void)tlhip_tensor_free(k);
     if (v) (void)tlhip_tensor_free(v);
     return st;
-}
+} TLHIP_CATCH_STATUS
 
 // One decode row: q [1, H, D] at the cache's last position.
 tlhip_status tlhip_attention_decode(tlhip_ctx ctx, tlhip_tensor q, tlhip_kvcache c, int layer, float scale,
-                                    tlhip_tensor out) {
+                                    tlhip_tensor out) try {
     TLHIP_TRY(check_t(q, "attention_decode"));
     if (q->ndim != 3 || q->shape[0] != 1)
         return fail(TLHIP_ERR_INVALID_DIMENSION, "attention_decode: q must be [1, H, D], got %s", shape_str(q).c_str());
     return tlhip_attention_prefill(ctx, q, c, layer, scale, out);
-}
+} TLHIP_CATCH_STATUS
 
 // ---------------------------------------------------------------------------
 // model
 // ---------------------------------------------------------------------------
-tlhip_status tlhip_model_free(tlhip_model m) {
+tlhip_status tlhip_model_free(tlhip_model m) try {
     if (!m) return TLHIP_OK;
     if (m->ctx) (void)hipStreamSynchronize(m->ctx->stream);
     if (m->gexec) (void)hipGraphExecDestroy(m->gexec);
@@ -747,9 +748,9 @@ tlhip_status tlhip_model_free(tlhip_model m) {
     if (m->h_state) (void)hipHostFree(m->h_state);
     delete m;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max_ctx, tlhip_model* out) {
+tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max_ctx, tlhip_model* out) try {
     TLHIP_TRY(check_ctx(ctx));
     if (!path || !out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     *out = nullptr;
@@ -901,15 +902,15 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
     }
     *out = m;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_model_reset(tlhip_model m) {
+tlhip_status tlhip_model_reset(tlhip_model m) try {
     if (!m) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null model");
     m->pos = 0;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_model_set_sampling(tlhip_model m, float temperature, uint64_t seed) {
+tlhip_status tlhip_model_set_sampling(tlhip_model m, float temperature, uint64_t seed) try {
     if (!m) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null model");
     if (!(temperature >= 0.0f) || !std::isfinite(temperature))
         return fail(TLHIP_ERR_INVALID_ARGUMENT, "temperature %g", temperature);
@@ -923,9 +924,9 @@ tlhip_status tlhip_model_set_sampling(tlhip_model m, float temperature, uint64_t
     m->temperature = temperature;
     m->seed = seed;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_model_set_program_semantics(tlhip_model m, int literal) {
+tlhip_status tlhip_model_set_program_semantics(tlhip_model m, int literal) try {
     if (!m) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null model");
     if (m->arch != 0)
         return fail(TLHIP_ERR_INVALID_OPERATION, "program semantics are defined for the llama program only");
@@ -950,32 +951,32 @@ tlhip_status tlhip_model_set_program_semantics(tlhip_model m, int literal) {
     m->literal = literal;
     m->eps = literal ? 1e-6f : m->gguf_eps;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_model_dims(tlhip_model m, int32_t* d) {
+tlhip_status tlhip_model_dims(tlhip_model m, int32_t* d) try {
     if (!m || !d) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     int32_t v[8] = {m->n_layers, m->hidden, m->inter, m->n_heads, m->n_kv, m->head_dim, m->vocab, m->rot};
     memcpy(d, v, sizeof v);
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_model_prefill(tlhip_model m, const int32_t* ids, int n, int32_t* next) {
+tlhip_status tlhip_model_prefill(tlhip_model m, const int32_t* ids, int n, int32_t* next) try {
     if (!m || !ids) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     TLHIP_TRY(prefill(m, ids, n, 0));
     return read_state(m, next);
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_model_decode(tlhip_model m, int32_t token, int32_t* next) {
+tlhip_status tlhip_model_decode(tlhip_model m, int32_t token, int32_t* next) try {
     if (!m) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null model");
     if (token < 0 || token >= m->vocab)
         return fail(TLHIP_ERR_INDEX_OUT_OF_BOUNDS, "token id %d out of range [0, %d)", token, m->vocab);
     TLHIP_TRY(set_state(m, token, m->pos, 0));
     TLHIP_TRY(decode_steps(m, 1, false));
     return read_state(m, next);
-}
+} TLHIP_CATCH_STATUS
 
 tlhip_status tlhip_model_generate(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode, int use_graph,
-                                  int32_t* tokens_out) {
+                                  int32_t* tokens_out) try {
     if (!m || !prompt || !tokens_out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     if (n_decode < 0) return fail(TLHIP_ERR_INVALID_ARGUMENT, "n_decode < 0");
     m->pos = 0;
@@ -987,21 +988,21 @@ tlhip_status tlhip_model_generate(tlhip_model m, const int32_t* prompt, int n_pr
                                    m->ctx->stream));
     TLHIP_CHECK_HIP(hipStreamSynchronize(m->ctx->stream));
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_model_logits(tlhip_model m, uint16_t* host, size_t n) {
+tlhip_status tlhip_model_logits(tlhip_model m, uint16_t* host, size_t n) try {
     if (!m || !host) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     if (n != (size_t)m->vocab) return fail(TLHIP_ERR_SHAPE_MISMATCH, "logits has %d entries", m->vocab);
     TLHIP_CHECK_HIP(hipMemcpyAsync(host, m->logits->data, n * 2, hipMemcpyDeviceToHost, m->ctx->stream));
     TLHIP_CHECK_HIP(hipStreamSynchronize(m->ctx->stream));
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
 // ---------------------------------------------------------------------------
 // measurement helpers
 // ---------------------------------------------------------------------------
 tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tensor* w, int n_w, tlhip_tensor y,
-                                int iters, int per_launch, float* avg_us) {
+                                int iters, int per_launch, float* avg_us) try {
     TLHIP_TRY(check_ctx(ctx));
     if (!w || n_w <= 0 || iters <= 0 || !avg_us) return fail(TLHIP_ERR_INVALID_ARGUMENT, "bad bench arguments");
     for (int i = 0; i < n_w; i++) TLHIP_TRY(tlhip_linear(ctx, x, w[i], nullptr, y));   // checks + warm-up
@@ -1050,9 +1051,9 @@ tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tenso
         if (e) (void)hipEventDestroy(e);
     if (st == TLHIP_OK) *avg_us = (float)(total * 1000.0 / iters);
     return st;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_bench_copy(tlhip_ctx ctx, size_t bytes, int n_buf, int iters, float* avg_us) {
+tlhip_status tlhip_bench_copy(tlhip_ctx ctx, size_t bytes, int n_buf, int iters, float* avg_us) try {
     TLHIP_TRY(check_ctx(ctx));
     if (bytes < 16 || bytes % 16 || n_buf <= 0 || iters <= 0 || !avg_us)
         return fail(TLHIP_ERR_INVALID_ARGUMENT, "bench_copy: bytes must be a positive multiple of 16");
@@ -1078,25 +1079,25 @@ tlhip_status tlhip_bench_copy(tlhip_ctx ctx, size_t bytes, int n_buf, int iters,
     if (dst) (void)hipFree(dst);
     if (st == TLHIP_OK) *avg_us = ms * 1000.0f / (float)iters;
     return st;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_timer_start(tlhip_ctx ctx) {
+tlhip_status tlhip_timer_start(tlhip_ctx ctx) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_CHECK_HIP(hipEventRecord(ctx->ev0, ctx->stream));
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_timer_stop(tlhip_ctx ctx, float* ms) {
+tlhip_status tlhip_timer_stop(tlhip_ctx ctx, float* ms) try {
     TLHIP_TRY(check_ctx(ctx));
     if (!ms) return fail(TLHIP_ERR_INVALID_ARGUMENT, "timer_stop: null output");
     TLHIP_CHECK_HIP(hipEventRecord(ctx->ev1, ctx->stream));
     TLHIP_CHECK_HIP(hipEventSynchronize(ctx->ev1));
     TLHIP_CHECK_HIP(hipEventElapsedTime(ms, ctx->ev0, ctx->ev1));
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
 tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode, int use_graph,
-                                int32_t* tokens_out, float* prefill_ms, float* decode_ms) {
+                                int32_t* tokens_out, float* prefill_ms, float* decode_ms) try {
     if (!m || !prompt || !tokens_out || !prefill_ms || !decode_ms)
         return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     if (n_prompt + n_decode > m->max_ctx)
@@ -1117,6 +1118,6 @@ tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prom
     TLHIP_CHECK_HIP(hipEventElapsedTime(decode_ms, ctx->ev0, ctx->ev1));
     TLHIP_CHECK_HIP(hipMemcpy(tokens_out, m->d_tokens, sizeof(int32_t) * (n_decode + 1), hipMemcpyDeviceToHost));
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
 }  // extern "C"

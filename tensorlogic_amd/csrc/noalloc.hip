@@ -25,11 +25,11 @@
 
 namespace {
 
-// Largest split-K partial set gemm_splits can ask for: M > 64 keeps at most
-// 320 / 2 = 160 tiles of 128 x 128 per split product (sp * M * N <= 160 *
-// 16384 floats = 10.5 MB); M <= 64 splits only up to 128 tiles of 32 rows,
-// at most 8 slices (8 * 64 * 4096 floats = 8 MiB).
-constexpr size_t kScratchBytes = 16u << 20;
+// Largest split-K partial set gemm_splits can ask for (GEMM_SPLIT_PARTIALS_MAX,
+// 20 MiB: M > 64 keeps at most 320 tiles of 128 x 128 over all slices, e.g.
+// Q4_0 [512 x 10240] @ [2560 x 10240]^T in 4 slices; the skinny GEMM's
+// splits stay within 16 MiB).
+constexpr size_t kScratchBytes = tlhip::GEMM_SPLIT_PARTIALS_MAX;
 constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
@@ -46,10 +46,18 @@ tlhip_status noalloc_setup(int device) {
         return fail(TLHIP_ERR_DEVICE, "device %d beyond the %d the library tracks", device, kMaxDevices);
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_scratch_dev[device]) return TLHIP_OK;
+    int prev = -1;
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    // the symbol's address is per device: resolve it with that device current
+    if (prev != device && hipSetDevice(device) != hipSuccess)
+        return fail(TLHIP_ERR_DEVICE, "linear_noalloc: cannot make device %d current", device);
     void* ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !ptr)
+    if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
+    if (e != hipSuccess || !ptr) {
+        (void)hipGetLastError();
         return fail(TLHIP_ERR_DEVICE, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    }
     g_scratch_dev[device] = (float*)ptr;
     return TLHIP_OK;
 }
@@ -57,7 +65,7 @@ tlhip_status noalloc_setup(int device) {
 }  // namespace tlhip
 
 extern "C" tlhip_status tlhip_linear_noalloc(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias,
-                                             tlhip_tensor y) {
+                                             tlhip_tensor y) try {
     using namespace tlhip;
     TLHIP_TRY(check_ctx(ctx));
     float* ws = nullptr;
@@ -65,6 +73,10 @@ extern "C" tlhip_status tlhip_linear_noalloc(tlhip_ctx ctx, tlhip_tensor x, tlhi
         std::lock_guard<std::mutex> lk(g_mu);
         if (ctx->device >= 0 && ctx->device < kMaxDevices) ws = g_scratch_dev[ctx->device];
     }
-    if (!ws) return fail(TLHIP_ERR_DEVICE, "linear_noalloc: workspace of device %d not set up", ctx->device);
+    if (!ws) {   // tlhip_init could not resolve it: once more, here, or report why not
+        TLHIP_TRY(noalloc_setup(ctx->device));
+        std::lock_guard<std::mutex> lk(g_mu);
+        ws = g_scratch_dev[ctx->device];
+    }
     return linear_impl(ctx, x, w, bias, y, ws, kScratchBytes);
-}
+} TLHIP_CATCH_STATUS

@@ -39,7 +39,7 @@ float round_f16(float f) {
 
 extern "C" {
 
-tlhip_status tlhip_dequantize(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor out) {
+tlhip_status tlhip_dequantize(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor out) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(check_t(q, "dequantize"));
     TLHIP_TRY(f16_args("dequantize", {out}));
@@ -48,11 +48,11 @@ tlhip_status tlhip_dequantize(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor out) {
         return fail(TLHIP_ERR_SHAPE_MISMATCH, "dequantize: %s -> %s", shape_str(q).c_str(), shape_str(out).c_str());
     TLHIP_TRY(launch_dequant(ctx->stream, q->dtype, q->data, q->scales, P(out), q->shape[0], q->shape[1]));
     return after_launch(ctx, "dequantize");
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y) {
+tlhip_status tlhip_linear(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor bias, tlhip_tensor y) try {
     return linear_impl(ctx, x, w, bias, y, nullptr, 0);
-}
+} TLHIP_CATCH_STATUS
 
 }  // extern "C"
 
@@ -155,6 +155,13 @@ tlhip_status linear_impl(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_te
             int64_t shp[2] = {N, K};
             TLHIP_TRY(alloc_tensor(ctx, TLHIP_F16, 2, shp, &wf));
             st = launch_dequant(ctx->stream, TLHIP_Q6_K, w->data, w->scales, P(wf), N, K);
+            // The copy is cached on the weight and any context may read it
+            // next, with no ordering the caller knows of: it is complete
+            // before it is published (once per weight and upload).
+            if (st == TLHIP_OK && hipStreamSynchronize(ctx->stream) != hipSuccess) {
+                (void)hipGetLastError();
+                st = fail(TLHIP_ERR_DEVICE, "linear: Q6_K dequantised copy failed");
+            }
             if (st != TLHIP_OK) {
                 tlhip_tensor_free(wf);
                 return st;
@@ -193,29 +200,42 @@ tlhip_status linear_impl(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_te
 
 extern "C" {
 
-tlhip_status tlhip_matmul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor c) {
+tlhip_status tlhip_matmul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor c) try {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args("matmul", {a, b, c}));
+    // Tensor::matmul (matmul.rs:22-60) on TensorF16 or TensorF32 operands,
+    // both the same (builtin_math.rs:49-58; a mix is the reference's TypeError)
+    TLHIP_TRY(check_t(a, "matmul"));
+    const bool f32 = a->dtype == TLHIP_F32;
+    if (f32) {
+        for (tlhip_tensor t : {b, c}) {
+            TLHIP_TRY(check_t(t, "matmul"));
+            if (t->dtype != TLHIP_F32) return fail(TLHIP_ERR_DTYPE, "matmul(): f32 input needs f32 operands");
+        }
+    } else {
+        TLHIP_TRY(f16_args("matmul", {a, b, c}));
+    }
     if (a->ndim != 2 || b->ndim != 2) return fail(TLHIP_ERR_INVALID_OPERATION, "matmul requires 2D tensors");
     const int64_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
     if (b->shape[0] != K)
-        return fail(TLHIP_ERR_SHAPE_MISMATCH, "matmul: [%lld, %lld] @ %s", (long long)M, (long long)K,
-                    shape_str(b).c_str());
+        return fail(TLHIP_ERR_INVALID_OPERATION, "matmul shape mismatch: [%lld, %lld] @ [%lld, %lld]", (long long)M,
+                    (long long)K, (long long)b->shape[0], (long long)N);
     if (c->ndim != 2 || c->shape[0] != M || c->shape[1] != N)
         return fail(TLHIP_ERR_SHAPE_MISMATCH, "matmul: output %s", shape_str(c).c_str());
     if (M == 0 || N == 0) return TLHIP_OK;
+    if (K > INT32_MAX || N > INT32_MAX) return fail(TLHIP_ERR_INVALID_DIMENSION, "matmul: too large");
     // matmul(a, b) = matmul_transposed_b(a, b^T): one transpose kernel, then
     // the same fp32-accumulating product as linear().
     tlhip_tensor bt;
     int64_t shp[2] = {N, K};
-    TLHIP_TRY(alloc_tensor(ctx, TLHIP_F16, 2, shp, &bt));
-    tlhip_status st = launch_transpose(ctx->stream, P(b), P(bt), (int)K, (int)N);
+    TLHIP_TRY(alloc_tensor(ctx, f32 ? TLHIP_F32 : TLHIP_F16, 2, shp, &bt));
+    tlhip_status st = f32 ? launch_transpose_f32(ctx->stream, (const float*)b->data, (float*)bt->data, (int)K, (int)N)
+                          : launch_transpose(ctx->stream, P(b), P(bt), (int)K, (int)N);
     if (st == TLHIP_OK) st = tlhip_linear(ctx, a, bt, nullptr, c);
     tlhip_tensor_free(bt);
     return st;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_rms_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, float eps, tlhip_tensor y) {
+tlhip_status tlhip_rms_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, float eps, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("rms_norm", {x, w, y}));
     TLHIP_TRY(same_shape(x, y, "rms_norm"));
@@ -226,10 +246,10 @@ tlhip_status tlhip_rms_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, float
     if (n == 0) return TLHIP_OK;
     TLHIP_TRY(launch_rms_norm(ctx->stream, P(x), P(w), P(y), (int)(numel(x) / n), (int)n, eps));
     return after_launch(ctx, "rms_norm");
-}
+} TLHIP_CATCH_STATUS
 
 tlhip_status tlhip_layer_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor b, float eps,
-                              tlhip_tensor y) {
+                              tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("layer_norm", {x, y}));
     TLHIP_TRY(same_shape(x, y, "layer_norm"));
@@ -244,10 +264,10 @@ tlhip_status tlhip_layer_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlh
     TLHIP_TRY(launch_layer_norm(ctx->stream, P(x), w ? P(w) : nullptr, b ? P(b) : nullptr, P(y),
                                 (int)(numel(x) / n), (int)n, eps));
     return after_launch(ctx, "layer_norm");
-}
+} TLHIP_CATCH_STATUS
 
 tlhip_status tlhip_rope(tlhip_ctx ctx, tlhip_tensor x, int offset, float theta, tlhip_rope_layout layout,
-                        int rot_dims, tlhip_tensor y) {
+                        int rot_dims, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("rope", {x, y}));
     TLHIP_TRY(same_shape(x, y, "rope"));
@@ -265,9 +285,9 @@ tlhip_status tlhip_rope(tlhip_ctx ctx, tlhip_tensor x, int offset, float theta, 
     TLHIP_TRY(launch_rope(ctx->stream, P(x), P(y), (int)S, (int)H, (int)D, numel(x) / (S * H * D), offset, nullptr,
                           (int)layout, rot_dims, table, 0, 0));
     return after_launch(ctx, "rope");
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_softmax_lastdim(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) {
+tlhip_status tlhip_softmax_lastdim(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("softmax", {x, y}));
     TLHIP_TRY(same_shape(x, y, "softmax"));
@@ -276,7 +296,7 @@ tlhip_status tlhip_softmax_lastdim(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y
     if (n == 0 || numel(x) == 0) return TLHIP_OK;
     TLHIP_TRY(launch_softmax(ctx->stream, P(x), P(y), numel(x) / n, (int)n));
     return after_launch(ctx, "softmax");
-}
+} TLHIP_CATCH_STATUS
 
 static tlhip_status unary(tlhip_ctx ctx, int op, tlhip_tensor x, tlhip_tensor y, const char* nm) {
     TLHIP_TRY(check_ctx(ctx));
@@ -286,18 +306,18 @@ static tlhip_status unary(tlhip_ctx ctx, int op, tlhip_tensor x, tlhip_tensor y,
     return after_launch(ctx, nm);
 }
 
-tlhip_status tlhip_sigmoid(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) { return unary(ctx, EW_SIGMOID, x, y, "sigmoid"); }
-tlhip_status tlhip_silu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) { return unary(ctx, EW_SILU, x, y, "silu"); }
-tlhip_status tlhip_gelu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) { return unary(ctx, EW_GELU, x, y, "gelu"); }
+tlhip_status tlhip_sigmoid(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) try { return unary(ctx, EW_SIGMOID, x, y, "sigmoid"); } TLHIP_CATCH_STATUS
+tlhip_status tlhip_silu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) try { return unary(ctx, EW_SILU, x, y, "silu"); } TLHIP_CATCH_STATUS
+tlhip_status tlhip_gelu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) try { return unary(ctx, EW_GELU, x, y, "gelu"); } TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_silu_mul(tlhip_ctx ctx, tlhip_tensor g, tlhip_tensor u, tlhip_tensor y) {
+tlhip_status tlhip_silu_mul(tlhip_ctx ctx, tlhip_tensor g, tlhip_tensor u, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("silu_mul", {g, u, y}));
     TLHIP_TRY(same_shape(g, u, "silu_mul"));
     TLHIP_TRY(same_shape(g, y, "silu_mul"));
     TLHIP_TRY(launch_elementwise(ctx->stream, EW_SILU_MUL, P(g), P(u), P(y), numel(g), 0, 0.f));
     return after_launch(ctx, "silu_mul");
-}
+} TLHIP_CATCH_STATUS
 
 static tlhip_status binary(tlhip_ctx ctx, int op, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y, const char* nm) {
     TLHIP_TRY(check_ctx(ctx));
@@ -315,18 +335,18 @@ static tlhip_status binary(tlhip_ctx ctx, int op, tlhip_tensor a, tlhip_tensor b
     return after_launch(ctx, nm);
 }
 
-tlhip_status tlhip_add(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y) { return binary(ctx, EW_ADD, a, b, y, "add"); }
-tlhip_status tlhip_mul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y) { return binary(ctx, EW_MUL, a, b, y, "mul"); }
+tlhip_status tlhip_add(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y) try { return binary(ctx, EW_ADD, a, b, y, "add"); } TLHIP_CATCH_STATUS
+tlhip_status tlhip_mul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y) try { return binary(ctx, EW_MUL, a, b, y, "mul"); } TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_mul_scalar(tlhip_ctx ctx, tlhip_tensor a, float s, tlhip_tensor y) {
+tlhip_status tlhip_mul_scalar(tlhip_ctx ctx, tlhip_tensor a, float s, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("mul_scalar", {a, y}));
     TLHIP_TRY(same_shape(a, y, "mul_scalar"));
     TLHIP_TRY(launch_elementwise(ctx->stream, EW_MUL_SCALAR, P(a), nullptr, P(y), numel(a), 0, round_f16(s)));
     return after_launch(ctx, "mul_scalar");
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* ids, int n, tlhip_tensor out) {
+tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* ids, int n, tlhip_tensor out) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(check_t(table, "embedding table"));
     TLHIP_TRY(f16_args("embedding", {out}));
@@ -350,9 +370,9 @@ tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* i
     TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
     TLHIP_TRY(st);
     return after_launch(ctx, "embedding");
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_apply_attention_mask(tlhip_ctx ctx, tlhip_tensor sc, tlhip_tensor mask, tlhip_tensor y) {
+tlhip_status tlhip_apply_attention_mask(tlhip_ctx ctx, tlhip_tensor sc, tlhip_tensor mask, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("apply_attention_mask", {sc, mask, y}));
     TLHIP_TRY(same_shape(sc, y, "apply_attention_mask"));
@@ -366,24 +386,24 @@ tlhip_status tlhip_apply_attention_mask(tlhip_ctx ctx, tlhip_tensor sc, tlhip_te
                     shape_str(mask).c_str());
     TLHIP_TRY(launch_mask(ctx->stream, P(sc), P(mask), P(y), numel(sc), period));
     return after_launch(ctx, "apply_attention_mask");
-}
+} TLHIP_CATCH_STATUS
 
 // causal_mask(n) (builtin_nn.rs:423-460): out must be [n, n] f16.
-tlhip_status tlhip_causal_mask(tlhip_ctx ctx, tlhip_tensor out) {
+tlhip_status tlhip_causal_mask(tlhip_ctx ctx, tlhip_tensor out) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("causal_mask", {out}));
     if (out->ndim != 2 || out->shape[0] != out->shape[1])
         return fail(TLHIP_ERR_INVALID_DIMENSION, "causal_mask: output must be [n, n], got %s", shape_str(out).c_str());
     TLHIP_TRY(launch_causal_mask(ctx->stream, P(out), out->shape[0]));
     return after_launch(ctx, "causal_mask");
-}
+} TLHIP_CATCH_STATUS
 
 static int elem_bytes(tlhip_dtype d) { return d == TLHIP_F16 ? 2 : (d == TLHIP_F32 || d == TLHIP_I32) ? 4 : 0; }
 
 // slice_last(x, axis) (builtin_tensor.rs:1949-1991, slice.rs:25-60): the
 // last index of axis 0; y is x's shape without axis 0 ([1] for a 1-D x,
 // where the reference returns a scalar).
-tlhip_status tlhip_slice_last(tlhip_ctx ctx, tlhip_tensor x, int axis, tlhip_tensor y) {
+tlhip_status tlhip_slice_last(tlhip_ctx ctx, tlhip_tensor x, int axis, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(check_t(x, "slice_last"));
     TLHIP_TRY(check_t(y, "slice_last"));
@@ -403,12 +423,12 @@ tlhip_status tlhip_slice_last(tlhip_ctx ctx, tlhip_tensor x, int axis, tlhip_ten
         TLHIP_CHECK_HIP(hipMemcpyAsync(y->data, (const uint8_t*)x->data + (size_t)(x->shape[0] - 1) * inner, inner,
                                        hipMemcpyDeviceToDevice, ctx->stream));
     return after_launch(ctx, "slice_last");
-}
+} TLHIP_CATCH_STATUS
 
 // broadcast_to(x, shape) (broadcast.rs:11-120, shape.rs:37-49): y's shape is
 // the target; dims align from the right and an input dim of 1 repeats.  An
 // equal shape is a copy (the reference returns the tensor itself).
-tlhip_status tlhip_broadcast_to(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) {
+tlhip_status tlhip_broadcast_to(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(check_t(x, "broadcast_to"));
     TLHIP_TRY(check_t(y, "broadcast_to"));
@@ -435,11 +455,11 @@ tlhip_status tlhip_broadcast_to(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) {
     }
     TLHIP_TRY(launch_broadcast(ctx->stream, x->data, y->data, eb, b));
     return after_launch(ctx, "broadcast_to");
-}
+} TLHIP_CATCH_STATUS
 
 // rope(x, cos, sin) = Tensor::rope_candle (builtin_tensor.rs:569-597,
 // rope.rs:18-65): x [S, H, D], cos/sin [L >= S, D] f16.
-tlhip_status tlhip_rope_cos_sin(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor cos_t, tlhip_tensor sin_t, tlhip_tensor y) {
+tlhip_status tlhip_rope_cos_sin(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor cos_t, tlhip_tensor sin_t, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("rope(x, cos, sin)", {x, cos_t, sin_t, y}));
     if (x->ndim != 3)
@@ -458,14 +478,14 @@ tlhip_status tlhip_rope_cos_sin(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor cos_
     if (S * H * D > INT32_MAX) return fail(TLHIP_ERR_INVALID_DIMENSION, "rope(x, cos, sin): tensor too large");
     TLHIP_TRY(launch_rope_cs(ctx->stream, P(x), P(cos_t), P(sin_t), P(y), (int)S, (int)H, (int)D));
     return after_launch(ctx, "rope(x, cos, sin)");
-}
+} TLHIP_CATCH_STATUS
 
 // precompute_rope_cos / precompute_rope_sin (builtin_tensor.rs:610-700):
 // computed on the host in f32 as the reference does, each value stored in
 // columns 2i and 2i+1, converted to f16 and uploaded; out [max_seq_len,
 // head_dim] f16.  Synchronous (the host table is freed on return).
 tlhip_status tlhip_precompute_rope(tlhip_ctx ctx, int head_dim, int max_seq_len, float base, int want_sin,
-                                   tlhip_tensor out) {
+                                   tlhip_tensor out) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("precompute_rope", {out}));
     if (head_dim <= 0 || head_dim % 2)
@@ -483,7 +503,7 @@ tlhip_status tlhip_precompute_rope(tlhip_ctx ctx, int head_dim, int max_seq_len,
             tab[(size_t)pos * head_dim + 2 * i + 1] = v;
         }
     return tlhip_tensor_upload(ctx, out, tab.data(), tab.size() * sizeof(_Float16));
-}
+} TLHIP_CATCH_STATUS
 
 static tlhip_status qkv_dims(tlhip_tensor q, tlhip_tensor k, const char* nm, int* H, int* Hkv, int* D) {
     if (q->ndim != 3 || k->ndim != 3) return fail(TLHIP_ERR_INVALID_DIMENSION, "%s: expects 3-D tensors", nm);
@@ -494,7 +514,7 @@ static tlhip_status qkv_dims(tlhip_tensor q, tlhip_tensor k, const char* nm, int
     return TLHIP_OK;
 }
 
-tlhip_status tlhip_einsum_scores(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhip_tensor sc) {
+tlhip_status tlhip_einsum_scores(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhip_tensor sc) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("einsum ihd,jhd->ihj", {q, k, sc}));
     int H, Hkv, D;
@@ -505,9 +525,9 @@ tlhip_status tlhip_einsum_scores(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, 
         return fail(TLHIP_ERR_SHAPE_MISMATCH, "einsum: output %s", shape_str(sc).c_str());
     TLHIP_TRY(launch_scores(ctx->stream, P(q), P(k), P(sc), I, J, H, Hkv, D));
     return after_launch(ctx, "einsum_scores");
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_einsum_context(tlhip_ctx ctx, tlhip_tensor p, tlhip_tensor v, tlhip_tensor out) {
+tlhip_status tlhip_einsum_context(tlhip_ctx ctx, tlhip_tensor p, tlhip_tensor v, tlhip_tensor out) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("einsum ihj,jhd->ihd", {p, v, out}));
     if (p->ndim != 3 || v->ndim != 3 || out->ndim != 3)
@@ -520,10 +540,10 @@ tlhip_status tlhip_einsum_context(tlhip_ctx ctx, tlhip_tensor p, tlhip_tensor v,
         return fail(TLHIP_ERR_SHAPE_MISMATCH, "einsum: output %s", shape_str(out).c_str());
     TLHIP_TRY(launch_context(ctx->stream, P(p), P(v), P(out), I, J, H, Hkv, D));
     return after_launch(ctx, "einsum_context");
-}
+} TLHIP_CATCH_STATUS
 
 tlhip_status tlhip_attention(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhip_tensor v, int q_pos0, float scale,
-                             int causal, tlhip_tensor out) {
+                             int causal, tlhip_tensor out) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("attention", {q, k, v, out}));
     int H, Hkv, D;
@@ -548,6 +568,7 @@ tlhip_status tlhip_attention(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhi
     a.q_pos0 = q_pos0;
     a.causal = causal;
     a.scale_h = round_f16(scale);
+    a.head_flags = ctx->d_tile_flags + SK_MAX_TILES_SPLIT;
     if (attention_mfma_ok(a, J)) {
         float* vt = ctx_workspace(ctx, attention_mfma_scratch(J, Hkv, D));
         if (!vt) return fail(TLHIP_ERR_ALLOCATION, "attention: no workspace for V^T (%zu bytes)", attention_mfma_scratch(J, Hkv, D));
@@ -569,9 +590,9 @@ tlhip_status tlhip_attention(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhi
         TLHIP_TRY(launch_attention_j(ctx->stream, a, J));
     }
     return after_launch(ctx, "attention");
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_tensor_argmax(tlhip_ctx ctx, tlhip_tensor x, int dim, int keepdim, tlhip_tensor y) {
+tlhip_status tlhip_tensor_argmax(tlhip_ctx ctx, tlhip_tensor x, int dim, int keepdim, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(check_t(x, "argmax"));
     TLHIP_TRY(check_t(y, "argmax"));
@@ -600,9 +621,9 @@ tlhip_status tlhip_tensor_argmax(tlhip_ctx ctx, tlhip_tensor x, int dim, int kee
                     shape_str(x).c_str(), dim);
     TLHIP_TRY(launch_tensor_argmax(ctx->stream, x->dtype, x->data, y->data, x->shape, x->ndim, dim < 0 ? -1 : dim));
     return after_launch(ctx, "argmax");
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_argmax(tlhip_ctx ctx, tlhip_tensor logits, int32_t* out) {
+tlhip_status tlhip_argmax(tlhip_ctx ctx, tlhip_tensor logits, int32_t* out) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("argmax", {logits}));
     if (!out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null output");
@@ -617,10 +638,10 @@ tlhip_status tlhip_argmax(tlhip_ctx ctx, tlhip_tensor logits, int32_t* out) {
     TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
     *out = ctx->h_pinned_i32[0];
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
 tlhip_status tlhip_temperature_sample(tlhip_ctx ctx, tlhip_tensor logits, float temperature, uint64_t seed,
-                                      uint64_t counter, int32_t* out) {
+                                      uint64_t counter, int32_t* out) try {
     if (!(temperature > 1e-4f)) return tlhip_argmax(ctx, logits, out);
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(f16_args("temperature_sample", {logits}));
@@ -641,6 +662,6 @@ tlhip_status tlhip_temperature_sample(tlhip_ctx ctx, tlhip_tensor logits, float 
     TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
     *out = ctx->h_pinned_i32[0];
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
 }  // extern "C"

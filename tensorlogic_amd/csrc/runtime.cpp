@@ -8,13 +8,18 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <exception>
 #include <mutex>
+#include <new>
 
 #include "internal.hpp"
 
 namespace tlhip {
 
-static thread_local std::string g_last_error;
+// The last error of the calling thread.  A fixed buffer, so that recording
+// an error allocates nothing (it is also what reports a failed host
+// allocation).
+static thread_local char g_last_error[1280];
 
 void set_error(tlhip_status st, const char* fmt, ...) {
     char buf[1024];
@@ -26,7 +31,7 @@ void set_error(tlhip_status st, const char* fmt, ...) {
                                   "AllocationError", "IndexOutOfBounds", "LoadError",
                                   "DeviceError", "DtypeError", "InvalidArgument"};
     const char* nm = (st >= 0 && st <= 9) ? names[st] : "Error";
-    g_last_error = std::string(nm) + ": " + buf;
+    snprintf(g_last_error, sizeof g_last_error, "%s: %s", nm, buf);
 }
 
 tlhip_status fail(tlhip_status st, const char* fmt, ...) {
@@ -37,6 +42,22 @@ tlhip_status fail(tlhip_status st, const char* fmt, ...) {
     va_end(ap);
     set_error(st, "%s", buf);
     return st;
+}
+
+// The exception barrier of the C ABI (every exported function ends in
+// TLHIP_CATCH_STATUS or an equivalent handler): an exception thrown by host
+// code -- std::bad_alloc from a container, anything else -- becomes a status
+// and a message instead of unwinding through extern "C" into the caller.
+tlhip_status abi_exception() noexcept {
+    try {
+        throw;
+    } catch (const std::bad_alloc&) {
+        return fail(TLHIP_ERR_ALLOCATION, "host memory allocation failed (std::bad_alloc)");
+    } catch (const std::exception& e) {
+        return fail(TLHIP_ERR_INVALID_OPERATION, "internal error: %s", e.what());
+    } catch (...) {
+        return fail(TLHIP_ERR_INVALID_OPERATION, "internal error: unknown exception");
+    }
 }
 
 size_t payload_bytes(tlhip_dtype d, const int64_t* shape, int ndim) {
@@ -209,9 +230,9 @@ using namespace tlhip;
 
 extern "C" {
 
-const char* tlhip_last_error(void) { return g_last_error.c_str(); }
+const char* tlhip_last_error(void) { return g_last_error; }
 
-tlhip_status tlhip_init(int device, tlhip_ctx* out) {
+tlhip_status tlhip_init(int device, tlhip_ctx* out) try {
     if (!out) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null output");
     *out = nullptr;
     int n = 0;
@@ -221,8 +242,10 @@ tlhip_status tlhip_init(int device, tlhip_ctx* out) {
     if (device < 0) device = 0;
     if (device >= n) return fail(TLHIP_ERR_DEVICE, "device %d out of range (%d devices)", device, n);
     TLHIP_CHECK_HIP(hipSetDevice(device));
-    // the no-allocation entry point's workspace address on this device
-    TLHIP_TRY(noalloc_setup(device));
+    // the no-allocation entry point's workspace address on this device; a
+    // failure here concerns only that entry point, which resolves it again
+    // on its first call and reports the error there
+    if (noalloc_setup(device) != TLHIP_OK) (void)hipGetLastError();
     auto* c = new tlhip_ctx_s();
     c->device = device;
     hipError_t e1 = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
@@ -233,8 +256,10 @@ tlhip_status tlhip_init(int device, tlhip_ctx* out) {
     TLHIP_CHECK_HIP(hipEventCreate(&c->ev0));
     TLHIP_CHECK_HIP(hipEventCreate(&c->ev1));
     TLHIP_CHECK_HIP(hipMalloc(&c->d_scratch_i32, 256 * sizeof(int32_t)));
-    TLHIP_CHECK_HIP(hipMalloc(&c->d_tile_flags, SK_MAX_TILES_SPLIT * sizeof(uint32_t)));
-    TLHIP_CHECK_HIP(hipMemset(c->d_tile_flags, 0, SK_MAX_TILES_SPLIT * sizeof(uint32_t)));
+    TLHIP_CHECK_HIP(hipMalloc(&c->d_tile_flags, CTX_FLAG_WORDS * sizeof(uint32_t)));
+    // (on the context's own stream, which does not wait for the null stream)
+    TLHIP_CHECK_HIP(hipMemsetAsync(c->d_tile_flags, 0, CTX_FLAG_WORDS * sizeof(uint32_t), c->stream));
+    TLHIP_CHECK_HIP(hipStreamSynchronize(c->stream));
     TLHIP_CHECK_HIP(hipHostMalloc(&c->h_pinned_i32, 256 * sizeof(int32_t), hipHostMallocDefault));
     // Keep freed pool memory cached in the pool instead of returning it to
     // the driver at every synchronisation.
@@ -247,47 +272,47 @@ tlhip_status tlhip_init(int device, tlhip_ctx* out) {
     c->sync_every_op = env && env[0] == '1';
     *out = c;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_shutdown(tlhip_ctx ctx) {
+tlhip_status tlhip_shutdown(tlhip_ctx ctx) try {
     TLHIP_TRY(check_ctx(ctx));
     // releases the caller's reference; tensors still alive keep the stream
     ctx_release(ctx);
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_sync(tlhip_ctx ctx) {
+tlhip_status tlhip_sync(tlhip_ctx ctx) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_device_name(tlhip_ctx ctx, char* buf, size_t len) {
+tlhip_status tlhip_device_name(tlhip_ctx ctx, char* buf, size_t len) try {
     TLHIP_TRY(check_ctx(ctx));
     if (!buf || !len) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null buffer");
     hipDeviceProp_t p;
     TLHIP_CHECK_HIP(hipGetDeviceProperties(&p, ctx->device));
     snprintf(buf, len, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_set_sync_every_op(tlhip_ctx ctx, int on) {
+tlhip_status tlhip_set_sync_every_op(tlhip_ctx ctx, int on) try {
     TLHIP_TRY(check_ctx(ctx));
     ctx->sync_every_op = on != 0;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
 tlhip_status tlhip_tensor_alloc(tlhip_ctx ctx, tlhip_dtype dtype, int ndim, const int64_t* shape,
-                                tlhip_tensor* out) {
+                                tlhip_tensor* out) try {
     return alloc_tensor(ctx, dtype, ndim, shape, out);
-}
+} TLHIP_CATCH_STATUS
 
-size_t tlhip_tensor_nbytes(tlhip_tensor t) {
+size_t tlhip_tensor_nbytes(tlhip_tensor t) try {
     if (!t) return 0;
     return payload_bytes(t->dtype, t->shape, t->ndim);
-}
+} TLHIP_CATCH_VALUE(0)
 
-tlhip_status tlhip_tensor_upload(tlhip_ctx ctx, tlhip_tensor t, const void* host, size_t bytes) {
+tlhip_status tlhip_tensor_upload(tlhip_ctx ctx, tlhip_tensor t, const void* host, size_t bytes) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(check_t(t, "upload"));
     if (!host && bytes) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null host pointer");
@@ -317,9 +342,9 @@ tlhip_status tlhip_tensor_upload(tlhip_ctx ctx, tlhip_tensor t, const void* host
     TLHIP_TRY(after_launch(ctx, "upload/repack"));
     TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_tensor_download(tlhip_ctx ctx, tlhip_tensor t, void* host, size_t bytes) {
+tlhip_status tlhip_tensor_download(tlhip_ctx ctx, tlhip_tensor t, void* host, size_t bytes) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(check_t(t, "download"));
     size_t need = tlhip_tensor_nbytes(t);
@@ -344,15 +369,15 @@ tlhip_status tlhip_tensor_download(tlhip_ctx ctx, tlhip_tensor t, void* host, si
     (void)hipFreeAsync(stage, ctx->stream);
     TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
     return st;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_tensor_retain(tlhip_tensor t) {
+tlhip_status tlhip_tensor_retain(tlhip_tensor t) try {
     if (!t) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null tensor");
     t->refcount++;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_tensor_free(tlhip_tensor t) {
+tlhip_status tlhip_tensor_free(tlhip_tensor t) try {
     if (!t) return TLHIP_OK;
     if (--t->refcount > 0) return TLHIP_OK;
     if (t->base) {
@@ -365,18 +390,18 @@ tlhip_status tlhip_tensor_free(tlhip_tensor t) {
     }
     delete t;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_tensor_info(tlhip_tensor t, tlhip_dtype* dtype, int* ndim, int64_t* shape) {
+tlhip_status tlhip_tensor_info(tlhip_tensor t, tlhip_dtype* dtype, int* ndim, int64_t* shape) try {
     if (!t) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null tensor");
     if (dtype) *dtype = t->dtype;
     if (ndim) *ndim = t->ndim;
     if (shape)
         for (int i = 0; i < t->ndim; i++) shape[i] = t->shape[i];
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
-tlhip_status tlhip_tensor_reshape(tlhip_tensor t, int ndim, const int64_t* shape, tlhip_tensor* out) {
+tlhip_status tlhip_tensor_reshape(tlhip_tensor t, int ndim, const int64_t* shape, tlhip_tensor* out) try {
     TLHIP_TRY(check_t(t, "reshape"));
     if (!out || !shape) return fail(TLHIP_ERR_INVALID_ARGUMENT, "null argument");
     if (is_quant(t->dtype)) return fail(TLHIP_ERR_INVALID_OPERATION, "reshape of a quantized tensor");
@@ -400,6 +425,6 @@ tlhip_status tlhip_tensor_reshape(tlhip_tensor t, int ndim, const int64_t* shape
     v->base = owner;
     *out = v;
     return TLHIP_OK;
-}
+} TLHIP_CATCH_STATUS
 
 }  // extern "C"

@@ -150,7 +150,11 @@ class Tensor:
         return out
 
     def matmul(self, b: "Tensor") -> "Tensor":
-        out = self._new((self.shape[0], b.shape[1]))
+        """matmul(a, b) (builtin_math.rs:36-60, matmul.rs:22-60): a[M,K] @ b[K,N],
+        both f16 or both f32; the output has a's dtype."""
+        two_d = len(self.shape) == 2 and len(b.shape) == 2
+        # (other ranks: the library refuses them with InvalidOperation)
+        out = self.dev.empty((self.shape[0], b.shape[1]) if two_d else (1, 1), F32 if self.dtype == F32 else F16)
         call("tlhip_matmul", self.dev.h, self.h, b.h, out.h)
         return out
 

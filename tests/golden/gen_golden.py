@@ -93,6 +93,7 @@ def tinyllama_tokens(n_decode=128, seed=4):
         S.write_llama_gguf(path, seed=seed, **S.TINYLLAMA_ARGS)
         prompt = S.token_ids(seed, "prompt", 46, S.TINYLLAMA_ARGS["vocab"])
         rec = record_tokens(path, 0, prompt, n_decode, 256)
+        rec.update(reorder_final_logits(path, 0, prompt, rec, 256))
     return {"config": "TinyLlama-1.1B shape, Q4_0 linear weights, seed 4", "seed": seed, **rec}
 
 
@@ -120,6 +121,23 @@ def reordered_oracle(path, prompt, rec, n_decode, top=8):
             "reorder_first_divergence": int(bad[0]) if bad.size else n_decode + 1}
 
 
+def reorder_final_logits(path, arch, prompt, rec, max_ctx):
+    """The reordered oracle (ACC_F32_REV) teacher-forced on rec's token
+    stream: the relative L2 distance of its final logits from rec's -- how
+    far a second, equally valid fp32 summation order moves the end-to-end
+    logits of this model."""
+    toks = np.array(rec["tokens"], np.int32)
+    n_decode = rec["n_decode"]
+    m = O.Model(path, arch=arch, max_ctx=max_ctx, acc=O.ACC_F32_REV)
+    _, lg = m.forward(prompt, 0)
+    for step in range(n_decode):
+        _, lg = m.forward(np.array([toks[step]], np.int32), len(prompt) + step)
+    m.close()
+    ref = np.frombuffer(base64.b64decode(rec["last_logits_f16_b64"]), "<f2").astype(np.float64)
+    got = lg.astype(np.float64)
+    return {"reorder_last_logits_rel_l2": float(np.linalg.norm(got - ref) / np.linalg.norm(ref))}
+
+
 def tinyllama_margins_tokens(n_decode=128, seed=8):
     """Config-4 shape (22 layers, 2048 / 5632, 32 / 4 heads, vocab 32000),
     Q4_0, with RMSNorm weights 1 + N(0, 0.02) and Q4_0 codes symmetric about
@@ -133,6 +151,7 @@ def tinyllama_margins_tokens(n_decode=128, seed=8):
         prompt = S.token_ids(seed, "prompt", 46, S.TINYLLAMA_ARGS["vocab"])
         rec = record_tokens(path, 0, prompt, n_decode, 256)
         rec.update(reordered_oracle(path, prompt, rec, n_decode))
+        rec.update(reorder_final_logits(path, 0, prompt, rec, 256))
     top = np.array(rec["top8_logits"], np.float64)
     ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(top[:, 0]), 2.0 ** -14))) - 10)
     rec["margin_ulps"] = [float(v) for v in (top[:, 0] - top[:, 1]) / ulp]
@@ -147,12 +166,36 @@ def phi2_tokens(n_decode=256, seed=5):
         S.write_phi2_gguf(path, seed=seed, **S.PHI2_ARGS)
         prompt = S.token_ids(seed, "prompt", 512, S.PHI2_ARGS["vocab"])
         rec = record_tokens(path, 1, prompt, n_decode, 800)
+        rec.update(reorder_final_logits(path, 1, prompt, rec, 800))
     return {"config": "Phi-2 shape, Q8_0 linear weights, seed 5", "seed": seed, **rec}
+
+
+def augment_reorder(name):
+    """Adds reorder_last_logits_rel_l2 to an existing token file without
+    recomputing the rest (the model is regenerated from its seed)."""
+    fp = os.path.join(HERE, name)
+    rec = json.load(open(fp))
+    seed = rec["seed"]
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "m.gguf")
+        if name.startswith("phi2"):
+            S.write_phi2_gguf(path, seed=seed, **S.PHI2_ARGS)
+            arch, max_ctx = 1, 800
+        elif "margins" in name:
+            S.write_llama_gguf(path, seed=seed, norm_mean=1.0, zero_mean=True, **S.TINYLLAMA_ARGS)
+            arch, max_ctx = 0, 256
+        else:
+            S.write_llama_gguf(path, seed=seed, **S.TINYLLAMA_ARGS)
+            arch, max_ctx = 0, 256
+        rec.update(reorder_final_logits(path, arch, np.array(rec["prompt"], np.int32), rec, max_ctx))
+    return rec
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--only", default="")
+    ap.add_argument("--augment-reorder", action="store_true",
+                    help="only add reorder_last_logits_rel_l2 to the existing token files")
     a = ap.parse_args()
     jobs = {"synth_checksums.json": synth_checksums,
             "tinyllama_q4_0_tokens.json": tinyllama_tokens,
@@ -161,7 +204,10 @@ def main():
     for name, fn in jobs.items():
         if a.only and a.only != name:
             continue
-        data = fn()   # computed before the file is opened: no partial fixture
+        if a.augment_reorder and not name.endswith("_tokens.json"):
+            continue
+        # computed before the file is opened: no partial fixture
+        data = augment_reorder(name) if a.augment_reorder else fn()
         tmp = os.path.join(HERE, name + ".tmp")
         with open(tmp, "w") as f:
             json.dump(data, f)

@@ -16,26 +16,32 @@ from tensorlogic_amd import Model
 from tensorlogic_amd.gguf import GGML_F16, GGML_F32, GGML_Q4_0, GGML_Q8_0
 from tensorlogic_amd import synth as S
 
-from test_gpu_ops import assert_close
+from test_gpu_ops import _log_figures, assert_close, assert_logits_close, reorder_rel_l2
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 TINY_LLAMA = dict(n_layers=2, hidden=256, inter=512, n_heads=4, n_kv=2, vocab=1000)
 TINY_PHI2 = dict(n_layers=2, hidden=320, inter=1280, n_heads=4, vocab=1000, rot=32)
+# bound on the device's teacher-forced logit deviation in the margins test, as
+# a multiple of the reordered oracle's (largest and mean); measured on MI355X:
+# device 15.0 / 8.34 f16 ulps (largest / mean) against the reordered oracle's
+# 12 / 5.81, ratios 1.25 and 1.44
+DEV_RATIO = 1.5
 
 
 def _compare(dev, oracle, path, arch, prompt, n_decode, max_ctx=256):
     om = oracle.Model(path, arch=arch, max_ctx=max_ctx)
     ref_toks, margins, ref_logits = om.generate(prompt, n_decode)
     om.close()
+    rrl = reorder_rel_l2(oracle, path, arch, prompt, ref_toks, ref_logits, max_ctx)
     m = Model(dev, path, arch=arch, max_ctx=max_ctx)
     for use_graph in (False, True):
         toks = m.generate(prompt, n_decode, use_graph=use_graph)
         mism = np.nonzero(toks != ref_toks)[0]
         assert mism.size == 0, (f"graph={use_graph}: first mismatch at step {mism[0]}: "
                                 f"{toks[mism[0]]} vs {ref_toks[mism[0]]} (oracle margin {margins[mism[0]]:.3g})")
-        assert_close(m.logits(), ref_logits, what="final logits")
+        assert_logits_close(m.logits(), ref_logits, rrl)
     # host-driven prefill / decode API gives the same stream
     m.reset()
     t = m.prefill(prompt)
@@ -205,7 +211,7 @@ def _teacher_forced(dev, path, arch, g, max_ctx):
             mism.append((step, int(tok), int(ref[step]), float(margins[step])))
     print(f"teacher-forced: worst top-k deviation {worst_ulps:.2f} ulp; near-tie steps {exempt}")
     assert not mism, f"argmax differs at determined steps (step, device, oracle, margin): {mism}"
-    assert_close(m.logits(), _last_logits(g), what="final logits")
+    assert_logits_close(m.logits(), _last_logits(g), g.get("reorder_last_logits_rel_l2", 0.0))
     # free-running graph replay agrees up to the first near-tie
     toks = m.generate(prompt, n, use_graph=True)
     first = exempt[0] if exempt else n + 1
@@ -260,7 +266,7 @@ def test_tinyllama_margins_free_running(dev, tmp_path):
     the margin is 7 ulps.  So no implementation that sums in another order
     reproduces all 129 free-running tokens, and the checks are:
       * teacher-forced on the oracle's stream, the device's top-8 deviation
-        stays within twice the reordered oracle's (largest and mean), and
+        stays within 1.5 times the reordered oracle's (largest and mean), and
         its argmax equals the oracle's at every step whose margin exceeds
         twice the larger of the two deviations there;
       * free-running, graph replay and direct launches give the same 129
@@ -293,10 +299,11 @@ def test_tinyllama_margins_free_running(dev, tmp_path):
         if margin[step] > 2 * max(d, rdev[step]) and tok != ref[step]:
             mism.append((step, int(tok), int(ref[step]), float(margin[step])))
     ddev = np.array(ddev)
-    print(f"teacher-forced deviation (f16 ulps): device max {ddev.max():.1f} mean {ddev.mean():.2f}; "
-          f"reordered oracle max {rdev.max():.1f} mean {rdev.mean():.2f}")
-    assert ddev.max() <= 2 * rdev.max(), "device deviation beyond twice a reordered oracle's"
-    assert ddev.mean() <= 2 * rdev.mean(), "device deviation beyond twice a reordered oracle's (mean)"
+    figs = (f"teacher-forced deviation (f16 ulps): device max {ddev.max():.1f} mean {ddev.mean():.2f}; "
+            f"reordered oracle max {rdev.max():.1f} mean {rdev.mean():.2f}")
+    print(figs)
+    assert ddev.max() <= DEV_RATIO * rdev.max(), f"device deviation beyond {DEV_RATIO}x a reordered oracle's: {figs}"
+    assert ddev.mean() <= DEV_RATIO * rdev.mean(), f"device mean deviation beyond {DEV_RATIO}x a reordered oracle's: {figs}"
     assert not mism, f"argmax differs at determined steps (step, device, oracle, margin): {mism}"
     # free-running
     streams = {}
@@ -311,6 +318,11 @@ def test_tinyllama_margins_free_running(dev, tmp_path):
     first_bad = int(bad[0]) if bad.size else n + 1
     print(f"free-running: first divergence {first_bad} (reordered oracle: "
           f"{g['reorder_first_divergence']}); {len(set(ref.tolist()))} distinct ids in {n + 1} steps")
+    _log_figures({"what": "tinyllama margins model", "dev_max_ulps": float(ddev.max()),
+                  "dev_mean_ulps": float(ddev.mean()), "reorder_max_ulps": float(rdev.max()),
+                  "reorder_mean_ulps": float(rdev.mean()), "first_divergence": first_bad,
+                  "first_near_tie": first_tie, "reorder_first_divergence": int(g["reorder_first_divergence"]),
+                  "n_steps": n + 1})
     assert first_bad >= first_tie, f"stream leaves the oracle's at step {first_bad} before any near-tie"
     if bad.size:
         assert margin[first_bad] <= 2 * ddev.max(), (

@@ -5,6 +5,9 @@ matmul / layer outputs within max-abs 2e-2 and relative L2 1e-3 of the
 fp32-accumulated oracle (the oracle stores f16 exactly where the reference
 does).  Elementwise ops that evaluate exp/tanh are held to 1 f16 ulp.
 """
+import json
+import os
+
 import numpy as np
 import pytest
 
@@ -25,14 +28,24 @@ def f16_ulp(x):
     return 2.0 ** (e - 10)
 
 
+def _log_figures(rec):
+    """Append one parity record (JSON line) to $TL_PARITY_LOG when it is set."""
+    path = os.environ.get("TL_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(rec) + "\n")
+
+
 def assert_close(got, ref, max_abs=MAX_ABS, rel_l2=REL_L2, what=""):
-    """max-abs <= 2e-2 (or one f16 ulp of the reference value where that is
-    coarser) and rel-L2 <= 1e-3.  Both sides are f16 results: two fp32 sums
-    taken in different orders round to neighbouring f16 values now and then,
-    and on small outputs (the random-init model's logits are ~0.1, where one
-    ulp is ~1e-3 relative) that alone reaches the 1e-3 bar.  So the rel-L2
-    counts each element's difference beyond one f16 ulp of the reference; the
-    plain rel-L2 is reported beside it."""
+    """The north star's bars: plain relative L2 ||got - ref|| / ||ref|| <= 1e-3
+    and max-abs <= 2e-2.
+
+    One named relaxation of the max-abs bar: where the reference value is
+    beyond |32|, one f16 ulp (2^-5 and up) is itself coarser than 2e-2, and
+    two fp32 sums taken in different orders round to neighbouring f16 values
+    now and then, so there the element bound is one f16 ulp of the reference
+    value.  The rel-L2 is asserted plain; the rel-L2 of each element's
+    difference beyond one f16 ulp is reported beside it as a diagnostic."""
     g = np.asarray(got, np.float64).ravel()
     r = np.asarray(ref, np.float64).ravel()
     assert g.shape == r.shape, what
@@ -40,13 +53,49 @@ def assert_close(got, ref, max_abs=MAX_ABS, rel_l2=REL_L2, what=""):
     d = np.abs(g - r)
     ma = float(d.max()) if d.size else 0.0
     nr = max(np.linalg.norm(r), 1e-30)
-    rl_raw = float(np.linalg.norm(d) / nr) if d.size else 0.0
-    rl = float(np.linalg.norm(np.maximum(d - f16_ulp(r), 0.0)) / nr) if d.size else 0.0
+    rl = float(np.linalg.norm(d) / nr) if d.size else 0.0
+    rl_ulp = float(np.linalg.norm(np.maximum(d - f16_ulp(r), 0.0)) / nr) if d.size else 0.0
     bound = np.maximum(max_abs, f16_ulp(r))
     bad = np.nonzero(d > bound)[0]
-    assert bad.size == 0 and rl <= rel_l2, (f"{what}: max_abs {ma:.3e} rel_l2 beyond 1 ulp {rl:.3e} "
-                                           f"(plain {rl_raw:.3e}); {bad.size} elements beyond max(2e-2, 1 ulp)")
+    _log_figures({"what": what, "n": int(d.size), "max_abs": ma, "rel_l2": rl, "rel_l2_beyond_ulp": rl_ulp,
+                  "max_ref": float(np.abs(r).max()) if d.size else 0.0})
+    assert bad.size == 0 and rl <= rel_l2, (f"{what}: max_abs {ma:.3e} rel_l2 {rl:.3e} (beyond 1 ulp "
+                                           f"{rl_ulp:.3e}); {bad.size} elements beyond max(2e-2, 1 ulp)")
     return ma, rl
+
+
+# Named exemption of the rel-L2 bar: end-to-end decoder logits.
+LOGITS_REORDER_RATIO = 1.5
+
+
+def assert_logits_close(got, ref, reorder_rel_l2, what="final logits"):
+    """End-to-end decoder logits, after every layer and decode step of a
+    model.  The north star's bars are for matmul and layer outputs (held
+    plain by assert_close everywhere else); at the end of a decoder the f16
+    roundings of every earlier op have compounded, and two equally valid
+    fp32 summation orders already differ by about the 1e-3 bar there: the
+    oracle with every sum in descending order (ACC_F32_REV) is 0.80-1.0e-3
+    from the oracle on the 2-layer program models.  So the rel-L2 bound here
+    is max(1e-3, 1.5 x the reordered oracle's own distance on the same model
+    and token stream), reorder_rel_l2; the max-abs bar is assert_close's."""
+    bound = max(REL_L2, LOGITS_REORDER_RATIO * reorder_rel_l2)
+    _log_figures({"what": f"{what} (reordered oracle)", "reorder_rel_l2": float(reorder_rel_l2), "bound": bound})
+    return assert_close(got, ref, rel_l2=bound, what=f"{what} (reordered oracle at {reorder_rel_l2:.3e})")
+
+
+def reorder_rel_l2(oracle, path, arch, prompt, ref_toks, ref_logits, max_ctx, literal=None):
+    """The reordered oracle (ACC_F32_REV) teacher-forced on ref_toks: the
+    relative L2 distance of its final logits from ref_logits."""
+    m = oracle.Model(path, arch=arch, max_ctx=max_ctx, acc=oracle.ACC_F32_REV)
+    if literal is not None:
+        m.set_program_semantics(literal)
+    prompt = np.asarray(prompt, np.int32)
+    _, lg = m.forward(prompt, 0)
+    for step in range(len(ref_toks) - 1):
+        _, lg = m.forward(np.array([ref_toks[step]], np.int32), len(prompt) + step)
+    m.close()
+    r = np.asarray(ref_logits, np.float64).ravel()
+    return float(np.linalg.norm(np.asarray(lg, np.float64).ravel() - r) / np.linalg.norm(r))
 
 
 def ulp_diff(a, b):
@@ -301,6 +350,61 @@ def test_matmul_known_answer(dev):
     a = dev.tensor(np.array([[1, 2], [3, 4]], np.float16))
     b = dev.tensor(np.array([[5, 6], [7, 8]], np.float16))
     assert a.matmul(b).numpy().astype(np.float32).tolist() == [[19, 22], [43, 50]]
+
+
+@pytest.mark.parametrize("M,K,N", [(33, 65, 130), (1, 64, 33), (5, 32, 1), (46, 2048, 5632), (512, 2048, 2048),
+                                   (7, 100, 31)])
+def test_matmul_oracle(dev, oracle, M, K, N):
+    """matmul(a, b) = a[M,K] @ b[K,N] (matmul.rs:22-60, builtin_math.rs:36-60)
+    at shapes that cross the transpose's 32 x 32 tiles with ragged edges, and
+    at the config-2 / prefill shapes.  Two checks: the oracle's fp32-
+    accumulated product of a and b^T (the rel-L2 / max-abs bars), and
+    integer-valued operands in {-1, 0, 1}, whose products and sums are exact
+    in fp32 and in f16 (|sum| <= K <= 2048), so the result must equal numpy's
+    integer product bit for bit -- a transposed or shifted element of b fails
+    it whatever the summation order."""
+    a = S.normal_f16(31, f"mma{M}x{K}", (M, K))
+    b = S.normal_f16(31, f"mmb{K}x{N}", (K, N))
+    y = dev.tensor(a).matmul(dev.tensor(b)).numpy()
+    assert y.shape == (M, N)
+    ref = oracle.linear(a, np.ascontiguousarray(b.T))
+    assert_close(y, ref, what=f"matmul {M}x{K} @ {K}x{N}")
+    rng = np.random.default_rng(M * 7 + K * 3 + N)
+    ai = rng.integers(-1, 2, (M, K)).astype(np.int64)
+    bi = rng.integers(-1, 2, (K, N)).astype(np.int64)
+    yi = dev.tensor(ai.astype(np.float16)).matmul(dev.tensor(bi.astype(np.float16))).numpy()
+    assert np.array_equal(yi.astype(np.int64), ai @ bi)
+
+
+@pytest.mark.parametrize("M,K,N", [(33, 65, 130), (46, 2048, 300), (1, 7, 5)])
+def test_matmul_f32(dev, oracle, M, K, N):
+    """matmul on TensorF32 operands (builtin_math.rs:55-58): every output is
+    the k-ordered fused sum of matmul_tiled_32x32_f32 / matmul_tiled_f32 /
+    matmul_f32 (unified.metal:337-500; zero padding adds nothing), i.e. the
+    oracle's f32 linear of a and b^T, bit for bit."""
+    from tensorlogic_amd import F32
+    rng = np.random.default_rng(M + 3 * K + 5 * N)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b = (0.05 * rng.standard_normal((K, N))).astype(np.float32)
+    got = dev.tensor(a, F32).matmul(dev.tensor(b, F32)).numpy()
+    want = oracle.linear_f32(a, np.ascontiguousarray(b.T))
+    assert got.dtype == np.float32 and got.shape == (M, N)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    with pytest.raises(TLHipError) as e:
+        dev.tensor(a, F32).matmul(dev.tensor(b.astype(np.float16)))
+    assert e.value.kind == "DtypeError"
+
+
+def test_matmul_shape_errors(dev):
+    """matmul.rs:27-42: rank != 2 and an inner-dimension mismatch are both
+    InvalidOperation."""
+    a = dev.tensor(np.zeros((2, 3), np.float16))
+    with pytest.raises(TLHipError) as e:
+        a.matmul(dev.tensor(np.zeros((4, 5), np.float16)))
+    assert e.value.kind == "InvalidOperation"
+    with pytest.raises(TLHipError) as e:
+        a.matmul(dev.tensor(np.zeros((3,), np.float16)))
+    assert e.value.kind == "InvalidOperation"
 
 
 def test_linear_shape_errors(dev):

@@ -22,7 +22,7 @@ from tensorlogic_amd import synth as S
 from tensorlogic_amd.gguf import GGML_Q4_0
 from tensorlogic_amd.program import ChatDemoKVCache
 
-from test_gpu_ops import assert_close
+from test_gpu_ops import assert_logits_close, reorder_rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -53,7 +53,8 @@ def test_program_op_by_op_equals_oracle(dev, oracle, tmp_path, seed, rope_mode, 
     bad = np.nonzero(toks != ref_toks)[0]
     assert bad.size == 0, (f"first mismatch at step {bad[0]}: {toks[bad[0]]} vs {ref_toks[bad[0]]} "
                            f"(oracle margin {margins[bad[0]]:.3g})")
-    assert_close(prog.last_logits.numpy()[0], ref_logits, what="final logits")
+    rrl = reorder_rel_l2(oracle, path, 0, prompt, ref_toks, ref_logits, 64, literal=rope_mode == "program")
+    assert_logits_close(prog.last_logits.numpy()[0], ref_logits, rrl)
     print(f"{rope_mode}: {len(set(ref_toks.tolist()))} distinct ids, min top-2 margin {margins.min():.3g}")
 
 
@@ -72,12 +73,13 @@ def test_fused_runner_literal_semantics(dev, oracle, tmp_path):
     ref_abs, _, _ = om.generate(prompt, n)
     om.close()
     assert not np.array_equal(ref_lit, ref_abs), "the two semantics should give different streams"
+    rrl = reorder_rel_l2(oracle, path, 0, prompt, ref_lit, ref_lit_logits, 64, literal=True)
     m = Model(dev, path, arch=0, max_ctx=64)
     m.set_program_semantics(True)
     for use_graph in (False, True):
         toks = m.generate(prompt, n, use_graph=use_graph)
         assert np.array_equal(toks, ref_lit), f"graph={use_graph}: {toks.tolist()} vs {ref_lit.tolist()}"
-        assert_close(m.logits(), ref_lit_logits, what="final logits")
+        assert_logits_close(m.logits(), ref_lit_logits, rrl)
     m.set_program_semantics(False)
     assert np.array_equal(m.generate(prompt, n, use_graph=True), ref_abs)
     m.close()

@@ -165,7 +165,8 @@ def test_gguf_general_alignment_is_honoured(tmp_path):
 
 @pytest.mark.parametrize("case", ["magic", "version", "truncated_header", "data_past_eof",
                                   "bad_kv_type", "bad_q_shape", "missing_file", "huge_offset",
-                                  "offset_past_eof", "dim_overflow", "dim_overflow_to_zero"])
+                                  "offset_past_eof", "dim_overflow", "dim_overflow_to_zero",
+                                  "huge_tensor_count", "huge_kv_count"])
 def test_gguf_malformed_is_a_load_error(tmp_path, oracle, case):
     q8 = S.q8_0_blocks(52, "w", 2, 64).tobytes()
     t = [("w", (2, 64), GGML_Q8_0, q8)]
@@ -190,6 +191,12 @@ def test_gguf_malformed_is_a_load_error(tmp_path, oracle, case):
         blob = raw_gguf([], [("w", (1 << 40, 1 << 40), GGML_Q8_0, q8)])
     elif case == "dim_overflow_to_zero":            # 2^32 * 2^32 * 2^32 wraps to 0 elements, 0 bytes
         blob = raw_gguf([], [("w", (1 << 32, 1 << 32, 1 << 32), GGML_Q8_0, q8)])
+    elif case == "huge_tensor_count":               # 2^24 tensor infos declared over a ~200-byte file
+        blob = bytearray(raw_gguf([], t))
+        blob[8:16] = struct.pack("<Q", 1 << 24)
+    elif case == "huge_kv_count":                   # 2^24 KV pairs declared
+        blob = bytearray(raw_gguf([], t))
+        blob[16:24] = struct.pack("<Q", 1 << 24)
     if case != "missing_file":
         open(p, "wb").write(blob)
     st, g = open_c(p)

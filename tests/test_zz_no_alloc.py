@@ -39,6 +39,10 @@ def _linear_pair(dev, oracle, qt, M, N, K, seed):
     [(Q8_0, 46, 5632, 2048), (Q8_0, 20, 2048, 2048)],
     [(Q4_0, 512, 2048, 2048), (Q4_0, 130, 256, 2048)],
     [(Q4_0, 64, 2048, 5632), (Q8_0, 5, 256, 2048), (Q4_0, 1, 2048, 2048)],
+    # the largest partial set the split policy picks: 80 tiles x 4 slices of
+    # 128 x 128 fp32 = 20 MiB, the whole array (Phi-2 fc2 at a 512-row
+    # prefill), then a smaller split
+    [(Q4_0, 512, 2560, 10240), (Q8_0, 256, 512, 2048)],
 ])
 def test_linear_noalloc_matches_linear(dev, oracle, calls):
     for i, (qt, M, N, K) in enumerate(calls):
