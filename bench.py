@@ -218,11 +218,12 @@ def op_by_op_decode(dev, path: str, prompt, steps: int, warmup: int = 2):
     dev.sync()
     t0 = time.perf_counter()
     for _ in range(steps):
-        tok = temperature_sample(prog.decode(tok), 0.0)
+        logits = prog.decode(tok)
+        tok = temperature_sample(logits, 0.0)
         toks.append(tok)
     dev.sync()
     dt = time.perf_counter() - t0
-    last = prog.last_logits.numpy()[0].astype(np.float32)
+    last = logits.numpy()[0].astype(np.float32)
     del prog
     return dict(tok_s=steps / dt, ms_per_token=dt * 1e3 / steps, prefill_ms=prefill_s * 1e3,
                 steps=steps), toks, last

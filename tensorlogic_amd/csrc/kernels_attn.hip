@@ -1790,10 +1790,100 @@ __global__ void context_kernel(const uint16_t* __restrict__ p, const uint16_t* _
     out[idx] = f2h(acc);
 }
 
+// The two einsums for head dims 64 / 80 / 128, laid out for the memory
+// system as the fused attention kernels are: a K / V row is read by 8 lanes
+// (lane c holds dims EPL*c .. EPL*c + EPL - 1, EPL = D / 8) with 16-byte
+// loads where the row allows, instead of one lane walking a row serially.
+// scores: 8 lanes per output (i, h, j), 32 outputs per workgroup, the 8
+// partial dot products combined with an xor tree.
+template <int D>
+__global__ __launch_bounds__(256) void scores8_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                      uint16_t* __restrict__ out, int I, int J, int H, int Hkv) {
+    constexpr int EPL = D / 8, NW = EPL / 2;
+    const int c = threadIdx.x & 7;
+    const int64_t n = (int64_t)I * H * J;
+    const int64_t o = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+    const int64_t oc = o < n ? o : n - 1;   // (clamped: every load stays inside the tensors)
+    const int j = (int)(oc % J), h = (int)((oc / J) % H), i = (int)(oc / ((int64_t)J * H));
+    const int kvh = h / (H / Hkv);
+    uint32_t qw[NW], kw[NW];
+    load_row_words<NW>((const uint32_t*)(q + ((size_t)i * H + h) * D + EPL * c), qw);
+    load_row_words<NW>((const uint32_t*)(k + ((size_t)j * Hkv + kvh) * D + EPL * c), kw);
+    float acc = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NW; t++) {
+        const h2 a2 = as_h2(qw[t]), b2 = as_h2(kw[t]);
+        acc += (float)a2[0] * (float)b2[0];
+        acc += (float)a2[1] * (float)b2[1];
+    }
+    acc = group8_sum(acc);
+    if (c == 0 && o < n) out[o] = f2h(acc);
+}
+
+// context: one 256-thread workgroup per row (i, h); 32 key groups of 8
+// lanes, each holding keys g, g + 32, ... (8 rows' loads in flight per
+// pass); the key groups' partial rows summed within each wave, then over the
+// waves, in a fixed order.
+template <int D>
+__global__ __launch_bounds__(256) void context8_kernel(const uint16_t* __restrict__ p, const uint16_t* __restrict__ v,
+                                                       uint16_t* __restrict__ out, int J, int H, int Hkv) {
+    constexpr int EPL = D / 8, NW = EPL / 2, NG = 32, UNR = 8;
+    __shared__ float part[4][D];
+    const int row = blockIdx.x, h = row % H, tid = threadIdx.x, c = tid & 7, g = tid >> 3;
+    const int kvh = h / (H / Hkv);
+    const uint16_t* pr = p + (size_t)row * J;
+    const uint32_t* vb = (const uint32_t*)(v + (size_t)kvh * D + EPL * c);
+    const size_t wstride = (size_t)Hkv * D / 2;
+    float o[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; e++) o[e] = 0.0f;
+    for (int j0 = g; j0 < J; j0 += NG * UNR) {
+        uint32_t vw[UNR][NW];
+        float pj[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {   // (unconditional, clamped rows)
+            const int jc = min(j0 + NG * u, J - 1);
+            load_row_words<NW>(vb + (size_t)jc * wstride, vw[u]);
+            pj[u] = h2f(pr[jc]);
+        }
+#pragma unroll
+        for (int u = 0; u < UNR; u++) {
+            if (j0 + NG * u < J) {
+#pragma unroll
+                for (int t = 0; t < NW; t++) {
+                    const h2 v2 = as_h2(vw[u][t]);
+                    o[2 * t] += pj[u] * (float)v2[0];
+                    o[2 * t + 1] += pj[u] * (float)v2[1];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; e++) o[e] = stride8_sum(o[e]);
+    if ((tid & 63) < 8)
+#pragma unroll
+        for (int e = 0; e < EPL; e++) part[tid >> 6][EPL * c + e] = o[e];
+    lds_barrier();
+    if (tid < D) out[(size_t)row * D + tid] = f2h(((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid]);
+}
+
+// The 8-lane kernels for D = 64 / 80 / 128 on 4-byte aligned tensors, the
+// one-output-per-thread kernels otherwise.
+static bool einsum8_ok(const void* a, const void* b, int D) {
+    return (D == 64 || D == 80 || D == 128) && ((uintptr_t)a & 3) == 0 && ((uintptr_t)b & 3) == 0;
+}
+
 tlhip_status launch_scores(hipStream_t s, const uint16_t* q, const uint16_t* k, uint16_t* sc, int I,
                            int J, int H, int Hkv, int D) {
     int64_t n = (int64_t)I * H * J;
     if (n <= 0) return TLHIP_OK;
+    if (einsum8_ok(q, k, D)) {
+        const dim3 grid((unsigned)((n + 31) / 32));
+        if (D == 64) hipLaunchKernelGGL(scores8_kernel<64>, grid, dim3(256), 0, s, q, k, sc, I, J, H, Hkv);
+        else if (D == 80) hipLaunchKernelGGL(scores8_kernel<80>, grid, dim3(256), 0, s, q, k, sc, I, J, H, Hkv);
+        else hipLaunchKernelGGL(scores8_kernel<128>, grid, dim3(256), 0, s, q, k, sc, I, J, H, Hkv);
+        return TLHIP_OK;
+    }
     hipLaunchKernelGGL(scores_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, q, k, sc, I, J, H,
                        Hkv, D);
     return TLHIP_OK;
@@ -1803,6 +1893,13 @@ tlhip_status launch_context(hipStream_t s, const uint16_t* p, const uint16_t* v,
                             int J, int H, int Hkv, int D) {
     int64_t n = (int64_t)I * H * D;
     if (n <= 0) return TLHIP_OK;
+    if (J > 0 && einsum8_ok(p, v, D) && (int64_t)I * H <= 0x7fffffff) {
+        const dim3 grid((unsigned)(I * H));
+        if (D == 64) hipLaunchKernelGGL(context8_kernel<64>, grid, dim3(256), 0, s, p, v, out, J, H, Hkv);
+        else if (D == 80) hipLaunchKernelGGL(context8_kernel<80>, grid, dim3(256), 0, s, p, v, out, J, H, Hkv);
+        else hipLaunchKernelGGL(context8_kernel<128>, grid, dim3(256), 0, s, p, v, out, J, H, Hkv);
+        return TLHIP_OK;
+    }
     hipLaunchKernelGGL(context_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, v, out, I, J,
                        H, Hkv, D);
     return TLHIP_OK;

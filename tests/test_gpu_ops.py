@@ -510,6 +510,28 @@ def test_mask_and_einsums(dev, oracle):
     assert_close(fused, ref, what="fused attention")
 
 
+@pytest.mark.parametrize("I,J,H,Hkv,D", [(1, 190, 32, 32, 64), (1, 47, 32, 4, 64), (46, 46, 32, 4, 64),
+                                         (1, 300, 32, 32, 80), (3, 257, 8, 2, 128), (2, 1, 4, 4, 64),
+                                         (5, 700, 4, 1, 80)])
+def test_einsums_head_dims(dev, oracle, I, J, H, Hkv, D):
+    """The program's two einsums (einsum.rs:653-886, unified.metal:2524-2684)
+    at the head dims the 8-lanes-per-row kernels take (64 / 80 / 128), with
+    and without GQA, key counts that leave partial key groups and passes
+    (J = 1, 47, 257, 700), against the oracle's restatement of each."""
+    q = S.normal_f16(17, f"eq{I}{H}{D}", (I, H, D))
+    k = S.normal_f16(17, f"ek{J}{Hkv}{D}", (J, Hkv, D))
+    v = S.normal_f16(17, f"ev{J}{Hkv}{D}", (J, Hkv, D))
+    sc = einsum("ihd,jhd->ihj", dev.tensor(q), dev.tensor(k)).numpy()
+    assert sc.shape == (I, H, J)
+    assert_close(sc, oracle.einsum_scores(q, k), what=f"einsum scores {I}x{J} H{H}/{Hkv} D{D}")
+    rng = np.random.default_rng(I * 31 + J)
+    p = rng.random((I, H, J)).astype(np.float32)
+    p = (p / p.sum(-1, keepdims=True)).astype(np.float16)
+    out = einsum("ihj,jhd->ihd", dev.tensor(p), dev.tensor(v)).numpy()
+    assert out.shape == (I, H, D)
+    assert_close(out, oracle.einsum_context(p, v), what=f"einsum context {I}x{J} H{H}/{Hkv} D{D}")
+
+
 # S < 128 runs the one-workgroup-per-row kernels; S >= 128 the matrix-core
 # prefill kernels (two q-tiles per head pair of waves under causal masking,
 # key halves split between the waves, transposed V): the staged one (K / V
