@@ -36,6 +36,7 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
+sys.path.insert(1, os.path.join(ROOT, "tests"))   # tests/obo.py: the program's op-by-op C driver
 
 HBM_PEAK_GBS = 8000.0
 GEMV_KERNEL = "gemv_m1_kernel<3, 1, 2, 0> (Q4_0 fused dequant-GEMV, one activation row, 2 rows per wave, plain-store epilogue)"
@@ -460,6 +461,13 @@ def main():
     m.close()
     n_cmp = min(len(obo_toks), len(lit_toks))
     obo_match = obo_toks[:n_cmp] == lit_toks.tolist()[:n_cmp] and obo_toks == fused_toks.tolist()
+    # the same call sequence issued from C: the ABI's own per-token cost
+    import obo as obo_c
+    c_toks, c_logits, c_prefill_ms, c_ms = obo_c.run(path, prompt, obo_warm, obo_steps, len(prompt) + obo_steps + obo_warm + 4,
+                                                     S.TINYLLAMA_ARGS["vocab"])
+    c_match = c_toks.tolist() == fused_toks.tolist()
+    log(f"decode, program op by op from C through the C ABI: {1000.0 / c_ms:.1f} tok/s ({c_ms:.2f} ms/token); "
+        f"tokens equal to the fused runner's: {c_match}")
     dl = (obo_logits - fused_logits).astype(np.float64)
     obo_max_abs = float(np.abs(dl).max())
     obo_rel_l2 = float(np.linalg.norm(dl) / np.linalg.norm(fused_logits.astype(np.float64)))
@@ -540,6 +548,13 @@ def main():
                                     tokens_equal_fused_literal=obo_match,
                                     final_logits_vs_fused_literal={"max_abs": obo_max_abs,
                                                                    "rel_l2": obo_rel_l2}),
+            "decode_op_by_op_from_c": {"tok_s": round(1000.0 / c_ms, 3), "ms_per_token": round(c_ms, 3),
+                                       "prefill_ms": round(c_prefill_ms, 3), "steps": obo_steps,
+                                       "what": "the same program's tlhip_* call sequence issued from C "
+                                               "(tests/obo_driver.c), greedy, wall clock",
+                                       "tokens_equal_fused_literal": c_match,
+                                       "final_logits_max_abs_vs_fused_literal": float(
+                                           np.abs(c_logits.astype(np.float64) - fused_logits).max())},
             "hbm_bytes_per_token": weights_per_token,
             "decode_hbm_roofline_frac": round(tok_s * weights_per_token / (HBM_PEAK_GBS * 1e9), 4),
             "gemv_2048x5632": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in gem.items()},

@@ -96,3 +96,22 @@ def test_program_semantics_llama_only(dev, tmp_path):
         m.set_program_semantics(True)
     assert e.value.kind == "InvalidOperation"
     m.close()
+
+
+def test_program_op_by_op_from_c(dev, oracle, tmp_path):
+    """The program's call sequence issued from C (tests/obo_driver.c through
+    libtlhip.so, no Python between the calls) gives the oracle program's
+    tokens at every step and its final logits within the decoder-logits bar,
+    like the Python runner."""
+    import obo
+    path = _model(tmp_path, 47)
+    prompt = S.token_ids(47, "prompt", 30, SMALL["vocab"])
+    n = 24
+    ref_toks, margins, ref_logits = OracleProgram(path, "program", 1e-6).generate(prompt, n)
+    toks, logits, _, _ = obo.run(path, prompt, 0, n, 64, SMALL["vocab"])
+    bad = np.nonzero(toks != ref_toks)[0]
+    assert bad.size == 0, f"first mismatch at step {bad[0]}: {toks[bad[0]]} vs {ref_toks[bad[0]]}"
+    rrl = reorder_rel_l2(oracle, path, 0, prompt, ref_toks, ref_logits, 64, literal=True)
+    assert_logits_close(logits, ref_logits, rrl)
+    prog = ChatDemoKVCache(dev, path, max_ctx=64)
+    assert np.array_equal(prog.generate(prompt, n), toks)
