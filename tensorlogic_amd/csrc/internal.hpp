@@ -16,7 +16,9 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/tl_hip.h"
@@ -78,6 +80,13 @@ struct tlhip_ctx_s {
     float* d_ws = nullptr;              // linear's split-K partials, grown on demand
     size_t ws_bytes = 0;
     int32_t* h_pinned_i32 = nullptr;    // pinned host mirror
+    // Blocks of freed tensors kept for this context's next allocations,
+    // keyed by size class (block_class in runtime.cpp).  Reuse is stream-
+    // ordered as hipFreeAsync's is: a block freed on the host is written
+    // only by work queued after the free on this context's stream.
+    std::mutex cache_mu;
+    std::unordered_map<size_t, std::vector<void*>> block_cache;
+    size_t cached_bytes = 0;
 };
 
 struct tlhip_tensor_s {
