@@ -719,6 +719,73 @@ __device__ __forceinline__ void load_quad_buf(__amdgpu_buffer_rsrc_t r, int it, 
     }
 }
 
+// Flat task layout (FN > 0 in the M = 1 kernels): the wave's RI consecutive
+// rows taken as one contiguous stream of RI * FN blocks -- rows are
+// contiguous in the packed layout, so the stream is one stretch of memory --
+// and task t = lane + 64 i is block t % FN of row t / FN.  With FN blocks per
+// row not a multiple of 64 the lane-per-block layout leaves lanes idle in
+// the last pass (K = 2560: 80 blocks in 2 x 64 slots, 3 of 8 slots
+// computing on zeros); here RI * FN / 64 tasks per lane keep every lane busy
+// (4 rows of 80 blocks: 5 tasks each).  A task slot spans at most two rows
+// (FN >= 64): lanes below the row boundary add into the lower row's sum, the
+// others into the upper's.
+template <int FN, int RI>
+struct Flat {
+    static_assert(FN >= 64, "a task slot spans at most two rows");
+    static constexpr int IT = (RI * FN + 63) / 64;
+};
+
+// Loads of the wave's flat task stream, all issued before any use, through
+// range-checked buffer loads over the rows that exist (a task past them, or
+// every task of a wave past N, reads a zero weight with no memory request).
+template <int WT, int FN, int RI>
+__device__ __forceinline__ void load_flat(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
+                                          u4 (&q)[Flat<FN, RI>::IT][BlkLoads<WT>::n],
+                                          uint32_t (&ds)[Flat<FN, RI>::IT]) {
+    constexpr int NL = BlkLoads<WT>::n, IT = Flat<FN, RI>::IT;
+    const int row_bytes = WT == TLHIP_Q4_0 ? K / 2 : (WT == TLHIP_Q8_0 ? K : K * 2);
+    const int rows = row0 < N ? min(RI, N - row0) : 0;
+    const size_t r0 = (size_t)min(row0, N - 1);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)(wq + r0 * row_bytes), (short)0,
+                                                                        rows * row_bytes, BUF_RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc((void*)(wd + r0 * FN), (short)0,
+                                                                        WT == TLHIP_F16 ? 0 : rows * FN * 2, BUF_RSRC_WORD3);
+#pragma unroll
+    for (int i = 0; i < IT; i++) {
+        const int gb = lane + 64 * i;
+#pragma unroll
+        for (int l = 0; l < NL; l++)
+            q[i][l] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rq, gb * (16 * NL) + 16 * l, 0, 0));
+        ds[i] = WT == TLHIP_F16 ? 0u : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rd, gb * 2, 0, 0);
+    }
+}
+
+// The block dots of the flat task stream into the RI row sums; CH(b, xc)
+// fetches block b's activation chunk in the pair order of WT's unpacking.
+template <int WT, int FN, int RI, int I = 0, typename CH>
+__device__ __forceinline__ void dot_flat(const u4 (&q)[Flat<FN, RI>::IT][BlkLoads<WT>::n],
+                                         const uint32_t (&ds)[Flat<FN, RI>::IT], const CH& chunk, int lane,
+                                         float (&acc)[RI]) {
+    if constexpr (I < Flat<FN, RI>::IT) {
+        const int gb = lane + 64 * I;
+        const int r = gb / FN;
+        uint32_t xc[16];
+        chunk(gb - r * FN, xc);
+        constexpr int rlo = (64 * I) / FN;
+        constexpr int rhi = (64 * I + 63) / FN < RI ? (64 * I + 63) / FN : RI - 1;
+        if constexpr (rlo == rhi) {
+            acc[rlo] = block_dot<WT>(q[I], ds[I], xc, acc[rlo]);
+        } else {
+            const bool lo = gb < (rlo + 1) * FN;
+            float c = lo ? acc[rlo] : acc[rhi];
+            c = block_dot<WT>(q[I], ds[I], xc, c);
+            acc[rlo] = lo ? c : acc[rlo];
+            acc[rhi] = lo ? acc[rhi] : c;
+        }
+        dot_flat<WT, FN, RI, I + 1>(q, ds, chunk, lane, acc);
+    }
+}
+
 // Plain GEMV of one activation row (M = 1) with the single-row epilogues
 // (STORE, BIAS, RESID, BIAS_RESID, BIAS_GELU): the decoder's output and
 // down projections and linear() on one row.  The arithmetic is
@@ -747,7 +814,7 @@ struct Gemv1Params {
 // [2048 x 5632] + residual 4.10 -> 3.99 us, [5632 x 2048] 3.81 -> 3.71 us,
 // bit-identical outputs); EPI < 0: chosen at run time from p.epi and the
 // pointers present.
-template <int WT, int NB, int RI, int EPI = -1>
+template <int WT, int NB, int RI, int EPI = -1, int FN = 0>
 __global__ __launch_bounds__(256) void gemv_m1_kernel(Gemv1Params p) {
     __shared__ u4 xs[4][NB * 64];
     const bool has_bias = EPI < 0 ? p.bias != nullptr : (EPI == EPI_BIAS || EPI == EPI_BIAS_RESID || EPI == EPI_BIAS_GELU);
@@ -763,9 +830,13 @@ __global__ __launch_bounds__(256) void gemv_m1_kernel(Gemv1Params p) {
         for (int k = 0; k < NB; k++) load_quad_buf<WT>(rx, (int)threadIdx.x + 256 * k, xw[k]);
     }
     __builtin_amdgcn_sched_barrier(0);   // the activation loads go out first
+    constexpr int FIT = FN > 0 ? Flat<(FN > 0 ? FN : 64), RI>::IT : 1;
     u4 q[RI][NB][NL];
     uint32_t ds[RI][NB];
-    load_rows_buf<WT, NB, RI>(p.wq, p.wd, p.N, p.K, row0, lane, q, ds);
+    u4 qf[FIT][NL];
+    uint32_t dsf[FIT];
+    if constexpr (FN > 0) load_flat<WT, FN, RI>(p.wq, p.wd, p.N, p.K, row0, lane, qf, dsf);
+    else load_rows_buf<WT, NB, RI>(p.wq, p.wd, p.N, p.K, row0, lane, q, ds);
     // the epilogue's f16 operands: one per row, the same address in every
     // lane; an absent operand is never loaded (the branch is uniform)
     uint32_t eb[RI], er[RI];
@@ -793,17 +864,23 @@ __global__ __launch_bounds__(256) void gemv_m1_kernel(Gemv1Params p) {
     float acc[RI];
 #pragma unroll
     for (int ri = 0; ri < RI; ri++) acc[ri] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NB; i++) {
-        const int b = lane + 64 * i;
-        uint32_t xc[16];
+    auto chunk = [&](int b, uint32_t (&xc)[16]) {
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const u4 t = xs[v][b];
             xc[4 * v] = t[0]; xc[4 * v + 1] = t[1]; xc[4 * v + 2] = t[2]; xc[4 * v + 3] = t[3];
         }
+    };
+    if constexpr (FN > 0) {
+        dot_flat<WT, FN, RI>(qf, dsf, chunk, lane, acc);
+    } else {
 #pragma unroll
-        for (int ri = 0; ri < RI; ri++) acc[ri] = block_dot<WT>(q[ri][i], ds[ri][i], xc, acc[ri]);
+        for (int i = 0; i < NB; i++) {
+            uint32_t xc[16];
+            chunk(lane + 64 * i, xc);
+#pragma unroll
+            for (int ri = 0; ri < RI; ri++) acc[ri] = block_dot<WT>(q[ri][i], ds[ri][i], xc, acc[ri]);
+        }
     }
 #pragma unroll
     for (int ri = 0; ri < RI; ri++) acc[ri] = wave_sum<64>(acc[ri]);
@@ -864,7 +941,7 @@ __device__ __forceinline__ GemvParams norm_view(const GemvParams& k) {
     return p;
 }
 
-template <int WT, int NB, int RI, int WPB, int PRO, int EPI = -1>
+template <int WT, int NB, int RI, int WPB, int PRO, int EPI = -1, int FN = 0>
 __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
     __shared__ u4 xs[4][NB * 64];
     __shared__ float red[2][WPB];
@@ -897,7 +974,11 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
     st.load(p, xsrc);
     // (unconditional: rows are clamped into the matrix, and loads under a
     // branch leave the compiler's wait counts imprecise after it)
-    load_rows_buf<WT, NB, RI>(p.wq, p.wd, p.N, p.K, row0, lane, q, ds);
+    constexpr int FIT = FN > 0 ? Flat<(FN > 0 ? FN : 64), RI>::IT : 1;
+    u4 qf[FIT][NL];
+    uint32_t dsf[FIT];
+    if constexpr (FN > 0) load_flat<WT, FN, RI>(p.wq, p.wd, p.N, p.K, row0, lane, qf, dsf);
+    else load_rows_buf<WT, NB, RI>(p.wq, p.wd, p.N, p.K, row0, lane, q, ds);
     EpiPre<RI, 1> pre;
     QkvPre qp[RI / 2 > 0 ? RI / 2 : 1];
     if (lane == 0 && row0 < p.N) {
@@ -916,14 +997,24 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
 #pragma unroll
     for (int ri = 0; ri < RI; ri++) acc[ri][0] = 0.0f;
     if (row0 < p.N) {
+        if constexpr (FN > 0) {
+            float af[RI];
 #pragma unroll
-        for (int i = 0; i < NB; i++) {
-            const int b = lane + 64 * i;
-            if (b < nbr) {
-                uint32_t xc[16];
-                NormStage<WT, NB, WPB, PRO>::chunk(xs, b, xc);
+            for (int ri = 0; ri < RI; ri++) af[ri] = 0.0f;
+            auto chunk = [&](int b, uint32_t (&xc)[16]) { NormStage<WT, NB, WPB, PRO>::chunk(xs, b, xc); };
+            dot_flat<WT, FN, RI>(qf, dsf, chunk, lane, af);
 #pragma unroll
-                for (int ri = 0; ri < RI; ri++) acc[ri][0] = block_dot<WT>(q[ri][i], ds[ri][i], xc, acc[ri][0]);
+            for (int ri = 0; ri < RI; ri++) acc[ri][0] = af[ri];
+        } else {
+#pragma unroll
+            for (int i = 0; i < NB; i++) {
+                const int b = lane + 64 * i;
+                if (b < nbr) {
+                    uint32_t xc[16];
+                    NormStage<WT, NB, WPB, PRO>::chunk(xs, b, xc);
+#pragma unroll
+                    for (int ri = 0; ri < RI; ri++) acc[ri][0] = block_dot<WT>(q[ri][i], ds[ri][i], xc, acc[ri][0]);
+                }
             }
         }
 #pragma unroll
@@ -973,6 +1064,25 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
 template <int WT, int NB, int PRO, int EPI = -1>
 static void launch_norm_shape(hipStream_t s, const GemvParams& p) {
     constexpr bool paired = EPI == EPI_QKV_ROPE || EPI == EPI_SWIGLU_PAIR;
+    if constexpr (NB == 2 && WT != TLHIP_Q6_K) {
+        if (p.K == 80 * 32) {
+            // 80 blocks per row (K = 2560): the flat task layout with the same
+            // rows per workgroup as the shapes below -- 4 rows per wave (5
+            // tasks per lane, none idle) from 8192 rows, 2 rows per wave (3
+            // tasks, 1 in 6 idle) below, where 4 would leave too few waves
+            // (measured on MI355X, Q8_0 Phi-2 decode: [10240 x 2560] + GELU
+            // 10.78 -> 9.55 us with 4 rows; [7680 x 2560] QKV 8.23 -> 9.54 us
+            // with 4 rows in 2-wave workgroups)
+            const bool pair = paired || p.epi == EPI_QKV_ROPE || p.epi == EPI_SWIGLU_PAIR;
+            if (!pair && p.N >= 16384)
+                hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 4, 8, PRO, EPI, 80>), dim3((p.N + 31) / 32), dim3(512), 0, s, p);
+            else if (!pair && p.N >= 8192)
+                hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 4, 4, PRO, EPI, 80>), dim3((p.N + 15) / 16), dim3(256), 0, s, p);
+            else
+                hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 2, 4, PRO, EPI, 80>), dim3((p.N + 7) / 8), dim3(256), 0, s, p);
+            return;
+        }
+    }
     if (!paired && p.N >= 16384 && p.epi != EPI_QKV_ROPE && p.epi != EPI_SWIGLU_PAIR) {
         const int wgs = (p.N + 31) / 32;   // 8 waves x 4 rows
         if constexpr (!paired) hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 4, 8, PRO, EPI>), dim3(wgs), dim3(512), 0, s, p);

@@ -6,23 +6,23 @@
 
 namespace tlhip {
 
-template <int WT, int NB, int RI>
+template <int WT, int NB, int RI, int FN = 0>
 static bool launch_m1_epi_nb(hipStream_t s, const Gemv1Params& p) {
     const dim3 grid((unsigned)(((p.N + RI - 1) / RI + 3) / 4)), block(256);
     const bool b = p.bias != nullptr, r = p.resid != nullptr;
     switch (p.epi) {
-        case EPI_STORE: hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_STORE>), grid, block, 0, s, p); return true;
+        case EPI_STORE: hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_STORE, FN>), grid, block, 0, s, p); return true;
         case EPI_BIAS:
             if (!b) return false;
-            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS, FN>), grid, block, 0, s, p);
             return true;
         case EPI_RESID:
             if (!r) return false;
-            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_RESID>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_RESID, FN>), grid, block, 0, s, p);
             return true;
         case EPI_BIAS_RESID:
             if (!b || !r) return false;
-            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS_RESID>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS_RESID, FN>), grid, block, 0, s, p);
             return true;
         default: return false;
     }
@@ -35,14 +35,20 @@ static bool launch_m1_epi_wt(hipStream_t s, const Gemv1Params& p, int nb, int ri
     if (ri == 2) {
         switch (nb) {
             case 1: return launch_m1_epi_nb<WT, 1, 2>(s, p);
-            case 2: return launch_m1_epi_nb<WT, 2, 2>(s, p);
+            case 2:
+                // 80 blocks per row (K = 2560): the flat task layout, 4 rows per
+                // wave from 8192 rows, 2 below (enough waves to fill the device)
+                if (WT != TLHIP_Q6_K && p.K == 80 * 32)
+                    return p.N >= 8192 ? launch_m1_epi_nb<WT, 2, 4, 80>(s, p) : launch_m1_epi_nb<WT, 2, 2, 80>(s, p);
+                return launch_m1_epi_nb<WT, 2, 2>(s, p);
             default: return false;
         }
     }
     switch (nb) {   // the block counts launch_m1 rounds to
         case 3: return launch_m1_epi_nb<WT, 3, 1>(s, p);
         case 4: return launch_m1_epi_nb<WT, 4, 1>(s, p);
-        case 5: case 6: return launch_m1_epi_nb<WT, 6, 1>(s, p);
+        case 5: return launch_m1_epi_nb<WT, 5, 1>(s, p);   // (K = 10240: 320 blocks, 5 x 64)
+        case 6: return launch_m1_epi_nb<WT, 6, 1>(s, p);
         case 7: case 8: return launch_m1_epi_nb<WT, 8, 1>(s, p);
         default: return false;
     }
