@@ -360,6 +360,7 @@ def main():
     ap.add_argument("--gemv-iters", type=int, default=480)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-phi2", action="store_true", help="skip the config-5 Phi-2 leg")
+    ap.add_argument("--phi2-steps", type=int, default=256, help="decode steps of the config-5 leg")
     ap.add_argument("--model", default="", help="reuse an existing TinyLlama GGUF file")
     ap.add_argument("--decode-launch", choices=("graph", "direct"), default="graph",
                     help="replay one captured HIP graph per decode step (default) or launch the same "
@@ -395,7 +396,7 @@ def main():
         print(json.dumps({"config3": c3}), flush=True)
         return
     if args.part == "phi2":
-        c5 = config5_phi2(dev, use_graph=args.decode_launch == "graph")
+        c5 = config5_phi2(dev, steps=args.phi2_steps, use_graph=args.decode_launch == "graph")
         log(f"Phi-2: prefill 512 {c5['prefill_512_ms']:.2f} ms, decode {c5['decode_tok_s']:.1f} tok/s")
         dev.close()
         print(json.dumps({"config5": c5}), flush=True)

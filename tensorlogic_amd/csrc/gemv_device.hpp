@@ -839,18 +839,30 @@ __global__ __launch_bounds__(256) void gemv_m1_kernel(Gemv1Params p) {
     else load_rows_buf<WT, NB, RI>(p.wq, p.wd, p.N, p.K, row0, lane, q, ds);
     // the epilogue's f16 operands: one per row, the same address in every
     // lane; an absent operand is never loaded (the branch is uniform)
+    // From 4 rows per wave lane ri finishes row row0 + ri (see the stores
+    // below) and loads its own operands; with fewer rows lane 0 finishes them
+    // all from operands loaded at one scalar offset each (measured on MI355X:
+    // the per-lane form cost config-4 decode 0.45 % at 2 rows per wave, and
+    // gained Phi-2 decode 1.8 % at 4).  Range-checked loads: rows past N
+    // read zero.
+    constexpr bool LANE_EPI = RI >= 4;
     uint32_t eb[RI], er[RI];
 #pragma unroll
     for (int ri = 0; ri < RI; ri++) eb[ri] = er[ri] = 0u;
+    const int erow = row0 + (lane < RI ? lane : 0);
     if (has_bias) {
         const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)p.bias, (short)0, p.N * 2, BUF_RSRC_WORD3);
+        if constexpr (LANE_EPI) eb[0] = __builtin_amdgcn_raw_buffer_load_b16(rb, erow * 2, 0, 0);
+        else
 #pragma unroll
-        for (int ri = 0; ri < RI; ri++) eb[ri] = __builtin_amdgcn_raw_buffer_load_b16(rb, 0, (row0 + ri) * 2, 0);
+            for (int ri = 0; ri < RI; ri++) eb[ri] = __builtin_amdgcn_raw_buffer_load_b16(rb, 0, (row0 + ri) * 2, 0);
     }
     if (has_resid) {
         const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc((void*)p.resid, (short)0, p.N * 2, BUF_RSRC_WORD3);
+        if constexpr (LANE_EPI) er[0] = __builtin_amdgcn_raw_buffer_load_b16(rr, erow * 2, 0, 0);
+        else
 #pragma unroll
-        for (int ri = 0; ri < RI; ri++) er[ri] = __builtin_amdgcn_raw_buffer_load_b16(rr, 0, (row0 + ri) * 2, 0);
+            for (int ri = 0; ri < RI; ri++) er[ri] = __builtin_amdgcn_raw_buffer_load_b16(rr, 0, (row0 + ri) * 2, 0);
     }
 #pragma unroll
     for (int k = 0; k < NB; k++) {
@@ -884,7 +896,14 @@ __global__ __launch_bounds__(256) void gemv_m1_kernel(Gemv1Params p) {
     }
 #pragma unroll
     for (int ri = 0; ri < RI; ri++) acc[ri] = wave_sum<64>(acc[ri]);
-    if (lane == 0) {
+    if constexpr (LANE_EPI) {
+        // every lane holds the RI row sums: lane ri stores row row0 + ri (the
+        // epilogues side by side instead of one after another in lane 0)
+        float a = acc[0];
+#pragma unroll
+        for (int ri = 1; ri < RI; ri++) a = lane == ri ? acc[ri] : a;
+        if (lane < RI && row0 + lane < p.N) p.y[row0 + lane] = epilogue_v(epi, a, (uint16_t)eb[0], (uint16_t)er[0]);
+    } else if (lane == 0) {
 #pragma unroll
         for (int ri = 0; ri < RI; ri++)
             if (row0 + ri < p.N) p.y[row0 + ri] = epilogue_v(epi, acc[ri], (uint16_t)eb[ri], (uint16_t)er[ri]);
@@ -981,15 +1000,18 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
     else load_rows_buf<WT, NB, RI>(p.wq, p.wd, p.N, p.K, row0, lane, q, ds);
     EpiPre<RI, 1> pre;
     QkvPre qp[RI / 2 > 0 ? RI / 2 : 1];
-    if (lane == 0 && row0 < p.N) {
-        if (p.epi == EPI_QKV_ROPE) {
-            const int pos = p.pos0 + (dev_pos ? pos_raw : 0);
+    if (lane == 0 && row0 < p.N && p.epi == EPI_QKV_ROPE) {
+        const int pos = p.pos0 + (dev_pos ? pos_raw : 0);
 #pragma unroll
-            for (int ri = 0; ri + 1 < RI; ri += 2)
-                if (row0 + ri + 1 < p.N) qkv_rope_pre(p, row0 + ri, pos, qp[ri / 2]);
-        } else {
-            epi_preload<RI, 1>(p, row0, pre);
-        }
+        for (int ri = 0; ri + 1 < RI; ri += 2)
+            if (row0 + ri + 1 < p.N) qkv_rope_pre(p, row0 + ri, pos, qp[ri / 2]);
+    }
+    // single-row epilogues and greedy keys: lane ri finishes row row0 + ri,
+    // so its bias / residual element is loaded by that lane, here
+    uint32_t eb1 = 0u, er1 = 0u;
+    if (lane < RI && row0 + lane < p.N && p.epi != EPI_QKV_ROPE && p.epi != EPI_SWIGLU_PAIR) {
+        if (p.bias) eb1 = p.bias[row0 + lane];
+        if (p.resid) er1 = p.resid[row0 + lane];
     }
     st.finish(p, xs, red);
 
@@ -1027,23 +1049,31 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
                 if (row0 + ri + 1 < p.N) qkv_rope_store(p, row0 + ri, acc[ri][0], acc[ri + 1][0], qp[ri / 2]);
         return;
     }
-    if (p.epi != EPI_ARGMAX) {
+    if (p.epi == EPI_SWIGLU_PAIR) {
         if (lane == 0 && row0 < p.N) store_rows<RI, 1>(p, row0, acc, pre);
         return;
     }
-    unsigned long long best = 0ull;
-    if (lane == 0 && row0 < p.N) {
+    // every lane holds the RI row sums: lane ri finishes row row0 + ri (the
+    // RI epilogues run side by side instead of one after another in lane 0)
+    float a = acc[0][0];
 #pragma unroll
-        for (int ri = 0; ri < RI; ri++) {
-            const int row = row0 + ri;
-            if (row < p.N) {
-                uint16_t r = f2h(acc[ri][0]);
-                if (p.bias) r = add_h(r, (uint16_t)pre.b[ri]);
-                p.y[row] = r;
-                best = umax64(best, amax_key(r, row));
-            }
-        }
+    for (int ri = 1; ri < RI; ri++) a = lane == ri ? acc[ri][0] : a;
+    const int row = row0 + lane;
+    const bool mine = lane < RI && row < p.N;
+    if (p.epi != EPI_ARGMAX) {
+        if (mine) p.y[row] = epilogue_v(p.epi, a, (uint16_t)eb1, (uint16_t)er1);
+        return;
     }
+    unsigned long long best = 0ull;
+    if (mine) {
+        uint16_t r = f2h(a);
+        if (p.bias) r = add_h(r, (uint16_t)eb1);
+        p.y[row] = r;
+        best = amax_key(r, row);
+    }
+    // the RI lanes' keys to lane 0 (lanes past RI hold 0), then the waves
+#pragma unroll
+    for (int o = 1; o < RI; o <<= 1) best = umax64(best, __shfl_xor(best, o, 64));
     if (lane == 0) wkey[w] = best;
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -1074,6 +1104,9 @@ static void launch_norm_shape(hipStream_t s, const GemvParams& p) {
             // 10.78 -> 9.55 us with 4 rows; [7680 x 2560] QKV 8.23 -> 9.54 us
             // with 4 rows in 2-wave workgroups)
             const bool pair = paired || p.epi == EPI_QKV_ROPE || p.epi == EPI_SWIGLU_PAIR;
+            // (8 waves x 4 rows from 8192 rows too unless the greedy keys fix
+            // 16 rows per workgroup: one quad of the 2560-element row per
+            // staging thread instead of two for a quarter of them)
             if (!pair && p.N >= 16384)
                 hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 4, 8, PRO, EPI, 80>), dim3((p.N + 31) / 32), dim3(512), 0, s, p);
             else if (!pair && p.N >= 8192)
