@@ -169,6 +169,23 @@ def config3_attention(dev, iters: int = 20):
     return res
 
 
+def config3_norm_rope(S: int = 2048, iters: int = 200):
+    """Config 3's elementwise legs at S = 2048, timed from C (tests/obo.py:
+    back-to-back calls between hipEvents, no Python between them):
+    rms_norm over [S, 2048] -- 4 * S * 2048 + 4096 algorithmic bytes (x in,
+    y out, the weight) -- and rope of the query [S, 32, 64] and key [S, 4, 64]
+    blocks -- 2 * 2 * S * (2048 + 256) bytes in and out for the pair."""
+    import obo
+    t = obo.time_legs(S, iters)
+    nb = 4 * S * 2048 + 4096
+    rb_q, rb_k = 2 * 2 * S * 2048, 2 * 2 * S * 256
+    rope_us = t["rope_q_us"] + t["rope_k_us"]
+    return {"rms_norm": dict(us=t["rms_norm_us"], bytes=nb, gbs=nb / t["rms_norm_us"] / 1e3,
+                             frac=nb / t["rms_norm_us"] / 1e3 / HBM_PEAK_GBS),
+            "rope_q_k": dict(us=rope_us, us_q=t["rope_q_us"], us_k=t["rope_k_us"], bytes=rb_q + rb_k,
+                             gbs=(rb_q + rb_k) / rope_us / 1e3, frac=(rb_q + rb_k) / rope_us / 1e3 / HBM_PEAK_GBS)}
+
+
 def config5_phi2(dev, steps: int = 256, n_prompt: int = 512, use_graph: bool = True):
     """Config 5: Phi-2-architecture decoder (2.7B, Q8_0 linear weights, random
     init), 512-token prompt prefilled through the MFMA GEMM and attention,
@@ -392,8 +409,11 @@ def main():
         c3 = config3_attention(dev)
         for k, v in c3.items():
             log(f"attention {k}: {v['us']:.2f} us, {v['tflops']:.2f} TFLOP/s")
+        nr = config3_norm_rope()
+        for k, v in nr.items():
+            log(f"config 3 {k} at S = 2048: {v['us']:.2f} us, {v['gbs']:.0f} GB/s ({v['frac']:.1%} of peak)")
         dev.close()
-        print(json.dumps({"config3": c3}), flush=True)
+        print(json.dumps({"config3": c3, "config3_norm_rope": nr}), flush=True)
         return
     if args.part == "phi2":
         c5 = config5_phi2(dev, steps=args.phi2_steps, use_graph=args.decode_launch == "graph")
@@ -492,6 +512,9 @@ def main():
     c3 = config3_attention(dev)
     for k, v in c3.items():
         log(f"attention {k}: {v['us']:.2f} us, {v['tflops']:.2f} TFLOP/s")
+    nr = config3_norm_rope()
+    for k, v in nr.items():
+        log(f"config 3 {k} at S = 2048: {v['us']:.2f} us, {v['gbs']:.0f} GB/s ({v['frac']:.1%} of peak)")
     q6 = q6k_lm_head(dev)
     log(f"Q6_K GEMV 32000x2048: {q6['us']:.2f} us, {q6['gbs']:.0f} GB/s")
     c5 = None
@@ -563,6 +586,7 @@ def main():
             "copy_reference": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in cp.items()},
             "config2_q8_0": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c2.items()},
             "config3_attention": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c3.items()},
+            "config3_norm_rope_S2048": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in nr.items()},
             "q6_k_gemv_32000x2048": {k: round(v, 3) for k, v in q6.items()},
             "config5_phi2_q8_0": {k: round(v, 3) for k, v in c5.items()} if c5 else None,
         },

@@ -269,12 +269,48 @@ __global__ void rope_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict
     }
 }
 
+// The interleaved layout with every dim rotated and dense rows: each thread
+// rotates 8 consecutive elements (4 adjacent pairs) of a head row with one
+// 16-byte load and store, and reads the 4 pairs' (cos, sin) as two 16-byte
+// loads of the table -- consecutive threads on consecutive 16 bytes.  The
+// arithmetic is rope_kernel's (rope_pair), bit for bit.
+__global__ void rope_vec8_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, int S, int H, int D,
+                                 int64_t groups, int offset, const int32_t* d_pos, const float* __restrict__ table) {
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= groups) return;
+    const int gpr = H * D / 8;   // 8-element groups per sequence row
+    const int s = (int)((g / gpr) % S);
+    const int e0 = (int)(g % (D / 8)) * 8;
+    const int pos = offset + s + (d_pos ? *d_pos : 0);
+    const u4 v = ((const u4*)x)[g];
+    const float4* tp = (const float4*)(table + 2 * ((size_t)pos * (D / 2) + e0 / 2));
+    const float4 t0 = tp[0], t1 = tp[1];
+    const float c[4] = {t0.x, t0.z, t1.x, t1.z}, sn[4] = {t0.y, t0.w, t1.y, t1.w};
+    u4 o;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const h2 p2 = as_h2(v[k]);
+        float r0, r1;
+        rope_pair((float)p2[0], (float)p2[1], c[k], sn[k], r0, r1);
+        o[k] = (uint32_t)f2h(r0) | ((uint32_t)f2h(r1) << 16);
+    }
+    ((u4*)y)[g] = o;
+}
+
 tlhip_status launch_rope(hipStream_t s, const uint16_t* x, uint16_t* y, int S, int H, int D,
                          int64_t batch, int offset, const int32_t* d_pos, int layout, int rot_dims,
                          const float* table, int x_row_stride, int y_row_stride) {
     const int half = rot_dims / 2;
     int64_t total = batch * S * (int64_t)H * (D - half);
     if (total <= 0) return TLHIP_OK;
+    const bool dense = (x_row_stride == 0 || x_row_stride == H * D) && (y_row_stride == 0 || y_row_stride == H * D);
+    if (layout == 0 && rot_dims == D && D % 8 == 0 && dense && ((uintptr_t)x & 15) == 0 && ((uintptr_t)y & 15) == 0 &&
+        ((uintptr_t)table & 15) == 0) {
+        const int64_t groups = batch * S * (int64_t)H * D / 8;
+        hipLaunchKernelGGL(rope_vec8_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s, x, y, S, H, D,
+                           groups, offset, d_pos, table);
+        return TLHIP_OK;
+    }
     hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, y, S,
                        H, D, batch, offset, d_pos, layout, rot_dims, table,
                        x_row_stride ? x_row_stride : H * D, y_row_stride ? y_row_stride : H * D);

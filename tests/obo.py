@@ -42,3 +42,15 @@ def run(path: str, prompt, warmup: int, steps: int, max_ctx: int, vocab: int, ro
     if rc != 0:
         raise RuntimeError(f"obo_run: {lib().obo_error().decode()}")
     return toks, logits.view(np.float16), float(ms[0]), float(ms[1])
+
+
+def time_legs(S: int = 2048, iters: int = 200):
+    """Config 3's rms_norm [S, 2048] and rope [S, 32, 64] / [S, 4, 64] from C:
+    us per call of each (hipEvents around back-to-back calls)."""
+    L = lib()
+    L.obo_time_legs.restype = C.c_int
+    L.obo_time_legs.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double)]
+    us = np.zeros(3, np.float64)
+    if L.obo_time_legs(S, iters, us.ctypes.data_as(C.POINTER(C.c_double))) != 0:
+        raise RuntimeError(f"obo_time_legs: {L.obo_error().decode()}")
+    return {"rms_norm_us": float(us[0]), "rope_q_us": float(us[1]), "rope_k_us": float(us[2])}

@@ -346,3 +346,63 @@ int obo_run(const char* path, const int32_t* prompt, int n_prompt, int warmup, i
 }
 
 const char* obo_error(void) { return g_err; }
+
+/* Config-3 elementwise legs timed from C (no Python between the calls):
+ * rms_norm over [S, 2048] (eps 1e-5, w = 1 + small noise) and rope of the
+ * query [S, 32, 64] and key [S, 4, 64] blocks, `iters` back-to-back calls of
+ * each between hipEvents on the context stream; us[0] = us per rms_norm,
+ * us[1] = us per query rope, us[2] = us per key rope.  Inputs are fixed
+ * pseudo-random f16 bit patterns: x, q, k of magnitude in [0.25, 2), w in
+ * [1, 1.04). */
+static int upload_rand(int nd, int64_t a, int64_t b, int64_t c, uint32_t seed, int weight, tlhip_tensor* t) {
+    int64_t n = a * (b ? b : 1) * (c ? c : 1);
+    static uint16_t buf[2048 * 2048 * 2];
+    if (n > (int64_t)(sizeof buf / 2)) {
+        snprintf(g_err, sizeof g_err, "upload_rand: %lld elements", (long long)n);
+        return -1;
+    }
+    uint32_t s = seed * 2654435761u + 1u;
+    for (int64_t i = 0; i < n; i++) {
+        s = s * 1664525u + 1013904223u;
+        const uint32_t r = s >> 8;
+        buf[i] = weight ? (uint16_t)(0x3C00u + r % 41u)
+                        : (uint16_t)(((r & 1u) << 15) | ((13u + (r >> 1) % 3u) << 10) | ((r >> 3) & 0x3FFu));
+    }
+    if (t_new(nd, a, b, c, 0, t)) return -1;
+    CK(tlhip_tensor_upload(C, *t, buf, (size_t)n * 2));
+    return 0;
+}
+
+int obo_time_legs(int S, int iters, double* us) {
+    tlhip_tensor x = NULL, w = NULL, y = NULL, q = NULL, k = NULL, qo = NULL, ko = NULL;
+    g_err[0] = 0;
+    CK(tlhip_init(0, &C));
+    int rc = upload_rand(2, S, 2048, 0, 1, 0, &x);
+    if (!rc) rc = upload_rand(1, 2048, 0, 0, 2, 1, &w);
+    if (!rc) rc = upload_rand(3, S, 32, 64, 3, 0, &q);
+    if (!rc) rc = upload_rand(3, S, 4, 64, 4, 0, &k);
+    if (!rc) rc = t_new(2, S, 2048, 0, 0, &y);
+    if (!rc) rc = t_new(3, S, 32, 64, 0, &qo);
+    if (!rc) rc = t_new(3, S, 4, 64, 0, &ko);
+    for (int leg = 0; !rc && leg < 3; leg++) {
+        for (int pass = 0; !rc && pass < 2; pass++) {   /* warm-up pass, then the timed one */
+            const int n = pass ? iters : 8;
+            if (pass && tlhip_timer_start(C) != TLHIP_OK) rc = -1;
+            for (int i = 0; !rc && i < n; i++) {
+                tlhip_status st = leg == 0 ? tlhip_rms_norm(C, x, w, 1e-5f, y)
+                                  : leg == 1 ? tlhip_rope(C, q, 0, 10000.0f, TLHIP_ROPE_INTERLEAVED, 0, qo)
+                                             : tlhip_rope(C, k, 0, 10000.0f, TLHIP_ROPE_INTERLEAVED, 0, ko);
+                if (st != TLHIP_OK) rc = -1;
+            }
+            float ms = 0.0f;
+            if (!rc && pass && tlhip_timer_stop(C, &ms) != TLHIP_OK) rc = -1;
+            if (!rc && pass) us[leg] = ms * 1000.0 / n;
+        }
+    }
+    if (rc && !g_err[0]) snprintf(g_err, sizeof g_err, "%s", tlhip_last_error());
+    tlhip_tensor arr[] = {x, w, y, q, k, qo, ko};
+    for (size_t i = 0; i < sizeof arr / sizeof arr[0]; i++)
+        if (arr[i]) tlhip_tensor_free(arr[i]);
+    tlhip_shutdown(C);
+    return rc;
+}
