@@ -547,6 +547,78 @@ __device__ __forceinline__ float ld_agent(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Dim tid of one head's result from its nc chunk partials (m_c, S_c, o_c),
+// summed in chunk order. Every chunk's three loads are in flight at once,
+// AS_B chunks at a time (indices clamped, loads unconditional); up to AS_B
+// chunks that is one round trip in all. The loads are agent-scope relaxed
+// atomics in both callers: the last arriver needs them (the partials were
+// published by other workgroups of the same launch, past this XCD's L2), and
+// for the combine kernel they keep the compiler from turning the
+// uniform-address m_c / S_c loads into scalar loads sunk into the per-chunk
+// branches, one round trip per chunk.
+__device__ __forceinline__ float asplit_combine(const float* pm, const float* ps, const float* po, int D, int nc, int J) {
+    constexpr int AS_B = 16;
+    float M = -INFINITY, num = 0.0f, den = 0.0f;
+    if (nc <= AS_B) {
+        float mv[AS_B], sv2[AS_B], ov[AS_B];
+#pragma unroll
+        for (int u = 0; u < AS_B; u++) {
+            const int kk = min(u, nc - 1);
+            mv[u] = ld_agent(pm + kk);
+            sv2[u] = ld_agent(ps + kk);
+            ov[u] = ld_agent(po + (size_t)kk * D);
+        }
+#pragma unroll
+        for (int u = 0; u < AS_B; u++)
+            if (u < nc) M = fmaxf(M, mv[u]);
+        const bool degenerate = !isfinite(M);
+#pragma unroll
+        for (int u = 0; u < AS_B; u++) {
+            if (u < nc) {
+                if (degenerate) {
+                    num += ov[u];
+                } else if (isfinite(mv[u])) {
+                    const float w = expf(mv[u] - M);
+                    num += w * ov[u];
+                    den += w * sv2[u];
+                }
+            }
+        }
+    } else {
+        for (int k = 0; k < nc; k += AS_B) {
+            float mv[AS_B];
+#pragma unroll
+            for (int u = 0; u < AS_B; u++) mv[u] = ld_agent(pm + min(k + u, nc - 1));
+#pragma unroll
+            for (int u = 0; u < AS_B; u++) M = fmaxf(M, mv[u]);   // (clamped repeats change nothing)
+        }
+        const bool degenerate = !isfinite(M);
+        for (int k = 0; k < nc; k += AS_B) {
+            float mv[AS_B], sv2[AS_B], ov[AS_B];
+#pragma unroll
+            for (int u = 0; u < AS_B; u++) {
+                const int kk = min(k + u, nc - 1);
+                mv[u] = ld_agent(pm + kk);
+                sv2[u] = ld_agent(ps + kk);
+                ov[u] = ld_agent(po + (size_t)kk * D);
+            }
+#pragma unroll
+            for (int u = 0; u < AS_B; u++) {
+                if (k + u < nc) {
+                    if (degenerate) {
+                        num += ov[u];
+                    } else if (isfinite(mv[u])) {
+                        const float w = expf(mv[u] - M);
+                        num += w * ov[u];
+                        den += w * sv2[u];
+                    }
+                }
+            }
+        }
+    }
+    return !isfinite(M) ? h2f(f2h(1.0f / (float)J)) * num : num / den;
+}
+
 template <int D, int NT, bool XCH>
 __global__ __launch_bounds__(NT) void asplit_kernel(AttnArgs a, SplitBufs b) {
     constexpr int EPL = D / 8, NW = EPL / 2, NWV = As<NT>::NWV, AS_NG = As<NT>::NG, AS_U = As<NT>::U;
@@ -656,122 +728,20 @@ __global__ __launch_bounds__(NT) void asplit_kernel(AttnArgs a, SplitBufs b) {
     if (!last) return;
     if (tid == 0) __hip_atomic_store(b.flags + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid >= D) return;
-    // Every chunk's (m_c, S_c, o_c[tid]) in flight at once, AS_B chunks at a
-    // time (indices clamped, loads unconditional: a load under a per-chunk
-    // condition is waited for at the condition's join, one round trip per
-    // chunk); then the sums in chunk order.
-    constexpr int AS_B = 16;
-    const float* pm = b.mx + hc;
-    const float* ps = b.sum + hc;
-    const float* po = b.o + hc * D + tid;
-    float M = -INFINITY, num = 0.0f, den = 0.0f;
-    if (nc <= AS_B) {
-        float mv[AS_B], sv2[AS_B], ov[AS_B];
-#pragma unroll
-        for (int u = 0; u < AS_B; u++) {
-            const int kk = min(u, nc - 1);
-            mv[u] = ld_agent(pm + kk);
-            sv2[u] = ld_agent(ps + kk);
-            ov[u] = ld_agent(po + (size_t)kk * D);
-        }
-#pragma unroll
-        for (int u = 0; u < AS_B; u++)
-            if (u < nc) M = fmaxf(M, mv[u]);
-        const bool degenerate = !isfinite(M);
-#pragma unroll
-        for (int u = 0; u < AS_B; u++) {
-            if (u < nc) {
-                if (degenerate) {
-                    num += ov[u];
-                } else if (isfinite(mv[u])) {
-                    const float w = expf(mv[u] - M);
-                    num += w * ov[u];
-                    den += w * sv2[u];
-                }
-            }
-        }
-    } else {
-        for (int k = 0; k < nc; k += AS_B) {
-            float mv[AS_B];
-#pragma unroll
-            for (int u = 0; u < AS_B; u++) mv[u] = ld_agent(pm + min(k + u, nc - 1));
-#pragma unroll
-            for (int u = 0; u < AS_B; u++) M = fmaxf(M, mv[u]);   // (clamped repeats change nothing)
-        }
-        const bool degenerate = !isfinite(M);
-        for (int k = 0; k < nc; k += AS_B) {
-            float mv[AS_B], sv2[AS_B], ov[AS_B];
-#pragma unroll
-            for (int u = 0; u < AS_B; u++) {
-                const int kk = min(k + u, nc - 1);
-                mv[u] = ld_agent(pm + kk);
-                sv2[u] = ld_agent(ps + kk);
-                ov[u] = ld_agent(po + (size_t)kk * D);
-            }
-#pragma unroll
-            for (int u = 0; u < AS_B; u++) {
-                if (k + u < nc) {
-                    if (degenerate) {
-                        num += ov[u];
-                    } else if (isfinite(mv[u])) {
-                        const float w = expf(mv[u] - M);
-                        num += w * ov[u];
-                        den += w * sv2[u];
-                    }
-                }
-            }
-        }
-    }
-    const float r = !isfinite(M) ? h2f(f2h(1.0f / (float)J)) * num : num / den;
+    const float r = asplit_combine(b.mx + hc, b.sum + hc, b.o + hc * D + tid, D, nc, J);
     a.out[(size_t)h * D + tid] = f2h(r);   // (one query row)
 }
 
 // The chunks of a head combined by a kernel of its own (the kernel boundary
 // orders the partials' stores before these loads): one workgroup per head,
-// thread d sums dim d over the chunks in chunk order, AS_B chunks' loads in
-// flight at a time.
+// thread d sums dim d over the chunks in chunk order.
 template <int D>
 __global__ __launch_bounds__(D) void asplit_combine_kernel(AttnArgs a, SplitBufs b) {
-    constexpr int AS_B = 16;
     const int h = blockIdx.x, tid = threadIdx.x;
     const int J = asplit_keys(a, b);
     const int nc = (J + AS_CH - 1) / AS_CH;
     const size_t hc = (size_t)h * b.nch;
-    const float* pm = b.mx + hc;
-    const float* ps = b.sum + hc;
-    const float* po = b.o + hc * D + tid;
-    float M = -INFINITY, num = 0.0f, den = 0.0f;
-    for (int k = 0; k < nc; k += AS_B) {
-        float mv[AS_B];
-#pragma unroll
-        for (int u = 0; u < AS_B; u++) mv[u] = pm[min(k + u, nc - 1)];
-#pragma unroll
-        for (int u = 0; u < AS_B; u++) M = fmaxf(M, mv[u]);   // (clamped repeats change nothing)
-    }
-    const bool degenerate = !isfinite(M);
-    for (int k = 0; k < nc; k += AS_B) {
-        float mv[AS_B], sv2[AS_B], ov[AS_B];
-#pragma unroll
-        for (int u = 0; u < AS_B; u++) {
-            const int kk = min(k + u, nc - 1);
-            mv[u] = pm[kk];
-            sv2[u] = ps[kk];
-            ov[u] = po[(size_t)kk * D];
-        }
-#pragma unroll
-        for (int u = 0; u < AS_B; u++) {
-            if (k + u < nc) {
-                if (degenerate) {
-                    num += ov[u];
-                } else if (isfinite(mv[u])) {
-                    const float w = expf(mv[u] - M);
-                    num += w * ov[u];
-                    den += w * sv2[u];
-                }
-            }
-        }
-    }
-    const float r = degenerate ? h2f(f2h(1.0f / (float)J)) * num : num / den;
+    const float r = asplit_combine(b.mx + hc, b.sum + hc, b.o + hc * D + tid, D, nc, J);
     a.out[(size_t)h * D + tid] = f2h(r);   // (one query row)
 }
 
