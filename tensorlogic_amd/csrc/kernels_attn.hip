@@ -489,7 +489,7 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
 // Decode attention split over key chunks (head dims 80 / 128, long caches),
 // one launch (flash decoding).  One workgroup per head streams every K/V
 // row of the head through one CU (~17 GB/s per CU for Phi-2's 5 KB-strided
-// rows); here each head's keys are cut into AS_CH-key chunks handled by
+// rows); here each head's keys are cut into CH-key chunks handled by
 // separate workgroups.  A chunk's workgroup computes
 //   s_j  = f16(f16(q.k_j) * scale)      (the one-workgroup kernels' lane
 //                                        order, so the same score values)
@@ -513,18 +513,26 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
 // a single row over a key count known at launch, which is also how a row
 // attends more keys than the one-workgroup kernels' LDS score row holds
 // (ATT_MAX_J).  Rows are read at min(j, kv_rows - 1), inside the allocation.
+// CH keys per chunk: AS_CH, or 2 * AS_CH for rows of AS_XCH_ROWS + 1 ..
+// AS_NT_ROWS keys (fewer, longer chunks, combined by the second kernel).
+// Measured on MI355X, one row over 2048 keys at head dim 64 (32 / 4 heads),
+// per call: 128-key chunks 8.5 us, 256 7.55 us, 512 8.7 us (all with the
+// combine kernel; the in-kernel exchange at 8 chunks of 256: 8.2 us).
 constexpr int AS_CH = 128;
 // NT threads per chunk workgroup: NT / 8 key groups of 8 lanes, each
-// holding AS_CH / (NT / 8) of the chunk's K / V rows.  512 threads (2 rows
-// per key group) up to 2048 cache rows, 256 (4 rows) beyond (measured on
-// MI355X with the earlier three-launch split: 512 threads faster at up to
-// 2048 keys, slower at 8192).
+// holding CH / (NT / 8) of the chunk's K / V rows.  512 threads up to 2048
+// cache rows, 256 beyond (measured on MI355X with the earlier three-launch
+// split: 512 threads faster at up to 2048 keys, slower at 8192; with
+// 256-key chunks at 2048 keys, 1024 threads 7.7 us and 256 threads 8.3 us
+// against 7.55 us for 512).
 constexpr int AS_NT_ROWS = 2048;
-template <int NT>
+template <int NT, int CH>
 struct As {
-    static constexpr int NG = NT / 8, U = AS_CH / NG, NWV = NT / 64;
+    static constexpr int NG = NT / 8, U = CH / NG, NWV = NT / 64;
+    static_assert(U >= 1 && CH % NG == 0, "chunk rows per key group");
 };
-// key chunks of one head at the longest row any entry point attends (65,536 keys)
+// key chunks of one head at the longest row any entry point attends (65,536
+// keys), at the shorter chunk length (the scratch bound for both)
 constexpr int AS_MAX_CH = kAttnMaxKeys / AS_CH;
 
 struct SplitBufs {
@@ -619,9 +627,9 @@ __device__ __forceinline__ float asplit_combine(const float* pm, const float* ps
     return !isfinite(M) ? h2f(f2h(1.0f / (float)J)) * num : num / den;
 }
 
-template <int D, int NT, bool XCH>
+template <int D, int NT, bool XCH, int CH>
 __global__ __launch_bounds__(NT) void asplit_kernel(AttnArgs a, SplitBufs b) {
-    constexpr int EPL = D / 8, NW = EPL / 2, NWV = As<NT>::NWV, AS_NG = As<NT>::NG, AS_U = As<NT>::U;
+    constexpr int EPL = D / 8, NW = EPL / 2, NWV = As<NT, CH>::NWV, AS_NG = As<NT, CH>::NG, AS_U = As<NT, CH>::U;
     __shared__ float red[2][NWV];
     __shared__ float part[NWV][D];
     __shared__ int last;
@@ -630,7 +638,7 @@ __global__ __launch_bounds__(NT) void asplit_kernel(AttnArgs a, SplitBufs b) {
     const size_t wstride = (size_t)a.Hkv * D / 2;
     const uint32_t* kbase = (const uint32_t*)(a.k + (size_t)kvh * D + EPL * c);
     const uint32_t* vbase = (const uint32_t*)(a.v + (size_t)kvh * D + EPL * c);
-    const int j0 = ch * AS_CH;
+    const int j0 = ch * CH;
     // every K and V row of the chunk in flight before anything waits
     uint32_t kw[AS_U][NW], vw[AS_U][NW];
 #pragma unroll
@@ -648,7 +656,7 @@ __global__ __launch_bounds__(NT) void asplit_kernel(AttnArgs a, SplitBufs b) {
         }
     }
     const int J = asplit_keys(a, b);
-    const int nc = (J + AS_CH - 1) / AS_CH;
+    const int nc = (J + CH - 1) / CH;
     if (ch >= nc) return;   // (uniform: chunk past the keys; it is not counted)
     float mx = -INFINITY, sv[AS_U];
 #pragma unroll
@@ -735,11 +743,11 @@ __global__ __launch_bounds__(NT) void asplit_kernel(AttnArgs a, SplitBufs b) {
 // The chunks of a head combined by a kernel of its own (the kernel boundary
 // orders the partials' stores before these loads): one workgroup per head,
 // thread d sums dim d over the chunks in chunk order.
-template <int D>
+template <int D, int CH>
 __global__ __launch_bounds__(D) void asplit_combine_kernel(AttnArgs a, SplitBufs b) {
     const int h = blockIdx.x, tid = threadIdx.x;
     const int J = asplit_keys(a, b);
-    const int nc = (J + AS_CH - 1) / AS_CH;
+    const int nc = (J + CH - 1) / CH;
     const size_t hc = (size_t)h * b.nch;
     const float r = asplit_combine(b.mx + hc, b.sum + hc, b.o + hc * D + tid, D, nc, J);
     a.out[(size_t)h * D + tid] = f2h(r);   // (one query row)
@@ -764,20 +772,22 @@ size_t attention_split_scratch(int H, int kv_rows, int D) {
     return (2 * (size_t)H * nch + (size_t)H * nch * D) * sizeof(float);
 }
 
-template <int D, int NT>
+template <int D, int NT, int CH>
 static void launch_split_d(hipStream_t s, const AttnArgs& a, const SplitBufs& b, dim3 grid, bool xch) {
-    if (xch) {
-        hipLaunchKernelGGL((asplit_kernel<D, NT, true>), grid, dim3(NT), 0, s, a, b);
-    } else {
-        hipLaunchKernelGGL((asplit_kernel<D, NT, false>), grid, dim3(NT), 0, s, a, b);
-        hipLaunchKernelGGL(asplit_combine_kernel<D>, dim3((unsigned)a.H), dim3(D), 0, s, a, b);
+    if constexpr (CH == AS_CH) {
+        if (xch) {
+            hipLaunchKernelGGL((asplit_kernel<D, NT, true, CH>), grid, dim3(NT), 0, s, a, b);
+            return;
+        }
     }
+    hipLaunchKernelGGL((asplit_kernel<D, NT, false, CH>), grid, dim3(NT), 0, s, a, b);
+    hipLaunchKernelGGL((asplit_combine_kernel<D, CH>), dim3((unsigned)a.H), dim3(D), 0, s, a, b);
 }
-template <int NT>
+template <int NT, int CH>
 static void launch_split_kernel(hipStream_t s, const AttnArgs& a, const SplitBufs& b, dim3 grid, bool xch) {
-    if (a.D == 64) launch_split_d<64, NT>(s, a, b, grid, xch);
-    else if (a.D == 80) launch_split_d<80, NT>(s, a, b, grid, xch);
-    else launch_split_d<128, NT>(s, a, b, grid, xch);
+    if (a.D == 64) launch_split_d<64, NT, CH>(s, a, b, grid, xch);
+    else if (a.D == 80) launch_split_d<80, NT, CH>(s, a, b, grid, xch);
+    else launch_split_d<128, NT, CH>(s, a, b, grid, xch);
 }
 // The in-kernel exchange up to AS_XCH_CHUNKS chunks per head, the combine
 // kernel beyond: each agent-scope round trip of the exchange (store ack,
@@ -785,23 +795,27 @@ static void launch_split_kernel(hipStream_t s, const AttnArgs& a, const SplitBuf
 // more chunks a head has, the later its last one arrives.  Measured on one
 // box: Phi-2 decode (7 chunks at 776 cache rows) 800.5 tok/s with the
 // exchange vs 774.3 with the combine kernel; one row over 2048 keys at head
-// dim 64 (16 chunks) 10.68 vs 9.32 us.
+// dim 64 in 16 chunks of 128 keys, 10.8 vs 8.4 us per call.
 constexpr int AS_XCH_CHUNKS = 8;
+constexpr int AS_XCH_ROWS = AS_XCH_CHUNKS * AS_CH;
 
 static tlhip_status launch_split(hipStream_t s, const AttnArgs& a, SplitBufs b, float* scratch) {
     if (!a.head_flags || a.H > ATTN_SPLIT_MAX_HEADS)
         return fail(TLHIP_ERR_INVALID_ARGUMENT, "attention: key-chunked path needs the context's counters and H <= %d",
                     ATTN_SPLIT_MAX_HEADS);
-    b.nch = (a.kv_rows + AS_CH - 1) / AS_CH;
+    const bool wide = a.kv_rows > AS_XCH_ROWS && a.kv_rows <= AS_NT_ROWS;   // 2 * AS_CH-key chunks
+    const int ch = wide ? 2 * AS_CH : AS_CH;
+    b.nch = (a.kv_rows + ch - 1) / ch;
     if (b.nch > AS_MAX_CH) return fail(TLHIP_ERR_INVALID_DIMENSION, "attention: %d key chunks > %d", b.nch, AS_MAX_CH);
     b.mx = scratch;
     b.sum = b.mx + (size_t)a.H * b.nch;
     b.o = b.sum + (size_t)a.H * b.nch;
     b.flags = a.head_flags;
     const dim3 grid((unsigned)b.nch, (unsigned)a.H);
-    const bool xch = b.nch <= AS_XCH_CHUNKS;
-    if (a.kv_rows <= AS_NT_ROWS) launch_split_kernel<512>(s, a, b, grid, xch);
-    else launch_split_kernel<256>(s, a, b, grid, xch);
+    const bool xch = !wide && b.nch <= AS_XCH_CHUNKS;
+    if (wide) launch_split_kernel<512, 2 * AS_CH>(s, a, b, grid, false);
+    else if (a.kv_rows <= AS_NT_ROWS) launch_split_kernel<512, AS_CH>(s, a, b, grid, xch);
+    else launch_split_kernel<256, AS_CH>(s, a, b, grid, xch);
     return TLHIP_OK;
 }
 

@@ -145,14 +145,24 @@ def test_tiny_phi2_greedy(dev, oracle, tmp_path):
 
 def test_tiny_phi2_long_cache_split_attention(dev, oracle, tmp_path):
     """Head dim 80 with a cache of more than 512 rows: decode attention runs
-    key-chunked (128-key chunks: scores, exp, P.V, combine) instead of one
-    workgroup per head.  A 520-token prompt then 24 steps cross the chunk
-    boundary at 640 keys from a partly filled fifth chunk; tokens must equal
-    the oracle's."""
+    key-chunked (128-key chunks, combined by the last workgroup of each head
+    to arrive) instead of one workgroup per head.  A 620-token prompt then
+    24 steps cross the chunk boundary at 640 keys from a partly filled fifth
+    chunk; tokens must equal the oracle's."""
     path = str(tmp_path / "tiny_phi2_long.gguf")
     S.write_phi2_gguf(path, seed=27, **TINY_PHI2)
     prompt = S.token_ids(27, "prompt", 620, TINY_PHI2["vocab"])
     _compare(dev, oracle, path, 1, prompt, 24, max_ctx=700)
+
+
+def test_tiny_phi2_wide_chunk_split_attention(dev, oracle, tmp_path):
+    """A cache of 1,025..2,048 rows: decode attention runs in 256-key chunks
+    combined by a second kernel.  A 1,020-token prompt then 12 steps cross
+    the 1,024-key chunk boundary; tokens must equal the oracle's."""
+    path = str(tmp_path / "tiny_phi2_wide.gguf")
+    S.write_phi2_gguf(path, seed=28, **TINY_PHI2)
+    prompt = S.token_ids(28, "prompt", 1020, TINY_PHI2["vocab"])
+    _compare(dev, oracle, path, 1, prompt, 12, max_ctx=1100)
 
 
 def test_long_prompt_chunked_prefill(dev, oracle, tmp_path):

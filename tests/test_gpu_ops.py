@@ -550,6 +550,8 @@ def test_einsums_head_dims(dev, oracle, I, J, H, Hkv, D):
     (3, 600, 4, 2, 80, 597, True), (2, 1100, 4, 4, 80, 0, False),
     # config 3 at its head layout: 32 query / 4 KV heads (GQA group 8), D = 64
     (2048, 2048, 32, 4, 64, 0, True), (1, 2048, 32, 4, 64, 2047, True), (256, 1024, 32, 4, 64, 768, True),
+    # one row over 1025..2048 keys: 256-key chunks and the combine kernel
+    (1, 1025, 4, 4, 80, 1024, True), (1, 1500, 8, 2, 128, 1499, True), (1, 1999, 32, 4, 64, 0, False),
     # staged kernel at head dims 80 and 128, ragged key counts, odd tile counts
     (300, 300, 8, 2, 80, 0, True), (200, 150, 8, 2, 80, 0, False), (129, 129, 4, 2, 128, 0, True),
     (256, 333, 8, 2, 128, 77, True), (160, 1000, 8, 1, 64, 840, True)])
