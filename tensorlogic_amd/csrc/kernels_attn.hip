@@ -633,7 +633,19 @@ __global__ __launch_bounds__(NT) void asplit_kernel(AttnArgs a, SplitBufs b) {
     __shared__ float red[2][NWV];
     __shared__ float part[NWV][D];
     __shared__ int last;
-    const int ch = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, c = tid & 7, g = tid >> 3;
+    // Workgroup i runs on XCD i % 8.  With GQA the default order (chunk
+    // fastest) gives each XCD the same chunk of every head, so a KV head's
+    // rows are read by one XCD per chunk.  Without GQA (H == Hkv) heads share
+    // nothing but the cache lines at their row boundaries (Phi-2: 160-byte
+    // head rows), so each XCD takes H/8 consecutive heads, all chunks, and
+    // its L2 fetches a shared line once.
+    int ch = blockIdx.x, h = blockIdx.y;
+    if (a.H == a.Hkv && (a.H & 7) == 0) {
+        const int id = blockIdx.x + gridDim.x * blockIdx.y, q = id >> 3;
+        h = (id & 7) * (a.H >> 3) + q / (int)gridDim.x;
+        ch = q % (int)gridDim.x;
+    }
+    const int tid = threadIdx.x, c = tid & 7, g = tid >> 3;
     const int kvh = h / (a.H / a.Hkv);
     const size_t wstride = (size_t)a.Hkv * D / 2;
     const uint32_t* kbase = (const uint32_t*)(a.k + (size_t)kvh * D + EPL * c);
