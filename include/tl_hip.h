@@ -154,19 +154,23 @@ tlhip_status tlhip_linear_noalloc(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w,
  * mismatch: InvalidOperation, as Tensor::matmul returns. */
 tlhip_status tlhip_matmul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor c);
 /* rms_norm(x, w[, eps]) (builtin_nn.rs:44-103, normalization.rs:42-250)
- * over the last dim.                                                       */
+ * over the last dim.  x, w, y all f16, or all f32 (the TensorF32 arm,
+ * rms_norm_simple_f32 / rms_norm_f32, unified.metal:1961-2036).            */
 tlhip_status tlhip_rms_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, float eps, tlhip_tensor y);
 /* layer_norm (normalization.rs:271-535); w and b may be NULL.             */
 tlhip_status tlhip_layer_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor b, float eps, tlhip_tensor y);
 /* rope(x[, offset]) (builtin_tensor.rs:514-556, rope.rs:71-300): x [..,S,H,D].
- * rot_dims 0 = D.  The reference's rope() is layout INTERLEAVED, theta 10000. */
+ * rot_dims 0 = D.  The reference's rope() is layout INTERLEAVED, theta 10000.
+ * x and y both f16, or both f32 (rope_f32, unified.metal:2420-2482).       */
 tlhip_status tlhip_rope(tlhip_ctx ctx, tlhip_tensor x, int offset, float theta,
                         tlhip_rope_layout layout, int rot_dims, tlhip_tensor y);
-/* softmax(x) over the last dim (activations.rs:107-230). */
+/* softmax(x) over the last dim (activations.rs:107-230); x and y both f16,
+ * or both f32 (softmax_simple_f32 / softmax_f32, unified.metal:2202-2340). */
 tlhip_status tlhip_softmax_lastdim(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y);
-/* sigmoid (activations.rs:239-266); silu = x * sigmoid(x) as the TL
- * function silu (chat_demo_optimized.tl:35-37); silu_mul = silu(g) * u
- * (swiglu_ffn's intermediate); gelu (tanh form, unified.metal:837-848).   */
+/* sigmoid (activations.rs:239-266; f16, or f32 in and out: sigmoid_f32,
+ * unified.metal:1129-1135); silu = x * sigmoid(x) as the TL function silu
+ * (chat_demo_optimized.tl:35-37); silu_mul = silu(g) * u (swiglu_ffn's
+ * intermediate); gelu (tanh form, unified.metal:837-848).                 */
 tlhip_status tlhip_sigmoid(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y);
 tlhip_status tlhip_silu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y);
 tlhip_status tlhip_silu_mul(tlhip_ctx ctx, tlhip_tensor gate, tlhip_tensor up, tlhip_tensor y);
@@ -206,8 +210,10 @@ tlhip_status tlhip_rope_cos_sin(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor cos_
 tlhip_status tlhip_precompute_rope(tlhip_ctx ctx, int head_dim, int max_seq_len, float base, int want_sin,
                                    tlhip_tensor out);
 /* einsum("ihd,jhd->ihj") and einsum("ihj,jhd->ihd") (einsum.rs:653-886),
- * fp32 accumulation, f16 out.  K/V may carry fewer heads than Q (GQA:
- * head h reads h / (H/Hkv)), replacing broadcast_to + contiguous.         */
+ * fp32 accumulation, f16 out; or all operands f32 (einsum_ihd_jhd_ihj_f32 /
+ * einsum_ihj_jhd_ihd_f32, unified.metal:2702-2768: fused sums in index
+ * order).  K/V may carry fewer heads than Q (GQA: head h reads
+ * h / (H/Hkv)), replacing broadcast_to + contiguous.                      */
 tlhip_status tlhip_einsum_scores(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhip_tensor scores);
 tlhip_status tlhip_einsum_context(tlhip_ctx ctx, tlhip_tensor p, tlhip_tensor v, tlhip_tensor out);
 /* Fused attention = einsum scores -> * scale (f16) -> causal mask (-10000)

@@ -85,6 +85,12 @@ def _declare(L):
         "tlo_causal_mask": (None, [i, vp]),
         "tlo_slice_last": (i, [vp, vp, i, i, i, vp]),
         "tlo_linear_f32": (None, [vp, vp, vp, i, i, i, vp]),
+        "tlo_rms_norm_f32": (None, [vp, vp, i, i, f, vp]),
+        "tlo_softmax_f32": (None, [vp, i, i, vp]),
+        "tlo_rope_f32": (None, [vp, i, i, i, i, f, i, i, vp]),
+        "tlo_sigmoid_f32": (None, [vp, sz, vp]),
+        "tlo_einsum_scores_f32": (None, [vp, vp, i, i, i, i, i, vp]),
+        "tlo_einsum_context_f32": (None, [vp, vp, i, i, i, i, i, vp]),
         "tlo_tensor_argmax": (C.c_int64, [vp, vp, i, i, vp]),
         "tlo_broadcast_to": (i, [vp, vp, i, vp, i, i, vp]),
         "tlo_rope_cos_sin": (i, [vp, i, i, i, vp, vp, i, vp]),
@@ -165,6 +171,64 @@ def linear_f32(x, w, bias=None) -> np.ndarray:
     y = np.empty((M, N), np.float32)
     lib().tlo_linear_f32(_p(x), _p(w), _p(b) if b is not None else None, M, N, K, _p(y))
     return y
+
+
+def _f(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def rms_norm_f32(x, w, eps=1e-6) -> np.ndarray:
+    """rms_norm on f32 operands (tlo_rms_norm_f32: the reference f32
+    kernels' summation order)."""
+    x, w = _f(x), _f(w)
+    n = x.shape[-1]
+    y = np.empty_like(x)
+    lib().tlo_rms_norm_f32(_p(x), _p(w), x.size // n, n, eps, _p(y))
+    return y
+
+
+def softmax_f32(x) -> np.ndarray:
+    x = _f(x)
+    n = x.shape[-1]
+    y = np.empty_like(x)
+    lib().tlo_softmax_f32(_p(x), x.size // n, n, _p(y))
+    return y
+
+
+def rope_f32(x, offset=0, theta=10000.0, layout=0, rot_dims=0) -> np.ndarray:
+    x = _f(x)
+    S, H, D = x.shape[-3], x.shape[-2], x.shape[-1]
+    lead = x.size // (S * H * D)
+    y = np.empty_like(x)
+    xf, yf = x.reshape(lead, S, H, D), y.reshape(lead, S, H, D)
+    for i in range(lead):
+        lib().tlo_rope_f32(_p(np.ascontiguousarray(xf[i])), S, H, D, offset, theta, layout, rot_dims, _p(yf[i]))
+    return y
+
+
+def sigmoid_f32(x) -> np.ndarray:
+    x = _f(x)
+    y = np.empty_like(x)
+    lib().tlo_sigmoid_f32(_p(x), x.size, _p(y))
+    return y
+
+
+def einsum_scores_f32(q, k) -> np.ndarray:
+    q, k = _f(q), _f(k)
+    I, H, D = q.shape
+    J, Hkv, _ = k.shape
+    out = np.empty((I, H, J), np.float32)
+    lib().tlo_einsum_scores_f32(_p(q), _p(k), I, J, H, Hkv, D, _p(out))
+    return out
+
+
+def einsum_context_f32(p, v) -> np.ndarray:
+    p, v = _f(p), _f(v)
+    I, H, J = p.shape
+    _, Hkv, D = v.shape
+    out = np.empty((I, H, D), np.float32)
+    lib().tlo_einsum_context_f32(_p(p), _p(v), I, J, H, Hkv, D, _p(out))
+    return out
 
 
 def linear_q(x, blocks, gtype, N, bias=None, acc=ACC_F32) -> np.ndarray:

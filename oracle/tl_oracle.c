@@ -384,6 +384,142 @@ void tlo_sigmoid(const uint16_t* x, size_t n, uint16_t* y) {
     for (size_t i = 0; i < n; i++) y[i] = sigmoid_h(x[i]);
 }
 
+/* ======================================================================== */
+/* the TensorF32 arms: f32 in, f32 out, f32 arithmetic                      */
+/* ======================================================================== */
+
+/* rms_norm_simple_f32 / rms_norm_f32 (unified.metal:1961-2036; dispatch
+   normalization.rs:139-177): rows of n <= 256 summed by one thread in
+   element order, longer rows as 256 partial sums (thread t: elements t,
+   t + 256, ...) reduced by a halving tree (partial t += partial t + stride,
+   stride 128 .. 1).  Each square joins its sum as one fused multiply-add,
+   the contraction Metal's default fast math makes of `sum += v * v`
+   (assumed, as in tlo_linear_f32).  rms = sqrt(sum / n + eps),
+   y = (x * (1 / rms)) * w. */
+void tlo_rms_norm_f32(const float* x, const float* w, int rows, int n, float eps, float* y) {
+    for (int r = 0; r < rows; r++) {
+        const float* xr = x + (size_t)r * n;
+        float sq;
+        if (n <= 256) {
+            sq = 0.0f;
+            for (int i = 0; i < n; i++) sq = fmaf(xr[i], xr[i], sq);
+        } else {
+            float part[256];
+            for (int t = 0; t < 256; t++) {
+                float s = 0.0f;
+                for (int i = t; i < n; i += 256) s = fmaf(xr[i], xr[i], s);
+                part[t] = s;
+            }
+            for (int st = 128; st > 0; st >>= 1)
+                for (int t = 0; t < st; t++) part[t] = part[t] + part[t + st];
+            sq = part[0];
+        }
+        const float mean_sq = sq / (float)n;
+        const float rms = sqrtf(mean_sq + eps);
+        const float inv = 1.0f / rms;
+        for (int i = 0; i < n; i++) {
+            const float nv = xr[i] * inv;
+            y[(size_t)r * n + i] = nv * w[i];
+        }
+    }
+}
+
+/* softmax_simple_f32 / softmax_f32 (unified.metal:2202-2340; both run as
+   one thread per row, activations.rs:155-209): max over the finite values
+   (0 if none), e = exp(x - max) (0 for a non-finite x), sum in element
+   order, y = e / sum, or 1/n everywhere when the sum is not a positive
+   finite number. */
+void tlo_softmax_f32(const float* x, int rows, int n, float* y) {
+    for (int r = 0; r < rows; r++) {
+        const float* xr = x + (size_t)r * n;
+        float* yr = y + (size_t)r * n;
+        float mx = -INFINITY;
+        for (int i = 0; i < n; i++) if (isfinite(xr[i])) mx = fmaxf(mx, xr[i]);
+        if (!isfinite(mx)) mx = 0.0f;
+        float sum = 0.0f;
+        for (int i = 0; i < n; i++) {
+            const float e = isfinite(xr[i]) ? expf(xr[i] - mx) : 0.0f;
+            yr[i] = e;
+            sum += e;
+        }
+        if (sum > 0.0f && isfinite(sum)) {
+            for (int i = 0; i < n; i++) yr[i] = yr[i] / sum;
+        } else {
+            const float u = 1.0f / (float)n;
+            for (int i = 0; i < n; i++) yr[i] = u;
+        }
+    }
+}
+
+/* rope_f32 (unified.metal:2420-2482): tlo_rope's angles and rotation with
+   f32 rows in and out. */
+void tlo_rope_f32(const float* x, int S, int H, int D, int offset, float theta, int layout, int rot_dims, float* y) {
+    if (rot_dims <= 0 || rot_dims > D) rot_dims = D;
+    const int half = rot_dims / 2;
+    float* cs = (float*)malloc(sizeof(float) * 2 * (size_t)(half > 0 ? half : 1));
+    for (int s = 0; s < S; s++) {
+        const int pos = offset + s;
+        for (int i = 0; i < half; i++) {
+            const float expo = (float)(2 * i) / (float)rot_dims;
+            const float freq = 1.0f / powf(theta, expo);
+            const float ang = (float)pos * freq;
+            cs[2 * i + 0] = (float)cos((double)ang);
+            cs[2 * i + 1] = (float)sin((double)ang);
+        }
+        for (int h = 0; h < H; h++) {
+            const float* xr = x + ((size_t)s * H + h) * D;
+            float* yr = y + ((size_t)s * H + h) * D;
+            for (int d = rot_dims; d < D; d++) yr[d] = xr[d];
+            for (int i = 0; i < half; i++) {
+                int i0, i1;
+                if (layout == TLO_ROPE_INTERLEAVED) { i0 = 2 * i; i1 = 2 * i + 1; }
+                else { i0 = i; i1 = i + half; }
+                const float c = cs[2 * i], sn = cs[2 * i + 1];
+                const float x0 = xr[i0], x1 = xr[i1];
+                const float a = x0 * c, bb = x1 * sn, e = x0 * sn, f = x1 * c;
+                yr[i0] = a - bb;
+                yr[i1] = e + f;
+            }
+        }
+    }
+    free(cs);
+}
+
+/* sigmoid_f32 (unified.metal:1129-1135) */
+void tlo_sigmoid_f32(const float* x, size_t n, float* y) {
+    for (size_t i = 0; i < n; i++) y[i] = 1.0f / (1.0f + expf(-x[i]));
+}
+
+/* einsum_ihd_jhd_ihj_f32 / einsum_ihj_jhd_ihd_f32 (unified.metal:2702-2768):
+   the sum over d (scores) or j (context) in index order, one fused
+   multiply-add per term; query head h reads KV head h / (H / Hkv). */
+void tlo_einsum_scores_f32(const float* q, const float* k, int I, int J, int H, int Hkv, int D, float* out) {
+    const int group = H / Hkv;
+    for (int i = 0; i < I; i++)
+        for (int h = 0; h < H; h++) {
+            const float* qr = q + ((size_t)i * H + h) * D;
+            for (int j = 0; j < J; j++) {
+                const float* kr = k + ((size_t)j * Hkv + h / group) * D;
+                float sum = 0.0f;
+                for (int d = 0; d < D; d++) sum = fmaf(qr[d], kr[d], sum);
+                out[((size_t)i * H + h) * J + j] = sum;
+            }
+        }
+}
+
+void tlo_einsum_context_f32(const float* p, const float* v, int I, int J, int H, int Hkv, int D, float* out) {
+    const int group = H / Hkv;
+    for (int i = 0; i < I; i++)
+        for (int h = 0; h < H; h++) {
+            const float* pr = p + ((size_t)i * H + h) * J;
+            for (int d = 0; d < D; d++) {
+                float sum = 0.0f;
+                for (int j = 0; j < J; j++) sum = fmaf(pr[j], v[((size_t)j * Hkv + h / group) * D + d], sum);
+                out[((size_t)i * H + h) * D + d] = sum;
+            }
+        }
+}
+
 void tlo_silu(const uint16_t* x, size_t n, uint16_t* y) {
     lut_init();
     for (size_t i = 0; i < n; i++) {

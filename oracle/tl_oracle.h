@@ -119,6 +119,14 @@ void tlo_rope_table(int max_pos, int rot_dims, float theta, float* cs);
 void tlo_softmax(const uint16_t* x, int rows, int n, uint16_t* y);
 /* sigmoid_cpu activations.rs:252-266: f16(1 / (1 + exp(-x))) in f32.       */
 void tlo_sigmoid(const uint16_t* x, size_t n, uint16_t* y);
+/* the TensorF32 arms (unified.metal:1129-1135, 1961-2036, 2202-2340,
+   2420-2482, 2702-2768): f32 in and out */
+void tlo_rms_norm_f32(const float* x, const float* w, int rows, int n, float eps, float* y);
+void tlo_softmax_f32(const float* x, int rows, int n, float* y);
+void tlo_rope_f32(const float* x, int S, int H, int D, int offset, float theta, int layout, int rot_dims, float* y);
+void tlo_sigmoid_f32(const float* x, size_t n, float* y);
+void tlo_einsum_scores_f32(const float* q, const float* k, int I, int J, int H, int Hkv, int D, float* out);
+void tlo_einsum_context_f32(const float* p, const float* v, int I, int J, int H, int Hkv, int D, float* out);
 /* TL silu(x) = x * sigmoid(x) (examples/chat_demo_optimized.tl:35-37):
  * s = sigmoid(x) stored f16, then f16(x * s).                              */
 void tlo_silu(const uint16_t* x, size_t n, uint16_t* y);

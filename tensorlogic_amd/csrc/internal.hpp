@@ -254,6 +254,16 @@ tlhip_status launch_rope(hipStream_t s, const uint16_t* x, uint16_t* y, int S, i
                          int64_t batch, int offset, const int32_t* d_pos, int layout,
                          int rot_dims, const float* table, int x_row_stride, int y_row_stride);
 tlhip_status launch_softmax(hipStream_t s, const uint16_t* x, uint16_t* y, int64_t rows, int n);
+// the TensorF32 arms (f32 in and out)
+tlhip_status launch_rms_norm_f32(hipStream_t s, const float* x, const float* w, float* y, int rows, int n, float eps);
+tlhip_status launch_softmax_f32(hipStream_t s, const float* x, float* y, int64_t rows, int n);
+tlhip_status launch_rope_f32(hipStream_t s, const float* x, float* y, int S, int H, int D, int64_t batch, int offset,
+                             int layout, int rot_dims, const float* table);
+tlhip_status launch_sigmoid_f32(hipStream_t s, const float* x, float* y, int64_t n);
+tlhip_status launch_scores_f32(hipStream_t s, const float* q, const float* k, float* sc, int I, int J, int H, int Hkv,
+                               int D);
+tlhip_status launch_context_f32(hipStream_t s, const float* p, const float* v, float* out, int I, int J, int H, int Hkv,
+                                int D);
 tlhip_status launch_tensor_argmax(hipStream_t s, tlhip_dtype dt, const void* x, void* y, const int64_t* shape, int nd,
                                   int dim);   // dim < 0: whole tensor; y: one element per line
 enum EwOp { EW_SIGMOID = 0, EW_SILU = 1, EW_GELU = 2, EW_ADD = 3, EW_MUL = 4, EW_MUL_SCALAR = 5,

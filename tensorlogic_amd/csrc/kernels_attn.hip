@@ -1901,4 +1901,57 @@ tlhip_status launch_context(hipStream_t s, const uint16_t* p, const uint16_t* v,
     return TLHIP_OK;
 }
 
+// einsum_ihd_jhd_ihj_f32 / einsum_ihj_jhd_ihd_f32 (unified.metal:2702-2768,
+// einsum.rs:740-886): one thread per output, the sum over d (scores) or j
+// (context) in index order, each term one fused multiply-add (the
+// contraction of `sum += A * B` under Metal's default fast math, assumed as
+// for the f32 linear).  Query head h reads KV head h / (H / Hkv); the
+// reference's kernels take equal head counts, which is Hkv == H.
+__global__ void scores_f32_kernel(const float* __restrict__ q, const float* __restrict__ k, float* __restrict__ sc,
+                                  int I, int J, int H, int Hkv, int D) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)I * H * J) return;
+    const int j = (int)(idx % J);
+    const int64_t ih = idx / J;
+    const int h = (int)(ih % H);
+    const float* qr = q + (size_t)ih * D;
+    const float* kr = k + ((size_t)j * Hkv + h / (H / Hkv)) * D;
+    float sum = 0.0f;
+    for (int d = 0; d < D; d++) sum = fmaf(qr[d], kr[d], sum);
+    sc[idx] = sum;
+}
+
+__global__ void context_f32_kernel(const float* __restrict__ p, const float* __restrict__ v, float* __restrict__ out,
+                                   int I, int J, int H, int Hkv, int D) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)I * H * D) return;
+    const int d = (int)(idx % D);
+    const int64_t ih = idx / D;
+    const int h = (int)(ih % H);
+    const float* pr = p + (size_t)ih * J;
+    const float* vc = v + (size_t)(h / (H / Hkv)) * D + d;
+    const size_t vstride = (size_t)Hkv * D;
+    float sum = 0.0f;
+    for (int j = 0; j < J; j++) sum = fmaf(pr[j], vc[(size_t)j * vstride], sum);
+    out[idx] = sum;
+}
+
+tlhip_status launch_scores_f32(hipStream_t s, const float* q, const float* k, float* sc, int I, int J, int H, int Hkv,
+                               int D) {
+    const int64_t n = (int64_t)I * H * J;
+    if (n <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(scores_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, q, k, sc, I, J, H, Hkv,
+                       D);
+    return TLHIP_OK;
+}
+
+tlhip_status launch_context_f32(hipStream_t s, const float* p, const float* v, float* out, int I, int J, int H, int Hkv,
+                                int D) {
+    const int64_t n = (int64_t)I * H * D;
+    if (n <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(context_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, v, out, I, J, H,
+                       Hkv, D);
+    return TLHIP_OK;
+}
+
 }  // namespace tlhip

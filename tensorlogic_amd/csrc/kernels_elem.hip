@@ -1050,4 +1050,146 @@ tlhip_status launch_transpose_f32(hipStream_t s, const float* src, float* dst, i
     return launch_transpose_t(s, src, dst, rows, cols);
 }
 
+// ---------------------------------------------------------------------------
+// The TensorF32 arms of rms_norm, softmax, rope and sigmoid (f32 in, f32
+// out, f32 arithmetic).
+
+// rms_norm_simple_f32 / rms_norm_f32 (unified.metal:1961-2036, dispatched by
+// normalization.rs:139-177): the sum of squares in the reference's order --
+// rows of n <= 256 by one thread in element order; longer rows as 256
+// partial sums (thread t: elements t, t + 256, ...) and then a halving tree,
+// partial t adding partial t + stride for stride = 128, 64, ..., 1.  Each
+// square joins its partial sum as one fused multiply-add, the contraction
+// Metal's default fast math makes of `sum += v * v` (assumed, as for the f32
+// linear).  Then rms = sqrt(sum / n + eps) and y = (x * (1 / rms)) * w.
+__global__ __launch_bounds__(256) void rms_norm_f32_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                           float* __restrict__ y, int n, float eps) {
+    __shared__ float part[256];
+    const float* xr = x + (size_t)blockIdx.x * n;
+    float* yr = y + (size_t)blockIdx.x * n;
+    const int t = threadIdx.x;
+    if (n <= 256) {
+        if (t == 0) {
+            float s = 0.0f;
+            for (int i = 0; i < n; i++) s = fmaf(xr[i], xr[i], s);
+            part[0] = s;
+        }
+        __syncthreads();
+    } else {
+        float s = 0.0f;
+        for (int i = t; i < n; i += 256) s = fmaf(xr[i], xr[i], s);
+        part[t] = s;
+        __syncthreads();
+        for (int st = 128; st > 0; st >>= 1) {
+            if (t < st) part[t] = part[t] + part[t + st];
+            __syncthreads();
+        }
+    }
+    const float mean_sq = part[0] / (float)n;
+    const float rms = sqrtf(mean_sq + eps);
+    const float inv = 1.0f / rms;
+    for (int i = t; i < n; i += 256) yr[i] = (xr[i] * inv) * w[i];
+}
+
+tlhip_status launch_rms_norm_f32(hipStream_t s, const float* x, const float* w, float* y, int rows, int n, float eps) {
+    if (rows <= 0 || n <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(rms_norm_f32_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, w, y, n, eps);
+    return TLHIP_OK;
+}
+
+// softmax_simple_f32 / softmax_f32 (unified.metal:2202-2340; both run one
+// thread per row, activations.rs:155-209): max over the finite values (0 if
+// none), e = exp(x - max) (0 for a non-finite x), y = e / sum, or 1/n
+// everywhere when the sum is not a positive finite number.  The max and the
+// exponentials are spread over the workgroup; the sum is taken in element
+// order by one thread, as the reference's: a tree sum drifts from that
+// running f32 sum by ~20 ulps at 1000 elements.
+__global__ __launch_bounds__(256) void softmax_f32_kernel(const float* __restrict__ x, float* __restrict__ y, int n) {
+    __shared__ float red[4];
+    __shared__ float total;
+    const float* xr = x + (size_t)blockIdx.x * n;
+    float* yr = y + (size_t)blockIdx.x * n;
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = xr[i];
+        if (isfinite(v)) mx = fmaxf(mx, v);
+    }
+    mx = block_max256(mx, red);
+    if (!isfinite(mx)) mx = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = xr[i];
+        yr[i] = isfinite(v) ? expf(v - mx) : 0.0f;
+    }
+    __syncthreads();   // (the block's global writes are visible to thread 0 after it)
+    if (threadIdx.x == 0) {
+        float s = 0.0f;
+        for (int i = 0; i < n; i++) s += yr[i];
+        total = s;
+    }
+    __syncthreads();
+    const float sum = total;
+    if (sum > 0.0f && isfinite(sum)) {
+        for (int i = threadIdx.x; i < n; i += 256) yr[i] = yr[i] / sum;
+    } else {
+        const float u = 1.0f / (float)n;
+        for (int i = threadIdx.x; i < n; i += 256) yr[i] = u;
+    }
+}
+
+tlhip_status launch_softmax_f32(hipStream_t s, const float* x, float* y, int64_t rows, int n) {
+    if (rows <= 0 || n <= 0) return TLHIP_OK;
+    if (rows > 0x7fffffff) return fail(TLHIP_ERR_INVALID_DIMENSION, "softmax: %lld rows", (long long)rows);
+    hipLaunchKernelGGL(softmax_f32_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, y, n);
+    return TLHIP_OK;
+}
+
+// rope_f32 (unified.metal:2420-2482): rope_kernel's indexing, table and
+// rotation (rope_pair, separately rounded products) with f32 rows in and
+// out.
+__global__ void rope_f32_kernel(const float* __restrict__ x, float* __restrict__ y, int S, int H, int D, int64_t batch,
+                                int offset, int layout, int rot, const float* __restrict__ table) {
+    const int half = rot / 2;
+    const int64_t per_row = (int64_t)H * (D - half);
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= batch * S * per_row) return;
+    const int64_t row = idx / per_row, rem = idx % per_row;
+    const int h = (int)(rem / (D - half)), e = (int)(rem % (D - half));
+    const int pos = offset + (int)(row % S);
+    const float* xr = x + ((size_t)row * H + h) * D;
+    float* yr = y + ((size_t)row * H + h) * D;
+    if (e < half) {
+        int i0, i1;
+        rope_indices(layout, e, half, i0, i1);
+        const float c = table[2 * ((size_t)pos * half + e)], sn = table[2 * ((size_t)pos * half + e) + 1];
+        float r0, r1;
+        rope_pair(xr[i0], xr[i1], c, sn, r0, r1);
+        yr[i0] = r0;
+        yr[i1] = r1;
+    } else {
+        const int d = rot + (e - half);
+        yr[d] = xr[d];
+    }
+}
+
+tlhip_status launch_rope_f32(hipStream_t s, const float* x, float* y, int S, int H, int D, int64_t batch, int offset,
+                             int layout, int rot_dims, const float* table) {
+    const int64_t total = batch * S * (int64_t)H * (D - rot_dims / 2);
+    if (total <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(rope_f32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, x, y, S, H, D, batch,
+                       offset, layout, rot_dims, table);
+    return TLHIP_OK;
+}
+
+// sigmoid_f32 (unified.metal:1129-1135): 1 / (1 + exp(-x)).
+__global__ void sigmoid_f32_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = 1.0f / (1.0f + expf(-x[i]));
+}
+
+tlhip_status launch_sigmoid_f32(hipStream_t s, const float* x, float* y, int64_t n) {
+    if (n <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(sigmoid_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
+    return TLHIP_OK;
+}
+
 }  // namespace tlhip

@@ -28,6 +28,20 @@ tlhip_status f16_args(const char* op, std::initializer_list<tlhip_tensor> ts) {
 }
 
 uint16_t* P(tlhip_tensor t) { return (uint16_t*)t->data; }
+float* F(tlhip_tensor t) { return (float*)t->data; }
+
+// Operands of an op with a TensorF16 and a TensorF32 arm: all F16 or all F32
+// (a mix is the reference's TypeError); *f32 tells which.
+tlhip_status float_args(const char* op, std::initializer_list<tlhip_tensor> ts, bool* f32) {
+    const tlhip_tensor first = *ts.begin();
+    TLHIP_TRY(check_t(first, op));
+    *f32 = first->dtype == TLHIP_F32;
+    for (tlhip_tensor t : ts) {
+        TLHIP_TRY(check_t(t, op));
+        TLHIP_TRY(check_dtype(t, *f32 ? TLHIP_F32 : TLHIP_F16, op));
+    }
+    return TLHIP_OK;
+}
 
 float round_f16(float f) {
     // scalar operands of f16 ops are f16 values (T::from_f32)
@@ -237,14 +251,16 @@ tlhip_status tlhip_matmul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_t
 
 tlhip_status tlhip_rms_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, float eps, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args("rms_norm", {x, w, y}));
+    bool f32;
+    TLHIP_TRY(float_args("rms_norm", {x, w, y}, &f32));
     TLHIP_TRY(same_shape(x, y, "rms_norm"));
     const int64_t n = last_dim(x);
     if (w->ndim != 1 || w->shape[0] != n)
         return fail(TLHIP_ERR_SHAPE_MISMATCH, "rms_norm: weight %s for normalized_shape [%lld]", shape_str(w).c_str(),
                     (long long)n);
     if (n == 0) return TLHIP_OK;
-    TLHIP_TRY(launch_rms_norm(ctx->stream, P(x), P(w), P(y), (int)(numel(x) / n), (int)n, eps));
+    if (f32) TLHIP_TRY(launch_rms_norm_f32(ctx->stream, F(x), F(w), F(y), (int)(numel(x) / n), (int)n, eps));
+    else TLHIP_TRY(launch_rms_norm(ctx->stream, P(x), P(w), P(y), (int)(numel(x) / n), (int)n, eps));
     return after_launch(ctx, "rms_norm");
 } TLHIP_CATCH_STATUS
 
@@ -269,7 +285,8 @@ tlhip_status tlhip_layer_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlh
 tlhip_status tlhip_rope(tlhip_ctx ctx, tlhip_tensor x, int offset, float theta, tlhip_rope_layout layout,
                         int rot_dims, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args("rope", {x, y}));
+    bool f32;
+    TLHIP_TRY(float_args("rope", {x, y}, &f32));
     TLHIP_TRY(same_shape(x, y, "rope"));
     if (x->ndim < 3) return fail(TLHIP_ERR_INVALID_OPERATION, "RoPE requires at least 3D tensor (got %dD)", x->ndim);
     const int64_t D = x->shape[x->ndim - 1], H = x->shape[x->ndim - 2], S = x->shape[x->ndim - 3];
@@ -282,19 +299,25 @@ tlhip_status tlhip_rope(tlhip_ctx ctx, tlhip_tensor x, int offset, float theta, 
     if (numel(x) == 0) return TLHIP_OK;
     const float* table;
     TLHIP_TRY(rope_table(ctx, theta, rot_dims, offset + (int)S, &table));
-    TLHIP_TRY(launch_rope(ctx->stream, P(x), P(y), (int)S, (int)H, (int)D, numel(x) / (S * H * D), offset, nullptr,
-                          (int)layout, rot_dims, table, 0, 0));
+    if (f32)
+        TLHIP_TRY(launch_rope_f32(ctx->stream, F(x), F(y), (int)S, (int)H, (int)D, numel(x) / (S * H * D), offset,
+                                  (int)layout, rot_dims, table));
+    else
+        TLHIP_TRY(launch_rope(ctx->stream, P(x), P(y), (int)S, (int)H, (int)D, numel(x) / (S * H * D), offset,
+                              nullptr, (int)layout, rot_dims, table, 0, 0));
     return after_launch(ctx, "rope");
 } TLHIP_CATCH_STATUS
 
 tlhip_status tlhip_softmax_lastdim(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args("softmax", {x, y}));
+    bool f32;
+    TLHIP_TRY(float_args("softmax", {x, y}, &f32));
     TLHIP_TRY(same_shape(x, y, "softmax"));
     if (x->ndim == 0) return fail(TLHIP_ERR_INVALID_OPERATION, "softmax requires non-empty tensor");
     const int64_t n = last_dim(x);
     if (n == 0 || numel(x) == 0) return TLHIP_OK;
-    TLHIP_TRY(launch_softmax(ctx->stream, P(x), P(y), numel(x) / n, (int)n));
+    if (f32) TLHIP_TRY(launch_softmax_f32(ctx->stream, F(x), F(y), numel(x) / n, (int)n));
+    else TLHIP_TRY(launch_softmax(ctx->stream, P(x), P(y), numel(x) / n, (int)n));
     return after_launch(ctx, "softmax");
 } TLHIP_CATCH_STATUS
 
@@ -306,7 +329,16 @@ static tlhip_status unary(tlhip_ctx ctx, int op, tlhip_tensor x, tlhip_tensor y,
     return after_launch(ctx, nm);
 }
 
-tlhip_status tlhip_sigmoid(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) try { return unary(ctx, EW_SIGMOID, x, y, "sigmoid"); } TLHIP_CATCH_STATUS
+tlhip_status tlhip_sigmoid(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) try {
+    TLHIP_TRY(check_ctx(ctx));
+    TLHIP_TRY(check_t(x, "sigmoid"));
+    if (x->dtype != TLHIP_F32) return unary(ctx, EW_SIGMOID, x, y, "sigmoid");
+    bool f32;
+    TLHIP_TRY(float_args("sigmoid", {x, y}, &f32));
+    TLHIP_TRY(same_shape(x, y, "sigmoid"));
+    TLHIP_TRY(launch_sigmoid_f32(ctx->stream, F(x), F(y), numel(x)));
+    return after_launch(ctx, "sigmoid");
+} TLHIP_CATCH_STATUS
 tlhip_status tlhip_silu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) try { return unary(ctx, EW_SILU, x, y, "silu"); } TLHIP_CATCH_STATUS
 tlhip_status tlhip_gelu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) try { return unary(ctx, EW_GELU, x, y, "gelu"); } TLHIP_CATCH_STATUS
 
@@ -516,20 +548,23 @@ static tlhip_status qkv_dims(tlhip_tensor q, tlhip_tensor k, const char* nm, int
 
 tlhip_status tlhip_einsum_scores(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhip_tensor sc) try {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args("einsum ihd,jhd->ihj", {q, k, sc}));
+    bool f32;
+    TLHIP_TRY(float_args("einsum ihd,jhd->ihj", {q, k, sc}, &f32));
     int H, Hkv, D;
     TLHIP_TRY(qkv_dims(q, k, "einsum ihd,jhd->ihj", &H, &Hkv, &D));
     const int I = (int)q->shape[0], J = (int)k->shape[0];
     if (q->shape[2] != D) return fail(TLHIP_ERR_SHAPE_MISMATCH, "einsum: head_dim mismatch");
     if (sc->ndim != 3 || sc->shape[0] != I || sc->shape[1] != H || sc->shape[2] != J)
         return fail(TLHIP_ERR_SHAPE_MISMATCH, "einsum: output %s", shape_str(sc).c_str());
-    TLHIP_TRY(launch_scores(ctx->stream, P(q), P(k), P(sc), I, J, H, Hkv, D));
+    if (f32) TLHIP_TRY(launch_scores_f32(ctx->stream, F(q), F(k), F(sc), I, J, H, Hkv, D));
+    else TLHIP_TRY(launch_scores(ctx->stream, P(q), P(k), P(sc), I, J, H, Hkv, D));
     return after_launch(ctx, "einsum_scores");
 } TLHIP_CATCH_STATUS
 
 tlhip_status tlhip_einsum_context(tlhip_ctx ctx, tlhip_tensor p, tlhip_tensor v, tlhip_tensor out) try {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args("einsum ihj,jhd->ihd", {p, v, out}));
+    bool f32;
+    TLHIP_TRY(float_args("einsum ihj,jhd->ihd", {p, v, out}, &f32));
     if (p->ndim != 3 || v->ndim != 3 || out->ndim != 3)
         return fail(TLHIP_ERR_INVALID_DIMENSION, "einsum ihj,jhd->ihd expects 3-D tensors");
     const int I = (int)p->shape[0], H = (int)p->shape[1], J = (int)p->shape[2];
@@ -538,7 +573,8 @@ tlhip_status tlhip_einsum_context(tlhip_ctx ctx, tlhip_tensor p, tlhip_tensor v,
         return fail(TLHIP_ERR_SHAPE_MISMATCH, "einsum: P %s, V %s", shape_str(p).c_str(), shape_str(v).c_str());
     if (out->shape[0] != I || out->shape[1] != H || out->shape[2] != D)
         return fail(TLHIP_ERR_SHAPE_MISMATCH, "einsum: output %s", shape_str(out).c_str());
-    TLHIP_TRY(launch_context(ctx->stream, P(p), P(v), P(out), I, J, H, Hkv, D));
+    if (f32) TLHIP_TRY(launch_context_f32(ctx->stream, F(p), F(v), F(out), I, J, H, Hkv, D));
+    else TLHIP_TRY(launch_context(ctx->stream, P(p), P(v), P(out), I, J, H, Hkv, D));
     return after_launch(ctx, "einsum_context");
 } TLHIP_CATCH_STATUS
 

@@ -131,6 +131,10 @@ class Tensor:
     def _new(self, shape):
         return self.dev.empty(shape)
 
+    def _like(self, shape):
+        """An output in this tensor's float type (the ops with a TensorF32 arm)."""
+        return self.dev.empty(shape, F32 if self.dtype == F32 else F16)
+
     def dequantize(self) -> "Tensor":
         out = self._new(self.shape)
         call("tlhip_dequantize", self.dev.h, self.h, out.h)
@@ -171,7 +175,7 @@ class Tensor:
             x = self.reshape((self.numel() // int(np.prod(ns)), int(np.prod(ns))))
             w = weight.reshape((int(np.prod(ns)),))
             return x.rms_norm([int(np.prod(ns))], w, eps).reshape(self.shape)
-        out = self._new(self.shape)
+        out = self._like(self.shape)
         call("tlhip_rms_norm", self.dev.h, self.h, weight.h, float(eps), out.h)
         return out
 
@@ -184,13 +188,13 @@ class Tensor:
     def rope(self, position_offset: int = 0, theta: float = 10000.0, layout: int = ROPE_INTERLEAVED,
              rot_dims: int = 0) -> "Tensor":
         """Tensor::rope (rope.rs:71-118); layout/theta/rot_dims extend it."""
-        out = self._new(self.shape)
+        out = self._like(self.shape)
         call("tlhip_rope", self.dev.h, self.h, int(position_offset), float(theta), int(layout),
              int(rot_dims), out.h)
         return out
 
     def softmax(self) -> "Tensor":
-        out = self._new(self.shape)
+        out = self._like(self.shape)
         call("tlhip_softmax_lastdim", self.dev.h, self.h, out.h)
         return out
 
@@ -200,7 +204,9 @@ class Tensor:
         return out
 
     def sigmoid(self):
-        return self._unary("tlhip_sigmoid")
+        out = self._like(self.shape)
+        call("tlhip_sigmoid", self.dev.h, self.h, out.h)
+        return out
 
     def silu(self):
         return self._unary("tlhip_silu")
@@ -285,11 +291,11 @@ def einsum(eq: str, a: Tensor, b: Tensor) -> Tensor:
     """The two attention einsums the TL programs use (einsum.rs:653-886)."""
     eq = eq.replace(" ", "")
     if eq == "ihd,jhd->ihj":
-        out = a.dev.empty((a.shape[0], a.shape[1], b.shape[0]))
+        out = a._like((a.shape[0], a.shape[1], b.shape[0]))
         call("tlhip_einsum_scores", a.dev.h, a.h, b.h, out.h)
         return out
     if eq == "ihj,jhd->ihd":
-        out = a.dev.empty((a.shape[0], a.shape[1], b.shape[2]))
+        out = a._like((a.shape[0], a.shape[1], b.shape[2]))
         call("tlhip_einsum_context", a.dev.h, a.h, b.h, out.h)
         return out
     raise TLHipError(3, f"einsum pattern {eq} not supported")
