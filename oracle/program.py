@@ -1,7 +1,7 @@
-"""debug/chat_demo_with_kvcache.tl composed from the oracle's one-builtin
-functions -- TEST INFRASTRUCTURE ONLY (the checker of
-tensorlogic_amd.program.ChatDemoKVCache, which runs the same sequence on the
-device).
+"""debug/chat_demo_with_kvcache.tl and examples/chat_demo_optimized.tl
+composed from the oracle's one-builtin functions -- TEST INFRASTRUCTURE ONLY
+(the checker of tensorlogic_amd.program.ChatDemoKVCache / ChatDemoOptimized,
+which run the same sequences on the device).
 
 Each statement of the program maps to one oracle call, in the program's
 order, with its f16 storage points:
@@ -28,6 +28,15 @@ prefill row s at position s and every decode row at position 0
 as rope(x, offset) allows -- the decoder runner's default.  `eps` is the
 rms_norm eps: the builtin default 1e-6 (builtin_nn.rs:84-92) for the program
 as written.
+
+ChatDemoOptimized restates examples/chat_demo_optimized.tl's loop
+(:200-239): no cache; each step embeds every token so far and runs
+transformer_layer (:104-138) over all rows -- rms_norm, linear q/k/v,
+tinyllama_gqa_attention (rope with no offset over the full sequence, so row
+s at position s; broadcast_to; einsum; * 0.125; the broadcast causal mask;
+softmax; einsum; linear W_o), the residual, rms_norm, swiglu_ffn, the
+residual -- then slice_last, rms_norm, linear(output) and
+temperature_sample, stopping at EOS.
 """
 from __future__ import annotations
 
@@ -38,17 +47,18 @@ from . import oracle as O
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0 = 0, 1, 2, 8
 
 
-class ChatDemoKVCache:
-    def __init__(self, path: str, rope_mode: str = "program", eps: float = 1e-6, scale: float = 0.125):
-        if rope_mode not in ("program", "absolute"):
-            raise ValueError(rope_mode)
+class _ChatDemoProgram:
+    """The weights and builtins the two chat programs share."""
+
+    def __init__(self, path: str, eps: float = 1e-6, scale: float = 0.125, acc: int = O.ACC_F32):
+        self.acc = acc   # ACC_F32_REV: every linear's sums in descending order (the reordered oracle)
         g = O.GGUF(path)
         self.n_layers = g.kv_u32("llama.block_count")
         self.hidden = g.kv_u32("llama.embedding_length")
         self.n_heads = g.kv_u32("llama.attention.head_count")
         self.n_kv = g.kv_u32("llama.attention.head_count_kv")
         self.head_dim = self.hidden // self.n_heads
-        self.rope_mode, self.eps, self.scale = rope_mode, eps, scale
+        self.eps, self.scale = eps, scale
 
         def vec(name):
             t, dims, raw = g.tensor(name)
@@ -74,16 +84,12 @@ class ChatDemoKVCache:
                                 for k in ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
                                           "ffn_norm", "ffn_gate", "ffn_up", "ffn_down")})
         g.close()
-        self.cache_k = [None] * self.n_layers
-        self.cache_v = [None] * self.n_layers
-        self.pos = 0
 
     # -- builtins ------------------------------------------------------------
-    @staticmethod
-    def linear(x, w):
+    def linear(self, x, w):
         if w[0] == "q":
-            return O.linear_q(x, w[2], w[1], w[3])
-        return O.linear(x, w[1])
+            return O.linear_q(x, w[2], w[1], w[3], acc=self.acc)
+        return O.linear(x, w[1], acc=self.acc)
 
     def rms_norm(self, x, w):
         return O.rms_norm(x, w, self.eps)
@@ -107,6 +113,31 @@ class ChatDemoKVCache:
         p = O.softmax(O.apply_attention_mask(scaled, np.ascontiguousarray(mask)))
         return O.einsum_context(p, v_exp)
 
+    def gqa_attention(self, Q, K, V, W_o):
+        """tinyllama_gqa_attention (chat_demo_optimized.tl:43-101 /
+        chat_demo_with_kvcache.tl:43-89) over S rows."""
+        S, NH, NKV, D = Q.shape[0], self.n_heads, self.n_kv, self.head_dim
+        Q_rope = O.rope(Q.reshape(S, NH, D))
+        K_rope = O.rope(K.reshape(S, NKV, D))
+        mask = np.broadcast_to(O.causal_mask(S).reshape(S, 1, S), (S, NH, S))
+        att = self.attend(Q_rope, self.expand(K_rope), self.expand(V.reshape(S, NKV, D)), mask)
+        return self.linear(att.reshape(S, self.hidden), W_o)
+
+    def head_logits(self, x):
+        last = O.slice_last(x, 0).reshape(1, self.hidden)
+        return self.linear(self.rms_norm(last, self.out_norm), self.out)
+
+
+class ChatDemoKVCache(_ChatDemoProgram):
+    def __init__(self, path: str, rope_mode: str = "program", eps: float = 1e-6, scale: float = 0.125):
+        if rope_mode not in ("program", "absolute"):
+            raise ValueError(rope_mode)
+        super().__init__(path, eps, scale)
+        self.rope_mode = rope_mode
+        self.cache_k = [None] * self.n_layers
+        self.cache_v = [None] * self.n_layers
+        self.pos = 0
+
     # -- the program ---------------------------------------------------------
     def prefill(self, ids):
         """The prompt pass; returns the logits [1, V] of the last row."""
@@ -120,17 +151,11 @@ class ChatDemoKVCache:
             K_rope = O.rope(K.reshape(S, NKV, D))
             self.cache_k[li] = K_rope
             self.cache_v[li] = V.reshape(S, NKV, D)
-            # tinyllama_gqa_attention(Q, K, V, W_o)
-            Q_rope = O.rope(Q.reshape(S, NH, D))
-            K_rope2 = O.rope(K.reshape(S, NKV, D))
-            mask = np.broadcast_to(O.causal_mask(S).reshape(S, 1, S), (S, NH, S))
-            att = self.attend(Q_rope, self.expand(K_rope2), self.expand(V.reshape(S, NKV, D)), mask)
-            attn_out = self.linear(att.reshape(S, H), L["attn_output"])
+            attn_out = self.gqa_attention(Q, K, V, L["attn_output"])
             x1 = O.add(x, attn_out)
             x = O.add(x1, self.swiglu_ffn(self.rms_norm(x1, L["ffn_norm"]), L))
         self.pos = S
-        last = O.slice_last(x, 0).reshape(1, H)
-        return self.linear(self.rms_norm(last, self.out_norm), self.out)
+        return self.head_logits(x)
 
     def decode(self, token):
         """One decode step for `token`; returns the logits [1, V]."""
@@ -165,3 +190,40 @@ class ChatDemoKVCache:
             if step < n_decode:
                 lg = self.decode(t)[0]
         return np.array(toks, np.int32), np.array(margins), lg
+
+
+class ChatDemoOptimized(_ChatDemoProgram):
+    """examples/chat_demo_optimized.tl's generation loop, no cache."""
+
+    def forward(self, ids):
+        """The logits [1, V] of the last row after the n_layers
+        transformer_layer calls over every token so far."""
+        x = O.embedding(self.emb, np.asarray(ids, np.int32))
+        for L in self.layers:
+            x_norm1 = self.rms_norm(x, L["attn_norm"])
+            Q = self.linear(x_norm1, L["attn_q"])
+            K = self.linear(x_norm1, L["attn_k"])
+            V = self.linear(x_norm1, L["attn_v"])
+            x1 = O.add(x, self.gqa_attention(Q, K, V, L["attn_output"]))
+            x = O.add(x1, self.swiglu_ffn(self.rms_norm(x1, L["ffn_norm"]), L))
+        return self.head_logits(x)
+
+    def generate(self, prompt, max_steps=10, temperature=0.8, seed=0, eos=2):
+        """The program's loop with the draw splitmix64(seed, step) (greedy for
+        T <= 1e-4); returns prompt + generated ids, the per-step logits and
+        each step's draw."""
+        gen = [int(t) for t in np.asarray(prompt, np.int32)]
+        logits, draws = [], []
+        for step in range(max_steps):
+            lg = self.forward(gen)[0]
+            logits.append(lg)
+            if temperature <= 1e-4:
+                t, u = O.argmax_last(lg), None
+            else:
+                u = O.sample_uniform(seed, step)
+                t = O.sample_temperature(lg, temperature, u)
+            draws.append(u)
+            if t == eos:
+                break
+            gen.append(t)
+        return np.array(gen, np.int32), logits, draws

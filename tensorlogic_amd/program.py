@@ -1,4 +1,5 @@
-"""debug/chat_demo_with_kvcache.tl run unchanged, one TL builtin at a time.
+"""debug/chat_demo_with_kvcache.tl and examples/chat_demo_optimized.tl run
+unchanged, one TL builtin at a time.
 
 Each statement of the program's prefill (chat_demo_with_kvcache.tl:130-186)
 and decode loop (:208-296), and of its helper functions silu / swiglu_ffn /
@@ -22,6 +23,13 @@ builtin_tensor.rs:531-546) and rms_norm at the builtin default eps 1e-6
 rope(x, offset) allows.  Head counts come from the GGUF file where the
 program hard-codes TinyLlama's (32 / 4 heads of 64); its literal `* 0.125`
 is 1 / sqrt(64), the scale argument.
+
+examples/chat_demo_optimized.tl (ChatDemoOptimized) has no cache: every
+step re-embeds the whole token list and runs its transformer_layer
+(:104-138) over all rows -- rope(Q_heads) / rope(K_heads) with no offset on
+the full sequence rotate row s at position s -- then slice_last, the final
+rms_norm, the output linear and temperature_sample(logits, 0.8), stopping
+at EOS (id 2) or after 10 steps (:200-239).
 """
 from __future__ import annotations
 
@@ -30,12 +38,12 @@ import numpy as np
 from .tensor import GGUF, Device, KVCache, Tensor, causal_mask, einsum, embedding, temperature_sample
 
 
-class ChatDemoKVCache:
-    def __init__(self, dev: Device, path: str, max_ctx: int = 512, rope_mode: str = "program",
-                 eps: float = 1e-6, scale: float = 0.125):
-        if rope_mode not in ("program", "absolute"):
-            raise ValueError(rope_mode)
-        self.dev, self.rope_mode, self.eps, self.scale = dev, rope_mode, eps, scale
+class _ChatDemoProgram:
+    """The weights (get_tensor / model.blk[i].X.weight) and the helper
+    functions the two chat programs share."""
+
+    def __init__(self, dev: Device, path: str, eps: float = 1e-6, scale: float = 0.125):
+        self.dev, self.eps, self.scale = dev, eps, scale
         g = GGUF(path)
         self.n_layers = g.kv_u32("llama.block_count")
         self.hidden = g.kv_u32("llama.embedding_length")
@@ -54,9 +62,6 @@ class ChatDemoKVCache:
                                           "ffn_norm", "ffn_gate", "ffn_up", "ffn_down")})
         g.close()
         self.vocab = self.emb.shape[0]
-        self.max_ctx = max_ctx
-        self.cache = KVCache(dev, self.n_layers, max_ctx, self.n_kv, self.head_dim)   # KVCache::new_f16(22)
-        self.pos = 0
 
     # -- the program's helper functions (chat_demo_with_kvcache.tl:26-89) -----
     def rms_norm(self, x: Tensor, w: Tensor) -> Tensor:
@@ -93,6 +98,33 @@ class ChatDemoKVCache:
         attn_output = einsum("ihj,jhd->ihd", attn_weights, self.expand(V_heads, S))
         return attn_output.reshape((S, self.hidden)).linear(W_o)
 
+    def transformer_layer(self, x: Tensor, L, S: int) -> Tensor:
+        """transformer_layer (chat_demo_optimized.tl:104-138)."""
+        x_norm1 = self.rms_norm(x, L["attn_norm"])
+        Q = x_norm1.linear(L["attn_q"])
+        K = x_norm1.linear(L["attn_k"])
+        V = x_norm1.linear(L["attn_v"])
+        attn_out = self.tinyllama_gqa_attention(Q, K, V, L["attn_output"], S)
+        x1 = x + attn_out
+        return x1 + self.swiglu_ffn(self.rms_norm(x1, L["ffn_norm"]), L)
+
+    def head_logits(self, x: Tensor) -> Tensor:
+        """slice_last(x, 0) -> reshape [1, hidden] -> rms_norm -> linear(output)."""
+        last = x.slice_last(0).reshape((1, self.hidden))
+        return self.rms_norm(last, self.out_norm).linear(self.out)
+
+
+class ChatDemoKVCache(_ChatDemoProgram):
+    def __init__(self, dev: Device, path: str, max_ctx: int = 512, rope_mode: str = "program",
+                 eps: float = 1e-6, scale: float = 0.125):
+        if rope_mode not in ("program", "absolute"):
+            raise ValueError(rope_mode)
+        super().__init__(dev, path, eps, scale)
+        self.rope_mode = rope_mode
+        self.max_ctx = max_ctx
+        self.cache = KVCache(dev, self.n_layers, max_ctx, self.n_kv, self.head_dim)   # KVCache::new_f16(22)
+        self.pos = 0
+
     # -- prefill (:130-186) ------------------------------------------------------
     def prefill(self, ids) -> Tensor:
         """The prompt pass; fills the cache and returns the logits [1, V]."""
@@ -112,8 +144,7 @@ class ChatDemoKVCache:
             x1 = x + attn_out
             x = x1 + self.swiglu_ffn(self.rms_norm(x1, L["ffn_norm"]), L)
         self.pos = S
-        last_pos = x.slice_last(0).reshape((1, self.hidden))
-        return self.rms_norm(last_pos, self.out_norm).linear(self.out)
+        return self.head_logits(x)
 
     # -- decode step (:208-296) -----------------------------------------------
     def decode(self, token: int) -> Tensor:
@@ -157,3 +188,33 @@ class ChatDemoKVCache:
                 logits = self.decode(t)
         self.last_logits = logits
         return np.array(toks, np.int32)
+
+
+class ChatDemoOptimized(_ChatDemoProgram):
+    """examples/chat_demo_optimized.tl's generation loop (:200-239), no cache."""
+
+    def forward(self, ids) -> Tensor:
+        """embedding of every token so far, the 22 (n_layers) transformer
+        layers over all rows, the logits [1, V] of the last row."""
+        ids = np.asarray(ids, np.int32)
+        x = embedding(self.emb, ids)
+        for L in self.layers:
+            x = self.transformer_layer(x, L, ids.size)
+        return self.head_logits(x)
+
+    def generate(self, prompt, max_steps: int = 10, temperature: float = 0.8, seed: int = 0,
+                 eos: int = 2) -> np.ndarray:
+        """The program's loop: up to max_steps tokens chosen by
+        temperature_sample(logits, T) (draw splitmix64(seed, step)), stopping
+        before appending EOS; returns prompt + generated ids."""
+        gen = [int(t) for t in np.asarray(prompt, np.int32)]
+        self.step_logits = []   # each step's logits tensor (the sampler's input)
+        for step in range(max_steps):
+            logits = self.forward(gen)
+            t = temperature_sample(logits, temperature, seed, step)
+            self.step_logits.append(logits)
+            self.last_logits = logits
+            if t == eos:
+                break
+            gen.append(t)
+        return np.array(gen, np.int32)

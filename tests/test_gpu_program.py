@@ -12,15 +12,22 @@ must be within the linear bars.  The program's semantics are its literal
 ones (rope(x) with no offset in decode, rms_norm eps 1e-6); the absolute-
 position variant is checked as well.  The fused runner in its literal mode
 (tlhip_model_set_program_semantics) must produce the same stream.
+
+examples/chat_demo_optimized.tl's loop (no cache: every step re-embeds the
+token list and runs the layers over all rows) runs the same way through
+tensorlogic_amd.program.ChatDemoOptimized against oracle/program.py's
+restatement of it: the same ids at every step, greedy and at the program's
+temperature 0.8 (same draws), and each step's logits within the bars.
 """
 import numpy as np
 import pytest
 
 from oracle.program import ChatDemoKVCache as OracleProgram
+from oracle.program import ChatDemoOptimized as OracleOptimized
 from tensorlogic_amd import Model
 from tensorlogic_amd import synth as S
 from tensorlogic_amd.gguf import GGML_Q4_0
-from tensorlogic_amd.program import ChatDemoKVCache
+from tensorlogic_amd.program import ChatDemoKVCache, ChatDemoOptimized
 
 from test_gpu_ops import assert_logits_close, reorder_rel_l2
 
@@ -115,3 +122,87 @@ def test_program_op_by_op_from_c(dev, oracle, tmp_path):
     assert_logits_close(logits, ref_logits, rrl)
     prog = ChatDemoKVCache(dev, path, max_ctx=64)
     assert np.array_equal(prog.generate(prompt, n), toks)
+
+
+def _loop_orders(oracle, path, ids):
+    """The final logits of the oracle's decoder over `ids` in one prefill, in
+    two fp32 summation orders (every linear and attention sum forward, and
+    descending), in the program's semantics (eps 1e-6; a prefill rotates row
+    s at position s) -- which equals the no-cache loop's step bit for bit
+    (test_oracle_program.py)."""
+    ids = np.ascontiguousarray(ids, np.int32)
+    out = []
+    for acc in (oracle.ACC_F32, oracle.ACC_F32_REV):
+        m = oracle.Model(path, arch=0, max_ctx=64, acc=acc)
+        m.set_program_semantics(True)
+        out.append(np.asarray(m.forward(ids, 0)[1], np.float64).ravel())
+        m.close()
+    return out
+
+
+def _rel(a, b):
+    a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def _loop_order_noise(oracle, path, ids):
+    fwd, rev = _loop_orders(oracle, path, ids)
+    return _rel(rev, fwd)
+
+
+def test_optimized_loop_op_by_op_equals_oracle(dev, oracle, tmp_path):
+    """Greedy: the same ids as the oracle's loop at every step, and the last
+    step's logits within the end-to-end logits bound."""
+    seed = 47
+    path = _model(tmp_path, seed)
+    prompt = S.token_ids(seed, "prompt", 30, SMALL["vocab"])
+    ref_gen, ref_logits, _ = OracleOptimized(path, 1e-6).generate(prompt, 10, 0.0, eos=2)
+    prog = ChatDemoOptimized(dev, path, eps=1e-6)
+    gen = prog.generate(prompt, 10, 0.0, eos=2)
+    assert np.array_equal(gen, ref_gen), f"device {gen[len(prompt):]} vs oracle {ref_gen[len(prompt):]}"
+    # the last forward ran over the prompt and the first len(ref_logits) - 1 generated ids
+    ids = ref_gen[:len(prompt) + len(ref_logits) - 1]
+    rrl = _loop_order_noise(oracle, path, ids)
+    assert_logits_close(prog.last_logits.numpy()[0], ref_logits[-1], rrl, what="optimized loop final logits")
+
+
+def test_optimized_loop_sampled(dev, oracle, tmp_path):
+    """At the program's temperature 0.8 a logit a few f16 ulps away moves the
+    CDF by ~1 %, so the device's free-running stream may leave the oracle's
+    at a draw near a CDF step; the loop is checked teacher-forced on its own
+    stream instead: the logits of all its steps together are within the
+    end-to-end logits bound of the oracle's forward over the same ids (1.5x
+    the distance between two fp32 summation orders of the oracle's decoder
+    over those ids, at least 1e-3; single steps of this 2-layer model
+    scatter around that ratio, so the bound is applied to the whole stream
+    and the per-step ratios are printed), each element within the max-abs
+    bar; and every id is the oracle sampler's for the device's logits and
+    the same draw (or its neighbour where the draw lies on a CDF step within
+    f32 rounding of the running sum)."""
+    from test_gpu_ops import _sample_ok
+    seed = 51
+    path = _model(tmp_path, seed)
+    prompt = S.token_ids(seed, "prompt", 30, SMALL["vocab"])
+    prog = ChatDemoOptimized(dev, path, eps=1e-6)
+    gen = prog.generate(prompt, 10, 0.8, seed=5, eos=2)
+    ref = OracleOptimized(path, 1e-6)
+    n0 = len(prompt)
+    dev_all, ref_all, fwd_all, rev_all, ratios = [], [], [], [], []
+    for step, lg_t in enumerate(prog.step_logits):
+        lg = lg_t.numpy()[0]
+        ids = gen[:n0 + step]
+        want = ref.forward(ids)[0]
+        fwd, rev = _loop_orders(oracle, path, ids)
+        dev_all.append(lg)
+        ref_all.append(want)
+        fwd_all.append(fwd)
+        rev_all.append(rev)
+        ratios.append(_rel(lg, want) / _rel(rev, fwd))
+        pick = int(gen[n0 + step]) if n0 + step < len(gen) else 2
+        r = oracle.sample_uniform(5, step)
+        want_id = oracle.sample_temperature(lg, 0.8, r)
+        assert pick == want_id or _sample_ok(lg, 0.8, r, pick), f"step {step}: {pick} vs {want_id}"
+    print("per-step device / reordered distance ratios:", " ".join(f"{x:.2f}" for x in ratios))
+    assert_logits_close(np.concatenate(dev_all), np.concatenate(ref_all),
+                        _rel(np.concatenate(rev_all), np.concatenate(fwd_all)),
+                        what=f"sampled loop logits, {len(dev_all)} steps")

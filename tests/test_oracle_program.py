@@ -9,7 +9,7 @@ numpy decoder (test_oracle_decoder.py).  CPU only.
 import numpy as np
 import pytest
 
-from oracle.program import ChatDemoKVCache
+from oracle.program import ChatDemoKVCache, ChatDemoOptimized
 from tensorlogic_amd import synth as S
 
 # head_dim 64, so the program's literal `* 0.125` is 1 / sqrt(head_dim)
@@ -69,3 +69,42 @@ def test_program_semantics_are_llama_only(oracle, tmp_path):
     with pytest.raises(ValueError):
         m.set_program_semantics(True)
     m.close()
+
+
+def test_optimized_loop_equals_cached_absolute(oracle, model_path):
+    """examples/chat_demo_optimized.tl recomputes every row each step (no
+    cache), with rope over the full sequence (row s at position s) and the
+    builtin rms_norm eps 1e-6: per output row the oracle's arithmetic does
+    not depend on how many rows a call holds, so each step's logits equal
+    the cached program's at absolute positions with eps 1e-6 bit for bit --
+    and those differ from the program-as-written decode (rows at position
+    0), so the check tells the two apart."""
+    prompt = S.token_ids(31, "prompt", 12, SMALL["vocab"])
+    n = 5
+    gen, logits, _ = ChatDemoOptimized(model_path, 1e-6).generate(prompt, max_steps=n, temperature=0.0, eos=-1)
+    assert len(gen) == len(prompt) + n and len(logits) == n
+    cached = ChatDemoKVCache(model_path, "absolute", 1e-6)
+    lit = ChatDemoKVCache(model_path, "program", 1e-6)
+    lg, ll = cached.prefill(prompt)[0], lit.prefill(prompt)[0]
+    differs = False
+    for step in range(n):
+        assert np.array_equal(logits[step].view(np.uint16), lg.view(np.uint16)), f"step {step}"
+        assert int(gen[len(prompt) + step]) == oracle.argmax_last(lg)
+        differs |= not np.array_equal(lg.view(np.uint16), ll.view(np.uint16))
+        if step < n - 1:
+            tok = int(gen[len(prompt) + step])
+            lg, ll = cached.decode(tok)[0], lit.decode(tok)[0]
+    assert differs
+
+
+def test_optimized_loop_stops_at_eos_and_samples(oracle, model_path):
+    """The loop ends before appending EOS; at T = 0.8 each step's id is the
+    inverse-CDF pick of softmax(logits / T) for that step's draw."""
+    prompt = S.token_ids(31, "prompt", 12, SMALL["vocab"])
+    prog = ChatDemoOptimized(model_path, 1e-6)
+    gen, logits, draws = prog.generate(prompt, max_steps=4, temperature=0.8, seed=3, eos=-1)
+    for step, (lg, u) in enumerate(zip(logits, draws)):
+        assert int(gen[len(prompt) + step]) == oracle.sample_temperature(lg, 0.8, u)
+    first = int(gen[len(prompt)])
+    gen2, logits2, _ = prog.generate(prompt, max_steps=4, temperature=0.8, seed=3, eos=first)
+    assert len(gen2) == len(prompt) and len(logits2) == 1
