@@ -78,6 +78,9 @@ struct GemvParams {
     const uint16_t* embd;
     const int32_t* d_token;
     uint16_t* x_out;
+    // normalised GEMV (QKV epilogue): the f16 normalised row, written by
+    // workgroup 0 for a later GEMV of the same normalisation
+    uint16_t* xn_out;
     // EPI_ARGMAX: per-workgroup (value, index) keys
     unsigned long long* amax_slots;
 };
@@ -108,7 +111,7 @@ __device__ __forceinline__ void kernarg_fence(const GemvParams& p) {
     asm volatile("" ::"s"(p.x), "s"(p.wq), "s"(p.wd), "s"(p.bias), "s"(p.resid), "s"(p.y), "s"(p.M), "s"(p.N),
                  "s"(p.K), "s"(p.ldy), "s"(p.epi), "s"(p.norm_w), "s"(p.norm_b), "s"(p.eps), "s"(p.nq), "s"(p.nk),
                  "s"(p.head_dim), "s"(p.rot), "s"(p.layout), "s"(p.pos0), "s"(p.rope_tab), "s"(p.d_pos),
-                 "s"(p.q_out), "s"(p.kc), "s"(p.vc), "s"(p.embd), "s"(p.d_token), "s"(p.x_out), "s"(p.amax_slots));
+                 "s"(p.q_out), "s"(p.kc), "s"(p.vc), "s"(p.embd), "s"(p.d_token), "s"(p.x_out), "s"(p.xn_out), "s"(p.amax_slots));
     __builtin_amdgcn_sched_barrier(0);   // nothing that uses them moves above
 }
 
@@ -229,6 +232,7 @@ struct NormStage {
     static constexpr int NT = WPB * 64;
     static constexpr int IPT = (NB * 256 + NT - 1) / NT;
     uint32_t xw[IPT][4], ww[IPT][4], bw[IPT][4];   // raw f16 pairs until finish()
+    uint32_t xn[IPT][4];   // the normalised quads in natural element order (for xn_out)
 
     __device__ __forceinline__ static void load_buf(const uint16_t* __restrict__ src, int K, int it, uint32_t w[4]) {
         const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, K * 2, BUF_RSRC_WORD3);
@@ -259,6 +263,28 @@ struct NormStage {
             load_buf(xsrc, p.K, it, xw[k]);
             load_buf(p.norm_w, p.K, it, ww[k]);
             if (PRO == PRO_LN) load_buf(p.norm_b, p.K, it, bw[k]);
+        }
+    }
+
+    // Workgroup 0 writes the normalised row to xn_out, after its own work:
+    // stores issued before the dot products would sit in the same in-order
+    // counter as the weight loads the products wait for.  Natural element
+    // order: one 16-byte store per quad (Q4_0's quad halves: two 8-byte ones).
+    __device__ __forceinline__ void store_xn(const GemvParams& p) const {
+        if (!p.xn_out || blockIdx.x != 0) return;
+        const int items = (p.K >> 5) * 4;
+#pragma unroll
+        for (int k = 0; k < IPT; k++) {
+            const int it = threadIdx.x + k * NT;
+            if (it >= items) continue;
+            const int b = it >> 2, v = it & 3;
+            uint16_t* dst = p.xn_out + (size_t)b * 32;
+            if (xo_nibble<WT>()) {
+                *(uint2*)(dst + 4 * v) = uint2{xn[k][0], xn[k][1]};
+                *(uint2*)(dst + 16 + 4 * v) = uint2{xn[k][2], xn[k][3]};
+            } else {
+                *(u4*)(dst + 8 * v) = u4{xn[k][0], xn[k][1], xn[k][2], xn[k][3]};
+            }
         }
     }
 
@@ -316,6 +342,14 @@ struct NormStage {
             for (int e = 0; e < 8; e++)
                 f[k][e] = PRO == PRO_RMS ? (f[k][e] * inv) * w[e] : (((f[k][e] - mean) * inv) * w[e]) + bb[e];
             xs[v][b] = pack_quad<WT>(f[k]);
+            if (p.xn_out)   // (the same f16 values the dot products read)
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    h2 h;
+                    h[0] = (h16)f[k][2 * t];
+                    h[1] = (h16)f[k][2 * t + 1];
+                    xn[k][t] = as_u32(h);
+                }
         }
         lds_barrier();
     }
@@ -955,6 +989,7 @@ __device__ __forceinline__ GemvParams norm_view(const GemvParams& k) {
         p.embd = k.embd;
         p.d_token = k.d_token;
         p.x_out = k.x_out;
+        p.xn_out = k.xn_out;
     }
     if (EPI == EPI_ARGMAX) p.amax_slots = k.amax_slots;
     return p;
@@ -1047,6 +1082,7 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
 #pragma unroll
             for (int ri = 0; ri + 1 < RI; ri += 2)
                 if (row0 + ri + 1 < p.N) qkv_rope_store(p, row0 + ri, acc[ri][0], acc[ri + 1][0], qp[ri / 2]);
+        st.store_xn(p);
         return;
     }
     if (p.epi == EPI_SWIGLU_PAIR) {

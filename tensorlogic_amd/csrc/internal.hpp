@@ -187,6 +187,9 @@ struct GemvArgs {
     const uint16_t* embd = nullptr;
     const int32_t* d_token = nullptr;
     uint16_t* x_out = nullptr;
+    // normalised GEMV with the QKV epilogue: workgroup 0 also writes the f16
+    // normalised row here (Phi-2's MLP reads the same layer_norm output)
+    uint16_t* xn_out = nullptr;
     // EPI_ARGMAX: one (value, index) key per workgroup, gemv_norm_slots(N) of them
     unsigned long long* amax_slots = nullptr;
     // GEMM split-K workspace (fp32 partials); none = no split

@@ -355,6 +355,7 @@ static GemvParams make_params(const GemvArgs& a, int epi) {
     p.embd = a.embd;
     p.d_token = a.d_token;
     p.x_out = a.x_out;
+    p.xn_out = a.xn_out;
     p.amax_slots = a.amax_slots;
     return p;
 }

@@ -24,6 +24,10 @@ static bool launch_m1_epi_nb(hipStream_t s, const Gemv1Params& p) {
             if (!b || !r) return false;
             hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS_RESID, FN>), grid, block, 0, s, p);
             return true;
+        case EPI_BIAS_GELU:
+            if (!b) return false;
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS_GELU, FN>), grid, block, 0, s, p);
+            return true;
         default: return false;
     }
 }

@@ -392,6 +392,9 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
             a.q_out = P(m->qrot);
             a.kc = kc;
             a.vc = vc;
+            // phi2: the MLP's layer_norm is this one (same row, same weights):
+            // the normalised row is kept for the fc1 GEMV
+            if (m->arch == 1) a.xn_out = P(m->xn);
             TLHIP_TRY(launch_gemv(s, L.qkv.w->dtype, a, EPI_QKV_ROPE));
         } else {
             if (m->arch == 0) TLHIP_TRY(launch_rms_norm(s, P(m->x), P(L.norm_w), P(m->xn), S, H, m->eps));
@@ -463,14 +466,11 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
             }
             TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_RESID, P(m->x), 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
         } else {
-            // phi2: the MLP reads the same layer_norm output as attention
-            if (row1) {
-                GemvArgs a = fused_norm_args(m, L.up, P(m->x), L.norm_w, L.norm_b);
-                a.y = P(m->hmid);
-                TLHIP_TRY(launch_gemv(s, L.up.w->dtype, a, EPI_BIAS_GELU));
-            }
+            // phi2: the MLP reads the same layer_norm output as attention --
+            // with one row, the one the QKV launch wrote (measured on MI355X:
+            // fc1 [10240 x 2560] Q8_0 as its own normalised GEMV 8.67 us)
+            TLHIP_TRY(linear_into(s, L.up, P(m->xn), S, P(m->hmid), EPI_BIAS_GELU, nullptr, 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
             TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
-            if (!row1) TLHIP_TRY(linear_into(s, L.up, P(m->xn), S, P(m->hmid), EPI_BIAS_GELU, nullptr, 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
             TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
         }
     }
