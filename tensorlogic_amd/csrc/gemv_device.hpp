@@ -848,20 +848,21 @@ struct Gemv1Params {
 // [2048 x 5632] + residual 4.10 -> 3.99 us, [5632 x 2048] 3.81 -> 3.71 us,
 // bit-identical outputs); EPI < 0: chosen at run time from p.epi and the
 // pointers present.
-template <int WT, int NB, int RI, int EPI = -1, int FN = 0>
-__global__ __launch_bounds__(256) void gemv_m1_kernel(Gemv1Params p) {
+template <int WT, int NB, int RI, int EPI = -1, int FN = 0, int WPB = 4>
+__global__ __launch_bounds__(WPB * 64) void gemv_m1_kernel(Gemv1Params p) {
+    constexpr int NT = WPB * 64, NSX = (NB * 256 + NT - 1) / NT;   // activation quads per thread
     __shared__ u4 xs[4][NB * 64];
     const bool has_bias = EPI < 0 ? p.bias != nullptr : (EPI == EPI_BIAS || EPI == EPI_BIAS_RESID || EPI == EPI_BIAS_GELU);
     const bool has_resid = EPI < 0 ? p.resid != nullptr : (EPI == EPI_RESID || EPI == EPI_BIAS_RESID);
     const int epi = EPI < 0 ? p.epi : EPI;
     constexpr int NL = BlkLoads<WT>::n;
     const int lane = threadIdx.x & 63;
-    const int row0 = ((int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6)) * RI;
-    uint32_t xw[NB][4];
+    const int row0 = ((int)blockIdx.x * WPB + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6)) * RI;
+    uint32_t xw[NSX][4];
     {
         const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, (short)0, p.K * 2, BUF_RSRC_WORD3);
 #pragma unroll
-        for (int k = 0; k < NB; k++) load_quad_buf<WT>(rx, (int)threadIdx.x + 256 * k, xw[k]);
+        for (int k = 0; k < NSX; k++) load_quad_buf<WT>(rx, (int)threadIdx.x + NT * k, xw[k]);
     }
     __builtin_amdgcn_sched_barrier(0);   // the activation loads go out first
     constexpr int FIT = FN > 0 ? Flat<(FN > 0 ? FN : 64), RI>::IT : 1;
@@ -899,11 +900,12 @@ __global__ __launch_bounds__(256) void gemv_m1_kernel(Gemv1Params p) {
             for (int ri = 0; ri < RI; ri++) er[ri] = __builtin_amdgcn_raw_buffer_load_b16(rr, 0, (row0 + ri) * 2, 0);
     }
 #pragma unroll
-    for (int k = 0; k < NB; k++) {
-        const int it = threadIdx.x + 256 * k;
+    for (int k = 0; k < NSX; k++) {
+        const int it = threadIdx.x + NT * k;
         const uint32_t* w = xw[k];
-        xs[it & 3][it >> 2] = WT == TLHIP_F16 ? u4{w[0], w[1], w[2], w[3]}
-                                              : u4{pack_lo(w[0], w[1]), pack_hi(w[0], w[1]), pack_lo(w[2], w[3]), pack_hi(w[2], w[3])};
+        if (NT * NSX == NB * 256 || it < NB * 256)   // (the staging row holds NB * 256 quads)
+            xs[it & 3][it >> 2] = WT == TLHIP_F16 ? u4{w[0], w[1], w[2], w[3]}
+                                                  : u4{pack_lo(w[0], w[1]), pack_hi(w[0], w[1]), pack_lo(w[2], w[3]), pack_hi(w[2], w[3])};
     }
     lds_barrier();
     if (row0 >= p.N) return;   // (uniform: only the last workgroup has idle waves)

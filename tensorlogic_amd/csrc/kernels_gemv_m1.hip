@@ -6,27 +6,27 @@
 
 namespace tlhip {
 
-template <int WT, int NB, int RI, int FN = 0>
+template <int WT, int NB, int RI, int FN = 0, int WPB = 4>
 static bool launch_m1_epi_nb(hipStream_t s, const Gemv1Params& p) {
-    const dim3 grid((unsigned)(((p.N + RI - 1) / RI + 3) / 4)), block(256);
+    const dim3 grid((unsigned)(((p.N + RI - 1) / RI + WPB - 1) / WPB)), block(WPB * 64);
     const bool b = p.bias != nullptr, r = p.resid != nullptr;
     switch (p.epi) {
-        case EPI_STORE: hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_STORE, FN>), grid, block, 0, s, p); return true;
+        case EPI_STORE: hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_STORE, FN, WPB>), grid, block, 0, s, p); return true;
         case EPI_BIAS:
             if (!b) return false;
-            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS, FN>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS, FN, WPB>), grid, block, 0, s, p);
             return true;
         case EPI_RESID:
             if (!r) return false;
-            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_RESID, FN>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_RESID, FN, WPB>), grid, block, 0, s, p);
             return true;
         case EPI_BIAS_RESID:
             if (!b || !r) return false;
-            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS_RESID, FN>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS_RESID, FN, WPB>), grid, block, 0, s, p);
             return true;
         case EPI_BIAS_GELU:
             if (!b) return false;
-            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS_GELU, FN>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((gemv_m1_kernel<WT, NB, RI, EPI_BIAS_GELU, FN, WPB>), grid, block, 0, s, p);
             return true;
         default: return false;
     }
