@@ -518,6 +518,9 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
 // Measured on MI355X, one row over 2048 keys at head dim 64 (32 / 4 heads),
 // per call: 128-key chunks 8.5 us, 256 7.55 us, 512 8.7 us (all with the
 // combine kernel; the in-kernel exchange at 8 chunks of 256: 8.2 us).
+// Not for shorter rows: Phi-2 decode (head dim 80, 513..776 cache rows) ran
+// 819 (exchange) / 809 (combine kernel) tok/s in 256-key chunks against 855.5
+// in 128-key chunks with the exchange.
 constexpr int AS_CH = 128;
 // NT threads per chunk workgroup: NT / 8 key groups of 8 lanes, each
 // holding CH / (NT / 8) of the chunk's K / V rows.  512 threads up to 2048
