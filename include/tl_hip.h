@@ -157,7 +157,9 @@ tlhip_status tlhip_matmul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_t
  * over the last dim.  x, w, y all f16, or all f32 (the TensorF32 arm,
  * rms_norm_simple_f32 / rms_norm_f32, unified.metal:1961-2036).            */
 tlhip_status tlhip_rms_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, float eps, tlhip_tensor y);
-/* layer_norm (normalization.rs:271-535); w and b may be NULL.             */
+/* layer_norm (normalization.rs:271-535); w and b may be NULL.  All f16, or
+ * all f32 (layer_norm_f32 / layer_norm_simple_f32, unified.metal:1833-1958:
+ * per-row sums in element order).                                          */
 tlhip_status tlhip_layer_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor b, float eps, tlhip_tensor y);
 /* rope(x[, offset]) (builtin_tensor.rs:514-556, rope.rs:71-300): x [..,S,H,D].
  * rot_dims 0 = D.  The reference's rope() is layout INTERLEAVED, theta 10000.
@@ -170,22 +172,28 @@ tlhip_status tlhip_softmax_lastdim(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y
 /* sigmoid (activations.rs:239-266; f16, or f32 in and out: sigmoid_f32,
  * unified.metal:1129-1135); silu = x * sigmoid(x) as the TL function silu
  * (chat_demo_optimized.tl:35-37); silu_mul = silu(g) * u (swiglu_ffn's
- * intermediate); gelu (tanh form, unified.metal:837-848).                 */
+ * intermediate); gelu (tanh form, unified.metal:837-848; f32: gelu_f32,
+ * :1051-1062).  Each takes all-f16 or all-f32 operands.                   */
 tlhip_status tlhip_sigmoid(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y);
 tlhip_status tlhip_silu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y);
 tlhip_status tlhip_silu_mul(tlhip_ctx ctx, tlhip_tensor gate, tlhip_tensor up, tlhip_tensor y);
 tlhip_status tlhip_gelu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y);
-/* add / mul (elementwise.rs, add_f16/mul_f16 unified.metal:701-729); b
- * may be a 1-D tensor matching a's last dim (row broadcast, as bias).     */
+/* add / mul (elementwise.rs, add_f16/mul_f16 unified.metal:701-729; f32:
+ * add_f32/mul_f32, :934-962); b may be a 1-D tensor matching a's last dim
+ * (row broadcast, as bias).  All f16 or all f32.                          */
 tlhip_status tlhip_add(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y);
 tlhip_status tlhip_mul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y);
-/* tensor * scalar (mul_scalar): the scalar is rounded to f16 first.       */
+/* tensor * scalar (mul_scalar(scalar: T), elementwise.rs:724-780): for an
+ * f16 tensor the scalar is rounded to f16 first; for an f32 tensor it is
+ * used as given (mul_scalar_f32, unified.metal:984-992).                  */
 tlhip_status tlhip_mul_scalar(tlhip_ctx ctx, tlhip_tensor a, float s, tlhip_tensor y);
 /* embedding(table, ids) (builtin_nn.rs:627-812): table [V,H] F16/Q4_0/Q8_0/Q6_K,
- * ids host int32[n] (bounds-checked on the host), out [n,H] f16.          */
+ * ids host int32[n] (bounds-checked on the host), out [n,H] f16; an F32
+ * table gives f32 rows (embedding_lookup_f32, unified.metal:678-694).     */
 tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* ids, int n, tlhip_tensor out);
 /* apply_attention_mask(scores, mask) (masking.rs:36-51,147-165): where
- * mask == 0 the score becomes -10000.  mask broadcasts over leading dims. */
+ * mask == 0 the score becomes -10000.  mask broadcasts over leading dims.
+ * All f16, or all f32 (apply_attention_mask_f32, unified.metal:4491-4503). */
 tlhip_status tlhip_apply_attention_mask(tlhip_ctx ctx, tlhip_tensor scores, tlhip_tensor mask, tlhip_tensor y);
 /* causal_mask(n) (builtin_nn.rs:423-460, masking.rs:192-207): out [n, n]
  * f16 = 1 where j <= i, else 0.                                          */

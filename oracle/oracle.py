@@ -91,6 +91,10 @@ def _declare(L):
         "tlo_sigmoid_f32": (None, [vp, sz, vp]),
         "tlo_einsum_scores_f32": (None, [vp, vp, i, i, i, i, i, vp]),
         "tlo_einsum_context_f32": (None, [vp, vp, i, i, i, i, i, vp]),
+        "tlo_layer_norm_f32": (None, [vp, vp, vp, i, i, f, vp]),
+        "tlo_gelu_f32": (None, [vp, sz, vp]),
+        "tlo_silu_f32": (None, [vp, sz, vp]),
+        "tlo_swiglu_f32": (None, [vp, vp, sz, vp]),
         "tlo_tensor_argmax": (C.c_int64, [vp, vp, i, i, vp]),
         "tlo_broadcast_to": (i, [vp, vp, i, vp, i, i, vp]),
         "tlo_rope_cos_sin": (i, [vp, i, i, i, vp, vp, i, vp]),
@@ -211,6 +215,65 @@ def sigmoid_f32(x) -> np.ndarray:
     y = np.empty_like(x)
     lib().tlo_sigmoid_f32(_p(x), x.size, _p(y))
     return y
+
+
+def layer_norm_f32(x, w=None, b=None, eps=1e-5) -> np.ndarray:
+    """layer_norm on f32 operands (tlo_layer_norm_f32: per-row sums in
+    element order)."""
+    x = _f(x)
+    n = x.shape[-1]
+    wf = _f(w) if w is not None else None
+    bf = _f(b) if b is not None else None
+    y = np.empty_like(x)
+    lib().tlo_layer_norm_f32(_p(x), _p(wf) if wf is not None else None, _p(bf) if bf is not None else None,
+                             x.size // n, n, eps, _p(y))
+    return y
+
+
+def _unary_f32(fn, x) -> np.ndarray:
+    x = _f(x)
+    y = np.empty_like(x)
+    getattr(lib(), fn)(_p(x), x.size, _p(y))
+    return y
+
+
+def gelu_f32(x) -> np.ndarray:
+    return _unary_f32("tlo_gelu_f32", x)
+
+
+def silu_f32(x) -> np.ndarray:
+    return _unary_f32("tlo_silu_f32", x)
+
+
+def swiglu_f32(g, u) -> np.ndarray:
+    g, u = _f(g), _f(u)
+    y = np.empty_like(g)
+    lib().tlo_swiglu_f32(_p(g), _p(u), g.size, _p(y))
+    return y
+
+
+def add_f32(a, b) -> np.ndarray:
+    """add_f32 / mul_f32 / mul_scalar_f32 (unified.metal:934-992): one IEEE
+    f32 operation per element (numpy's float32 arithmetic rounds the same);
+    b may be a row repeated over a's last dim."""
+    return (_f(a) + _f(b)).astype(np.float32)
+
+
+def mul_f32(a, b) -> np.ndarray:
+    return (_f(a) * _f(b)).astype(np.float32)
+
+
+def mul_scalar_f32(a, s) -> np.ndarray:
+    return (_f(a) * np.float32(s)).astype(np.float32)
+
+
+def apply_attention_mask_f32(scores, mask) -> np.ndarray:
+    """apply_attention_mask_f32 (unified.metal:4491-4503): mask == 0 gives
+    -10000; a [I, J] mask applies to every head of [I, H, J] scores."""
+    sc, m = _f(scores), _f(mask)
+    if m.ndim == 2 and sc.ndim == 3:
+        m = m[:, None, :]
+    return np.where(m == 0.0, np.float32(-10000.0), sc).astype(np.float32)
 
 
 def einsum_scores_f32(q, k) -> np.ndarray:

@@ -490,6 +490,67 @@ void tlo_sigmoid_f32(const float* x, size_t n, float* y) {
     for (size_t i = 0; i < n; i++) y[i] = 1.0f / (1.0f + expf(-x[i]));
 }
 
+/* layer_norm_f32 / layer_norm_simple_f32 (unified.metal:1833-1958;
+   dispatch normalization.rs:396-441), per row: sum in element order, mean =
+   sum / n; squared deviations summed in element order, each as one fused
+   multiply-add (the contraction assumed for `sq_sum += diff * diff`, as in
+   tlo_rms_norm_f32); inv_std = 1 / sqrt(sq_sum / n + eps); y = (x - mean) *
+   inv_std, then * w and + b, fused into one multiply-add when both are
+   given.  Element order is what the reference computes for one row (its
+   long-row kernel then runs as one thread) and for rows of <= 256 (the
+   simple kernel). */
+void tlo_layer_norm_f32(const float* x, const float* w, const float* b, int rows, int n, float eps, float* y) {
+    for (int r = 0; r < rows; r++) {
+        const float* xr = x + (size_t)r * n;
+        float* yr = y + (size_t)r * n;
+        float s = 0.0f;
+        for (int i = 0; i < n; i++) s += xr[i];
+        const float mean = s / (float)n;
+        float q = 0.0f;
+        for (int i = 0; i < n; i++) {
+            const float d = xr[i] - mean;
+            q = fmaf(d, d, q);
+        }
+        const float inv_std = 1.0f / sqrtf(q / (float)n + eps);
+        for (int i = 0; i < n; i++) {
+            const float t = (xr[i] - mean) * inv_std;
+            if (w && b) yr[i] = fmaf(t, w[i], b[i]);
+            else if (w) yr[i] = t * w[i];
+            else if (b) yr[i] = t + b[i];
+            else yr[i] = t;
+        }
+    }
+}
+
+/* gelu_f32 (unified.metal:1051-1062): x3 = (x * x) * x, inner = sqrt(2/pi)
+   * (x + 0.044715 * x3) with the multiply-add fused (assumed contraction),
+   y = (0.5 * x) * (1 + tanh(inner)). */
+void tlo_gelu_f32(const float* x, size_t n, float* y) {
+    for (size_t i = 0; i < n; i++) {
+        const float v = x[i];
+        const float x3 = (v * v) * v;
+        const float inner = 0.7978845608f * fmaf(0.044715f, x3, v);
+        y[i] = (0.5f * v) * (1.0f + tanhf(inner));
+    }
+}
+
+/* TL silu(x) = x * sigmoid(x) and swiglu(g, u) = silu(g) * u on f32
+   tensors: sigmoid_f32, then mul_f32 (each step rounded to f32). */
+void tlo_silu_f32(const float* x, size_t n, float* y) {
+    for (size_t i = 0; i < n; i++) {
+        const float s = 1.0f / (1.0f + expf(-x[i]));
+        y[i] = x[i] * s;
+    }
+}
+
+void tlo_swiglu_f32(const float* g, const float* u, size_t n, float* y) {
+    for (size_t i = 0; i < n; i++) {
+        const float s = 1.0f / (1.0f + expf(-g[i]));
+        const float a = g[i] * s;
+        y[i] = a * u[i];
+    }
+}
+
 /* einsum_ihd_jhd_ihj_f32 / einsum_ihj_jhd_ihd_f32 (unified.metal:2702-2768):
    the sum over d (scores) or j (context) in index order, one fused
    multiply-add per term; query head h reads KV head h / (H / Hkv). */

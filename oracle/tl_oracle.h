@@ -127,6 +127,13 @@ void tlo_rope_f32(const float* x, int S, int H, int D, int offset, float theta, 
 void tlo_sigmoid_f32(const float* x, size_t n, float* y);
 void tlo_einsum_scores_f32(const float* q, const float* k, int I, int J, int H, int Hkv, int D, float* out);
 void tlo_einsum_context_f32(const float* p, const float* v, int I, int J, int H, int Hkv, int D, float* out);
+/* layer_norm_f32 (unified.metal:1833-1958): per-row sums in element order,
+   the squares fused; gelu_f32 (:1051-1062); TL silu / swiglu on f32
+   (sigmoid_f32 then mul_f32). */
+void tlo_layer_norm_f32(const float* x, const float* w, const float* b, int rows, int n, float eps, float* y);
+void tlo_gelu_f32(const float* x, size_t n, float* y);
+void tlo_silu_f32(const float* x, size_t n, float* y);
+void tlo_swiglu_f32(const float* g, const float* u, size_t n, float* y);
 /* TL silu(x) = x * sigmoid(x) (examples/chat_demo_optimized.tl:35-37):
  * s = sigmoid(x) stored f16, then f16(x * s).                              */
 void tlo_silu(const uint16_t* x, size_t n, uint16_t* y);

@@ -273,6 +273,14 @@ enum EwOp { EW_SIGMOID = 0, EW_SILU = 1, EW_GELU = 2, EW_ADD = 3, EW_MUL = 4, EW
             EW_SILU_MUL = 6 };
 tlhip_status launch_elementwise(hipStream_t s, int op, const uint16_t* a, const uint16_t* b,
                                 uint16_t* y, int64_t n, int64_t b_period, float scalar);
+tlhip_status launch_elementwise_f32(hipStream_t s, int op, const float* a, const float* b, float* y, int64_t n,
+                                    int64_t b_period, float scalar);
+tlhip_status launch_layer_norm_f32(hipStream_t s, const float* x, const float* w, const float* b, float* y, int rows,
+                                   int n, float eps);
+tlhip_status launch_mask_f32(hipStream_t s, const float* sc, const float* mask, float* y, int64_t n,
+                             int64_t mask_period);
+tlhip_status launch_embedding_f32(hipStream_t s, const float* table, const int32_t* ids, float* out, int n,
+                                  int hidden);
 tlhip_status launch_causal_mask(hipStream_t s, uint16_t* out, int64_t n);
 // broadcast_to: target dims and, per target dim, the input stride (0 where
 // the input has size 1 or no dim)

@@ -1192,4 +1192,154 @@ tlhip_status launch_sigmoid_f32(hipStream_t s, const float* x, float* y, int64_t
     return TLHIP_OK;
 }
 
+// The TensorF32 elementwise ops: add_f32 / mul_f32 / mul_scalar_f32
+// (unified.metal:934-992, one IEEE f32 operation each; b may repeat every
+// bp elements as in the f16 kernel), silu = x * sigmoid_f32(x) and
+// silu(g) * u with every step rounded to f32 (the TL functions, as the
+// f16 kernel), and gelu_f32 (unified.metal:1051-1062): x3 = x * x * x,
+// inner = sqrt(2/pi) * (x + 0.044715 * x3) with the multiply-add fused (the
+// contraction assumed for the reference's f32 kernels), 0.5 * x * (1 +
+// tanh(inner)).
+__device__ __forceinline__ float sigmoid_f(float v) { return 1.0f / (1.0f + expf(-v)); }
+__device__ __forceinline__ float gelu_f(float x) {
+    const float x3 = __fmul_rn(__fmul_rn(x, x), x);
+    const float inner = __fmul_rn(0.7978845608f, fmaf(0.044715f, x3, x));
+    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+}
+
+__global__ void elementwise_f32_kernel(int op, const float* __restrict__ a, const float* __restrict__ b,
+                                       float* __restrict__ y, int64_t n, int64_t bp, float sc) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float av = a[i];
+    float r;
+    switch (op) {
+        case EW_SIGMOID: r = sigmoid_f(av); break;
+        case EW_SILU: r = __fmul_rn(av, sigmoid_f(av)); break;
+        case EW_GELU: r = gelu_f(av); break;
+        case EW_ADD: r = __fadd_rn(av, b[bp ? i % bp : i]); break;
+        case EW_MUL: r = __fmul_rn(av, b[bp ? i % bp : i]); break;
+        case EW_MUL_SCALAR: r = __fmul_rn(av, sc); break;
+        case EW_SILU_MUL: r = __fmul_rn(__fmul_rn(av, sigmoid_f(av)), b[i]); break;
+        default: r = av;
+    }
+    y[i] = r;
+}
+
+tlhip_status launch_elementwise_f32(hipStream_t s, int op, const float* a, const float* b, float* y, int64_t n,
+                                    int64_t b_period, float scalar) {
+    if (n <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(elementwise_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, op, a, b, y, n,
+                       b_period, scalar);
+    return TLHIP_OK;
+}
+
+// layer_norm_f32 / layer_norm_simple_f32 (unified.metal:1833-1958,
+// dispatched by normalization.rs:396-441) per row: sum in element order,
+// mean = sum / n; the squared deviations summed in element order, each as
+// one fused multiply-add (the contraction assumed for `sq_sum += diff *
+// diff`); inv_std = 1 / sqrt(sq_sum / n + eps); y = (x - mean) * inv_std,
+// then * w and + b (fused into one multiply-add when both are given).
+// Element order is what the reference's dispatch computes for a single row
+// (one thread) and for rows of at most 256 (the simple kernel); its
+// multi-row dispatch of the long-row kernel shares one threadgroup between
+// rows, which this restates per row.  Thread 0 takes both sums; every
+// thread normalises.
+__global__ __launch_bounds__(256) void layer_norm_f32_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                             const float* __restrict__ b, float* __restrict__ y,
+                                                             int n, float eps) {
+    __shared__ float stat[2];
+    const float* xr = x + (size_t)blockIdx.x * n;
+    float* yr = y + (size_t)blockIdx.x * n;
+    if (threadIdx.x == 0) {
+        float s = 0.0f;
+        for (int i = 0; i < n; i++) s = __fadd_rn(s, xr[i]);
+        const float mean = s / (float)n;
+        float q = 0.0f;
+        for (int i = 0; i < n; i++) {
+            const float d = __fsub_rn(xr[i], mean);
+            q = fmaf(d, d, q);
+        }
+        stat[0] = mean;
+        stat[1] = 1.0f / sqrtf(__fadd_rn(q / (float)n, eps));
+    }
+    __syncthreads();
+    const float mean = stat[0], inv_std = stat[1];
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float t = __fmul_rn(__fsub_rn(xr[i], mean), inv_std);
+        float v;
+        if (w && b) v = fmaf(t, w[i], b[i]);
+        else if (w) v = __fmul_rn(t, w[i]);
+        else if (b) v = __fadd_rn(t, b[i]);
+        else v = t;
+        yr[i] = v;
+    }
+}
+
+tlhip_status launch_layer_norm_f32(hipStream_t s, const float* x, const float* w, const float* b, float* y, int rows,
+                                   int n, float eps) {
+    if (rows <= 0 || n <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(layer_norm_f32_kernel, dim3((unsigned)rows), dim3(256), 0, s, x, w, b, y, n, eps);
+    return TLHIP_OK;
+}
+
+// apply_attention_mask_f32 (unified.metal:4491-4503): y = mask == 0 ?
+// -10000 : score (-0 counts as 0, NaN keeps the score), with mask_kernel's
+// two mask layouts.
+__global__ void mask_f32_kernel(const float* __restrict__ sc, const float* __restrict__ mask, float* __restrict__ y,
+                                int64_t n, int64_t period, int64_t inner, int64_t heads) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t mi;
+    if (heads > 1) {
+        const int64_t j = i % inner, row = (i / inner) / heads;
+        mi = row * inner + j;
+    } else {
+        mi = i % period;
+    }
+    y[i] = mask[mi] == 0.0f ? -10000.0f : sc[i];
+}
+
+tlhip_status launch_mask_f32(hipStream_t s, const float* sc, const float* mask, float* y, int64_t n,
+                             int64_t mask_period) {
+    if (n <= 0) return TLHIP_OK;
+    int64_t period = mask_period, inner = 1, heads = 1;
+    if (mask_period < 0) {
+        const int64_t enc = -mask_period;
+        inner = enc >> 16;
+        heads = enc & 0xffff;
+        period = 0;
+    }
+    hipLaunchKernelGGL(mask_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, sc, mask, y, n, period,
+                       inner, heads);
+    return TLHIP_OK;
+}
+
+// embedding_lookup_f32 (unified.metal:678-694): out[s, :] = table[id_s, :]
+// for an f32 table, four floats per thread where the rows allow.
+__global__ void embedding_f32_kernel(const float* __restrict__ table, const int32_t* __restrict__ ids,
+                                     float* __restrict__ out, int n, int hidden, int vec) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (vec) {
+        const int q = hidden / 4;
+        if (i >= (int64_t)n * q) return;
+        const int s = (int)(i / q), c = (int)(i % q);
+        ((float4*)out)[i] = ((const float4*)table)[(size_t)ids[s] * q + c];
+    } else {
+        if (i >= (int64_t)n * hidden) return;
+        const int s = (int)(i / hidden), c = (int)(i % hidden);
+        out[i] = table[(size_t)ids[s] * hidden + c];
+    }
+}
+
+tlhip_status launch_embedding_f32(hipStream_t s, const float* table, const int32_t* ids, float* out, int n,
+                                  int hidden) {
+    const bool vec = hidden % 4 == 0 && ((uintptr_t)table | (uintptr_t)out) % 16 == 0;
+    const int64_t total = (int64_t)n * (vec ? hidden / 4 : hidden);
+    if (total <= 0) return TLHIP_OK;
+    hipLaunchKernelGGL(embedding_f32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, table, ids, out,
+                       n, hidden, vec ? 1 : 0);
+    return TLHIP_OK;
+}
+
 }  // namespace tlhip

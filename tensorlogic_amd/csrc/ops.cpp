@@ -267,18 +267,24 @@ tlhip_status tlhip_rms_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, float
 tlhip_status tlhip_layer_norm(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor w, tlhip_tensor b, float eps,
                               tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args("layer_norm", {x, y}));
+    bool f32;
+    TLHIP_TRY(float_args("layer_norm", {x, y}, &f32));
     TLHIP_TRY(same_shape(x, y, "layer_norm"));
     const int64_t n = last_dim(x);
     for (tlhip_tensor t : {w, b}) {
         if (!t) continue;
-        TLHIP_TRY(f16_args("layer_norm", {t}));
+        TLHIP_TRY(check_t(t, "layer_norm"));
+        TLHIP_TRY(check_dtype(t, f32 ? TLHIP_F32 : TLHIP_F16, "layer_norm"));
         if (t->ndim != 1 || t->shape[0] != n)
             return fail(TLHIP_ERR_SHAPE_MISMATCH, "layer_norm: param %s for [%lld]", shape_str(t).c_str(), (long long)n);
     }
     if (n == 0) return TLHIP_OK;
-    TLHIP_TRY(launch_layer_norm(ctx->stream, P(x), w ? P(w) : nullptr, b ? P(b) : nullptr, P(y),
-                                (int)(numel(x) / n), (int)n, eps));
+    if (f32)
+        TLHIP_TRY(launch_layer_norm_f32(ctx->stream, F(x), w ? F(w) : nullptr, b ? F(b) : nullptr, F(y),
+                                        (int)(numel(x) / n), (int)n, eps));
+    else
+        TLHIP_TRY(launch_layer_norm(ctx->stream, P(x), w ? P(w) : nullptr, b ? P(b) : nullptr, P(y),
+                                    (int)(numel(x) / n), (int)n, eps));
     return after_launch(ctx, "layer_norm");
 } TLHIP_CATCH_STATUS
 
@@ -323,9 +329,11 @@ tlhip_status tlhip_softmax_lastdim(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y
 
 static tlhip_status unary(tlhip_ctx ctx, int op, tlhip_tensor x, tlhip_tensor y, const char* nm) {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args(nm, {x, y}));
+    bool f32;
+    TLHIP_TRY(float_args(nm, {x, y}, &f32));
     TLHIP_TRY(same_shape(x, y, nm));
-    TLHIP_TRY(launch_elementwise(ctx->stream, op, P(x), nullptr, P(y), numel(x), 0, 0.f));
+    if (f32) TLHIP_TRY(launch_elementwise_f32(ctx->stream, op, F(x), nullptr, F(y), numel(x), 0, 0.f));
+    else TLHIP_TRY(launch_elementwise(ctx->stream, op, P(x), nullptr, P(y), numel(x), 0, 0.f));
     return after_launch(ctx, nm);
 }
 
@@ -344,16 +352,19 @@ tlhip_status tlhip_gelu(tlhip_ctx ctx, tlhip_tensor x, tlhip_tensor y) try { ret
 
 tlhip_status tlhip_silu_mul(tlhip_ctx ctx, tlhip_tensor g, tlhip_tensor u, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args("silu_mul", {g, u, y}));
+    bool f32;
+    TLHIP_TRY(float_args("silu_mul", {g, u, y}, &f32));
     TLHIP_TRY(same_shape(g, u, "silu_mul"));
     TLHIP_TRY(same_shape(g, y, "silu_mul"));
-    TLHIP_TRY(launch_elementwise(ctx->stream, EW_SILU_MUL, P(g), P(u), P(y), numel(g), 0, 0.f));
+    if (f32) TLHIP_TRY(launch_elementwise_f32(ctx->stream, EW_SILU_MUL, F(g), F(u), F(y), numel(g), 0, 0.f));
+    else TLHIP_TRY(launch_elementwise(ctx->stream, EW_SILU_MUL, P(g), P(u), P(y), numel(g), 0, 0.f));
     return after_launch(ctx, "silu_mul");
 } TLHIP_CATCH_STATUS
 
 static tlhip_status binary(tlhip_ctx ctx, int op, tlhip_tensor a, tlhip_tensor b, tlhip_tensor y, const char* nm) {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args(nm, {a, b, y}));
+    bool f32;
+    TLHIP_TRY(float_args(nm, {a, b, y}, &f32));
     TLHIP_TRY(same_shape(a, y, nm));
     int64_t period = 0;
     if (numel(b) != numel(a)) {
@@ -363,7 +374,8 @@ static tlhip_status binary(tlhip_ctx ctx, int op, tlhip_tensor a, tlhip_tensor b
     } else {
         TLHIP_TRY(same_shape(a, b, nm));
     }
-    TLHIP_TRY(launch_elementwise(ctx->stream, op, P(a), P(b), P(y), numel(a), period, 0.f));
+    if (f32) TLHIP_TRY(launch_elementwise_f32(ctx->stream, op, F(a), F(b), F(y), numel(a), period, 0.f));
+    else TLHIP_TRY(launch_elementwise(ctx->stream, op, P(a), P(b), P(y), numel(a), period, 0.f));
     return after_launch(ctx, nm);
 }
 
@@ -372,16 +384,25 @@ tlhip_status tlhip_mul(tlhip_ctx ctx, tlhip_tensor a, tlhip_tensor b, tlhip_tens
 
 tlhip_status tlhip_mul_scalar(tlhip_ctx ctx, tlhip_tensor a, float s, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args("mul_scalar", {a, y}));
+    bool f32;
+    TLHIP_TRY(float_args("mul_scalar", {a, y}, &f32));
     TLHIP_TRY(same_shape(a, y, "mul_scalar"));
-    TLHIP_TRY(launch_elementwise(ctx->stream, EW_MUL_SCALAR, P(a), nullptr, P(y), numel(a), 0, round_f16(s)));
+    // the scalar is a value of the tensor's type (mul_scalar(scalar: T))
+    if (f32) TLHIP_TRY(launch_elementwise_f32(ctx->stream, EW_MUL_SCALAR, F(a), nullptr, F(y), numel(a), 0, s));
+    else TLHIP_TRY(launch_elementwise(ctx->stream, EW_MUL_SCALAR, P(a), nullptr, P(y), numel(a), 0, round_f16(s)));
     return after_launch(ctx, "mul_scalar");
 } TLHIP_CATCH_STATUS
 
 tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* ids, int n, tlhip_tensor out) try {
     TLHIP_TRY(check_ctx(ctx));
     TLHIP_TRY(check_t(table, "embedding table"));
-    TLHIP_TRY(f16_args("embedding", {out}));
+    // an f32 table gives f32 rows (embedding_lookup_f32); every other table f16
+    const bool f32 = table->dtype == TLHIP_F32;
+    if (!f32 && table->dtype != TLHIP_F16 && !is_quant(table->dtype))
+        return fail(TLHIP_ERR_DTYPE, "embedding: table must be F16, F32, Q4_0, Q8_0 or Q6_K (dtype %d)",
+                    (int)table->dtype);
+    TLHIP_TRY(check_t(out, "embedding"));
+    TLHIP_TRY(check_dtype(out, f32 ? TLHIP_F32 : TLHIP_F16, "embedding"));
     if (table->ndim != 2) return fail(TLHIP_ERR_INVALID_DIMENSION, "embedding table must be 2-D");
     const int64_t V = table->shape[0], Hd = table->shape[1];
     if (n < 0 || (n > 0 && !ids)) return fail(TLHIP_ERR_INVALID_ARGUMENT, "embedding: bad ids");
@@ -395,8 +416,9 @@ tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* i
     int32_t* d_ids = nullptr;
     TLHIP_CHECK_HIP(hipMallocAsync(&d_ids, sizeof(int32_t) * n, ctx->stream));
     TLHIP_CHECK_HIP(hipMemcpyAsync(d_ids, ids, sizeof(int32_t) * n, hipMemcpyHostToDevice, ctx->stream));
-    tlhip_status st = launch_embedding(ctx->stream, table->dtype, table->data, table->scales, d_ids, nullptr, P(out),
-                                       n, (int)Hd, (int)V);
+    tlhip_status st = f32 ? launch_embedding_f32(ctx->stream, F(table), d_ids, F(out), n, (int)Hd)
+                          : launch_embedding(ctx->stream, table->dtype, table->data, table->scales, d_ids, nullptr,
+                                             P(out), n, (int)Hd, (int)V);
     (void)hipFreeAsync(d_ids, ctx->stream);
     // the host ids buffer must stay valid until the copy ran
     TLHIP_CHECK_HIP(hipStreamSynchronize(ctx->stream));
@@ -406,7 +428,8 @@ tlhip_status tlhip_embedding(tlhip_ctx ctx, tlhip_tensor table, const int32_t* i
 
 tlhip_status tlhip_apply_attention_mask(tlhip_ctx ctx, tlhip_tensor sc, tlhip_tensor mask, tlhip_tensor y) try {
     TLHIP_TRY(check_ctx(ctx));
-    TLHIP_TRY(f16_args("apply_attention_mask", {sc, mask, y}));
+    bool f32;
+    TLHIP_TRY(float_args("apply_attention_mask", {sc, mask, y}, &f32));
     TLHIP_TRY(same_shape(sc, y, "apply_attention_mask"));
     int64_t period;
     if (numel(mask) == numel(sc)) period = numel(sc);
@@ -416,7 +439,8 @@ tlhip_status tlhip_apply_attention_mask(tlhip_ctx ctx, tlhip_tensor sc, tlhip_te
     else
         return fail(TLHIP_ERR_SHAPE_MISMATCH, "apply_attention_mask: scores %s, mask %s", shape_str(sc).c_str(),
                     shape_str(mask).c_str());
-    TLHIP_TRY(launch_mask(ctx->stream, P(sc), P(mask), P(y), numel(sc), period));
+    if (f32) TLHIP_TRY(launch_mask_f32(ctx->stream, F(sc), F(mask), F(y), numel(sc), period));
+    else TLHIP_TRY(launch_mask(ctx->stream, P(sc), P(mask), P(y), numel(sc), period));
     return after_launch(ctx, "apply_attention_mask");
 } TLHIP_CATCH_STATUS
 

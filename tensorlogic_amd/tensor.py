@@ -180,7 +180,7 @@ class Tensor:
         return out
 
     def layer_norm(self, weight=None, bias=None, eps: float = 1e-5) -> "Tensor":
-        out = self._new(self.shape)
+        out = self._like(self.shape)
         call("tlhip_layer_norm", self.dev.h, self.h, weight.h if weight is not None else None,
              bias.h if bias is not None else None, float(eps), out.h)
         return out
@@ -199,7 +199,7 @@ class Tensor:
         return out
 
     def _unary(self, fn):
-        out = self._new(self.shape)
+        out = self._like(self.shape)
         call(fn, self.dev.h, self.h, out.h)
         return out
 
@@ -215,22 +215,22 @@ class Tensor:
         return self._unary("tlhip_gelu")
 
     def silu_mul(self, up: "Tensor") -> "Tensor":
-        out = self._new(self.shape)
+        out = self._like(self.shape)
         call("tlhip_silu_mul", self.dev.h, self.h, up.h, out.h)
         return out
 
     def add(self, other: "Tensor") -> "Tensor":
-        out = self._new(self.shape)
+        out = self._like(self.shape)
         call("tlhip_add", self.dev.h, self.h, other.h, out.h)
         return out
 
     def mul(self, other: "Tensor") -> "Tensor":
-        out = self._new(self.shape)
+        out = self._like(self.shape)
         call("tlhip_mul", self.dev.h, self.h, other.h, out.h)
         return out
 
     def mul_scalar(self, s: float) -> "Tensor":
-        out = self._new(self.shape)
+        out = self._like(self.shape)
         call("tlhip_mul_scalar", self.dev.h, self.h, float(s), out.h)
         return out
 
@@ -260,7 +260,7 @@ class Tensor:
         return out
 
     def apply_attention_mask(self, mask: "Tensor") -> "Tensor":
-        out = self._new(self.shape)
+        out = self._like(self.shape)
         call("tlhip_apply_attention_mask", self.dev.h, self.h, mask.h, out.h)
         return out
 
@@ -334,7 +334,7 @@ def precompute_rope_sin(dev: Device, head_dim: int, max_seq_len: int, base: floa
 
 def embedding(table: Tensor, ids) -> Tensor:
     ids = np.ascontiguousarray(np.atleast_1d(ids), dtype=np.int32)
-    out = table.dev.empty((ids.size, table.shape[1]))
+    out = table.dev.empty((ids.size, table.shape[1]), F32 if table.dtype == F32 else F16)
     call("tlhip_embedding", table.dev.h, table.h, ids.ctypes.data_as(C.POINTER(C.c_int32)), ids.size, out.h)
     return out
 

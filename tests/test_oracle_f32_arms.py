@@ -289,3 +289,150 @@ def test_einsum_f32_fused_index_order(oracle):
                 fc[i, h, d] = fused_sum(p[i, h], v[:, h, d])
                 uc[i, h, d] = unfused_sum(p[i, h], v[:, h, d])
     assert np.array_equal(bits(ctx), bits(fc)) and not np.array_equal(bits(fc), bits(uc))
+
+
+# ---------------------------------------------------------------------------
+# layer_norm (layer_norm_f32 / layer_norm_simple_f32)
+# ---------------------------------------------------------------------------
+def test_layer_norm_f32_known_answers(oracle):
+    # normalization.rs:541-600 (basic: [[1, 2, 3], [4, 5, 6]] over the last
+    # dim: mean 0, variance 1) and :674-705 (3-D [2, 3, 4] of i / 10)
+    y = oracle.layer_norm_f32(f32([[1, 2, 3], [4, 5, 6]]), None, None, 1e-5)
+    want = np.array([-1, 0, 1], np.float64) / np.sqrt(2.0 / 3.0 + 1e-5)
+    for r in range(2):
+        assert np.all(ulps(y[r], want) <= 2) and y[r, 1] == 0
+    x3 = (np.arange(24, dtype=np.float64) / 10).astype(np.float32).reshape(2, 3, 4)
+    y3 = oracle.layer_norm_f32(x3, None, None, 1e-5)
+    assert y3.shape == (2, 3, 4)
+    assert np.all(np.abs(y3.astype(np.float64).mean(-1)) < 4e-6)   # (the reference test: 1e-2)
+    # :605-670 (affine): [[1, 2], [3, 4]] with w = [2, 3], b = [0.5, 1]
+    ya = oracle.layer_norm_f32(f32([[1, 2], [3, 4]]), f32([2, 3]), f32([0.5, 1]), 1e-5)
+    t = 1.0 / np.sqrt(0.25 + 1e-5) * 0.5
+    assert np.all(ulps(ya, [[-2 * t + 0.5, 3 * t + 1]] * 2) <= 2)
+
+
+def test_layer_norm_f32_closed_form(oracle):
+    """float64 closed form (biased variance, weight then bias): a dropped
+    term, the unbiased variance (a 1/n change) or a swapped weight / bias
+    fails the 2e-6 relative bound at these sizes."""
+    rng = np.random.default_rng(4)
+    for n in (64, 2560):
+        x = (rng.standard_normal((3, n)) * 2 + 0.5).astype(np.float32)
+        w = rng.standard_normal(n).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        x64 = x.astype(np.float64)
+        mu = x64.mean(-1, keepdims=True)
+        nz = (x64 - mu) / np.sqrt(((x64 - mu) ** 2).mean(-1, keepdims=True) + 1e-5)
+        for ww, bb in ((w, b), (w, None), (None, b), (None, None)):
+            want = nz * (ww if ww is not None else 1.0) + (bb if bb is not None else 0.0)
+            got = oracle.layer_norm_f32(x, ww, bb, 1e-5)
+            assert np.max(np.abs(got - want)) < 2e-6 * max(1.0, np.max(np.abs(want)))
+        unbiased = nz * np.sqrt((n - 1) / n)
+        assert np.max(np.abs(oracle.layer_norm_f32(x, None, None, 1e-5) - unbiased)) > 1e-5
+
+
+def _ln_ref(xr, w, b, eps, order="reference"):
+    """Step-by-step layer_norm of one f32 row: element-order sum; squared
+    deviations in element order, fused (one rounding per term) or not, or as
+    256 strided partial sums and a halving tree; y = fma(t, w, b)."""
+    n = xr.size
+    s = np.float32(0.0)
+    for v in xr:
+        s = np.float32(s + v)
+    mean = np.float32(s / np.float32(n))
+    d = (xr - mean).astype(np.float32)
+    if order == "reference":
+        q = fused_sum(d, d)
+    elif order == "unfused":
+        q = unfused_sum(d, d)
+    else:
+        part = [fused_sum(d[t::256], d[t::256]) for t in range(256)]
+        st = 128
+        while st:
+            for t in range(st):
+                part[t] = np.float32(part[t] + part[t + st])
+            st >>= 1
+        q = part[0]
+    var = np.float32(q / np.float32(n))
+    inv = np.float32(np.float32(1.0) / np.float32(np.sqrt(np.float32(var + np.float32(eps)), dtype=np.float32)))
+    t = (d * inv).astype(np.float32)
+    return np.array([np.float32(float(a) * float(c) + float(e)) for a, c, e in zip(t, w, b)], np.float32)
+
+
+@pytest.mark.parametrize("n", [200, 1024])
+def test_layer_norm_f32_summation_order(oracle, n):
+    """Both sums in element order, the squares fused, the weight and bias one
+    fused multiply-add: the oracle equals that emulation bit for bit (grid
+    values, so each float64 step of the emulation is exact or rounds once),
+    and the emulation differs from unfused squares and from a 256-partial
+    tree on some of the 16 rows -- so the test tells those orders apart."""
+    rng = np.random.default_rng(17 + n)
+    R = 16
+    x = grid(rng, (R, n)) + np.float32(0.25)
+    w = np.ones(n, np.float32)
+    b = np.zeros(n, np.float32)
+    got = oracle.layer_norm_f32(x, w, b, 1e-5)
+    refs = [_ln_ref(x[r], w, b, 1e-5) for r in range(R)]
+    for r in range(R):
+        assert np.array_equal(bits(got[r]), bits(refs[r]))
+    assert any(not np.array_equal(bits(refs[r]), bits(_ln_ref(x[r], w, b, 1e-5, "unfused"))) for r in range(R))
+    assert any(not np.array_equal(bits(refs[r]), bits(_ln_ref(x[r], w, b, 1e-5, "tree"))) for r in range(R))
+    # with a weight and a bias on the grid: one fused multiply-add per element
+    wv, bv = grid(rng, (n,), 8), grid(rng, (n,), 8)
+    gotw = oracle.layer_norm_f32(x[:2], wv, bv, 1e-5)
+    for r in range(2):
+        assert np.array_equal(bits(gotw[r]), bits(_ln_ref(x[r], wv, bv, 1e-5)))
+
+
+# ---------------------------------------------------------------------------
+# gelu (gelu_f32), silu / swiglu, add / mul / mul_scalar, apply_attention_mask
+# ---------------------------------------------------------------------------
+def test_gelu_f32_known_answers_and_closed_form(oracle):
+    # activations.rs:900-940: GELU(0) = 0, GELU(-2) ~ -0.0454, GELU(-1) ~
+    # -0.1587, GELU(1) ~ 0.8413, GELU(2) ~ 1.9545
+    y = oracle.gelu_f32(f32([-2, -1, 0, 1, 2]))
+    assert y[2] == 0
+    assert np.all(np.abs(y - f32([-0.0454, -0.1587, 0, 0.8413, 1.9545])) < 2e-4)
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(4000) * 4).astype(np.float32)
+    g = oracle.gelu_f32(x)
+    v = x.astype(np.float64)
+    want = 0.5 * v * (1 + np.tanh(0.7978845608 * (v + 0.044715 * v ** 3)))
+    # (for x << 0, 1 + tanh cancels: the f32 steps then carry ~|x| * 2^-24 absolute error)
+    assert np.all(np.abs(g - want) <= 4e-6 * np.abs(want) + 3e-7 * np.abs(v))
+    # the tanh form's odd part: gelu(x) - gelu(-x) = x
+    assert np.max(np.abs((g - oracle.gelu_f32(-x)) - x) / np.maximum(np.abs(x), 1.0)) < 2e-6
+
+
+def test_silu_swiglu_f32(oracle):
+    # activations.rs:844-870: silu(x) = x * sigmoid(x), silu(0) = 0
+    x = f32([-2, -1, 0, 1, 2])
+    s = oracle.silu_f32(x)
+    assert s[2] == 0
+    want = x.astype(np.float64) / (1 + np.exp(-x.astype(np.float64)))
+    assert np.all(ulps(s, want) <= 3)
+    # composed of the oracle's own f32 steps: sigmoid, then one product each
+    rng = np.random.default_rng(10)
+    g = (rng.standard_normal(1000) * 3).astype(np.float32)
+    u = rng.standard_normal(1000).astype(np.float32)
+    sg = oracle.sigmoid_f32(g)
+    assert np.array_equal(bits(oracle.silu_f32(g)), bits(g * sg))
+    assert np.array_equal(bits(oracle.swiglu_f32(g, u)), bits((g * sg).astype(np.float32) * u))
+
+
+def test_add_mul_mask_f32(oracle):
+    # one IEEE operation each: integers and halves add and multiply exactly
+    a, b = f32([1.5, -2, 3, 0.25]), f32([0.5, 4, -3, 8])
+    assert np.array_equal(oracle.add_f32(a, b), f32([2, 2, 0, 8.25]))
+    assert np.array_equal(oracle.mul_f32(a, b), f32([0.75, -8, -9, 2]))
+    # the f32 scalar is not rounded to f16: 0.1 stays 0.1f
+    assert oracle.mul_scalar_f32(f32([1.0]), 0.1)[0] == np.float32(0.1)
+    assert np.float32(np.float16(0.1)) != np.float32(0.1)
+    # masking.rs:325-355: scores [1, 2, 3, 4], mask [1, 0, 1, 1]
+    m = oracle.apply_attention_mask_f32(f32([[1, 2], [3, 4]]), f32([[1, 0], [1, 1]]))
+    assert np.array_equal(m, f32([[1, -10000], [3, 4]]))
+    # a [I, J] mask over [I, H, J] scores masks every head alike
+    sc = np.arange(12, dtype=np.float32).reshape(2, 3, 2)
+    mm = oracle.apply_attention_mask_f32(sc, f32([[1, 0], [0, 1]]))
+    assert np.all(mm[0, :, 1] == -10000) and np.all(mm[1, :, 0] == -10000)
+    assert np.array_equal(mm[0, :, 0], sc[0, :, 0]) and np.array_equal(mm[1, :, 1], sc[1, :, 1])
