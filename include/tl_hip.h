@@ -224,6 +224,28 @@ tlhip_status tlhip_precompute_rope(tlhip_ctx ctx, int head_dim, int max_seq_len,
  * h / (H/Hkv)), replacing broadcast_to + contiguous.                      */
 tlhip_status tlhip_einsum_scores(tlhip_ctx ctx, tlhip_tensor q, tlhip_tensor k, tlhip_tensor scores);
 tlhip_status tlhip_einsum_context(tlhip_ctx ctx, tlhip_tensor p, tlhip_tensor v, tlhip_tensor out);
+/* einsum(equation, operands...) (eval.rs:3264-3318 -> Tensor::einsum,
+ * einsum.rs:39-82), parsed as the reference parses it (einsum.rs:84-128:
+ * at most one "->"; without it the output is every index occurring once,
+ * sorted).  "ihd,jhd->ihj" / "ihj,jhd->ihd" on rank-3 operands are
+ * tlhip_einsum_scores / tlhip_einsum_context (the reference's Metal path,
+ * f16 or f32).  Every other equation (the reference's Metal path panics on
+ * them) computes general_einsum_cpu (einsum.rs:207-333) on f16 operands:
+ * per output element, products in operand order and sums over the summed
+ * indices nested outermost first, every step rounded to f16.  The
+ * reference nests two or more summed indices in HashSet order, which Rust
+ * randomises per process; here they nest in order of first appearance in
+ * the inputs.  Up to 4 operands, 8 output and 8 summed indices; a scalar
+ * result is a [1] tensor.  Errors: operand count -> InvalidOperation, mixed
+ * f16 / f32 -> DtypeError (the reference's TypeError), a repeated index of
+ * two sizes -> ShapeMismatch, unknown output index or a spec whose length
+ * is not the operand's rank -> InvalidOperation; f32 operands of a general
+ * equation -> InvalidOperation.  tlhip_einsum_shape gives the output shape
+ * (ndim and up to 8 dims) without launching anything.                     */
+tlhip_status tlhip_einsum_shape(const char* equation, const tlhip_tensor* operands, int n_operands, int* ndim,
+                                int64_t* shape);
+tlhip_status tlhip_einsum(tlhip_ctx ctx, const char* equation, const tlhip_tensor* operands, int n_operands,
+                          tlhip_tensor out);
 /* Fused attention = einsum scores -> * scale (f16) -> causal mask (-10000)
  * -> softmax -> einsum context, with the reference's f16 storage points.
  * q [S,H,D]; k, v [J,Hkv,D] (a KV cache's first J rows); query row s sits

@@ -415,6 +415,77 @@ def einsum_scores(q, k) -> np.ndarray:
     return out
 
 
+def einsum_parse(equation: str):
+    """parse_einsum_equation / infer_output_spec (einsum.rs:84-128): at most
+    one "->", inputs split at ',' and trimmed; without "->" the output is
+    every index occurring exactly once, sorted.  Returns (input specs,
+    output spec)."""
+    parts = equation.split("->")
+    if len(parts) > 2:
+        raise ValueError("Invalid einsum equation: too many arrows")
+    ins = [x.strip() for x in parts[0].split(",")]
+    if len(parts) == 2:
+        return ins, parts[1].strip()
+    counts = {}
+    for c in parts[0]:
+        if c.isalpha():
+            counts[c] = counts.get(c, 0) + 1
+    return ins, "".join(sorted(c for c, n in counts.items() if n == 1))
+
+
+def einsum_general(equation: str, *ops) -> np.ndarray:
+    """general_einsum_cpu / sum_over_indices (einsum.rs:207-333) on f16
+    operands, vectorised over the output elements: the product starts at f16
+    one and multiplies the operands' elements in operand order, each product
+    rounded to f16 (the `half` crate computes in f32 and rounds, as numpy's
+    float16 arithmetic does); the summed indices nest outermost first, each
+    level an f16 running sum from +0 of the inner level's results.  The
+    reference nests two or more summed indices in HashSet order (random per
+    process); this restatement nests them in order of first appearance, the
+    order the library fixes.  A scalar result has shape (1,)."""
+    ins, out = einsum_parse(equation)
+    ops = [_h(o) for o in ops]
+    if len(ins) != len(ops):
+        raise ValueError(f"Expected {len(ins)} operands, got {len(ops)}")
+    dims, order = {}, []
+    for spec, o in zip(ins, ops):
+        if len(spec) != o.ndim:
+            raise ValueError(f"spec {spec} for a {o.ndim}-d operand")
+        for c, d in zip(spec, o.shape):
+            if c not in dims:
+                dims[c] = d
+                order.append(c)
+            elif dims[c] != d:
+                raise ValueError(f"index {c}: {dims[c]} vs {d}")
+    out_dims = [dims[c] for c in out]
+    sums = [c for c in order if c not in out]
+    coords = {c: g.reshape(-1) for c, g in zip(out, np.indices(out_dims))} if out else {}
+    n_out = int(np.prod(out_dims)) if out else 1
+    flat = [o.reshape(-1) for o in ops]
+
+    def product(vals):
+        prod = np.full(n_out, np.float16(1.0), np.float16)
+        for spec, o, f in zip(ins, ops, flat):
+            lin = np.zeros(n_out, np.int64)
+            for c, d in zip(spec, o.shape):
+                lin = lin * d + vals[c]
+            prod = (prod * f[lin]).astype(np.float16)
+        return prod
+
+    def level(li, vals):
+        if li == len(sums):
+            return product(vals)
+        c = sums[li]
+        acc = np.zeros(n_out, np.float16)
+        for i in range(dims[c]):
+            vals[c] = np.full(n_out, i, np.int64)
+            acc = (acc + level(li + 1, vals)).astype(np.float16)
+        return acc
+
+    res = level(0, dict(coords))
+    return res.reshape(out_dims if out else (1,))
+
+
 def einsum_context(p, v, acc=ACC_F32) -> np.ndarray:
     """einsum("ihj,jhd->ihd", p [I,H,J], v [J,Hkv,D]) (tlo_einsum_context)."""
     p, v = _h(p), _h(v)

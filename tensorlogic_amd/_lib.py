@@ -80,6 +80,8 @@ SIGNATURES = {
     "tlhip_precompute_rope": (_i, [_vp, _i, _i, _f, _i, _vp]),
     "tlhip_einsum_scores": (_i, [_vp, _vp, _vp, _vp]),
     "tlhip_einsum_context": (_i, [_vp, _vp, _vp, _vp]),
+    "tlhip_einsum_shape": (_i, [C.c_char_p, C.POINTER(_vp), _i, C.POINTER(_i), C.POINTER(C.c_int64)]),
+    "tlhip_einsum": (_i, [_vp, C.c_char_p, C.POINTER(_vp), _i, _vp]),
     "tlhip_attention": (_i, [_vp, _vp, _vp, _vp, _i, _f, _i, _vp]),
     "tlhip_argmax": (_i, [_vp, _vp, _i32p]),
     "tlhip_tensor_argmax": (_i, [_vp, _vp, _i, _i, _vp]),

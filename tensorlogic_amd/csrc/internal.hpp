@@ -282,6 +282,20 @@ tlhip_status launch_mask_f32(hipStream_t s, const float* sc, const float* mask, 
 tlhip_status launch_embedding_f32(hipStream_t s, const float* table, const int32_t* ids, float* out, int n,
                                   int hidden);
 tlhip_status launch_causal_mask(hipStream_t s, uint16_t* out, int64_t n);
+// general einsum (f16, general_einsum_cpu's arithmetic): for each output
+// element, the operands' element offsets are the sums of coordinate x
+// stride over the output indices and the summed indices (nested outermost
+// first); sizes and strides in elements.
+constexpr int EINSUM_MAX_OPS = 4, EINSUM_MAX_SUM = 8;
+struct EinsumPlan {
+    int n_ops = 0, n_out = 0, n_sum = 0;
+    int64_t out_dim[8] = {};
+    int64_t sum_dim[EINSUM_MAX_SUM] = {};
+    int64_t out_stride[EINSUM_MAX_OPS][8] = {};
+    int64_t sum_stride[EINSUM_MAX_OPS][EINSUM_MAX_SUM] = {};
+    const uint16_t* op[EINSUM_MAX_OPS] = {};
+};
+tlhip_status launch_einsum_general(hipStream_t s, const EinsumPlan& p, uint16_t* out, int64_t n_out, int64_t n_sum);
 // broadcast_to: target dims and, per target dim, the input stride (0 where
 // the input has size 1 or no dim)
 struct BcastDims {

@@ -1051,6 +1051,72 @@ tlhip_status launch_transpose_f32(hipStream_t s, const float* src, float* dst, i
 }
 
 // ---------------------------------------------------------------------------
+// general einsum (general_einsum_cpu / sum_over_indices, einsum.rs:207-333)
+// on f16 tensors, one thread per output element: the product of the
+// operands' elements starts at f16 one and multiplies them in operand order,
+// each product rounded to f16; the summed indices nest outermost first, and
+// every level keeps its own f16 running sum from +0 of the completed inner
+// level's sums (the innermost of the products), each addition rounded to
+// f16 -- the reference's recursion.  With no summed index the output is the
+// product itself.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint16_t einsum_product(const EinsumPlan& p, const int64_t* off) {
+    uint16_t prod = 0x3C00u;
+    for (int k = 0; k < p.n_ops; k++) prod = f2h(h2f(prod) * h2f(p.op[k][off[k]]));
+    return prod;
+}
+
+__global__ __launch_bounds__(256) void einsum_general_kernel(EinsumPlan p, uint16_t* __restrict__ out, int64_t n_out,
+                                                             int64_t n_sum) {
+    for (int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x; o < n_out; o += (int64_t)gridDim.x * 256) {
+        int64_t off[EINSUM_MAX_OPS] = {};
+        int64_t rem = o;
+        for (int d = p.n_out - 1; d >= 0; d--) {
+            const int64_t c = rem % p.out_dim[d];
+            rem /= p.out_dim[d];
+            for (int k = 0; k < p.n_ops; k++) off[k] += c * p.out_stride[k][d];
+        }
+        uint16_t r;
+        if (p.n_sum == 0) {
+            r = einsum_product(p, off);
+        } else {
+            uint16_t acc[EINSUM_MAX_SUM];
+            int64_t idx[EINSUM_MAX_SUM];
+            for (int d = 0; d < EINSUM_MAX_SUM; d++) {
+                acc[d] = 0;
+                idx[d] = 0;
+            }
+            const int last = p.n_sum - 1;
+            for (int64_t s = 0; s < n_sum; s++) {
+                acc[last] = f2h(h2f(acc[last]) + h2f(einsum_product(p, off)));
+                // advance the innermost index; a level that wraps hands its
+                // sum to the level outside it
+                for (int d = last; d >= 0; d--) {
+                    idx[d]++;
+                    for (int k = 0; k < p.n_ops; k++) off[k] += p.sum_stride[k][d];
+                    if (idx[d] < p.sum_dim[d]) break;
+                    for (int k = 0; k < p.n_ops; k++) off[k] -= p.sum_stride[k][d] * p.sum_dim[d];
+                    idx[d] = 0;
+                    if (d > 0) {
+                        acc[d - 1] = f2h(h2f(acc[d - 1]) + h2f(acc[d]));
+                        acc[d] = 0;
+                    }
+                }
+            }
+            r = acc[0];
+        }
+        out[o] = r;
+    }
+}
+
+tlhip_status launch_einsum_general(hipStream_t s, const EinsumPlan& p, uint16_t* out, int64_t n_out, int64_t n_sum) {
+    if (n_out <= 0) return TLHIP_OK;
+    const int64_t blocks = std::min<int64_t>((n_out + 255) / 256, 65536);
+    hipLaunchKernelGGL(einsum_general_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, out, n_out, n_sum);
+    return TLHIP_OK;
+}
+
+// ---------------------------------------------------------------------------
 // The TensorF32 arms of rms_norm, softmax, rope and sigmoid (f32 in, f32
 // out, f32 arithmetic).
 

@@ -287,18 +287,19 @@ class Tensor:
         return out
 
 
-def einsum(eq: str, a: Tensor, b: Tensor) -> Tensor:
-    """The two attention einsums the TL programs use (einsum.rs:653-886)."""
-    eq = eq.replace(" ", "")
-    if eq == "ihd,jhd->ihj":
-        out = a._like((a.shape[0], a.shape[1], b.shape[0]))
-        call("tlhip_einsum_scores", a.dev.h, a.h, b.h, out.h)
-        return out
-    if eq == "ihj,jhd->ihd":
-        out = a._like((a.shape[0], a.shape[1], b.shape[2]))
-        call("tlhip_einsum_context", a.dev.h, a.h, b.h, out.h)
-        return out
-    raise TLHipError(3, f"einsum pattern {eq} not supported")
+def einsum(eq: str, *ops: Tensor) -> Tensor:
+    """einsum(equation, tensors...) (eval.rs:3264-3318, einsum.rs:39-82):
+    the attention equations through their kernels, any other equation as
+    the reference's general f16 einsum; a scalar result has shape (1,)."""
+    if not ops:
+        raise TLHipError(3, "einsum requires at least one tensor")
+    arr = (C.c_void_p * len(ops))(*[t.h for t in ops])
+    nd = C.c_int()
+    shp = (C.c_int64 * 8)()
+    call("tlhip_einsum_shape", eq.encode(), arr, len(ops), C.byref(nd), shp)
+    out = ops[0]._like(tuple(shp[i] for i in range(nd.value)))
+    call("tlhip_einsum", ops[0].dev.h, eq.encode(), arr, len(ops), out.h)
+    return out
 
 
 def attention(q: Tensor, k: Tensor, v: Tensor, q_pos0: int = 0, scale: float | None = None,
