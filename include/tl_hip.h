@@ -235,8 +235,9 @@ tlhip_status tlhip_einsum_context(tlhip_ctx ctx, tlhip_tensor p, tlhip_tensor v,
  * indices nested outermost first, every step rounded to f16.  The
  * reference nests two or more summed indices in HashSet order, which Rust
  * randomises per process; here they nest in order of first appearance in
- * the inputs.  Up to 4 operands, 8 output and 8 summed indices; a scalar
- * result is a [1] tensor.  Errors: operand count -> InvalidOperation, mixed
+ * the inputs.  Up to 4 operands, 8 output and 8 summed indices, at most
+ * 2^31 summed terms per output element and 2^36 in all (one thread walks
+ * an element's terms); a scalar result is a [1] tensor.  Errors: operand count -> InvalidOperation, mixed
  * f16 / f32 -> DtypeError (the reference's TypeError), a repeated index of
  * two sizes -> ShapeMismatch, unknown output index or a spec whose length
  * is not the operand's rank -> InvalidOperation; f32 operands of a general

@@ -148,8 +148,15 @@ tlhip_status plan_einsum(const char* equation, const tlhip_tensor* ops, int n, E
         if (__builtin_mul_overflow(e->n_sum, p.sum_dim[d], &e->n_sum))
             return fail(TLHIP_ERR_INVALID_OPERATION, "einsum: summation space too large");
     }
-    if (e->n_out > 0 && e->n_sum > 0 && e->n_sum > (int64_t)1 << 40)
-        return fail(TLHIP_ERR_INVALID_OPERATION, "einsum: summation space too large");
+    // one thread walks an output element's whole summation space: bound it
+    // (2^31 terms per element, 2^36 in all) so that one launch cannot hold
+    // the device for minutes
+    int64_t work = 0;
+    if (e->n_sum > ((int64_t)1 << 31) || __builtin_mul_overflow(e->n_out, e->n_sum, &work) ||
+        work > ((int64_t)1 << 36))
+        return fail(TLHIP_ERR_INVALID_OPERATION,
+                    "einsum: %lld output elements x %lld summed terms is beyond the general kernel's bound",
+                    (long long)e->n_out, (long long)e->n_sum);
     // element strides of every operand along each output / summed index (a
     // repeated index in one operand, e.g. "ii", adds its strides: the diagonal)
     for (int k = 0; k < n; k++) {

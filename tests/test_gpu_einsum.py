@@ -96,6 +96,11 @@ def test_errors(dev):
         with pytest.raises(TLHipError) as e:
             einsum(eq, *ops)
         assert e.value.kind == kind, eq
+    # a summation space beyond the general kernel's bound is refused up front
+    big = dev.tensor(h(np.ones((2048, 2048))))
+    with pytest.raises(TLHipError) as e:
+        einsum("ij,kl->", big, big)
+    assert e.value.kind == "InvalidOperation"
     f = dev.tensor(np.ones((3, 5), np.float32), F32)
     with pytest.raises(TLHipError) as e:
         einsum("ij,jk->ik", a, f)
