@@ -40,14 +40,28 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
 // Q4_0: bytes j..j+3 of the 16 payload bytes hold elements j..j+3 in their
 // low nibbles and j+16..j+19 in their high nibbles; out = (e0,e2) (e1,e3)
 // (e16,e18) (e17,e19) relative to j.
+// (a & m) | o as the one instruction v_and_or_b32.  Written out because
+// the compiler splits it into v_and + v_or when m and o are constants (a
+// three-operand instruction takes no literal here); the mask comes in a
+// scalar register, the or-value in a vector register, both set once.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(o));
+    return r;
+}
+
 __device__ __forceinline__ void q4_unpack(uint32_t w, h2 dd, h2 out[4]) {
-    const h2 bias = {(h16)-1032.0f, (h16)-1032.0f};
-    const uint32_t k = 0x64646464u;
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    out[0] = (as_h2(__builtin_amdgcn_perm(k, lo, 0x04020400u)) + bias) * dd;
-    out[1] = (as_h2(__builtin_amdgcn_perm(k, lo, 0x04030401u)) + bias) * dd;
-    out[2] = (as_h2(__builtin_amdgcn_perm(k, hi, 0x04020400u)) + bias) * dd;
-    out[3] = (as_h2(__builtin_amdgcn_perm(k, hi, 0x04030401u)) + bias) * dd;
+    // A low nibble q under the exponent bits 0x6400 is the f16 1024 + q; a
+    // high nibble left in place (bits 4..7, q << 4) under 0x5400 is 64 + q
+    // (mantissa step 1/16 at 64).  Both are exact, so subtracting 1032 / 72
+    // gives q - 8 exactly, and one mask-or per pair (a shift per two pairs)
+    // replaces the masks, shift and byte permutes.
+    const h2 blo = {(h16)-1032.0f, (h16)-1032.0f}, bhi = {(h16)-72.0f, (h16)-72.0f};
+    const uint32_t s = w >> 8;
+    out[0] = (as_h2(and_or(w, 0x000F000Fu, 0x64006400u)) + blo) * dd;
+    out[1] = (as_h2(and_or(s, 0x000F000Fu, 0x64006400u)) + blo) * dd;
+    out[2] = (as_h2(and_or(w, 0x00F000F0u, 0x54005400u)) + bhi) * dd;
+    out[3] = (as_h2(and_or(s, 0x00F000F0u, 0x54005400u)) + bhi) * dd;
 }
 
 // Q8_0: four int8 (e0..e3) -> (e0,e2) (e1,e3).
