@@ -244,12 +244,13 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs ak, int J_fixe
         sc[j] = h2f(f2h(e));
         sum += e;
     }
-    sum = block_sum1<NWV>(sum, red[1]);
+    sum = block_sum1<NWV>(sum, red[1]);   // (its barrier also publishes the e values in sc[])
     const bool degenerate = !(sum > 0.0f && isfinite(sum));
     const int Jp = degenerate ? J : Jv;
     const float uni = h2f(f2h(1.0f / (float)J));
-    for (int j = tid; j < Jp; j += NT) sc[j] = degenerate ? uni : h2f(f2h(sc[j] / sum));
-    __syncthreads();
+    // P_j = f16(e_j / sum), or the uniform row, formed by the lanes that use
+    // it: no pass over the score row and no barrier between the sum and P.V
+    auto pval = [&](int j) { return degenerate ? uni : h2f(f2h(sc[j] / sum)); };
 
     float o[8];
 #pragma unroll
@@ -259,7 +260,7 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs ak, int J_fixe
         for (int u = 0; u < UNR; u++) {
             const int j = g + NG * u;
             if (j < Jp) {
-                const float pj = sc[j];
+                const float pj = pval(j);
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
                     const h2 v2 = as_h2(vv[u][t]);
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(NT) void attention64_kernel(AttnArgs ak, int J_fixe
             for (int u = 0; u < UNR; u++) {
                 const int j = j0 + NG * u;
                 if (j < Jp) {
-                    const float pj = sc[j];
+                    const float pj = pval(j);
 #pragma unroll
                     for (int t = 0; t < 4; t++) {
                         const h2 v2 = as_h2(vv[u][t]);
@@ -429,12 +430,12 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
         sc[j] = h2f(f2h(e));
         sum += e;
     }
-    sum = block_sum1<NWV>(sum, red[1]);
+    sum = block_sum1<NWV>(sum, red[1]);   // (its barrier also publishes the e values in sc[])
     const bool degenerate = !(sum > 0.0f && isfinite(sum));
     const int Jp = degenerate ? J : Jv;
     const float uni = h2f(f2h(1.0f / (float)J));
-    for (int j = tid; j < Jp; j += NT) sc[j] = degenerate ? uni : h2f(f2h(sc[j] / sum));
-    __syncthreads();
+    // P_j formed where it is used, as in attention64_kernel
+    auto pval = [&](int j) { return degenerate ? uni : h2f(f2h(sc[j] / sum)); };
 
     float o[EPL];
 #pragma unroll
@@ -460,7 +461,7 @@ __global__ __launch_bounds__(ADK_THREADS) void attention_dk_kernel(AttnArgs a, i
         for (int u = 0; u < U; u++) {
             const int j = j0 + NG * u;
             if (j < Jp) {
-                const float pj = sc[j];
+                const float pj = pval(j);
 #pragma unroll
                 for (int t = 0; t < NW; t++) {
                     const h2 v2 = as_h2(vw[u][t]);
