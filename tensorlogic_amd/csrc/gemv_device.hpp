@@ -83,6 +83,10 @@ struct GemvParams {
     uint16_t* xn_out;
     // EPI_ARGMAX: per-workgroup (value, index) keys
     unsigned long long* amax_slots;
+    // LayerNorm prologue (QKV and greedy-key epilogues): the row is
+    // f16(x + x_add) -- the residual stream's last addition, made here --
+    // and workgroup 0 writes that sum to x_out
+    const uint16_t* x_add;
 };
 
 // Fourth word of a raw buffer resource descriptor on gfx9-family GPUs
@@ -111,7 +115,8 @@ __device__ __forceinline__ void kernarg_fence(const GemvParams& p) {
     asm volatile("" ::"s"(p.x), "s"(p.wq), "s"(p.wd), "s"(p.bias), "s"(p.resid), "s"(p.y), "s"(p.M), "s"(p.N),
                  "s"(p.K), "s"(p.ldy), "s"(p.epi), "s"(p.norm_w), "s"(p.norm_b), "s"(p.eps), "s"(p.nq), "s"(p.nk),
                  "s"(p.head_dim), "s"(p.rot), "s"(p.layout), "s"(p.pos0), "s"(p.rope_tab), "s"(p.d_pos),
-                 "s"(p.q_out), "s"(p.kc), "s"(p.vc), "s"(p.embd), "s"(p.d_token), "s"(p.x_out), "s"(p.xn_out), "s"(p.amax_slots));
+                 "s"(p.q_out), "s"(p.kc), "s"(p.vc), "s"(p.embd), "s"(p.d_token), "s"(p.x_out), "s"(p.xn_out), "s"(p.amax_slots),
+                 "s"(p.x_add));
     __builtin_amdgcn_sched_barrier(0);   // nothing that uses them moves above
 }
 
@@ -232,6 +237,7 @@ struct NormStage {
     static constexpr int NT = WPB * 64;
     static constexpr int IPT = (NB * 256 + NT - 1) / NT;
     uint32_t xw[IPT][4], ww[IPT][4], bw[IPT][4];   // raw f16 pairs until finish()
+    uint32_t aw[IPT][4];   // LayerNorm with x_add: the added row
     uint32_t xn[IPT][4];   // the normalised quads in natural element order (for xn_out)
 
     __device__ __forceinline__ static void load_buf(const uint16_t* __restrict__ src, int K, int it, uint32_t w[4]) {
@@ -263,6 +269,7 @@ struct NormStage {
             load_buf(xsrc, p.K, it, xw[k]);
             load_buf(p.norm_w, p.K, it, ww[k]);
             if (PRO == PRO_LN) load_buf(p.norm_b, p.K, it, bw[k]);
+            if (PRO == PRO_LN && p.x_add) load_buf(p.x_add, p.K, it, aw[k]);
         }
     }
 
@@ -293,7 +300,15 @@ struct NormStage {
         float f[IPT][8];
 #pragma unroll
         for (int k = 0; k < IPT; k++) to_float(xw[k], f[k]);   // (quads past the row read zeros)
-        if (p.x_out && blockIdx.x == 0)   // the residual copy of an embedded row
+        if (PRO == PRO_LN && p.x_add)
+#pragma unroll
+            for (int k = 0; k < IPT; k++) {
+                float g[8];
+                to_float(aw[k], g);
+#pragma unroll
+                for (int e = 0; e < 8; e++) f[k][e] = h2f(f2h(f[k][e] + g[e]));   // the residual's f16 add
+            }
+        if (p.x_out && blockIdx.x == 0)   // the residual copy of an embedded or summed row
 #pragma unroll
             for (int k = 0; k < IPT; k++) {
                 const int it = threadIdx.x + k * NT;
@@ -848,8 +863,10 @@ struct Gemv1Params {
 // [2048 x 5632] + residual 4.10 -> 3.99 us, [5632 x 2048] 3.81 -> 3.71 us,
 // bit-identical outputs); EPI < 0: chosen at run time from p.epi and the
 // pointers present.
+// The body takes its workgroup index as bx, so that a launch of another
+// kernel can run it on some of its workgroups (WPB * 64 threads each).
 template <int WT, int NB, int RI, int EPI = -1, int FN = 0, int WPB = 4>
-__global__ __launch_bounds__(WPB * 64) void gemv_m1_kernel(Gemv1Params p) {
+__device__ __forceinline__ void gemv_m1_body(const Gemv1Params& p, int bx) {
     constexpr int NT = WPB * 64, NSX = (NB * 256 + NT - 1) / NT;   // activation quads per thread
     __shared__ u4 xs[4][NB * 64];
     const bool has_bias = EPI < 0 ? p.bias != nullptr : (EPI == EPI_BIAS || EPI == EPI_BIAS_RESID || EPI == EPI_BIAS_GELU);
@@ -857,7 +874,7 @@ __global__ __launch_bounds__(WPB * 64) void gemv_m1_kernel(Gemv1Params p) {
     const int epi = EPI < 0 ? p.epi : EPI;
     constexpr int NL = BlkLoads<WT>::n;
     const int lane = threadIdx.x & 63;
-    const int row0 = ((int)blockIdx.x * WPB + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6)) * RI;
+    const int row0 = (bx * WPB + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6)) * RI;
     uint32_t xw[NSX][4];
     {
         const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)p.x, (short)0, p.K * 2, BUF_RSRC_WORD3);
@@ -946,6 +963,11 @@ __global__ __launch_bounds__(WPB * 64) void gemv_m1_kernel(Gemv1Params p) {
     }
 }
 
+template <int WT, int NB, int RI, int EPI = -1, int FN = 0, int WPB = 4>
+__global__ __launch_bounds__(WPB * 64) void gemv_m1_kernel(Gemv1Params p) {
+    gemv_m1_body<WT, NB, RI, EPI, FN, WPB>(p, (int)blockIdx.x);
+}
+
 // Normalised GEMV (M = 1): norm(x) staged once per workgroup in LDS (the
 // weight loads are issued first, so they are in flight during it), then
 // the same block dots.  EPI_ARGMAX additionally reduces the workgroup's
@@ -992,8 +1014,12 @@ __device__ __forceinline__ GemvParams norm_view(const GemvParams& k) {
         p.d_token = k.d_token;
         p.x_out = k.x_out;
         p.xn_out = k.xn_out;
+        if (PRO == PRO_LN) p.x_add = k.x_add;
     }
-    if (EPI == EPI_ARGMAX) p.amax_slots = k.amax_slots;
+    if (EPI == EPI_ARGMAX) {
+        p.amax_slots = k.amax_slots;
+        if (PRO == PRO_LN) p.x_add = k.x_add;
+    }
     return p;
 }
 

@@ -192,6 +192,9 @@ struct GemvArgs {
     uint16_t* xn_out = nullptr;
     // EPI_ARGMAX: one (value, index) key per workgroup, gemv_norm_slots(N) of them
     unsigned long long* amax_slots = nullptr;
+    // normalised GEMV with layer_norm (QKV / greedy-key epilogues): the row
+    // normalised is f16(x + x_add), and workgroup 0 writes it to x_out
+    const uint16_t* x_add = nullptr;
     // GEMM split-K workspace (fp32 partials); none = no split
     float* ws = nullptr;
     size_t ws_bytes = 0;
@@ -352,6 +355,13 @@ size_t attention_mfma_scratch(int J, int Hkv, int D);
 bool attention_split_ok(const AttnArgs& a);
 size_t attention_split_scratch(int H, int kv_rows, int D);
 tlhip_status launch_attention_split(hipStream_t s, const AttnArgs& a, float* scratch);
+// Phi-2's decode step: that split attention and fc1 (GEMV + bias + GELU on
+// the normalised row, weight type wt) in one launch; false (nothing
+// launched) when the shapes are not the ones it is built for.
+bool launch_attention_split_fc1(hipStream_t s, const AttnArgs& a, float* scratch, tlhip_dtype wt, const GemvArgs& f);
+// Phi-2's decode step: dense + bias + residual and fc2 + bias (one row
+// each) in one launch; false (nothing launched) for other shapes.
+bool launch_m1_pair(hipStream_t s, tlhip_dtype wt, const GemvArgs& d, int epi_d, const GemvArgs& f, int epi_f);
 // The same split for one query row over J keys known at launch (no device
 // position; kv_rows is taken as J); scratch of attention_split_scratch(H, J, D).
 bool attention_split_j_ok(const AttnArgs& a, int J);

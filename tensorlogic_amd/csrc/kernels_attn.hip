@@ -15,6 +15,7 @@
 // sum or the output; the degenerate all-non-finite row falls back to the
 // reference's uniform 1/J over every key.
 #include "device_common.hpp"
+#include "gemv_device.hpp"
 #include "internal.hpp"
 
 namespace tlhip {
@@ -631,8 +632,11 @@ __device__ __forceinline__ float asplit_combine(const float* pm, const float* ps
     return !isfinite(M) ? h2f(f2h(1.0f / (float)J)) * num : num / den;
 }
 
+// The body takes the workgroup's place (bx = chunk slot, by = head slot,
+// gx = chunk slots per head), so that a launch of another kernel can run it
+// on some of its workgroups (NT threads each).
 template <int D, int NT, bool XCH, int CH>
-__global__ __launch_bounds__(NT) void asplit_kernel(AttnArgs a, SplitBufs b) {
+__device__ __forceinline__ void asplit_body(const AttnArgs& a, const SplitBufs& b, int bx, int by, int gx) {
     constexpr int EPL = D / 8, NW = EPL / 2, NWV = As<NT, CH>::NWV, AS_NG = As<NT, CH>::NG, AS_U = As<NT, CH>::U;
     __shared__ float red[2][NWV];
     __shared__ float part[NWV][D];
@@ -643,11 +647,11 @@ __global__ __launch_bounds__(NT) void asplit_kernel(AttnArgs a, SplitBufs b) {
     // nothing but the cache lines at their row boundaries (Phi-2: 160-byte
     // head rows), so each XCD takes H/8 consecutive heads, all chunks, and
     // its L2 fetches a shared line once.
-    int ch = blockIdx.x, h = blockIdx.y;
+    int ch = bx, h = by;
     if (a.H == a.Hkv && (a.H & 7) == 0) {
-        const int id = blockIdx.x + gridDim.x * blockIdx.y, q = id >> 3;
-        h = (id & 7) * (a.H >> 3) + q / (int)gridDim.x;
-        ch = q % (int)gridDim.x;
+        const int id = bx + gx * by, q = id >> 3;
+        h = (id & 7) * (a.H >> 3) + q / gx;
+        ch = q % gx;
     }
     const int tid = threadIdx.x, c = tid & 7, g = tid >> 3;
     const int kvh = h / (a.H / a.Hkv);
@@ -756,6 +760,11 @@ __global__ __launch_bounds__(NT) void asplit_kernel(AttnArgs a, SplitBufs b) {
     a.out[(size_t)h * D + tid] = f2h(r);   // (one query row)
 }
 
+template <int D, int NT, bool XCH, int CH>
+__global__ __launch_bounds__(NT) void asplit_kernel(AttnArgs a, SplitBufs b) {
+    asplit_body<D, NT, XCH, CH>(a, b, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.x);
+}
+
 // The chunks of a head combined by a kernel of its own (the kernel boundary
 // orders the partials' stores before these loads): one workgroup per head,
 // thread d sums dim d over the chunks in chunk order.
@@ -840,6 +849,43 @@ tlhip_status launch_attention_split(hipStream_t s, const AttnArgs& a, float* scr
         return fail(TLHIP_ERR_INVALID_ARGUMENT, "attention: split decode path needs a device position, S = 1, D 64/80/128");
     SplitBufs b = {};
     return launch_split(s, a, b, scratch);
+}
+
+// Phi-2 decode: the key-chunked attention (in-kernel exchange) and fc1 in
+// one launch.  fc1 reads only the normalised row the QKV launch wrote, so
+// the two are independent, and in one grid the attention's chunk
+// workgroups -- waiting on their K / V rows and on each other's partials --
+// and fc1's weight-streaming workgroups share the device instead of running
+// one after the other.  Workgroups [0, nA) are the attention's (chunk slot
+// id % nch, head slot id / nch, the order of its own launch, so the same
+// XCD placement), the rest fc1's row blocks (8 waves x 4 rows of the flat
+// K = 2560 layout).  Same arithmetic as the two launches, so the same bits.
+template <int D, int CH, int WT, int NB, int RI, int FN>
+__global__ __launch_bounds__(512) void asplit_fc1_kernel(AttnArgs a, SplitBufs b, Gemv1Params p, int nA) {
+    const int id = (int)blockIdx.x;
+    if (id < nA) asplit_body<D, 512, true, CH>(a, b, id % b.nch, id / b.nch, b.nch);
+    else gemv_m1_body<WT, NB, RI, EPI_BIAS_GELU, FN, 8>(p, id - nA);
+}
+
+bool launch_attention_split_fc1(hipStream_t s, const AttnArgs& a, float* scratch, tlhip_dtype wt, const GemvArgs& f) {
+    if (!attention_split_ok(a) || !scratch || !a.head_flags || a.H > ATTN_SPLIT_MAX_HEADS) return false;
+    // the shapes of Phi-2's decode step: head dim 80 over at most
+    // AS_XCH_ROWS cache rows (128-key chunks, in-kernel exchange), fc1 a
+    // Q8_0 [N >= 8192, 2560] GEMV + bias + GELU on one row
+    if (a.D != 80 || a.kv_rows > AS_XCH_ROWS || wt != TLHIP_Q8_0 || f.M != 1 || f.K != 80 * 32 || f.N < 8192 ||
+        !f.bias || !f.x || !f.y)
+        return false;
+    SplitBufs b = {};
+    b.nch = (a.kv_rows + AS_CH - 1) / AS_CH;
+    b.mx = scratch;
+    b.sum = b.mx + (size_t)a.H * b.nch;
+    b.o = b.sum + (size_t)a.H * b.nch;
+    b.flags = a.head_flags;
+    const Gemv1Params p = {f.x, (const uint8_t*)f.wq, f.wd, f.bias, nullptr, f.y, f.N, f.K, EPI_BIAS_GELU};
+    const int nA = b.nch * a.H, nF = (f.N + 31) / 32;   // 8 waves x 4 rows per fc1 workgroup
+    hipLaunchKernelGGL((asplit_fc1_kernel<80, AS_CH, TLHIP_Q8_0, 2, 4, 80>), dim3((unsigned)(nA + nF)), dim3(512), 0, s,
+                       a, b, p, nA);
+    return true;
 }
 
 // One row over J keys; scratch holds attention_split_scratch(H, J, D) bytes.

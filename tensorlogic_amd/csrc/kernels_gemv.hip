@@ -357,6 +357,7 @@ static GemvParams make_params(const GemvArgs& a, int epi) {
     p.x_out = a.x_out;
     p.xn_out = a.xn_out;
     p.amax_slots = a.amax_slots;
+    p.x_add = a.x_add;
     return p;
 }
 

@@ -58,6 +58,34 @@ static bool launch_m1_epi_wt(hipStream_t s, const Gemv1Params& p, int nb, int ri
     }
 }
 
+// Two independent single-row GEMVs in one launch: workgroups [0, nA) run
+// the first (NBA blocks per lane pass, RIA rows per wave, epilogue EPA,
+// task layout FNA), the rest the second.  Phi-2's decode step pairs dense
+// [2560 x 2560] + bias + residual with fc2 [2560 x 10240] + bias: the two
+// read different rows (attention output, fc1 output), and the residual's
+// last addition (x + dense + fc2) is left to the next layer_norm prologue.
+template <int WT, int NBA, int RIA, int EPA, int FNA, int NBB, int RIB, int EPB, int FNB>
+__global__ __launch_bounds__(256) void gemv_m1_pair_kernel(Gemv1Params pa, Gemv1Params pb, int nA) {
+    const int id = (int)blockIdx.x;
+    if (id < nA) gemv_m1_body<WT, NBA, RIA, EPA, FNA, 4>(pa, id);
+    else gemv_m1_body<WT, NBB, RIB, EPB, FNB, 4>(pb, id - nA);
+}
+
+bool launch_m1_pair(hipStream_t s, tlhip_dtype wt, const GemvArgs& d, int epi_d, const GemvArgs& f, int epi_f) {
+    // the shapes it is built for: Q8_0, dense [N <= 8192, 2560] + bias + residual
+    // (flat layout, 2 rows per wave) and fc2 [N, 10240] + bias (5 passes,
+    // one row per wave), one activation row each
+    if (wt != TLHIP_Q8_0 || d.M != 1 || f.M != 1 || epi_d != EPI_BIAS_RESID || epi_f != EPI_BIAS) return false;
+    if (d.K != 80 * 32 || d.N < 1024 || d.N >= 8192 || !d.bias || !d.resid) return false;
+    if (f.K != 5 * 64 * 32 || f.N < 1024 || !f.bias) return false;
+    const Gemv1Params pa = {d.x, (const uint8_t*)d.wq, d.wd, d.bias, d.resid, d.y, d.N, d.K, EPI_BIAS_RESID};
+    const Gemv1Params pb = {f.x, (const uint8_t*)f.wq, f.wd, f.bias, nullptr, f.y, f.N, f.K, EPI_BIAS};
+    const int nA = (d.N + 7) / 8, nB = (f.N + 3) / 4;   // 4 waves x 2 rows / x 1 row
+    hipLaunchKernelGGL((gemv_m1_pair_kernel<TLHIP_Q8_0, 2, 2, EPI_BIAS_RESID, 80, 5, 1, EPI_BIAS, 0>),
+                       dim3((unsigned)(nA + nB)), dim3(256), 0, s, pa, pb, nA);
+    return true;
+}
+
 bool launch_m1_epi(hipStream_t s, tlhip_dtype wt, const Gemv1Params& p, int nb, int ri) {
     if (p.N < 1024) return false;
     switch (wt) {

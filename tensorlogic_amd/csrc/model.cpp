@@ -85,6 +85,9 @@ struct tlhip_model_s {
     uint64_t seed = 0;
     hipGraphExec_t gexec = nullptr;
     hipGraph_t graph = nullptr;
+    // phi2, one row: x + dense (x1) and fc2 + bias (mlp) of a layer whose
+    // dense and fc2 shared a launch; the next layer_norm prologue adds them
+    tlhip_tensor x1 = nullptr, mlp = nullptr;
 };
 
 namespace {
@@ -370,6 +373,10 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
         }
     };
     const int qkv_w = H + 2 * kvd;
+    // phi2, one row: after a layer whose dense and fc2 shared one launch the
+    // residual is x1 + mlp, added by the next layer_norm prologue (which
+    // writes the sum back to x for that layer's dense)
+    bool pending_add = false;
     for (int li = 0; li < m->n_layers; li++) {
         Layer& L = m->layers[li];
         uint16_t* kc = P(m->kv->k[li]);
@@ -379,6 +386,11 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
             // q / k rows were loaded in rotary-pair order
             GemvArgs a = fused_norm_args(m, L.qkv, P(m->x), L.norm_w, L.norm_b);
             embed_into(a, li);
+            if (pending_add) {
+                a.x = P(m->x1);
+                a.x_add = P(m->mlp);
+                a.x_out = P(m->x);
+            }
             a.nq = H;
             a.nk = kvd;
             a.head_dim = D;
@@ -443,10 +455,27 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
         at.kv_rows = m->max_ctx;
         at.scale_h = (float)(_Float16)(1.0f / sqrtf((float)D));
         at.head_flags = m->ctx->d_tile_flags + SK_MAX_TILES_SPLIT;
+        // phi2, decode: fc1 reads only the normalised row the QKV launch
+        // wrote, so it shares the attention's launch when the shapes allow
+        bool fc1_done = false;
         if (decode) {
             at.d_pos = d_pos;
-            if (m->d_asplit && attention_split_ok(at)) TLHIP_TRY(launch_attention_split(s, at, m->d_asplit));
-            else TLHIP_TRY(launch_attention(s, at));
+            if (m->arch == 1 && row1 && m->d_asplit) {
+                GemvArgs f;
+                f.x = P(m->xn);
+                f.wq = L.up.w->data;
+                f.wd = L.up.w->scales;
+                f.bias = L.up.b ? P(L.up.b) : nullptr;
+                f.y = P(m->hmid);
+                f.M = 1;
+                f.N = (int)L.up.w->shape[0];
+                f.K = (int)L.up.w->shape[1];
+                fc1_done = launch_attention_split_fc1(s, at, m->d_asplit, L.up.w->dtype, f);
+            }
+            if (!fc1_done) {
+                if (m->d_asplit && attention_split_ok(at)) TLHIP_TRY(launch_attention_split(s, at, m->d_asplit));
+                else TLHIP_TRY(launch_attention(s, at));
+            }
         } else {
             at.q_pos0 = pos0;
             if (attention_mfma_ok(at, pos0 + S)) TLHIP_TRY(launch_attention_mfma(s, at, pos0 + S, m->d_vt));
@@ -469,9 +498,36 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
             // phi2: the MLP reads the same layer_norm output as attention --
             // with one row, the one the QKV launch wrote (measured on MI355X:
             // fc1 [10240 x 2560] Q8_0 as its own normalised GEMV 8.67 us)
-            TLHIP_TRY(linear_into(s, L.up, P(m->xn), S, P(m->hmid), EPI_BIAS_GELU, nullptr, 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
-            TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
-            TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
+            if (!fc1_done)
+                TLHIP_TRY(linear_into(s, L.up, P(m->xn), S, P(m->hmid), EPI_BIAS_GELU, nullptr, 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
+            // one row: dense (x1 = x + dense + bias) and fc2 (mlp = fc2 + bias)
+            // in one launch; the reference's x + dense + mlp is then completed,
+            // with the same f16 roundings, by the next layer_norm prologue
+            bool paired = false;
+            if (row1 && m->x1 && m->mlp && L.o.b && L.down.b && L.o.w->dtype == L.down.w->dtype) {
+                GemvArgs d, f;
+                d.x = P(m->att);
+                d.wq = L.o.w->data;
+                d.wd = L.o.w->scales;
+                d.bias = P(L.o.b);
+                d.resid = P(m->x);
+                d.y = P(m->x1);
+                d.N = (int)L.o.w->shape[0];
+                d.K = (int)L.o.w->shape[1];
+                f.x = P(m->hmid);
+                f.wq = L.down.w->data;
+                f.wd = L.down.w->scales;
+                f.bias = P(L.down.b);
+                f.y = P(m->mlp);
+                f.N = (int)L.down.w->shape[0];
+                f.K = (int)L.down.w->shape[1];
+                paired = launch_m1_pair(s, L.o.w->dtype, d, EPI_BIAS_RESID, f, EPI_BIAS);
+            }
+            if (!paired) {
+                TLHIP_TRY(linear_into(s, L.o, P(m->att), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
+                TLHIP_TRY(linear_into(s, L.down, P(m->hmid), S, P(m->x), EPI_BIAS_RESID, P(m->x), 0, m->ws, m->ws_bytes, m->ctx->d_tile_flags));
+            }
+            pending_add = paired;
         }
     }
     const uint16_t* last = P(m->x) + (size_t)(S - 1) * H;
@@ -479,6 +535,10 @@ tlhip_status enqueue_forward(tlhip_model m, int S, int pos0, const int32_t* ids_
         // final norm + lm_head (+ bias) + per-workgroup greedy keys, then the
         // one-workgroup reduction that picks the token and advances d_state
         GemvArgs a = fused_norm_args(m, m->out, last, m->out_norm_w, m->out_norm_b);
+        if (pending_add) {   // (one row)
+            a.x = P(m->x1);
+            a.x_add = P(m->mlp);
+        }
         a.y = P(m->logits);
         a.amax_slots = m->d_amax;
         TLHIP_TRY(launch_gemv(s, m->out.w->dtype, a, EPI_ARGMAX));
@@ -735,7 +795,7 @@ tlhip_status tlhip_model_free(tlhip_model m) try {
     tlhip_tensor_free(m->out_norm_b);
     free_lin(m->out);
     tlhip_kvcache_free(m->kv);
-    for (tlhip_tensor t : {m->x, m->xn, m->qkv, m->qrot, m->att, m->hmid, m->logits}) tlhip_tensor_free(t);
+    for (tlhip_tensor t : {m->x, m->xn, m->qkv, m->qrot, m->att, m->hmid, m->logits, m->x1, m->mlp}) tlhip_tensor_free(t);
     if (m->d_amax) (void)hipFree(m->d_amax);
     if (m->d_vt) (void)hipFree(m->d_vt);
     if (m->d_asplit) (void)hipFree(m->d_asplit);
@@ -851,6 +911,11 @@ tlhip_status tlhip_model_load(tlhip_ctx ctx, const char* path, int arch, int max
         if ((st = alloc_tensor(ctx, TLHIP_F16, 2, s_x, &m->att)) != TLHIP_OK) break;
         if ((st = alloc_tensor(ctx, TLHIP_F16, 2, s_h, &m->hmid)) != TLHIP_OK) break;
         if ((st = alloc_tensor(ctx, TLHIP_F16, 1, s_l, &m->logits)) != TLHIP_OK) break;
+        if (arch == 1) {
+            const int64_t s_r[2] = {1, H};
+            if ((st = alloc_tensor(ctx, TLHIP_F16, 2, s_r, &m->x1)) != TLHIP_OK) break;
+            if ((st = alloc_tensor(ctx, TLHIP_F16, 2, s_r, &m->mlp)) != TLHIP_OK) break;
+        }
         hipError_t e = hipMalloc(&m->d_state, 4 * sizeof(int32_t));
         if (e == hipSuccess) e = hipMalloc(&m->d_amax, sizeof(unsigned long long) * gemv_norm_slots(m->vocab));
         if (e == hipSuccess) e = hipMalloc(&m->d_vt, attention_mfma_scratch(m->max_ctx, m->n_kv, m->head_dim));
