@@ -193,9 +193,11 @@ def _last_logits(g):
     return np.array(g["last_logits"], np.float16)
 
 
-def _teacher_forced(dev, path, arch, g, max_ctx):
+def _teacher_forced(dev, path, arch, g, max_ctx, check_direct=False):
     """Decodes the oracle's own token stream on the device and checks every
-    step (see test_tinyllama_full_golden_tokens); returns the near-tie steps."""
+    step (see test_tinyllama_full_golden_tokens); returns the near-tie steps.
+    check_direct: the free-running stream from kernels launched one by one
+    must equal the graph-replayed one."""
     prompt = np.array(g["prompt"], np.int32)
     ref = np.array(g["tokens"], np.int32)
     margins = np.array(g["margins"], np.float64)
@@ -227,6 +229,9 @@ def _teacher_forced(dev, path, arch, g, max_ctx):
     first = exempt[0] if exempt else n + 1
     bad = np.nonzero(toks[:first] != ref[:first])[0]
     assert bad.size == 0, f"free-running stream differs at step {bad[0]} before the first near-tie ({first})"
+    if check_direct:
+        direct = m.generate(prompt, n, use_graph=False)
+        assert np.array_equal(direct, toks), "direct launches and graph replay give different streams"
     m.close()
     return exempt
 
@@ -256,11 +261,13 @@ def test_phi2_full_golden_tokens(dev, tmp_path):
     """Phi-2 shape (2.7B), Q8_0, 512-token prompt, 256 greedy steps (config 5):
     the same teacher-forced check, through MFMA prefill of 512 rows and the
     fused decode path (LayerNorm + fused QKV + half-rotation partial RoPE +
-    parallel GELU MLP)."""
+    parallel GELU MLP; at these shapes attention shares a grid with fc1 and
+    dense with fc2, the residual's last addition made by the next layer_norm
+    prologue), and the same stream from graph replay and direct launches."""
     g = _golden("phi2_q8_0_tokens.json")
     path = str(tmp_path / "phi2.gguf")
     S.write_phi2_gguf(path, seed=g["seed"], **S.PHI2_ARGS)
-    _teacher_forced(dev, path, 1, g, 800)
+    _teacher_forced(dev, path, 1, g, 800, check_direct=True)
 
 
 def test_tinyllama_margins_free_running(dev, tmp_path):
