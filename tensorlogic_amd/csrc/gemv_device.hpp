@@ -95,6 +95,10 @@ struct GemvParams {
 // and returns zeros past it.
 constexpr int BUF_RSRC_WORD3 = 0x00020000;
 
+// Cache-policy bits of a load: the instruction's nt (non-temporal) bit on
+// gfx950.
+constexpr int CP_STREAM = 2;
+
 // 0 in a VGPR the compiler cannot see through: indexing a uniform address
 // with it makes the load a vector load (in-order completion) instead of a
 // scalar one.
@@ -387,6 +391,23 @@ template <int WT> struct BlkLoads {
     static constexpr int n = WT == TLHIP_Q4_0 ? 1 : (WT == TLHIP_Q8_0 || WT == TLHIP_Q6_K ? 2 : 4);
 };
 
+// Cache policy of the one-row GEMVs' weight loads.  Q4_0 rows are read
+// non-temporally: each is read once per pass, and one load instruction
+// covers whole 128-byte lines (16 bytes per lane, consecutive lanes).
+// Measured on MI355X (A/B of library builds on one box, same tokens):
+// config-4 decode under graph replay 1985 -> 2181 tok/s; under the
+// profiler's serialised launches the GEMV durations are unchanged and the
+// decode attention, whose K/V rows then stay cached, 5.05 -> 4.60 us per
+// layer, so most of the gain is at the kernel boundaries.  The Q4_0 [5632
+// x 2048] GEMV alone over 48 rotating weight copies is unchanged (3.52 vs
+// 3.51 us).  Q8_0, f16 and Q6_K keep plain loads: a Q8_0 block is two
+// 16-byte loads per lane 32 bytes apart, so each instruction covers half
+// of every line and the second relies on the line the first brought into
+// L2; non-temporal, Phi-2 decode lost 1050 -> 1002 tok/s (dense + fc2
+// 8.66 -> 9.48 us per launch).
+template <int WT>
+constexpr int weight_cp() { return WT == TLHIP_Q4_0 ? CP_STREAM : 0; }
+
 template <int WT>
 __device__ __forceinline__ float block_dot(const u4* q, uint32_t dbits, const uint32_t xc[16], float acc) {
     if (WT == TLHIP_Q4_0) {
@@ -552,9 +573,10 @@ __device__ __forceinline__ void load_rows(const GemvParams& p, int row0, int lan
 // What this saves is the per-lane 64-bit address arithmetic load_rows
 // issues before its first weight load; on MI355X that delay, repeated for
 // every wave a SIMD holds, cost 0.2-0.3 us of a 4 us GEMV.
-template <int WT, int NB, int RI>
-__device__ __forceinline__ void load_rows_buf(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
-                                              u4 (&q)[RI][NB][BlkLoads<WT>::n], uint32_t (&ds)[RI][NB]) {
+// AUX: the loads' cache-policy bits (weight_cp).
+template <int WT, int NB, int RI, int AUX>
+__device__ __forceinline__ void load_rows_buf_cp(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
+                                                 u4 (&q)[RI][NB][BlkLoads<WT>::n], uint32_t (&ds)[RI][NB]) {
     constexpr int NL = BlkLoads<WT>::n;
     const int nbr = K >> 5;
     if (WT == TLHIP_Q6_K) {
@@ -592,10 +614,16 @@ __device__ __forceinline__ void load_rows_buf(const uint8_t* wq, const uint16_t*
             const int b = lane + 64 * i;
 #pragma unroll
             for (int l = 0; l < NL; l++)
-                q[ri][i][l] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rq, b * (16 * NL) + 16 * l, 0, 0));
-            ds[ri][i] = WT == TLHIP_F16 ? 0u : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rd, b * 2, 0, 0);
+                q[ri][i][l] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rq, b * (16 * NL) + 16 * l, 0, AUX));
+            ds[ri][i] = WT == TLHIP_F16 ? 0u : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rd, b * 2, 0, AUX);
         }
     }
+}
+
+template <int WT, int NB, int RI>
+__device__ __forceinline__ void load_rows_buf(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
+                                              u4 (&q)[RI][NB][BlkLoads<WT>::n], uint32_t (&ds)[RI][NB]) {
+    load_rows_buf_cp<WT, NB, RI, weight_cp<WT>()>(wq, wd, N, K, row0, lane, q, ds);
 }
 
 // Lane 0's bias / residual elements of the wave's rows, loaded right after
@@ -787,10 +815,10 @@ struct Flat {
 // Loads of the wave's flat task stream, all issued before any use, through
 // range-checked buffer loads over the rows that exist (a task past them, or
 // every task of a wave past N, reads a zero weight with no memory request).
-template <int WT, int FN, int RI>
-__device__ __forceinline__ void load_flat(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
-                                          u4 (&q)[Flat<FN, RI>::IT][BlkLoads<WT>::n],
-                                          uint32_t (&ds)[Flat<FN, RI>::IT]) {
+template <int WT, int FN, int RI, int AUX>
+__device__ __forceinline__ void load_flat_cp(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
+                                             u4 (&q)[Flat<FN, RI>::IT][BlkLoads<WT>::n],
+                                             uint32_t (&ds)[Flat<FN, RI>::IT]) {
     constexpr int NL = BlkLoads<WT>::n, IT = Flat<FN, RI>::IT;
     const int row_bytes = WT == TLHIP_Q4_0 ? K / 2 : (WT == TLHIP_Q8_0 ? K : K * 2);
     const int rows = row0 < N ? min(RI, N - row0) : 0;
@@ -804,9 +832,16 @@ __device__ __forceinline__ void load_flat(const uint8_t* wq, const uint16_t* wd,
         const int gb = lane + 64 * i;
 #pragma unroll
         for (int l = 0; l < NL; l++)
-            q[i][l] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rq, gb * (16 * NL) + 16 * l, 0, 0));
-        ds[i] = WT == TLHIP_F16 ? 0u : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rd, gb * 2, 0, 0);
+            q[i][l] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rq, gb * (16 * NL) + 16 * l, 0, AUX));
+        ds[i] = WT == TLHIP_F16 ? 0u : (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rd, gb * 2, 0, AUX);
     }
+}
+
+template <int WT, int FN, int RI>
+__device__ __forceinline__ void load_flat(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
+                                          u4 (&q)[Flat<FN, RI>::IT][BlkLoads<WT>::n],
+                                          uint32_t (&ds)[Flat<FN, RI>::IT]) {
+    load_flat_cp<WT, FN, RI, weight_cp<WT>()>(wq, wd, N, K, row0, lane, q, ds);
 }
 
 // The block dots of the flat task stream into the RI row sums; CH(b, xc)
