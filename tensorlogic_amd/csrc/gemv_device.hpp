@@ -236,6 +236,50 @@ __device__ __forceinline__ u4 pack_quad(const float f[8]) {
     return u4{pack_lo(w[0], w[1]), pack_hi(w[0], w[1]), pack_lo(w[2], w[3]), pack_hi(w[2], w[3])};
 }
 
+// Q8_0 in the one-row GEMVs (load_rows_buf, load_flat and their dots): a
+// lane's two 16-byte words are halves of two blocks, so that each load
+// instruction reads 1 KB of consecutive bytes -- whole 128-byte lines -- and
+// can be non-temporal.  Word l of pass i holds half (lane & 1) of block
+// 64 i + 32 l + (lane >> 1) of the lane's row (or flat task stream), i.e.
+// bytes 16 * (128 i + 64 l + lane) of it; each word has its own scale.
+// (With both halves of block lane + 64 i in one lane, each instruction
+// covers every other 16 bytes and the second relies on the line the first
+// brought into L2, which a non-temporal load does not keep.)
+template <int WT>
+constexpr bool half_slots() { return WT == TLHIP_Q8_0; }
+template <int WT>
+constexpr int ds_per() { return half_slots<WT>() ? 2 : 1; }
+// Block of word l of pass i (half_slots) in a lane's row or task stream.
+__device__ __forceinline__ int half_block(int i, int l, int lane) { return 64 * i + 32 * l + (lane >> 1); }
+
+// Index into the activation staging (u4 xs[4][NB * 64], taken flat) of quad v
+// of block b: quad-major (xs[v][b]; lane l's reads of block l are
+// consecutive 16-byte words) or, for half_slots, block-major (lane pairs
+// read the two halves of one block: consecutive 32-byte pieces).
+template <int WT, int NB>
+__device__ __forceinline__ int xs_at(int b, int v) { return half_slots<WT>() ? b * 4 + v : v * (NB * 64) + b; }
+
+// The staged activation chunks of a block (16 pairs in the pair order of
+// WT's unpacking) or of half of one (pairs 8h .. 8h + 7).
+template <int WT, int NB>
+struct XsChunk {
+    const u4* xs;
+    __device__ __forceinline__ void operator()(int b, uint32_t (&xc)[16]) const {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const u4 t = xs[xs_at<WT, NB>(b, v)];
+            xc[4 * v] = t[0]; xc[4 * v + 1] = t[1]; xc[4 * v + 2] = t[2]; xc[4 * v + 3] = t[3];
+        }
+    }
+    __device__ __forceinline__ void half(int b, int h, uint32_t (&xc)[8]) const {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const u4 t = xs[xs_at<WT, NB>(b, 2 * h + j)];
+            xc[4 * j] = t[0]; xc[4 * j + 1] = t[1]; xc[4 * j + 2] = t[2]; xc[4 * j + 3] = t[3];
+        }
+    }
+};
+
 template <int WT, int NB, int WPB, int PRO>
 struct NormStage {
     static constexpr int NT = WPB * 64;
@@ -360,7 +404,7 @@ struct NormStage {
 #pragma unroll
             for (int e = 0; e < 8; e++)
                 f[k][e] = PRO == PRO_RMS ? (f[k][e] * inv) * w[e] : (((f[k][e] - mean) * inv) * w[e]) + bb[e];
-            xs[v][b] = pack_quad<WT>(f[k]);
+            (&xs[0][0])[xs_at<WT, NB>(b, v)] = pack_quad<WT>(f[k]);
             if (p.xn_out)   // (the same f16 values the dot products read)
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
@@ -373,14 +417,6 @@ struct NormStage {
         lds_barrier();
     }
 
-    // Block b's 16 normalised pairs, already in the pair order of WT's unpacking.
-    __device__ __forceinline__ static void chunk(const u4 (*xs)[NB * 64], int b, uint32_t xc[16]) {
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const u4 t = xs[v][b];
-            xc[4 * v] = t[0]; xc[4 * v + 1] = t[1]; xc[4 * v + 2] = t[2]; xc[4 * v + 3] = t[3];
-        }
-    }
 };
 
 // Weight payload of one 32-element block: Q4_0 1 x 16 B, Q8_0 2 x 16 B, F16 4 x 16 B.
@@ -391,22 +427,21 @@ template <int WT> struct BlkLoads {
     static constexpr int n = WT == TLHIP_Q4_0 ? 1 : (WT == TLHIP_Q8_0 || WT == TLHIP_Q6_K ? 2 : 4);
 };
 
-// Cache policy of the one-row GEMVs' weight loads.  Q4_0 rows are read
-// non-temporally: each is read once per pass, and one load instruction
-// covers whole 128-byte lines (16 bytes per lane, consecutive lanes).
-// Measured on MI355X (A/B of library builds on one box, same tokens):
-// config-4 decode under graph replay 1985 -> 2181 tok/s; under the
-// profiler's serialised launches the GEMV durations are unchanged and the
-// decode attention, whose K/V rows then stay cached, 5.05 -> 4.60 us per
-// layer, so most of the gain is at the kernel boundaries.  The Q4_0 [5632
-// x 2048] GEMV alone over 48 rotating weight copies is unchanged (3.52 vs
-// 3.51 us).  Q8_0, f16 and Q6_K keep plain loads: a Q8_0 block is two
-// 16-byte loads per lane 32 bytes apart, so each instruction covers half
-// of every line and the second relies on the line the first brought into
-// L2; non-temporal, Phi-2 decode lost 1050 -> 1002 tok/s (dense + fc2
-// 8.66 -> 9.48 us per launch).
+// Cache policy of the one-row GEMVs' weight loads.  Q4_0 and Q8_0 rows are
+// read non-temporally: each is read once per pass, and every load
+// instruction covers whole 128-byte lines (16 bytes per lane, consecutive
+// lanes; Q8_0 through half_slots).  Measured on MI355X (A/B of library
+// builds on one box, same tokens): config-4 decode under graph replay
+// 1985 -> 2181 tok/s; under the profiler's serialised launches the GEMV
+// durations are unchanged and the decode attention 5.05 -> 4.60 us per
+// layer, so most of the gain is at the kernel boundaries; the Q4_0
+// [5632 x 2048] GEMV alone over 48 rotating weight copies is unchanged
+// (3.52 vs 3.51 us).  Phi-2 (Q8_0) decode 1065 -> 1114 tok/s with
+// half_slots; with Q8_0's earlier layout (both words of a block in one
+// lane, each instruction covering every other 16 bytes) non-temporal loads
+// lost 1050 -> 1002 tok/s.  f16 and Q6_K keep plain loads.
 template <int WT>
-constexpr int weight_cp() { return WT == TLHIP_Q4_0 ? CP_STREAM : 0; }
+constexpr int weight_cp() { return WT == TLHIP_Q4_0 || WT == TLHIP_Q8_0 ? CP_STREAM : 0; }
 
 template <int WT>
 __device__ __forceinline__ float block_dot(const u4* q, uint32_t dbits, const uint32_t xc[16], float acc) {
@@ -449,6 +484,22 @@ __device__ __forceinline__ float block_dot(const u4* q, uint32_t dbits, const ui
         for (int v = 0; v < 4; v++)
 #pragma unroll
             for (int t = 0; t < 4; t++) acc = fdot2(as_h2(q[v][t]), as_h2(xc[4 * v + t]), acc);
+    }
+    return acc;
+}
+
+// Q8_0 half block: 16 int8 (one 16-byte word) against pairs 8h .. 8h + 7 of
+// the block's activation chunk -- block_dot's arithmetic for one of its two
+// words.
+__device__ __forceinline__ float q8_half_dot(const u4& q, uint32_t dbits, const uint32_t xc[8], float acc) {
+    h16 dh = __builtin_bit_cast(h16, (uint16_t)dbits);
+    h2 dd = {dh, dh};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        h2 r[2];
+        q8_unpack(q[t], dd, r);
+        acc = fdot2(r[0], as_h2(xc[2 * t + 0]), acc);
+        acc = fdot2(r[1], as_h2(xc[2 * t + 1]), acc);
     }
     return acc;
 }
@@ -576,7 +627,7 @@ __device__ __forceinline__ void load_rows(const GemvParams& p, int row0, int lan
 // AUX: the loads' cache-policy bits (weight_cp).
 template <int WT, int NB, int RI, int AUX>
 __device__ __forceinline__ void load_rows_buf_cp(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
-                                                 u4 (&q)[RI][NB][BlkLoads<WT>::n], uint32_t (&ds)[RI][NB]) {
+                                                 u4 (&q)[RI][NB][BlkLoads<WT>::n], uint32_t (&ds)[RI][NB * ds_per<WT>()]) {
     constexpr int NL = BlkLoads<WT>::n;
     const int nbr = K >> 5;
     if (WT == TLHIP_Q6_K) {
@@ -611,6 +662,14 @@ __device__ __forceinline__ void load_rows_buf_cp(const uint8_t* wq, const uint16
                                                                             WT == TLHIP_F16 ? 0 : nbr * 2, BUF_RSRC_WORD3);
 #pragma unroll
         for (int i = 0; i < NB; i++) {
+            if constexpr (half_slots<WT>()) {
+#pragma unroll
+                for (int l = 0; l < 2; l++) {
+                    q[ri][i][l] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rq, 16 * (128 * i + 64 * l + lane), 0, AUX));
+                    ds[ri][2 * i + l] = __builtin_amdgcn_raw_buffer_load_b16(rd, half_block(i, l, lane) * 2, 0, AUX);
+                }
+                continue;
+            }
             const int b = lane + 64 * i;
 #pragma unroll
             for (int l = 0; l < NL; l++)
@@ -622,7 +681,7 @@ __device__ __forceinline__ void load_rows_buf_cp(const uint8_t* wq, const uint16
 
 template <int WT, int NB, int RI>
 __device__ __forceinline__ void load_rows_buf(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
-                                              u4 (&q)[RI][NB][BlkLoads<WT>::n], uint32_t (&ds)[RI][NB]) {
+                                              u4 (&q)[RI][NB][BlkLoads<WT>::n], uint32_t (&ds)[RI][NB * ds_per<WT>()]) {
     load_rows_buf_cp<WT, NB, RI, weight_cp<WT>()>(wq, wd, N, K, row0, lane, q, ds);
 }
 
@@ -818,7 +877,7 @@ struct Flat {
 template <int WT, int FN, int RI, int AUX>
 __device__ __forceinline__ void load_flat_cp(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
                                              u4 (&q)[Flat<FN, RI>::IT][BlkLoads<WT>::n],
-                                             uint32_t (&ds)[Flat<FN, RI>::IT]) {
+                                             uint32_t (&ds)[Flat<FN, RI>::IT * ds_per<WT>()]) {
     constexpr int NL = BlkLoads<WT>::n, IT = Flat<FN, RI>::IT;
     const int row_bytes = WT == TLHIP_Q4_0 ? K / 2 : (WT == TLHIP_Q8_0 ? K : K * 2);
     const int rows = row0 < N ? min(RI, N - row0) : 0;
@@ -829,6 +888,14 @@ __device__ __forceinline__ void load_flat_cp(const uint8_t* wq, const uint16_t* 
                                                                         WT == TLHIP_F16 ? 0 : rows * FN * 2, BUF_RSRC_WORD3);
 #pragma unroll
     for (int i = 0; i < IT; i++) {
+        if constexpr (half_slots<WT>()) {
+#pragma unroll
+            for (int l = 0; l < 2; l++) {
+                q[i][l] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(rq, 16 * (128 * i + 64 * l + lane), 0, AUX));
+                ds[2 * i + l] = __builtin_amdgcn_raw_buffer_load_b16(rd, half_block(i, l, lane) * 2, 0, AUX);
+            }
+            continue;
+        }
         const int gb = lane + 64 * i;
 #pragma unroll
         for (int l = 0; l < NL; l++)
@@ -840,17 +907,44 @@ __device__ __forceinline__ void load_flat_cp(const uint8_t* wq, const uint16_t* 
 template <int WT, int FN, int RI>
 __device__ __forceinline__ void load_flat(const uint8_t* wq, const uint16_t* wd, int N, int K, int row0, int lane,
                                           u4 (&q)[Flat<FN, RI>::IT][BlkLoads<WT>::n],
-                                          uint32_t (&ds)[Flat<FN, RI>::IT]) {
+                                          uint32_t (&ds)[Flat<FN, RI>::IT * ds_per<WT>()]) {
     load_flat_cp<WT, FN, RI, weight_cp<WT>()>(wq, wd, N, K, row0, lane, q, ds);
 }
 
+// Half-block words (half_slots) of pass I, word L, into the row sums.
+template <int WT, int FN, int RI, int I, int L, typename CH>
+__device__ __forceinline__ void dot_flat_half(const u4& q, uint32_t d, const CH& chunk, int lane, float (&acc)[RI]) {
+    const int gb = half_block(I, L, lane);
+    const int r = gb / FN;
+    uint32_t xc[8];
+    chunk.half(gb - r * FN, lane & 1, xc);
+    constexpr int rlo = (64 * I + 32 * L) / FN;
+    constexpr int rhi = (64 * I + 32 * L + 31) / FN < RI ? (64 * I + 32 * L + 31) / FN : RI - 1;
+    if constexpr (rlo >= RI) {
+        return;   // (every block of the word is past the stream: zero weights)
+    } else if constexpr (rlo == rhi) {
+        acc[rlo] = q8_half_dot(q, d, xc, acc[rlo]);
+    } else {
+        const bool lo = gb < (rlo + 1) * FN;
+        float c = lo ? acc[rlo] : acc[rhi];
+        c = q8_half_dot(q, d, xc, c);
+        acc[rlo] = lo ? c : acc[rlo];
+        acc[rhi] = lo ? acc[rhi] : c;
+    }
+}
+
 // The block dots of the flat task stream into the RI row sums; CH(b, xc)
-// fetches block b's activation chunk in the pair order of WT's unpacking.
+// fetches block b's activation chunk in the pair order of WT's unpacking
+// (CH.half(b, h, xc): its pairs 8h .. 8h + 7, for half_slots).
 template <int WT, int FN, int RI, int I = 0, typename CH>
 __device__ __forceinline__ void dot_flat(const u4 (&q)[Flat<FN, RI>::IT][BlkLoads<WT>::n],
-                                         const uint32_t (&ds)[Flat<FN, RI>::IT], const CH& chunk, int lane,
-                                         float (&acc)[RI]) {
-    if constexpr (I < Flat<FN, RI>::IT) {
+                                         const uint32_t (&ds)[Flat<FN, RI>::IT * ds_per<WT>()], const CH& chunk,
+                                         int lane, float (&acc)[RI]) {
+    if constexpr (I < Flat<FN, RI>::IT && half_slots<WT>()) {
+        dot_flat_half<WT, FN, RI, I, 0>(q[I][0], ds[2 * I], chunk, lane, acc);
+        dot_flat_half<WT, FN, RI, I, 1>(q[I][1], ds[2 * I + 1], chunk, lane, acc);
+        dot_flat<WT, FN, RI, I + 1>(q, ds, chunk, lane, acc);
+    } else if constexpr (I < Flat<FN, RI>::IT) {
         const int gb = lane + 64 * I;
         const int r = gb / FN;
         uint32_t xc[16];
@@ -919,9 +1013,9 @@ __device__ __forceinline__ void gemv_m1_body(const Gemv1Params& p, int bx) {
     __builtin_amdgcn_sched_barrier(0);   // the activation loads go out first
     constexpr int FIT = FN > 0 ? Flat<(FN > 0 ? FN : 64), RI>::IT : 1;
     u4 q[RI][NB][NL];
-    uint32_t ds[RI][NB];
+    uint32_t ds[RI][NB * ds_per<WT>()];
     u4 qf[FIT][NL];
-    uint32_t dsf[FIT];
+    uint32_t dsf[FIT * ds_per<WT>()];
     if constexpr (FN > 0) load_flat<WT, FN, RI>(p.wq, p.wd, p.N, p.K, row0, lane, qf, dsf);
     else load_rows_buf<WT, NB, RI>(p.wq, p.wd, p.N, p.K, row0, lane, q, ds);
     // the epilogue's f16 operands: one per row, the same address in every
@@ -956,23 +1050,28 @@ __device__ __forceinline__ void gemv_m1_body(const Gemv1Params& p, int bx) {
         const int it = threadIdx.x + NT * k;
         const uint32_t* w = xw[k];
         if (NT * NSX == NB * 256 || it < NB * 256)   // (the staging row holds NB * 256 quads)
-            xs[it & 3][it >> 2] = WT == TLHIP_F16 ? u4{w[0], w[1], w[2], w[3]}
-                                                  : u4{pack_lo(w[0], w[1]), pack_hi(w[0], w[1]), pack_lo(w[2], w[3]), pack_hi(w[2], w[3])};
+            (&xs[0][0])[xs_at<WT, NB>(it >> 2, it & 3)] =
+                WT == TLHIP_F16 ? u4{w[0], w[1], w[2], w[3]}
+                                : u4{pack_lo(w[0], w[1]), pack_hi(w[0], w[1]), pack_lo(w[2], w[3]), pack_hi(w[2], w[3])};
     }
     lds_barrier();
     if (row0 >= p.N) return;   // (uniform: only the last workgroup has idle waves)
     float acc[RI];
 #pragma unroll
     for (int ri = 0; ri < RI; ri++) acc[ri] = 0.0f;
-    auto chunk = [&](int b, uint32_t (&xc)[16]) {
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const u4 t = xs[v][b];
-            xc[4 * v] = t[0]; xc[4 * v + 1] = t[1]; xc[4 * v + 2] = t[2]; xc[4 * v + 3] = t[3];
-        }
-    };
+    const XsChunk<WT, NB> chunk{&xs[0][0]};
     if constexpr (FN > 0) {
         dot_flat<WT, FN, RI>(qf, dsf, chunk, lane, acc);
+    } else if constexpr (half_slots<WT>()) {
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+#pragma unroll
+            for (int l = 0; l < 2; l++) {
+                uint32_t xc[8];
+                chunk.half(half_block(i, l, lane), lane & 1, xc);
+#pragma unroll
+                for (int ri = 0; ri < RI; ri++) acc[ri] = q8_half_dot(q[ri][i][l], ds[ri][2 * i + l], xc, acc[ri]);
+            }
     } else {
 #pragma unroll
         for (int i = 0; i < NB; i++) {
@@ -1070,7 +1169,7 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
     const int nbr = p.K >> 5;
     constexpr int NL = BlkLoads<WT>::n;
     u4 q[RI][NB][NL];
-    uint32_t ds[RI][NB];   // scales zero-extended: no packing that would force an early wait
+    uint32_t ds[RI][NB * ds_per<WT>()];   // scales zero-extended: no packing that would force an early wait
     // The decode position (only lane 0's RoPE table loads depend on it) is
     // read first, as a vector load: those retire in order, so waiting for it
     // later does not wait for the activation and weight loads issued after
@@ -1093,7 +1192,7 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
     // branch leave the compiler's wait counts imprecise after it)
     constexpr int FIT = FN > 0 ? Flat<(FN > 0 ? FN : 64), RI>::IT : 1;
     u4 qf[FIT][NL];
-    uint32_t dsf[FIT];
+    uint32_t dsf[FIT * ds_per<WT>()];
     if constexpr (FN > 0) load_flat<WT, FN, RI>(p.wq, p.wd, p.N, p.K, row0, lane, qf, dsf);
     else load_rows_buf<WT, NB, RI>(p.wq, p.wd, p.N, p.K, row0, lane, q, ds);
     EpiPre<RI, 1> pre;
@@ -1112,6 +1211,7 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
         if (p.resid) er1 = p.resid[row0 + lane];
     }
     st.finish(p, xs, red);
+    const XsChunk<WT, NB> chunk{&xs[0][0]};
 
     float acc[RI][1];
 #pragma unroll
@@ -1121,17 +1221,29 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
             float af[RI];
 #pragma unroll
             for (int ri = 0; ri < RI; ri++) af[ri] = 0.0f;
-            auto chunk = [&](int b, uint32_t (&xc)[16]) { NormStage<WT, NB, WPB, PRO>::chunk(xs, b, xc); };
             dot_flat<WT, FN, RI>(qf, dsf, chunk, lane, af);
 #pragma unroll
             for (int ri = 0; ri < RI; ri++) acc[ri][0] = af[ri];
+        } else if constexpr (half_slots<WT>()) {
+#pragma unroll
+            for (int i = 0; i < NB; i++)
+#pragma unroll
+                for (int l = 0; l < 2; l++) {
+                    const int b = half_block(i, l, lane);
+                    if (b < nbr) {
+                        uint32_t xc[8];
+                        chunk.half(b, lane & 1, xc);
+#pragma unroll
+                        for (int ri = 0; ri < RI; ri++) acc[ri][0] = q8_half_dot(q[ri][i][l], ds[ri][2 * i + l], xc, acc[ri][0]);
+                    }
+                }
         } else {
 #pragma unroll
             for (int i = 0; i < NB; i++) {
                 const int b = lane + 64 * i;
                 if (b < nbr) {
                     uint32_t xc[16];
-                    NormStage<WT, NB, WPB, PRO>::chunk(xs, b, xc);
+                    chunk(b, xc);
 #pragma unroll
                     for (int ri = 0; ri < RI; ri++) acc[ri][0] = block_dot<WT>(q[ri][i], ds[ri][i], xc, acc[ri][0]);
                 }
