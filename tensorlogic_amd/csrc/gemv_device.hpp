@@ -439,9 +439,11 @@ template <int WT> struct BlkLoads {
 // (3.52 vs 3.51 us).  Phi-2 (Q8_0) decode 1065 -> 1114 tok/s with
 // half_slots; with Q8_0's earlier layout (both words of a block in one
 // lane, each instruction covering every other 16 bytes) non-temporal loads
-// lost 1050 -> 1002 tok/s.  f16 and Q6_K keep plain loads.
+// lost 1050 -> 1002 tok/s.  Q6_K's planes are read the same way (16, 8
+// and 2 bytes per lane, consecutive lanes).  f16 rows (64 bytes per lane)
+// keep plain loads.
 template <int WT>
-constexpr int weight_cp() { return WT == TLHIP_Q4_0 || WT == TLHIP_Q8_0 ? CP_STREAM : 0; }
+constexpr int weight_cp() { return WT == TLHIP_F16 ? 0 : CP_STREAM; }
 
 template <int WT>
 __device__ __forceinline__ float block_dot(const u4* q, uint32_t dbits, const uint32_t xc[16], float acc) {
@@ -643,10 +645,10 @@ __device__ __forceinline__ void load_rows_buf_cp(const uint8_t* wq, const uint16
 #pragma unroll
             for (int i = 0; i < NB; i++) {
                 const int b = lane + 64 * i;
-                q[ri][i][0] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r4, b * 16, 0, 0));
-                const uint2 h = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r2, b * 8, 0, 0));
-                const uint32_t s2 = __builtin_amdgcn_raw_buffer_load_b16(rs, b * 2, 0, 0);
-                const uint32_t dv = __builtin_amdgcn_raw_buffer_load_b16(rd, (b >> 3) * 2, 0, 0);
+                q[ri][i][0] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r4, b * 16, 0, AUX));
+                const uint2 h = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r2, b * 8, 0, AUX));
+                const uint32_t s2 = __builtin_amdgcn_raw_buffer_load_b16(rs, b * 2, 0, AUX);
+                const uint32_t dv = __builtin_amdgcn_raw_buffer_load_b16(rd, (b >> 3) * 2, 0, AUX);
                 q[ri][i][1] = u4{h.x, h.y, s2 | (dv << 16), 0u};
                 ds[ri][i] = 0u;
             }

@@ -32,13 +32,20 @@ static bool launch_m1_epi_nb(hipStream_t s, const Gemv1Params& p) {
     }
 }
 
-// Two rows per wave up to two 64-block passes per row, one row per wave
-// beyond (the shapes launch_m1 picks for M = 1 from 1024 rows).
+// Two rows per wave up to two 64-block passes per row (Q4_0 from 32768 rows:
+// four), one row per wave beyond (the shapes launch_m1 picks for M = 1 from
+// 1024 rows).  Q4_0, K = 2048, cold weights, measured on MI355X: 65536 rows
+// 14.1-14.4 us with four rows per wave against 14.7-14.8 with two (eight
+// waves per workgroup: 15.3-15.4 with two rows, 14.4-14.7 with four),
+// 32768 rows 8.4-8.5 against 8.8.
 template <int WT>
 static bool launch_m1_epi_wt(hipStream_t s, const Gemv1Params& p, int nb, int ri) {
     if (ri == 2) {
         switch (nb) {
-            case 1: return launch_m1_epi_nb<WT, 1, 2>(s, p);
+            case 1:
+                if constexpr (WT == TLHIP_Q4_0)
+                    if (p.N >= 32768) return launch_m1_epi_nb<WT, 1, 4>(s, p);
+                return launch_m1_epi_nb<WT, 1, 2>(s, p);
             case 2:
                 // 80 blocks per row (K = 2560): the flat task layout, 4 rows per
                 // wave from 8192 rows, 2 below (enough waves to fill the device)

@@ -168,7 +168,7 @@ def test_dequant_reference_known_answers(dev):
 @pytest.mark.parametrize("qt", [Q4_0, Q8_0])
 @pytest.mark.parametrize("M,N,K", [(1, 2048, 2048), (1, 5632, 2048), (1, 2048, 5632), (2, 256, 2048),
                                    (3, 512, 1024), (4, 1000, 2048), (1, 37, 64), (1, 2560, 10240),
-                                   (1, 2560, 2560), (1, 1030, 2560), (1, 10240, 2560)])
+                                   (1, 2560, 2560), (1, 1030, 2560), (1, 10240, 2560), (1, 32771, 2048)])
 def test_linear_quant_gemv(dev, oracle, qt, M, N, K):
     gen = S.q4_0_blocks if qt == Q4_0 else S.q8_0_blocks
     blocks = gen(2, f"W{N}x{K}", N, K)
@@ -275,14 +275,16 @@ def test_linear_bias_and_f16_odd_shapes(dev, oracle):
 
 
 @pytest.mark.parametrize("qt", [Q4_0, Q8_0, F16])
-@pytest.mark.parametrize("N,K", [(37, 96), (1025, 2048), (300, 5632), (2, 32), (1030, 5632), (2560, 2560), (1030, 2560)])
+@pytest.mark.parametrize("N,K", [(37, 96), (1025, 2048), (300, 5632), (2, 32), (1030, 5632), (2560, 2560), (1030, 2560),
+                                 (32771, 2048)])
 def test_linear_one_row_bias(dev, oracle, qt, N, K):
     """One activation row with a bias: the compact M = 1 GEMV (rows per wave
     1 or 2, blocks past the row read as zero weights: K = 96 and 5632 leave
     lanes without a block, K = 32 all but one); from 1024 rows the
-    epilogue-specialised instantiations, two rows per wave at K = 2048 and
-    one at K = 5632 (three 64-block passes), with idle waves in the last
-    workgroup at N = 1030."""
+    epilogue-specialised instantiations, two rows per wave at K = 2048 (Q4_0
+    from 32768 rows: four, the last wave with three rows) and one at
+    K = 5632 (three 64-block passes), with idle waves in the last workgroup
+    at N = 1030."""
     x = S.normal_f16(9, f"x1b{K}", (1, K))
     b = S.normal_f16(9, f"b1b{N}", (N,))
     if qt == F16:
