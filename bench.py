@@ -586,7 +586,8 @@ def main():
             "hbm_bytes_per_token": weights_per_token,
             "decode_hbm_roofline_frac": round(tok_s * weights_per_token / (HBM_PEAK_GBS * 1e9), 4),
             "gemv_2048x5632": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in gem.items()},
-            "gemv_q4_0_size_sweep_k2048": {k: {kk: round(vv, 4) for kk, vv in v.items()} for k, v in sweep.items()},
+            "gemv_q4_0_size_sweep_k2048": {k: {kk: vv if isinstance(vv, list) else round(vv, 4) for kk, vv in v.items()}
+                                           for k, v in sweep.items()},
             "copy_reference": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in cp.items()},
             "config2_q8_0": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c2.items()},
             "config3_attention": {k: {kk: round(vv, 3) for kk, vv in v.items()} for k, v in c3.items()},
