@@ -112,6 +112,25 @@ def test_tiny_llama_sampled_decode(dev, oracle, tmp_path):
     assert a[0] == oracle.sample_temperature(lg, 0.8, r) or _sample_ok(lg.astype(np.float16), 0.8, r, int(a[0]))
 
 
+def test_tiny_llama_graph_step_counts(dev, oracle, tmp_path):
+    """Decode runs replay an 8-step graph and a 1-step graph for the rest:
+    13 steps (8 + 5), 8, 7 and 1 step give the direct launches' tokens, and
+    the oracle's greedy stream."""
+    path = str(tmp_path / "tiny_llama_steps.gguf")
+    S.write_llama_gguf(path, seed=26, **TINY_LLAMA)
+    prompt = S.token_ids(26, "prompt", 46, TINY_LLAMA["vocab"])
+    m = Model(dev, path, arch=0, max_ctx=128)
+    om = oracle.Model(path, arch=0, max_ctx=128)
+    ref, _, _ = om.generate(prompt, 13)
+    om.close()
+    for n in (13, 8, 7, 1):
+        g = m.generate(prompt, n, use_graph=True)
+        d = m.generate(prompt, n, use_graph=False)
+        assert np.array_equal(g, d), n
+        assert np.array_equal(g, ref[:n + 1]), n
+    m.close()
+
+
 def test_tiny_llama_chat_turn(dev, tmp_path):
     """The chat loop of chat_demo_optimized.tl:176-262 end to end on the
     device: template -> tokens -> sampled decode (T = 0.8) -> text; the same
