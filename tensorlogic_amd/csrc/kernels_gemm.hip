@@ -3,15 +3,20 @@
 // y[M, N] = x[M, K] . W[N, K]^T, W packed Q4_0 / Q8_0 or f16.  Each K step
 // stages an activation tile and a weight tile in LDS; the weight tile is
 // dequantised while it is written to LDS (RNE_f16((q-8)*d) / RNE_f16(q*d)
-// with v_pk_mul_f16, the exact values of gguf.rs:22-112), then
-// v_mfma_f32_32x32x8_f16 accumulates in fp32 as the reference's tiled
-// matmul does (unified.metal:4291-4348).  Output f16 with the same epilogues
-// as the GEMV (bias, residual add, SwiGLU on interleaved gate/up rows).
+// with v_pk_mul_f16, the exact values of gguf.rs:22-112), then the matrix
+// cores accumulate in fp32 as the reference's tiled matmul does
+// (unified.metal:4291-4348): v_mfma_f32_32x32x16_f16 in gemm2_kernel and
+// gemm_lds_kernel, v_mfma_f32_16x16x32_f16 in gemm_skinny_kernel, and
+// v_mfma_f32_32x32x8_f16 in the K % 64 != 0 fallback gemm_kernel.  Output
+// f16 with the same epilogues as the GEMV (bias, residual add, SwiGLU on
+// interleaved gate/up rows).
 //
-// Three kernels: gemm_kernel (K % 64 != 0; 64 x 64 x 32 tiles), gemm2_kernel
-// (M <= 64: register-staged, two LDS buffers) and gemm_lds_kernel (M > 64:
-// 128 x 128 tiles, three or four LDS stages filled by direct global->LDS
-// loads).
+// Four kernels: gemm_kernel (K % 64 != 0; 64 x 64 x 32 tiles),
+// gemm_skinny_kernel (M <= 64: a ring of LDS stages per wave filled by
+// direct global->LDS loads, split over K with a fence-free exchange),
+// gemm2_kernel (register-staged, two LDS buffers, where the skinny plan does
+// not apply) and gemm_lds_kernel (M > 64: 128 x 128 tiles, three or four
+// LDS stages filled by direct global->LDS loads).
 #include <type_traits>
 
 #include "device_common.hpp"
