@@ -1301,8 +1301,9 @@ __global__ __launch_bounds__(WPB * 64) void gemv_norm_kernel(GemvParams pk) {
 // Launch shapes of the normalised GEMV (M = 1) by row count: 8 waves x 4
 // rows from 16384 rows (not for the paired epilogues), 8 waves x 2 rows from
 // 8192, else 4 waves x 2 rows; the epilogue-specialised paired kernels take
-// 4 waves x 2 rows at every size (measured at [11264 x 2048] Q4_0 under
-// graph replay: 6.27-6.29 vs 6.32-6.36 us with 8 waves).  gemv_norm_slots
+// 4 waves x 2 rows, the SwiGLU pair 4 waves x 4 rows from 8192 (measured at
+// [11264 x 2048] Q4_0 under graph replay: 6.27-6.29 vs 6.32-6.36 us with 8
+// waves x 2 rows).  gemv_norm_slots
 // gives the workgroup count of the greedy-key epilogue's shapes.
 template <int WT, int NB, int PRO, int EPI = -1>
 static void launch_norm_shape(hipStream_t s, const GemvParams& p) {
@@ -1335,6 +1336,11 @@ static void launch_norm_shape(hipStream_t s, const GemvParams& p) {
     } else if (p.N >= 8192 && !paired) {
         const int wgs = (p.N + 15) / 16;   // 8 waves x 2 rows
         hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 2, 8, PRO, EPI>), dim3(wgs), dim3(512), 0, s, p);
+    } else if (EPI == EPI_SWIGLU_PAIR && p.N >= 8192) {
+        // 4 waves x 4 rows (measured on MI355X, config-4 decode with its
+        // [11264 x 2048] Q4_0 gate/up + SwiGLU: 2202 -> 2219 tok/s against 2
+        // rows per wave, same tokens)
+        hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 4, 4, PRO, EPI>), dim3((p.N + 15) / 16), dim3(256), 0, s, p);
     } else {
         const int wgs = (p.N + 7) / 8;     // 4 waves x 2 rows
         hipLaunchKernelGGL((gemv_norm_kernel<WT, NB, 2, 4, PRO, EPI>), dim3(wgs), dim3(256), 0, s, p);
