@@ -968,9 +968,12 @@ __device__ __forceinline__ void dot_flat(const u4 (&q)[Flat<FN, RI>::IT][BlkLoad
 
 // Plain GEMV of one activation row (M = 1) with the single-row epilogues
 // (STORE, BIAS, RESID, BIAS_RESID, BIAS_GELU): the decoder's output and
-// down projections and linear() on one row.  The arithmetic is
-// gemv_kernel's, bit for bit (same block dots, same lane partial sums, same
-// wave reduction); what differs is how the loads are addressed.  Its
+// down projections and linear() on one row.  The per-block arithmetic is
+// gemv_kernel's (the same dequantised weights and products, fp32 sums, the
+// same wave reduction); the lane partial sums are gemv_kernel's for the
+// row-per-wave layout of Q4_0, Q6_K and f16, and in another order for the
+// flat layout and Q8_0's half-block words (the same values up to fp32
+// summation order).  What differs besides is how the loads are addressed.  Its
 // parameter block holds only what these epilogues read, fetched as the
 // code first needs it; the wave's rows are scalar (the wave index is read
 // through readfirstlane), and every load is a range-checked buffer load
