@@ -324,8 +324,9 @@ tlhip_status tlhip_model_prefill(tlhip_model m, const int32_t* ids, int n, int32
 /* One decode step for `token` at the current position; returns the next. */
 tlhip_status tlhip_model_decode(tlhip_model m, int32_t token, int32_t* next_token);
 /* prefill(prompt) then n_decode greedy steps; tokens_out gets 1 + n_decode
- * ids.  use_graph = 1 replays one captured HIP graph per step, with the
- * token and position kept on the device (no per-token host sync).        */
+ * ids.  use_graph = 1 replays captured HIP graphs (one of 8 steps while 8
+ * or more remain, then one of 1 step), with the token and position kept on
+ * the device (no per-token host sync).                                    */
 tlhip_status tlhip_model_generate(tlhip_model m, const int32_t* prompt, int n_prompt,
                                   int n_decode, int use_graph, int32_t* tokens_out);
 /* Copies the last computed logits row (f16, vocab entries) to host.       */
@@ -362,10 +363,11 @@ tlhip_status tlhip_bench_linear(tlhip_ctx ctx, tlhip_tensor x, const tlhip_tenso
  * bandwidth reference of the device and the known-size kernel that scales
  * the profiler's HBM byte counters.  Allocates and frees its own buffers. */
 tlhip_status tlhip_bench_copy(tlhip_ctx ctx, size_t bytes, int n_buf, int iters, float* avg_us);
-/* Times `n_decode` greedy steps after a prefill (use_graph = 1: one
- * captured HIP graph replayed per step; 0: the same kernels launched one
- * by one); returns the prefill and total decode ms (hipEvents on the
- * context stream) and the 1 + n_decode tokens.                           */
+/* Times `n_decode` greedy steps after a prefill (use_graph = 1: captured
+ * HIP graphs of 8 and 1 steps replayed, as tlhip_model_generate, captured
+ * before the timed region; 0: the same kernels launched one by one);
+ * returns the prefill and total decode ms (hipEvents on the context
+ * stream) and the 1 + n_decode tokens.                                    */
 tlhip_status tlhip_bench_decode(tlhip_model m, const int32_t* prompt, int n_prompt, int n_decode,
                                 int use_graph, int32_t* tokens_out, float* prefill_ms, float* decode_ms);
 /* Event pair on the context stream around any sequence of asynchronous
