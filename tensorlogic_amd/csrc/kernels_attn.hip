@@ -1292,10 +1292,12 @@ struct FaWave {
     }
 };
 
-template <int D>
-__global__ __launch_bounds__(fa_heads<D>() * 128) void attention_mfma_kernel(AttnArgs a, const uint16_t* __restrict__ vt, int J,
+// HPW heads per workgroup (two waves each); the heads share no operands
+// here, so HPW only sets the launch granularity.
+template <int D, int HPW = fa_heads<D>()>
+__global__ __launch_bounds__(HPW * 128) void attention_mfma_kernel(AttnArgs a, const uint16_t* __restrict__ vt, int J,
                                                              int Jp, int nqt) {
-    constexpr int HPW = fa_heads<D>(), NT = (D + 31) / 32;
+    constexpr int NT = (D + 31) / 32;
     __shared__ float stm[HPW][64], sts[HPW][64];
     __shared__ float ob[HPW][NT * 16 * 64];
     __shared__ __attribute__((aligned(16))) uint16_t ot[HPW][32 * fa_ot_stride<D>()];
@@ -1733,12 +1735,23 @@ static bool attention_staged_ok(const AttnArgs& a, int J) {
            jp * a.Hkv * a.D * 2 < 0x80000000u;
 }
 
+// Heads per workgroup of the operands-from-memory kernel without GQA: one,
+// so a prefill fills the device (Phi-2, 32 heads at S = 512: 256 workgroups
+// instead of 64; measured on MI355X, 512-token prefill 7.97 -> 7.52 ms, 7.60
+// with two heads per workgroup, same tokens).
+constexpr int FA_HPW_NOGQA = 1;
 template <int D>
 static void launch_fa(hipStream_t s, const AttnArgs& a, const uint16_t* vt, int J, int Jp, int nqt, int gx, bool staged) {
     constexpr int HPW = fa_heads<D>();
     const dim3 grid(gx, (a.H + HPW - 1) / HPW), block(HPW * 128);
-    if (staged) hipLaunchKernelGGL(attention_mfma_staged_kernel<D>, grid, block, 0, s, a, vt, J, Jp, nqt);
-    else hipLaunchKernelGGL(attention_mfma_kernel<D>, grid, block, 0, s, a, vt, J, Jp, nqt);
+    if (staged) {
+        hipLaunchKernelGGL(attention_mfma_staged_kernel<D>, grid, block, 0, s, a, vt, J, Jp, nqt);
+    } else if (a.H == a.Hkv) {
+        constexpr int H1 = FA_HPW_NOGQA;
+        hipLaunchKernelGGL((attention_mfma_kernel<D, H1>), dim3(gx, (a.H + H1 - 1) / H1), dim3(H1 * 128), 0, s, a, vt, J, Jp, nqt);
+    } else {
+        hipLaunchKernelGGL(attention_mfma_kernel<D>, grid, block, 0, s, a, vt, J, Jp, nqt);
+    }
 }
 
 // Prefill over J keys through the matrix cores; vt holds
