@@ -370,10 +370,98 @@ __global__ void rope_kv_kernel(const uint16_t* __restrict__ qkv, int qkv_stride,
     }
 }
 
+// rope_kv_kernel with 8 output elements per thread and 16-byte accesses,
+// for the model's two layouts: 0 (interleaved pairs (2i, 2i+1) rotated in
+// place, every dim rotated: rot == D) and 2 (pair-permuted rows, pair i at
+// (2i, 2i+1), rotated into (i, i + half); dims >= rot pass through).  The
+// per-pair arithmetic is rope_kv_kernel's (rope_pair, the same table
+// entries).  Item e of a row: q heads, then k heads, each head D / 8 items
+// (layout 2: half / 8 items of 8 pairs writing (i, i + half), then the
+// pass-through dims 8 at a time; layout 0: 4 pairs each), then V, D / 8
+// 16-byte copies per KV head.
+__global__ void rope_kv8_kernel(const uint16_t* __restrict__ qkv, int qkv_stride, int S, int H, int Hkv, int D,
+                                int layout, int rot, const float* __restrict__ table, int pos0,
+                                const int32_t* d_pos, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
+                                uint16_t* __restrict__ vc) {
+    const int half = rot / 2, per_head = D / 8;
+    const int nq = H * per_head, nk = Hkv * per_head, per_row = nq + nk + Hkv * per_head;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)S * per_row) return;
+    const int s = (int)(idx / per_row);
+    int e = (int)(idx % per_row);
+    const int pos = pos0 + (d_pos ? *d_pos : 0) + s;
+    const uint16_t* row = qkv + (size_t)s * qkv_stride;
+    if (e >= nq + nk) {   // V: copy into the cache
+        e -= nq + nk;
+        *(u4*)(vc + (size_t)pos * Hkv * D + 8 * e) = *(const u4*)(row + (size_t)(H + Hkv) * D + 8 * e);
+        return;
+    }
+    const bool is_k = e >= nq;
+    if (is_k) e -= nq;
+    const int h = e / per_head, pe = e % per_head;
+    const uint16_t* xr = row + (size_t)(is_k ? H + h : h) * D;
+    uint16_t* yr = is_k ? kc + (size_t)pos * Hkv * D + (size_t)h * D : q_out + (size_t)s * H * D + (size_t)h * D;
+    const float* tp = table + 2 * (size_t)pos * half;
+    if (layout == 0) {   // pairs 4 pe .. 4 pe + 3 in place
+        const u4 x = *(const u4*)(xr + 8 * pe);
+        u4 y;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const h2 v = as_h2(x[k]);
+            const int i = 4 * pe + k;
+            float r0, r1;
+            rope_pair((float)v[0], (float)v[1], tp[2 * i], tp[2 * i + 1], r0, r1);
+            h2 o;
+            o[0] = (h16)r0;
+            o[1] = (h16)r1;
+            y[k] = as_u32(o);
+        }
+        *(u4*)(yr + 8 * pe) = y;
+        return;
+    }
+    const int hr = half / 8;
+    if (pe >= hr) {   // pass-through dims rot + 8 (pe - hr) ..
+        const int d = rot + 8 * (pe - hr);
+        *(u4*)(yr + d) = *(const u4*)(xr + d);
+        return;
+    }
+    // pairs 8 pe .. 8 pe + 7 (input elements 16 pe .. 16 pe + 15)
+    const u4 xa = *(const u4*)(xr + 16 * pe), xb = *(const u4*)(xr + 16 * pe + 8);
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 8; k += 2) {
+        float r[2][2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const h2 v = as_h2(k + u < 4 ? xa[k + u] : xb[k + u - 4]);
+            const int i = 8 * pe + k + u;
+            rope_pair((float)v[0], (float)v[1], tp[2 * i], tp[2 * i + 1], r[u][0], r[u][1]);
+        }
+        h2 o0, o1;
+        o0[0] = (h16)r[0][0];
+        o0[1] = (h16)r[1][0];
+        o1[0] = (h16)r[0][1];
+        o1[1] = (h16)r[1][1];
+        lo[k / 2] = as_u32(o0);
+        hi[k / 2] = as_u32(o1);
+    }
+    *(u4*)(yr + 8 * pe) = u4{lo[0], lo[1], lo[2], lo[3]};
+    *(u4*)(yr + half + 8 * pe) = u4{hi[0], hi[1], hi[2], hi[3]};
+}
+
 tlhip_status launch_rope_kv(hipStream_t s, const uint16_t* qkv, int qkv_stride, int S, int H,
                             int Hkv, int D, int layout, int rot_dims, const float* table, int pos0,
                             const int32_t* d_pos, uint16_t* q_out, uint16_t* kcache,
                             uint16_t* vcache) {
+    const bool vec = D % 8 == 0 && qkv_stride % 8 == 0 && ((layout == 0 && rot_dims == D) || (layout == 2 && rot_dims % 16 == 0)) &&
+                     ((uintptr_t)qkv | (uintptr_t)q_out | (uintptr_t)kcache | (uintptr_t)vcache | (uintptr_t)table) % 16 == 0;
+    if (vec) {
+        const int64_t total = (int64_t)S * (H + 2 * Hkv) * (D / 8);
+        if (total <= 0) return TLHIP_OK;
+        hipLaunchKernelGGL(rope_kv8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, qkv, qkv_stride, S,
+                           H, Hkv, D, layout, rot_dims, table, pos0, d_pos, q_out, kcache, vcache);
+        return TLHIP_OK;
+    }
     const int per_head = D - rot_dims / 2;
     int64_t total = (int64_t)S * ((H + Hkv) * per_head + Hkv * D);
     if (total <= 0) return TLHIP_OK;
