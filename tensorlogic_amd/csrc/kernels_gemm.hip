@@ -1111,6 +1111,36 @@ __global__ void gemm_reduce_kernel(GemmParams p, const float* __restrict__ part,
     }
 }
 
+// gemm_reduce_kernel for 4 consecutive columns per thread (16-byte partial
+// loads, one 8-byte store; the SwiGLU pair epilogue: two outputs, one
+// 4-byte store): the same sums in slice order and the same epilogue per
+// element.  N and the output row stride multiples of 4 (SwiGLU: of 2 for
+// the output), the partials 16-byte and the other pointers 8-byte aligned.
+__global__ void gemm_reduce4_kernel(GemmParams p, const float* __restrict__ part, int splits) {
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    const int64_t total = (int64_t)p.M * p.N;
+    if (i >= total) return;
+    const int m = (int)(i / p.N), n = (int)(i % p.N);
+    float4 v = *(const float4*)(part + i);
+    for (int z = 1; z < splits; z++) {
+        const float4 t = *(const float4*)(part + (size_t)z * total + i);
+        v.x += t.x;
+        v.y += t.y;
+        v.z += t.z;
+        v.w += t.w;
+    }
+    if (p.epi == EPI_SWIGLU_PAIR) {
+        const uint32_t o0 = swiglu_h(f2h(v.x), f2h(v.y)), o1 = swiglu_h(f2h(v.z), f2h(v.w));
+        *(uint32_t*)(p.y + (size_t)m * p.ldy + n / 2) = o0 | (o1 << 16);
+        return;
+    }
+    const size_t ri = (size_t)m * p.N + n;
+    const uint32_t o0 = epilogue_h(p.epi, v.x, p.bias, p.resid, ri, n);
+    const uint32_t o1 = epilogue_h(p.epi, v.y, p.bias, p.resid, ri + 1, n + 1);
+    const uint32_t o2 = epilogue_h(p.epi, v.z, p.bias, p.resid, ri + 2, n + 2);
+    const uint32_t o3 = epilogue_h(p.epi, v.w, p.bias, p.resid, ri + 3, n + 3);
+    *(uint2*)(p.y + (size_t)m * p.ldy + n) = uint2{o0 | (o1 << 16), o2 | (o3 << 16)};
+}
 
 constexpr int GL_BM = 128, GL_BN = 128;
 
@@ -1239,8 +1269,14 @@ tlhip_status launch_gemm(hipStream_t s, tlhip_dtype wt, const GemvArgs& a, int e
         else launch_gemm2<TLHIP_F16>(s, p, splits, part);
         if (splits > 1) {
             const int64_t total = (int64_t)p.M * p.N;
-            hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, p,
-                               (const float*)part, splits);
+            const bool vec = p.N % 4 == 0 && p.ldy % (p.epi == EPI_SWIGLU_PAIR ? 2 : 4) == 0 &&
+                             ((uintptr_t)p.y | (uintptr_t)p.bias | (uintptr_t)p.resid) % 8 == 0 && (uintptr_t)part % 16 == 0;
+            if (vec)
+                hipLaunchKernelGGL(gemm_reduce4_kernel, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0, s, p,
+                                   (const float*)part, splits);
+            else
+                hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, p,
+                                   (const float*)part, splits);
         }
         return TLHIP_OK;
     }
