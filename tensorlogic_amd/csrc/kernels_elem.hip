@@ -375,16 +375,21 @@ __global__ void rope_kv_kernel(const uint16_t* __restrict__ qkv, int qkv_stride,
 // place, every dim rotated: rot == D) and 2 (pair-permuted rows, pair i at
 // (2i, 2i+1), rotated into (i, i + half); dims >= rot pass through).  The
 // per-pair arithmetic is rope_kv_kernel's (rope_pair, the same table
-// entries).  Item e of a row: q heads, then k heads, each head D / 8 items
-// (layout 2: half / 8 items of 8 pairs writing (i, i + half), then the
-// pass-through dims 8 at a time; layout 0: 4 pairs each), then V, D / 8
+// entries).  Item e of a row: q heads, then k heads, each head
+// rope8_items(layout, D, rot) items (layout 2: half / 8 items of 8 pairs,
+// each writing 16 outputs (i, i + half), then (D - rot) / 8 items copying
+// the pass-through dims; layout 0: D / 8 items of 4 pairs), then V, D / 8
 // 16-byte copies per KV head.
+__host__ __device__ __forceinline__ int rope8_items(int layout, int D, int rot) {
+    return layout == 2 ? rot / 16 + (D - rot) / 8 : D / 8;
+}
+
 __global__ void rope_kv8_kernel(const uint16_t* __restrict__ qkv, int qkv_stride, int S, int H, int Hkv, int D,
                                 int layout, int rot, const float* __restrict__ table, int pos0,
                                 const int32_t* d_pos, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
                                 uint16_t* __restrict__ vc) {
-    const int half = rot / 2, per_head = D / 8;
-    const int nq = H * per_head, nk = Hkv * per_head, per_row = nq + nk + Hkv * per_head;
+    const int half = rot / 2, per_head = rope8_items(layout, D, rot);
+    const int nq = H * per_head, nk = Hkv * per_head, per_row = nq + nk + Hkv * (D / 8);
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (int64_t)S * per_row) return;
     const int s = (int)(idx / per_row);
@@ -456,7 +461,7 @@ tlhip_status launch_rope_kv(hipStream_t s, const uint16_t* qkv, int qkv_stride, 
     const bool vec = D % 8 == 0 && qkv_stride % 8 == 0 && ((layout == 0 && rot_dims == D) || (layout == 2 && rot_dims % 16 == 0)) &&
                      ((uintptr_t)qkv | (uintptr_t)q_out | (uintptr_t)kcache | (uintptr_t)vcache | (uintptr_t)table) % 16 == 0;
     if (vec) {
-        const int64_t total = (int64_t)S * (H + 2 * Hkv) * (D / 8);
+        const int64_t total = (int64_t)S * ((H + Hkv) * rope8_items(layout, D, rot_dims) + Hkv * (D / 8));
         if (total <= 0) return TLHIP_OK;
         hipLaunchKernelGGL(rope_kv8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, qkv, qkv_stride, S,
                            H, Hkv, D, layout, rot_dims, table, pos0, d_pos, q_out, kcache, vcache);

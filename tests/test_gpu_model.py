@@ -162,6 +162,19 @@ def test_tiny_phi2_greedy(dev, oracle, tmp_path):
     _compare(dev, oracle, path, 1, prompt, 24)
 
 
+@pytest.mark.parametrize("n_prompt", [65, 200])
+def test_tiny_phi2_prefill_past_64_rows(dev, oracle, tmp_path, n_prompt):
+    """A prompt of more than 64 rows takes the tiled GEMM and the separate
+    RoPE + cache write (8 outputs per thread; partial rotary: per head of 80
+    dims 16 rotated pairs written to (i, i + 16) and 48 dims passed through),
+    and from 128 rows the matrix-core attention with one head per workgroup:
+    tokens and final logits equal the oracle's."""
+    path = str(tmp_path / "tiny_phi2_rows.gguf")
+    S.write_phi2_gguf(path, seed=29, **TINY_PHI2)
+    prompt = S.token_ids(29, "prompt", n_prompt, TINY_PHI2["vocab"])
+    _compare(dev, oracle, path, 1, prompt, 4, max_ctx=256)
+
+
 def test_tiny_phi2_long_cache_split_attention(dev, oracle, tmp_path):
     """Head dim 80 with a cache of more than 512 rows: decode attention runs
     key-chunked (128-key chunks, combined by the last workgroup of each head
