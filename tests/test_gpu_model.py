@@ -197,6 +197,20 @@ def test_tiny_phi2_wide_chunk_split_attention(dev, oracle, tmp_path):
     _compare(dev, oracle, path, 1, prompt, 12, max_ctx=1100)
 
 
+def test_llama_prefill_split_k(dev, oracle, tmp_path):
+    """A one-layer llama with hidden 1024 and FFN 2048: a 130-row prompt
+    runs the tiled GEMM split over K for every projection (2 or 4 slices), so
+    the split-K sums with the store, residual and SwiGLU-pair epilogues (four
+    columns per thread), then the separate RoPE + cache write (interleaved
+    pairs) and the staged matrix-core attention (16 / 4 heads); tokens and
+    final logits equal the oracle's."""
+    dims = dict(n_layers=1, hidden=1024, inter=2048, n_heads=16, n_kv=4, vocab=1000)
+    path = str(tmp_path / "llama_split_k.gguf")
+    S.write_llama_gguf(path, seed=31, **dims)
+    prompt = S.token_ids(31, "prompt", 130, dims["vocab"])
+    _compare(dev, oracle, path, 0, prompt, 4, max_ctx=256)
+
+
 def test_long_prompt_chunked_prefill(dev, oracle, tmp_path):
     # more prompt tokens than one prefill chunk holds (512 rows)
     path = str(tmp_path / "tiny_llama_long.gguf")
